@@ -1,0 +1,129 @@
+/* C ABI of libmaloq_hip.so: MI355X (gfx950) kernels for MALOQ's equivariant
+ * message-passing hot path.
+ *
+ * Conventions for every entry point:
+ *   - All pointers are device pointers unless stated otherwise; tensors are
+ *     row-major and contiguous.
+ *   - `stream` is a hipStream_t passed as void*; work is enqueued, never synced.
+ *   - Return 0 on success, non-zero on error; maloq_last_error() gives the text.
+ *   - fp32 unless a `dtype` argument says otherwise (0 = fp32, 1 = bf16 with
+ *     fp32 accumulation).
+ *
+ * Each declaration names the reference interface (file:line under
+ * src/maloq/) it replaces.
+ */
+#ifndef MALOQ_HIP_H
+#define MALOQ_HIP_H
+
+#include <stdint.h>
+
+#define MALOQ_ABI_VERSION 1
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+int maloq_abi_version(void);
+const char* maloq_last_error(void);
+
+/* ------------------------------------------------------------ Wigner-D -- */
+
+/* Euler triple (alpha, beta, gamma) per edge, as fed to wigner_D:
+ * (-gamma, -beta, -alpha) with gamma = Philox(seed, edge) * 2*pi.
+ * edge_vec [E,3] (e3nn y-z-x frame), eulers [E,3].
+ * Replaces extract_euler_angles, helm/triton_kernels/wigner_fused.py:383-397
+ * (and init_edge_rot_euler_angles, helm/common/rotation.py:68-83). */
+int maloq_edge_euler(const float* edge_vec, int64_t num_edges, uint64_t seed, float* eulers,
+                     void* stream);
+
+/* Dense block-diagonal Wigner-D [E,d,d], d=(lmax+1)^2, 0<=lmax<=8, built from
+ * edge vectors in one launch.  jd_packed: J_0..J_lmax row-major, concatenated.
+ * eulers_out (nullable) receives the angles used.  wigner / wigner_inv
+ * (either nullable) receive D and D^T.  write_zeros != 0 also stores the
+ * off-diagonal zeros (else only diagonal blocks are written).
+ * Replaces edge_vec_to_wigner_fused, helm/triton_kernels/wigner_fused.py:403-486,
+ * plus the transpose().contiguous() of helm/esen_osh.py:294. */
+int maloq_edge_vec_to_wigner(const float* edge_vec, int64_t num_edges, uint64_t seed, int lmax,
+                             const float* jd_packed, float* eulers_out, float* wigner,
+                             float* wigner_inv, int write_zeros, void* stream);
+
+/* Same, from given Euler triples [E,3].
+ * Replaces eulers_to_wigner, helm/common/rotation.py:19-39. */
+int maloq_wigner_from_euler(const float* eulers, int64_t num_edges, int lmax,
+                            const float* jd_packed, float* wigner, float* wigner_inv,
+                            int write_zeros, void* stream);
+
+/* ------------------------------------------------------ basis transform -- */
+
+/* Block-sparse row transform on label rows:
+ *   out[r, o] = sum_{k < len[o]} in[r, col(src[o] + k)] * w[woff[o] + k]
+ * with col(c) = in_col_map ? in_col_map[c] : c.  in [R, t_in], out [R, t_out].
+ * One call implements get_H (utils_tensor_decomp.py:154-161), get_net_out
+ * (:163-169) and the get_H backward (basis_transform_triton_backend.py:1070-1073),
+ * depending on the tables built by the host; sorted irreps via the maps.
+ * Replaces BalancedTritonE3TensorDecompL2._get_H_impl/_get_net_out_impl,
+ * fock_utils/basis_transform_triton_backend.py:1366-1438 (kernels K6/K8). */
+int maloq_label_transform(const float* in, int64_t num_rows, int t_in, const int32_t* in_col_map,
+                          float* out, int t_out, const int32_t* ocol_src, const int32_t* ocol_len,
+                          const int32_t* ocol_woff, const float* w, int max_len, void* stream);
+
+/* Fused Fock -> irreps: gather every (row i, col j) atom-pair block of the
+ * Fock matrix by its element-pair template and contract it with the CG tables.
+ *   dense  (data_offsets == NULL): block at fock[off[i]*ld + off[j]], ld = row stride;
+ *   sparse (data_offsets != NULL): block r at fock[data_offsets[r]], n_i x n_j row-major.
+ * pair_kind: int32 [100*100] element-pair -> compact kind (-1 absent).
+ * sub_origin: int32 [num_kinds, nblocks, 2] (r0, c0) of CG block b in that kind's
+ * atom-pair block, or (-1, -1) if absent.  ocol_block/ocol_len/ocol_woff: per
+ * output column its CG block, length n1*n2 and weight offset; block_n2 [nblocks].
+ * Replaces cupy_single_matrix2label(forward=True) + get_net_out,
+ * fock_utils/matrix2labels_kernels.py:946-1036 (K12) / :1038-1115 (K13) and
+ * fock_targets_batched.py:426-441. */
+int maloq_fock_to_irreps(const float* fock, int64_t ld, const int64_t* data_offsets,
+                         const int32_t* fock_block_offsets, const int32_t* atomic_numbers,
+                         const int32_t* rows, const int32_t* cols, int64_t num_rows,
+                         const int32_t* pair_kind, const int32_t* sub_origin, int nblocks,
+                         const int32_t* block_n2, float* out, int t_out, const int32_t* ocol_block,
+                         const int32_t* ocol_len, const int32_t* ocol_woff, const float* w,
+                         int max_block_elems, void* stream);
+
+/* Fused irreps -> Fock: get_H per row, then scatter the covered entries of each
+ * atom-pair block into the Fock storage (dense or block-sparse, as above).
+ * hcol_block/hcol_src/hcol_len/hcol_woff: per H-space column its CG block, the
+ * first irreps column, the length and the weight offset; hcol_pos [t_h]: the
+ * flat position a*n2+b of the column inside its block.
+ * Replaces get_H + cupy_single_matrix2label(forward=False),
+ * train_utils/splittrainer.py:546-597 over matrix2labels_kernels.py:946-1036. */
+int maloq_irreps_to_fock(const float* irreps, int64_t num_rows, int t_in, float* fock,
+                         int64_t ld, const int64_t* data_offsets,
+                         const int32_t* fock_block_offsets, const int32_t* atomic_numbers,
+                         const int32_t* rows, const int32_t* cols, const int32_t* pair_kind,
+                         const int32_t* sub_origin, int nblocks, const int32_t* block_n2,
+                         int t_h, const int32_t* hcol_block, const int32_t* hcol_pos,
+                         const int32_t* hcol_src, const int32_t* hcol_len,
+                         const int32_t* hcol_woff, const float* w, void* stream);
+
+/* Plain Fock <-> label copy (no CG), dense or block-sparse storage as above.
+ * forward != 0: label[r, out0 + k] = block(r)[r0 + k/w, c0 + k%w];
+ * forward == 0: the reverse copy.  Template CSR: tmpl_ptr [100*100+1],
+ * tmpl [n, 5] = (r0, r1, c0, c1, out0).
+ * Replaces cupy_single_matrix2label / cupy_single_matrix2label_sparse,
+ * fock_utils/matrix2labels_kernels.py:946-1115 (kernels K12, K13). */
+int maloq_matrix2label(float* fock, int64_t ld, const int64_t* data_offsets,
+                       const int32_t* fock_block_offsets, const int32_t* atomic_numbers,
+                       const int32_t* rows, const int32_t* cols, int64_t num_rows,
+                       const int32_t* tmpl_ptr, const int32_t* tmpl, float* target,
+                       int64_t target_ld, int forward, void* stream);
+
+/* ------------------------------------------------------- segment scatter -- */
+
+/* out[n, :] = sum_{p in [seg_ptr[n], seg_ptr[n+1])} msg[perm ? perm[p] : p, :],
+ * summed in p order (deterministic).  msg [E, width], out [N, width].
+ * Replaces index_add_, helm/esen_block.py:194-206 and helm/nn/embedding.py:129-131. */
+int maloq_segment_sum(const float* msg, const int64_t* perm, const int64_t* seg_ptr,
+                      int64_t num_segments, int64_t width, float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MALOQ_HIP_H */

@@ -1,0 +1,87 @@
+"""ctypes binding of libmaloq_hip.so (the C ABI declared in include/maloq_hip.h).
+
+The product path has no fallback: if the library is missing or cannot be
+loaded, every op raises.  torch is imported first so that the library binds to
+the HIP runtime torch already loaded (same SONAME), which makes torch's device
+pointers and streams valid arguments.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (load torch's HIP runtime before ours)
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmaloq_hip.so")
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_u64 = ctypes.c_uint64
+
+# name -> argtypes (every symbol declared in include/maloq_hip.h)
+SIGNATURES = {
+    "maloq_abi_version": [],
+    "maloq_last_error": [],
+    "maloq_edge_euler": [_p, _i64, _u64, _p, _p],
+    "maloq_edge_vec_to_wigner": [_p, _i64, _u64, _i32, _p, _p, _p, _p, _i32, _p],
+    "maloq_wigner_from_euler": [_p, _i64, _i32, _p, _p, _p, _i32, _p],
+    "maloq_label_transform": [_p, _i64, _i32, _p, _p, _i32, _p, _p, _p, _p, _i32, _p],
+    "maloq_fock_to_irreps": [_p, _i64, _p, _p, _p, _p, _p, _i64, _p, _p, _i32, _p, _p, _i32,
+                             _p, _p, _p, _p, _i32, _p],
+    "maloq_irreps_to_fock": [_p, _i64, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i32, _p,
+                             _i32, _p, _p, _p, _p, _p, _p, _p],
+    "maloq_matrix2label": [_p, _i64, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _i64, _i32, _p],
+    "maloq_segment_sum": [_p, _p, _p, _i64, _i64, _p, _p],
+}
+
+_lib = None
+
+
+class MaloqHipError(RuntimeError):
+    pass
+
+
+def load():
+    """Load (once) and return the ctypes library; raise if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise MaloqHipError(
+            f"{LIB_PATH} is missing: build it with `python -m maloq_amd.build` "
+            "(there is no CPU fallback for the HIP path)"
+        )
+    lib = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_GLOBAL)
+    for name, argtypes in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_char_p if name == "maloq_last_error" else ctypes.c_int
+    _lib = lib
+    return lib
+
+
+def call(name: str, *args) -> None:
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.maloq_last_error().decode(errors="replace")
+        raise MaloqHipError(f"{name} failed ({rc}): {msg}")
+
+
+def ptr(t) -> int | None:
+    """Device pointer of a tensor (None for None)."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def stream_of(device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_cuda(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError("maloq_amd HIP ops need tensors on a ROCm GPU device")

@@ -1,0 +1,160 @@
+"""HIP Wigner backend: drop-in for ``maloq.helm.triton_kernels``.
+
+``edge_vec_to_wigner_fused`` and ``extract_euler_angles`` keep the reference's
+signatures and contracts (src/maloq/helm/triton_kernels/wigner_fused.py:383-486):
+AssertionError for lmax outside 0..8, ``seed=None`` draws a random seed,
+``out`` must be a zeroed contiguous [E, d, d] buffer (only diagonal blocks are
+written), E = 0 returns an empty [0, d, d] tensor without a launch.
+
+The random roll gamma comes from a Philox4x32-10 counter RNG keyed by
+(seed, edge index); ``extract_euler_angles`` returns exactly the angles the
+Wigner kernel uses, so parity is checked at those angles, as the reference's
+own tests do (tests/test_wigner_backend.py:58-102).
+"""
+from __future__ import annotations
+
+import random
+
+import numpy as np
+import torch
+
+from . import _lib
+from .so3 import jd_matrices, pack_jd
+
+_JD_CACHE: dict = {}
+
+
+def _packed_jd(Jd, lmax: int, device) -> torch.Tensor:
+    """Jd (list of per-l tensors, or None for the closed-form tables) packed on device."""
+    if Jd is None:
+        key = ("closed-form", lmax, str(device))
+        if key not in _JD_CACHE:
+            _JD_CACHE[key] = torch.from_numpy(pack_jd(jd_matrices(lmax), lmax)).to(device)
+        return _JD_CACHE[key]
+    if len(Jd) <= lmax:
+        raise ValueError(f"Jd has {len(Jd)} entries, need {lmax + 1}")
+    key = ("list", lmax, str(device), tuple(int(j.data_ptr()) if torch.is_tensor(j) else id(j) for j in Jd[: lmax + 1]))
+    hit = _JD_CACHE.get(key)
+    if hit is None:
+        mats = [np.asarray(j.detach().cpu().double() if torch.is_tensor(j) else j, dtype=np.float64) for j in Jd[: lmax + 1]]
+        hit = torch.from_numpy(pack_jd(mats, lmax)).to(device)
+        if len(_JD_CACHE) > 64:
+            _JD_CACHE.clear()
+        _JD_CACHE[key] = hit
+    return hit
+
+
+def _check_vec(edge_distance_vec):
+    if edge_distance_vec.dim() != 2 or edge_distance_vec.shape[1] != 3:
+        raise ValueError(f"edge_distance_vec must be [E, 3], got {tuple(edge_distance_vec.shape)}")
+    if edge_distance_vec.dtype != torch.float32:
+        raise ValueError("the HIP Wigner backend computes in fp32; got " + str(edge_distance_vec.dtype))
+    _lib.require_cuda(edge_distance_vec)
+
+
+def extract_euler_angles(edge_distance_vec: torch.Tensor, seed: int) -> torch.Tensor:
+    """[E, 3] (alpha, beta, gamma) exactly as the Wigner kernel computes them."""
+    _check_vec(edge_distance_vec)
+    E = edge_distance_vec.shape[0]
+    eulers = torch.empty(E, 3, device=edge_distance_vec.device, dtype=torch.float32)
+    if E > 0:
+        v = edge_distance_vec.contiguous()
+        _lib.call("maloq_edge_euler", _lib.ptr(v), E, int(seed) & (2**64 - 1), _lib.ptr(eulers),
+                  _lib.stream_of(v.device))
+    return eulers
+
+
+def edge_vec_to_wigner_fused(edge_distance_vec, Jd, lmax: int = 4, seed: int | None = None, out=None):
+    """Block-diagonal Wigner-D [E, d, d] from edge vectors in one HIP launch."""
+    assert 0 <= lmax <= 8, f"lmax must be 0-8, got {lmax}"
+    _check_vec(edge_distance_vec)
+    E = edge_distance_vec.shape[0]
+    d = (lmax + 1) ** 2
+    device = edge_distance_vec.device
+    if seed is None:
+        seed = random.randint(0, 2**31 - 1)
+    if out is not None:
+        assert out.shape == (E, d, d), f"out shape {tuple(out.shape)} != expected ({E}, {d}, {d})"
+        assert out.is_contiguous(), "out must be contiguous (row-major stride)"
+        assert out.dtype == torch.float32, "out must be float32"
+        wigner, write_zeros = out, 0
+    else:
+        wigner, write_zeros = torch.empty(E, d, d, device=device, dtype=torch.float32), 1
+    if E == 0:
+        return wigner
+    jd = _packed_jd(Jd, lmax, device)
+    v = edge_distance_vec.contiguous()
+    _lib.call("maloq_edge_vec_to_wigner", _lib.ptr(v), E, int(seed) & (2**64 - 1), lmax,
+              _lib.ptr(jd), None, _lib.ptr(wigner), None, write_zeros, _lib.stream_of(device))
+    return wigner
+
+
+def wigner_and_inverse(edge_distance_vec, Jd, lmax: int, seed: int | None = None, eulers_out=None):
+    """(D, D^T) written by one launch: replaces the Wigner build plus the
+    ``transpose(1, 2).contiguous()`` of ``_get_rotmat_and_wigner`` (esen_osh.py:266-296)."""
+    assert 0 <= lmax <= 8, f"lmax must be 0-8, got {lmax}"
+    _check_vec(edge_distance_vec)
+    E, d, device = edge_distance_vec.shape[0], (lmax + 1) ** 2, edge_distance_vec.device
+    if seed is None:
+        seed = random.randint(0, 2**31 - 1)
+    w = torch.empty(E, d, d, device=device, dtype=torch.float32)
+    wi = torch.empty_like(w)
+    if E > 0:
+        jd = _packed_jd(Jd, lmax, device)
+        v = edge_distance_vec.contiguous()
+        _lib.call("maloq_edge_vec_to_wigner", _lib.ptr(v), E, int(seed) & (2**64 - 1), lmax,
+                  _lib.ptr(jd), _lib.ptr(eulers_out), _lib.ptr(w), _lib.ptr(wi), 1,
+                  _lib.stream_of(device))
+    return w, wi
+
+
+def wigner_from_eulers(eulers: torch.Tensor, Jd, lmax: int, inverse: bool = False):
+    """Dense [E, d, d] Wigner-D (or its transpose) at given Euler triples."""
+    assert 0 <= lmax <= 8, f"lmax must be 0-8, got {lmax}"
+    _lib.require_cuda(eulers)
+    if eulers.dtype != torch.float32 or eulers.dim() != 2 or eulers.shape[1] != 3:
+        raise ValueError("eulers must be float32 [E, 3]")
+    E, d = eulers.shape[0], (lmax + 1) ** 2
+    w = torch.empty(E, d, d, device=eulers.device, dtype=torch.float32)
+    if E > 0:
+        jd = _packed_jd(Jd, lmax, eulers.device)
+        e = eulers.contiguous()
+        _lib.call("maloq_wigner_from_euler", _lib.ptr(e), E, lmax, _lib.ptr(jd),
+                  None if inverse else _lib.ptr(w), _lib.ptr(w) if inverse else None, 1,
+                  _lib.stream_of(eulers.device))
+    return w
+
+
+class EdgeFrames:
+    """Per-edge rotation frames for the fused message kernels: the Euler triples
+    [E, 3] (what wigner_D consumes) plus lmax.  Built once per forward, shared by
+    every layer, like the reference's (wigner, wigner_inv) pair."""
+
+    def __init__(self, eulers: torch.Tensor, lmax: int, Jd=None):
+        self.eulers = eulers
+        self.lmax = lmax
+        self.Jd = Jd
+
+    @property
+    def num_edges(self) -> int:
+        return self.eulers.shape[0]
+
+    def dense(self, inverse: bool = False) -> torch.Tensor:
+        return wigner_from_eulers(self.eulers, self.Jd, self.lmax, inverse=inverse)
+
+
+def get_rotmat_and_wigner(edge_distance_vecs, Jd_buffers, lmax: int, wigner_backend: str = "hip",
+                          seed: int | None = None):
+    """Backend switch of eSEN_Backbone._get_rotmat_and_wigner (esen_osh.py:266-296)
+    for the 'hip' value: returns the dense (wigner, wigner_inv) pair, both from
+    one launch."""
+    if wigner_backend != "hip":
+        raise ValueError(f"maloq_amd implements wigner_backend='hip' only, got '{wigner_backend}'")
+    return wigner_and_inverse(edge_distance_vecs, Jd_buffers, lmax, seed=seed)
+
+
+def edge_frames(edge_distance_vecs, lmax: int, Jd=None, seed: int | None = None) -> EdgeFrames:
+    """Euler triples for the fused message block (no dense [E, d, d] in HBM)."""
+    if seed is None:
+        seed = random.randint(0, 2**31 - 1)
+    return EdgeFrames(extract_euler_angles(edge_distance_vecs, seed), lmax, Jd)

@@ -1,0 +1,337 @@
+"""Pins of the CPU oracle (and of the product's host-side tables) against the
+reference's own data and against what the mathematics fixes.  CPU only."""
+import copy
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import rotation as orot
+from oracle import so2 as oso2
+from oracle import message as omsg
+from oracle import tensor_decomp as otd
+from oracle import matrix2labels as om2l
+from oracle.so3 import CoefficientMapping as OMapping
+
+from maloq_amd import so3 as pso3
+from maloq_amd import tensor_decomp as ptd
+
+
+
+@pytest.fixture(autouse=True)
+def _fp64_default():
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    yield
+    torch.set_default_dtype(old)
+
+
+def Ry(t):
+    c, s = math.cos(t), math.sin(t)
+    return np.array([[c, 0, s], [0, 1, 0], [-s, 0, c]])
+
+
+def Rx(t):
+    c, s = math.cos(t), math.sin(t)
+    return np.array([[1, 0, 0], [0, c, -s], [0, s, c]])
+
+
+def yxy_angles(R):
+    beta = math.acos(max(-1.0, min(1.0, R[1, 1])))
+    alpha = math.atan2(R[0, 1], R[2, 1])
+    gamma = math.atan2(R[1, 0], -R[1, 2])
+    return alpha, beta, gamma
+
+
+def D(l, a, b, c, Jd):
+    t = lambda x: torch.tensor([x])
+    return orot.wigner_D(l, t(a), t(b), t(c), Jd)[0].numpy()
+
+
+@pytest.fixture(scope="module")
+def Jd():
+    return orot.load_jd()
+
+
+# ------------------------------------------------------------------ J / D
+def test_jd_fixture_is_symmetric_orthogonal_involution(Jd):
+    for l, J in enumerate(Jd):
+        J = J.numpy()
+        assert J.shape == (2 * l + 1, 2 * l + 1)
+        assert np.abs(J - J.T).max() < 1e-14
+        assert np.abs(J @ J - np.eye(2 * l + 1)).max() < 1e-13
+
+
+def test_product_closed_form_jd_matches_reference_data(Jd):
+    ours = pso3.jd_matrices(11)
+    for l in range(12):
+        assert np.abs(ours[l] - Jd[l].numpy()).max() < 1e-13, l
+
+
+def test_wigner_l1_is_yxy_rotation(Jd):
+    rng = np.random.default_rng(0)
+    for _ in range(10):
+        a, b, c = rng.uniform(-6, 6, 3)
+        assert np.abs(D(1, a, b, c, Jd) - Ry(a) @ Rx(b) @ Ry(c)).max() < 1e-13
+
+
+@pytest.mark.parametrize("l", [0, 1, 2, 3, 4, 6, 8])
+def test_wigner_orthogonal_and_homomorphism(l, Jd):
+    rng = np.random.default_rng(l)
+    for _ in range(5):
+        a1, b1, c1, a2, b2, c2 = rng.uniform(-3, 3, 6)
+        D1, D2 = D(l, a1, b1, c1, Jd), D(l, a2, b2, c2, Jd)
+        assert np.abs(D1 @ D1.T - np.eye(2 * l + 1)).max() < 1e-12
+        R = (Ry(a1) @ Rx(b1) @ Ry(c1)) @ (Ry(a2) @ Rx(b2) @ Ry(c2))
+        D12 = D(l, *yxy_angles(R), Jd)
+        assert np.abs(D1 @ D2 - D12).max() < 1e-10
+
+
+def test_edge_frame_alignment(Jd):
+    """The reference's own check (esen_osh.py:333-335): D^1 v = (0, |v|, 0)."""
+    rng = np.random.default_rng(1)
+    v = torch.from_numpy(rng.standard_normal((50, 3)))
+    a, b, c = orot.init_edge_rot_euler_angles(v, torch.from_numpy(rng.uniform(0, 1, 50)))
+    w = orot.eulers_to_wigner((a, b, c), 0, 1, Jd)
+    r = torch.bmm(w[:, 1:4, 1:4], v.unsqueeze(-1)).squeeze(-1)
+    assert torch.allclose(r[:, 1], v.norm(dim=1), atol=1e-12)
+    assert r[:, [0, 2]].abs().max() < 1e-12
+    assert torch.all(w[:, 0, 0] == 1.0)
+
+
+# ------------------------------------------------------ coefficient tables
+@pytest.mark.parametrize("lmax,mmax", [(0, 0), (2, 2), (4, 2), (4, 4), (6, 2), (6, 6), (8, 3)])
+def test_coefficient_mapping_matches_oracle(lmax, mmax):
+    o = OMapping(lmax, mmax)
+    p = pso3.CoefficientMapping(lmax, mmax)
+    assert p.m_size == o.m_size
+    assert np.array_equal(p.to_m, o.to_m.numpy().astype(np.float32))
+    assert np.array_equal(p.to_m_index, torch.argmax(o.to_m, dim=1).numpy())
+    full_p, full_o = pso3.CoefficientMapping(lmax, lmax), OMapping(lmax, lmax)
+    assert np.array_equal(full_p.coefficient_idx(lmax, mmax), full_o.coefficient_idx(lmax, mmax).numpy())
+    # closed-form m_size and kept-row count
+    assert p.m_size == [lmax - m + 1 for m in range(mmax + 1)]
+    assert p.res_size == sum(min(2 * l + 1, 2 * mmax + 1) for l in range(lmax + 1))
+    kr = pso3.kept_rows(lmax, mmax)
+    ci = full_p.coefficient_idx(lmax, mmax)
+    assert [l * l + i for l, i in kr] == list(ci[p.to_m_index])
+
+
+# --------------------------------------------------------------- CG tables
+@pytest.mark.parametrize("l1,l2", [(0, 0), (0, 2), (1, 1), (1, 2), (2, 2), (2, 3), (3, 3)])
+def test_cg_invariance_norm_and_product_parity(l1, l2, Jd):
+    rng = np.random.default_rng(l1 * 10 + l2)
+    for l3 in range(abs(l1 - l2), l1 + l2 + 1):
+        C = otd.wigner_3j(l1, l2, l3).numpy()
+        assert abs(np.linalg.norm(C) - 1.0) < 1e-12
+        a, b, c = rng.uniform(-3, 3, 3)
+        rot = np.einsum("ai,bj,ck,ijk->abc", D(l1, a, b, c, Jd), D(l2, a, b, c, Jd), D(l3, a, b, c, Jd), C)
+        assert np.abs(rot - C).max() < 1e-11
+        assert np.abs(pso3.wigner_3j(l1, l2, l3) - C).max() < 1e-13
+        # cyclic symmetry is what makes get_H o get_net_out the identity
+        assert np.abs(otd.wigner_3j(l2, l3, l1).numpy() - C.transpose(1, 2, 0)).max() < 1e-13
+
+
+@pytest.mark.parametrize("l", [0, 1, 2, 3])
+def test_cg_scalar_coupling_signs(l):
+    """(0,l,l) and (l,l,0) are +delta/sqrt(2l+1): the sign the reference's
+    element_scale_shifts data implies for l=0 labels (negative core s, positive
+    polarisation d on-site means)."""
+    e = np.eye(2 * l + 1) / math.sqrt(2 * l + 1)
+    assert np.abs(otd.wigner_3j(0, l, l).numpy()[0] - e).max() < 1e-14
+    assert np.abs(otd.wigner_3j(l, l, 0).numpy()[:, :, 0] - e).max() < 1e-14
+
+
+BASES = {
+    "mock": {1: [0], 6: [0, 0, 1], 8: [0, 0, 1]},
+    "def2svp_qm7": {9: [0, 0, 0, 1, 1, 2], 8: [0, 0, 0, 1, 1, 2], 7: [0, 0, 0, 1, 1, 2], 6: [0, 0, 0, 1, 1, 2], 1: [0, 0, 1]},
+    "cfg3": {1: [0, 0, 1], 6: [0, 0, 0, 1, 1, 2], 7: [0, 0, 0, 1, 1, 2], 8: [0, 0, 0, 1, 1, 2]},
+    "sio2_dzvp": {14: [0, 0, 1, 1, 2], 8: [0, 0, 1, 1, 2]},
+    "nabla": {35: [0, 0, 0, 0, 0, 1, 1, 1, 1, 2, 2, 2], 17: [0, 0, 0, 0, 1, 1, 1, 2], 16: [0, 0, 0, 0, 1, 1, 1, 2],
+              9: [0, 0, 0, 1, 1, 2], 8: [0, 0, 0, 1, 1, 2], 1: [0, 0, 1]},
+    "diffuse": {1: [0, 0, 0, 1, 1], 6: [0, 0, 0, 0, 0, 1, 1, 1, 2, 2, 3, 0, 2]},
+}
+
+
+@pytest.mark.parametrize("name", list(BASES))
+def test_basis_tables_match_oracle(name):
+    b1, b2 = copy.deepcopy(BASES[name]), copy.deepcopy(BASES[name])
+    t_o, ls_o, js_o, sl_o, full_o = otd.make_output_irreps(b1)
+    eb_o = otd.process_targets(b1, t_o, full_o)
+    tm_o = otd.get_orbital_template(eb_o, sl_o)
+    t_p, req_p, simp_p, ls_p, js_p, sl_p, full_p = ptd.make_output_irreps(b2)
+    eb_p = ptd.process_targets(b2, t_p, ls_p, js_p, full_p)
+    tm_p = ptd.get_orbital_template(eb_p, sl_p)
+    assert ls_p == ls_o and js_p == js_o and full_p == full_o
+    assert [int(x) for x in sl_p] == [int(x) for x in sl_o]
+    assert eb_p == eb_o
+    assert tm_p == tm_o
+    # closed form: T = (sum_l (2l+1))^2 over ls_list
+    T = sum(2 * (l % 10) + 1 for l in ls_p) ** 2
+    assert int(sl_p[-1]) == T == req_p.dim
+    assert sum(len(t) for t in tm_p) == sum(len(e) for e in eb_p)
+
+
+def test_config3_sizes():
+    t = ptd.BasisTables(BASES["cfg3"])
+    assert t.ls_list == [0, 0, 0, 1, 1, 2] and len(t.out_js_list) == 36
+    assert t.orbital_starts[-1] == 196
+    assert sum(((2 * a + 1) * (2 * b + 1)) ** 2 for a, b in t.out_js_list) == 2116
+    assert ptd.BasisTables(BASES["sio2_dzvp"]).orbital_starts[-1] == 169
+
+
+@pytest.mark.parametrize("if_sort", [False, True])
+@pytest.mark.parametrize("name", ["mock", "cfg3", "diffuse"])
+def test_e3tensordecomp_tables_and_round_trip(name, if_sort):
+    b = copy.deepcopy(BASES[name])
+    _, req, simp, ls, js, sl, full = ptd.make_output_irreps(b)
+    o = otd.E3TensorDecomp(js, if_sort=if_sort)
+    p = ptd.e3TensorDecomp(simp if if_sort else req, js, torch.float64, if_sort=if_sort)
+    assert p.in_slices == o.in_slices and p.H_slices == o.H_slices
+    assert torch.abs(p.W_global - o.W_global).max() < 1e-13
+    assert torch.abs(p.W_global_inv - o.W_global_inv).max() < 1e-13
+    if if_sort:
+        assert np.array_equal(p.sort_perm, o.sort_perm.numpy())
+        assert [ir.l for _, ir in p.required_irreps_out] == sorted(set(o.irreps_ls))
+    g = torch.Generator().manual_seed(0)
+    H = torch.randn(17, o.H_slices[-1], generator=g)
+    x = o.get_net_out(H)
+    assert torch.abs(o.get_H(x) - H).max() < 1e-12
+    assert torch.abs(p.get_net_out(H) - x).max() < 1e-12
+
+
+def test_reference_mock_get_H_matches_dense_assembly():
+    """Mirror of tests/test_basis_transform_triton_backend.py:11-54 on the CPU oracle."""
+    b = copy.deepcopy(BASES["mock"])
+    _, req, simp, ls, js, sl, full = ptd.make_output_irreps(b)
+    o = otd.E3TensorDecomp(js, if_sort=True)
+    x = torch.randn(256, o.in_slices[-1], generator=torch.Generator().manual_seed(1))
+    rows = sum(w.shape[2] for w in o.wms)
+    cols = [w.shape[0] * w.shape[1] for w in o.wms]
+    W = torch.zeros(sum(cols), rows)
+    oc = 0
+    for i in range(len(js)):
+        s = slice(o.in_slices[i], o.in_slices[i + 1])
+        W[oc:oc + cols[i], s] = o.wms[i].reshape(-1, s.stop - s.start)
+        oc += cols[i]
+    ref = o.sort_inverse(x) @ W.T
+    assert torch.allclose(o.get_H(x), ref, atol=1e-12)
+
+
+# -------------------------------------------------------- matrix2labels
+def test_matrix2label_round_trip_is_identity_on_covered_entries():
+    from maloq_amd.synth import dense_hamiltonian, atom_pair_rows, radius_graph
+    t = ptd.BasisTables(BASES["cfg3"])
+    rng = np.random.default_rng(3)
+    Z = rng.choice([1, 6, 7, 8], size=7)
+    pos = rng.uniform(0, 4, (7, 3))
+    H, off = dense_hamiltonian(Z, pos, t.orbitals_per_atom(Z), seed=4)
+    src, dst, _ = radius_graph(pos, 3.0)
+    rows, cols = atom_pair_rows(src, dst, len(Z))
+    target = np.zeros((len(rows), 196), np.float32)
+    om2l.single_matrix2label(t.orbital_template, off, Z, rows, cols, H, target, True)
+    H2 = np.zeros_like(H)
+    om2l.single_matrix2label(t.orbital_template, off, Z, rows, cols, H2, target, False)
+    covered = H2 != 0
+    assert np.array_equal(H2[covered], H[covered])
+    # every covered entry is one of the listed atom-pair blocks
+    mask = np.zeros_like(H, dtype=bool)
+    for i, j in zip(rows, cols):
+        mask[off[i]:off[i + 1], off[j]:off[j + 1]] = True
+    assert np.all(mask[covered])
+    assert np.array_equal(H2[mask], H[mask])
+
+
+# ------------------------------------------------------------ message block
+def _conv_params(lmax, mmax, c_in, c_out, gen, extra=0, bias=True):
+    m_size = [lmax - m + 1 for m in range(mmax + 1)]
+    k0 = m_size[0] * c_in
+    w0 = torch.randn(m_size[0] * c_out + extra, k0, generator=gen) / math.sqrt(k0)
+    b0 = torch.randn(m_size[0] * c_out + extra, generator=gen) * 0.1 if bias else None
+    wm = []
+    for m in range(1, mmax + 1):
+        k = m_size[m] * c_in
+        wm.append(torch.randn(2 * m_size[m] * c_out, k, generator=gen) / math.sqrt(k) / math.sqrt(2))
+    return {"w0": w0, "b0": b0, "wm": wm, "c_out": c_out}
+
+
+def _random_graph(n, e, gen):
+    src = torch.randint(0, n, (e,), generator=gen)
+    dst = torch.randint(0, n, (e,), generator=gen)
+    return torch.stack([src, dst])
+
+
+@pytest.mark.parametrize("lmax,mmax,gate", [(2, 2, False), (4, 2, False), (4, 2, True), (3, 1, True)])
+def test_message_block_is_gamma_invariant(lmax, mmax, gate, Jd):
+    g = torch.Generator().manual_seed(lmax * 7 + mmax)
+    N, E, C = 6, 20, 4
+    x = torch.randn(N, (lmax + 1) ** 2, C, generator=g)
+    ei = _random_graph(N, E, g)
+    vec = torch.randn(E, 3, generator=g)
+    conv = _conv_params(lmax, mmax, C, C, g, extra=lmax * C if gate else 0)
+    ksum = C * sum(lmax - m + 1 for m in range(mmax + 1)) + C * sum(lmax - m + 1 for m in range(1, mmax + 1))
+    rad = torch.rand(E, ksum, generator=g) + 0.5
+    outs = []
+    for s in range(3):
+        u = torch.rand(E, generator=torch.Generator().manual_seed(100 + s))
+        eul = orot.init_edge_rot_euler_angles(vec, u)
+        outs.append(omsg.message_block(x, ei, eul, Jd, lmax, mmax, conv, rad=rad, gate=gate))
+    assert torch.allclose(outs[0], outs[1], atol=1e-11)
+    assert torch.allclose(outs[0], outs[2], atol=1e-11)
+
+
+def test_message_block_global_equivariance_config1(Jd):
+    """Config 1 of the benchmark: rotate positions by R and node features by D(R):
+    the block's output rotates by D(R)."""
+    from maloq_amd.synth import config1_graph
+    gph = config1_graph()
+    lmax = mmax = 2
+    C = 32
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(gph.num_nodes, 9, C, generator=g)
+    ei = torch.from_numpy(np.stack([gph.src, gph.dst]))
+    conv = _conv_params(lmax, mmax, C, C, g)
+    vec = torch.from_numpy(gph.edge_distance_vec())
+    a, b, c = 0.3, 1.1, -0.7
+    R = torch.from_numpy(Ry(a) @ Rx(b) @ Ry(c))
+    Dfull = torch.block_diag(*[torch.from_numpy(D(l, a, b, c, Jd)) for l in range(lmax + 1)])
+    u = torch.rand(len(vec), generator=g)
+    out = omsg.message_block(x, ei, orot.init_edge_rot_euler_angles(vec, u), Jd, lmax, mmax, conv)
+    out_r = omsg.message_block(torch.einsum("ij,njc->nic", Dfull, x), ei,
+                               orot.init_edge_rot_euler_angles(vec @ R.T, u), Jd, lmax, mmax, conv)
+    assert torch.allclose(out_r, torch.einsum("ij,njc->nic", Dfull, out), atol=1e-10)
+
+
+def test_so2_convolution_brute_force():
+    """Per-element loops against the vectorised oracle, tiny sizes."""
+    lmax, mmax, C = 2, 2, 2
+    g = torch.Generator().manual_seed(5)
+    conv = _conv_params(lmax, mmax, C, C, g)
+    E = 3
+    x = torch.randn(E, 9, C, generator=g)
+    rad = torch.rand(E, 3 * C + 2 * C + 1 * C, generator=g)
+    got = oso2.so2_convolution(x, rad, conv["w0"], conv["b0"], conv["wm"], [3, 2, 1], C)
+    ref = torch.zeros_like(got)
+    for e in range(E):
+        # m = 0: rows 0..2, flattened (l, c)
+        v = [x[e, l, c] * rad[e, l * C + c] for l in range(3) for c in range(C)]
+        for o in range(3 * C):
+            ref[e, o // C, o % C] = sum(conv["w0"][o, k] * v[k] for k in range(3 * C)) + conv["b0"][o]
+        off_r, row = 3 * C, 3
+        for m in (1, 2):
+            ms = 3 - m
+            W = conv["wm"][m - 1]
+            half = ms * C
+            xp = [x[e, row + i // C, i % C] * rad[e, off_r + i] for i in range(ms * C)]
+            xm = [x[e, row + ms + i // C, i % C] * rad[e, off_r + i] for i in range(ms * C)]
+            for o in range(half):
+                Ar = sum(W[o, k] * xp[k] for k in range(ms * C))
+                Ai = sum(W[half + o, k] * xp[k] for k in range(ms * C))
+                Br = sum(W[o, k] * xm[k] for k in range(ms * C))
+                Bi = sum(W[half + o, k] * xm[k] for k in range(ms * C))
+                ref[e, row + o // C, o % C] = Ar - Bi
+                ref[e, row + ms + o // C, o % C] = Br + Ai
+            row += 2 * ms
+            off_r += ms * C
+    assert torch.allclose(got, ref, atol=1e-12)
