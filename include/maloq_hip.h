@@ -114,6 +114,67 @@ int maloq_matrix2label(float* fock, int64_t ld, const int64_t* data_offsets,
                        const int32_t* tmpl_ptr, const int32_t* tmpl, float* target,
                        int64_t target_ld, int forward, void* stream);
 
+/* -------------------------------------------------- fused message block -- */
+
+/* Floats of the partial-segment buffer the message entry points need. */
+int64_t maloq_message_partials_floats(int lmax, int gate, int64_t num_edges, int c_out);
+
+/* Bytes of the packed weight fragments for a (dtype, lmax, mmax, gate,
+ * kernel-input channels c_k, kernel-output channels c_n); -1 if unsupported. */
+int64_t maloq_message_wpack_bytes(int dtype, int lmax, int mmax, int gate, int c_k, int c_n);
+
+/* Fused message block, forward:
+ *   out[n] = sum_{e: dst[e]=n} D_e^T SO2(D_e x[src[e]] (*) rad[e]) [gate],
+ * with D_e the kept rows |m| <= mmax of the Wigner-D of eulers[e].
+ * Edges must be sorted by dst (non-decreasing).  edge_idx (nullable) maps the
+ * kernel's edge order to rows of eulers / rad.  x [N_src, d, c_in] (fp32 or
+ * bf16 per dtype), rad [E, sum_m (lmax-m+1) c_in] (nullable), wpack from the
+ * host packer, bias [gate ? lmax*c_out + (lmax+1)*c_out : (lmax+1)*c_out]
+ * fp32 (nullable), out [num_nodes, d, c_out] fp32, seg_ptr [num_nodes+1] CSR
+ * of dst, partials of maloq_message_partials_floats floats.  save_y (nullable)
+ * receives the rotated, radially scaled input rows [E, d', c_in] in m-major
+ * order (the SO(2) layer's input, kept for the weight gradient).
+ * Replaces Edgewise.forward_node, helm/esen_block.py:146-208 (bmm(wigner),
+ * einsum(to_m), SO2_Convolution helm/nn/so2_layers.py:139-214, GateActivation
+ * helm/nn/activation.py:57-77, bmm(wigner_inv), index_add_). */
+int maloq_message_fwd(int dtype, int lmax, int mmax, int gate, const void* x, int c_in,
+                      const int32_t* src, const int32_t* dst, const int32_t* edge_idx,
+                      int64_t num_edges, const float* eulers, const void* rad, const void* wpack,
+                      const float* bias, const float* jd, float* out, int64_t num_nodes, int c_out,
+                      const int64_t* seg_ptr, float* partials, void* save_y, void* stream);
+
+/* Input and radial-scale gradients of the (ungated) fused block:
+ *   grad_x[n] = sum_{e: src[e]=n} D_e^T rad[e] (*) SO2^T(D_e grad_out[dst[e]]),
+ *   grad_rad[e] = SO2^T(D_e grad_out[dst[e]]) (*) (D_e x[src[e]]).
+ * Edges in src-sorted order: src_sorted non-decreasing, dst_by_src the
+ * matching dst, edge_idx the row of eulers / rad / grad_rad (the forward's
+ * edge order).  wpack_t: weights packed for the transposed GEMM.  save_dz
+ * (nullable) receives the rotated output-gradient rows [E, d', c_out] (m-major,
+ * indexed by edge_idx) for the weight gradient.
+ * Replaces the autograd backward of Edgewise.forward_node (esen_block.py:146-208). */
+int maloq_message_bwd_dx(int dtype, int lmax, int mmax, const float* grad_out, int c_out,
+                         const int32_t* dst_by_src, const int32_t* src_sorted,
+                         const int32_t* edge_idx, int64_t num_edges, const float* eulers,
+                         const void* rad, void* grad_rad, const void* x, const void* wpack_t,
+                         const float* jd, float* grad_x, int64_t num_nodes, int c_in,
+                         const int64_t* seg_ptr_src, float* partials, void* save_dz, void* stream);
+
+/* Floats of the split-K partials buffer of maloq_message_dw. */
+int64_t maloq_message_dw_partials_floats(int lmax, int mmax, int c_out, int c_in, int splits);
+
+/* Weight gradients of the SO(2) linear from the saved rows:
+ *   dW_0 = sum_e dZ_0(e)^T Y_0(e);  for m >= 1 with C_m = sum_e dZ_m^T Y_m over
+ *   the stacked (+m, -m) rows: dWr = C[+,+] + C[-,-], dWi = C[-,+] - C[+,-],
+ *   dW_m = [dWr; dWi] in the layout of so2_m_conv[m-1].fc.weight.
+ * dz [E, d', c_out], y [E, d', c_in] (dtype), dw0 [(lmax+1) c_out, (lmax+1) c_in],
+ * dw_m [2 (lmax-m+1) c_out, (lmax-m+1) c_in] fp32.  Split-K over edges,
+ * partials summed in split order (deterministic).
+ * Replaces the autograd weight gradient of SO2_Convolution
+ * (helm/nn/so2_layers.py:139-214, SO2_m_Conv :61-67). */
+int maloq_message_dw(int dtype, int lmax, int mmax, const void* dz, const void* y,
+                     int64_t num_edges, int c_out, int c_in, int splits, float* partials,
+                     float* dw0, float* dw1, float* dw2, float* dw3, void* stream);
+
 /* ------------------------------------------------------- segment scatter -- */
 
 /* out[n, :] = sum_{p in [seg_ptr[n], seg_ptr[n+1])} msg[perm ? perm[p] : p, :],

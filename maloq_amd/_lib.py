@@ -34,6 +34,20 @@ SIGNATURES = {
                              _i32, _p, _p, _p, _p, _p, _p, _p],
     "maloq_matrix2label": [_p, _i64, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _i64, _i32, _p],
     "maloq_segment_sum": [_p, _p, _p, _i64, _i64, _p, _p],
+    "maloq_message_partials_floats": [_i32, _i32, _i64, _i32],
+    "maloq_message_wpack_bytes": [_i32, _i32, _i32, _i32, _i32, _i32],
+    "maloq_message_fwd": [_i32, _i32, _i32, _i32, _p, _i32, _p, _p, _p, _i64, _p, _p, _p, _p, _p,
+                          _p, _i64, _i32, _p, _p, _p, _p],
+    "maloq_message_bwd_dx": [_i32, _i32, _i32, _p, _i32, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p,
+                             _p, _i64, _i32, _p, _p, _p, _p],
+    "maloq_message_dw_partials_floats": [_i32, _i32, _i32, _i32, _i32],
+    "maloq_message_dw": [_i32, _i32, _i32, _p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p],
+}
+RESTYPES = {
+    "maloq_last_error": ctypes.c_char_p,
+    "maloq_message_partials_floats": ctypes.c_int64,
+    "maloq_message_wpack_bytes": ctypes.c_int64,
+    "maloq_message_dw_partials_floats": ctypes.c_int64,
 }
 
 _lib = None
@@ -57,7 +71,7 @@ def load():
     for name, argtypes in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = argtypes
-        fn.restype = ctypes.c_char_p if name == "maloq_last_error" else ctypes.c_int
+        fn.restype = RESTYPES.get(name, ctypes.c_int)
     _lib = lib
     return lib
 

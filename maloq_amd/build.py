@@ -29,8 +29,16 @@ FLAGS = [
 ]
 
 
-def _compile(src: str) -> str:
+def _deps_mtime(src: str) -> float:
+    """Newest mtime among the source and the headers of csrc/ (coarse but safe)."""
+    hdrs = glob.glob(os.path.join(CSRC, "*.h")) + glob.glob(os.path.join(HERE, "..", "include", "*.h"))
+    return max([os.path.getmtime(src)] + [os.path.getmtime(h) for h in hdrs])
+
+
+def _compile(src: str, incremental: bool = False) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
+    if incremental and os.path.exists(obj) and os.path.getmtime(obj) >= _deps_mtime(src):
+        return obj
     cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -38,11 +46,13 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = True) -> str:
+def build(verbose: bool = True, incremental: bool = False) -> str:
+    """Compile every HIP source (``incremental`` reuses objects newer than their
+    inputs; the default always recompiles)."""
     os.makedirs(BUILD_DIR, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
+        objs = list(ex.map(lambda s: _compile(s, incremental), srcs))
     tmp = OUT + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -55,5 +65,5 @@ def build(verbose: bool = True) -> str:
 
 
 if __name__ == "__main__":
-    build()
+    build(incremental="--incremental" in sys.argv)
     sys.exit(0)

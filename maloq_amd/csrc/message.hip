@@ -1,0 +1,154 @@
+// C ABI of the fused message block (forward and input gradient) and the
+// partial-segment fixup.  The kernels themselves are in message_impl.h and
+// are instantiated per lmax in message_l{2,4,6}.hip.
+#include "message_launch.h"
+#include "../../include/maloq_hip.h"
+
+namespace maloq {
+namespace msg {
+
+// Node outputs of segments cut by tile boundaries (summed in tile order) and
+// of empty segments (zero).  seg_ptr: CSR of the segment ids over edges.
+__global__ void message_fixup_kernel(const int64_t* __restrict__ seg_ptr, int64_t nseg,
+                                     const float* __restrict__ part, float* __restrict__ out,
+                                     int64_t row_elems, int TE) {
+  const int64_t node = blockIdx.y;
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (node >= nseg || c >= row_elems) return;
+  const int64_t s0 = seg_ptr[node], s1 = seg_ptr[node + 1];
+  float* o = out + node * row_elems + c;
+  if (s1 == s0) {
+    *o = 0.f;
+    return;
+  }
+  const int64_t t0 = s0 / TE, t1 = (s1 - 1) / TE;
+  if (t0 == t1) return;  // written by the main kernel
+  float sum = part[((t0 * 2) + ((s0 == t0 * TE) ? 0 : 1)) * row_elems + c];
+  for (int64_t t = t0 + 1; t <= t1; ++t) sum += part[(t * 2) * row_elems + c];
+  *o = sum;
+}
+
+static int64_t frags_per_cb(int lmax, int mmax, int gate, int c_k, int kc) {
+  int64_t total = 0;
+  for (int l = 0; l <= lmax; ++l) {
+    int nb = (lmax + 1) + (gate ? lmax : 0);
+    for (int m = 1; m <= (mmax < l ? mmax : l); ++m) nb += 4 * (lmax - m + 1);
+    total += static_cast<int64_t>(nb) * (c_k / kc);
+  }
+  return total;
+}
+
+static int fixup(const int64_t* seg_ptr, int64_t nseg, const float* part, float* out,
+                 int64_t row_elems, int TE, hipStream_t s) {
+  if (nseg == 0) return MALOQ_OK;
+  const unsigned gx = static_cast<unsigned>((row_elems + 255) / 256);
+  for (int64_t s0 = 0; s0 < nseg; s0 += 65535) {
+    const int64_t ns = (nseg - s0) < 65535 ? (nseg - s0) : 65535;
+    hipLaunchKernelGGL(message_fixup_kernel, dim3(gx, static_cast<unsigned>(ns)), dim3(256), 0, s,
+                       seg_ptr + s0, ns, part, out + s0 * row_elems, row_elems, TE);
+    int rc = check_launch("message_fixup_kernel");
+    if (rc) return rc;
+  }
+  return MALOQ_OK;
+}
+
+static int dispatch(int lmax, int mmax, int dtype, int gate, int mode, const Args& a,
+                    hipStream_t s) {
+  switch (lmax) {
+    case 2: return launch_l2(mmax, dtype, gate, mode, a, s);
+    case 4: return launch_l4(mmax, dtype, gate, mode, a, s);
+    case 6: return launch_l6(mmax, dtype, gate, mode, a, s);
+    default: break;
+  }
+  MALOQ_REQUIRE(false, "unsupported lmax %d (built: 2, 4, 6 with mmax 2)", lmax);
+}
+
+static int check_common(int dtype, int lmax, int mmax, int c_k, int c_n, int64_t E) {
+  MALOQ_REQUIRE(dtype == 0 || dtype == 1, "dtype must be 0 (fp32) or 1 (bf16)");
+  MALOQ_REQUIRE(lmax >= 0 && mmax >= 0 && mmax <= lmax, "bad lmax/mmax");
+  const int kc = dtype == 1 ? BF16::KC : F32::KC;
+  MALOQ_REQUIRE(c_k > 0 && c_k % kc == 0, "input channels must be a positive multiple of %d", kc);
+  MALOQ_REQUIRE(c_n > 0 && c_n % CB == 0, "output channels must be a positive multiple of %d", CB);
+  MALOQ_REQUIRE(E >= 0 && E < (int64_t(1) << 31), "edge count out of range");
+  return MALOQ_OK;
+}
+
+}  // namespace msg
+}  // namespace maloq
+
+using namespace maloq;
+using namespace maloq::msg;
+
+extern "C" int64_t maloq_message_partials_floats(int lmax, int gate, int64_t num_edges, int c_out) {
+  const int64_t d = static_cast<int64_t>(lmax + 1) * (lmax + 1);
+  const int64_t ntiles = (num_edges + tile_edges(lmax, gate) - 1) / tile_edges(lmax, gate);
+  return ntiles * 2 * d * c_out;
+}
+
+extern "C" int64_t maloq_message_wpack_bytes(int dtype, int lmax, int mmax, int gate, int c_k,
+                                             int c_n) {
+  const int kc = dtype == 1 ? BF16::KC : F32::KC;
+  if (c_k % kc != 0 || c_n % CB != 0) return -1;
+  return frags_per_cb(lmax, mmax, gate, c_k, kc) * (c_n / CB) * FRAG;
+}
+
+extern "C" int maloq_message_fwd(int dtype, int lmax, int mmax, int gate, const void* x, int c_in,
+                                 const int32_t* src, const int32_t* dst, const int32_t* edge_idx,
+                                 int64_t num_edges, const float* eulers, const void* rad,
+                                 const void* wpack, const float* bias, const float* jd,
+                                 float* out, int64_t num_nodes, int c_out, const int64_t* seg_ptr,
+                                 float* partials, void* save_y, void* stream) {
+  int rc = check_common(dtype, lmax, mmax, c_in, c_out, num_edges);
+  if (rc) return rc;
+  MALOQ_REQUIRE(num_nodes >= 0, "num_nodes < 0");
+  MALOQ_REQUIRE(out && seg_ptr && jd && wpack, "null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t d = static_cast<int64_t>(lmax + 1) * (lmax + 1);
+  if (num_edges > 0) {
+    MALOQ_REQUIRE(x && src && dst && eulers && partials, "null pointer");
+    Args a{};
+    a.x = x; a.gidx = src; a.seg = dst; a.eidx = edge_idx; a.eulers = eulers; a.rad = rad;
+    a.wpack = static_cast<const char*>(wpack); a.bias = bias; a.jd = jd; a.out = out;
+    a.save_a = save_y;
+    a.part = partials; a.E = num_edges; a.C_k = c_in; a.C_n = c_out; a.n_cb = c_out / CB;
+    a.extra = gate ? lmax * c_out : 0; a.ntiles = (num_edges + tile_edges(lmax, gate) - 1) / tile_edges(lmax, gate);
+    const int kc = dtype == 1 ? BF16::KC : F32::KC;
+    a.frags_per_cb = frags_per_cb(lmax, mmax, gate, c_in, kc);
+    rc = dispatch(lmax, mmax, dtype, gate, FWD, a, s);
+    if (rc) return rc;
+  }
+  return fixup(seg_ptr, num_nodes, partials, out, d * c_out, tile_edges(lmax, gate), s);
+}
+
+extern "C" int maloq_message_bwd_dx(int dtype, int lmax, int mmax, const float* grad_out,
+                                    int c_out, const int32_t* dst_by_src,
+                                    const int32_t* src_sorted, const int32_t* edge_idx,
+                                    int64_t num_edges, const float* eulers, const void* rad,
+                                    void* grad_rad, const void* x, const void* wpack_t,
+                                    const float* jd, float* grad_x, int64_t num_nodes, int c_in,
+                                    const int64_t* seg_ptr_src, float* partials, void* save_dz,
+                                    void* stream) {
+  // kernel input channels = c_out (gradient side), output channels = c_in
+  int rc = check_common(dtype, lmax, mmax, c_out, c_in, num_edges);
+  if (rc) return rc;
+  MALOQ_REQUIRE(grad_x && seg_ptr_src && jd && wpack_t, "null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t d = static_cast<int64_t>(lmax + 1) * (lmax + 1);
+  if (num_edges > 0) {
+    MALOQ_REQUIRE(grad_out && dst_by_src && src_sorted && eulers && partials && edge_idx,
+                  "null pointer");
+    MALOQ_REQUIRE(rad == nullptr || x != nullptr, "x is needed for the radial gradient");
+    Args a{};
+    a.x = grad_out; a.gidx = dst_by_src; a.seg = src_sorted; a.eidx = edge_idx;
+    a.eulers = eulers; a.rad = rad; a.drad = grad_rad; a.xsrc = x; a.xsrc_idx = src_sorted;
+    a.wpack = static_cast<const char*>(wpack_t); a.bias = nullptr; a.jd = jd; a.out = grad_x;
+    a.save_a = save_dz;
+    a.part = partials; a.E = num_edges; a.C_k = c_out; a.C_n = c_in; a.n_cb = c_in / CB;
+    a.extra = 0; a.ntiles = (num_edges + tile_edges(lmax, 0) - 1) / tile_edges(lmax, 0);
+    const int kc = dtype == 1 ? BF16::KC : F32::KC;
+    a.frags_per_cb = frags_per_cb(lmax, mmax, 0, c_out, kc);
+    rc = dispatch(lmax, mmax, dtype, 0, BWD_DX, a, s);
+    if (rc) return rc;
+  }
+  return fixup(seg_ptr_src, num_nodes, partials, grad_x, d * c_in, tile_edges(lmax, 0), s);
+}

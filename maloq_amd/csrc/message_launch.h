@@ -1,0 +1,53 @@
+#pragma once
+// Host-side launch helpers shared by the per-lmax instantiation files.
+#include "message_impl.h"
+
+namespace maloq {
+namespace msg {
+
+// Waves per workgroup and 32-edge row tiles per workgroup for each lmax.
+// (lmax <= 4, no gate): 4 waves x 64 edges; gated or lmax > 4: 32-edge tiles
+// (4 or 8 waves) so the accumulators of a wave stay within 256 registers.
+template <int L, bool GATE>
+struct Cfg {
+  static constexpr int NW = (L <= 4) ? 4 : 8;
+  static constexpr int RT = (L <= 4 && !GATE) ? 2 : 1;
+};
+
+inline int tile_edges(int lmax, int gate) { return (lmax <= 4 && !gate) ? 64 : 32; }
+
+template <int L, int M, bool GATE, class TM, class TX, int MODE>
+int launch(const Args& a, hipStream_t s) {
+  constexpr int NW = Cfg<L, GATE>::NW, RT = Cfg<L, GATE>::RT;
+  using P = Plan<L, M, GATE, NW, RT>;
+  // Must match the workgroup -> (tile, channel block) mapping of Kernel::run.
+  int64_t grid = a.ntiles * a.n_cb;
+  if (a.n_cb > 1 && (8 % a.n_cb) == 0) {
+    const int per = 8 / a.n_cb;
+    grid = ((a.ntiles + per - 1) / per) * 8;
+  }
+  MALOQ_REQUIRE(grid < (int64_t(1) << 31), "grid too large");
+  hipLaunchKernelGGL((message_kernel<L, M, GATE, NW, RT, TM, TX, MODE>),
+                     dim3(static_cast<unsigned>(grid)), dim3(P::NT), 0, s, a);
+  return check_launch("message_kernel");
+}
+
+// dtype: 0 fp32, 1 bf16; mode: FWD or BWD_DX.
+template <int L, int M>
+int launch_lm(int dtype, int gate, int mode, const Args& a, hipStream_t s) {
+  if (mode == FWD) {
+    if (dtype == 1)
+      return gate ? launch<L, M, true, BF16, BF16, FWD>(a, s) : launch<L, M, false, BF16, BF16, FWD>(a, s);
+    return gate ? launch<L, M, true, F32, F32, FWD>(a, s) : launch<L, M, false, F32, F32, FWD>(a, s);
+  }
+  MALOQ_REQUIRE(!gate, "gated backward is not implemented");
+  if (dtype == 1) return launch<L, M, false, BF16, F32, BWD_DX>(a, s);
+  return launch<L, M, false, F32, F32, BWD_DX>(a, s);
+}
+
+int launch_l2(int mmax, int dtype, int gate, int mode, const Args& a, hipStream_t s);
+int launch_l4(int mmax, int dtype, int gate, int mode, const Args& a, hipStream_t s);
+int launch_l6(int mmax, int dtype, int gate, int mode, const Args& a, hipStream_t s);
+
+}  // namespace msg
+}  // namespace maloq

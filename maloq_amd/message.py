@@ -1,0 +1,310 @@
+"""Fused equivariant message block on the HIP kernels (forward + gradients).
+
+Host side of ``maloq_message_fwd`` / ``maloq_message_bwd_dx`` (include/maloq_hip.h):
+
+* ``MessagePlan``      dst-sorted edge order, CSR pointers and the src-sorted
+                       order of the backward, built once per graph.
+* ``pack_weights``     the SO(2) weights (reference layout of SO2_Convolution:
+                       ``fc_m0.weight`` [N0, K0], ``so2_m_conv[m-1].fc.weight``
+                       [2 half_m, K_m], so2_layers.py:106-130) gathered into the
+                       kernel's MFMA fragment order with the complex +-m mix
+                       folded in ([[Wr, Wi], [-Wi, Wr]]).
+* ``message_block``    autograd function: node output of
+                       rotate -> [radial scale] -> SO(2) -> [bias, gate] ->
+                       inverse rotate -> segment sum (Edgewise.forward_node,
+                       esen_block.py:146-208), with input, radial-scale, weight
+                       and bias gradients.
+
+Edge inputs (Euler triples, radial scales) are expected in the plan's
+dst-sorted order (``plan.sort_edges``).
+"""
+from __future__ import annotations
+
+import functools
+
+import numpy as np
+import torch
+
+from . import _lib
+from .so3 import jd_matrices, pack_jd
+
+FRAG_ELEMS = {torch.bfloat16: 512, torch.float32: 256}
+KC = {torch.bfloat16: 16, torch.float32: 8}
+CB = 32
+DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1}
+
+
+def _csr(keys: torch.Tensor, n: int) -> torch.Tensor:
+    counts = torch.bincount(keys, minlength=n)
+    return torch.cat([torch.zeros(1, dtype=torch.int64, device=keys.device), torch.cumsum(counts, 0)])
+
+
+class MessagePlan:
+    """Edge orderings of one graph for the fused kernels.
+
+    ``perm[p]`` is the original edge id of dst-sorted position p (stable:
+    ties keep the original order).  The backward visits the same edges sorted
+    by source: ``bwd_eidx[q]`` is the dst-sorted position of its q-th edge.
+    """
+
+    def __init__(self, edge_index: torch.Tensor, num_nodes: int):
+        src, dst = edge_index[0].long(), edge_index[1].long()
+        self.num_nodes = int(num_nodes)
+        self.num_edges = int(src.shape[0])
+        self.device = src.device
+        self.perm = torch.sort(dst, stable=True).indices
+        src_s, dst_s = src[self.perm], dst[self.perm]
+        self.src = src_s.int().contiguous()
+        self.dst = dst_s.int().contiguous()
+        self.seg_ptr = _csr(dst_s, self.num_nodes)
+        q = torch.sort(src_s, stable=True).indices
+        self.bwd_eidx = q.int().contiguous()
+        self.bwd_src = src_s[q].int().contiguous()
+        self.bwd_dst = dst_s[q].int().contiguous()
+        self.seg_ptr_src = _csr(src_s, self.num_nodes)
+
+    def sort_edges(self, t: torch.Tensor) -> torch.Tensor:
+        return t[self.perm].contiguous()
+
+
+# ------------------------------------------------------------ weight packing
+def _frag_list(lmax, mmax, gate, l_k):
+    """Canonical B-fragment order of one K step at kernel-input degree l_k."""
+    out = [("g0", 0, 0, l) for l in range(lmax + 1)]
+    if gate:
+        out += [("gate", 0, 0, l) for l in range(1, lmax + 1)]
+    for m in range(1, min(mmax, l_k) + 1):
+        for kf in (0, 1):
+            for pm in (0, 1):
+                out += [(m, kf, pm, l) for l in range(m, lmax + 1)]
+    return out
+
+
+@functools.lru_cache(maxsize=32)
+def _pack_index(dtype_code, lmax, mmax, gate, c_in, c_out, mode):
+    """Gather index and sign, per packed element, into the flat weight vector
+    cat(W0.flatten(), W1.flatten(), ..., [0]).  mode 0: forward GEMM (kernel
+    input = c_in); mode 1: transposed GEMM of the input gradient."""
+    bf16 = dtype_code == 1
+    kc = 16 if bf16 else 8
+    fe = 512 if bf16 else 256
+    extra = lmax * c_out if gate else 0
+    n0 = extra + (lmax + 1) * c_out
+    k0 = (lmax + 1) * c_in
+    offs = [0, n0 * k0]
+    for m in range(1, mmax + 1):
+        offs.append(offs[-1] + 2 * (lmax - m + 1) * c_out * (lmax - m + 1) * c_in)
+    zero = offs[-1]
+    # element (k, col) of a fragment
+    e = np.arange(fe)
+    if bf16:
+        k_of = (e // 256) * 8 + (e % 8)
+        col_of = (e // 8) % 32
+    else:
+        k_of = 2 * (e % 4) + (e // 128)
+        col_of = (e // 4) % 32
+    c_k, c_n = (c_in, c_out) if mode == 0 else (c_out, c_in)
+    idx_parts, sgn_parts = [], []
+    for cb in range(c_n // CB):
+        cn = cb * CB + col_of
+        for l_k in range(lmax + 1):
+            frags = _frag_list(lmax, mmax, gate and mode == 0, l_k)
+            for ks in range(c_k // kc):
+                ck = ks * kc + k_of
+                for g, kf, pm, l_n in frags:
+                    sgn = np.ones(fe, np.int8)
+                    if mode == 0:
+                        c, co, l_in, l_out = ck, cn, l_k, l_n
+                    else:
+                        c, co, l_in, l_out = cn, ck, l_n, l_k
+                    if g == "g0":
+                        idx = offs[0] + (extra + l_out * c_out + co) * k0 + l_in * c_in + c
+                    elif g == "gate":
+                        idx = offs[0] + ((l_out - 1) * c_out + co) * k0 + l_in * c_in + c
+                    else:
+                        m = g
+                        kfw, pmw = (kf, pm) if mode == 0 else (pm, kf)
+                        km = (lmax - m + 1) * c_in
+                        half = (lmax - m + 1) * c_out
+                        ko = (l_out - m) * c_out + co
+                        ki = (l_in - m) * c_in + c
+                        if kfw == pmw:            # Wr
+                            row = ko
+                        else:                     # +/- Wi
+                            row = half + ko
+                            if kfw == 1:          # x- -> y+: -Wi
+                                sgn = -sgn
+                        idx = offs[m] + row * km + ki
+                    idx_parts.append(np.asarray(idx, np.int64))
+                    sgn_parts.append(sgn)
+    return np.concatenate(idx_parts), np.concatenate(sgn_parts), zero
+
+
+_PACK_DEV: dict = {}
+
+
+def pack_weights(w0, wm, lmax, mmax, gate, c_in, c_out, dtype, mode=0):
+    """Packed B fragments (raw bytes on the weights' device) for the kernels."""
+    code = DTYPE_CODE[dtype]
+    key = (code, lmax, mmax, bool(gate), c_in, c_out, mode, str(w0.device))
+    hit = _PACK_DEV.get(key)
+    if hit is None:
+        idx, sgn, zero = _pack_index(code, lmax, mmax, bool(gate), c_in, c_out, mode)
+        hit = (torch.from_numpy(idx).to(w0.device), torch.from_numpy(sgn).to(w0.device), zero)
+        _PACK_DEV[key] = hit
+    idx, sgn, zero = hit
+    with torch.no_grad():
+        flat = torch.cat([w0.reshape(-1)] + [w.reshape(-1) for w in wm[:mmax]] +
+                         [w0.new_zeros(1)]).float()
+        assert flat.numel() == zero + 1, "weight shapes do not match (lmax, mmax, channels)"
+        packed = (flat[idx] * sgn).to(dtype)
+    want = _lib.load().maloq_message_wpack_bytes(code, lmax, mmax, int(bool(gate and mode == 0)),
+                                                c_in if mode == 0 else c_out,
+                                                c_out if mode == 0 else c_in)
+    assert packed.numel() * packed.element_size() == want, (packed.numel(), want)
+    return packed
+
+
+_JD: dict = {}
+
+
+def _jd_dev(lmax, device):
+    key = (lmax, str(device))
+    if key not in _JD:
+        _JD[key] = torch.from_numpy(pack_jd(jd_matrices(lmax), lmax)).to(device)
+    return _JD[key]
+
+
+def rad_width(lmax, mmax, c_in):
+    return sum((lmax - m + 1) * c_in for m in range(mmax + 1))
+
+
+# ---------------------------------------------------------------- raw calls
+def kept_rows(lmax, mmax):
+    return (lmax + 1) + sum(2 * (lmax - m + 1) for m in range(1, mmax + 1))
+
+
+def message_forward(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=False, wpack=None,
+                    save_y=None):
+    """Node output [N, d, c_out] fp32 of the fused block (no autograd).
+    ``save_y`` [E, d', c_in] (x dtype) receives the SO(2) layer's input rows."""
+    dt = x.dtype
+    if dt not in DTYPE_CODE:
+        raise ValueError(f"unsupported dtype {dt}")
+    _lib.require_cuda(x, eulers, w0)
+    N, d, c_in = x.shape
+    assert d == (lmax + 1) ** 2, "x must be [N, (lmax+1)^2, C]"
+    n0 = w0.shape[0]
+    c_out = n0 // (lmax + 1 + (lmax if gate else 0))
+    if wpack is None:
+        wpack = pack_weights(w0, wm, lmax, mmax, gate, c_in, c_out, dt, 0)
+    E = plan.num_edges
+    out = torch.empty(plan.num_nodes, d, c_out, device=x.device, dtype=torch.float32)
+    lib = _lib.load()
+    parts = torch.empty(max(1, lib.maloq_message_partials_floats(lmax, int(gate), E, c_out)),
+                        device=x.device, dtype=torch.float32)
+    if rad is not None:
+        assert rad.shape == (E, rad_width(lmax, mmax, c_in)), "rad must be [E, sum_m (lmax-m+1) C_in]"
+        rad = rad.to(dt).contiguous()
+    bias = b0.float().contiguous() if b0 is not None else None
+    xc = x.contiguous()
+    eul = eulers.float().contiguous()
+    _lib.call("maloq_message_fwd", DTYPE_CODE[dt], lmax, mmax, int(gate), _lib.ptr(xc), c_in,
+              _lib.ptr(plan.src), _lib.ptr(plan.dst), None, E, _lib.ptr(eul), _lib.ptr(rad),
+              _lib.ptr(wpack), _lib.ptr(bias), _lib.ptr(_jd_dev(lmax, x.device)), _lib.ptr(out),
+              plan.num_nodes, c_out, _lib.ptr(plan.seg_ptr), _lib.ptr(parts), _lib.ptr(save_y),
+              _lib.stream_of(x.device))
+    return out
+
+
+def message_backward_dx(grad_out, x, plan, eulers, rad, w0, wm, lmax, mmax, wpack_t=None,
+                        need_rad_grad=True, save_dz=None):
+    """(grad_x fp32 [N, d, c_in], grad_rad [E, KR] or None) of the ungated block.
+    ``save_dz`` [E, d', c_out] (x dtype) receives the rotated output-gradient rows."""
+    dt = x.dtype
+    N, d, c_in = x.shape
+    c_out = grad_out.shape[2]
+    if wpack_t is None:
+        wpack_t = pack_weights(w0, wm, lmax, mmax, False, c_in, c_out, dt, 1)
+    E = plan.num_edges
+    gx = torch.empty(N, d, c_in, device=x.device, dtype=torch.float32)
+    lib = _lib.load()
+    parts = torch.empty(max(1, lib.maloq_message_partials_floats(lmax, 0, E, c_in)),
+                        device=x.device, dtype=torch.float32)
+    grad_rad = None
+    if rad is not None:
+        rad = rad.to(dt).contiguous()
+        if need_rad_grad:
+            grad_rad = torch.empty_like(rad)
+    g = grad_out.float().contiguous()
+    eul = eulers.float().contiguous()
+    xc = x.contiguous()
+    _lib.call("maloq_message_bwd_dx", DTYPE_CODE[dt], lmax, mmax, _lib.ptr(g), c_out,
+              _lib.ptr(plan.bwd_dst), _lib.ptr(plan.bwd_src), _lib.ptr(plan.bwd_eidx), E,
+              _lib.ptr(eul), _lib.ptr(rad), _lib.ptr(grad_rad), _lib.ptr(xc), _lib.ptr(wpack_t),
+              _lib.ptr(_jd_dev(lmax, x.device)), _lib.ptr(gx), N, c_in, _lib.ptr(plan.seg_ptr_src),
+              _lib.ptr(parts), _lib.ptr(save_dz), _lib.stream_of(x.device))
+    return gx, grad_rad
+
+
+def message_weight_grad(dz, y, lmax, mmax, c_out, c_in, splits=None):
+    """(dW0 [(L+1) c_out, (L+1) c_in], [dW_m [2 (L-m+1) c_out, (L-m+1) c_in]], db0)
+    in fp32 from the saved rows (deterministic split-K over edges)."""
+    E = dz.shape[0]
+    if splits is None:
+        splits = max(1, min(16, E // 2048))
+    lib = _lib.load()
+    parts = torch.empty(max(1, lib.maloq_message_dw_partials_floats(lmax, mmax, c_out, c_in, splits)),
+                        device=dz.device, dtype=torch.float32)
+    dw0 = torch.empty((lmax + 1) * c_out, (lmax + 1) * c_in, device=dz.device, dtype=torch.float32)
+    dwm = [torch.empty(2 * (lmax - m + 1) * c_out, (lmax - m + 1) * c_in, device=dz.device,
+                       dtype=torch.float32) for m in range(1, mmax + 1)]
+    ptrs = [_lib.ptr(w) for w in dwm] + [None] * (3 - len(dwm))
+    _lib.call("maloq_message_dw", DTYPE_CODE[dz.dtype], lmax, mmax, _lib.ptr(dz), _lib.ptr(y), E,
+              c_out, c_in, splits, _lib.ptr(parts), _lib.ptr(dw0), ptrs[0], ptrs[1], ptrs[2],
+              _lib.stream_of(dz.device))
+    db0 = dz[:, : lmax + 1, :].float().sum(0).reshape(-1)
+    return dw0, dwm, db0
+
+
+class _MessageBlockFn(torch.autograd.Function):
+    """Autograd wrapper: gradients for x, rad, W0, b0, W_m (ungated block)."""
+
+    @staticmethod
+    def forward(ctx, x, rad, w0, b0, plan, eulers, lmax, mmax, *wm):
+        dt = x.dtype
+        need_w = ctx.needs_input_grad[2] or ctx.needs_input_grad[3] or any(ctx.needs_input_grad[8:])
+        E = plan.num_edges
+        y = torch.empty(E, kept_rows(lmax, mmax), x.shape[2], device=x.device, dtype=dt) if need_w else None
+        out = message_forward(x, plan, eulers, rad, w0, b0, list(wm), lmax, mmax, gate=False, save_y=y)
+        ctx.plan, ctx.lmax, ctx.mmax, ctx.has_b0 = plan, lmax, mmax, b0 is not None
+        ctx.save_for_backward(x, rad, eulers, w0, y, *wm)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        x, rad, eulers, w0, y, *wm = ctx.saved_tensors
+        plan, lmax, mmax = ctx.plan, ctx.lmax, ctx.mmax
+        need_w = y is not None
+        dz = torch.empty(plan.num_edges, kept_rows(lmax, mmax), g.shape[2], device=g.device,
+                         dtype=x.dtype) if need_w else None
+        gx, grad_rad = message_backward_dx(g, x, plan, eulers, rad, w0, wm, lmax, mmax,
+                                           need_rad_grad=ctx.needs_input_grad[1], save_dz=dz)
+        dw0 = db0 = None
+        dwm = [None] * len(wm)
+        if need_w:
+            dw0, dwm, db0 = message_weight_grad(dz, y, lmax, mmax, g.shape[2], x.shape[2])
+            dw0 = dw0.to(w0.dtype)
+            dwm = [d.to(w.dtype) for d, w in zip(dwm, wm)]
+            db0 = db0 if ctx.has_b0 else None
+        return (gx.to(x.dtype) if ctx.needs_input_grad[0] else None, grad_rad, dw0, db0, None, None,
+                None, None, *dwm)
+
+
+def message_block(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=False):
+    """Differentiable fused block.  Gated blocks are forward-only for now."""
+    if gate:
+        if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in [x, rad, w0, b0, *wm]):
+            raise NotImplementedError("the gated fused block has no backward yet")
+        return message_forward(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=True)
+    return _MessageBlockFn.apply(x, rad, w0, b0, plan, eulers, lmax, mmax, *wm[:mmax])

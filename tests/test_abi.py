@@ -12,7 +12,7 @@ LIB = os.path.join(ROOT, "maloq_amd", "libmaloq_hip.so")
 
 def declared_symbols():
     txt = open(os.path.join(ROOT, "include", "maloq_hip.h")).read()
-    return re.findall(r"^(?:int|const char\*)\s+(maloq_\w+)\(", txt, re.M)
+    return re.findall(r"^(?:int|int64_t|const char\*)\s+(maloq_\w+)\(", txt, re.M)
 
 
 def test_header_declares_symbols():

@@ -1,0 +1,186 @@
+"""GPU parity of the fused message block against the CPU oracle
+(oracle.message.message_block, a restatement of Edgewise.forward_node).
+
+Bars: fp32 within 1e-5 of the output scale (max |ref|); bf16 within 2e-2 of
+the output scale, the oracle being evaluated in fp64 on the bf16-rounded
+inputs, radial scales and weights (the reference path itself is fp32-only).
+Segment sums are checked bitwise for run-to-run determinism.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import message as omsg
+from oracle import rotation as orot
+
+pytestmark = pytest.mark.gpu
+
+
+def _conv(lmax, mmax, c_in, c_out, gen, gate):
+    m_size = [lmax - m + 1 for m in range(mmax + 1)]
+    extra = lmax * c_out if gate else 0
+    k0 = m_size[0] * c_in
+    w0 = torch.randn(m_size[0] * c_out + extra, k0, generator=gen, dtype=torch.float64) / math.sqrt(k0)
+    b0 = torch.randn(m_size[0] * c_out + extra, generator=gen, dtype=torch.float64) * 0.1
+    wm = []
+    for m in range(1, mmax + 1):
+        k = m_size[m] * c_in
+        wm.append(torch.randn(2 * m_size[m] * c_out, k, generator=gen, dtype=torch.float64) / math.sqrt(k) / math.sqrt(2))
+    return {"w0": w0, "b0": b0, "wm": wm, "c_out": c_out}
+
+
+def _graph(N, E, gen, star=False):
+    src = torch.randint(0, N, (E,), generator=gen)
+    dst = torch.randint(0, max(1, N - 3), (E,), generator=gen)   # last nodes: no in-edges
+    if star:
+        dst[: E // 2] = 1                                           # one node with > 64 in-edges
+    return torch.stack([src, dst])
+
+
+def _run(lmax, mmax, dtype, gate, use_rad, N, E, c_in, c_out, seed, device, star=False):
+    from maloq_amd import message as M
+    from maloq_amd.wigner import extract_euler_angles
+    gen = torch.Generator().manual_seed(seed)
+    d = (lmax + 1) ** 2
+    x = torch.randn(N, d, c_in, generator=gen, dtype=torch.float64)
+    ei = _graph(N, E, gen, star)
+    conv = _conv(lmax, mmax, c_in, c_out, gen, gate)
+    kr = M.rad_width(lmax, mmax, c_in)
+    rad = (torch.rand(E, kr, generator=gen, dtype=torch.float64) + 0.5) if use_rad else None
+    vec = torch.randn(E, 3, generator=gen).float().to(device)
+    eul = extract_euler_angles(vec, seed=seed)                      # original edge order
+    # quantise inputs the way the device path sees them
+    q = (lambda t: t.to(dtype).double()) if dtype == torch.bfloat16 else (lambda t: t.float().double())
+    xq, radq = q(x), (q(rad) if rad is not None else None)
+    convq = {"w0": q(conv["w0"]), "b0": conv["b0"].float().double(), "wm": [q(w) for w in conv["wm"]],
+             "c_out": c_out}
+    e64 = eul.cpu().double()
+    ref = omsg.message_block(xq, ei, (e64[:, 0], e64[:, 1], e64[:, 2]), orot.load_jd(), lmax, mmax,
+                             convq, rad=radq, gate=gate)
+    plan = M.MessagePlan(ei.to(device), N)
+    outs = []
+    for _ in range(2):
+        out = M.message_forward(x.to(device=device, dtype=dtype), plan, plan.sort_edges(eul),
+                                plan.sort_edges(rad.to(device)) if rad is not None else None,
+                                conv["w0"].to(device).float(), conv["b0"].to(device).float(),
+                                [w.to(device).float() for w in conv["wm"]], lmax, mmax, gate=gate)
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]), "fused block is not run-to-run deterministic"
+    got = outs[0].cpu().double()
+    scale = ref.abs().max().item()
+    err = (got - ref).abs().max().item() / max(scale, 1e-30)
+    return err, got, ref
+
+
+@pytest.mark.parametrize("lmax,mmax", [(2, 2), (4, 2), (6, 2)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("gate", [False, True])
+def test_forward_matches_oracle(lmax, mmax, dtype, gate, device):
+    print(f"case lmax={lmax} mmax={mmax} dtype={dtype} gate={gate}", flush=True)
+    err, got, ref = _run(lmax, mmax, dtype, gate, True, N=40, E=530, c_in=32, c_out=64, seed=lmax * 10 + int(gate),
+                         device=device)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    assert err < tol, f"rel err {err}"
+    assert torch.all(got[-3:] == 0), "nodes without in-edges must be exactly zero"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_forward_no_radial_star_graph(dtype, device):
+    """A node with > 64 in-edges spans several tiles (partials + fixup)."""
+    err, _, _ = _run(4, 2, dtype, False, False, N=20, E=400, c_in=16 if dtype == torch.bfloat16 else 8,
+                     c_out=32, seed=3, device=device, star=True)
+    assert err < (1e-5 if dtype == torch.float32 else 2e-2)
+
+
+def test_forward_empty_graph(device):
+    from maloq_amd import message as M
+    plan = M.MessagePlan(torch.zeros(2, 0, dtype=torch.long, device=device), 5)
+    w0 = torch.randn(5 * 32, 5 * 32, device=device)
+    wm = [torch.randn(2 * 4 * 32, 4 * 32, device=device), torch.randn(2 * 3 * 32, 3 * 32, device=device)]
+    out = M.message_forward(torch.randn(5, 25, 32, device=device), plan, torch.zeros(0, 3, device=device),
+                            None, w0, None, wm, 4, 2)
+    assert out.shape == (5, 25, 32) and torch.all(out == 0)
+
+
+def test_config2_scale_against_oracle_subset(device):
+    """Config-2 graph (32 x 40 atoms, ~30k edges, lmax 4, C 128) in bf16: the
+    nodes of the first molecule against the oracle (their in-edges only)."""
+    from maloq_amd import message as M
+    from maloq_amd.synth import config2_graph
+    from maloq_amd.wigner import extract_euler_angles
+    g = config2_graph()
+    lmax, mmax, C = 4, 2, 128
+    gen = torch.Generator().manual_seed(0)
+    N, E = g.num_nodes, g.num_edges
+    x = torch.randn(N, 25, C, generator=gen, dtype=torch.float64)
+    conv = _conv(lmax, mmax, C, C, gen, False)
+    rad = torch.rand(E, M.rad_width(lmax, mmax, C), generator=gen, dtype=torch.float64) + 0.5
+    ei = torch.from_numpy(np.stack([g.src, g.dst]))
+    vec = torch.from_numpy(g.edge_distance_vec()).float().to(device)
+    eul = extract_euler_angles(vec, seed=1)
+    plan = M.MessagePlan(ei.to(device), N)
+    dt = torch.bfloat16
+    out = M.message_forward(x.to(device=device, dtype=dt), plan, plan.sort_edges(eul),
+                            plan.sort_edges(rad.to(device)), conv["w0"].to(device).float(),
+                            conv["b0"].to(device).float(), [w.to(device).float() for w in conv["wm"]],
+                            lmax, mmax)
+    mol0 = np.nonzero(g.mol == 0)[0]
+    sel = np.isin(g.dst, mol0)
+    q = lambda t: t.to(dt).double()
+    e64 = eul.cpu().double()[torch.from_numpy(sel)]
+    ref = omsg.message_block(q(x), ei[:, torch.from_numpy(sel)], (e64[:, 0], e64[:, 1], e64[:, 2]),
+                             orot.load_jd(), lmax, mmax,
+                             {"w0": q(conv["w0"]), "b0": conv["b0"].float().double(),
+                              "wm": [q(w) for w in conv["wm"]], "c_out": C},
+                             rad=q(rad)[torch.from_numpy(sel)])
+    got = out.cpu().double()[mol0]
+    err = (got - ref[mol0]).abs().max().item() / ref[mol0].abs().max().item()
+    assert err < 2e-2, err
+
+
+@pytest.mark.parametrize("lmax,mmax", [(2, 2), (4, 2), (6, 2)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_backward_matches_oracle_autograd(lmax, mmax, dtype, device):
+    """Gradients of x, rad, W0, b0 and W_m against fp64 autograd through the oracle."""
+    from maloq_amd import message as M
+    from maloq_amd.wigner import extract_euler_angles
+    print(f"bwd case lmax={lmax} dtype={dtype}", flush=True)
+    gen = torch.Generator().manual_seed(100 + lmax)
+    N, E, c_in, c_out = 30, 300, 32, 32
+    d = (lmax + 1) ** 2
+    q = (lambda t: t.to(dtype).double()) if dtype == torch.bfloat16 else (lambda t: t.float().double())
+    x = q(torch.randn(N, d, c_in, generator=gen, dtype=torch.float64))
+    ei = _graph(N, E, gen)
+    conv = _conv(lmax, mmax, c_in, c_out, gen, False)
+    conv = {"w0": q(conv["w0"]), "b0": conv["b0"].float().double(), "wm": [q(w) for w in conv["wm"]], "c_out": c_out}
+    rad = q(torch.rand(E, M.rad_width(lmax, mmax, c_in), generator=gen, dtype=torch.float64) + 0.5)
+    gout = torch.randn(N, d, c_out, generator=gen, dtype=torch.float64)
+    vec = torch.randn(E, 3, generator=gen).float().to(device)
+    eul = extract_euler_angles(vec, seed=7)
+    e64 = eul.cpu().double()
+    leaves = [x.clone().requires_grad_(), rad.clone().requires_grad_(), conv["w0"].clone().requires_grad_(),
+              conv["b0"].clone().requires_grad_()] + [w.clone().requires_grad_() for w in conv["wm"]]
+    ref = omsg.message_block(leaves[0], ei, (e64[:, 0], e64[:, 1], e64[:, 2]), orot.load_jd(), lmax, mmax,
+                             {"w0": leaves[2], "b0": leaves[3], "wm": leaves[4:], "c_out": c_out}, rad=leaves[1])
+    (ref * gout).sum().backward()
+    plan = M.MessagePlan(ei.to(device), N)
+    dl = [x.to(device=device, dtype=dtype).requires_grad_(),
+          plan.sort_edges(rad.to(device=device, dtype=dtype)).requires_grad_(),
+          conv["w0"].to(device).float().requires_grad_(), conv["b0"].to(device).float().requires_grad_()] + \
+         [w.to(device).float().requires_grad_() for w in conv["wm"]]
+    out = M.message_block(dl[0], plan, plan.sort_edges(eul), dl[1], dl[2], dl[3], dl[4:], lmax, mmax)
+    out.backward(gout.float().to(device))
+    tol = 1e-4 if dtype == torch.float32 else 3e-2
+    inv = torch.empty_like(plan.perm)
+    inv[plan.perm] = torch.arange(E, device=device)
+    names = ["x", "rad", "w0", "b0"] + [f"w{m}" for m in range(1, mmax + 1)]
+    for name, a, b in zip(names, dl, leaves):
+        ga = a.grad
+        if name == "rad":
+            ga = ga[inv]   # back to the original edge order
+        ga = ga.cpu().double()
+        err = (ga - b.grad).abs().max().item() / max(b.grad.abs().max().item(), 1e-30)
+        assert err < tol, f"grad {name}: rel err {err}"
