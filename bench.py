@@ -1,0 +1,413 @@
+#!/usr/bin/env python3
+"""Benchmark of MALOQ's equivariant message-passing hot path on one MI355X.
+
+Headline workload: the reference benchmark's config 2 (32 molecules x 40
+atoms, ~30k directed edges, lmax 4, mmax 2, 128 channels, 8 Gaussian RBFs).
+A step is one fused message block, forward and backward, with inputs already
+resident in HBM: per-edge Euler angles + Wigner-D, the radial MLP (torch), the
+fused rotate -> SO(2) -> inverse-rotate -> segment-sum kernel, and its input,
+radial and weight gradients.  `value` is edges per second.
+
+The JSON line also carries the roofline of the dominant kernel (the fused
+forward launch, MFMA-bound), the CPU baseline (the build's own CPU
+restatement of the reference's PyTorch path, timed on a bounded sample) and
+the basis-transform throughput (config 3, H-blocks/s) with its HBM roofline.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--dtype bf16|fp32]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+PEAK_BF16 = 2.5e15      # dense MFMA, MI355X
+PEAK_FP32 = 157.3e12
+PEAK_HBM = 8.0e12
+
+
+def fused_flops_per_edge(L, M, c_in, c_out):
+    """Algorithmic FLOPs of rotate -> SO(2) -> inverse rotate -> scatter per edge."""
+    rot = sum(min(2 * l + 1, 2 * M + 1) * (2 * l + 1) for l in range(L + 1))
+    mac = (L + 1) ** 2 * c_in * c_out + sum(4 * (L - m + 1) ** 2 * c_in * c_out for m in range(1, M + 1))
+    return 2 * (rot * c_in + mac + rot * c_out) + (L + 1) ** 2 * c_out
+
+
+def make_radial(n_rbf, hidden, out, device):
+    import torch
+    from torch import nn
+    return nn.Sequential(nn.Linear(n_rbf, hidden), nn.LayerNorm(hidden), nn.SiLU(),
+                         nn.Linear(hidden, hidden), nn.LayerNorm(hidden), nn.SiLU(),
+                         nn.Linear(hidden, out)).to(device)
+
+
+def gaussian_rbf(dist, start, stop, num):
+    import torch
+    offset = torch.linspace(start, stop, num, device=dist.device)
+    coeff = -0.5 / (offset[1] - offset[0]).item() ** 2
+    return torch.exp(coeff * (dist.view(-1, 1) - offset.view(1, -1)) ** 2)
+
+
+def message_workload(dtype_name, seed=0):
+    """Tensors of config 2 on cuda:0."""
+    import numpy as np
+    import torch
+    from maloq_amd import message as M
+    from maloq_amd import synth
+
+    dev = torch.device("cuda:0")
+    dt = {"bf16": torch.bfloat16, "fp32": torch.float32}[dtype_name]
+    g = synth.config2_graph()
+    L, Mm, C = 4, 2, 128
+    gen = torch.Generator().manual_seed(seed)
+    N, E = g.num_nodes, g.num_edges
+    plan = M.MessagePlan(torch.from_numpy(np.stack([g.src, g.dst])).to(dev), N)
+    vec = plan.sort_edges(torch.from_numpy(g.edge_distance_vec()).float().to(dev))
+    dist = vec.norm(dim=1)
+    x = torch.randn(N, (L + 1) ** 2, C, generator=gen).to(device=dev, dtype=dt).requires_grad_()
+    k0 = (L + 1) * C
+    w0 = (torch.randn((L + 1) * C, k0, generator=gen) / math.sqrt(k0)).to(dev).requires_grad_()
+    b0 = torch.zeros((L + 1) * C, device=dev, requires_grad=True)
+    wm = []
+    for m in range(1, Mm + 1):
+        k = (L - m + 1) * C
+        wm.append((torch.randn(2 * (L - m + 1) * C, k, generator=gen) / math.sqrt(k)).to(dev).requires_grad_())
+    torch.manual_seed(seed)
+    radial = make_radial(8, 64, M.rad_width(L, Mm, C), dev)
+    gout = torch.randn(N, (L + 1) ** 2, C, generator=gen).to(dev)
+    return dict(graph=g, plan=plan, vec=vec, dist=dist, x=x, w0=w0, b0=b0, wm=wm, radial=radial,
+                gout=gout, L=L, M=Mm, C=C, dt=dt, N=N, E=E)
+
+
+def message_step(w, backward=True):
+    from maloq_amd import message as M
+    from maloq_amd.wigner import extract_euler_angles
+    eul = extract_euler_angles(w["vec"], seed=1234)
+    rad = w["radial"](gaussian_rbf(w["dist"], 0.0, 6.0, 8)).to(w["dt"])
+    out = M.message_block(w["x"], w["plan"], eul, rad, w["w0"], w["b0"], w["wm"], w["L"], w["M"])
+    if backward:
+        out.backward(w["gout"])
+    return out
+
+
+def time_steps(fn, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def kernel_time_events(fn, reps):
+    """Average duration of fn's launches, HIP events on the current stream."""
+    import torch
+    s = torch.cuda.current_stream()
+    fn()
+    s.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(s)
+    for _ in range(reps):
+        fn()
+    b.record(s)
+    b.synchronize()
+    return a.elapsed_time(b) / 1e3 / reps
+
+
+def fused_forward_launch_time(w, reps=20):
+    import torch
+    from maloq_amd import message as M
+    from maloq_amd.wigner import extract_euler_angles
+    with torch.no_grad():
+        eul = extract_euler_angles(w["vec"], seed=1234)
+        rad = w["radial"](gaussian_rbf(w["dist"], 0.0, 6.0, 8)).to(w["dt"])
+        x = w["x"].detach()
+        wpack = M.pack_weights(w["w0"], w["wm"], w["L"], w["M"], False, w["C"], w["C"], w["dt"], 0)
+        f = lambda: M.message_forward(x, w["plan"], eul, rad, w["w0"], w["b0"], w["wm"], w["L"], w["M"],
+                                      wpack=wpack)
+        return kernel_time_events(f, reps)
+
+
+# ---------------------------------------------------------- basis transform
+CFG3_BASIS = {1: [0, 0, 1], 6: [0, 0, 0, 1, 1, 2], 7: [0, 0, 0, 1, 1, 2], 8: [0, 0, 0, 1, 1, 2]}
+
+
+def basis_workload():
+    """Config 3 as one block list (all on-site + off-site < 8 A blocks of 64
+    molecules), so the whole batch is one launch."""
+    import numpy as np
+    import torch
+    from maloq_amd import synth
+    from maloq_amd import tensor_decomp as ptd
+    from maloq_amd.basis_transform import HipE3TensorDecomp
+
+    dev = torch.device("cuda:0")
+    t = ptd.BasisTables(CFG3_BASIS)
+    base = ptd.e3TensorDecomp(t.req_output_irreps, t.out_js_list, torch.float32, device_torch=dev)
+    hip = HipE3TensorDecomp(base)
+    Zs, offs, rows, cols, data = [], [0], [], [], []
+    atom0 = 0
+    n_bytes = 0
+    mols = synth.config3_molecules()
+    for m, (z, p) in enumerate(mols):
+        H, off = synth.dense_hamiltonian(z, p, t.orbitals_per_atom(z), seed=m, cutoff=8.0)
+        src, dst, _ = synth.radius_graph(p, 8.0)
+        r, c = synth.atom_pair_rows(src, dst, len(z))
+        for i, j in zip(r, c):
+            blk = H[off[i]:off[i + 1], off[j]:off[j + 1]]
+            data.append(blk.reshape(-1))
+            n_bytes += 4 * blk.size
+        rows.append(r + atom0)
+        cols.append(c + atom0)
+        Zs.append(z)
+        offs.extend((off[1:] + offs[-1]).tolist())
+        atom0 += len(z)
+    rows = np.concatenate(rows).astype(np.int32)
+    cols = np.concatenate(cols).astype(np.int32)
+    Z = np.concatenate(Zs).astype(np.int32)
+    off = np.asarray(offs, np.int32)
+    sizes = np.array([d.size for d in data], np.int64)
+    bdo = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+    flat = torch.from_numpy(np.concatenate(data).astype(np.float32)).to(dev)
+    return dict(tables=t, hip=hip, base=base, Z=Z, off=off, rows=rows, cols=cols,
+                bdo=torch.from_numpy(bdo).to(dev), data=flat, n_blocks=len(rows),
+                block_bytes=n_bytes, T=base.in_slices[-1], mols=mols)
+
+
+def basis_timing(bw, reps=50):
+    import torch
+    hip, t = bw["hip"], bw["tables"]
+    args = (bw["off"], bw["Z"], bw["rows"], bw["cols"], t.orbital_template)
+    # upload index arrays once (the dataset's device-resident tables)
+    import numpy as np
+    dev = bw["data"].device
+    dev_args = tuple(torch.as_tensor(np.asarray(a, np.int32), device=dev) for a in args[:4])
+    out = hip.fock_to_irreps(bw["data"], *args, block_data_offsets=bw["bdo"])
+    fwd = kernel_time_events(lambda: hip.fock_to_irreps(bw["data"], *dev_args, t.orbital_template,
+                                                        block_data_offsets=bw["bdo"]), reps)
+    back = torch.empty_like(bw["data"])
+    inv = kernel_time_events(lambda: hip.irreps_to_fock(out, back, *dev_args, t.orbital_template,
+                                                        block_data_offsets=bw["bdo"]), reps)
+    rt = ((back - bw["data"]).abs().max() / bw["data"].abs().max()).item()
+    return fwd, inv, rt
+
+
+# ---------------------------------------------------------------- CPU legs
+def cpu_message_baseline(budget_s=15.0):
+    """The build's CPU restatement of the reference path (bmm(wigner), einsum
+    to_m, SO2_Convolution, einsum, bmm(wigner_inv), index_add_), fp32 torch on
+    the host cores, forward + backward, on the first molecules of config 2."""
+    import numpy as np
+    import torch
+    from oracle import message as omsg
+    from oracle import rotation as orot
+    from maloq_amd import synth
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    g = synth.config2_graph()
+    L, Mm, C = 4, 2, 128
+    gen = torch.Generator().manual_seed(0)
+    Jd = orot.load_jd(torch.float32)
+    conv = {"w0": torch.randn(5 * C, 5 * C, generator=gen) / math.sqrt(5 * C),
+            "b0": torch.zeros(5 * C),
+            "wm": [torch.randn(2 * (L - m + 1) * C, (L - m + 1) * C, generator=gen) / math.sqrt((L - m + 1) * C)
+                   for m in (1, 2)], "c_out": C}
+    for k in ("w0", "b0"):
+        conv[k].requires_grad_()
+    for wmm in conv["wm"]:
+        wmm.requires_grad_()
+
+    def run(nmol):
+        sel = np.isin(g.mol[g.dst], np.arange(nmol))
+        nodes = np.nonzero(np.isin(g.mol, np.arange(nmol)))[0]
+        ei = torch.from_numpy(np.stack([g.src[sel], g.dst[sel]]))
+        vec = torch.from_numpy(g.edge_distance_vec()[sel]).float()
+        x = torch.randn(len(nodes), 25, C, generator=gen).requires_grad_()
+        rad = torch.rand(int(sel.sum()), 1536, generator=gen).requires_grad_()
+        t0 = time.perf_counter()
+        eul = orot.init_edge_rot_euler_angles(vec, torch.rand(len(vec), generator=gen))
+        out = omsg.message_block(x, ei, eul, Jd, L, Mm, conv, rad=rad)
+        out.backward(torch.ones_like(out))
+        return time.perf_counter() - t0, int(sel.sum())
+
+    run(1)  # warm-up
+    t1, e1 = run(1)
+    nmol = max(1, min(32, int(budget_s / 5 / max(t1, 1e-3))))
+    times = []
+    for _ in range(5):
+        t, e = run(nmol)
+        times.append(t)
+    t = sorted(times)[len(times) // 2]
+    return {"value": e / t, "unit": "edges/s", "cores": cores, "kind": "port",
+            "sample": f"config 2, first {nmol} molecule(s) ({e} edges), fp32 torch CPU, fwd+bwd, median of 5",
+            "threads": torch.get_num_threads(), "cpu": _cpu_model()}
+
+
+def cpu_basis_baseline(bw, budget_s=8.0):
+    """numpy_single_matrix2label restated + dense get_net_out matmul, per molecule."""
+    import numpy as np
+    import torch
+    from oracle import matrix2labels as om2l
+    from oracle import tensor_decomp as otd
+    from maloq_amd import synth
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    t = bw["tables"]
+    o = otd.E3TensorDecomp(t.out_js_list, dtype=torch.float32)
+    total_blocks, total_t = 0, 0.0
+    for m, (z, p) in enumerate(bw["mols"]):
+        H, off = synth.dense_hamiltonian(z, p, t.orbitals_per_atom(z), seed=m, cutoff=8.0)
+        src, dst, _ = synth.radius_graph(p, 8.0)
+        r, c = synth.atom_pair_rows(src, dst, len(z))
+        t0 = time.perf_counter()
+        lab = np.zeros((len(r), 196), np.float32)
+        om2l.single_matrix2label(t.orbital_template, off, z, r, c, H, lab, True)
+        o.get_net_out(torch.from_numpy(lab))
+        total_t += time.perf_counter() - t0
+        total_blocks += len(r)
+        if total_t > budget_s:
+            break
+    return {"value": total_blocks / total_t, "unit": "H-blocks/s", "cores": cores, "kind": "port",
+            "sample": f"config 3, {m + 1} molecule(s) ({total_blocks} blocks), numpy gather + fp32 matmul"}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def load_traffic(name):
+    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/traffic.json)."""
+    p = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        return json.load(open(p)).get(name)
+    except (OSError, ValueError):
+        return None
+
+
+def profile_only(args):
+    """Runs one piece of the path --reps times (for rocprofv3 passes)."""
+    import torch
+    if args.only == "copy":
+        # plain copy of a known size: calibrates FETCH_SIZE / WRITE_SIZE
+        a = torch.ones(64 * 1024 * 1024, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(args.reps):
+            b.copy_(a)
+    elif args.only in ("fwd", "step"):
+        w = message_workload(args.dtype)
+        if args.only == "fwd":
+            fused_forward_launch_time(w, reps=args.reps)
+        else:
+            for _ in range(args.reps):
+                message_step(w, True)
+    else:
+        bw = basis_workload()
+        basis_timing(bw, reps=args.reps)
+    torch.cuda.synchronize()
+    print(f"[bench] --only {args.only}: {args.reps} reps done", file=sys.stderr, flush=True)
+    return 0
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp32"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--no-extras", action="store_true", help="headline only")
+    ap.add_argument("--only", choices=["fwd", "step", "basis", "copy"],
+                    help="profiling mode: run one piece a few times and exit (no JSON line)")
+    ap.add_argument("--reps", type=int, default=5, help="launches in --only mode")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the hot path runs on a single MI355X; multi-GPU sharding is design-only)", file=sys.stderr)
+        return 2
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        return 1
+    if args.only:
+        return profile_only(args)
+    print(f"[bench] workload: config 2 fused message block ({args.dtype}) ...", file=sys.stderr, flush=True)
+    w = message_workload(args.dtype)
+    t_step = time_steps(lambda: message_step(w, True), args.steps, args.warmup)
+    E = w["E"]
+    print(f"[bench] fwd+bwd {t_step * 1e3:.3f} ms/step, {E / t_step:.4g} edges/s", file=sys.stderr, flush=True)
+    t_fwd_launch = fused_forward_launch_time(w)
+    f_edge = fused_flops_per_edge(w["L"], w["M"], w["C"], w["C"])
+    peak = PEAK_BF16 if args.dtype == "bf16" else PEAK_FP32
+    achieved = f_edge * E / t_fwd_launch
+    t_fwd_step = time_steps(lambda: message_step(w, False), args.steps, args.warmup)
+    result = {
+        "metric": "edges/sec fused rotate+SO2 (lmax=4,C=128); H-blocks/sec basis transform; %roofline",
+        "value": E / t_step,
+        "unit": "edges/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": t_step * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": args.dtype,
+        "data": "synthetic (seeded config-2 geometry, random-init weights)",
+        "config": {"workload": "config2 fused message block fwd+bwd: Euler/Wigner-D, radial MLP, "
+                               "rotate->SO(2)->inverse rotate->segment sum, input/radial/weight grads",
+                   "molecules": 32, "atoms_per_molecule": 40, "edges": E, "nodes": w["N"],
+                   "lmax": w["L"], "mmax": w["M"], "channels": w["C"], "rbf": 8, "cutoff_A": 6.0},
+        "roofline": {"kernel": "message_kernel<4,2> forward (+fixup)", "bound": "mfma",
+                     "achieved": achieved / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
+                     "frac": achieved / peak, "traffic": load_traffic(f"message_fwd_{args.dtype}"),
+                     "flops_per_edge": f_edge, "launch_ms": t_fwd_launch * 1e3},
+        "fwd_edges_per_s": E / t_fwd_step,
+    }
+    del w
+    torch.cuda.empty_cache()
+    if not args.no_extras:
+        if args.dtype == "bf16":
+            w32 = message_workload("fp32")
+            t32 = time_steps(lambda: message_step(w32, True), max(3, args.steps // 4), 2)
+            result["fp32_fwd_bwd_edges_per_s"] = w32["E"] / t32
+            tl32 = fused_forward_launch_time(w32, reps=5)
+            result["fp32_fwd_roofline_frac"] = f_edge * w32["E"] / tl32 / PEAK_FP32
+            del w32
+        print("[bench] basis transform (config 3) ...", file=sys.stderr, flush=True)
+        bw = basis_workload()
+        tf, ti, rt = basis_timing(bw)
+        bpb = (bw["block_bytes"] + 4 * bw["T"] * bw["n_blocks"]) / bw["n_blocks"]
+        result["basis_transform"] = {
+            "metric": "H-blocks/s", "fwd": bw["n_blocks"] / tf, "inv": bw["n_blocks"] / ti,
+            "blocks": bw["n_blocks"], "round_trip_rel_err": rt,
+            "roofline": {"bound": "hbm", "achieved": bpb * bw["n_blocks"] / tf / 1e9, "peak": PEAK_HBM / 1e9,
+                         "unit": "GB/s", "frac": bpb * bw["n_blocks"] / tf / PEAK_HBM,
+                         "bytes_per_block": bpb, "traffic": load_traffic("fock_to_irreps")},
+        }
+    if not args.no_cpu:
+        print("[bench] CPU baseline ...", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_message_baseline()
+        if not args.no_extras:
+            result["basis_transform"]["cpu_baseline"] = cpu_basis_baseline(bw)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -29,6 +29,8 @@ from .tensor_decomp import MAX_ELEMENTS
 
 
 def _i32(a, device):
+    if torch.is_tensor(a):
+        return a.to(device=device, dtype=torch.int32).contiguous()
     return torch.as_tensor(np.ascontiguousarray(np.asarray(a, dtype=np.int32)), device=device)
 
 
@@ -56,7 +58,9 @@ class HipE3TensorDecomp:
         self.total_in_dim, self.total_h_dim = int(ins[-1]), int(hs[-1])
         self.sort_perm = getattr(decomp_obj, "sort_perm", None)
         if decomp_obj.sort is not None and self.sort_perm is None:
-            raise ValueError("sorted base object without an explicit column permutation")
+            # a reference e3TensorDecomp: read the permutation off its sort module
+            eye = torch.eye(int(decomp_obj.in_slices[-1]), dtype=torch.float64)
+            self.sort_perm = torch.argmax(decomp_obj.sort(eye.to(decomp_obj.device)).cpu(), dim=0).numpy()
         wms = [np.asarray(w.detach().cpu().double()) for w in decomp_obj.wms]
         wms_h = [np.asarray(w.detach().cpu().double()) for w in decomp_obj.wms_H]
 
@@ -209,7 +213,7 @@ class HipE3TensorDecomp:
         r_ = _i32(rows, dev)
         c_ = _i32(cols, dev)
         R = int(r_.shape[0])
-        sizes = np.diff(np.asarray(fock_block_offsets))
+        sizes = torch.diff(off) if torch.is_tensor(off) else np.diff(np.asarray(fock_block_offsets))
         maxe = int(sizes.max()) ** 2 if len(sizes) else 1
         ld, bdo = self._storage(fock, block_data_offsets)
         out = torch.empty(R, self.total_in_dim, device=dev, dtype=torch.float32)
