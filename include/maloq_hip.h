@@ -123,41 +123,53 @@ int64_t maloq_message_partials_floats(int lmax, int gate, int64_t num_edges, int
  * kernel-input channels c_k, kernel-output channels c_n); -1 if unsupported. */
 int64_t maloq_message_wpack_bytes(int dtype, int lmax, int mmax, int gate, int c_k, int c_n);
 
+/* Kept rows d' = (lmax+1) + sum_{m=1..mmax} 2 (lmax-m+1) of the m-major layout,
+ * and kept Wigner-D entries per edge sum_l (1 + 2 min(mmax, l)) (2l+1). */
+int maloq_message_kept_rows(int lmax, int mmax);
+int maloq_message_wigner_floats(int lmax, int mmax);
+
 /* Fused message block, forward:
  *   out[n] = sum_{e: dst[e]=n} D_e^T SO2(D_e x[src[e]] (*) rad[e]) [gate],
  * with D_e the kept rows |m| <= mmax of the Wigner-D of eulers[e].
- * Edges must be sorted by dst (non-decreasing).  edge_idx (nullable) maps the
- * kernel's edge order to rows of eulers / rad.  x [N_src, d, c_in] (fp32 or
- * bf16 per dtype), rad [E, sum_m (lmax-m+1) c_in] (nullable), wpack from the
- * host packer, bias [gate ? lmax*c_out + (lmax+1)*c_out : (lmax+1)*c_out]
- * fp32 (nullable), out [num_nodes, d, c_out] fp32, seg_ptr [num_nodes+1] CSR
- * of dst, partials of maloq_message_partials_floats floats.  save_y (nullable)
- * receives the rotated, radially scaled input rows [E, d', c_in] in m-major
- * order (the SO(2) layer's input, kept for the weight gradient).
+ * Edges must be sorted by dst (non-decreasing); per-edge arrays (eulers, rad)
+ * follow that order.  x [N_src, d, c_in] (fp32 or bf16 per dtype), rad
+ * [E, sum_m (lmax-m+1) c_in] (nullable), wpack from the host packer, bias
+ * [gate ? lmax*c_out + (lmax+1)*c_out : (lmax+1)*c_out] fp32 (nullable),
+ * out [num_nodes, d, c_out] fp32, seg_ptr [num_nodes+1] CSR of dst, partials
+ * of maloq_message_partials_floats floats.  Workspaces (also the saved
+ * tensors of the backward): y_ws [E, d', c_in] (dtype) receives the rotated,
+ * radially scaled SO(2) input rows (m-major), r_ws (nullable, same shape) the
+ * unscaled rows, dk_ws [E, maloq_message_wigner_floats] fp32 the kept
+ * Wigner-D rows.  Two kernels: a per-edge prep (Wigner rows + rotation) and
+ * the SO(2) MFMA GEMM with inverse rotation and segment sum, then a fixup for
+ * segments cut by tile boundaries.
  * Replaces Edgewise.forward_node, helm/esen_block.py:146-208 (bmm(wigner),
  * einsum(to_m), SO2_Convolution helm/nn/so2_layers.py:139-214, GateActivation
  * helm/nn/activation.py:57-77, bmm(wigner_inv), index_add_). */
 int maloq_message_fwd(int dtype, int lmax, int mmax, int gate, const void* x, int c_in,
-                      const int32_t* src, const int32_t* dst, const int32_t* edge_idx,
-                      int64_t num_edges, const float* eulers, const void* rad, const void* wpack,
-                      const float* bias, const float* jd, float* out, int64_t num_nodes, int c_out,
-                      const int64_t* seg_ptr, float* partials, void* save_y, void* stream);
+                      const int32_t* src, const int32_t* dst, int64_t num_edges,
+                      const float* eulers, const void* rad, const void* wpack, const float* bias,
+                      const float* jd, float* out, int64_t num_nodes, int c_out,
+                      const int64_t* seg_ptr, float* partials, void* y_ws, void* r_ws,
+                      float* dk_ws, void* stream);
 
 /* Input and radial-scale gradients of the (ungated) fused block:
  *   grad_x[n] = sum_{e: src[e]=n} D_e^T rad[e] (*) SO2^T(D_e grad_out[dst[e]]),
- *   grad_rad[e] = SO2^T(D_e grad_out[dst[e]]) (*) (D_e x[src[e]]).
+ *   grad_rad[e] = SO2^T(D_e grad_out[dst[e]]) (*) R_e   (R_e = D_e x[src[e]]).
  * Edges in src-sorted order: src_sorted non-decreasing, dst_by_src the
- * matching dst, edge_idx the row of eulers / rad / grad_rad (the forward's
- * edge order).  wpack_t: weights packed for the transposed GEMM.  save_dz
- * (nullable) receives the rotated output-gradient rows [E, d', c_out] (m-major,
- * indexed by edge_idx) for the weight gradient.
+ * matching dst, edge_idx the forward (dst-sorted) position of each edge,
+ * which indexes dk (forward dk_ws), rad, grad_rad, r_saved (forward r_ws) and
+ * dz_ws.  wpack_t: weights packed for the transposed GEMM.  dz_ws [E, d',
+ * c_out] (dtype) receives the rotated output-gradient rows (for the weight
+ * gradient).
  * Replaces the autograd backward of Edgewise.forward_node (esen_block.py:146-208). */
 int maloq_message_bwd_dx(int dtype, int lmax, int mmax, const float* grad_out, int c_out,
                          const int32_t* dst_by_src, const int32_t* src_sorted,
-                         const int32_t* edge_idx, int64_t num_edges, const float* eulers,
-                         const void* rad, void* grad_rad, const void* x, const void* wpack_t,
-                         const float* jd, float* grad_x, int64_t num_nodes, int c_in,
-                         const int64_t* seg_ptr_src, float* partials, void* save_dz, void* stream);
+                         const int32_t* edge_idx, int64_t num_edges, const float* dk,
+                         const void* rad, void* grad_rad, const void* r_saved,
+                         const void* wpack_t, const float* jd, float* grad_x, int64_t num_nodes,
+                         int c_in, const int64_t* seg_ptr_src, float* partials, void* dz_ws,
+                         void* stream);
 
 /* Floats of the split-K partials buffer of maloq_message_dw. */
 int64_t maloq_message_dw_partials_floats(int lmax, int mmax, int c_out, int c_in, int splits);

@@ -36,8 +36,10 @@ SIGNATURES = {
     "maloq_segment_sum": [_p, _p, _p, _i64, _i64, _p, _p],
     "maloq_message_partials_floats": [_i32, _i32, _i64, _i32],
     "maloq_message_wpack_bytes": [_i32, _i32, _i32, _i32, _i32, _i32],
-    "maloq_message_fwd": [_i32, _i32, _i32, _i32, _p, _i32, _p, _p, _p, _i64, _p, _p, _p, _p, _p,
-                          _p, _i64, _i32, _p, _p, _p, _p],
+    "maloq_message_kept_rows": [_i32, _i32],
+    "maloq_message_wigner_floats": [_i32, _i32],
+    "maloq_message_fwd": [_i32, _i32, _i32, _i32, _p, _i32, _p, _p, _i64, _p, _p, _p, _p, _p, _p,
+                          _i64, _i32, _p, _p, _p, _p, _p, _p],
     "maloq_message_bwd_dx": [_i32, _i32, _i32, _p, _i32, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p,
                              _p, _i64, _i32, _p, _p, _p, _p],
     "maloq_message_dw_partials_floats": [_i32, _i32, _i32, _i32, _i32],

@@ -63,6 +63,17 @@ static int dispatch(int lmax, int mmax, int dtype, int gate, int mode, const Arg
   MALOQ_REQUIRE(false, "unsupported lmax %d (built: 2, 4, 6 with mmax 2)", lmax);
 }
 
+static int prep_dispatch(int lmax, int mmax, int dtype, int mode, const PrepArgs& a,
+                         hipStream_t s) {
+  switch (lmax) {
+    case 2: return prep_l2(mmax, dtype, mode, a, s);
+    case 4: return prep_l4(mmax, dtype, mode, a, s);
+    case 6: return prep_l6(mmax, dtype, mode, a, s);
+    default: break;
+  }
+  MALOQ_REQUIRE(false, "unsupported lmax %d (built: 2, 4, 6 with mmax 2)", lmax);
+}
+
 static int check_common(int dtype, int lmax, int mmax, int c_k, int c_n, int64_t E) {
   MALOQ_REQUIRE(dtype == 0 || dtype == 1, "dtype must be 0 (fp32) or 1 (bf16)");
   MALOQ_REQUIRE(lmax >= 0 && mmax >= 0 && mmax <= lmax, "bad lmax/mmax");
@@ -73,16 +84,32 @@ static int check_common(int dtype, int lmax, int mmax, int c_k, int c_n, int64_t
   return MALOQ_OK;
 }
 
+static int kept_rows(int lmax, int mmax) {
+  int r = lmax + 1;
+  for (int m = 1; m <= mmax; ++m) r += 2 * (lmax - m + 1);
+  return r;
+}
+
+static int wigner_floats(int lmax, int mmax) {
+  int s = 0;
+  for (int l = 0; l <= lmax; ++l) s += (1 + 2 * (mmax < l ? mmax : l)) * (2 * l + 1);
+  return s;
+}
+
 }  // namespace msg
 }  // namespace maloq
 
 using namespace maloq;
 using namespace maloq::msg;
 
+extern "C" int maloq_message_kept_rows(int lmax, int mmax) { return kept_rows(lmax, mmax); }
+
+extern "C" int maloq_message_wigner_floats(int lmax, int mmax) { return wigner_floats(lmax, mmax); }
+
 extern "C" int64_t maloq_message_partials_floats(int lmax, int gate, int64_t num_edges, int c_out) {
   const int64_t d = static_cast<int64_t>(lmax + 1) * (lmax + 1);
-  const int64_t ntiles = (num_edges + tile_edges(lmax, gate) - 1) / tile_edges(lmax, gate);
-  return ntiles * 2 * d * c_out;
+  const int64_t te = tile_edges(lmax, gate);
+  return ((num_edges + te - 1) / te) * 2 * d * c_out;
 }
 
 extern "C" int64_t maloq_message_wpack_bytes(int dtype, int lmax, int mmax, int gate, int c_k,
@@ -93,11 +120,11 @@ extern "C" int64_t maloq_message_wpack_bytes(int dtype, int lmax, int mmax, int 
 }
 
 extern "C" int maloq_message_fwd(int dtype, int lmax, int mmax, int gate, const void* x, int c_in,
-                                 const int32_t* src, const int32_t* dst, const int32_t* edge_idx,
-                                 int64_t num_edges, const float* eulers, const void* rad,
-                                 const void* wpack, const float* bias, const float* jd,
-                                 float* out, int64_t num_nodes, int c_out, const int64_t* seg_ptr,
-                                 float* partials, void* save_y, void* stream) {
+                                 const int32_t* src, const int32_t* dst, int64_t num_edges,
+                                 const float* eulers, const void* rad, const void* wpack,
+                                 const float* bias, const float* jd, float* out, int64_t num_nodes,
+                                 int c_out, const int64_t* seg_ptr, float* partials, void* y_ws,
+                                 void* r_ws, float* dk_ws, void* stream) {
   int rc = check_common(dtype, lmax, mmax, c_in, c_out, num_edges);
   if (rc) return rc;
   MALOQ_REQUIRE(num_nodes >= 0, "num_nodes < 0");
@@ -105,13 +132,18 @@ extern "C" int maloq_message_fwd(int dtype, int lmax, int mmax, int gate, const 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t d = static_cast<int64_t>(lmax + 1) * (lmax + 1);
   if (num_edges > 0) {
-    MALOQ_REQUIRE(x && src && dst && eulers && partials, "null pointer");
+    MALOQ_REQUIRE(x && src && dst && eulers && partials && y_ws && dk_ws, "null pointer");
+    PrepArgs p{};
+    p.x = x; p.gidx = src; p.eidx = nullptr; p.eulers = eulers; p.rad = rad; p.jd = jd;
+    p.y = y_ws; p.r = r_ws; p.dk = dk_ws; p.build_d = 1; p.E = num_edges; p.C = c_in;
+    rc = prep_dispatch(lmax, mmax, dtype, FWD, p, s);
+    if (rc) return rc;
     Args a{};
-    a.x = x; a.gidx = src; a.seg = dst; a.eidx = edge_idx; a.eulers = eulers; a.rad = rad;
-    a.wpack = static_cast<const char*>(wpack); a.bias = bias; a.jd = jd; a.out = out;
-    a.save_a = save_y;
+    a.a_src = y_ws; a.dk = dk_ws; a.seg = dst; a.eidx = nullptr;
+    a.wpack = static_cast<const char*>(wpack); a.bias = bias; a.out = out;
     a.part = partials; a.E = num_edges; a.C_k = c_in; a.C_n = c_out; a.n_cb = c_out / CB;
-    a.extra = gate ? lmax * c_out : 0; a.ntiles = (num_edges + tile_edges(lmax, gate) - 1) / tile_edges(lmax, gate);
+    a.extra = gate ? lmax * c_out : 0;
+    a.ntiles = (num_edges + tile_edges(lmax, gate) - 1) / tile_edges(lmax, gate);
     const int kc = dtype == 1 ? BF16::KC : F32::KC;
     a.frags_per_cb = frags_per_cb(lmax, mmax, gate, c_in, kc);
     rc = dispatch(lmax, mmax, dtype, gate, FWD, a, s);
@@ -123,10 +155,10 @@ extern "C" int maloq_message_fwd(int dtype, int lmax, int mmax, int gate, const 
 extern "C" int maloq_message_bwd_dx(int dtype, int lmax, int mmax, const float* grad_out,
                                     int c_out, const int32_t* dst_by_src,
                                     const int32_t* src_sorted, const int32_t* edge_idx,
-                                    int64_t num_edges, const float* eulers, const void* rad,
-                                    void* grad_rad, const void* x, const void* wpack_t,
+                                    int64_t num_edges, const float* dk, const void* rad,
+                                    void* grad_rad, const void* r_saved, const void* wpack_t,
                                     const float* jd, float* grad_x, int64_t num_nodes, int c_in,
-                                    const int64_t* seg_ptr_src, float* partials, void* save_dz,
+                                    const int64_t* seg_ptr_src, float* partials, void* dz_ws,
                                     void* stream) {
   // kernel input channels = c_out (gradient side), output channels = c_in
   int rc = check_common(dtype, lmax, mmax, c_out, c_in, num_edges);
@@ -135,14 +167,19 @@ extern "C" int maloq_message_bwd_dx(int dtype, int lmax, int mmax, const float* 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t d = static_cast<int64_t>(lmax + 1) * (lmax + 1);
   if (num_edges > 0) {
-    MALOQ_REQUIRE(grad_out && dst_by_src && src_sorted && eulers && partials && edge_idx,
+    MALOQ_REQUIRE(grad_out && dst_by_src && src_sorted && edge_idx && dk && partials && dz_ws,
                   "null pointer");
-    MALOQ_REQUIRE(rad == nullptr || x != nullptr, "x is needed for the radial gradient");
+    MALOQ_REQUIRE(rad == nullptr || r_saved != nullptr, "the radial gradient needs the saved rows");
+    PrepArgs p{};
+    p.x = grad_out; p.gidx = dst_by_src; p.eidx = edge_idx; p.eulers = nullptr; p.rad = nullptr;
+    p.jd = jd; p.y = dz_ws; p.r = nullptr; p.dk = const_cast<float*>(dk); p.build_d = 0;
+    p.E = num_edges; p.C = c_out;
+    rc = prep_dispatch(lmax, mmax, dtype, BWD_DX, p, s);
+    if (rc) return rc;
     Args a{};
-    a.x = grad_out; a.gidx = dst_by_src; a.seg = src_sorted; a.eidx = edge_idx;
-    a.eulers = eulers; a.rad = rad; a.drad = grad_rad; a.xsrc = x; a.xsrc_idx = src_sorted;
-    a.wpack = static_cast<const char*>(wpack_t); a.bias = nullptr; a.jd = jd; a.out = grad_x;
-    a.save_a = save_dz;
+    a.a_src = dz_ws; a.dk = dk; a.seg = src_sorted; a.eidx = edge_idx;
+    a.rad = rad; a.drad = grad_rad; a.rsave = r_saved;
+    a.wpack = static_cast<const char*>(wpack_t); a.bias = nullptr; a.out = grad_x;
     a.part = partials; a.E = num_edges; a.C_k = c_out; a.C_n = c_in; a.n_cb = c_in / CB;
     a.extra = 0; a.ntiles = (num_edges + tile_edges(lmax, 0) - 1) / tile_edges(lmax, 0);
     const int kc = dtype == 1 ? BF16::KC : F32::KC;

@@ -45,12 +45,14 @@ typedef float f32x16 __attribute__((__vector_size__(16 * sizeof(float))));
 struct BF16 {
   using raw = uint16_t;
   static constexpr int KC = 16;  // channels per K step (one fragment)
+  static constexpr int VEC = 8;  // elements per 16-byte lane load
   static __device__ __forceinline__ float load(const raw* p) { return bf16_to_f32(*p); }
   static __device__ __forceinline__ raw cvt(float v) { return f32_to_bf16(v); }
 };
 struct F32 {
   using raw = float;
   static constexpr int KC = 8;
+  static constexpr int VEC = 4;
   static __device__ __forceinline__ float load(const raw* p) { return *p; }
   static __device__ __forceinline__ raw cvt(float v) { return v; }
 };
@@ -76,7 +78,10 @@ __device__ __forceinline__ int frag_off<BF16>(int row, int k) {
 }
 template <>
 __device__ __forceinline__ int frag_off<F32>(int row, int k) {
-  return (((k & 1) * 32 + row) * 4 + (k >> 1)) * 4;
+  // channel k of an 8-wide K step: lane half k/4, slot k%4.  MFMA j of the
+  // four 32x32x2 steps pairs channels j and 4+j in A and B alike, so the K
+  // order is a permutation shared by both operands and the sum is exact.
+  return (((k >> 2) * 32 + row) * 4 + (k & 3)) * 4;
 }
 
 // ------------------------------------------------------- compile-time plan
@@ -157,27 +162,24 @@ struct Plan {
   static constexpr int M2_BYTES = TE * (2 * L + 1) * (2 * L + 1) * 4 + TE * 3 * 2 * (L + 1) * 4;
   static constexpr int EPI_BYTES = NW * TE * 33 * 4;
   static constexpr int cmax(int a, int b) { return a > b ? a : b; }
-  static constexpr int STAGE_BYTES = cmax(cmax(A_BYTES + B_BYTES, M2_BYTES), EPI_BYTES);
+  static constexpr int STAGE_BYTES = cmax(A_BYTES + B_BYTES, EPI_BYTES);
 };
 
 enum Mode { FWD = 0, BWD_DX = 1 };
 
 struct Args {
-  const void* x;          // [N_in, d, C_k] gathered rows (TX)
-  const int32_t* gidx;    // [E] gather row per edge (kernel edge order)
+  const void* a_src;      // [E_all, d', C_k] (TM raw): rotated rows, m-major, by edge id
+  const float* dk;        // [E_all, DS] kept Wigner rows per edge id
   const int32_t* seg;     // [E] segment id per edge, non-decreasing
-  const int32_t* eidx;    // [E] nullable: index into per-edge arrays
-  const float* eulers;    // [E_all, 3]
-  const void* rad;        // [E_all, KR] (TM raw) or null
+  const int32_t* eidx;    // [E] nullable: edge id of each kernel-order edge
+  const void* rad;        // BWD_DX: [E_all, KR] (TM raw) or null
   void* drad;             // BWD_DX: [E_all, KR] (TM raw) output, nullable
-  const void* xsrc;       // BWD_DX: forward input rows [N_src, d, C_n] (TM raw) for d(rad)
-  const int32_t* xsrc_idx;// BWD_DX: row of xsrc per edge (kernel order)
+  const void* rsave;      // BWD_DX: unscaled rotated forward inputs [E_all, d', C_n] (TM raw)
   const char* wpack;      // packed B fragments
   const float* bias;      // FWD: [N0] or null
   const float* jd;        // packed J_0..J_L
   float* out;             // [N_out, d, C_n]
   float* part;            // [ntiles, 2, d, C_n]
-  void* save_a;           // nullable: A operand rows [E_all, d', C_k] (TM raw), m-major
   int64_t E;
   int C_k, C_n;           // kernel input / output channels
   int n_cb;               // C_n / CB
@@ -226,115 +228,34 @@ struct Kernel {
   static constexpr int d = (L + 1) * (L + 1);
   static constexpr int NT = P::NT;
   static constexpr int KC = TM::KC;
-  // threads per edge in the prologue (threads beyond TE * TPE skip it)
-  static constexpr int TPE = (NT / TE) < KC ? (NT / TE) : KC;
-  static constexpr int CPT = KC / TPE;  // channels per thread in the prologue
-  static_assert(CPT >= 1, "KC must cover the threads of an edge");
 
   struct Smem {
-    float J[jd_size(L)];
     float D[TE * P::DS];
-    float eul[TE * 3];
     int seg[TE];
-    int gid[TE];
     int eid[TE];
-    int xid[TE];
     alignas(16) char stage[P::STAGE_BYTES];
   };
 
-  // ------------------------------------------ kept Wigner rows per edge
-  static __device__ void build_d(Smem& s, int tid) {
-    float* m2 = reinterpret_cast<float*>(s.stage);
-    float* trig = m2 + TE * (2 * L + 1) * (2 * L + 1);
-    for (int q = tid; q < TE * 3 * (L + 1); q += NT) {
-      const int e = q / (3 * (L + 1)), r = q % (3 * (L + 1));
-      const int ang = r / (L + 1), m = r % (L + 1);
-      float sn, cs;
-      sincosf(static_cast<float>(m) * s.eul[e * 3 + ang], &sn, &cs);
-      trig[(e * 3 + ang) * 2 * (L + 1) + m] = cs;
-      trig[(e * 3 + ang) * 2 * (L + 1) + (L + 1) + m] = sn;
-    }
-    __syncthreads();
-    for (int l = 0; l <= L; ++l) {
-      const int n = 2 * l + 1;
-      const float* J = s.J + jd_offset(l);
-      for (int q = tid; q < TE * n; q += NT) {
-        const int e = q / n, k = q % n;
-        const float* tb = trig + (e * 3 + 1) * 2 * (L + 1);
-        const float* tc = trig + (e * 3 + 2) * 2 * (L + 1);
-        wigner_m2_row(l, k, J, tb, tb + (L + 1), tc, tc + (L + 1), m2 + (e * n + k) * n);
-      }
-      __syncthreads();
-      const int nql = P::nq(l);
-      const int dof = P::doff(l);
-      for (int q = tid; q < TE * nql * n; q += NT) {
-        const int e = q / (nql * n), r = q % (nql * n);
-        const int qi = r / n, j = r % n;
-        const int mm = (qi + 1) >> 1;
-        const int i = (qi == 0) ? l : ((qi & 1) ? l + mm : l - mm);
-        const int ii = 2 * l - i;
-        const float* ta = trig + (e * 3 + 0) * 2 * (L + 1);
-        const float* M2 = m2 + e * n * n;
-        float va = 0.f, vb = 0.f;
-        for (int k = 0; k < n; ++k) {
-          va = fmaf(J[i * n + k], M2[k * n + j], va);
-          vb = fmaf(J[ii * n + k], M2[k * n + j], vb);
-        }
-        float v = va;
-        if (i != l) {
-          const int f = l - i;
-          v = xcos(ta, f) * va + xsin(ta + (L + 1), f) * vb;
-        }
-        s.D[e * P::DS + dof + qi * n + j] = v;
-      }
-      __syncthreads();
-    }
-  }
-
   // ------------------------------------------------------------ prologue
+  // A fragments of one K step: for every kept row type q of degree LI and
+  // 32-edge row tile rt, lane (row, half) copies 16 bytes of the rotated rows
+  // (channels c0 + half * VEC ...) straight into fragment order.
   template <int LI>
-  static __device__ __forceinline__ void stage_a(Smem& s, const Args& a, int tid, int c0, int cb) {
-    constexpr int n = 2 * LI + 1;
+  static __device__ __forceinline__ void stage_a(Smem& s, const Args& a, int wave, int lane,
+                                                 int c0) {
     constexpr int nql = P::nq(LI);
-    if (tid >= TE * TPE) return;
-    const int e = tid / TPE, part = tid % TPE;
-    const int cbase = c0 + part * CPT;
-    const bool valid = s.eid[e] >= 0;
-    float xv[n][CPT];
-    if (valid) {
-      const typename TX::raw* xp = reinterpret_cast<const typename TX::raw*>(a.x) +
-                                   (static_cast<int64_t>(s.gid[e]) * d + LI * LI) * a.C_k + cbase;
-#pragma unroll
-      for (int j = 0; j < n; ++j)
-#pragma unroll
-        for (int c = 0; c < CPT; ++c) xv[j][c] = TX::load(xp + j * a.C_k + c);
-    } else {
-#pragma unroll
-      for (int j = 0; j < n; ++j)
-#pragma unroll
-        for (int c = 0; c < CPT; ++c) xv[j][c] = 0.f;
-    }
-    const float* Dl = s.D + e * P::DS + P::doff(LI);
-    const typename TM::raw* rp = nullptr;
-    if (MODE == FWD && a.rad != nullptr && valid)
-      rp = reinterpret_cast<const typename TM::raw*>(a.rad) +
-           static_cast<int64_t>(s.eid[e]) * rad_width<L, M>(a.C_k);
-    const int rt = e >> 5, row = e & 31;
-#pragma unroll
-    for (int q = 0; q < nql; ++q) {
-#pragma unroll
-      for (int c = 0; c < CPT; ++c) {
-        float v = 0.f;
-#pragma unroll
-        for (int j = 0; j < n; ++j) v = fmaf(Dl[q * n + j], xv[j][c], v);
-        if (rp) v *= TM::load(rp + rad_slot<L, M>(q, LI, cbase + c, a.C_k));
-        if (a.save_a != nullptr && cb == 0 && valid)
-          reinterpret_cast<typename TM::raw*>(a.save_a)[(static_cast<int64_t>(s.eid[e]) * P::DP +
-                                                         P::mrow(q, LI)) * a.C_k + cbase + c] = TM::cvt(v);
-        const int k = part * CPT + c;
-        *reinterpret_cast<typename TM::raw*>(s.stage + (q * RT + rt) * FRAG + frag_off<TM>(row, k)) =
-            TM::cvt(v);
+    const int row = lane & 31, half = lane >> 5;
+    for (int f = wave; f < nql * RT; f += NW) {
+      const int q = f / RT, rt = f % RT;
+      const int e = rt * 32 + row;
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (s.eid[e] >= 0) {
+        const typename TM::raw* src = reinterpret_cast<const typename TM::raw*>(a.a_src) +
+                                      (static_cast<int64_t>(s.eid[e]) * P::DP + P::mrow(q, LI)) * a.C_k +
+                                      c0 + half * TM::VEC;
+        v = *reinterpret_cast<const uint4*>(src);
       }
+      *reinterpret_cast<uint4*>(s.stage + (q * RT + rt) * FRAG + lane * 16) = v;
     }
   }
 
@@ -403,7 +324,7 @@ struct Kernel {
     const char* wbase = a.wpack + (static_cast<int64_t>(cb) * a.frags_per_cb + foff) * FRAG;
     constexpr int nb = P::nbfrag(LI);
     for (int ks = 0; ks < nks; ++ks) {
-      stage_a<LI>(s, a, tid, ks * KC, cb);
+      stage_a<LI>(s, a, wave, lane, ks * KC);
       stage_b(s, wbase + static_cast<int64_t>(ks) * nb * FRAG, nb, tid);
       __syncthreads();
       mma_dispatch<LI>(acc, s, wave, lane);
@@ -507,38 +428,27 @@ struct Kernel {
   }
 
   // BWD_DX: the accumulators hold dY on the forward-input side of degree l.
-  // Writes d(rad) = sum_(+/-) dY * R (R = kept rows of D x[src], recomputed)
-  // and scales dY by rad before the inverse rotation.
+  // Writes d(rad) = sum_(+/-) dY * R (R: unscaled rotated forward inputs, saved
+  // by the forward) and scales dY by rad before the inverse rotation.
   template <int l, int rt, int sb>
   static __device__ __forceinline__ void bwd_radial(f32x16 (&acc)[P::MS], Smem& s, const Args& a,
                                                     int col, int lane) {
     if (a.rad == nullptr) return;
-    constexpr int n = 2 * l + 1;
     const int64_t rw = rad_width<L, M>(a.C_n);
-static_for<16>([&](auto II) {
+    static_for<16>([&](auto II) {
       constexpr int i = decltype(II)::value;
       const int e = rt * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
       if (s.eid[e] < 0) return;
       const int64_t eo = static_cast<int64_t>(s.eid[e]) * rw;
       const typename TM::raw* rp = reinterpret_cast<const typename TM::raw*>(a.rad) + eo;
-      float xv[n];
-      const typename TM::raw* xp = reinterpret_cast<const typename TM::raw*>(a.xsrc) +
-                                   (static_cast<int64_t>(s.xid[e]) * d + l * l) * a.C_n + col;
-#pragma unroll
-      for (int j = 0; j < n; ++j) xv[j] = TM::load(xp + static_cast<int64_t>(j) * a.C_n);
-      const float* Dl = s.D + e * P::DS + P::doff(l);
-      float rq[P::nq(l)];
-#pragma unroll
-      for (int q = 0; q < P::nq(l); ++q) {
-        float v = 0.f;
-#pragma unroll
-        for (int j = 0; j < n; ++j) v = fmaf(Dl[q * n + j], xv[j], v);
-        rq[q] = v;
-      }
+      const typename TM::raw* rs = reinterpret_cast<const typename TM::raw*>(a.rsave) +
+                                   static_cast<int64_t>(s.eid[e]) * P::DP * a.C_n + col;
       {
         const int slot = rad_slot<L, M>(0, l, col, a.C_n);
         const float dy = acc[sb][i];
-        if (a.drad) reinterpret_cast<typename TM::raw*>(a.drad)[eo + slot] = TM::cvt(dy * rq[0]);
+        if (a.drad)
+          reinterpret_cast<typename TM::raw*>(a.drad)[eo + slot] =
+              TM::cvt(dy * TM::load(rs + P::mrow(0, l) * a.C_n));
         acc[sb][i] = dy * TM::load(rp + slot);
       }
       static_for<M>([&](auto MI) {
@@ -549,7 +459,8 @@ static_for<16>([&](auto II) {
           const float dyp = acc[sb + 1 + 2 * (m - 1)][i], dym = acc[sb + 2 + 2 * (m - 1)][i];
           if (a.drad)
             reinterpret_cast<typename TM::raw*>(a.drad)[eo + slot] =
-                TM::cvt(dyp * rq[2 * m - 1] + dym * rq[2 * m]);
+                TM::cvt(dyp * TM::load(rs + P::mrow(2 * m - 1, l) * a.C_n) +
+                        dym * TM::load(rs + P::mrow(2 * m, l) * a.C_n));
           acc[sb + 1 + 2 * (m - 1)][i] = dyp * r;
           acc[sb + 2 + 2 * (m - 1)][i] = dym * r;
         }
@@ -587,25 +498,22 @@ static_for<16>([&](auto II) {
     if (tile >= a.ntiles) return;  // whole workgroup exits together
     const int64_t e0 = tile * TE;
     const int nvalid = static_cast<int>((a.E - e0) < TE ? (a.E - e0) : TE);
-    for (int i = tid; i < jd_size(L); i += NT) s.J[i] = a.jd[i];
     if (tid < TE) {
       const bool v = tid < nvalid;
       const int64_t p = e0 + tid;
-      const int ei = v ? (a.eidx ? a.eidx[p] : static_cast<int>(p)) : -1;
       s.seg[tid] = v ? a.seg[p] : -1;
-      s.gid[tid] = v ? a.gidx[p] : 0;
-      s.eid[tid] = ei;
-      s.xid[tid] = (v && a.xsrc_idx) ? a.xsrc_idx[p] : 0;
-      s.eul[tid * 3 + 0] = v ? a.eulers[static_cast<int64_t>(ei) * 3 + 0] : 0.f;
-      s.eul[tid * 3 + 1] = v ? a.eulers[static_cast<int64_t>(ei) * 3 + 1] : 0.f;
-      s.eul[tid * 3 + 2] = v ? a.eulers[static_cast<int64_t>(ei) * 3 + 2] : 0.f;
+      s.eid[tid] = v ? (a.eidx ? a.eidx[p] : static_cast<int>(p)) : -1;
+    }
+    __syncthreads();
+    // kept Wigner rows of the tile's edges
+    for (int i = tid; i < TE * P::DS; i += NT) {
+      const int e = i / P::DS, k = i - e * P::DS;
+      s.D[i] = s.eid[e] >= 0 ? a.dk[static_cast<int64_t>(s.eid[e]) * P::DS + k] : 0.f;
     }
     __syncthreads();
     const bool first_partial = (e0 > 0) && (a.seg[e0 - 1] == a.seg[e0]);
     const bool last_partial =
         (e0 + nvalid < a.E) && (a.seg[e0 + nvalid] == a.seg[e0 + nvalid - 1]);
-    build_d(s, tid);
-
     f32x16 acc[P::MS];
 #pragma unroll
     for (int k = 0; k < P::MS; ++k)
@@ -631,3 +539,211 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 ? 2 : 1)) void message_kernel(Arg
 }  // namespace msg
 }  // namespace maloq
 
+
+namespace maloq {
+namespace msg {
+
+// --------------------------------------------------------------- edge prep
+// Per edge, once: the kept rows |m| <= mmax of its Wigner-D (from the Euler
+// triple) and the rotated, optionally radially scaled operand of the SO(2)
+// GEMM,  Y[e, (m, l), c] = sum_j D_l[e][(m), j] x[g(e), l^2 + j, c] (* rad),
+// stored m-major by edge id ([E, d', C]), which is also the saved input of
+// the weight gradient.  Replaces the bmm(wigner) + einsum(to_m) of
+// esen_block.py:181,184 (and, with x = dL/dout gathered by dst, the rotation
+// of the output gradient in the backward).
+struct PrepArgs {
+  const void* x;        // [N, d, C] (TX raw)
+  const int32_t* gidx;  // [E] gather row per kernel-order edge
+  const int32_t* eidx;  // [E] nullable: edge id per kernel-order edge
+  const float* eulers;  // [E_all, 3] by edge id
+  const void* rad;      // [E_all, KR] (TM raw) or null
+  const float* jd;      // packed J_0..J_L
+  void* y;              // [E_all, d', C] (TM raw) by edge id
+  void* r;              // nullable: unscaled rows, same layout
+  float* dk;            // [E_all, DS] kept Wigner rows by edge id
+  int build_d;          // 1: compute and write dk; 0: read dk
+  int64_t E;
+  int C;
+};
+
+template <class TX, int V>
+__device__ __forceinline__ void load_vec(const typename TX::raw* p, float (&o)[V]);
+template <>
+__device__ __forceinline__ void load_vec<BF16, 8>(const uint16_t* p, float (&o)[8]) {
+  const uint4 v = *reinterpret_cast<const uint4*>(p);
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    o[2 * k] = __uint_as_float(w[k] << 16);
+    o[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+  }
+}
+template <>
+__device__ __forceinline__ void load_vec<F32, 8>(const float* p, float (&o)[8]) {
+  const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+  o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+}
+template <>
+__device__ __forceinline__ void load_vec<F32, 4>(const float* p, float (&o)[4]) {
+  const float4 a = *reinterpret_cast<const float4*>(p);
+  o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+}
+
+template <class TM, int V>
+__device__ __forceinline__ void store_vec(typename TM::raw* p, const float (&v)[V]);
+template <>
+__device__ __forceinline__ void store_vec<BF16, 8>(uint16_t* p, const float (&v)[8]) {
+  uint4 w;
+  w.x = f32_to_bf16(v[0]) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
+  w.y = f32_to_bf16(v[2]) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
+  w.z = f32_to_bf16(v[4]) | (static_cast<uint32_t>(f32_to_bf16(v[5])) << 16);
+  w.w = f32_to_bf16(v[6]) | (static_cast<uint32_t>(f32_to_bf16(v[7])) << 16);
+  *reinterpret_cast<uint4*>(p) = w;
+}
+template <>
+__device__ __forceinline__ void store_vec<F32, 4>(float* p, const float (&v)[4]) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
+template <int L, int M, class TM, class TX>
+struct Prep {
+  static constexpr int TE = 32;
+  static constexpr int NT = 256;
+  using P = Plan<L, M, false, 4, 1>;
+  static constexpr int d = (L + 1) * (L + 1);
+  static constexpr int V = TM::VEC;
+
+  struct Smem {
+    float J[jd_size(L)];
+    float D[TE * P::DS];
+    float eul[TE * 3];
+    int gid[TE];
+    int eid[TE];
+    float m2[TE * (2 * L + 1) * (2 * L + 1)];
+    float trig[TE * 3 * 2 * (L + 1)];
+  };
+
+  static __device__ void build_d(Smem& s, int tid) {
+    for (int q = tid; q < TE * 3 * (L + 1); q += NT) {
+      const int e = q / (3 * (L + 1)), r = q % (3 * (L + 1));
+      const int ang = r / (L + 1), m = r % (L + 1);
+      float sn, cs;
+      sincosf(static_cast<float>(m) * s.eul[e * 3 + ang], &sn, &cs);
+      s.trig[(e * 3 + ang) * 2 * (L + 1) + m] = cs;
+      s.trig[(e * 3 + ang) * 2 * (L + 1) + (L + 1) + m] = sn;
+    }
+    __syncthreads();
+    for (int l = 0; l <= L; ++l) {
+      const int n = 2 * l + 1;
+      const float* J = s.J + jd_offset(l);
+      for (int q = tid; q < TE * n; q += NT) {
+        const int e = q / n, k = q % n;
+        const float* tb = s.trig + (e * 3 + 1) * 2 * (L + 1);
+        const float* tc = s.trig + (e * 3 + 2) * 2 * (L + 1);
+        wigner_m2_row(l, k, J, tb, tb + (L + 1), tc, tc + (L + 1), s.m2 + (e * n + k) * n);
+      }
+      __syncthreads();
+      const int nql = P::nq(l);
+      const int dof = P::doff(l);
+      for (int q = tid; q < TE * nql * n; q += NT) {
+        const int e = q / (nql * n), r = q % (nql * n);
+        const int qi = r / n, j = r % n;
+        const int mm = (qi + 1) >> 1;
+        const int i = (qi == 0) ? l : ((qi & 1) ? l + mm : l - mm);
+        const int ii = 2 * l - i;
+        const float* ta = s.trig + (e * 3 + 0) * 2 * (L + 1);
+        const float* M2 = s.m2 + e * n * n;
+        float va = 0.f, vb = 0.f;
+        for (int k = 0; k < n; ++k) {
+          va = fmaf(J[i * n + k], M2[k * n + j], va);
+          vb = fmaf(J[ii * n + k], M2[k * n + j], vb);
+        }
+        float v = va;
+        if (i != l) {
+          const int f = l - i;
+          v = xcos(ta, f) * va + xsin(ta + (L + 1), f) * vb;
+        }
+        s.D[e * P::DS + dof + qi * n + j] = v;
+      }
+      __syncthreads();
+    }
+  }
+
+  static __device__ void run(const PrepArgs& a) {
+    __shared__ Smem s;
+    const int tid = threadIdx.x;
+    const int64_t e0 = static_cast<int64_t>(blockIdx.x) * TE;
+    const int nvalid = static_cast<int>((a.E - e0) < TE ? (a.E - e0) : TE);
+    for (int i = tid; i < jd_size(L); i += NT) s.J[i] = a.jd[i];
+    if (tid < TE) {
+      const bool v = tid < nvalid;
+      const int64_t p = e0 + tid;
+      const int ei = v ? (a.eidx ? a.eidx[p] : static_cast<int>(p)) : -1;
+      s.eid[tid] = ei;
+      s.gid[tid] = v ? a.gidx[p] : 0;
+      for (int k = 0; k < 3; ++k)
+        s.eul[tid * 3 + k] = (v && a.build_d) ? a.eulers[static_cast<int64_t>(ei) * 3 + k] : 0.f;
+    }
+    __syncthreads();
+    if (a.build_d) {
+      build_d(s, tid);
+      for (int i = tid; i < nvalid * P::DS; i += NT) {
+        const int e = i / P::DS, k = i - e * P::DS;
+        a.dk[static_cast<int64_t>(s.eid[e]) * P::DS + k] = s.D[i];
+      }
+    } else {
+      for (int i = tid; i < TE * P::DS; i += NT) {
+        const int e = i / P::DS, k = i - e * P::DS;
+        s.D[i] = s.eid[e] >= 0 ? a.dk[static_cast<int64_t>(s.eid[e]) * P::DS + k] : 0.f;
+      }
+      __syncthreads();
+    }
+    const int nch = a.C / V;
+    const int64_t rw = rad_width<L, M>(a.C);
+    for (int u = tid; u < nvalid * nch; u += NT) {
+      const int e = u / nch, c0 = (u - e * nch) * V;
+      const int64_t eid = s.eid[e];
+      const typename TX::raw* xg = reinterpret_cast<const typename TX::raw*>(a.x) +
+                                   static_cast<int64_t>(s.gid[e]) * d * a.C + c0;
+      typename TM::raw* yo = reinterpret_cast<typename TM::raw*>(a.y) + eid * P::DP * a.C + c0;
+      typename TM::raw* ro = a.r ? reinterpret_cast<typename TM::raw*>(a.r) + eid * P::DP * a.C + c0 : nullptr;
+      const typename TM::raw* rp = a.rad ? reinterpret_cast<const typename TM::raw*>(a.rad) + eid * rw + c0 : nullptr;
+      static_for<L + 1>([&](auto LI) {
+        constexpr int l = decltype(LI)::value;
+        constexpr int n = 2 * l + 1;
+        float xv[n][V];
+#pragma unroll
+        for (int j = 0; j < n; ++j) load_vec<TX, V>(xg + (l * l + j) * a.C, xv[j]);
+        const float* Dl = s.D + e * P::DS + P::doff(l);
+#pragma unroll
+        for (int q = 0; q < P::nq(l); ++q) {
+          float o[V];
+#pragma unroll
+          for (int c = 0; c < V; ++c) {
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 0; j < n; ++j) acc = fmaf(Dl[q * n + j], xv[j][c], acc);
+            o[c] = acc;
+          }
+          const int64_t ro_off = static_cast<int64_t>(P::mrow(q, l)) * a.C;
+          if (ro) store_vec<TM, V>(ro + ro_off, o);
+          if (rp) {
+            float rv[V];
+            load_vec<TM, V>(rp + rad_slot<L, M>(q, l, 0, a.C), rv);
+#pragma unroll
+            for (int c = 0; c < V; ++c) o[c] *= rv[c];
+          }
+          store_vec<TM, V>(yo + ro_off, o);
+        }
+      });
+    }
+  }
+};
+
+template <int L, int M, class TM, class TX>
+__global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
+  Prep<L, M, TM, TX>::run(a);
+}
+
+}  // namespace msg
+}  // namespace maloq

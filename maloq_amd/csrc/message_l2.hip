@@ -9,5 +9,10 @@ int launch_l2(int mmax, int dtype, int gate, int mode, const Args& a, hipStream_
   return launch_lm<2, 2>(dtype, gate, mode, a, s);
 }
 
+int prep_l2(int mmax, int dtype, int mode, const PrepArgs& a, hipStream_t s) {
+  MALOQ_REQUIRE(mmax == 2, "lmax=2: built for mmax = 2 only, got %d", mmax);
+  return prep_lm<2, 2>(dtype, mode, a, s);
+}
+
 }  // namespace msg
 }  // namespace maloq

@@ -41,13 +41,33 @@ int launch_lm(int dtype, int gate, int mode, const Args& a, hipStream_t s) {
     return gate ? launch<L, M, true, F32, F32, FWD>(a, s) : launch<L, M, false, F32, F32, FWD>(a, s);
   }
   MALOQ_REQUIRE(!gate, "gated backward is not implemented");
-  if (dtype == 1) return launch<L, M, false, BF16, F32, BWD_DX>(a, s);
+  if (dtype == 1) return launch<L, M, false, BF16, BF16, BWD_DX>(a, s);
   return launch<L, M, false, F32, F32, BWD_DX>(a, s);
+}
+
+// Edge prep: mode FWD gathers x (dtype) and applies rad; mode BWD_DX gathers
+// fp32 output gradients and writes dtype rows.
+template <int L, int M>
+int prep_lm(int dtype, int mode, const PrepArgs& a, hipStream_t s) {
+  const int64_t grid = (a.E + 31) / 32;
+  MALOQ_REQUIRE(grid < (int64_t(1) << 31), "grid too large");
+  if (dtype == 1) {
+    if (mode == FWD)
+      hipLaunchKernelGGL((prep_kernel<L, M, BF16, BF16>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((prep_kernel<L, M, BF16, F32>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((prep_kernel<L, M, F32, F32>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);
+  }
+  return check_launch("prep_kernel");
 }
 
 int launch_l2(int mmax, int dtype, int gate, int mode, const Args& a, hipStream_t s);
 int launch_l4(int mmax, int dtype, int gate, int mode, const Args& a, hipStream_t s);
 int launch_l6(int mmax, int dtype, int gate, int mode, const Args& a, hipStream_t s);
+int prep_l2(int mmax, int dtype, int mode, const PrepArgs& a, hipStream_t s);
+int prep_l4(int mmax, int dtype, int mode, const PrepArgs& a, hipStream_t s);
+int prep_l6(int mmax, int dtype, int mode, const PrepArgs& a, hipStream_t s);
 
 }  // namespace msg
 }  // namespace maloq

@@ -101,7 +101,7 @@ def _pack_index(dtype_code, lmax, mmax, gate, c_in, c_out, mode):
         k_of = (e // 256) * 8 + (e % 8)
         col_of = (e // 8) % 32
     else:
-        k_of = 2 * (e % 4) + (e // 128)
+        k_of = (e // 128) * 4 + (e % 4)
         col_of = (e // 4) % 32
     c_k, c_n = (c_in, c_out) if mode == 0 else (c_out, c_in)
     idx_parts, sgn_parts = [], []
@@ -184,10 +184,17 @@ def kept_rows(lmax, mmax):
     return (lmax + 1) + sum(2 * (lmax - m + 1) for m in range(1, mmax + 1))
 
 
+def wigner_floats(lmax, mmax):
+    return sum((1 + 2 * min(mmax, l)) * (2 * l + 1) for l in range(lmax + 1))
+
+
 def message_forward(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=False, wpack=None,
-                    save_y=None):
+                    save=None):
     """Node output [N, d, c_out] fp32 of the fused block (no autograd).
-    ``save_y`` [E, d', c_in] (x dtype) receives the SO(2) layer's input rows."""
+
+    ``save``: dict that receives the workspaces kept for the backward
+    ("y" rotated scaled rows, "r" unscaled rows if ``rad`` is given, "dk" the
+    kept Wigner-D rows), all indexed by dst-sorted edge position."""
     dt = x.dtype
     if dt not in DTYPE_CODE:
         raise ValueError(f"unsupported dtype {dt}")
@@ -199,52 +206,57 @@ def message_forward(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=False, wp
     if wpack is None:
         wpack = pack_weights(w0, wm, lmax, mmax, gate, c_in, c_out, dt, 0)
     E = plan.num_edges
-    out = torch.empty(plan.num_nodes, d, c_out, device=x.device, dtype=torch.float32)
+    dev = x.device
+    out = torch.empty(plan.num_nodes, d, c_out, device=dev, dtype=torch.float32)
     lib = _lib.load()
     parts = torch.empty(max(1, lib.maloq_message_partials_floats(lmax, int(gate), E, c_out)),
-                        device=x.device, dtype=torch.float32)
+                        device=dev, dtype=torch.float32)
     if rad is not None:
         assert rad.shape == (E, rad_width(lmax, mmax, c_in)), "rad must be [E, sum_m (lmax-m+1) C_in]"
         rad = rad.to(dt).contiguous()
+    y = torch.empty(max(E, 1), kept_rows(lmax, mmax), c_in, device=dev, dtype=dt)
+    r = torch.empty_like(y) if (save is not None and rad is not None) else None
+    dk = torch.empty(max(E, 1), wigner_floats(lmax, mmax), device=dev, dtype=torch.float32)
     bias = b0.float().contiguous() if b0 is not None else None
     xc = x.contiguous()
     eul = eulers.float().contiguous()
     _lib.call("maloq_message_fwd", DTYPE_CODE[dt], lmax, mmax, int(gate), _lib.ptr(xc), c_in,
-              _lib.ptr(plan.src), _lib.ptr(plan.dst), None, E, _lib.ptr(eul), _lib.ptr(rad),
-              _lib.ptr(wpack), _lib.ptr(bias), _lib.ptr(_jd_dev(lmax, x.device)), _lib.ptr(out),
-              plan.num_nodes, c_out, _lib.ptr(plan.seg_ptr), _lib.ptr(parts), _lib.ptr(save_y),
-              _lib.stream_of(x.device))
+              _lib.ptr(plan.src), _lib.ptr(plan.dst), E, _lib.ptr(eul), _lib.ptr(rad),
+              _lib.ptr(wpack), _lib.ptr(bias), _lib.ptr(_jd_dev(lmax, dev)), _lib.ptr(out),
+              plan.num_nodes, c_out, _lib.ptr(plan.seg_ptr), _lib.ptr(parts), _lib.ptr(y),
+              _lib.ptr(r), _lib.ptr(dk), _lib.stream_of(dev))
+    if save is not None:
+        save.update(y=y, r=r, dk=dk)
     return out
 
 
-def message_backward_dx(grad_out, x, plan, eulers, rad, w0, wm, lmax, mmax, wpack_t=None,
-                        need_rad_grad=True, save_dz=None):
-    """(grad_x fp32 [N, d, c_in], grad_rad [E, KR] or None) of the ungated block.
-    ``save_dz`` [E, d', c_out] (x dtype) receives the rotated output-gradient rows."""
-    dt = x.dtype
-    N, d, c_in = x.shape
+def message_backward_dx(grad_out, x_shape, dt, plan, saved, rad, w0, wm, lmax, mmax,
+                        wpack_t=None, need_rad_grad=True):
+    """(grad_x fp32 [N, d, c_in], grad_rad or None, dz [E, d', c_out]) of the
+    ungated block, from the forward's saved workspaces."""
+    N, d, c_in = x_shape
     c_out = grad_out.shape[2]
+    dev = grad_out.device
     if wpack_t is None:
         wpack_t = pack_weights(w0, wm, lmax, mmax, False, c_in, c_out, dt, 1)
     E = plan.num_edges
-    gx = torch.empty(N, d, c_in, device=x.device, dtype=torch.float32)
+    gx = torch.empty(N, d, c_in, device=dev, dtype=torch.float32)
     lib = _lib.load()
     parts = torch.empty(max(1, lib.maloq_message_partials_floats(lmax, 0, E, c_in)),
-                        device=x.device, dtype=torch.float32)
+                        device=dev, dtype=torch.float32)
     grad_rad = None
     if rad is not None:
         rad = rad.to(dt).contiguous()
         if need_rad_grad:
             grad_rad = torch.empty_like(rad)
+    dz = torch.empty(max(E, 1), kept_rows(lmax, mmax), c_out, device=dev, dtype=dt)
     g = grad_out.float().contiguous()
-    eul = eulers.float().contiguous()
-    xc = x.contiguous()
     _lib.call("maloq_message_bwd_dx", DTYPE_CODE[dt], lmax, mmax, _lib.ptr(g), c_out,
               _lib.ptr(plan.bwd_dst), _lib.ptr(plan.bwd_src), _lib.ptr(plan.bwd_eidx), E,
-              _lib.ptr(eul), _lib.ptr(rad), _lib.ptr(grad_rad), _lib.ptr(xc), _lib.ptr(wpack_t),
-              _lib.ptr(_jd_dev(lmax, x.device)), _lib.ptr(gx), N, c_in, _lib.ptr(plan.seg_ptr_src),
-              _lib.ptr(parts), _lib.ptr(save_dz), _lib.stream_of(x.device))
-    return gx, grad_rad
+              _lib.ptr(saved["dk"]), _lib.ptr(rad), _lib.ptr(grad_rad), _lib.ptr(saved.get("r")),
+              _lib.ptr(wpack_t), _lib.ptr(_jd_dev(lmax, dev)), _lib.ptr(gx), N, c_in,
+              _lib.ptr(plan.seg_ptr_src), _lib.ptr(parts), _lib.ptr(dz), _lib.stream_of(dev))
+    return gx, grad_rad, dz
 
 
 def message_weight_grad(dz, y, lmax, mmax, c_out, c_in, splits=None):
@@ -272,32 +284,34 @@ class _MessageBlockFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, rad, w0, b0, plan, eulers, lmax, mmax, *wm):
-        dt = x.dtype
-        need_w = ctx.needs_input_grad[2] or ctx.needs_input_grad[3] or any(ctx.needs_input_grad[8:])
-        E = plan.num_edges
-        y = torch.empty(E, kept_rows(lmax, mmax), x.shape[2], device=x.device, dtype=dt) if need_w else None
-        out = message_forward(x, plan, eulers, rad, w0, b0, list(wm), lmax, mmax, gate=False, save_y=y)
+        saved = {}
+        out = message_forward(x, plan, eulers, rad, w0, b0, list(wm), lmax, mmax, gate=False, save=saved)
         ctx.plan, ctx.lmax, ctx.mmax, ctx.has_b0 = plan, lmax, mmax, b0 is not None
-        ctx.save_for_backward(x, rad, eulers, w0, y, *wm)
+        ctx.x_shape, ctx.dt = tuple(x.shape), x.dtype
+        ctx.has_r = saved["r"] is not None
+        ctx.save_for_backward(rad, w0, saved["y"], saved["dk"], saved["r"] if ctx.has_r else None, *wm)
         return out
 
     @staticmethod
     def backward(ctx, g):
-        x, rad, eulers, w0, y, *wm = ctx.saved_tensors
+        rad, w0, y, dk, r, *wm = ctx.saved_tensors
         plan, lmax, mmax = ctx.plan, ctx.lmax, ctx.mmax
-        need_w = y is not None
-        dz = torch.empty(plan.num_edges, kept_rows(lmax, mmax), g.shape[2], device=g.device,
-                         dtype=x.dtype) if need_w else None
-        gx, grad_rad = message_backward_dx(g, x, plan, eulers, rad, w0, wm, lmax, mmax,
-                                           need_rad_grad=ctx.needs_input_grad[1], save_dz=dz)
+        gx, grad_rad, dz = message_backward_dx(g, ctx.x_shape, ctx.dt, plan, {"dk": dk, "r": r}, rad, w0,
+                                               wm, lmax, mmax, need_rad_grad=ctx.needs_input_grad[1])
+        need_w = ctx.needs_input_grad[2] or ctx.needs_input_grad[3] or any(ctx.needs_input_grad[8:])
         dw0 = db0 = None
         dwm = [None] * len(wm)
-        if need_w:
-            dw0, dwm, db0 = message_weight_grad(dz, y, lmax, mmax, g.shape[2], x.shape[2])
+        if need_w and plan.num_edges > 0:
+            dw0, dwm, db0 = message_weight_grad(dz[: plan.num_edges], y[: plan.num_edges], lmax, mmax,
+                                                g.shape[2], ctx.x_shape[2])
             dw0 = dw0.to(w0.dtype)
             dwm = [d.to(w.dtype) for d, w in zip(dwm, wm)]
             db0 = db0 if ctx.has_b0 else None
-        return (gx.to(x.dtype) if ctx.needs_input_grad[0] else None, grad_rad, dw0, db0, None, None,
+        elif need_w:
+            dw0 = torch.zeros_like(w0)
+            dwm = [torch.zeros_like(w) for w in wm]
+            db0 = torch.zeros((lmax + 1) * g.shape[2], device=g.device) if ctx.has_b0 else None
+        return (gx.to(ctx.dt) if ctx.needs_input_grad[0] else None, grad_rad, dw0, db0, None, None,
                 None, None, *dwm)
 
 
