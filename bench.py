@@ -189,14 +189,19 @@ def basis_timing(bw, reps=50):
     import numpy as np
     dev = bw["data"].device
     dev_args = tuple(torch.as_tensor(np.asarray(a, np.int32), device=dev) for a in args[:4])
+    # the row plan (per-structure: block bases and kinds, ordered by kind) is
+    # built once, like the message graph's sort; its cost is reported apart
+    make = lambda: hip.make_plan(bw["data"], *dev_args, t.orbital_template, block_data_offsets=bw["bdo"])
+    plan = make()
+    plan_s = kernel_time_events(make, max(1, reps // 5))
     out = hip.fock_to_irreps(bw["data"], *args, block_data_offsets=bw["bdo"])
     fwd = kernel_time_events(lambda: hip.fock_to_irreps(bw["data"], *dev_args, t.orbital_template,
-                                                        block_data_offsets=bw["bdo"]), reps)
+                                                        block_data_offsets=bw["bdo"], plan=plan), reps)
     back = torch.empty_like(bw["data"])
     inv = kernel_time_events(lambda: hip.irreps_to_fock(out, back, *dev_args, t.orbital_template,
-                                                        block_data_offsets=bw["bdo"]), reps)
+                                                        block_data_offsets=bw["bdo"], plan=plan), reps)
     rt = ((back - bw["data"]).abs().max() / bw["data"].abs().max()).item()
-    return fwd, inv, rt
+    return fwd, inv, rt, plan_s
 
 
 # ---------------------------------------------------------------- CPU legs
@@ -391,11 +396,11 @@ def main(argv=None):
             del w32
         print("[bench] basis transform (config 3) ...", file=sys.stderr, flush=True)
         bw = basis_workload()
-        tf, ti, rt = basis_timing(bw)
+        tf, ti, rt, tplan = basis_timing(bw)
         bpb = (bw["block_bytes"] + 4 * bw["T"] * bw["n_blocks"]) / bw["n_blocks"]
         result["basis_transform"] = {
             "metric": "H-blocks/s", "fwd": bw["n_blocks"] / tf, "inv": bw["n_blocks"] / ti,
-            "blocks": bw["n_blocks"], "round_trip_rel_err": rt,
+            "blocks": bw["n_blocks"], "round_trip_rel_err": rt, "plan_ms": tplan * 1e3,
             "roofline": {"bound": "hbm", "achieved": bpb * bw["n_blocks"] / tf / 1e9, "peak": PEAK_HBM / 1e9,
                          "unit": "GB/s", "frac": bpb * bw["n_blocks"] / tf / PEAK_HBM,
                          "bytes_per_block": bpb, "traffic": load_traffic("fock_to_irreps")},

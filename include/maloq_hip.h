@@ -55,52 +55,72 @@ int maloq_wigner_from_euler(const float* eulers, int64_t num_edges, int lmax,
 
 /* ------------------------------------------------------ basis transform -- */
 
-/* Block-sparse row transform on label rows:
- *   out[r, o] = sum_{k < len[o]} in[r, col(src[o] + k)] * w[woff[o] + k]
- * with col(c) = in_col_map ? in_col_map[c] : c.  in [R, t_in], out [R, t_out].
- * One call implements get_H (utils_tensor_decomp.py:154-161), get_net_out
- * (:163-169) and the get_H backward (basis_transform_triton_backend.py:1070-1073),
- * depending on the tables built by the host; sorted irreps via the maps.
+/* CG tables shared by the three transform entry points below.  The transform
+ * is block diagonal: CG block b (one shell pair l1 x l2) maps the n = (2l1+1)(2l2+1)
+ * columns col0 .. col0+n-1 of an unsorted label row to the same columns of the
+ * unsorted irreps row (and back).
+ *   blocks [nblocks, 3] = (n, col0, woff); the block matrix is w[woff + j*n + k]
+ *     (output column j, input column k), n in {1,3,5,7,9,15,21,25,35,49} (l <= 3);
+ *   sched  [5 + nblocks]: sched[0..4] are offsets into sched + 5 of the block ids
+ *     each of the 4 waves of a workgroup contracts (sched[4] = nblocks);
+ *   t      row width, at most 1279 (one 32-row tile of fp32 in LDS).
+ * Sorted irreps rows use perm (sorted column j <-> unsorted column perm[j]). */
+
+/* Label/irreps rows -> rows, [R, t] -> [R, t]:
+ *   out[r, j] = Y[r, perm_out ? perm_out[j] : j],  Y = blockdiag(W) X,
+ *   X[r, perm_in ? perm_in[j] : j] = in[r, j].
+ * With the host's tables one call implements get_net_out
+ * (utils_tensor_decomp.py:163-169), get_H (:154-161) and the get_H backward
+ * (basis_transform_triton_backend.py:1064-1073).
  * Replaces BalancedTritonE3TensorDecompL2._get_H_impl/_get_net_out_impl,
  * fock_utils/basis_transform_triton_backend.py:1366-1438 (kernels K6/K8). */
-int maloq_label_transform(const float* in, int64_t num_rows, int t_in, const int32_t* in_col_map,
-                          float* out, int t_out, const int32_t* ocol_src, const int32_t* ocol_len,
-                          const int32_t* ocol_woff, const float* w, int max_len, void* stream);
+int maloq_label_transform(const float* in, const int32_t* perm_in, float* out,
+                          const int32_t* perm_out, int64_t num_rows, int t, int nblocks,
+                          const int32_t* blocks, const float* w, const int32_t* sched,
+                          void* stream);
 
-/* Fused Fock -> irreps: gather every (row i, col j) atom-pair block of the
- * Fock matrix by its element-pair template and contract it with the CG tables.
- *   dense  (data_offsets == NULL): block at fock[off[i]*ld + off[j]], ld = row stride;
- *   sparse (data_offsets != NULL): block r at fock[data_offsets[r]], n_i x n_j row-major.
- * pair_kind: int32 [100*100] element-pair -> compact kind (-1 absent).
- * sub_origin: int32 [num_kinds, nblocks, 2] (r0, c0) of CG block b in that kind's
- * atom-pair block, or (-1, -1) if absent.  ocol_block/ocol_len/ocol_woff: per
- * output column its CG block, length n1*n2 and weight offset; block_n2 [nblocks].
+/* Row plan of the Fock-side transforms, int4 per atom pair r (i = rows[r],
+ * j = cols[r]): (base lo, base hi, r, (kind + 1) | n_i << 16 | n_j << 24), where
+ *   dense  (data_offsets == NULL): the block starts at fock[off[i]*ld + off[j]], row stride ld;
+ *   sparse (data_offsets != NULL): block r at fock[data_offsets[r]], n_j = off[j+1]-off[j]
+ *          columns, row-major (SparseBlockMatrix, matrix2labels_kernels.py:43-48);
+ * kind = pair_kind[Z_i*100 + Z_j] (-1: no template, the row is all zero), n_i, n_j <= 255,
+ * n_i * n_j <= maxe.  row_meta: [num_rows, 4] int32, 16-byte aligned.  The transforms
+ * below take the plan in any row order (the host orders it by kind); entry p of the
+ * plan reads and writes row r = plan[p].z.  Replaces the per-call index lists of
+ * cupy_single_matrix2label (matrix2labels_kernels.py:978-994). */
+int maloq_basis_row_meta(int64_t ld, const int64_t* data_offsets,
+                         const int32_t* fock_block_offsets, const int32_t* atomic_numbers,
+                         const int32_t* rows, const int32_t* cols, int64_t num_rows,
+                         const int32_t* pair_kind, int maxe, int32_t* row_meta, void* stream);
+
+/* Fused Fock -> irreps over a row plan: gather every atom-pair block into its
+ * label row, then get_net_out; out [R, t] in original row order.
+ * ld: the dense row stride, 0 for block-list storage (as in the plan).
+ * raw_slot [kinds, maxe]: element q = a*n_j + b of a block of that kind goes to label
+ * column raw_slot[kind*maxe + q], or nowhere if -1; label columns no element reaches
+ * are zero.  kind_blocks [kinds, 2] (or NULL): bit b set if the kind has CG block b
+ * (nblocks <= 64); blocks that no row of a 32-row tile has are skipped.
  * Replaces cupy_single_matrix2label(forward=True) + get_net_out,
  * fock_utils/matrix2labels_kernels.py:946-1036 (K12) / :1038-1115 (K13) and
  * fock_targets_batched.py:426-441. */
-int maloq_fock_to_irreps(const float* fock, int64_t ld, const int64_t* data_offsets,
-                         const int32_t* fock_block_offsets, const int32_t* atomic_numbers,
-                         const int32_t* rows, const int32_t* cols, int64_t num_rows,
-                         const int32_t* pair_kind, const int32_t* sub_origin, int nblocks,
-                         const int32_t* block_n2, float* out, int t_out, const int32_t* ocol_block,
-                         const int32_t* ocol_len, const int32_t* ocol_woff, const float* w,
-                         int max_block_elems, void* stream);
+int maloq_fock_to_irreps(const float* fock, int64_t ld, const int32_t* row_meta,
+                         int64_t num_rows, const int32_t* raw_slot, int maxe,
+                         const uint32_t* kind_blocks, float* out, const int32_t* perm_out,
+                         int t, int nblocks, const int32_t* blocks, const float* w,
+                         const int32_t* sched, void* stream);
 
-/* Fused irreps -> Fock: get_H per row, then scatter the covered entries of each
- * atom-pair block into the Fock storage (dense or block-sparse, as above).
- * hcol_block/hcol_src/hcol_len/hcol_woff: per H-space column its CG block, the
- * first irreps column, the length and the weight offset; hcol_pos [t_h]: the
- * flat position a*n2+b of the column inside its block.
+/* Fused irreps -> Fock over a row plan: get_H per row, then scatter the label
+ * columns that the row's element pair has into its atom-pair block (tables as
+ * above; every Fock entry is written by one (row, column), entries no template
+ * covers are left untouched).
  * Replaces get_H + cupy_single_matrix2label(forward=False),
  * train_utils/splittrainer.py:546-597 over matrix2labels_kernels.py:946-1036. */
-int maloq_irreps_to_fock(const float* irreps, int64_t num_rows, int t_in, float* fock,
-                         int64_t ld, const int64_t* data_offsets,
-                         const int32_t* fock_block_offsets, const int32_t* atomic_numbers,
-                         const int32_t* rows, const int32_t* cols, const int32_t* pair_kind,
-                         const int32_t* sub_origin, int nblocks, const int32_t* block_n2,
-                         int t_h, const int32_t* hcol_block, const int32_t* hcol_pos,
-                         const int32_t* hcol_src, const int32_t* hcol_len,
-                         const int32_t* hcol_woff, const float* w, void* stream);
+int maloq_irreps_to_fock(const float* irreps, const int32_t* perm_in, float* fock, int64_t ld,
+                         const int32_t* row_meta, int64_t num_rows, const int32_t* raw_slot,
+                         int maxe, const uint32_t* kind_blocks, int t, int nblocks,
+                         const int32_t* blocks, const float* w, const int32_t* sched,
+                         void* stream);
 
 /* Plain Fock <-> label copy (no CG), dense or block-sparse storage as above.
  * forward != 0: label[r, out0 + k] = block(r)[r0 + k/w, c0 + k%w];

@@ -27,11 +27,10 @@ SIGNATURES = {
     "maloq_edge_euler": [_p, _i64, _u64, _p, _p],
     "maloq_edge_vec_to_wigner": [_p, _i64, _u64, _i32, _p, _p, _p, _p, _i32, _p],
     "maloq_wigner_from_euler": [_p, _i64, _i32, _p, _p, _p, _i32, _p],
-    "maloq_label_transform": [_p, _i64, _i32, _p, _p, _i32, _p, _p, _p, _p, _i32, _p],
-    "maloq_fock_to_irreps": [_p, _i64, _p, _p, _p, _p, _p, _i64, _p, _p, _i32, _p, _p, _i32,
-                             _p, _p, _p, _p, _i32, _p],
-    "maloq_irreps_to_fock": [_p, _i64, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i32, _p,
-                             _i32, _p, _p, _p, _p, _p, _p, _p],
+    "maloq_label_transform": [_p, _p, _p, _p, _i64, _i32, _i32, _p, _p, _p, _p],
+    "maloq_basis_row_meta": [_i64, _p, _p, _p, _p, _p, _i64, _p, _i32, _p, _p],
+    "maloq_fock_to_irreps": [_p, _i64, _p, _i64, _p, _i32, _p, _p, _p, _i32, _i32, _p, _p, _p, _p],
+    "maloq_irreps_to_fock": [_p, _p, _p, _i64, _p, _i64, _p, _i32, _p, _i32, _i32, _p, _p, _p, _p],
     "maloq_matrix2label": [_p, _i64, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _i64, _i32, _p],
     "maloq_segment_sum": [_p, _p, _p, _i64, _i64, _p, _p],
     "maloq_message_partials_floats": [_i32, _i32, _i64, _i32],

@@ -34,6 +34,111 @@ def _i32(a, device):
     return torch.as_tensor(np.ascontiguousarray(np.asarray(a, dtype=np.int32)), device=device)
 
 
+# (2 l1 + 1)(2 l2 + 1) for l1, l2 <= 3: the block sizes the kernel is built for
+_SUPPORTED_N = frozenset((2 * a + 1) * (2 * b + 1) for a in range(4) for b in range(4))
+_WAVES = 4  # waves per workgroup of the transform kernel
+
+
+def _wave_schedule(sizes):
+    """Longest-processing-time split of the CG blocks over the 4 waves of a
+    workgroup (cost n^2 FMAs + 2n LDS accesses per row).  Layout: 5 offsets,
+    then the block ids of wave 0, wave 1, ..."""
+    load = [0] * _WAVES
+    lists = [[] for _ in range(_WAVES)]
+    for b in sorted(range(len(sizes)), key=lambda i: (-sizes[i], i)):
+        w = min(range(_WAVES), key=lambda k: (load[k], k))
+        lists[w].append(b)
+        load[w] += sizes[b] * sizes[b] + 2 * sizes[b]
+    offs = np.cumsum([0] + [len(x) for x in lists])
+    return np.concatenate([offs, np.concatenate([np.array(x, np.int64) for x in lists])]).astype(np.int32)
+
+
+def cg_block_tables(decomp_obj):
+    """Host tables of the transform kernels for an e3TensorDecomp (numpy):
+
+    * ``blocks`` [nblocks, 3] = (n, first column, weight offset);
+    * ``w_fwd`` / ``w_inv`` / ``w_adj``: the n x n block matrices, row-major
+      [output column][input column], of get_net_out (W[t][h] = wms_H[b] as
+      [n, n], utils_tensor_decomp.py:118), get_H (W[h][t] = wms[b] as [n, n],
+      :117) and the transpose of get_H's block (its adjoint);
+    * ``sched``: the per-wave block lists (_wave_schedule).
+    """
+    ins, hs = decomp_obj.in_slices, decomp_obj.H_slices
+    if list(map(int, ins)) != list(map(int, hs)):
+        raise ValueError("label and irreps sides of the CG blocks must share their columns")
+    blocks, w_fwd, w_inv, w_adj = [], [], [], []
+    woff = 0
+    for b in range(len(decomp_obj.out_js_list)):
+        n = int(ins[b + 1]) - int(ins[b])
+        if n not in _SUPPORTED_N:
+            raise ValueError(f"CG block {b} of size {n} is not a shell pair with l <= 3")
+        fwd = np.asarray(decomp_obj.wms_H[b].detach().cpu().double()).reshape(n, n)
+        inv = np.asarray(decomp_obj.wms[b].detach().cpu().double()).reshape(n, n)
+        blocks.append((n, int(ins[b]), woff))
+        w_fwd.append(fwd.reshape(-1)); w_inv.append(inv.reshape(-1)); w_adj.append(inv.T.reshape(-1))
+        woff += n * n
+    return {"blocks": np.array(blocks, np.int32), "sched": _wave_schedule([n for n, _, _ in blocks]),
+            "w_fwd": np.concatenate(w_fwd), "w_inv": np.concatenate(w_inv), "w_adj": np.concatenate(w_adj)}
+
+
+def template_slot_tables(orbital_template, h_slices):
+    """Per element-pair tables of a template (numpy):
+
+    * ``pair_kind`` [100*100]: element-pair key Z_i*100+Z_j -> kind, or -1;
+    * ``raw_slot`` [kinds, maxe]: element q = a * n_j + b of an atom-pair block of
+      that kind (row-major, n_i x n_j orbitals) goes to label column
+      raw_slot[kind, q], -1 if no shell pair of the template covers it.  The
+      columns are those of the template's row-major copies
+      (numpy_single_matrix2label, matrix2labels_kernels.py:1117-1170);
+      maxe = the largest n_i * n_j;
+    * ``kind_blocks`` [kinds, 2] uint32: bit b set if the kind has CG block b
+      (the block whose label columns start at h_slices[b]).
+    """
+    T = int(h_slices[-1])
+    starts = {int(x): b for b, x in enumerate(h_slices[:-1])}
+    pair_kind = np.full(MAX_ELEMENTS * MAX_ELEMENTS, -1, np.int32)
+    kinds, masks = [], []
+    for k, entries in enumerate(orbital_template):
+        if not entries:
+            continue
+        ni = max(rs.stop for rs, _, _ in entries)
+        nj = max(cs.stop for _, cs, _ in entries)
+        if ni > 255 or nj > 255:
+            raise ValueError("atom-pair blocks are limited to 255 x 255 orbitals")
+        sl = np.full(ni * nj, -1, np.int64)
+        mask = 0
+        for rs, cs, os_ in entries:
+            n1, n2 = rs.stop - rs.start, cs.stop - cs.start
+            if os_.stop - os_.start != n1 * n2 or os_.stop > T or int(os_.start) not in starts:
+                raise ValueError("orbital template entry does not match its CG block")
+            a_, b_ = np.meshgrid(np.arange(rs.start, rs.stop), np.arange(cs.start, cs.stop), indexing="ij")
+            sl[(a_ * nj + b_).reshape(-1)] = np.arange(os_.start, os_.stop)
+            mask |= 1 << starts[int(os_.start)]
+        pair_kind[k] = len(kinds)
+        kinds.append(sl)
+        masks.append(mask)
+    maxe = max([len(x) for x in kinds] + [1])
+    raw = np.full((max(len(kinds), 1), maxe), -1, np.int32)
+    for k, sl in enumerate(kinds):
+        raw[k, :len(sl)] = sl
+    kb = np.zeros((max(len(kinds), 1), 2), np.uint32)
+    for k, m in enumerate(masks):
+        kb[k, 0] = m & 0xFFFFFFFF
+        kb[k, 1] = (m >> 32) & 0xFFFFFFFF
+    return pair_kind, raw, kb
+
+
+class BasisPlan:
+    """Row plan of the Fock-side transforms for one structure: per atom pair the
+    block base, its original row index, element-pair kind and shape
+    (maloq_basis_row_meta), ordered by kind so that the 32-row tiles of the
+    transform hold one or a few element pairs.  Build it once per (index lists,
+    storage) and pass it to fock_to_irreps / irreps_to_fock."""
+
+    def __init__(self, meta, num_rows, ld, template_key):
+        self.meta, self.num_rows, self.ld, self.template_key = meta, num_rows, ld, template_key
+
+
 class _GetH(torch.autograd.Function):
     @staticmethod
     def forward(ctx, net_out, obj):
@@ -61,67 +166,14 @@ class HipE3TensorDecomp:
             # a reference e3TensorDecomp: read the permutation off its sort module
             eye = torch.eye(int(decomp_obj.in_slices[-1]), dtype=torch.float64)
             self.sort_perm = torch.argmax(decomp_obj.sort(eye.to(decomp_obj.device)).cpu(), dim=0).numpy()
-        wms = [np.asarray(w.detach().cpu().double()) for w in decomp_obj.wms]
-        wms_h = [np.asarray(w.detach().cpu().double()) for w in decomp_obj.wms_H]
-
-        # block geometry
-        self.block_n2 = np.array([(2 * (l2 % 10) + 1) for _, l2 in decomp_obj.out_js_list], np.int32)
-        in_block = np.zeros(self.total_in_dim, np.int32)
-        h_block = np.zeros(self.total_h_dim, np.int32)
-        for b in range(self.num_blocks):
-            in_block[ins[b]:ins[b + 1]] = b
-            h_block[hs[b]:hs[b + 1]] = b
-        self.h_block = h_block
-
-        # net_out (unsorted column c) from H:  W row = wms_H[b][t, :]
-        w_parts, src, ln, woff = [], [], [], []
-        off = 0
-        for c in range(self.total_in_dim):
-            b = in_block[c]
-            t = c - ins[b]
-            row = wms_h[b].reshape(ins[b + 1] - ins[b], -1)[t]
-            w_parts.append(row); src.append(hs[b]); ln.append(len(row)); woff.append(off)
-            off += len(row)
-        netout_tab = (np.array(src), np.array(ln), np.array(woff), np.concatenate(w_parts))
-        # H column from net_out:  W row = wms[b][h, :]
-        w_parts, src, ln, woff = [], [], [], []
-        off = 0
-        for c in range(self.total_h_dim):
-            b = h_block[c]
-            h = c - hs[b]
-            row = wms[b].reshape(hs[b + 1] - hs[b], -1)[h]
-            w_parts.append(row); src.append(ins[b]); ln.append(len(row)); woff.append(off)
-            off += len(row)
-        geth_tab = (np.array(src), np.array(ln), np.array(woff), np.concatenate(w_parts))
-        # adjoint of get_H:  net_out grad column c = sum_h gH[h] wms[b][h, t]
-        w_parts, src, ln, woff = [], [], [], []
-        off = 0
-        for c in range(self.total_in_dim):
-            b = in_block[c]
-            t = c - ins[b]
-            col = wms[b].reshape(hs[b + 1] - hs[b], -1)[:, t]
-            w_parts.append(col); src.append(hs[b]); ln.append(len(col)); woff.append(off)
-            off += len(col)
-        adj_tab = (np.array(src), np.array(ln), np.array(woff), np.concatenate(w_parts))
-
-        perm = self.sort_perm
+        tabs = cg_block_tables(decomp_obj)
         dev = self.device
-
-        def upload(tab, rows=None):
-            s, l_, w_o, w = tab
-            if rows is not None:
-                s, l_, w_o = s[rows], l_[rows], w_o[rows]
-            return (_i32(s, dev), _i32(l_, dev), _i32(w_o, dev),
-                    torch.as_tensor(w.astype(np.float32), device=dev), int(np.max(l_)))
-
-        self._netout = upload(netout_tab, perm)
-        self._adj = upload(adj_tab, perm)
-        self._geth = upload(geth_tab)
-        # get_H reads sorted input: unsorted column c lives at sorted position inv[c]
-        self._geth_in_map = _i32(np.argsort(perm), dev) if perm is not None else None
-        self._netout_block = _i32(in_block if perm is None else in_block[perm], dev)
-        self._h_tabs = None
-        self.block_n2_dev = _i32(self.block_n2, dev)
+        self._blocks = _i32(tabs["blocks"].reshape(-1), dev)
+        self._sched = _i32(tabs["sched"], dev)
+        f32 = lambda a: torch.as_tensor(a.astype(np.float32), device=dev)
+        self._w_fwd, self._w_inv, self._w_adj = f32(tabs["w_fwd"]), f32(tabs["w_inv"]), f32(tabs["w_adj"])
+        self._perm = _i32(self.sort_perm, dev) if self.sort_perm is not None else None
+        self.block_n2 = np.array([(2 * (l2 % 10) + 1) for _, l2 in decomp_obj.out_js_list], np.int32)
         self._templates = {}
 
     @property
@@ -136,30 +188,28 @@ class HipE3TensorDecomp:
         if x.dim() != 2 or x.shape[1] != width:
             raise ValueError(f"expected [R, {width}], got {tuple(x.shape)}")
 
-    def _transform(self, x, tab, t_out, in_map=None):
-        src, ln, woff, w, mx = tab
+    def _transform(self, x, w, perm_in=None, perm_out=None):
         x = x.contiguous()
-        out = torch.empty(x.shape[0], t_out, device=x.device, dtype=torch.float32)
-        if x.shape[0]:
-            _lib.call("maloq_label_transform", _lib.ptr(x), x.shape[0], x.shape[1], _lib.ptr(in_map),
-                      _lib.ptr(out), t_out, _lib.ptr(src), _lib.ptr(ln), _lib.ptr(woff), _lib.ptr(w),
-                      mx, _lib.stream_of(x.device))
+        out = torch.empty_like(x)
+        _lib.call("maloq_label_transform", _lib.ptr(x), _lib.ptr(perm_in), _lib.ptr(out), _lib.ptr(perm_out),
+                  x.shape[0], x.shape[1], self.num_blocks, _lib.ptr(self._blocks), _lib.ptr(w),
+                  _lib.ptr(self._sched), _lib.stream_of(x.device))
         return out
 
     def _get_H_impl(self, net_out):
         self._check(net_out, self.total_in_dim)
-        return self._transform(net_out, self._geth, self.total_h_dim, self._geth_in_map)
+        return self._transform(net_out, self._w_inv, perm_in=self._perm)
 
     def _get_H_adjoint(self, grad):
         self._check(grad, self.total_h_dim)
-        return self._transform(grad, self._adj, self.total_in_dim)
+        return self._transform(grad, self._w_adj, perm_out=self._perm)
 
     def get_H(self, net_out):
         return _GetH.apply(net_out, self)
 
     def get_net_out(self, H):
         self._check(H, self.total_h_dim)
-        return self._transform(H, self._netout, self.total_in_dim)
+        return self._transform(H, self._w_fwd, perm_out=self._perm)
 
     # ------------------------------------------------ fused Fock <-> irreps
     def _template_tables(self, orbital_template):
@@ -167,29 +217,13 @@ class HipE3TensorDecomp:
         hit = self._templates.get(key)
         if hit is not None and hit[0] is orbital_template:
             return hit[1]
-        starts = {int(s): b for b, s in enumerate(self._decomp_obj.H_slices[:-1])}
-        pair_kind = np.full(MAX_ELEMENTS * MAX_ELEMENTS, -1, np.int32)
-        origins = []
-        for k, entries in enumerate(orbital_template):
-            if not entries:
-                continue
-            org = np.full((self.num_blocks, 2), -1, np.int32)
-            for rs, cs, os_ in entries:
-                b = starts[int(os_.start)]
-                org[b] = (rs.start, cs.start)
-            pair_kind[k] = len(origins)
-            origins.append(org)
-        sub = np.stack(origins) if origins else np.full((1, self.num_blocks, 2), -1, np.int32)
-        tabs = (_i32(pair_kind, self.device), _i32(sub.reshape(-1), self.device))
+        pair_kind, raw, kb = template_slot_tables(orbital_template, self._decomp_obj.H_slices)
+        dev = self.device
+        tabs = {"pair_kind": _i32(pair_kind, dev), "raw": _i32(raw.reshape(-1), dev), "maxe": int(raw.shape[1]),
+                "kind_blocks": (torch.as_tensor(kb.reshape(-1).view(np.int32), device=dev)
+                                if self.num_blocks <= 64 else None)}
         self._templates[key] = (orbital_template, tabs)
         return tabs
-
-    def _h_tables(self):
-        if self._h_tabs is None:
-            hs = self._decomp_obj.H_slices
-            pos = np.arange(self.total_h_dim) - np.asarray(hs)[self.h_block]
-            self._h_tabs = (_i32(self.h_block, self.device), _i32(pos, self.device))
-        return self._h_tabs
 
     @staticmethod
     def _storage(fock, sparse_offsets):
@@ -199,61 +233,68 @@ class HipE3TensorDecomp:
             return fock.stride(0), None
         return 0, sparse_offsets.to(torch.int64).contiguous()
 
-    def fock_to_irreps(self, fock, fock_block_offsets, atomic_numbers, rows, cols, orbital_template,
-                       block_data_offsets=None):
-        """Labels in the irreps basis for every atom pair (rows[r], cols[r]):
-        gather by template + get_net_out in one launch."""
+    def make_plan(self, fock, fock_block_offsets, atomic_numbers, rows, cols, orbital_template,
+                  block_data_offsets=None):
+        """BasisPlan for the atom pairs (rows[r], cols[r]) of ``fock`` (dense, or
+        the block list of ``block_data_offsets``)."""
         _lib.require_cuda(fock)
+        dev = fock.device
+        tabs = self._template_tables(orbital_template)
+        off, Z, r_, c_ = (_i32(x, dev) for x in (fock_block_offsets, atomic_numbers, rows, cols))
+        ld, bdo = self._storage(fock, block_data_offsets)
+        R = int(r_.shape[0])
+        meta = torch.empty(max(R, 1), 4, device=dev, dtype=torch.int32)
+        _lib.call("maloq_basis_row_meta", ld, _lib.ptr(bdo), _lib.ptr(off), _lib.ptr(Z), _lib.ptr(r_),
+                  _lib.ptr(c_), R, _lib.ptr(tabs["pair_kind"]), tabs["maxe"], _lib.ptr(meta),
+                  _lib.stream_of(dev))
+        if R > 1:
+            kind = torch.bitwise_and(meta[:R, 3], 0xFFFF)
+            meta = meta[:R][torch.argsort(kind, stable=True)].contiguous()
+        return BasisPlan(meta, R, ld, id(orbital_template))
+
+    def _plan_for(self, plan, fock, fock_block_offsets, atomic_numbers, rows, cols, orbital_template,
+                  block_data_offsets):
         if fock.dtype != torch.float32:
             raise ValueError("Unsupported dtype for the Fock matrix; only float32 is supported.")
-        dev = fock.device
-        pk, sub = self._template_tables(orbital_template)
-        off = _i32(fock_block_offsets, dev)
-        Z = _i32(atomic_numbers, dev)
-        r_ = _i32(rows, dev)
-        c_ = _i32(cols, dev)
-        R = int(r_.shape[0])
-        sizes = torch.diff(off) if torch.is_tensor(off) else np.diff(np.asarray(fock_block_offsets))
-        maxe = int(sizes.max()) ** 2 if len(sizes) else 1
-        ld, bdo = self._storage(fock, block_data_offsets)
-        out = torch.empty(R, self.total_in_dim, device=dev, dtype=torch.float32)
-        if R:
-            src, ln, woff, w, mx = self._netout
-            _lib.call("maloq_fock_to_irreps", _lib.ptr(fock), ld, _lib.ptr(bdo), _lib.ptr(off),
-                      _lib.ptr(Z), _lib.ptr(r_), _lib.ptr(c_), R, _lib.ptr(pk), _lib.ptr(sub),
-                      self.num_blocks, _lib.ptr(self.block_n2_dev), _lib.ptr(out), self.total_in_dim,
-                      _lib.ptr(self._netout_block), _lib.ptr(ln), _lib.ptr(woff), _lib.ptr(w), maxe,
-                      _lib.stream_of(dev))
+        if plan is None:
+            return self.make_plan(fock, fock_block_offsets, atomic_numbers, rows, cols, orbital_template,
+                                  block_data_offsets)
+        ld, _ = self._storage(fock, block_data_offsets)
+        if plan.ld != ld or plan.template_key != id(orbital_template):
+            raise ValueError("plan was built for another Fock storage or template")
+        return plan
+
+    def fock_to_irreps(self, fock, fock_block_offsets, atomic_numbers, rows, cols, orbital_template,
+                       block_data_offsets=None, plan=None):
+        """Labels in the irreps basis for every atom pair (rows[r], cols[r]):
+        gather by template + get_net_out in one launch (plus the row plan if
+        none is given)."""
+        _lib.require_cuda(fock)
+        plan = self._plan_for(plan, fock, fock_block_offsets, atomic_numbers, rows, cols, orbital_template,
+                              block_data_offsets)
+        tabs = self._template_tables(orbital_template)
+        out = torch.empty(plan.num_rows, self.total_in_dim, device=fock.device, dtype=torch.float32)
+        _lib.call("maloq_fock_to_irreps", _lib.ptr(fock), plan.ld, _lib.ptr(plan.meta), plan.num_rows,
+                  _lib.ptr(tabs["raw"]), tabs["maxe"], _lib.ptr(tabs["kind_blocks"]), _lib.ptr(out),
+                  _lib.ptr(self._perm), self.total_in_dim, self.num_blocks, _lib.ptr(self._blocks),
+                  _lib.ptr(self._w_fwd), _lib.ptr(self._sched), _lib.stream_of(fock.device))
         return out
 
     def irreps_to_fock(self, net_out, fock, fock_block_offsets, atomic_numbers, rows, cols,
-                       orbital_template, block_data_offsets=None):
+                       orbital_template, block_data_offsets=None, plan=None):
         """get_H per row, scattered into ``fock`` (in place) at the template's entries."""
         self._check(net_out, self.total_in_dim)
         _lib.require_cuda(fock)
-        if fock.dtype != torch.float32:
-            raise ValueError("Unsupported dtype for the Fock matrix; only float32 is supported.")
-        dev = fock.device
-        if self.sort_perm is not None:
-            net_out = net_out[:, torch.as_tensor(np.argsort(self.sort_perm), device=dev)]
-        net_out = net_out.contiguous()
-        pk, sub = self._template_tables(orbital_template)
-        hb, hp = self._h_tables()
-        off = _i32(fock_block_offsets, dev)
-        Z = _i32(atomic_numbers, dev)
-        r_ = _i32(rows, dev)
-        c_ = _i32(cols, dev)
-        R = int(r_.shape[0])
-        if R != net_out.shape[0]:
+        plan = self._plan_for(plan, fock, fock_block_offsets, atomic_numbers, rows, cols, orbital_template,
+                              block_data_offsets)
+        if plan.num_rows != net_out.shape[0]:
             raise ValueError("net_out rows must match the atom-pair list")
-        ld, bdo = self._storage(fock, block_data_offsets)
-        if R:
-            src, ln, woff, w, mx = self._geth
-            _lib.call("maloq_irreps_to_fock", _lib.ptr(net_out), R, self.total_in_dim, _lib.ptr(fock), ld,
-                      _lib.ptr(bdo), _lib.ptr(off), _lib.ptr(Z), _lib.ptr(r_), _lib.ptr(c_), _lib.ptr(pk),
-                      _lib.ptr(sub), self.num_blocks, _lib.ptr(self.block_n2_dev), self.total_h_dim,
-                      _lib.ptr(hb), _lib.ptr(hp), _lib.ptr(src), _lib.ptr(ln), _lib.ptr(woff), _lib.ptr(w),
-                      _lib.stream_of(dev))
+        tabs = self._template_tables(orbital_template)
+        net_out = net_out.contiguous()
+        _lib.call("maloq_irreps_to_fock", _lib.ptr(net_out), _lib.ptr(self._perm), _lib.ptr(fock), plan.ld,
+                  _lib.ptr(plan.meta), plan.num_rows, _lib.ptr(tabs["raw"]), tabs["maxe"],
+                  _lib.ptr(tabs["kind_blocks"]), self.total_in_dim, self.num_blocks, _lib.ptr(self._blocks),
+                  _lib.ptr(self._w_inv), _lib.ptr(self._sched), _lib.stream_of(fock.device))
         return fock
 
 

@@ -1,11 +1,30 @@
 // Fock-matrix <-> irreps-label basis transform (gfx950).
 //
-// HBM-bound work: every kernel stages a tile of rows (label rows, or the
-// atom-pair blocks of the Fock matrix) in LDS with coalesced loads, then each
-// thread produces one output column for a chunk of rows from block-local dot
-// products against the Clebsch-Gordan tables (tiny, L1/L2 resident).  The
-// inverse scatter is deterministic: every Fock entry is written by exactly
-// one (row, column) pair, no atomics.
+// The transform is block diagonal: every Clebsch-Gordan block b (one shell
+// pair l1 x l2 of the label row) maps its n = (2l1+1)(2l2+1) label columns to
+// the same number of irreps columns by a dense n x n matrix.  Unsorted, the
+// label and irreps sides of a block occupy the same columns, so a block can be
+// contracted in place.
+//
+// One workgroup owns 32 rows (atom pairs) and works in three phases over a
+// [32, t] fp32 tile in LDS (odd row pitch: lane-per-row reads are bank-conflict
+// free):
+//   1. load: label/irreps rows with coalesced row copies, or the atom-pair
+//      blocks of the Fock matrix walked in memory order (coalesced), every
+//      element dropped into its label column through a per-element-pair table;
+//   2. contract: each of the 4 waves takes a fixed list of CG blocks (longest-
+//      processing-time balanced on the host); lane = row, so the n x n block
+//      matrix is the same for all 64 lanes and is read with scalar loads, and
+//      every FMA takes its weight from an SGPR.  A block that no row of the
+//      tile has (an element pair without that shell pair) is skipped;
+//   3. store: coalesced rows (through the sort permutation) or the atom-pair
+//      blocks again in memory order (every Fock entry written by exactly one
+//      (row, column): deterministic, no atomics).
+//
+// Fock-side calls run on a row plan: maloq_basis_row_meta describes every row
+// (block base, original row index, element-pair kind, block shape) once per
+// structure, and the host orders the plan by kind so that tiles hold one or a
+// few element pairs and the block skip in phase 2 takes effect.
 //
 // Reference semantics: e3TensorDecomp.get_H / get_net_out
 // (fock_utils/utils_tensor_decomp.py:154-169), the Triton kernels K6/K8
@@ -17,165 +36,314 @@
 namespace maloq {
 
 constexpr int kThreads = 256;
-constexpr int kChunk = 8;  // rows per thread-unit
 constexpr int kMaxElements = 100;
 
-// ---------------------------------------------------------------- labels
-__global__ __launch_bounds__(kThreads) void label_transform_kernel(
-    const float* __restrict__ in, int64_t R, int t_in, const int32_t* __restrict__ in_col_map,
-    float* __restrict__ out, int t_out, const int32_t* __restrict__ ocol_src,
-    const int32_t* __restrict__ ocol_len, const int32_t* __restrict__ ocol_woff,
-    const float* __restrict__ w, int G) {
-  extern __shared__ float smem[];
-  float* sIn = smem;  // [G][t_in]
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * G;
-  const int nrows = static_cast<int>((R - r0) < G ? (R - r0) : G);
-  const int64_t n_in = static_cast<int64_t>(nrows) * t_in;
-  const float* src = in + r0 * t_in;
-  for (int64_t i = threadIdx.x; i < n_in; i += blockDim.x) sIn[i] = src[i];
-  __syncthreads();
-  const int nchunks = (nrows + kChunk - 1) / kChunk;
-  const int units = nchunks * t_out;
-  for (int u = threadIdx.x; u < units; u += blockDim.x) {
-    const int o = u % t_out, ch = u / t_out;
-    const int s = ocol_src[o], len = ocol_len[o], wo = ocol_woff[o];
-    float acc[kChunk];
-#pragma unroll
-    for (int g = 0; g < kChunk; ++g) acc[g] = 0.f;
-    const int gbase = ch * kChunk;
-    for (int k = 0; k < len; ++k) {
-      const float wv = w[wo + k];
-      const int c = in_col_map ? in_col_map[s + k] : s + k;
-#pragma unroll
-      for (int g = 0; g < kChunk; ++g) {
-        const int gg = gbase + g;
-        if (gg < nrows) acc[g] = fmaf(sIn[gg * t_in + c], wv, acc[g]);
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < kChunk; ++g) {
-      const int gg = gbase + g;
-      if (gg < nrows) out[(r0 + gg) * t_out + o] = acc[g];
-    }
-  }
-}
+namespace bt {
 
-// Locates atom-pair block r: base offset into `fock` and its row stride.
-struct BlockRef {
-  int64_t base;
-  int64_t ld;
-  int ni, nj, kind;
+// 32 rows per workgroup: a 25 KB tile lets six workgroups share a CU, which
+// hides more load latency than the idle upper half-wave of phase 2 costs.
+constexpr int kRows = 32;            // rows per workgroup
+constexpr int kWaves = kThreads / 64;
+constexpr int kPassRows = kRows / kWaves;  // rows per wave per load pass (x 4 chunks of 64)
+constexpr int kMaxTileBytes = 160 * 1024;
+constexpr int kMaxSkipBlocks = 64;   // blocks covered by the per-kind presence masks
+
+enum Side { ROWS = 0, FOCK = 1 };
+
+struct Args {
+  const float* in;          // ROWS input [R, t]
+  const int32_t* perm_in;   // input column j -> unsorted column, or null
+  float* out;               // ROWS output [R, t]
+  const int32_t* perm_out;  // output column j <- unsorted column, or null
+  int64_t R;
+  int t, tp;                // row width, LDS row pitch (odd)
+  // Fock side
+  float* fock;
+  int64_t ld;               // dense row stride, or 0 for block-list storage
+  const int4* meta;         // [R] row plan (maloq_basis_row_meta), processing order
+  const int32_t* raw_slot;  // [kinds, maxe]: label column of block element q, or -1
+  int maxe;                 // row length of raw_slot (largest n_i * n_j)
+  const uint32_t* kind_blocks;  // [kinds, 2]: CG blocks present for the kind (bit b), or null
+  // CG tables
+  int nblocks;
+  const int32_t* blocks;    // [nblocks, 3]: n, first column, weight offset
+  const float* w;
+  const int32_t* sched;     // [kWaves + 1] offsets into sched + kWaves + 1 of block ids
 };
 
-__device__ __forceinline__ BlockRef block_ref(int64_t r, int64_t ld, const int64_t* data_offsets,
-                                              const int32_t* off, const int32_t* Z,
-                                              const int32_t* rows, const int32_t* cols,
-                                              const int32_t* pair_kind) {
-  BlockRef b;
+struct Smem {
+  int64_t base[kRows];
+  int64_t row[kRows];  // original row index
+  int kind[kRows];
+  int ne[kRows];       // elements of the atom-pair block (n_i * n_j)
+  int nj[kRows];
+  float rnj[kRows];    // 1 / n_j
+};
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Row plan entry r: int4 (base lo, base hi, r, (kind + 1) | n_i << 16 | n_j << 24).
+__global__ __launch_bounds__(kThreads) void row_meta_kernel(
+    int64_t R, int64_t ld, const int64_t* __restrict__ data_offsets,
+    const int32_t* __restrict__ off, const int32_t* __restrict__ Z,
+    const int32_t* __restrict__ rows, const int32_t* __restrict__ cols,
+    const int32_t* __restrict__ pair_kind, int maxe, int4* __restrict__ meta) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (r >= R) return;
   const int i = rows[r], j = cols[r];
   const int oi = off[i], oj = off[j];
-  b.ni = off[i + 1] - oi;
-  b.nj = off[j + 1] - oj;
-  if (data_offsets) {
-    b.base = data_offsets[r];
-    b.ld = b.nj;
-  } else {
-    b.base = static_cast<int64_t>(oi) * ld + oj;
-    b.ld = ld;
-  }
-  b.kind = pair_kind ? pair_kind[Z[i] * kMaxElements + Z[j]] : -1;
-  return b;
+  const int ni = off[i + 1] - oi, nj = off[j + 1] - oj;
+  const int64_t base = data_offsets ? data_offsets[r] : static_cast<int64_t>(oi) * ld + oj;
+  int kind = pair_kind[Z[i] * kMaxElements + Z[j]];
+  // a block larger than the template's rows cannot be one of its element pairs
+  if (ni > 255 || nj > 255 || ni * nj > maxe) kind = -1;
+  meta[r] = make_int4(static_cast<int>(base & 0xffffffff), static_cast<int>(base >> 32),
+                      static_cast<int>(r), (kind + 1) | ((ni & 255) << 16) | ((nj & 255) << 24));
 }
 
-__global__ __launch_bounds__(kThreads) void fock_to_irreps_kernel(
-    const float* __restrict__ fock, int64_t ld, const int64_t* __restrict__ data_offsets,
-    const int32_t* __restrict__ off, const int32_t* __restrict__ Z,
-    const int32_t* __restrict__ rows, const int32_t* __restrict__ cols, int64_t R,
-    const int32_t* __restrict__ pair_kind, const int32_t* __restrict__ sub_origin, int nblocks,
-    const int32_t* __restrict__ block_n2, float* __restrict__ out, int t_out,
-    const int32_t* __restrict__ ocol_block, const int32_t* __restrict__ ocol_len,
-    const int32_t* __restrict__ ocol_woff, const float* __restrict__ w, int maxe, int G) {
-  extern __shared__ float smem[];
-  float* sBlk = smem;                                          // [G][maxe]
-  int* sMeta = reinterpret_cast<int*>(sBlk + static_cast<int64_t>(G) * maxe);  // [G][2]: nj, kind
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * G;
-  const int nrows = static_cast<int>((R - r0) < G ? (R - r0) : G);
-  // One wave-sized group of threads per row loads its block.
-  for (int g = threadIdx.x / 64; g < nrows; g += blockDim.x / 64) {
-    const BlockRef b = block_ref(r0 + g, ld, data_offsets, off, Z, rows, cols, pair_kind);
-    const int ne = b.ni * b.nj;
-    for (int q = threadIdx.x % 64; q < ne; q += 64) {
-      const int a = q / b.nj, c = q - a * b.nj;
-      sBlk[g * maxe + q] = fock[b.base + a * b.ld + c];
-    }
-    if (threadIdx.x % 64 == 0) {
-      sMeta[2 * g] = b.nj;
-      sMeta[2 * g + 1] = b.kind;
-    }
+__device__ __forceinline__ void load_meta(const Args& a, Smem& s, int64_t r0, int nrows) {
+  const int g = threadIdx.x;
+  if (g >= kRows) return;
+  if (g >= nrows) {
+    s.kind[g] = -1;
+    s.ne[g] = 0;
+    s.row[g] = -1;
+    return;
   }
-  __syncthreads();
-  const int nchunks = (nrows + kChunk - 1) / kChunk;
-  const int units = nchunks * t_out;
-  for (int u = threadIdx.x; u < units; u += blockDim.x) {
-    const int o = u % t_out, ch = u / t_out;
-    const int blk = ocol_block[o], len = ocol_len[o], wo = ocol_woff[o], n2 = block_n2[blk];
-    for (int g = ch * kChunk; g < min(nrows, (ch + 1) * kChunk); ++g) {
-      const int nj = sMeta[2 * g], kind = sMeta[2 * g + 1];
-      float acc = 0.f;
-      if (kind >= 0) {
-        const int rr = sub_origin[(kind * nblocks + blk) * 2], cc = sub_origin[(kind * nblocks + blk) * 2 + 1];
-        if (rr >= 0) {
-          const float* blkp = sBlk + g * maxe + rr * nj + cc;
-          int a = 0, bcol = 0;
-          for (int k = 0; k < len; ++k) {
-            acc = fmaf(blkp[a * nj + bcol], w[wo + k], acc);
-            if (++bcol == n2) { bcol = 0; ++a; }
-          }
-        }
+  const int4 m = a.meta[r0 + g];
+  s.base[g] = static_cast<int64_t>(static_cast<uint32_t>(m.x)) | (static_cast<int64_t>(m.y) << 32);
+  s.row[g] = static_cast<uint32_t>(m.z);
+  const int kind = (m.w & 0xffff) - 1, ni = (m.w >> 16) & 255, nj = (m.w >> 24) & 255;
+  s.kind[g] = kind;
+  s.ne[g] = kind >= 0 ? ni * nj : 0;
+  s.nj[g] = nj;
+  s.rnj[g] = nj > 0 ? 1.0f / static_cast<float>(nj) : 0.f;
+}
+
+// Offset of element q = a * n_j + b of tile row g's atom-pair block from its
+// base.  a = floor((q + 1/2) / n_j) in fp32 is exact: the quotient's distance to
+// the nearest integer is >= 1/(2 n_j) >= 2^-9, far above the rounding error
+// for q < 2^16.
+__device__ __forceinline__ int elem_offset(const Args& a, const Smem& s, int g, int q) {
+  if (a.ld == 0) return q;  // block list: n_i x n_j row-major
+  const int nj = s.nj[g];
+  const int ar = static_cast<int>((static_cast<float>(q) + 0.5f) * s.rnj[g]);
+  return ar * static_cast<int>(a.ld) + (q - ar * nj);
+}
+
+// Original row index of tile row g.
+template <bool PLAN>
+__device__ __forceinline__ int64_t row_of(const Smem& s, int64_t r0, int g) {
+  if constexpr (PLAN)
+    return s.row[g];
+  else
+    return r0 + g;
+}
+
+template <int SIDE, bool PLAN>
+__device__ __forceinline__ void load_tile(const Args& a, const Smem& s, float* tile, int64_t r0,
+                                          int nrows) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if constexpr (SIDE == ROWS) {
+    // wave w copies rows w, w + 4, ... in passes of kPassRows rows x 256
+    // columns (coalesced along the row), all loads of a pass in flight
+    for (int c0 = 0; c0 < a.t; c0 += 256) {
+      int dc[4];
+#pragma unroll
+      for (int ch = 0; ch < 4; ++ch) {
+        const int c = c0 + ch * 64 + lane;
+        dc[ch] = c < a.t ? (a.perm_in ? a.perm_in[c] : c) : -1;
       }
-      out[(r0 + g) * t_out + o] = acc;
+      for (int i0 = 0; i0 < kRows / kWaves; i0 += kPassRows) {
+        float v[kPassRows][4];
+#pragma unroll
+        for (int i = 0; i < kPassRows; ++i)
+#pragma unroll
+          for (int ch = 0; ch < 4; ++ch) {
+            const int g = wave + kWaves * (i0 + i), c = c0 + ch * 64 + lane;
+            const bool ok = g < nrows && c < a.t;
+            const float x = a.in[ok ? row_of<PLAN>(s, r0, g) * a.t + c : 0];
+            v[i][ch] = ok ? x : 0.f;
+          }
+#pragma unroll
+        for (int i = 0; i < kPassRows; ++i)
+#pragma unroll
+          for (int ch = 0; ch < 4; ++ch) {
+            const int g = wave + kWaves * (i0 + i);
+            if (g < nrows && dc[ch] >= 0) tile[g * a.tp + dc[ch]] = v[i][ch];
+          }
+      }
+    }
+  } else {
+    // Zero the tile (label columns the element pair lacks stay zero), then
+    // wave w walks the atom-pair blocks of rows w, w + 4, ... in memory order
+    // (coalesced), passes of kPassRows rows x 256 elements, and drops every
+    // element into its label column.
+    for (int i = threadIdx.x; i < kRows * a.tp; i += kThreads) tile[i] = 0.f;
+    __syncthreads();
+    for (int q0 = 0; q0 < a.maxe; q0 += 256) {
+      for (int i0 = 0; i0 < kRows / kWaves; i0 += kPassRows) {
+        float v[kPassRows][4];
+        int dst[kPassRows][4];
+#pragma unroll
+        for (int i = 0; i < kPassRows; ++i)
+#pragma unroll
+          for (int ch = 0; ch < 4; ++ch) {
+            const int g = wave + kWaves * (i0 + i), q = q0 + ch * 64 + lane;
+            const bool ok = q < s.ne[g];
+            const int col = ok ? a.raw_slot[s.kind[g] * a.maxe + q] : -1;
+            const float x = a.fock[ok ? s.base[g] + elem_offset(a, s, g, q) : 0];
+            v[i][ch] = x;
+            dst[i][ch] = col >= 0 ? g * a.tp + col : -1;
+          }
+#pragma unroll
+        for (int i = 0; i < kPassRows; ++i)
+#pragma unroll
+          for (int ch = 0; ch < 4; ++ch)
+            if (dst[i][ch] >= 0) tile[dst[i][ch]] = v[i][ch];
+      }
     }
   }
 }
 
-__global__ __launch_bounds__(kThreads) void irreps_to_fock_kernel(
-    const float* __restrict__ irreps, int64_t R, int t_in, float* __restrict__ fock, int64_t ld,
-    const int64_t* __restrict__ data_offsets, const int32_t* __restrict__ off,
-    const int32_t* __restrict__ Z, const int32_t* __restrict__ rows,
-    const int32_t* __restrict__ cols, const int32_t* __restrict__ pair_kind,
-    const int32_t* __restrict__ sub_origin, int nblocks, const int32_t* __restrict__ block_n2,
-    int t_h, const int32_t* __restrict__ hcol_block, const int32_t* __restrict__ hcol_pos,
-    const int32_t* __restrict__ hcol_src, const int32_t* __restrict__ hcol_len,
-    const int32_t* __restrict__ hcol_woff, const float* __restrict__ w, int G) {
-  extern __shared__ float smem[];
-  float* sIn = smem;  // [G][t_in]
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * G;
-  const int nrows = static_cast<int>((R - r0) < G ? (R - r0) : G);
-  const int64_t n_in = static_cast<int64_t>(nrows) * t_in;
-  const float* src = irreps + r0 * t_in;
-  for (int64_t i = threadIdx.x; i < n_in; i += blockDim.x) sIn[i] = src[i];
-  __syncthreads();
-  const int nchunks = (nrows + kChunk - 1) / kChunk;
-  const int units = nchunks * t_h;
-  for (int u = threadIdx.x; u < units; u += blockDim.x) {
-    const int h = u % t_h, ch = u / t_h;
-    const int blk = hcol_block[h], pos = hcol_pos[h], s = hcol_src[h], len = hcol_len[h],
-              wo = hcol_woff[h], n2 = block_n2[blk];
-    const int pa = pos / n2, pb = pos - pa * n2;
-    for (int g = ch * kChunk; g < min(nrows, (ch + 1) * kChunk); ++g) {
-      const BlockRef b = block_ref(r0 + g, ld, data_offsets, off, Z, rows, cols, pair_kind);
-      if (b.kind < 0) continue;
-      const int rr = sub_origin[(b.kind * nblocks + blk) * 2];
-      const int cc = sub_origin[(b.kind * nblocks + blk) * 2 + 1];
-      if (rr < 0) continue;
-      float acc = 0.f;
-      for (int k = 0; k < len; ++k) acc = fmaf(sIn[g * t_in + s + k], w[wo + k], acc);
-      fock[b.base + static_cast<int64_t>(rr + pa) * b.ld + cc + pb] = acc;
+template <int SIDE, bool PLAN>
+__device__ __forceinline__ void store_tile(const Args& a, const Smem& s, const float* tile,
+                                           int64_t r0, int nrows) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if constexpr (SIDE == ROWS) {
+    for (int c = lane; c < a.t; c += 64) {
+      const int sc = a.perm_out ? a.perm_out[c] : c;
+      for (int g = wave; g < nrows; g += kWaves)
+        a.out[row_of<PLAN>(s, r0, g) * a.t + c] = tile[g * a.tp + sc];
+    }
+  } else {
+    // every element of every atom-pair block a label column covers, in memory order
+    for (int q0 = 0; q0 < a.maxe; q0 += 256) {
+      for (int i0 = 0; i0 < kRows / kWaves; i0 += kPassRows) {
+        int col[kPassRows][4];
+#pragma unroll
+        for (int i = 0; i < kPassRows; ++i)
+#pragma unroll
+          for (int ch = 0; ch < 4; ++ch) {
+            const int g = wave + kWaves * (i0 + i), q = q0 + ch * 64 + lane;
+            col[i][ch] = q < s.ne[g] ? a.raw_slot[s.kind[g] * a.maxe + q] : -1;
+          }
+#pragma unroll
+        for (int i = 0; i < kPassRows; ++i)
+#pragma unroll
+          for (int ch = 0; ch < 4; ++ch) {
+            const int g = wave + kWaves * (i0 + i), q = q0 + ch * 64 + lane;
+            if (col[i][ch] >= 0)
+              a.fock[s.base[g] + elem_offset(a, s, g, q)] = tile[g * a.tp + col[i][ch]];
+          }
+      }
     }
   }
 }
+
+// y = W x for one CG block of one row, in place; W row-major [N][N].
+template <int N>
+__device__ __forceinline__ void contract(float* row, const float* __restrict__ W) {
+  float x[N];
+#pragma unroll
+  for (int k = 0; k < N; ++k) x[k] = row[k];
+  if constexpr (N <= 25) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      float y = 0.f;
+#pragma unroll
+      for (int k = 0; k < N; ++k) y = fmaf(W[j * N + k], x[k], y);
+      row[j] = y;
+    }
+  } else {
+    for (int j = 0; j < N; ++j) {
+      float y = 0.f;
+#pragma unroll
+      for (int k = 0; k < N; ++k) y = fmaf(W[j * N + k], x[k], y);
+      row[j] = y;
+    }
+  }
+}
+
+template <bool SKIP>
+__device__ __forceinline__ void contract_tile(const Args& a, const Smem& s, float* tile) {
+  const int wave = uniform(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int beg = uniform(a.sched[wave]), end = uniform(a.sched[wave + 1]);
+  const int32_t* ids = a.sched + kWaves + 1;
+  // lane = row; with 32 rows the upper half-wave repeats the lower one (same
+  // reads, same values written)
+  float* row = tile + (lane % kRows) * a.tp;
+  uint32_t have0 = 0xffffffffu, have1 = 0xffffffffu;  // CG blocks this lane's row has
+  if constexpr (SKIP) {
+    const int kind = s.kind[lane % kRows];
+    have0 = kind >= 0 ? a.kind_blocks[2 * kind] : 0u;
+    have1 = kind >= 0 ? a.kind_blocks[2 * kind + 1] : 0u;
+  }
+  for (int p = beg; p < end; ++p) {
+    const int b = uniform(ids[p]);
+    if constexpr (SKIP) {
+      const bool mine = ((b < 32 ? have0 >> b : have1 >> (b - 32)) & 1u) != 0;
+      if (__builtin_amdgcn_ballot_w64(mine) == 0) continue;  // no row of the tile has block b
+    }
+    const int n = uniform(a.blocks[3 * b]);
+    const int c0 = uniform(a.blocks[3 * b + 1]);
+    const float* W = a.w + uniform(a.blocks[3 * b + 2]);
+    switch (n) {  // (2 l1 + 1)(2 l2 + 1) for l1, l2 <= 3
+      case 1: contract<1>(row + c0, W); break;
+      case 3: contract<3>(row + c0, W); break;
+      case 5: contract<5>(row + c0, W); break;
+      case 7: contract<7>(row + c0, W); break;
+      case 9: contract<9>(row + c0, W); break;
+      case 15: contract<15>(row + c0, W); break;
+      case 21: contract<21>(row + c0, W); break;
+      case 25: contract<25>(row + c0, W); break;
+      case 35: contract<35>(row + c0, W); break;
+      case 49: contract<49>(row + c0, W); break;
+      default: break;  // rejected on the host
+    }
+  }
+}
+
+// IN/OUT: the two sides; PLAN: rows come from the row plan (Fock-side calls).
+template <int IN, int OUT>
+__global__ __launch_bounds__(kThreads) void transform_kernel(Args a) {
+  constexpr bool PLAN = IN == FOCK || OUT == FOCK;
+  extern __shared__ float tile[];  // [kRows][tp]
+  __shared__ Smem s;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kRows;
+  const int nrows = static_cast<int>((a.R - r0) < kRows ? (a.R - r0) : kRows);
+  if constexpr (PLAN) {
+    load_meta(a, s, r0, nrows);
+    __syncthreads();
+  }
+  load_tile<IN, PLAN>(a, s, tile, r0, nrows);
+  __syncthreads();
+  if (PLAN && a.kind_blocks != nullptr)
+    contract_tile<true>(a, s, tile);
+  else
+    contract_tile<false>(a, s, tile);
+  __syncthreads();
+  store_tile<OUT, PLAN>(a, s, tile, r0, nrows);
+}
+
+}  // namespace bt
 
 // ------------------------------------------------------- plain copy (K12/K13)
+__device__ __forceinline__ void block_base(int64_t r, int64_t ld, const int64_t* data_offsets,
+                                           const int32_t* off, const int32_t* rows,
+                                           const int32_t* cols, int64_t* base, int64_t* ldb) {
+  const int i = rows[r], j = cols[r];
+  const int oi = off[i], oj = off[j];
+  if (data_offsets) {
+    *base = data_offsets[r];
+    *ldb = off[j + 1] - oj;
+  } else {
+    *base = static_cast<int64_t>(oi) * ld + oj;
+    *ldb = ld;
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void matrix2label_kernel(
     float* __restrict__ fock, int64_t ld, const int64_t* __restrict__ data_offsets,
     const int32_t* __restrict__ off, const int32_t* __restrict__ Z,
@@ -185,7 +353,8 @@ __global__ __launch_bounds__(kThreads) void matrix2label_kernel(
   const int64_t r = static_cast<int64_t>(blockIdx.x) * (blockDim.x / 64) + threadIdx.x / 64;
   if (r >= R) return;
   const int lane = threadIdx.x % 64;
-  const BlockRef b = block_ref(r, ld, data_offsets, off, Z, rows, cols, nullptr);
+  int64_t base, ldb;
+  block_base(r, ld, data_offsets, off, rows, cols, &base, &ldb);
   const int key = Z[rows[r]] * kMaxElements + Z[cols[r]];
   float* trow = target + r * target_ld;
   for (int t = tmpl_ptr[key]; t < tmpl_ptr[key + 1]; ++t) {
@@ -194,7 +363,7 @@ __global__ __launch_bounds__(kThreads) void matrix2label_kernel(
     const int wdt = cb - ca, ne = (rb - ra) * wdt;
     for (int k = lane; k < ne; k += 64) {
       const int a = k / wdt, c = k - a * wdt;
-      const int64_t fp = b.base + static_cast<int64_t>(ra + a) * b.ld + ca + c;
+      const int64_t fp = base + static_cast<int64_t>(ra + a) * ldb + ca + c;
       if (forward)
         trow[o0 + k] = fock[fp];
       else
@@ -207,86 +376,130 @@ __global__ __launch_bounds__(kThreads) void matrix2label_kernel(
 
 using namespace maloq;
 
-static int rows_per_block(int row_floats, int64_t R) {
-  // Keep the staged tile under 64 KB of LDS and at most 64 rows.
-  int g = 64;
-  while (g > kChunk && static_cast<int64_t>(g) * row_floats * 4 > 64 * 1024) g /= 2;
-  (void)R;
-  return g;
+namespace {
+
+int check_tables(int t, int nblocks, const int32_t* blocks, const float* w, const int32_t* sched) {
+  MALOQ_REQUIRE(t > 0 && nblocks > 0, "bad sizes (t=%d, nblocks=%d)", t, nblocks);
+  MALOQ_REQUIRE(blocks && w && sched, "null CG table");
+  const int tp = t | 1;
+  MALOQ_REQUIRE(static_cast<int64_t>(bt::kRows) * tp * 4 <= bt::kMaxTileBytes,
+                "label width %d too large for one LDS tile", t);
+  return MALOQ_OK;
 }
 
-extern "C" int maloq_label_transform(const float* in, int64_t num_rows, int t_in,
-                                     const int32_t* in_col_map, float* out, int t_out,
-                                     const int32_t* ocol_src, const int32_t* ocol_len,
-                                     const int32_t* ocol_woff, const float* w, int max_len,
-                                     void* stream) {
-  MALOQ_REQUIRE(num_rows >= 0 && t_in > 0 && t_out > 0, "bad sizes");
-  (void)max_len;
+bt::Args base_args(int64_t R, int t, int nblocks, const int32_t* blocks, const float* w,
+                   const int32_t* sched) {
+  bt::Args a{};
+  a.R = R;
+  a.t = t;
+  a.tp = t | 1;
+  a.nblocks = nblocks;
+  a.blocks = blocks;
+  a.w = w;
+  a.sched = sched;
+  return a;
+}
+
+int set_fock_side(bt::Args& a, float* fock, int64_t ld, const int32_t* row_meta,
+                  const int32_t* raw_slot, int maxe, const uint32_t* kind_blocks) {
+  MALOQ_REQUIRE(fock && row_meta && raw_slot, "null pointer");
+  MALOQ_REQUIRE(ld >= 0 && ld < (int64_t(1) << 24), "dense Fock row stride %lld out of range",
+                static_cast<long long>(ld));
+  MALOQ_REQUIRE(maxe > 0 && maxe <= 65535, "raw_slot row length %d out of range", maxe);
+  MALOQ_REQUIRE((reinterpret_cast<uintptr_t>(row_meta) & 15) == 0, "row_meta must be 16-byte aligned");
+  MALOQ_REQUIRE(kind_blocks == nullptr || a.nblocks <= bt::kMaxSkipBlocks,
+                "block presence masks cover at most %d CG blocks", bt::kMaxSkipBlocks);
+  a.fock = fock;
+  a.ld = ld;
+  a.meta = reinterpret_cast<const int4*>(row_meta);
+  a.raw_slot = raw_slot;
+  a.maxe = maxe;
+  a.kind_blocks = kind_blocks;
+  return MALOQ_OK;
+}
+
+template <int IN, int OUT>
+int launch_transform(const bt::Args& a, void* stream, const char* name) {
+  const int64_t groups = (a.R + bt::kRows - 1) / bt::kRows;
+  const size_t shm = static_cast<size_t>(bt::kRows) * a.tp * sizeof(float);
+  hipLaunchKernelGGL((bt::transform_kernel<IN, OUT>), dim3(static_cast<unsigned>(groups)),
+                     dim3(kThreads), shm, static_cast<hipStream_t>(stream), a);
+  return check_launch(name);
+}
+
+}  // namespace
+
+extern "C" int maloq_label_transform(const float* in, const int32_t* perm_in, float* out,
+                                     const int32_t* perm_out, int64_t num_rows, int t,
+                                     int nblocks, const int32_t* blocks, const float* w,
+                                     const int32_t* sched, void* stream) {
+  MALOQ_REQUIRE(num_rows >= 0, "bad sizes");
+  if (int rc = check_tables(t, nblocks, blocks, w, sched)) return rc;
   if (num_rows == 0) return MALOQ_OK;
-  MALOQ_REQUIRE(in && out && ocol_src && ocol_len && ocol_woff && w, "null pointer");
-  const int G = rows_per_block(t_in, num_rows);
-  MALOQ_REQUIRE(static_cast<int64_t>(kChunk) * t_in * 4 <= 64 * 1024, "label width %d too large", t_in);
-  const int64_t blocks = (num_rows + G - 1) / G;
-  const size_t shm = static_cast<size_t>(G) * t_in * sizeof(float);
-  hipLaunchKernelGGL(label_transform_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads),
-                     shm, static_cast<hipStream_t>(stream), in, num_rows, t_in, in_col_map, out,
-                     t_out, ocol_src, ocol_len, ocol_woff, w, G);
-  return check_launch("label_transform_kernel");
+  MALOQ_REQUIRE(in && out, "null pointer");
+  bt::Args a = base_args(num_rows, t, nblocks, blocks, w, sched);
+  a.in = in;
+  a.perm_in = perm_in;
+  a.out = out;
+  a.perm_out = perm_out;
+  return launch_transform<bt::ROWS, bt::ROWS>(a, stream, "label transform");
 }
 
-extern "C" int maloq_fock_to_irreps(const float* fock, int64_t ld, const int64_t* data_offsets,
+extern "C" int maloq_basis_row_meta(int64_t ld, const int64_t* data_offsets,
                                     const int32_t* fock_block_offsets,
                                     const int32_t* atomic_numbers, const int32_t* rows,
                                     const int32_t* cols, int64_t num_rows,
-                                    const int32_t* pair_kind, const int32_t* sub_origin,
-                                    int nblocks, const int32_t* block_n2, float* out, int t_out,
-                                    const int32_t* ocol_block, const int32_t* ocol_len,
-                                    const int32_t* ocol_woff, const float* w,
-                                    int max_block_elems, void* stream) {
-  MALOQ_REQUIRE(num_rows >= 0 && t_out > 0 && nblocks > 0, "bad sizes");
+                                    const int32_t* pair_kind, int maxe, int32_t* row_meta,
+                                    void* stream) {
+  MALOQ_REQUIRE(num_rows >= 0 && num_rows < (int64_t(1) << 31), "bad number of rows");
   if (num_rows == 0) return MALOQ_OK;
-  MALOQ_REQUIRE(fock && fock_block_offsets && atomic_numbers && rows && cols && pair_kind &&
-                    sub_origin && block_n2 && out && ocol_block && ocol_len && ocol_woff && w,
+  MALOQ_REQUIRE(fock_block_offsets && atomic_numbers && rows && cols && pair_kind && row_meta,
                 "null pointer");
-  MALOQ_REQUIRE(max_block_elems > 0 && max_block_elems <= 8192, "max_block_elems out of range");
-  int G = 64;
-  while (G > kChunk && static_cast<int64_t>(G) * (max_block_elems + 2) * 4 > 64 * 1024) G /= 2;
-  const size_t shm = static_cast<size_t>(G) * max_block_elems * sizeof(float) + 2 * G * sizeof(int);
-  const int64_t blocks = (num_rows + G - 1) / G;
-  hipLaunchKernelGGL(fock_to_irreps_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads),
-                     shm, static_cast<hipStream_t>(stream), fock, ld, data_offsets,
-                     fock_block_offsets, atomic_numbers, rows, cols, num_rows, pair_kind,
-                     sub_origin, nblocks, block_n2, out, t_out, ocol_block, ocol_len, ocol_woff, w,
-                     max_block_elems, G);
-  return check_launch("fock_to_irreps_kernel");
+  MALOQ_REQUIRE(data_offsets || (ld > 0 && ld < (int64_t(1) << 24)),
+                "dense Fock row stride %lld out of range", static_cast<long long>(ld));
+  MALOQ_REQUIRE(maxe > 0 && maxe <= 65535, "raw_slot row length %d out of range", maxe);
+  MALOQ_REQUIRE((reinterpret_cast<uintptr_t>(row_meta) & 15) == 0, "row_meta must be 16-byte aligned");
+  const int64_t groups = (num_rows + kThreads - 1) / kThreads;
+  hipLaunchKernelGGL(bt::row_meta_kernel, dim3(static_cast<unsigned>(groups)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), num_rows, data_offsets ? 0 : ld,
+                     data_offsets, fock_block_offsets, atomic_numbers, rows, cols, pair_kind,
+                     maxe, reinterpret_cast<int4*>(row_meta));
+  return check_launch("row plan");
 }
 
-extern "C" int maloq_irreps_to_fock(const float* irreps, int64_t num_rows, int t_in, float* fock,
-                                    int64_t ld, const int64_t* data_offsets,
-                                    const int32_t* fock_block_offsets,
-                                    const int32_t* atomic_numbers, const int32_t* rows,
-                                    const int32_t* cols, const int32_t* pair_kind,
-                                    const int32_t* sub_origin, int nblocks,
-                                    const int32_t* block_n2, int t_h, const int32_t* hcol_block,
-                                    const int32_t* hcol_pos, const int32_t* hcol_src,
-                                    const int32_t* hcol_len, const int32_t* hcol_woff,
-                                    const float* w, void* stream) {
-  MALOQ_REQUIRE(num_rows >= 0 && t_in > 0 && t_h > 0 && nblocks > 0, "bad sizes");
+extern "C" int maloq_fock_to_irreps(const float* fock, int64_t ld, const int32_t* row_meta,
+                                    int64_t num_rows, const int32_t* raw_slot, int maxe,
+                                    const uint32_t* kind_blocks, float* out,
+                                    const int32_t* perm_out, int t, int nblocks,
+                                    const int32_t* blocks, const float* w, const int32_t* sched,
+                                    void* stream) {
+  MALOQ_REQUIRE(num_rows >= 0, "bad sizes");
+  if (int rc = check_tables(t, nblocks, blocks, w, sched)) return rc;
   if (num_rows == 0) return MALOQ_OK;
-  MALOQ_REQUIRE(irreps && fock && fock_block_offsets && atomic_numbers && rows && cols &&
-                    pair_kind && sub_origin && block_n2 && hcol_block && hcol_pos && hcol_src &&
-                    hcol_len && hcol_woff && w,
-                "null pointer");
-  const int G = rows_per_block(t_in, num_rows);
-  MALOQ_REQUIRE(static_cast<int64_t>(kChunk) * t_in * 4 <= 64 * 1024, "irreps width %d too large", t_in);
-  const size_t shm = static_cast<size_t>(G) * t_in * sizeof(float);
-  const int64_t blocks = (num_rows + G - 1) / G;
-  hipLaunchKernelGGL(irreps_to_fock_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads),
-                     shm, static_cast<hipStream_t>(stream), irreps, num_rows, t_in, fock, ld,
-                     data_offsets, fock_block_offsets, atomic_numbers, rows, cols, pair_kind,
-                     sub_origin, nblocks, block_n2, t_h, hcol_block, hcol_pos, hcol_src, hcol_len,
-                     hcol_woff, w, G);
-  return check_launch("irreps_to_fock_kernel");
+  MALOQ_REQUIRE(out, "null pointer");
+  bt::Args a = base_args(num_rows, t, nblocks, blocks, w, sched);
+  if (int rc = set_fock_side(a, const_cast<float*>(fock), ld, row_meta, raw_slot, maxe, kind_blocks))
+    return rc;
+  a.out = out;
+  a.perm_out = perm_out;
+  return launch_transform<bt::FOCK, bt::ROWS>(a, stream, "fock -> irreps");
+}
+
+extern "C" int maloq_irreps_to_fock(const float* irreps, const int32_t* perm_in, float* fock,
+                                    int64_t ld, const int32_t* row_meta, int64_t num_rows,
+                                    const int32_t* raw_slot, int maxe,
+                                    const uint32_t* kind_blocks, int t, int nblocks,
+                                    const int32_t* blocks, const float* w, const int32_t* sched,
+                                    void* stream) {
+  MALOQ_REQUIRE(num_rows >= 0, "bad sizes");
+  if (int rc = check_tables(t, nblocks, blocks, w, sched)) return rc;
+  if (num_rows == 0) return MALOQ_OK;
+  MALOQ_REQUIRE(irreps, "null pointer");
+  bt::Args a = base_args(num_rows, t, nblocks, blocks, w, sched);
+  if (int rc = set_fock_side(a, fock, ld, row_meta, raw_slot, maxe, kind_blocks)) return rc;
+  a.in = irreps;
+  a.perm_in = perm_in;
+  return launch_transform<bt::ROWS, bt::FOCK>(a, stream, "irreps -> fock");
 }
 
 extern "C" int maloq_matrix2label(float* fock, int64_t ld, const int64_t* data_offsets,

@@ -4,11 +4,18 @@
 // gradient rows of edge e (both saved in m-major order [E, d', C] by the
 // fused kernels), the gradient of every |m| group is a GEMM with the edges as
 // the reduction axis:  C_g = sum_e dZ_g(e)^T Y_g(e), g = 0..mmax.
-// Workgroups own 64x64 output tiles of one group and a contiguous edge range
-// (split-K); both operands are loaded edge-major (coalesced along channels)
-// and transposed through LDS into MFMA fragments.  Partial tiles are summed in
-// split order by dw_reduce_kernel, which also folds the +-m quadrants of
-// C_m back into the reference layout of so2_m_conv.fc.weight:
+//
+// Tiling.  A workgroup (4 waves) owns a 128 x 128 tile of one C_g and a
+// contiguous edge range (split-K).  Each K step covers KE edges (64 bf16 /
+// 16 fp32): every thread loads one VEC x VEC block (VEC edges x VEC columns,
+// one 16-byte load per edge, coalesced along the columns), transposes it in
+// registers and writes VEC 16-byte rows straight into MFMA fragment order, so
+// both operands are K(edge)-contiguous per lane.  Loads for step s+1 are
+// issued before the MFMAs of step s and land in the other LDS buffer (one
+// barrier per step).  Each wave computes a 64 x 64 sub-tile (2 x 2 MFMA
+// tiles of 32 x 32).  Partial tiles are summed in split order by
+// dw_reduce_kernel, which also folds the +-m quadrants of C_m back into the
+// reference layout of so2_m_conv.fc.weight:
 //   dWr = C[+,+] + C[-,-],   dWi = C[-,+] - C[+,-]      (so2_layers.py:61-67).
 // Deterministic: no atomics.
 #include "message_impl.h"
@@ -18,6 +25,7 @@ namespace maloq {
 namespace msg {
 
 constexpr int MAXG = 8;
+constexpr int DW_T = 128;  // output tile edge
 
 struct DwArgs {
   const void* dz;       // [E, dp, C_out]
@@ -25,18 +33,54 @@ struct DwArgs {
   int64_t E;
   int dp, C_out, C_in, ngroups, splits;
   int row0[MAXG], rows[MAXG];
-  int ntk[MAXG];             // 64-wide tiles along k (= rows * C_in)
+  int ntk[MAXG];             // DW_T-wide tiles along k (= rows * C_in)
   int64_t tile0[MAXG + 1];   // cumulative tile counts
   int64_t goff[MAXG + 1];    // element offset of group g in one split's partials
-  int64_t e_per_split;
+  int64_t e_per_split;       // multiple of the K step
   float* part;               // [splits, goff[ngroups]]
 };
 
 template <class TM>
+struct DwCfg {
+  static constexpr int VEC = TM::VEC;            // elements per 16-byte row
+  static constexpr int KC = TM::KC;              // edges per MFMA fragment
+  static constexpr int KE = VEC * VEC * 256 / (2 * DW_T);  // edges per K step (1 block per thread)
+  static constexpr int NSUB = KE / KC;           // fragment columns per step
+  static constexpr int FRAGS = (DW_T / 32) * NSUB;  // fragments per operand per step
+  static constexpr int STAGE = 2 * FRAGS * FRAG;    // A + B bytes per step
+};
+
+// Transposes a VEC x VEC block held as VEC rows of 16 bytes (row = edge,
+// VEC column elements) into VEC rows of VEC edges (row = column).
+__device__ __forceinline__ void transpose_block(const uint4 (&in)[8], uint4 (&out)[8], BF16) {
+  // 16-bit elements: word w of out[c] = (in[2w] elem c) | (in[2w+1] elem c) << 16
+  const uint32_t* iw = reinterpret_cast<const uint32_t*>(in);
+  uint32_t* ow = reinterpret_cast<uint32_t*>(out);
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t lo = iw[(2 * w) * 4 + (c >> 1)], hi = iw[(2 * w + 1) * 4 + (c >> 1)];
+      // v_perm_b32 selector: bytes of hi are 4..7, bytes of lo 0..3
+      const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+      ow[c * 4 + w] = __builtin_amdgcn_perm(hi, lo, sel);
+    }
+  }
+}
+__device__ __forceinline__ void transpose_block(const uint4 (&in)[4], uint4 (&out)[4], F32) {
+  const uint32_t* iw = reinterpret_cast<const uint32_t*>(in);
+  uint32_t* ow = reinterpret_cast<uint32_t*>(out);
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ow[c * 4 + e] = iw[e * 4 + c];
+}
+
+template <class TM>
 __global__ __launch_bounds__(256) void dw_kernel(DwArgs a) {
-  constexpr int KCE = TM::KC;  // edges per K step
-  __shared__ alignas(16) char sA[2 * FRAG];
-  __shared__ alignas(16) char sB[2 * FRAG];
+  using Cfg = DwCfg<TM>;
+  constexpr int VEC = Cfg::VEC, KE = Cfg::KE, NSUB = Cfg::NSUB;
+  __shared__ alignas(16) char smem[2 * Cfg::STAGE];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t ntiles = a.tile0[a.ngroups];
   const int64_t split = blockIdx.x / ntiles;
@@ -46,55 +90,87 @@ __global__ __launch_bounds__(256) void dw_kernel(DwArgs a) {
   const int64_t lt = t - a.tile0[g];
   const int tn = static_cast<int>(lt / a.ntk[g]), tk = static_cast<int>(lt % a.ntk[g]);
   const int Ng = a.rows[g] * a.C_out, Kg = a.rows[g] * a.C_in;
-  const int n0 = tn * 64, k0 = tk * 64;
   const int64_t eb = split * a.e_per_split;
   const int64_t ee = (eb + a.e_per_split) < a.E ? (eb + a.e_per_split) : a.E;
-  const typename TM::raw* dz = reinterpret_cast<const typename TM::raw*>(a.dz);
-  const typename TM::raw* y = reinterpret_cast<const typename TM::raw*>(a.y);
-  f32x16 acc;
+
+  // this thread's block: operand (0 = dZ -> A, 1 = Y -> B), column group, edge group
+  const int op = tid >> 7;
+  const int bi = tid & 127;
+  const int cg = bi % (DW_T / VEC), eg = bi / (DW_T / VEC);
+  const int C = op ? a.C_in : a.C_out;
+  const int col = (op ? tk : tn) * DW_T + cg * VEC;   // first column of the block in C_g
+  const int lim = op ? Kg : Ng;
+  const typename TM::raw* src = reinterpret_cast<const typename TM::raw*>(op ? a.y : a.dz);
+  int64_t coladdr = -1;  // element offset of (edge 0, col) or -1 if the block is outside the tile
+  if (col < lim) coladdr = static_cast<int64_t>(a.row0[g] + col / C) * C + col % C;
+  const int64_t estride = static_cast<int64_t>(a.dp) * C;
+  // LDS destination: fragment (col tile, k-substep), row = column within the tile
+  const int cl = cg * VEC;  // column within the 128 tile
+  const int e_in = eg * VEC;
+  const int frag = op * Cfg::FRAGS + (cl >> 5) * NSUB + e_in / TM::KC;
+  const int lds_off = frag * FRAG + frag_off<TM>(cl & 31, e_in % TM::KC);  // + c * row pitch below
+
+  uint4 regs[VEC];
+  auto load = [&](int64_t e0) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
-  // staging map: 64 columns x KCE edges per operand; each thread moves 64*KCE/256 values
-  constexpr int PER = 64 * KCE / 256;
-  for (int64_t e0 = eb; e0 < ee; e0 += KCE) {
-#pragma unroll
-    for (int p = 0; p < PER; ++p) {
-      const int q = tid * PER + p;        // 0 .. 64*KCE-1
-      const int el = q / 64, c = q % 64;  // edge in chunk, column in tile
-      const int64_t e = e0 + el;
-      // A: dZ^T rows n
-      {
-        const int n = n0 + c;
-        float v = 0.f;
-        if (e < ee && n < Ng) {
-          const int row = a.row0[g] + n / a.C_out, co = n % a.C_out;
-          v = TM::load(dz + (e * a.dp + row) * a.C_out + co);
-        }
-        *reinterpret_cast<typename TM::raw*>(sA + (c >> 5) * FRAG + frag_off<TM>(c & 31, el)) =
-            TM::cvt(v);
-      }
-      // B: Y columns k
-      {
-        const int k = k0 + c;
-        float v = 0.f;
-        if (e < ee && k < Kg) {
-          const int row = a.row0[g] + k / a.C_in, ci = k % a.C_in;
-          v = TM::load(y + (e * a.dp + row) * a.C_in + ci);
-        }
-        *reinterpret_cast<typename TM::raw*>(sB + (c >> 5) * FRAG + frag_off<TM>(c & 31, el)) =
-            TM::cvt(v);
-      }
+    for (int v = 0; v < VEC; ++v) {
+      const int64_t e = e0 + e_in + v;
+      regs[v] = make_uint4(0u, 0u, 0u, 0u);
+      if (coladdr >= 0 && e < ee) regs[v] = *reinterpret_cast<const uint4*>(src + e * estride + coladdr);
     }
-    __syncthreads();
-    mma(acc, sA + (wave >> 1) * FRAG, sB + (wave & 1) * FRAG, lane, TM{});
+  };
+  auto store = [&](int buf) {
+    uint4 tr[VEC];
+    transpose_block(regs, tr, TM{});
+    char* base = smem + buf * Cfg::STAGE + lds_off;
+#pragma unroll
+    for (int c = 0; c < VEC; ++c)
+      *reinterpret_cast<uint4*>(base + frag_off<TM>(c, 0) - frag_off<TM>(0, 0)) = tr[c];
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int wn = wave >> 1, wk = wave & 1;
+  const int64_t nsteps = ee > eb ? (ee - eb + KE - 1) / KE : 0;
+  if (nsteps > 0) {
+    load(eb);
+    store(0);
+  }
+  __syncthreads();
+  for (int64_t s = 0; s < nsteps; ++s) {
+    const bool more = s + 1 < nsteps;
+    if (more) load(eb + (s + 1) * KE);
+    const char* A = smem + (s & 1) * Cfg::STAGE;
+    const char* B = A + Cfg::FRAGS * FRAG;
+#pragma unroll
+    for (int ks = 0; ks < NSUB; ++ks) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          mma(acc[i][j], A + ((2 * wn + i) * NSUB + ks) * FRAG, B + ((2 * wk + j) * NSUB + ks) * FRAG,
+              lane, TM{});
+    }
+    if (more) store((s + 1) & 1);
     __syncthreads();
   }
   float* out = a.part + split * a.goff[a.ngroups] + a.goff[g];
-  const int k = k0 + (wave & 1) * 32 + (lane & 31);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int n = n0 + (wave >> 1) * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-    if (n < Ng && k < Kg) out[static_cast<int64_t>(n) * Kg + k] = acc[i];
+  for (int j = 0; j < 2; ++j) {
+    const int k = tk * DW_T + (2 * wk + j) * 32 + (lane & 31);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int n = tn * DW_T + (2 * wn + i) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (n < Ng && k < Kg) out[static_cast<int64_t>(n) * Kg + k] = acc[i][j][r];
+      }
   }
 }
 
@@ -158,12 +234,13 @@ static int dw_setup(DwArgs& a, int lmax, int mmax, int64_t E, int c_out, int c_i
     a.rows[g] = r;
     row += r;
     const int64_t Ng = static_cast<int64_t>(r) * c_out, Kg = static_cast<int64_t>(r) * c_in;
-    a.ntk[g] = static_cast<int>((Kg + 63) / 64);
-    a.tile0[g + 1] = a.tile0[g] + ((Ng + 63) / 64) * a.ntk[g];
+    a.ntk[g] = static_cast<int>((Kg + DW_T - 1) / DW_T);
+    a.tile0[g + 1] = a.tile0[g] + ((Ng + DW_T - 1) / DW_T) * a.ntk[g];
     a.goff[g + 1] = a.goff[g] + Ng * Kg;
   }
   a.dp = row;
-  a.e_per_split = (E + splits - 1) / splits;
+  // split boundaries on a multiple of the largest K step (64 edges)
+  a.e_per_split = ((E + splits - 1) / splits + 63) / 64 * 64;
   return MALOQ_OK;
 }
 

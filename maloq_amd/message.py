@@ -264,7 +264,10 @@ def message_weight_grad(dz, y, lmax, mmax, c_out, c_in, splits=None):
     in fp32 from the saved rows (deterministic split-K over edges)."""
     E = dz.shape[0]
     if splits is None:
-        splits = max(1, min(16, E // 2048))
+        # about 640 workgroups of 128 x 128 output tiles, >= 1024 edges per split
+        ntiles = sum(-(-r * c_out // 128) * -(-r * c_in // 128)
+                     for r in [lmax + 1] + [2 * (lmax - m + 1) for m in range(1, mmax + 1)])
+        splits = max(1, min(16, round(640 / ntiles), E // 1024))
     lib = _lib.load()
     parts = torch.empty(max(1, lib.maloq_message_dw_partials_floats(lmax, mmax, c_out, c_in, splits)),
                         device=dz.device, dtype=torch.float32)

@@ -222,3 +222,23 @@ def test_config3_full_scale_round_trip(device):
         hip.irreps_to_fock(irr, H2, off, z, rows, cols, t.orbital_template)
         worst = max(worst, ((H2 - Hd).abs().max() / Hd.abs().max()).item())
     assert worst < 1e-6
+
+
+def test_row_plan_reuse_and_mismatch(device):
+    """A prebuilt row plan (rows ordered by element-pair kind) gives the same
+    labels as the per-call plan; a plan for another storage is refused."""
+    from maloq_amd.basis_transform import HipE3TensorDecomp
+    t, base, ora = _tables(CFG3)
+    hip = HipE3TensorDecomp(base)
+    z, H, off, rows, cols = _molecules(1, t, seed0=40)[0]
+    Hd = torch.from_numpy(H).to(device)
+    plan = hip.make_plan(Hd, off, z, rows, cols, t.orbital_template)
+    a = hip.fock_to_irreps(Hd, off, z, rows, cols, t.orbital_template)
+    b = hip.fock_to_irreps(Hd, off, z, rows, cols, t.orbital_template, plan=plan)
+    assert torch.equal(a, b)
+    kinds = torch.bitwise_and(plan.meta[:, 3], 0xFFFF).cpu().numpy()
+    assert np.all(np.diff(kinds) >= 0), "plan rows are ordered by kind"
+    assert sorted(plan.meta[:, 2].cpu().tolist()) == list(range(len(rows)))
+    wide = torch.zeros(H.shape[0], H.shape[1] + 3, device=device)[:, :H.shape[1]]  # other row stride
+    with pytest.raises(ValueError):
+        hip.fock_to_irreps(wide, off, z, rows, cols, t.orbital_template, plan=plan)
