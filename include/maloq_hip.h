@@ -144,7 +144,9 @@ int64_t maloq_message_partials_floats(int lmax, int gate, int64_t num_edges, int
 int64_t maloq_message_wpack_bytes(int dtype, int lmax, int mmax, int gate, int c_k, int c_n);
 
 /* Kept rows d' = (lmax+1) + sum_{m=1..mmax} 2 (lmax-m+1) of the m-major layout,
- * and kept Wigner-D entries per edge sum_l (1 + 2 min(mmax, l)) (2l+1). */
+ * and floats per edge of the kept Wigner-D rows (|m| <= mmax) in the kernels'
+ * pair-major layout: per degree l, (l+1) column pairs (j, j+1) of the
+ * nq = 1 + 2 min(mmax, l) row types, [q][2] padded to a multiple of 4 floats. */
 int maloq_message_kept_rows(int lmax, int mmax);
 int maloq_message_wigner_floats(int lmax, int mmax);
 

@@ -28,11 +28,17 @@ __global__ void message_fixup_kernel(const int64_t* __restrict__ seg_ptr, int64_
   *o = sum;
 }
 
+// Packed B fragments per output-channel block: for every kernel-input degree
+// li and K step, per output degree lo: g0, [gate], (Wr, Wi) for m <= min(mmax, li, lo).
 static int64_t frags_per_cb(int lmax, int mmax, int gate, int c_k, int kc) {
   int64_t total = 0;
-  for (int l = 0; l <= lmax; ++l) {
-    int nb = (lmax + 1) + (gate ? lmax : 0);
-    for (int m = 1; m <= (mmax < l ? mmax : l); ++m) nb += 4 * (lmax - m + 1);
+  for (int li = 0; li <= lmax; ++li) {
+    int nb = 0;
+    for (int lo = 0; lo <= lmax; ++lo) {
+      int mm = mmax < li ? mmax : li;
+      mm = mm < lo ? mm : lo;
+      nb += 1 + ((gate && lo >= 1) ? 1 : 0) + 2 * mm;
+    }
     total += static_cast<int64_t>(nb) * (c_k / kc);
   }
   return total;
@@ -90,9 +96,12 @@ static int kept_rows(int lmax, int mmax) {
   return r;
 }
 
+// Floats per edge of the kept Wigner rows in the pair-major layout
+// (PairLayout in message_impl.h): per degree l, (l+1) column pairs of
+// 2 (1 + 2 min(mmax, l)) floats, each rounded up to a multiple of 4.
 static int wigner_floats(int lmax, int mmax) {
   int s = 0;
-  for (int l = 0; l <= lmax; ++l) s += (1 + 2 * (mmax < l ? mmax : l)) * (2 * l + 1);
+  for (int l = 0; l <= lmax; ++l) s += (l + 1) * ((2 * (1 + 2 * (mmax < l ? mmax : l)) + 3) / 4 * 4);
   return s;
 }
 

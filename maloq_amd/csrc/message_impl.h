@@ -1,32 +1,9 @@
 #pragma once
-// Device code of the fused equivariant message block on gfx950:
-//   gather x[src] -> rotate into the edge frame (kept rows |m| <= mmax of D)
-//   -> [radial scale] -> SO(2) per-m linear on MFMA (bf16 or fp32 operands,
-//   fp32 accumulation) [+ bias, gate] -> inverse rotation -> sorted-segment
-//   sum into nodes.
-//
-// Replaces Edgewise.forward_node (helm/esen_block.py:146-208): the dense
-// bmm(wigner), einsum(to_m), SO2_Convolution (helm/nn/so2_layers.py:139-214),
-// GateActivation (helm/nn/activation.py:57-77), einsum(to_m^T),
-// bmm(wigner_inv) and index_add_ all happen in one kernel, so edge features
-// never round-trip through HBM.  The same kernel, with transposed packed
-// weights and the radial scale moved to the epilogue, computes the input
-// gradient of the block (edges ordered by source there).
-//
-// Tiling.  A workgroup owns TE = 32 * RT consecutive edges (sorted by segment id)
-// and CB = 32 output channels.  The SO(2) linear is written as three (or more)
-// real GEMMs, one per |m|: for m > 0 the +m / -m rows are stacked along K and
-// the complex mix is folded into a packed [[Wr, Wi], [-Wi, Wr]] weight, so
-// every MFMA is a plain real product.  The K loop runs over (l_in, 16 or 8
-// input channels); per step the rotated A fragments (one per kept row type and
-// 32-edge row tile) and the packed B fragments live in LDS in the exact lane
-// order of v_mfma_f32_32x32x16_bf16 / v_mfma_f32_32x32x2f32 (1 KB per
-// fragment, one 16-byte ds_read per lane).  Each wave owns whole output
-// degrees l_out (all row tiles and all |m| tiles of that l_out), assigned by
-// a compile-time longest-processing-time schedule, so the inverse rotation is
-// done in registers straight from the accumulators and the segment sum stays
-// wave-local.  Segments cut by a tile boundary are written to a partials
-// buffer and summed in tile order by message_fixup_kernel (deterministic).
+// Shared device code of the fused equivariant message block on gfx950: operand
+// types, the compile-time plan of kept rows (|m| <= mmax) and Wigner entries,
+// kernel arguments, and the per-edge prep kernel (Wigner rows + rotation into
+// the edge frame).  The SO(2) GEMM with its inverse-rotation / segment-sum
+// epilogue is in message_gemm.h.
 #include <utility>
 
 #include "common.h"
@@ -156,20 +133,32 @@ struct Plan {
   }
   static constexpr int MS = max_slots();
   static constexpr int NT = NW * 64;
-  // LDS layout (bytes)
-  static constexpr int A_BYTES = (2 * M + 1) * RT * FRAG;
-  static constexpr int B_BYTES = nbfrag(L) * FRAG;
-  static constexpr int M2_BYTES = TE * (2 * L + 1) * (2 * L + 1) * 4 + TE * 3 * 2 * (L + 1) * 4;
-  static constexpr int EPI_BYTES = NW * TE * 33 * 4;
-  static constexpr int cmax(int a, int b) { return a > b ? a : b; }
-  static constexpr int STAGE_BYTES = cmax(A_BYTES + B_BYTES, EPI_BYTES);
+};
+
+// Kept Wigner rows of one edge in the pair-major layout shared by the prep
+// kernel, the dk workspace and the GEMM epilogue: per degree l, (l+1) column
+// pairs (j = 2p, 2p+1; column 2l+1 is zero); each pair is a [q][2] block of
+// the nq(l) kept row types, padded with zeros to a multiple of 4 floats, so
+// one 16-byte read gives D(q, j) and D(q, j+1) of two row types.
+template <int L, int M>
+struct PairLayout {
+  static constexpr int nq(int l) { return 1 + 2 * cmin(M, l); }
+  static constexpr int pblk(int l) { return (2 * nq(l) + 3) / 4 * 4; }
+  static constexpr int woff(int l) {
+    int s = 0;
+    for (int k = 0; k < l; ++k) s += (k + 1) * pblk(k);
+    return s;
+  }
+  static constexpr int WS = woff(L + 1);  // floats per edge (a multiple of 4)
+  // position of D(q, j) of degree l
+  static constexpr int at(int l, int q, int j) { return woff(l) + (j >> 1) * pblk(l) + 2 * q + (j & 1); }
 };
 
 enum Mode { FWD = 0, BWD_DX = 1 };
 
 struct Args {
   const void* a_src;      // [E_all, d', C_k] (TM raw): rotated rows, m-major, by edge id
-  const float* dk;        // [E_all, DS] kept Wigner rows per edge id
+  const float* dk;        // [E_all, WS] kept Wigner rows per edge id (pair layout)
   const int32_t* seg;     // [E] segment id per edge, non-decreasing
   const int32_t* eidx;    // [E] nullable: edge id of each kernel-order edge
   const void* rad;        // BWD_DX: [E_all, KR] (TM raw) or null
@@ -220,328 +209,7 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// ------------------------------------------------------------------ kernel
-template <int L, int M, bool GATE, int NW, int RT, class TM, class TX, int MODE>
-struct Kernel {
-  using P = Plan<L, M, GATE, NW, RT>;
-  static constexpr int TE = P::TE;
-  static constexpr int d = (L + 1) * (L + 1);
-  static constexpr int NT = P::NT;
-  static constexpr int KC = TM::KC;
 
-  struct Smem {
-    float D[TE * P::DS];
-    int seg[TE];
-    int eid[TE];
-    alignas(16) char stage[P::STAGE_BYTES];
-  };
-
-  // ------------------------------------------------------------ prologue
-  // A fragments of one K step: for every kept row type q of degree LI and
-  // 32-edge row tile rt, lane (row, half) copies 16 bytes of the rotated rows
-  // (channels c0 + half * VEC ...) straight into fragment order.
-  template <int LI>
-  static __device__ __forceinline__ void stage_a(Smem& s, const Args& a, int wave, int lane,
-                                                 int c0) {
-    constexpr int nql = P::nq(LI);
-    const int row = lane & 31, half = lane >> 5;
-    for (int f = wave; f < nql * RT; f += NW) {
-      const int q = f / RT, rt = f % RT;
-      const int e = rt * 32 + row;
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (s.eid[e] >= 0) {
-        const typename TM::raw* src = reinterpret_cast<const typename TM::raw*>(a.a_src) +
-                                      (static_cast<int64_t>(s.eid[e]) * P::DP + P::mrow(q, LI)) * a.C_k +
-                                      c0 + half * TM::VEC;
-        v = *reinterpret_cast<const uint4*>(src);
-      }
-      *reinterpret_cast<uint4*>(s.stage + (q * RT + rt) * FRAG + lane * 16) = v;
-    }
-  }
-
-  static __device__ __forceinline__ void stage_b(Smem& s, const char* src, int nfrag, int tid) {
-    const uint4* g = reinterpret_cast<const uint4*>(src);
-    uint4* d4 = reinterpret_cast<uint4*>(s.stage + P::A_BYTES);
-    const int n16 = nfrag * (FRAG / 16);
-    for (int i = tid; i < n16; i += NT) d4[i] = g[i];
-  }
-
-  // ------------------------------------------------------------ MFMA step
-  // slot of (degree l, row tile rt, tile type t); t: 0 = G0, [1 = gate],
-  // then (+,-) pairs per m.
-  template <int l, int rt>
-  static constexpr int slot0() { return P::tab.base[l] + rt * P::ntype(l); }
-  template <int l>
-  static constexpr int gt() { return (GATE && l >= 1) ? 1 : 0; }
-
-  template <int W, int LI>
-  static __device__ __forceinline__ void mma_step(f32x16 (&acc)[P::MS], const Smem& s, int lane) {
-    const char* A = s.stage;
-    const char* B = s.stage + P::A_BYTES;
-    static_for<L + 1>([&](auto LO) {
-      constexpr int l = decltype(LO)::value;
-      if constexpr (P::tab.owner[l] == W) {
-        static_for<RT>([&](auto RTI) {
-          constexpr int rt = decltype(RTI)::value;
-          constexpr int sb = slot0<l, rt>();
-          const char* A0 = A + (0 * RT + rt) * FRAG;
-          mma(acc[sb], A0, B + l * FRAG, lane, TM{});
-          if constexpr (GATE && l >= 1) mma(acc[sb + 1], A0, B + (L + 1 + (l - 1)) * FRAG, lane, TM{});
-          static_for<M>([&](auto MI) {
-            constexpr int m = decltype(MI)::value + 1;
-            if constexpr (m <= l && m <= LI) {
-              const char* Ap = A + ((2 * m - 1) * RT + rt) * FRAG;
-              const char* Am = A + ((2 * m) * RT + rt) * FRAG;
-              constexpr int gb = P::gbase(m), nl = L - m + 1, lo = l - m;
-              static_for<2>([&](auto PMI) {
-                constexpr int pm = decltype(PMI)::value;
-                constexpr int sl = sb + gt<l>() + 1 + 2 * (m - 1) + pm;
-                mma(acc[sl], Ap, B + (gb + (0 * 2 + pm) * nl + lo) * FRAG, lane, TM{});
-                mma(acc[sl], Am, B + (gb + (1 * 2 + pm) * nl + lo) * FRAG, lane, TM{});
-              });
-            }
-          });
-        });
-      }
-    });
-  }
-
-  template <int LI>
-  static __device__ __forceinline__ void mma_dispatch(f32x16 (&acc)[P::MS], const Smem& s,
-                                                      int wave, int lane) {
-    static_for<NW>([&](auto WI) {
-      constexpr int w = decltype(WI)::value;
-      if (wave == w) mma_step<w, LI>(acc, s, lane);
-    });
-  }
-
-  template <int LI>
-  static __device__ void kloop(f32x16 (&acc)[P::MS], Smem& s, const Args& a, int cb, int tid,
-                               int wave, int lane) {
-    const int nks = a.C_k / KC;
-    int64_t foff = 0;
-    for (int l = 0; l < LI; ++l) foff += static_cast<int64_t>(P::nbfrag(l)) * nks;
-    const char* wbase = a.wpack + (static_cast<int64_t>(cb) * a.frags_per_cb + foff) * FRAG;
-    constexpr int nb = P::nbfrag(LI);
-    for (int ks = 0; ks < nks; ++ks) {
-      stage_a<LI>(s, a, wave, lane, ks * KC);
-      stage_b(s, wbase + static_cast<int64_t>(ks) * nb * FRAG, nb, tid);
-      __syncthreads();
-      mma_dispatch<LI>(acc, s, wave, lane);
-      __syncthreads();
-    }
-  }
-
-  // ------------------------------------------------------------ epilogue
-  template <int W, int l>
-  static __device__ void epi_degree(f32x16 (&acc)[P::MS], Smem& s, const Args& a, int64_t tile,
-                                    int cb, int wave, int lane, int nvalid, bool first_partial,
-                                    bool last_partial) {
-    constexpr int n = 2 * l + 1;
-    float* stage = reinterpret_cast<float*>(s.stage) + wave * TE * 33;
-    const int co = lane & 31;
-    const int col = cb * CB + co;
-    static_for<RT>([&](auto RTI) {
-      constexpr int rt = decltype(RTI)::value;
-      constexpr int sb = slot0<l, rt>();
-      if constexpr (MODE == FWD) {
-        if (a.bias != nullptr) {
-          const float b0 = a.bias[a.extra + l * a.C_n + col];
-#pragma unroll
-          for (int i = 0; i < 16; ++i) acc[sb][i] += b0;
-          if constexpr (GATE && l >= 1) {
-            const float bg = a.bias[(l - 1) * a.C_n + col];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) acc[sb + 1][i] += bg;
-          }
-        }
-        if constexpr (GATE) {
-          if constexpr (l == 0) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-              const float z = acc[sb][i];
-              acc[sb][i] = z / (1.0f + __expf(-z));
-            }
-          } else {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-              const float g = tanhf(acc[sb + 1][i]);
-              acc[sb][i] *= g;
-              static_for<M>([&](auto MI) {
-                constexpr int m = decltype(MI)::value + 1;
-                if constexpr (m <= l) {
-                  acc[sb + 2 + 2 * (m - 1)][i] *= g;
-                  acc[sb + 3 + 2 * (m - 1)][i] *= g;
-                }
-              });
-            }
-          }
-        }
-      } else {
-        bwd_radial<l, rt, sb>(acc, s, a, col, lane);
-      }
-    });
-    for (int j = 0; j < n; ++j) {
-      static_for<RT>([&](auto RTI) {
-        constexpr int rt = decltype(RTI)::value;
-        constexpr int sb = slot0<l, rt>();
-        constexpr int g1 = gt<l>() + 1;
-        static_for<16>([&](auto II) {
-          constexpr int i = decltype(II)::value;
-          const int e = rt * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-          const float* Dl = s.D + e * P::DS + P::doff(l);
-          float v = Dl[j] * acc[sb][i];
-          static_for<M>([&](auto MI) {
-            constexpr int m = decltype(MI)::value + 1;
-            if constexpr (m <= l) {
-              v = fmaf(Dl[(2 * m - 1) * n + j], acc[sb + g1 + 2 * (m - 1)][i], v);
-              v = fmaf(Dl[(2 * m) * n + j], acc[sb + g1 + 1 + 2 * (m - 1)][i], v);
-            }
-          });
-          stage[e * 33 + co] = v;
-        });
-      });
-      wave_sync();
-      if (lane < 32) {
-        float sum = 0.f;
-        int cur = s.seg[0];
-        bool first = true;
-        const int64_t rowoff = static_cast<int64_t>(l * l + j) * a.C_n + col;
-        for (int r = 0; r < nvalid; ++r) {
-          sum += stage[r * 33 + co];
-          const bool last = (r + 1 == nvalid);
-          if (last || s.seg[r + 1] != cur) {
-            if ((first && first_partial) || (last && last_partial)) {
-              const int slot = first ? 0 : 1;
-              a.part[(tile * 2 + slot) * d * a.C_n + rowoff] = sum;
-            } else {
-              a.out[static_cast<int64_t>(cur) * d * a.C_n + rowoff] = sum;
-            }
-            sum = 0.f;
-            first = false;
-            if (!last) cur = s.seg[r + 1];
-          }
-        }
-      }
-      wave_sync();
-    }
-  }
-
-  // BWD_DX: the accumulators hold dY on the forward-input side of degree l.
-  // Writes d(rad) = sum_(+/-) dY * R (R: unscaled rotated forward inputs, saved
-  // by the forward) and scales dY by rad before the inverse rotation.
-  template <int l, int rt, int sb>
-  static __device__ __forceinline__ void bwd_radial(f32x16 (&acc)[P::MS], Smem& s, const Args& a,
-                                                    int col, int lane) {
-    if (a.rad == nullptr) return;
-    const int64_t rw = rad_width<L, M>(a.C_n);
-    static_for<16>([&](auto II) {
-      constexpr int i = decltype(II)::value;
-      const int e = rt * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-      if (s.eid[e] < 0) return;
-      const int64_t eo = static_cast<int64_t>(s.eid[e]) * rw;
-      const typename TM::raw* rp = reinterpret_cast<const typename TM::raw*>(a.rad) + eo;
-      const typename TM::raw* rs = reinterpret_cast<const typename TM::raw*>(a.rsave) +
-                                   static_cast<int64_t>(s.eid[e]) * P::DP * a.C_n + col;
-      {
-        const int slot = rad_slot<L, M>(0, l, col, a.C_n);
-        const float dy = acc[sb][i];
-        if (a.drad)
-          reinterpret_cast<typename TM::raw*>(a.drad)[eo + slot] =
-              TM::cvt(dy * TM::load(rs + P::mrow(0, l) * a.C_n));
-        acc[sb][i] = dy * TM::load(rp + slot);
-      }
-      static_for<M>([&](auto MI) {
-        constexpr int m = decltype(MI)::value + 1;
-        if constexpr (m <= l) {
-          const int slot = rad_slot<L, M>(2 * m - 1, l, col, a.C_n);
-          const float r = TM::load(rp + slot);
-          const float dyp = acc[sb + 1 + 2 * (m - 1)][i], dym = acc[sb + 2 + 2 * (m - 1)][i];
-          if (a.drad)
-            reinterpret_cast<typename TM::raw*>(a.drad)[eo + slot] =
-                TM::cvt(dyp * TM::load(rs + P::mrow(2 * m - 1, l) * a.C_n) +
-                        dym * TM::load(rs + P::mrow(2 * m, l) * a.C_n));
-          acc[sb + 1 + 2 * (m - 1)][i] = dyp * r;
-          acc[sb + 2 + 2 * (m - 1)][i] = dym * r;
-        }
-      });
-    });
-  }
-
-  template <int W>
-  static __device__ void epilogue(f32x16 (&acc)[P::MS], Smem& s, const Args& a, int64_t tile,
-                                  int cb, int wave, int lane, int nvalid, bool fp, bool lp) {
-    static_for<L + 1>([&](auto LO) {
-      constexpr int l = decltype(LO)::value;
-      if constexpr (P::tab.owner[l] == W) epi_degree<W, l>(acc, s, a, tile, cb, wave, lane, nvalid, fp, lp);
-    });
-  }
-
-  static __device__ void run(const Args& a) {
-    __shared__ Smem s;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    // XCD-aware mapping: workgroups of one channel block share a set of XCDs
-    // (consecutive workgroup ids are dispatched round-robin over the 8 XCDs),
-    // so each XCD's L2 holds the packed weights of fewer channel blocks.
-    const int64_t bid = blockIdx.x;
-    int64_t tile;
-    int cb;
-    if (a.n_cb > 1 && (8 % a.n_cb) == 0) {
-      const int per = 8 / a.n_cb;
-      const int xcd = static_cast<int>(bid % 8);
-      cb = xcd / per;
-      tile = (bid / 8) * per + (xcd % per);
-    } else {
-      cb = static_cast<int>(bid % a.n_cb);
-      tile = bid / a.n_cb;
-    }
-    if (tile >= a.ntiles) return;  // whole workgroup exits together
-    const int64_t e0 = tile * TE;
-    const int nvalid = static_cast<int>((a.E - e0) < TE ? (a.E - e0) : TE);
-    if (tid < TE) {
-      const bool v = tid < nvalid;
-      const int64_t p = e0 + tid;
-      s.seg[tid] = v ? a.seg[p] : -1;
-      s.eid[tid] = v ? (a.eidx ? a.eidx[p] : static_cast<int>(p)) : -1;
-    }
-    __syncthreads();
-    // kept Wigner rows of the tile's edges
-    for (int i = tid; i < TE * P::DS; i += NT) {
-      const int e = i / P::DS, k = i - e * P::DS;
-      s.D[i] = s.eid[e] >= 0 ? a.dk[static_cast<int64_t>(s.eid[e]) * P::DS + k] : 0.f;
-    }
-    __syncthreads();
-    const bool first_partial = (e0 > 0) && (a.seg[e0 - 1] == a.seg[e0]);
-    const bool last_partial =
-        (e0 + nvalid < a.E) && (a.seg[e0 + nvalid] == a.seg[e0 + nvalid - 1]);
-    f32x16 acc[P::MS];
-#pragma unroll
-    for (int k = 0; k < P::MS; ++k)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[k][i] = 0.f;
-
-    static_for<L + 1>([&](auto LI) {
-      kloop<decltype(LI)::value>(acc, s, a, cb, tid, wave, lane);
-    });
-
-    static_for<NW>([&](auto WI) {
-      constexpr int w = decltype(WI)::value;
-      if (wave == w) epilogue<w>(acc, s, a, tile, cb, wave, lane, nvalid, first_partial, last_partial);
-    });
-  }
-};
-
-template <int L, int M, bool GATE, int NW, int RT, class TM, class TX, int MODE>
-__global__ __launch_bounds__(NW * 64, (NW == 4 ? 2 : 1)) void message_kernel(Args a) {
-  Kernel<L, M, GATE, NW, RT, TM, TX, MODE>::run(a);
-}
-
-}  // namespace msg
-}  // namespace maloq
-
-
-namespace maloq {
-namespace msg {
 
 // --------------------------------------------------------------- edge prep
 // Per edge, once: the kept rows |m| <= mmax of its Wigner-D (from the Euler
@@ -560,7 +228,7 @@ struct PrepArgs {
   const float* jd;      // packed J_0..J_L
   void* y;              // [E_all, d', C] (TM raw) by edge id
   void* r;              // nullable: unscaled rows, same layout
-  float* dk;            // [E_all, DS] kept Wigner rows by edge id
+  float* dk;            // [E_all, WS] kept Wigner rows by edge id (pair layout)
   int build_d;          // 1: compute and write dk; 0: read dk
   int64_t E;
   int C;
@@ -610,12 +278,14 @@ struct Prep {
   static constexpr int TE = 32;
   static constexpr int NT = 256;
   using P = Plan<L, M, false, 4, 1>;
+  using PL = PairLayout<L, M>;
+  static constexpr int WS = PL::WS;
   static constexpr int d = (L + 1) * (L + 1);
   static constexpr int V = TM::VEC;
 
   struct Smem {
     float J[jd_size(L)];
-    float D[TE * P::DS];
+    alignas(16) float D[TE * WS];
     float eul[TE * 3];
     int gid[TE];
     int eid[TE];
@@ -644,7 +314,6 @@ struct Prep {
       }
       __syncthreads();
       const int nql = P::nq(l);
-      const int dof = P::doff(l);
       for (int q = tid; q < TE * nql * n; q += NT) {
         const int e = q / (nql * n), r = q % (nql * n);
         const int qi = r / n, j = r % n;
@@ -663,7 +332,7 @@ struct Prep {
           const int f = l - i;
           v = xcos(ta, f) * va + xsin(ta + (L + 1), f) * vb;
         }
-        s.D[e * P::DS + dof + qi * n + j] = v;
+        s.D[e * WS + PL::woff(l) + (j >> 1) * PL::pblk(l) + 2 * qi + (j & 1)] = v;
       }
       __syncthreads();
     }
@@ -686,15 +355,22 @@ struct Prep {
     }
     __syncthreads();
     if (a.build_d) {
+      // pads of the pair layout stay zero
+      for (int i = tid; i < TE * WS; i += NT) s.D[i] = 0.f;
+      __syncthreads();
       build_d(s, tid);
-      for (int i = tid; i < nvalid * P::DS; i += NT) {
-        const int e = i / P::DS, k = i - e * P::DS;
-        a.dk[static_cast<int64_t>(s.eid[e]) * P::DS + k] = s.D[i];
+      float4* dk4 = reinterpret_cast<float4*>(a.dk);
+      const float4* d4 = reinterpret_cast<const float4*>(s.D);
+      for (int i = tid; i < nvalid * (WS / 4); i += NT) {
+        const int e = i / (WS / 4), k = i - e * (WS / 4);
+        dk4[static_cast<int64_t>(s.eid[e]) * (WS / 4) + k] = d4[i];
       }
     } else {
-      for (int i = tid; i < TE * P::DS; i += NT) {
-        const int e = i / P::DS, k = i - e * P::DS;
-        s.D[i] = s.eid[e] >= 0 ? a.dk[static_cast<int64_t>(s.eid[e]) * P::DS + k] : 0.f;
+      const float4* dk4 = reinterpret_cast<const float4*>(a.dk);
+      float4* d4 = reinterpret_cast<float4*>(s.D);
+      for (int i = tid; i < TE * (WS / 4); i += NT) {
+        const int e = i / (WS / 4), k = i - e * (WS / 4);
+        d4[i] = s.eid[e] >= 0 ? dk4[static_cast<int64_t>(s.eid[e]) * (WS / 4) + k] : make_float4(0.f, 0.f, 0.f, 0.f);
       }
       __syncthreads();
     }
@@ -714,7 +390,7 @@ struct Prep {
         float xv[n][V];
 #pragma unroll
         for (int j = 0; j < n; ++j) load_vec<TX, V>(xg + (l * l + j) * a.C, xv[j]);
-        const float* Dl = s.D + e * P::DS + P::doff(l);
+        const float* Dl = s.D + e * WS;
 #pragma unroll
         for (int q = 0; q < P::nq(l); ++q) {
           float o[V];
@@ -722,7 +398,7 @@ struct Prep {
           for (int c = 0; c < V; ++c) {
             float acc = 0.f;
 #pragma unroll
-            for (int j = 0; j < n; ++j) acc = fmaf(Dl[q * n + j], xv[j][c], acc);
+            for (int j = 0; j < n; ++j) acc = fmaf(Dl[PL::at(l, q, j)], xv[j][c], acc);
             o[c] = acc;
           }
           const int64_t ro_off = static_cast<int64_t>(P::mrow(q, l)) * a.C;

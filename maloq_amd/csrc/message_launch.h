@@ -1,16 +1,17 @@
 #pragma once
 // Host-side launch helpers shared by the per-lmax instantiation files.
-#include "message_impl.h"
+#include "message_gemm.h"
 
 namespace maloq {
 namespace msg {
 
-// Waves per workgroup and 32-edge row tiles per workgroup for each lmax.
-// (lmax <= 4, no gate): 4 waves x 64 edges; gated or lmax > 4: 32-edge tiles
-// (4 or 8 waves) so the accumulators of a wave stay within 256 registers.
+// Waves per workgroup and 32-edge row tiles per workgroup for each lmax:
+// lmax <= 4 without gate: 4 waves x 64 edges; gated or lmax > 4: 4 waves x
+// 32 edges, so a wave's accumulators and operand registers stay within the
+// 256 registers of two resident workgroups per CU.
 template <int L, bool GATE>
 struct Cfg {
-  static constexpr int NW = (L <= 4) ? 4 : 8;
+  static constexpr int NW = 4;
   static constexpr int RT = (L <= 4 && !GATE) ? 2 : 1;
 };
 
@@ -19,17 +20,14 @@ inline int tile_edges(int lmax, int gate) { return (lmax <= 4 && !gate) ? 64 : 3
 template <int L, int M, bool GATE, class TM, class TX, int MODE>
 int launch(const Args& a, hipStream_t s) {
   constexpr int NW = Cfg<L, GATE>::NW, RT = Cfg<L, GATE>::RT;
-  using P = Plan<L, M, GATE, NW, RT>;
-  // Must match the workgroup -> (tile, channel block) mapping of Kernel::run.
-  int64_t grid = a.ntiles * a.n_cb;
-  if (a.n_cb > 1 && (8 % a.n_cb) == 0) {
-    const int per = 8 / a.n_cb;
-    grid = ((a.ntiles + per - 1) / per) * 8;
-  }
+  using P = GPlan<L, M, GATE, NW, RT>;
+  // Must match the workgroup -> (tile, channel block) mapping of Gemm::run:
+  // tiles in groups of 8 (one per XCD), n_cb workgroups per tile.
+  const int64_t grid = ((a.ntiles + 7) / 8) * 8 * a.n_cb;
   MALOQ_REQUIRE(grid < (int64_t(1) << 31), "grid too large");
-  hipLaunchKernelGGL((message_kernel<L, M, GATE, NW, RT, TM, TX, MODE>),
+  hipLaunchKernelGGL((gemm_kernel<L, M, GATE, NW, RT, TM, MODE>),
                      dim3(static_cast<unsigned>(grid)), dim3(P::NT), 0, s, a);
-  return check_launch("message_kernel");
+  return check_launch("gemm_kernel");
 }
 
 // dtype: 0 fp32, 1 bf16; mode: FWD or BWD_DX.

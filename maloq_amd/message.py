@@ -7,8 +7,8 @@ Host side of ``maloq_message_fwd`` / ``maloq_message_bwd_dx`` (include/maloq_hip
 * ``pack_weights``     the SO(2) weights (reference layout of SO2_Convolution:
                        ``fc_m0.weight`` [N0, K0], ``so2_m_conv[m-1].fc.weight``
                        [2 half_m, K_m], so2_layers.py:106-130) gathered into the
-                       kernel's MFMA fragment order with the complex +-m mix
-                       folded in ([[Wr, Wi], [-Wi, Wr]]).
+                       kernel's MFMA fragment order; Wr and Wi of each m are
+                       stored once and the kernel forms the complex +-m mix.
 * ``message_block``    autograd function: node output of
                        rotate -> [radial scale] -> SO(2) -> [bias, gate] ->
                        inverse rotate -> segment sum (Edgewise.forward_node,
@@ -69,33 +69,34 @@ class MessagePlan:
 
 # ------------------------------------------------------------ weight packing
 def _frag_list(lmax, mmax, gate, l_k):
-    """Canonical B-fragment order of one K step at kernel-input degree l_k."""
-    out = [("g0", 0, 0, l) for l in range(lmax + 1)]
-    if gate:
-        out += [("gate", 0, 0, l) for l in range(1, lmax + 1)]
-    for m in range(1, min(mmax, l_k) + 1):
-        for kf in (0, 1):
-            for pm in (0, 1):
-                out += [(m, kf, pm, l) for l in range(m, lmax + 1)]
+    """B fragments of one K step at kernel-input degree l_k, grouped by kernel-
+    output degree l_n: g0, [gate], then (Wr, Wi) for m = 1 .. min(mmax, l_k, l_n).
+    Wr and Wi are stored once; the kernel forms the complex mix (and -Wi)."""
+    out = []
+    for l_n in range(lmax + 1):
+        out.append(("g0", 0, l_n))
+        if gate and l_n >= 1:
+            out.append(("gate", 0, l_n))
+        for m in range(1, min(mmax, l_k, l_n) + 1):
+            out += [("wr", m, l_n), ("wi", m, l_n)]
     return out
 
 
 @functools.lru_cache(maxsize=32)
 def _pack_index(dtype_code, lmax, mmax, gate, c_in, c_out, mode):
-    """Gather index and sign, per packed element, into the flat weight vector
-    cat(W0.flatten(), W1.flatten(), ..., [0]).  mode 0: forward GEMM (kernel
-    input = c_in); mode 1: transposed GEMM of the input gradient."""
+    """Gather index, per packed element, into the flat weight vector
+    cat(W0.flatten(), W1.flatten(), ...).  mode 0: forward GEMM (kernel input =
+    c_in side); mode 1: transposed GEMM of the input gradient (kernel input =
+    c_out side).  Fragment order: output-channel block, kernel-input degree,
+    K step, then _frag_list; element order: the MFMA B operand's lane order."""
     bf16 = dtype_code == 1
     kc = 16 if bf16 else 8
     fe = 512 if bf16 else 256
     extra = lmax * c_out if gate else 0
-    n0 = extra + (lmax + 1) * c_out
     k0 = (lmax + 1) * c_in
-    offs = [0, n0 * k0]
+    offs = [0, (extra + (lmax + 1) * c_out) * k0]
     for m in range(1, mmax + 1):
         offs.append(offs[-1] + 2 * (lmax - m + 1) * c_out * (lmax - m + 1) * c_in)
-    zero = offs[-1]
-    # element (k, col) of a fragment
     e = np.arange(fe)
     if bf16:
         k_of = (e // 256) * 8 + (e % 8)
@@ -104,40 +105,33 @@ def _pack_index(dtype_code, lmax, mmax, gate, c_in, c_out, mode):
         k_of = (e // 128) * 4 + (e % 4)
         col_of = (e // 4) % 32
     c_k, c_n = (c_in, c_out) if mode == 0 else (c_out, c_in)
-    idx_parts, sgn_parts = [], []
-    for cb in range(c_n // CB):
-        cn = cb * CB + col_of
-        for l_k in range(lmax + 1):
-            frags = _frag_list(lmax, mmax, gate and mode == 0, l_k)
-            for ks in range(c_k // kc):
-                ck = ks * kc + k_of
-                for g, kf, pm, l_n in frags:
-                    sgn = np.ones(fe, np.int8)
-                    if mode == 0:
-                        c, co, l_in, l_out = ck, cn, l_k, l_n
-                    else:
-                        c, co, l_in, l_out = cn, ck, l_n, l_k
-                    if g == "g0":
-                        idx = offs[0] + (extra + l_out * c_out + co) * k0 + l_in * c_in + c
-                    elif g == "gate":
-                        idx = offs[0] + ((l_out - 1) * c_out + co) * k0 + l_in * c_in + c
-                    else:
-                        m = g
-                        kfw, pmw = (kf, pm) if mode == 0 else (pm, kf)
-                        km = (lmax - m + 1) * c_in
-                        half = (lmax - m + 1) * c_out
-                        ko = (l_out - m) * c_out + co
-                        ki = (l_in - m) * c_in + c
-                        if kfw == pmw:            # Wr
-                            row = ko
-                        else:                     # +/- Wi
-                            row = half + ko
-                            if kfw == 1:          # x- -> y+: -Wi
-                                sgn = -sgn
-                        idx = offs[m] + row * km + ki
-                    idx_parts.append(np.asarray(idx, np.int64))
-                    sgn_parts.append(sgn)
-    return np.concatenate(idx_parts), np.concatenate(sgn_parts), zero
+    cbs = np.arange(c_n // CB)
+    kss = np.arange(c_k // kc)
+    # [cb, ks, element] kernel-side channel indices
+    cn = (cbs[:, None, None] * CB + col_of[None, None, :]) + 0 * kss[None, :, None]
+    ck = (kss[None, :, None] * kc + k_of[None, None, :]) + 0 * cbs[:, None, None]
+    per_cb = []  # list over l_k of [cb, ks, frag, element]
+    for l_k in range(lmax + 1):
+        frags = []
+        for kind, m, l_n in _frag_list(lmax, mmax, gate and mode == 0, l_k):
+            if mode == 0:
+                c, co, l_in, l_out = ck, cn, l_k, l_n
+            else:
+                c, co, l_in, l_out = cn, ck, l_n, l_k
+            if kind == "g0":
+                idx = offs[0] + (extra + l_out * c_out + co) * k0 + l_in * c_in + c
+            elif kind == "gate":
+                idx = offs[0] + ((l_out - 1) * c_out + co) * k0 + l_in * c_in + c
+            else:
+                km = (lmax - m + 1) * c_in
+                row = (l_out - m) * c_out + co
+                if kind == "wi":
+                    row = row + (lmax - m + 1) * c_out
+                idx = offs[m] + row * km + (l_in - m) * c_in + c
+            frags.append(idx)
+        per_cb.append(np.stack(frags, axis=2))      # [cb, ks, nfrag, fe]
+    packed = np.concatenate([p.reshape(p.shape[0], -1) for p in per_cb], axis=1)  # [cb, ...]
+    return packed.reshape(-1).astype(np.int64), offs[-1]
 
 
 _PACK_DEV: dict = {}
@@ -149,15 +143,14 @@ def pack_weights(w0, wm, lmax, mmax, gate, c_in, c_out, dtype, mode=0):
     key = (code, lmax, mmax, bool(gate), c_in, c_out, mode, str(w0.device))
     hit = _PACK_DEV.get(key)
     if hit is None:
-        idx, sgn, zero = _pack_index(code, lmax, mmax, bool(gate), c_in, c_out, mode)
-        hit = (torch.from_numpy(idx).to(w0.device), torch.from_numpy(sgn).to(w0.device), zero)
+        idx, total = _pack_index(code, lmax, mmax, bool(gate), c_in, c_out, mode)
+        hit = (torch.from_numpy(idx).to(w0.device), total)
         _PACK_DEV[key] = hit
-    idx, sgn, zero = hit
+    idx, total = hit
     with torch.no_grad():
-        flat = torch.cat([w0.reshape(-1)] + [w.reshape(-1) for w in wm[:mmax]] +
-                         [w0.new_zeros(1)]).float()
-        assert flat.numel() == zero + 1, "weight shapes do not match (lmax, mmax, channels)"
-        packed = (flat[idx] * sgn).to(dtype)
+        flat = torch.cat([w0.reshape(-1)] + [w.reshape(-1) for w in wm[:mmax]]).float()
+        assert flat.numel() == total, "weight shapes do not match (lmax, mmax, channels)"
+        packed = flat[idx].to(dtype)
     want = _lib.load().maloq_message_wpack_bytes(code, lmax, mmax, int(bool(gate and mode == 0)),
                                                 c_in if mode == 0 else c_out,
                                                 c_out if mode == 0 else c_in)
@@ -185,7 +178,8 @@ def kept_rows(lmax, mmax):
 
 
 def wigner_floats(lmax, mmax):
-    return sum((1 + 2 * min(mmax, l)) * (2 * l + 1) for l in range(lmax + 1))
+    """Floats per edge of the kept Wigner rows in the kernels' pair-major layout."""
+    return sum((l + 1) * ((2 * (1 + 2 * min(mmax, l)) + 3) // 4 * 4) for l in range(lmax + 1))
 
 
 def message_forward(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=False, wpack=None,
