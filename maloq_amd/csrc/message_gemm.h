@@ -128,19 +128,16 @@ struct GPlan {
   static constexpr int NA = (nq(L) * RT * 64 + NT - 1) / NT;  // A chunks per thread
 };
 
-__device__ __forceinline__ uint4 neg_frag(uint4 v, BF16) {
-  return make_uint4(v.x ^ 0x80008000u, v.y ^ 0x80008000u, v.z ^ 0x80008000u, v.w ^ 0x80008000u);
+// One lane's 16 bytes of an MFMA operand fragment (a native vector, so that
+// arrays of fragments are promoted to registers).
+typedef unsigned int frag_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ frag_t neg_frag(frag_t v, BF16) { return v ^ 0x80008000u; }
+__device__ __forceinline__ frag_t neg_frag(frag_t v, F32) { return v ^ 0x80000000u; }
+__device__ __forceinline__ void mfma(f32x16& acc, frag_t a, frag_t b, BF16) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16((bf16x8)a, (bf16x8)b, acc, 0, 0, 0);
 }
-__device__ __forceinline__ uint4 neg_frag(uint4 v, F32) {
-  return make_uint4(v.x ^ 0x80000000u, v.y ^ 0x80000000u, v.z ^ 0x80000000u, v.w ^ 0x80000000u);
-}
-__device__ __forceinline__ void mfma(f32x16& acc, uint4 a, uint4 b, BF16) {
-  bf16x8 av, bv;
-  __builtin_memcpy(&av, &a, 16);
-  __builtin_memcpy(&bv, &b, 16);
-  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
-}
-__device__ __forceinline__ void mfma(f32x16& acc, uint4 a, uint4 b, F32) {
+__device__ __forceinline__ void mfma(f32x16& acc, frag_t a, frag_t b, F32) {
   acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.x), __uint_as_float(b.x), acc, 0, 0, 0);
   acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.y), __uint_as_float(b.y), acc, 0, 0, 0);
   acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.z), __uint_as_float(b.z), acc, 0, 0, 0);
@@ -150,7 +147,8 @@ __device__ __forceinline__ void mfma(f32x16& acc, uint4 a, uint4 b, F32) {
 template <int L, int M, bool GATE, int NW, int RT, class TM, int MODE>
 struct Gemm {
   using P = GPlan<L, M, GATE, NW, RT>;
-  static constexpr int TE = P::TE, NT = P::NT, KC = TM::KC, NA = P::NA;
+  static constexpr int TE = P::TE, NT = P::NT, KC = TM::KC;
+  static_assert(NW == 4, "the epilogue staging holds two waves per A stage");
   static constexpr int d = (L + 1) * (L + 1);
 
   struct Smem {
@@ -158,64 +156,99 @@ struct Gemm {
     float* optr[TE];  // destination row block of the segment ending at each edge
     int seg[TE];
     int eid[TE];
-    alignas(16) char u[P::U_BYTES];
   };
+  // A stages (two distinct LDS objects, so the compiler can tell a stage being
+  // filled by DMA from the one being read); after the K loop they hold the
+  // epilogue's per-wave staging (two waves per stage).
+  // per-wave epilogue staging: the 16-edge scan chunk or the 32 x 36 transpose tile
+  static constexpr int PW = (P::CH * 64 > 32 * 36 ? P::CH * 64 : 32 * 36) * 4;
+  static constexpr int SB = (P::A_BYTES > 2 * PW) ? P::A_BYTES : 2 * PW;
+  typedef __attribute__((address_space(3))) void lds_void;
 
   // ------------------------------------------------------------ A operand
+  // A staging: the nq(L) RT fragments of a K step are split over the waves,
+  // waves with the least MFMA work taking the most (their registers are free);
+  // wave W stages the fragments f with stager(f) == W, k-th of them in slot k.
+  // Row type q = f / RT, row tile f % RT; lane (row, half) copies 16 bytes of
+  // its edge's row.  Which fragments exist is a compile-time property of
+  // (W, k, LI), so every load is unconditional (which keeps the compiler's
+  // vmcnt accounting exact); lanes of edges beyond the tile read the tile's
+  // first edge, whose rows in those accumulator lanes are never stored.
+  struct ATab {
+    int frag[NW][P::nq(L) * RT];
+    int count[NW];
+  };
+  static constexpr ATab make_atab() {
+    ATab t{};
+    int order[NW] = {};
+    for (int w = 0; w < NW; ++w) order[w] = w;
+    for (int i = 0; i < NW; ++i)  // waves by ascending MFMA slots
+      for (int j = i + 1; j < NW; ++j)
+        if (P::tab.nslots[order[j]] < P::tab.nslots[order[i]]) {
+          const int x = order[i];
+          order[i] = order[j];
+          order[j] = x;
+        }
+    constexpr int F = P::nq(L) * RT;
+    for (int f = 0; f < F; ++f) {
+      int best = order[0];  // fewest staged so far, ties to the lighter wave
+      for (int i = 1; i < NW; ++i) {
+        const int w = order[i];
+        const int cb = t.count[best] - (best == order[0] ? (F + NW - 1) / NW - F / NW : 0);
+        const int cw = t.count[w] - (w == order[0] ? (F + NW - 1) / NW - F / NW : 0);
+        if (cw < cb) best = w;
+      }
+      t.frag[best][t.count[best]++] = f;
+    }
+    return t;
+  }
+  static constexpr ATab atab = make_atab();
+  static constexpr int NAW = [] {
+    int m = 1;
+    for (int w = 0; w < NW; ++w) m = atab.count[w] > m ? atab.count[w] : m;
+    return m;
+  }();
+  template <int W, int k>
+  static constexpr int afrag() { return atab.frag[W][k]; }
+  template <int W, int k, int LI>
+  static constexpr bool avalid() { return k < atab.count[W] && afrag<W, k>() < P::nq(LI) * RT; }
+
   struct AState {
-    int64_t ebase[NA];  // element offset of (edge, row 0, channel half) or -1
-    int q[NA];          // row type of the chunk (-1: thread has no chunk)
-    int64_t rowoff[NA];
-    uint4 reg[NA];
+    int64_t ebase[NAW];  // element offset of (edge, row 0, channel half)
   };
 
-  static __device__ __forceinline__ void a_init(AState& st, const Smem& s, const Args& a, int tid) {
-#pragma unroll
-    for (int k = 0; k < NA; ++k) {
-      const int c = tid + k * NT;
-      const int f = c >> 6, ln = c & 63;
-      const int q = f / RT, rt = f % RT;
-      st.q[k] = (c < P::nq(L) * RT * 64) ? q : -1;
-      const int e = rt * 32 + (ln & 31);
-      const int ei = (st.q[k] >= 0) ? s.eid[e] : -1;
-      st.ebase[k] = ei >= 0 ? static_cast<int64_t>(ei) * P::DP * a.C_k + (ln >> 5) * TM::VEC : -1;
-      st.rowoff[k] = 0;
-    }
+  template <int W>
+  static __device__ __forceinline__ void a_init(AState& st, const Smem& s, const Args& a, int lane) {
+    static_for<NAW>([&](auto K) {
+      constexpr int k = decltype(K)::value;
+      if constexpr (k >= atab.count[W]) return;
+      constexpr int rt = afrag<W, k>() % RT;
+      const int e = rt * 32 + (lane & 31);
+      const int ei = s.eid[e] >= 0 ? s.eid[e] : s.eid[0];
+      st.ebase[k] = static_cast<int64_t>(ei) * P::DP * a.C_k + (lane >> 5) * TM::VEC;
+    });
   }
-  template <int LI>
-  static __device__ __forceinline__ void a_rows(AState& st, const Args& a) {
-#pragma unroll
-    for (int k = 0; k < NA; ++k) {
-      int r = 0;
-      static_for<P::nq(LI)>([&](auto Q) {
-        if (st.q[k] == decltype(Q)::value) r = P::mrow(decltype(Q)::value, LI);
-      });
-      st.rowoff[k] = static_cast<int64_t>(r) * a.C_k;
-    }
-  }
-  template <int LI>
-  static __device__ __forceinline__ void a_load(AState& st, const Args& a, int ks) {
+  // Direct global -> LDS copies of this wave's fragments of step (LI, ks):
+  // lane i's 16 bytes land at stage + f*FRAG + 16 i, the MFMA lane order.
+  template <int W, int LI>
+  static __device__ __forceinline__ void a_dma(const AState& st, char* stage, const Args& a, int ks) {
     const typename TM::raw* y = reinterpret_cast<const typename TM::raw*>(a.a_src);
-#pragma unroll
-    for (int k = 0; k < NA; ++k) {
-      st.reg[k] = make_uint4(0u, 0u, 0u, 0u);
-      if (st.q[k] >= 0 && st.q[k] < P::nq(LI) && st.ebase[k] >= 0)
-        st.reg[k] = *reinterpret_cast<const uint4*>(y + st.ebase[k] + st.rowoff[k] + ks * KC);
-    }
-  }
-  template <int LI>
-  static __device__ __forceinline__ void a_store(const AState& st, Smem& s, int buf, int tid) {
-#pragma unroll
-    for (int k = 0; k < NA; ++k) {
-      const int c = tid + k * NT;
-      if (st.q[k] >= 0 && st.q[k] < P::nq(LI))
-        *reinterpret_cast<uint4*>(s.u + buf * P::A_BYTES + c * 16) = st.reg[k];
-    }
+    static_for<NAW>([&](auto K) {
+      constexpr int k = decltype(K)::value;
+      if constexpr (avalid<W, k, LI>()) {
+        constexpr int q = afrag<W, k>() / RT;
+#if defined(__HIP_DEVICE_COMPILE__)  // the host pass does not know gfx950's 16-byte form
+        __builtin_amdgcn_global_load_lds(
+            y + st.ebase[k] + static_cast<int64_t>(P::mrow(q, LI)) * a.C_k + ks * KC,
+            (lds_void*)(stage + afrag<W, k>() * FRAG), 16, 0, 0);
+#endif
+      }
+    });
   }
 
   // ------------------------------------------------------------ B operand
   template <int W, int LI>
-  static __device__ __forceinline__ void b_load(uint4 (&b)[P::NBW], const char* wp, int64_t foff,
+  static __device__ __forceinline__ void b_load(frag_t (&b)[P::NBW], const char* wp, int64_t foff,
                                                 int ks, int lane) {
     const char* base = wp + (foff + static_cast<int64_t>(ks) * P::nbfrag(LI)) * FRAG + lane * 16;
     static_for<L + 1>([&](auto LO) {
@@ -224,53 +257,132 @@ struct Gemm {
         static_for<P::nbl(LI, lo)>([&](auto T) {
           constexpr int t = decltype(T)::value;
           b[P::wboff(W, LI, lo) + t] =
-              *reinterpret_cast<const uint4*>(base + (P::bbase(LI, lo) + t) * FRAG);
+              *reinterpret_cast<const frag_t*>(base + (P::bbase(LI, lo) + t) * FRAG);
         });
       }
     });
   }
 
   // ------------------------------------------------------------ MFMA step
-  template <int W, int LI>
-  static __device__ __forceinline__ void step(f32x16 (&acc)[P::MSLOT], const char* A,
-                                              const uint4 (&b)[P::NBW], int lane) {
-    static_for<RT>([&](auto RTI) {
-      constexpr int rt = decltype(RTI)::value;
-      uint4 af[P::nq(LI)];
-      static_for<P::nq(LI)>([&](auto Q) {
-        constexpr int q = decltype(Q)::value;
-        af[q] = *reinterpret_cast<const uint4*>(A + (q * RT + rt) * FRAG + lane * 16);
-      });
-      static_for<L + 1>([&](auto LO) {
-        constexpr int lo = decltype(LO)::value;
-        if constexpr (P::tab.owner[lo] == W) {
-          constexpr int sb = P::tab.base[lo] + rt * P::ntype(lo);
-          constexpr int bo = P::wboff(W, LI, lo);
-          mfma(acc[sb], af[0], b[bo], TM{});
-          if constexpr (P::gt(lo)) mfma(acc[sb + 1], af[0], b[bo + 1], TM{});
-          static_for<M>([&](auto MI) {
-            constexpr int m = decltype(MI)::value + 1;
-            if constexpr (m <= LI && m <= lo) {
-              constexpr int bw = bo + 1 + P::gt(lo) + 2 * (m - 1);
-              constexpr int sp = sb + P::qtype(2 * m - 1, lo), sm = sb + P::qtype(2 * m, lo);
-              const uint4 wr = b[bw], wi = b[bw + 1], nwi = neg_frag(wi, TM{});
-              const uint4 ap = af[2 * m - 1], am = af[2 * m];
-              if constexpr (MODE == FWD) {
-                mfma(acc[sp], ap, wr, TM{});
-                mfma(acc[sm], ap, wi, TM{});
-                mfma(acc[sp], am, nwi, TM{});
-                mfma(acc[sm], am, wr, TM{});
-              } else {
-                mfma(acc[sp], ap, wr, TM{});
-                mfma(acc[sm], ap, nwi, TM{});
-                mfma(acc[sp], am, wi, TM{});
-                mfma(acc[sm], am, wr, TM{});
-              }
-            }
-          });
-        }
-      });
+  // Fragment (row type q, all row tiles) of the current stage.
+  template <int q>
+  static __device__ __forceinline__ void read_q(frag_t (&af)[RT], const char* A, int lane) {
+    static_for<RT>([&](auto R) {
+      constexpr int rt = decltype(R)::value;
+      af[rt] = *reinterpret_cast<const frag_t*>(A + (q * RT + rt) * FRAG + lane * 16);
     });
+  }
+  // m = 0 (and gate) products of every owned degree.
+  template <int W, int LI>
+  static __device__ __forceinline__ void mma_m0(f32x16 (&acc)[P::MSLOT], const frag_t (&a0)[RT],
+                                                const frag_t (&b)[P::NBW]) {
+    static_for<L + 1>([&](auto LO) {
+      constexpr int lo = decltype(LO)::value;
+      if constexpr (P::tab.owner[lo] == W) {
+        constexpr int bo = P::wboff(W, LI, lo);
+        static_for<RT>([&](auto R) {
+          constexpr int rt = decltype(R)::value;
+          constexpr int sb = P::tab.base[lo] + rt * P::ntype(lo);
+          mfma(acc[sb], a0[rt], b[bo], TM{});
+          if constexpr (P::gt(lo)) mfma(acc[sb + 1], a0[rt], b[bo + 1], TM{});
+        });
+      }
+    });
+  }
+  // +-m products of every owned degree.  Forward: y+ += Wr x+ - Wi x-,
+  // y- += Wi x+ + Wr x-; input gradient: dx+ += Wr dy+ + Wi dy-,
+  // dx- += -Wi dy+ + Wr dy-.  The negated Wi is formed after the last use of Wi.
+  template <int W, int LI, int m>
+  static __device__ __forceinline__ void mma_m(f32x16 (&acc)[P::MSLOT], const frag_t (&ap)[RT],
+                                               const frag_t (&am)[RT], const frag_t (&b)[P::NBW]) {
+    static_for<L + 1>([&](auto LO) {
+      constexpr int lo = decltype(LO)::value;
+      if constexpr (P::tab.owner[lo] == W && m <= lo) {
+        constexpr int bw = P::wboff(W, LI, lo) + 1 + P::gt(lo) + 2 * (m - 1);
+        const frag_t wr = b[bw], wi = b[bw + 1];
+        static_for<RT>([&](auto R) {
+          constexpr int rt = decltype(R)::value;
+          constexpr int sb = P::tab.base[lo] + rt * P::ntype(lo);
+          constexpr int sp = sb + P::qtype(2 * m - 1, lo), sm = sb + P::qtype(2 * m, lo);
+          if constexpr (MODE == FWD) {
+            mfma(acc[sm], ap[rt], wi, TM{});
+            mfma(acc[sm], am[rt], wr, TM{});
+            mfma(acc[sp], ap[rt], wr, TM{});
+          } else {
+            mfma(acc[sp], ap[rt], wr, TM{});
+            mfma(acc[sp], am[rt], wi, TM{});
+            mfma(acc[sm], am[rt], wr, TM{});
+          }
+        });
+        const frag_t nwi = neg_frag(wi, TM{});
+        static_for<RT>([&](auto R) {
+          constexpr int rt = decltype(R)::value;
+          constexpr int sb = P::tab.base[lo] + rt * P::ntype(lo);
+          if constexpr (MODE == FWD)
+            mfma(acc[sb + P::qtype(2 * m - 1, lo)], am[rt], nwi, TM{});
+          else
+            mfma(acc[sb + P::qtype(2 * m, lo)], ap[rt], nwi, TM{});
+        });
+      }
+    });
+  }
+
+  // One K step (LI, ks) of wave W: reads stage rd and B registers bc; the next
+  // step (degree NXT, or none if NXT < 0) gets its A fragments (DMA) into stage
+  // wr and its B fragments into registers bn.  The callers alternate the two
+  // stages and register sets by step parity, every choice static.  The
+  // barrier's vmcnt(0) wait is exactly the previous step's loads; the m = 0
+  // fragments are read before the next DMA is issued, the others from a stage
+  // no DMA targets.
+  template <int W, int LI, int NXT>
+  static __device__ __forceinline__ void kstep(f32x16 (&acc)[P::MSLOT], const frag_t (&bc)[P::NBW],
+                                               frag_t (&bn)[P::NBW], const AState& st,
+                                               const char* rd, char* wr, const Args& a,
+                                               const char* wp, int64_t foff, int ks, int nks,
+                                               int lane) {
+    __syncthreads();
+    frag_t a0[RT];
+    read_q<0>(a0, rd, lane);
+    if constexpr (NXT == LI) {
+      a_dma<W, LI>(st, wr, a, ks + 1);
+      b_load<W, LI>(bn, wp, foff, ks + 1, lane);
+    } else if constexpr (NXT >= 0) {
+      a_dma<W, NXT>(st, wr, a, 0);
+      b_load<W, NXT>(bn, wp, foff + static_cast<int64_t>(nks) * P::nbfrag(LI), 0, lane);
+    }
+    // keep the next step's loads ahead of this step's MFMAs
+    __builtin_amdgcn_sched_barrier(0);
+    mma_m0<W, LI>(acc, a0, bc);
+    static_for<M>([&](auto MI) {
+      constexpr int m = decltype(MI)::value + 1;
+      if constexpr (m <= LI) {
+        frag_t ap[RT], am[RT];
+        read_q<2 * m - 1>(ap, rd, lane);
+        read_q<2 * m>(am, rd, lane);
+        mma_m<W, LI, m>(acc, ap, am, bc);
+      }
+    });
+  }
+
+  // The nks K steps of input degree LI, starting with stage s0 / registers b0;
+  // EVENK: nks is even (else odd), which fixes the parity of the last steps.
+  template <int W, int LI, bool EVENK>
+  static __device__ __forceinline__ void kdegree(f32x16 (&acc)[P::MSLOT], frag_t (&b0)[P::NBW],
+                                                 frag_t (&b1)[P::NBW], const AState& st, char* s0,
+                                                 char* s1, const Args& a, const char* wp,
+                                                 int64_t foff, int nks, int lane) {
+    constexpr int NXT = LI < L ? LI + 1 : -1;
+    int ks = 0;
+    for (; ks + 2 < nks; ks += 2) {
+      kstep<W, LI, LI>(acc, b0, b1, st, s0, s1, a, wp, foff, ks, nks, lane);
+      kstep<W, LI, LI>(acc, b1, b0, st, s1, s0, a, wp, foff, ks + 1, nks, lane);
+    }
+    if constexpr (EVENK) {
+      kstep<W, LI, LI>(acc, b0, b1, st, s0, s1, a, wp, foff, ks, nks, lane);
+      kstep<W, LI, NXT>(acc, b1, b0, st, s1, s0, a, wp, foff, ks + 1, nks, lane);
+    } else {
+      kstep<W, LI, NXT>(acc, b0, b1, st, s0, s1, a, wp, foff, ks, nks, lane);
+    }
   }
 
   // ------------------------------------------------------------ epilogue
@@ -284,12 +396,12 @@ struct Gemm {
                                                    int col) {
     static_for<RT>([&](auto RTI) {
       constexpr int sb = P::tab.base[lo] + decltype(RTI)::value * P::ntype(lo);
-      if (a.bias != nullptr) {
-        const float b0 = a.bias[a.extra + lo * a.C_n + col];
+      {  // branch-free: a runtime branch around accumulator updates costs spills
+        const float b0 = a.bias != nullptr ? a.bias[a.extra + lo * a.C_n + col] : 0.f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[sb][i] += b0;
         if constexpr (P::gt(lo)) {
-          const float bg = a.bias[(lo - 1) * a.C_n + col];
+          const float bg = a.bias != nullptr ? a.bias[(lo - 1) * a.C_n + col] : 0.f;
 #pragma unroll
           for (int i = 0; i < 16; ++i) acc[sb + 1][i] += bg;
         }
@@ -317,43 +429,70 @@ struct Gemm {
 
   // Input gradient: the accumulators hold dY (forward-input side) of degree lo.
   // grad_rad = sum_(+-) dY * R (R: unscaled forward rows); dY *= rad.
+  // Each 32-edge x 32-channel block of dY is transposed through a per-wave
+  // LDS tile (pitch 36 floats: 16-byte rows, at most 2-way bank conflicts) into row layout, where lane (edge r,
+  // half h) holds channels 16h..16h+15 of one edge: R, rad and grad_rad then
+  // move as 32- or 64-byte vectors per lane; the scaled block is transposed
+  // back for the inverse rotation.
+  static __device__ __forceinline__ int tsw(int r, int c) { return r * 36 + c; }
+
   template <int lo>
   static __device__ __forceinline__ void radial(f32x16 (&acc)[P::MSLOT], const Smem& s,
-                                                const Args& a, int col, int lane) {
-    if (a.rad == nullptr) return;
+                                                const Args& a, int cb, float* tb, int lane) {
     const int64_t rw = rad_width<L, M>(a.C_n);
+    const int co = lane & 31, h = lane >> 5;
+    const int c0 = cb * CB + h * 16;  // first channel of this lane in row layout
     static_for<RT>([&](auto RTI) {
       constexpr int rt = decltype(RTI)::value;
       constexpr int sb = P::tab.base[lo] + rt * P::ntype(lo);
-      static_for<16>([&](auto II) {
-        constexpr int i = decltype(II)::value;
-        const int ei = s.eid[row_of(rt, i, lane >> 5)];
-        if (ei >= 0) {
-          const int64_t eo = static_cast<int64_t>(ei) * rw;
-          const typename TM::raw* rp = reinterpret_cast<const typename TM::raw*>(a.rad) + eo;
-          const typename TM::raw* rs = reinterpret_cast<const typename TM::raw*>(a.rsave) +
-                                       static_cast<int64_t>(ei) * P::DP * a.C_n + col;
-          typename TM::raw* dr = reinterpret_cast<typename TM::raw*>(a.drad);
-          {
-            const int slot = rad_slot<L, M>(0, lo, col, a.C_n);
-            const float dy = acc[sb][i];
-            if (dr) dr[eo + slot] = TM::cvt(dy * TM::load(rs + P::mrow(0, lo) * a.C_n));
-            acc[sb][i] = dy * TM::load(rp + slot);
+      const int ei = s.eid[rt * 32 + co];
+      const int64_t eis = ei >= 0 ? ei : s.eid[0];
+      const typename TM::raw* rsave = reinterpret_cast<const typename TM::raw*>(a.rsave) +
+                                      eis * P::DP * a.C_n + c0;
+      static_for<1 + (lo < M ? lo : M)>([&](auto MI) {
+        constexpr int m = decltype(MI)::value;
+        constexpr int q0 = m == 0 ? 0 : 2 * m - 1, nqm = m == 0 ? 1 : 2;
+        const typename TM::raw* radp = reinterpret_cast<const typename TM::raw*>(a.rad) + eis * rw +
+                                       rad_slot<L, M>(q0, lo, c0, a.C_n);
+        float dr[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) dr[k] = 0.f;
+        static_for<nqm>([&](auto QI) {
+          constexpr int q = q0 + decltype(QI)::value;
+          constexpr int slot = sb + P::qtype(q, lo);
+          __builtin_amdgcn_sched_barrier(0);  // one block at a time (register pressure)
+          // accumulator layout -> row layout
+#pragma unroll
+          for (int i = 0; i < 16; ++i) tb[tsw(8 * (i >> 2) + 4 * h + (i & 3), co)] = acc[slot][i];
+          wave_sync();
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {  // 4 channels at a time (register pressure)
+            float rr[4], rv[4];
+            load_vec<TM, 4>(rsave + P::mrow(q, lo) * a.C_n + 4 * g, rr);
+            load_vec<TM, 4>(radp + 4 * g, rv);
+            float4 t4 = *reinterpret_cast<const float4*>(tb + tsw(co, 16 * h + 4 * g));
+            dr[4 * g] = fmaf(t4.x, rr[0], dr[4 * g]);
+            dr[4 * g + 1] = fmaf(t4.y, rr[1], dr[4 * g + 1]);
+            dr[4 * g + 2] = fmaf(t4.z, rr[2], dr[4 * g + 2]);
+            dr[4 * g + 3] = fmaf(t4.w, rr[3], dr[4 * g + 3]);
+            t4.x *= rv[0]; t4.y *= rv[1]; t4.z *= rv[2]; t4.w *= rv[3];
+            *reinterpret_cast<float4*>(tb + tsw(co, 16 * h + 4 * g)) = t4;
           }
-          static_for<M>([&](auto MI) {
-            constexpr int m = decltype(MI)::value + 1;
-            if constexpr (m <= lo) {
-              constexpr int sp = sb + P::qtype(2 * m - 1, lo), sm = sb + P::qtype(2 * m, lo);
-              const int slot = rad_slot<L, M>(2 * m - 1, lo, col, a.C_n);
-              const float r = TM::load(rp + slot);
-              const float dyp = acc[sp][i], dym = acc[sm][i];
-              if (dr)
-                dr[eo + slot] = TM::cvt(dyp * TM::load(rs + P::mrow(2 * m - 1, lo) * a.C_n) +
-                                        dym * TM::load(rs + P::mrow(2 * m, lo) * a.C_n));
-              acc[sp][i] = dyp * r;
-              acc[sm][i] = dym * r;
-            }
-          });
+          wave_sync();
+#pragma unroll
+          for (int i = 0; i < 16; ++i) acc[slot][i] = tb[tsw(8 * (i >> 2) + 4 * h + (i & 3), co)];
+          wave_sync();
+        });
+        if (a.drad != nullptr && ei >= 0) {
+          typename TM::raw* dp = reinterpret_cast<typename TM::raw*>(a.drad) + ei * rw +
+                                 rad_slot<L, M>(q0, lo, c0, a.C_n);
+          float t[8];
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) t[k] = dr[8 * half + k];
+            store_vec<TM, 8>(dp + 8 * half, t);
+          }
         }
       });
     });
@@ -367,13 +506,12 @@ struct Gemm {
   // then store the sums of the segments that end in the chunk.
   template <int W, int lo>
   static __device__ __forceinline__ void rotate_sum(f32x16 (&acc)[P::MSLOT], Smem& s,
-                                                    const Args& a, int cb, int wave, int lane,
+                                                    const Args& a, int cb, float* buf, int lane,
                                                     uint64_t endmask) {
     constexpr int n = 2 * lo + 1;
     constexpr int nq = P::nq(lo);
     constexpr int PB = P::pblk(lo);
     const int co = lane & 31, h = lane >> 5;
-    float* buf = reinterpret_cast<float*>(s.u) + wave * (P::CH * 64);
     const float* Wl = s.W + P::woff(lo);
     const uint64_t startmask = (endmask << 1) | 1ull;
     for (int p = 0; p <= lo; ++p) {
@@ -433,8 +571,9 @@ struct Gemm {
     }
   }
 
-  template <int W>
-  static __device__ __forceinline__ void body(Smem& s, const Args& a, int cb, int tid, int nvalid) {
+  template <int W, bool EVENK, bool RAD>
+  static __device__ __forceinline__ void body(Smem& s, char* st0, char* st1, const Args& a, int cb,
+                                              int tid, int nvalid) {
     const int wave = tid >> 6, lane = tid & 63;
     f32x16 acc[P::MSLOT];
 #pragma unroll
@@ -445,40 +584,21 @@ struct Gemm {
     const int nks = a.C_k / KC;
     const char* wp = a.wpack + static_cast<int64_t>(cb) * a.frags_per_cb * FRAG;
     AState st;
-    a_init(st, s, a, tid);
-    uint4 bc[P::NBW], bn[P::NBW];
-    a_rows<0>(st, a);
-    a_load<0>(st, a, 0);
-    b_load<W, 0>(bc, wp, 0, 0, lane);
-    a_store<0>(st, s, 0, tid);
-    __syncthreads();
-    int buf = 0;
+    a_init<W>(st, s, a, lane);
+    frag_t b0[P::NBW], b1[P::NBW];
+    a_dma<W, 0>(st, st0, a, 0);
+    b_load<W, 0>(b0, wp, 0, 0, lane);
     int64_t foff = 0;
     static_for<L + 1>([&](auto LIc) {
       constexpr int LI = decltype(LIc)::value;
-      for (int ks = 0; ks < nks; ++ks) {
-        const bool more = ks + 1 < nks;
-        if (more) {
-          a_load<LI>(st, a, ks + 1);
-          b_load<W, LI>(bn, wp, foff, ks + 1, lane);
-        } else if constexpr (LI < L) {
-          a_rows<LI + 1>(st, a);
-          a_load<LI + 1>(st, a, 0);
-          b_load<W, LI + 1>(bn, wp, foff + static_cast<int64_t>(nks) * P::nbfrag(LI), 0, lane);
-        }
-        step<W, LI>(acc, s.u + buf * P::A_BYTES, bc, lane);
-        if (more) {
-          a_store<LI>(st, s, buf ^ 1, tid);
-        } else if constexpr (LI < L) {
-          a_store<LI + 1>(st, s, buf ^ 1, tid);
-        }
-        __syncthreads();
-        buf ^= 1;
-#pragma unroll
-        for (int k = 0; k < P::NBW; ++k) bc[k] = bn[k];
-      }
+      // parity of the degree's first global K step (LI * nks)
+      if constexpr (EVENK || (LI & 1) == 0)
+        kdegree<W, LI, EVENK>(acc, b0, b1, st, st0, st1, a, wp, foff, nks, lane);
+      else
+        kdegree<W, LI, EVENK>(acc, b1, b0, st, st1, st0, a, wp, foff, nks, lane);
       foff += static_cast<int64_t>(nks) * P::nbfrag(LI);
     });
+    __syncthreads();  // all A reads done before the stages become epilogue staging
 
     // segment ends of the tile: bit e set if edge e closes its segment
     const int le = lane < TE ? lane : TE - 1, ln = le + 1 < TE ? le + 1 : le;
@@ -489,15 +609,21 @@ struct Gemm {
       if constexpr (P::tab.owner[lo] == W) {
         if constexpr (MODE == FWD)
           bias_gate<lo>(acc, a, col);
-        else
-          radial<lo>(acc, s, a, col, lane);
-        rotate_sum<W, lo>(acc, s, a, cb, wave, lane, endmask);
+        else if constexpr (RAD)
+          radial<lo>(acc, s, a, cb,
+                     reinterpret_cast<float*>((wave < 2 ? st0 : st1) + (wave & 1) * PW), lane);
+        rotate_sum<W, lo>(acc, s, a, cb,
+                          reinterpret_cast<float*>((wave < 2 ? st0 : st1) + (wave & 1) * PW),
+                          lane, endmask);
       }
     });
   }
 
+  template <bool EVENK, bool RAD>
   static __device__ __forceinline__ void run(const Args& a) {
     __shared__ Smem s;
+    __shared__ alignas(16) char st0[SB];
+    __shared__ alignas(16) char st1[SB];
     const int tid = threadIdx.x, wave = tid >> 6;
     // XCD-aware mapping: consecutive workgroup ids go round-robin over the 8
     // XCDs.  The n_cb channel-block workgroups of one edge tile are the
@@ -554,14 +680,16 @@ struct Gemm {
     }
     static_for<NW>([&](auto WI) {
       constexpr int w = decltype(WI)::value;
-      if (wave == w) body<w>(s, a, cb, tid, nvalid);
+      if (wave == w) body<w, EVENK, RAD>(s, st0, st1, a, cb, tid, nvalid);
     });
   }
 };
 
-template <int L, int M, bool GATE, int NW, int RT, class TM, int MODE>
+// EVENK: the number of K steps per input degree (C_k / KC) is even.
+// RAD (input gradient only): a radial scale is given (its gradient is formed).
+template <int L, int M, bool GATE, int NW, int RT, class TM, int MODE, bool EVENK, bool RAD>
 __global__ __launch_bounds__(NW * 64, 2) void gemm_kernel(Args a) {
-  Gemm<L, M, GATE, NW, RT, TM, MODE>::run(a);
+  Gemm<L, M, GATE, NW, RT, TM, MODE>::template run<EVENK, RAD>(a);
 }
 
 }  // namespace msg

@@ -252,6 +252,14 @@ __device__ __forceinline__ void load_vec<F32, 8>(const float* p, float (&o)[8]) 
   o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
 }
 template <>
+__device__ __forceinline__ void load_vec<BF16, 4>(const uint16_t* p, float (&o)[4]) {
+  const uint2 v = *reinterpret_cast<const uint2*>(p);
+  o[0] = __uint_as_float(v.x << 16);
+  o[1] = __uint_as_float(v.x & 0xffff0000u);
+  o[2] = __uint_as_float(v.y << 16);
+  o[3] = __uint_as_float(v.y & 0xffff0000u);
+}
+template <>
 __device__ __forceinline__ void load_vec<F32, 4>(const float* p, float (&o)[4]) {
   const float4 a = *reinterpret_cast<const float4*>(p);
   o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
@@ -267,6 +275,11 @@ __device__ __forceinline__ void store_vec<BF16, 8>(uint16_t* p, const float (&v)
   w.z = f32_to_bf16(v[4]) | (static_cast<uint32_t>(f32_to_bf16(v[5])) << 16);
   w.w = f32_to_bf16(v[6]) | (static_cast<uint32_t>(f32_to_bf16(v[7])) << 16);
   *reinterpret_cast<uint4*>(p) = w;
+}
+template <>
+__device__ __forceinline__ void store_vec<F32, 8>(float* p, const float (&v)[8]) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
 }
 template <>
 __device__ __forceinline__ void store_vec<F32, 4>(float* p, const float (&v)[4]) {

@@ -25,8 +25,24 @@ int launch(const Args& a, hipStream_t s) {
   // tiles in groups of 8 (one per XCD), n_cb workgroups per tile.
   const int64_t grid = ((a.ntiles + 7) / 8) * 8 * a.n_cb;
   MALOQ_REQUIRE(grid < (int64_t(1) << 31), "grid too large");
-  hipLaunchKernelGGL((gemm_kernel<L, M, GATE, NW, RT, TM, MODE>),
-                     dim3(static_cast<unsigned>(grid)), dim3(P::NT), 0, s, a);
+  const dim3 g(static_cast<unsigned>(grid)), b(P::NT);
+  const bool even = (a.C_k / TM::KC) % 2 == 0;
+  if constexpr (MODE == FWD) {
+    if (even)
+      hipLaunchKernelGGL((gemm_kernel<L, M, GATE, NW, RT, TM, MODE, true, false>), g, b, 0, s, a);
+    else
+      hipLaunchKernelGGL((gemm_kernel<L, M, GATE, NW, RT, TM, MODE, false, false>), g, b, 0, s, a);
+  } else if (a.rad != nullptr) {
+    if (even)
+      hipLaunchKernelGGL((gemm_kernel<L, M, GATE, NW, RT, TM, MODE, true, true>), g, b, 0, s, a);
+    else
+      hipLaunchKernelGGL((gemm_kernel<L, M, GATE, NW, RT, TM, MODE, false, true>), g, b, 0, s, a);
+  } else {
+    if (even)
+      hipLaunchKernelGGL((gemm_kernel<L, M, GATE, NW, RT, TM, MODE, true, false>), g, b, 0, s, a);
+    else
+      hipLaunchKernelGGL((gemm_kernel<L, M, GATE, NW, RT, TM, MODE, false, false>), g, b, 0, s, a);
+  }
   return check_launch("gemm_kernel");
 }
 
