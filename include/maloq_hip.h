@@ -193,6 +193,12 @@ int maloq_message_bwd_dx(int dtype, int lmax, int mmax, const float* grad_out, i
                          int c_in, const int64_t* seg_ptr_src, float* partials, void* dz_ws,
                          void* stream);
 
+/* Rows to allocate for the saved SO(2) rows (y_ws of maloq_message_fwd, dz_ws of
+ * maloq_message_bwd_dx) so that maloq_message_dw can read them in whole 128-edge
+ * chunks: round_up(num_edges, 128) + 1.  Rows num_edges and up must be zero
+ * (the bf16 weight gradient reads them). */
+int64_t maloq_message_edge_rows(int64_t num_edges);
+
 /* Floats of the split-K partials buffer of maloq_message_dw. */
 int64_t maloq_message_dw_partials_floats(int lmax, int mmax, int c_out, int c_in, int splits);
 
@@ -200,7 +206,8 @@ int64_t maloq_message_dw_partials_floats(int lmax, int mmax, int c_out, int c_in
  *   dW_0 = sum_e dZ_0(e)^T Y_0(e);  for m >= 1 with C_m = sum_e dZ_m^T Y_m over
  *   the stacked (+m, -m) rows: dWr = C[+,+] + C[-,-], dWi = C[-,+] - C[+,-],
  *   dW_m = [dWr; dWi] in the layout of so2_m_conv[m-1].fc.weight.
- * dz [E, d', c_out], y [E, d', c_in] (dtype), dw0 [(lmax+1) c_out, (lmax+1) c_in],
+ * dz [E, d', c_out], y [E, d', c_in] (dtype; for bf16 with maloq_message_edge_rows(E)
+ * rows, zero from row E on, channels multiples of 8), dw0 [(lmax+1) c_out, (lmax+1) c_in],
  * dw_m [2 (lmax-m+1) c_out, (lmax-m+1) c_in] fp32.  Split-K over edges,
  * partials summed in split order (deterministic).
  * Replaces the autograd weight gradient of SO2_Convolution

@@ -41,6 +41,7 @@ SIGNATURES = {
                           _i64, _i32, _p, _p, _p, _p, _p, _p],
     "maloq_message_bwd_dx": [_i32, _i32, _i32, _p, _i32, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p,
                              _p, _i64, _i32, _p, _p, _p, _p],
+    "maloq_message_edge_rows": [_i64],
     "maloq_message_dw_partials_floats": [_i32, _i32, _i32, _i32, _i32],
     "maloq_message_dw": [_i32, _i32, _i32, _p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p],
 }
@@ -49,6 +50,7 @@ RESTYPES = {
     "maloq_message_partials_floats": ctypes.c_int64,
     "maloq_message_wpack_bytes": ctypes.c_int64,
     "maloq_message_dw_partials_floats": ctypes.c_int64,
+    "maloq_message_edge_rows": ctypes.c_int64,
 }
 
 _lib = None

@@ -1,5 +1,15 @@
 // Weight gradients of the SO(2) linear (gfx950).
 //
+// bf16: dw_tr_kernel.  A workgroup owns a 256 x 256 tile of one C_g and a
+// contiguous range of edges (split-K); each of its 4 waves a 128 x 128
+// quarter (4 x 4 MFMA 32x32 tiles, accumulators in AGPRs).  Both operands are
+// copied in their natural [edge][channel] layout straight from global memory
+// into a 4-stage LDS ring (global_load_lds, 16-byte chunks XOR-swizzled by
+// edge row), 32 edges per stage, three stages in flight; MFMA operands (8
+// consecutive edges of one channel per lane) come from ds_read_b64_tr_b16,
+// which transposes 4x4 blocks of 16-bit elements across each 16-lane group.
+// fp32: dw_kernel below (register transposes).
+//
 // With Y_e the rotated, radially scaled input rows and dZ_e the rotated output
 // gradient rows of edge e (both saved in m-major order [E, d', C] by the
 // fused kernels), the gradient of every |m| group is a GEMM with the edges as
@@ -174,6 +184,149 @@ __global__ __launch_bounds__(256) void dw_kernel(DwArgs a) {
   }
 }
 
+namespace trdw {
+constexpr int T = 256;                  // output tile edge
+constexpr int KE = 32;                  // edges per K step (two 16-edge MFMA k-substeps)
+constexpr int NS = 4;                   // LDS ring stages
+constexpr int PITCH = T * 2;            // bytes per staged edge row (bf16)
+constexpr int TILE = KE * PITCH;        // 16 KB per operand per stage
+constexpr int CHUNK = NS * KE;          // 128: split and padding granularity (edges)
+}  // namespace trdw
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef short v4s16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s16 lds_v4s16;
+
+// Transposed fragment read: 4 edges x 1 channel of a staged tile (see above).
+__device__ __forceinline__ v4s16 tr_read(const char* lds) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_v4s16*)((__attribute__((address_space(3))) const char*)lds));
+}
+
+// One K step on stage (sa, sb): 2 k-substeps x 4 x 4 MFMAs per wave.
+// la, lb: this lane's byte offsets inside the operand tiles (row, chunk and
+// wave-half part); the per-(ks, r, tile) offsets are compile-time.
+__device__ __forceinline__ void trdw_step(f32x16 (&acc)[4][4], const char* sa, const char* sb,
+                                          int la, int lb) {
+  using namespace trdw;
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    bf16x8 af[4], bfr[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      // chunk (within the 512-byte row) of the tile's 32 columns: 4 t + ..., XOR with 4 r
+      v4s16 a0 = tr_read(sa + la + (ks * 16 + 0) * PITCH + (((t >> 1) * 8 + 4 * ((t & 1) ^ 0)) * 16));
+      v4s16 a1 = tr_read(sa + la + (ks * 16 + 4) * PITCH + (((t >> 1) * 8 + 4 * ((t & 1) ^ 1)) * 16));
+      v4s16 b0 = tr_read(sb + lb + (ks * 16 + 0) * PITCH + (((t >> 1) * 8 + 4 * ((t & 1) ^ 0)) * 16));
+      v4s16 b1 = tr_read(sb + lb + (ks * 16 + 4) * PITCH + (((t >> 1) * 8 + 4 * ((t & 1) ^ 1)) * 16));
+      af[t] = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
+      bfr[t] = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+  }
+}
+
+__global__ __launch_bounds__(256, 1) void dw_tr_kernel(DwArgs a) {
+  using namespace trdw;
+  __shared__ alignas(16) char A0[TILE], B0[TILE], A1[TILE], B1[TILE], A2[TILE], B2[TILE],
+      A3[TILE], B3[TILE];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int64_t ntiles = a.tile0[a.ngroups];
+  const int64_t split = blockIdx.x / ntiles;
+  const int64_t t = blockIdx.x % ntiles;
+  int g = 0;
+  while (g + 1 < a.ngroups && t >= a.tile0[g + 1]) ++g;
+  const int64_t lt = t - a.tile0[g];
+  const int tn = static_cast<int>(lt / a.ntk[g]), tk = static_cast<int>(lt % a.ntk[g]);
+  const int Ng = a.rows[g] * a.C_out, Kg = a.rows[g] * a.C_in;
+  const int64_t eb = split * a.e_per_split;
+  const int64_t epad = (a.E + CHUNK - 1) / CHUNK * CHUNK;
+  const int64_t ee = (eb + a.e_per_split) < epad ? (eb + a.e_per_split) : epad;
+  const int nsteps = ee > eb ? static_cast<int>((ee - eb) / KE) : 0;  // a multiple of NS
+
+  // DMA: wave w copies chunks p = (4 w + j) 64 + lane of each operand tile
+  // (row r = p / 32, slot p % 32), loading global chunk (slot ^ (r & 7)).
+  const uint16_t* za = reinterpret_cast<const uint16_t*>(a.dz) +
+                       static_cast<int64_t>(a.row0[g]) * a.C_out + static_cast<int64_t>(tn) * T;
+  const uint16_t* yb = reinterpret_cast<const uint16_t*>(a.y) +
+                       static_cast<int64_t>(a.row0[g]) * a.C_in + static_cast<int64_t>(tk) * T;
+  const int64_t sa_e = static_cast<int64_t>(a.dp) * a.C_out, sb_e = static_cast<int64_t>(a.dp) * a.C_in;
+  int dr[4], dc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int p = (wave * 4 + j) * 64 + lane;
+    dr[j] = p >> 5;
+    dc[j] = ((p & 31) ^ (dr[j] & 7)) * 8;
+  }
+  // The copies are issued by inline asm, invisible to the compiler's wait
+  // insertion (which would otherwise drain the ring before LDS reads it cannot
+  // tell apart); the explicit vmcnt/barrier of each step orders them.
+  auto dma = [&](char* da, char* db, int step) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int64_t e = eb + static_cast<int64_t>(step) * KE + dr[j];
+      e = e < epad ? e : epad - 1;  // steps past the range: in-bounds, never read
+      const uint16_t* ga = za + e * sa_e + dc[j];
+      const uint16_t* gb = yb + e * sb_e + dc[j];
+      const unsigned la_s = __builtin_amdgcn_readfirstlane(
+          static_cast<unsigned>(reinterpret_cast<size_t>((__attribute__((address_space(3))) char*)(da + (wave * 4 + j) * 1024))));
+      const unsigned lb_s = __builtin_amdgcn_readfirstlane(
+          static_cast<unsigned>(reinterpret_cast<size_t>((__attribute__((address_space(3))) char*)(db + (wave * 4 + j) * 1024))));
+      asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(ga), "s"(la_s) : "memory", "m0");
+      asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gb), "s"(lb_s) : "memory", "m0");
+    }
+  };
+  // transposed reads: lane (g16 = lane/16, a = lane%4, kk = lane/4%4) addresses row
+  // 8 (g16/2) + 4 r + kk + 16 ks, column 32 t + 16 (g16%2) + 4 a of its wave's half
+  const int g16 = lane >> 4, aa = lane & 3, kk = (lane >> 2) & 3;
+  const int lrow = (8 * (g16 >> 1) + kk) * PITCH + (((2 * (g16 & 1) + (aa >> 1)) ^ kk) * 16) + (aa & 1) * 8;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int la = lrow + wm * 256, lb = lrow + wn * 256;  // the wave's 128-column half = 16 chunks
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  dma(A0, B0, 0);
+  dma(A1, B1, 1);
+  dma(A2, B2, 2);
+  for (int s = 0; s < nsteps; s += NS) {
+    // each step: this wave's copies of the step done (two later steps in flight),
+    // then all waves' (barrier); the stage refilled was read one step earlier
+#define MALOQ_TRDW_STEP(SA, SB, NA, NB, K)                                           \
+    asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory");     \
+    dma(NA, NB, s + K + 3);                                                         \
+    trdw_step(acc, SA, SB, la, lb);
+    MALOQ_TRDW_STEP(A0, B0, A3, B3, 0)
+    MALOQ_TRDW_STEP(A1, B1, A0, B0, 1)
+    MALOQ_TRDW_STEP(A2, B2, A1, B1, 2)
+    MALOQ_TRDW_STEP(A3, B3, A2, B2, 3)
+#undef MALOQ_TRDW_STEP
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no copy left in flight at exit
+
+  float* out = a.part + split * a.goff[a.ngroups] + a.goff[g];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = tk * T + wn * 128 + j * 32 + (lane & 31);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = tn * T + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (m < Ng && n < Kg) out[static_cast<int64_t>(m) * Kg + n] = acc[i][j][r];
+      }
+    }
+}
+
 // One thread per element of the reference-layout gradients:
 // dW0 [(L+1) C_out, (L+1) C_in], then dW_m [2 (L-m+1) C_out, (L-m+1) C_in].
 __global__ void dw_reduce_kernel(DwArgs a, int lmax, float* __restrict__ dw0,
@@ -217,7 +370,10 @@ __global__ void dw_reduce_kernel(DwArgs a, int lmax, float* __restrict__ dw0,
 using namespace maloq;
 using namespace maloq::msg;
 
-static int dw_setup(DwArgs& a, int lmax, int mmax, int64_t E, int c_out, int c_in, int splits) {
+// tile: output tile edge (128 for dw_kernel, 256 for dw_tr_kernel); gran:
+// split boundaries are multiples of this many edges.
+static int dw_setup(DwArgs& a, int lmax, int mmax, int64_t E, int c_out, int c_in, int splits,
+                    int tile, int gran) {
   MALOQ_REQUIRE(mmax >= 0 && mmax <= 3 && mmax <= lmax, "mmax out of range for the weight gradient");
   MALOQ_REQUIRE(splits >= 1 && splits <= 64, "splits out of range");
   a.E = E;
@@ -234,20 +390,28 @@ static int dw_setup(DwArgs& a, int lmax, int mmax, int64_t E, int c_out, int c_i
     a.rows[g] = r;
     row += r;
     const int64_t Ng = static_cast<int64_t>(r) * c_out, Kg = static_cast<int64_t>(r) * c_in;
-    a.ntk[g] = static_cast<int>((Kg + DW_T - 1) / DW_T);
-    a.tile0[g + 1] = a.tile0[g] + ((Ng + DW_T - 1) / DW_T) * a.ntk[g];
+    a.ntk[g] = static_cast<int>((Kg + tile - 1) / tile);
+    a.tile0[g + 1] = a.tile0[g] + ((Ng + tile - 1) / tile) * a.ntk[g];
     a.goff[g + 1] = a.goff[g] + Ng * Kg;
   }
   a.dp = row;
-  // split boundaries on a multiple of the largest K step (64 edges)
-  a.e_per_split = ((E + splits - 1) / splits + 63) / 64 * 64;
+  a.e_per_split = ((E + splits - 1) / splits + gran - 1) / gran * gran;
   return MALOQ_OK;
+}
+
+// Rows the bf16 weight gradient reads from dz / y: the edges rounded up to a
+// whole number of 128-edge chunks, plus one row (tiles that end past a row's
+// last column read into the next row).  Rows from num_edges on must be zero.
+static int64_t dw_rows(int64_t E) { return (E + trdw::CHUNK - 1) / trdw::CHUNK * trdw::CHUNK + 1; }
+
+extern "C" int64_t maloq_message_edge_rows(int64_t num_edges) {
+  return num_edges < 0 ? -1 : dw_rows(num_edges);
 }
 
 extern "C" int64_t maloq_message_dw_partials_floats(int lmax, int mmax, int c_out, int c_in,
                                                     int splits) {
   DwArgs a{};
-  if (dw_setup(a, lmax, mmax, 0, c_out, c_in, splits)) return -1;
+  if (dw_setup(a, lmax, mmax, 0, c_out, c_in, splits, DW_T, 64)) return -1;
   return a.goff[a.ngroups] * splits;
 }
 
@@ -259,8 +423,16 @@ extern "C" int maloq_message_dw(int dtype, int lmax, int mmax, const void* dz, c
   MALOQ_REQUIRE(num_edges >= 0, "num_edges < 0");
   MALOQ_REQUIRE(c_out > 0 && c_in > 0, "bad channels");
   DwArgs a{};
-  int rc = dw_setup(a, lmax, mmax, num_edges, c_out, c_in, splits);
+  int rc = dw_setup(a, lmax, mmax, num_edges, c_out, c_in, splits, DW_T, 64);
   if (rc) return rc;
+  // bf16 rows of at least one tile (a tile ending past a row's last column
+  // reads into the next row): the transpose-read kernel; else dw_kernel.
+  const bool tr = dtype == 1 && c_out % 8 == 0 && c_in % 8 == 0 &&
+                  static_cast<int64_t>(a.dp) * c_out >= trdw::T && static_cast<int64_t>(a.dp) * c_in >= trdw::T;
+  if (tr) {
+    rc = dw_setup(a, lmax, mmax, num_edges, c_out, c_in, splits, trdw::T, trdw::CHUNK);
+    if (rc) return rc;
+  }
   MALOQ_REQUIRE(partials && dw0, "null pointer");
   MALOQ_REQUIRE(mmax < 1 || dw1, "dw1 is null");
   MALOQ_REQUIRE(mmax < 2 || dw2, "dw2 is null");
@@ -272,7 +444,9 @@ extern "C" int maloq_message_dw(int dtype, int lmax, int mmax, const void* dz, c
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t grid = a.tile0[a.ngroups] * splits;
   MALOQ_REQUIRE(grid < (int64_t(1) << 31), "grid too large");
-  if (dtype == 1)
+  if (tr)
+    hipLaunchKernelGGL(dw_tr_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);
+  else if (dtype == 1)
     hipLaunchKernelGGL(dw_kernel<BF16>, dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);
   else
     hipLaunchKernelGGL(dw_kernel<F32>, dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);

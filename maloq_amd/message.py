@@ -173,6 +173,16 @@ def rad_width(lmax, mmax, c_in):
 
 
 # ---------------------------------------------------------------- raw calls
+def _edge_rows(E, rows, c, dev, dt):
+    """Saved SO(2) rows [edge_rows(E), rows, c]: the kernels write rows < E; the
+    rest are zero (the bf16 weight gradient reads whole 128-edge chunks)."""
+    n = int(_lib.load().maloq_message_edge_rows(E))
+    t = torch.empty(n, rows, c, device=dev, dtype=dt)
+    t[E:].zero_()
+    return t
+
+
+
 def kept_rows(lmax, mmax):
     return (lmax + 1) + sum(2 * (lmax - m + 1) for m in range(1, mmax + 1))
 
@@ -208,8 +218,9 @@ def message_forward(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=False, wp
     if rad is not None:
         assert rad.shape == (E, rad_width(lmax, mmax, c_in)), "rad must be [E, sum_m (lmax-m+1) C_in]"
         rad = rad.to(dt).contiguous()
-    y = torch.empty(max(E, 1), kept_rows(lmax, mmax), c_in, device=dev, dtype=dt)
-    r = torch.empty_like(y) if (save is not None and rad is not None) else None
+    y = _edge_rows(E, kept_rows(lmax, mmax), c_in, dev, dt)
+    r = torch.empty(max(E, 1), kept_rows(lmax, mmax), c_in, device=dev, dtype=dt) \
+        if (save is not None and rad is not None) else None
     dk = torch.empty(max(E, 1), wigner_floats(lmax, mmax), device=dev, dtype=torch.float32)
     bias = b0.float().contiguous() if b0 is not None else None
     xc = x.contiguous()
@@ -243,7 +254,7 @@ def message_backward_dx(grad_out, x_shape, dt, plan, saved, rad, w0, wm, lmax, m
         rad = rad.to(dt).contiguous()
         if need_rad_grad:
             grad_rad = torch.empty_like(rad)
-    dz = torch.empty(max(E, 1), kept_rows(lmax, mmax), c_out, device=dev, dtype=dt)
+    dz = _edge_rows(E, kept_rows(lmax, mmax), c_out, dev, dt)
     g = grad_out.float().contiguous()
     _lib.call("maloq_message_bwd_dx", DTYPE_CODE[dt], lmax, mmax, _lib.ptr(g), c_out,
               _lib.ptr(plan.bwd_dst), _lib.ptr(plan.bwd_src), _lib.ptr(plan.bwd_eidx), E,
@@ -253,15 +264,26 @@ def message_backward_dx(grad_out, x_shape, dt, plan, saved, rad, w0, wm, lmax, m
     return gx, grad_rad, dz
 
 
-def message_weight_grad(dz, y, lmax, mmax, c_out, c_in, splits=None):
+def message_weight_grad(dz, y, lmax, mmax, c_out, c_in, splits=None, num_edges=None):
     """(dW0 [(L+1) c_out, (L+1) c_in], [dW_m [2 (L-m+1) c_out, (L-m+1) c_in]], db0)
-    in fp32 from the saved rows (deterministic split-K over edges)."""
-    E = dz.shape[0]
+    in fp32 from the saved rows (deterministic split-K over edges).  ``dz`` and
+    ``y`` are the forward/backward workspaces: for bf16 they carry the zeroed
+    padding rows of ``maloq_message_edge_rows(num_edges)``."""
+    E = int(dz.shape[0] if num_edges is None else num_edges)
+    if dz.dtype == torch.bfloat16:
+        assert dz.shape[0] >= _lib.load().maloq_message_edge_rows(E) and y.shape[0] == dz.shape[0], \
+            "bf16 weight gradient needs the padded workspaces"
     if splits is None:
-        # about 640 workgroups of 128 x 128 output tiles, >= 1024 edges per split
-        ntiles = sum(-(-r * c_out // 128) * -(-r * c_in // 128)
-                     for r in [lmax + 1] + [2 * (lmax - m + 1) for m in range(1, mmax + 1)])
-        splits = max(1, min(16, round(640 / ntiles), E // 1024))
+        if dz.dtype == torch.bfloat16:
+            # 256 x 256 tiles, one workgroup per CU: about one wave of 256 workgroups
+            ntiles = sum(-(-r * c_out // 256) * -(-r * c_in // 256)
+                         for r in [lmax + 1] + [2 * (lmax - m + 1) for m in range(1, mmax + 1)])
+            splits = max(1, min(64, 256 // ntiles, -(-E // 128)))
+        else:
+            # about 640 workgroups of 128 x 128 output tiles, >= 1024 edges per split
+            ntiles = sum(-(-r * c_out // 128) * -(-r * c_in // 128)
+                         for r in [lmax + 1] + [2 * (lmax - m + 1) for m in range(1, mmax + 1)])
+            splits = max(1, min(16, round(640 / ntiles), E // 1024))
     lib = _lib.load()
     parts = torch.empty(max(1, lib.maloq_message_dw_partials_floats(lmax, mmax, c_out, c_in, splits)),
                         device=dz.device, dtype=torch.float32)
@@ -272,7 +294,7 @@ def message_weight_grad(dz, y, lmax, mmax, c_out, c_in, splits=None):
     _lib.call("maloq_message_dw", DTYPE_CODE[dz.dtype], lmax, mmax, _lib.ptr(dz), _lib.ptr(y), E,
               c_out, c_in, splits, _lib.ptr(parts), _lib.ptr(dw0), ptrs[0], ptrs[1], ptrs[2],
               _lib.stream_of(dz.device))
-    db0 = dz[:, : lmax + 1, :].float().sum(0).reshape(-1)
+    db0 = dz[:E, : lmax + 1, :].float().sum(0).reshape(-1)
     return dw0, dwm, db0
 
 
@@ -299,8 +321,8 @@ class _MessageBlockFn(torch.autograd.Function):
         dw0 = db0 = None
         dwm = [None] * len(wm)
         if need_w and plan.num_edges > 0:
-            dw0, dwm, db0 = message_weight_grad(dz[: plan.num_edges], y[: plan.num_edges], lmax, mmax,
-                                                g.shape[2], ctx.x_shape[2])
+            dw0, dwm, db0 = message_weight_grad(dz, y, lmax, mmax, g.shape[2], ctx.x_shape[2],
+                                                num_edges=plan.num_edges)
             dw0 = dw0.to(w0.dtype)
             dwm = [d.to(w.dtype) for d, w in zip(dwm, wm)]
             db0 = db0 if ctx.has_b0 else None

@@ -184,3 +184,39 @@ def test_backward_matches_oracle_autograd(lmax, mmax, dtype, device):
         ga = ga.cpu().double()
         err = (ga - b.grad).abs().max().item() / max(b.grad.abs().max().item(), 1e-30)
         assert err < tol, f"grad {name}: rel err {err}"
+
+
+@pytest.mark.parametrize("lmax,c_in,c_out,E,splits", [(4, 128, 128, 1000, None), (4, 128, 128, 1000, 3),
+                                                     (2, 32, 64, 37, None), (6, 64, 32, 260, 2)])
+def test_weight_grad_bf16_against_fp64(lmax, c_in, c_out, E, splits, device):
+    """maloq_message_dw (bf16): ragged edge counts, partial 256-column tiles,
+    several split-K ranges; against fp64 sums of the same bf16 rows, with the
+    +-m folding of so2_layers.py:61-67 (dWr = C++ + C--, dWi = C-+ - C+-)."""
+    from maloq_amd import message as M
+    print(f"dw case lmax={lmax} c_in={c_in} c_out={c_out} E={E} splits={splits}", flush=True)
+    mmax = 2
+    gen = torch.Generator().manual_seed(E + lmax)
+    P = M.kept_rows(lmax, mmax)
+    dz = M._edge_rows(E, P, c_out, device, torch.bfloat16)
+    y = M._edge_rows(E, P, c_in, device, torch.bfloat16)
+    dz[:E] = torch.randn(E, P, c_out, generator=gen).to(device=device, dtype=torch.bfloat16)
+    y[:E] = torch.randn(E, P, c_in, generator=gen).to(device=device, dtype=torch.bfloat16)
+    dw0, dwm, db0 = M.message_weight_grad(dz, y, lmax, mmax, c_out, c_in, splits=splits, num_edges=E)
+    torch.cuda.synchronize()
+    dzd, yd = dz[:E].double().cpu(), y[:E].double().cpu()
+    r0 = lmax + 1
+    ref0 = torch.einsum("en,ek->nk", dzd[:, :r0].reshape(E, -1), yd[:, :r0].reshape(E, -1))
+    scale = ref0.abs().max().item()
+    assert (dw0.double().cpu() - ref0).abs().max().item() / scale < 1e-5
+    row = r0
+    for m in range(1, mmax + 1):
+        nr = lmax - m + 1
+        Cm = torch.einsum("en,ek->nk", dzd[:, row:row + 2 * nr].reshape(E, -1), yd[:, row:row + 2 * nr].reshape(E, -1))
+        ho, hi = nr * c_out, nr * c_in
+        dwr = Cm[:ho, :hi] + Cm[ho:, hi:]
+        dwi = Cm[ho:, :hi] - Cm[:ho, hi:]
+        ref = torch.cat([dwr, dwi])
+        err = (dwm[m - 1].double().cpu() - ref).abs().max().item() / ref.abs().max().item()
+        assert err < 1e-5, (m, err)
+        row += 2 * nr
+    assert torch.allclose(db0.double().cpu(), dzd[:, :r0].sum(0).reshape(-1), rtol=1e-5, atol=1e-3)
