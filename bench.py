@@ -295,13 +295,66 @@ def _cpu_model():
     return "unknown"
 
 
+TRAFFIC_JSON = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+# kernels that make up one launch of each measured entry point
+TRAFFIC_GROUPS = {
+    "message_fwd": r"maloq::msg::(prep_kernel|gemm_kernel|message_fixup_kernel)",
+    "fock_to_irreps": r"maloq::bt::transform_kernel",
+}
+COPY_BYTES = 4 * 64 * 1024 * 1024        # the --only copy kernel: this many bytes read, as many written
+
+
 def load_traffic(name):
     """HBM bytes per launch measured with rocprofv3 --pmc (profiles/traffic.json)."""
-    p = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
     try:
-        return json.load(open(p)).get(name)
+        return json.load(open(TRAFFIC_JSON)).get(name)
     except (OSError, ValueError):
         return None
+
+
+def _pmc_medians(csv_path, counter):
+    """Median per-dispatch value of `counter`, by kernel name, from a rocprofv3 CSV."""
+    import csv
+    import statistics
+    vals = {}
+    with open(csv_path) as f:
+        for row in csv.DictReader(f):
+            if row["Counter_Name"] == counter:
+                vals.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+    return {k: statistics.median(v) for k, v in vals.items()}
+
+
+def traffic_from(root, dtype):
+    """Writes profiles/traffic.json from rocprofv3 --pmc runs under `root`:
+    <root>/<piece>_<COUNTER>/run_counter_collection.csv for piece in copy, fwd,
+    basis and COUNTER in FETCH_SIZE, WRITE_SIZE (KiB per dispatch).  Each
+    counter is scaled by what it reads for the plain copy of known size."""
+    import re
+    out = {}
+    scale = {}
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        med = _pmc_medians(os.path.join(root, f"copy_{ctr}", "run_counter_collection.csv"), ctr)
+        kib = max(med.values())
+        scale[ctr] = COPY_BYTES / (kib * 1024.0)
+    for name, piece in ((f"message_fwd_{dtype}", "fwd"), ("fock_to_irreps", "basis")):
+        group = TRAFFIC_GROUPS[name.rsplit("_", 1)[0] if name.startswith("message") else name]
+        tot = {}
+        for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+            med = _pmc_medians(os.path.join(root, f"{piece}_{ctr}", "run_counter_collection.csv"), ctr)
+            tot[ctr] = sum(v for k, v in med.items() if re.search(group, k)) * 1024.0 * scale[ctr]
+        out[name] = tot["FETCH_SIZE"] + tot["WRITE_SIZE"]
+        out[name + "_read"] = tot["FETCH_SIZE"]
+        out[name + "_write"] = tot["WRITE_SIZE"]
+    out["copy_scale"] = scale
+    try:
+        prev = json.load(open(TRAFFIC_JSON))
+    except (OSError, ValueError):
+        prev = {}
+    prev.update(out)
+    with open(TRAFFIC_JSON, "w") as f:
+        json.dump(prev, f, indent=1, sort_keys=True)
+    print(json.dumps(out))
+    return 0
 
 
 def profile_only(args):
@@ -321,8 +374,16 @@ def profile_only(args):
             for _ in range(args.reps):
                 message_step(w, True)
     else:
+        # forward transform only, so its counters are not mixed with the inverse
+        import numpy as np
         bw = basis_workload()
-        basis_timing(bw, reps=args.reps)
+        hip, t = bw["hip"], bw["tables"]
+        dev = bw["data"].device
+        dev_args = tuple(torch.as_tensor(np.asarray(a, np.int32), device=dev)
+                         for a in (bw["off"], bw["Z"], bw["rows"], bw["cols"]))
+        plan = hip.make_plan(bw["data"], *dev_args, t.orbital_template, block_data_offsets=bw["bdo"])
+        for _ in range(args.reps):
+            hip.fock_to_irreps(bw["data"], *dev_args, t.orbital_template, block_data_offsets=bw["bdo"], plan=plan)
     torch.cuda.synchronize()
     print(f"[bench] --only {args.only}: {args.reps} reps done", file=sys.stderr, flush=True)
     return 0
@@ -339,7 +400,11 @@ def main(argv=None):
     ap.add_argument("--only", choices=["fwd", "step", "basis", "copy"],
                     help="profiling mode: run one piece a few times and exit (no JSON line)")
     ap.add_argument("--reps", type=int, default=5, help="launches in --only mode")
+    ap.add_argument("--traffic-from", metavar="DIR",
+                    help="write profiles/traffic.json from rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE runs in DIR")
     args = ap.parse_args(argv)
+    if args.traffic_from:
+        return traffic_from(args.traffic_from, args.dtype)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(the hot path runs on a single MI355X; multi-GPU sharding is design-only)", file=sys.stderr)
@@ -378,7 +443,7 @@ def main(argv=None):
                                "rotate->SO(2)->inverse rotate->segment sum, input/radial/weight grads",
                    "molecules": 32, "atoms_per_molecule": 40, "edges": E, "nodes": w["N"],
                    "lmax": w["L"], "mmax": w["M"], "channels": w["C"], "rbf": 8, "cutoff_A": 6.0},
-        "roofline": {"kernel": "message_kernel<4,2> forward (+fixup)", "bound": "mfma",
+        "roofline": {"kernel": "maloq_message_forward: prep + gemm_kernel<4,2> + fixup", "bound": "mfma",
                      "achieved": achieved / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
                      "frac": achieved / peak, "traffic": load_traffic(f"message_fwd_{args.dtype}"),
                      "flops_per_edge": f_edge, "launch_ms": t_fwd_launch * 1e3},
