@@ -4,7 +4,7 @@
 Headline workload: the reference benchmark's config 2 (32 molecules x 40
 atoms, ~30k directed edges, lmax 4, mmax 2, 128 channels, 8 Gaussian RBFs).
 A step is one fused message block, forward and backward, with inputs already
-resident in HBM: per-edge Euler angles + Wigner-D, the radial MLP (torch), the
+resident in HBM: per-edge Euler angles + Wigner-D, the radial MLP (fused HIP), the
 fused rotate -> SO(2) -> inverse-rotate -> segment-sum kernel, and its input,
 radial and weight gradients.  `value` is edges per second.
 
@@ -37,11 +37,9 @@ def fused_flops_per_edge(L, M, c_in, c_out):
 
 
 def make_radial(n_rbf, hidden, out, device):
-    import torch
-    from torch import nn
-    return nn.Sequential(nn.Linear(n_rbf, hidden), nn.LayerNorm(hidden), nn.SiLU(),
-                         nn.Linear(hidden, hidden), nn.LayerNorm(hidden), nn.SiLU(),
-                         nn.Linear(hidden, out)).to(device)
+    """RadialMLP([n_rbf, hidden, hidden, out]) (radial.py:115-142), fused HIP kernels."""
+    from maloq_amd.radial import RadialMLP
+    return RadialMLP([n_rbf, hidden, hidden, out]).to(device)
 
 
 def gaussian_rbf(dist, start, stop, num):
@@ -86,7 +84,7 @@ def message_step(w, backward=True):
     from maloq_amd import message as M
     from maloq_amd.wigner import extract_euler_angles
     eul = extract_euler_angles(w["vec"], seed=1234)
-    rad = w["radial"](gaussian_rbf(w["dist"], 0.0, 6.0, 8)).to(w["dt"])
+    rad = w["radial"](gaussian_rbf(w["dist"], 0.0, 6.0, 8), out_dtype=w["dt"])
     out = M.message_block(w["x"], w["plan"], eul, rad, w["w0"], w["b0"], w["wm"], w["L"], w["M"])
     if backward:
         out.backward(w["gout"])
@@ -127,7 +125,7 @@ def fused_forward_launch_time(w, reps=20):
     from maloq_amd.wigner import extract_euler_angles
     with torch.no_grad():
         eul = extract_euler_angles(w["vec"], seed=1234)
-        rad = w["radial"](gaussian_rbf(w["dist"], 0.0, 6.0, 8)).to(w["dt"])
+        rad = w["radial"](gaussian_rbf(w["dist"], 0.0, 6.0, 8), out_dtype=w["dt"])
         x = w["x"].detach()
         wpack = M.pack_weights(w["w0"], w["wm"], w["L"], w["M"], False, w["C"], w["C"], w["dt"], 0)
         f = lambda: M.message_forward(x, w["plan"], eul, rad, w["w0"], w["b0"], w["wm"], w["L"], w["M"],
@@ -229,6 +227,11 @@ def cpu_message_baseline(budget_s=15.0):
         conv[k].requires_grad_()
     for wmm in conv["wm"]:
         wmm.requires_grad_()
+    # the reference's RadialMLP as torch modules (radial.py:115-142), fp32 CPU
+    torch.manual_seed(0)
+    radial = torch.nn.Sequential(torch.nn.Linear(8, 64), torch.nn.LayerNorm(64), torch.nn.SiLU(),
+                                 torch.nn.Linear(64, 64), torch.nn.LayerNorm(64), torch.nn.SiLU(),
+                                 torch.nn.Linear(64, 1536))
 
     def run(nmol):
         sel = np.isin(g.mol[g.dst], np.arange(nmol))
@@ -236,8 +239,8 @@ def cpu_message_baseline(budget_s=15.0):
         ei = torch.from_numpy(np.stack([g.src[sel], g.dst[sel]]))
         vec = torch.from_numpy(g.edge_distance_vec()[sel]).float()
         x = torch.randn(len(nodes), 25, C, generator=gen).requires_grad_()
-        rad = torch.rand(int(sel.sum()), 1536, generator=gen).requires_grad_()
         t0 = time.perf_counter()
+        rad = radial(gaussian_rbf(vec.norm(dim=1), 0.0, 6.0, 8))
         eul = orot.init_edge_rot_euler_angles(vec, torch.rand(len(vec), generator=gen))
         out = omsg.message_block(x, ei, eul, Jd, L, Mm, conv, rad=rad)
         out.backward(torch.ones_like(out))

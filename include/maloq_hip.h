@@ -216,6 +216,51 @@ int maloq_message_dw(int dtype, int lmax, int mmax, const void* dz, const void* 
                      int64_t num_edges, int c_out, int c_in, int splits, float* partials,
                      float* dw0, float* dw1, float* dw2, float* dw3, void* stream);
 
+/* ------------------------------------------------------------ RadialMLP -- */
+
+/* The radial function of SO2_Convolution: RadialMLP(channels_list)
+ * (helm/nn/radial.py:115-142, called at helm/nn/so2_layers.py:152-154), i.e.
+ *   u_0 = x;  u_i = SiLU(LayerNorm_i(W_i u_{i-1} + b_i)), i = 1..nhidden;
+ *   out = W_o u_H + b_o.
+ * widths[nhidden + 2] = channels_list: c_0 (multiple of 4, <= 128), hidden
+ * widths (multiples of 32, <= 128), c_out (multiple of 64).  Hidden-layer
+ * parameters are host arrays of nhidden device pointers (fp32, 16-byte aligned):
+ * weight[i] [c_{i+1}, c_i], bias[i], ln_weight[i], ln_bias[i] [c_{i+1}];
+ * eps is LayerNorm's.  out_weight [c_out, c_H], out_bias [c_out] fp32.
+ * dtype 0 = fp32, 1 = bf16: the output dtype and the output layer's MFMA
+ * operand type (fp32 accumulation); hidden layers always run in fp32. */
+
+/* Bytes of the packed output-layer weights (both layouts). */
+int64_t maloq_radial_pack_bytes(int dtype, int c_out, int c_hidden);
+
+/* Forward.  x [E, c_0] fp32; out [E, c_out] (dtype); wpack: workspace of
+ * maloq_radial_pack_bytes (written here, read by maloq_radial_bwd); save:
+ * nullable [E, c_H] (dtype), the last hidden activation for the backward.
+ * Replaces the forward of RadialMLP.net (torch Linear / LayerNorm / SiLU). */
+int maloq_radial_fwd(int dtype, int nhidden, const int* widths, const float* x,
+                     int64_t num_edges, const float* const* weight, const float* const* bias,
+                     const float* const* ln_weight, const float* const* ln_bias, float eps,
+                     const float* out_weight, const float* out_bias, void* wpack, void* out,
+                     void* save, void* stream);
+
+/* Floats of the partials workspace of maloq_radial_bwd. */
+int64_t maloq_radial_bwd_partials_floats(int dtype, int nhidden, const int* widths,
+                                         int64_t num_edges);
+
+/* Backward (num_edges >= 1).  grad [E, c_out] (dtype) = dL/dout; save and
+ * wpack as written by maloq_radial_fwd with the same parameters.  Outputs
+ * (fp32): grad_x [E, c_0] (nullable), grad_hidden = for each hidden layer in
+ * order [dW_i (c_{i+1} x c_i), db_i, dln_weight_i, dln_bias_i],
+ * grad_out_weight [c_out, c_H], grad_out_bias [c_out].  Per-tile and split-K
+ * partials are summed in a fixed order (deterministic).
+ * Replaces the autograd backward of RadialMLP.net. */
+int maloq_radial_bwd(int dtype, int nhidden, const int* widths, const float* x,
+                     int64_t num_edges, const float* const* weight, const float* const* bias,
+                     const float* const* ln_weight, const float* const* ln_bias, float eps,
+                     const void* wpack, const void* grad, const void* save, float* grad_x,
+                     float* partials, float* grad_hidden, float* grad_out_weight,
+                     float* grad_out_bias, void* stream);
+
 /* ------------------------------------------------------- segment scatter -- */
 
 /* out[n, :] = sum_{p in [seg_ptr[n], seg_ptr[n+1])} msg[perm ? perm[p] : p, :],

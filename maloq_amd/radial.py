@@ -1,0 +1,162 @@
+"""RadialMLP of the SO(2) convolution on MI355X.
+
+The reference builds the radial function of every SO2_Convolution as
+``RadialMLP(edge_channels_list + [num_channels_rad])`` (helm/nn/radial.py:115-142,
+helm/nn/so2_layers.py:133-137) and applies it to the edge features before the
+per-m linears (so2_layers.py:152-154):
+
+    Linear(c_0, c_1) -> LayerNorm(c_1) -> SiLU -> ... -> Linear(c_H, c_out)
+
+:class:`RadialMLP` keeps that module structure (``net`` is the same
+``nn.Sequential`` of Linear / LayerNorm / SiLU, so state dicts are
+interchangeable) but its forward and backward are the fused HIP kernels of
+``maloq_radial_fwd`` / ``maloq_radial_bwd``: one launch for the whole forward
+(the output written directly in the message rows' dtype), three for the
+backward (per-tile hidden gradients, split-K output-layer gradient, fixed-order
+sums).  There is no CPU path: tensors must live on the GPU.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+from torch import nn
+
+from . import _lib
+
+DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1}
+
+
+def _layers(channels_list):
+    layers = []
+    n = len(channels_list)
+    for i in range(1, n):
+        layers.append(nn.Linear(channels_list[i - 1], channels_list[i], bias=True))
+        if i < n - 1:
+            layers += [nn.LayerNorm(channels_list[i]), nn.SiLU()]
+    return layers
+
+
+class RadialMLP(nn.Module):
+    """Drop-in for the reference's RadialMLP (radial.py:115-142).
+
+    ``forward(inputs, out_dtype=None)``: inputs [E, c_0] fp32 on the GPU; the
+    result is [E, c_out] in ``out_dtype`` (default fp32; bfloat16 when it
+    feeds a bf16 message block)."""
+
+    def __init__(self, channels_list) -> None:
+        super().__init__()
+        self.channels_list = [int(c) for c in channels_list]
+        if len(self.channels_list) < 3:
+            raise ValueError("RadialMLP needs at least one hidden layer: [c_0, c_1, ..., c_out]")
+        self.net = nn.Sequential(*_layers(self.channels_list))
+
+    def forward(self, inputs: torch.Tensor, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+        return radial_mlp(inputs, self, out_dtype)
+
+
+def _params(mod: RadialMLP):
+    mods = list(mod.net)
+    lin = [m for m in mods if isinstance(m, nn.Linear)]
+    lns = [m for m in mods if isinstance(m, nn.LayerNorm)]
+    if len(lns) != len(lin) - 1:
+        raise ValueError("unexpected RadialMLP structure")
+    eps = lns[0].eps
+    for ln in lns:
+        if ln.weight is None or ln.bias is None:
+            raise ValueError("RadialMLP's LayerNorms must be affine")
+        if ln.eps != eps:
+            raise ValueError("RadialMLP's LayerNorms must share eps")
+    hidden = []
+    for li, ln in zip(lin[:-1], lns):
+        hidden += [li.weight, li.bias, ln.weight, ln.bias]
+    return eps, hidden + [lin[-1].weight, lin[-1].bias]
+
+
+def radial_mlp(inputs: torch.Tensor, mod: RadialMLP, out_dtype: torch.dtype | None = None):
+    """Fused forward (differentiable) of ``mod`` on ``inputs``."""
+    dt = out_dtype or torch.float32
+    if dt not in DTYPE_CODE:
+        raise ValueError(f"unsupported output dtype {dt}")
+    _lib.require_cuda(inputs)
+    eps, params = _params(mod)
+    widths = tuple(mod.channels_list)
+    if inputs.dim() != 2 or inputs.shape[1] != widths[0]:
+        raise ValueError(f"inputs must be [E, {widths[0]}]")
+    return _RadialFn.apply(inputs, dt, widths, eps, *params)
+
+
+def _ptr_array(ts):
+    return (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])
+
+
+def _widths_array(widths):
+    return (ctypes.c_int * len(widths))(*widths)
+
+
+class _RadialFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, dt, widths, eps, *params):
+        nh = len(widths) - 2
+        code = DTYPE_CODE[dt]
+        x = x.float().contiguous()
+        ps = [p.detach().float().contiguous() for p in params]
+        hid = [ps[4 * i: 4 * i + 4] for i in range(nh)]
+        wo, bo = ps[-2], ps[-1]
+        E, dev = x.shape[0], x.device
+        lib = _lib.load()
+        wpack = torch.empty(lib.maloq_radial_pack_bytes(code, widths[-1], widths[-2]), dtype=torch.uint8,
+                            device=dev)
+        out = torch.empty(E, widths[-1], dtype=dt, device=dev)
+        need = any(ctx.needs_input_grad[:1] + ctx.needs_input_grad[4:])
+        save = torch.empty(E, widths[-2], dtype=dt, device=dev) if need else None
+        wa = _widths_array(widths)
+        _lib.call("maloq_radial_fwd", code, nh, wa, _lib.ptr(x), E,
+                  _ptr_array([h[0] for h in hid]), _ptr_array([h[1] for h in hid]),
+                  _ptr_array([h[2] for h in hid]), _ptr_array([h[3] for h in hid]), float(eps),
+                  _lib.ptr(wo), _lib.ptr(bo), _lib.ptr(wpack), _lib.ptr(out), _lib.ptr(save),
+                  _lib.stream_of(dev))
+        ctx.widths, ctx.eps, ctx.dt, ctx.code = widths, eps, dt, code
+        ctx.param_dtypes = [p.dtype for p in params]
+        if need:
+            ctx.save_for_backward(x, wpack, save, *ps)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        x, wpack, save, *ps = ctx.saved_tensors
+        widths, code = ctx.widths, ctx.code
+        nh = len(widths) - 2
+        hid = [ps[4 * i: 4 * i + 4] for i in range(nh)]
+        E, dev = x.shape[0], x.device
+        cH, cout = widths[-2], widths[-1]
+        if E == 0:
+            grads = [torch.zeros_like(p) for p in ps]
+            dx = torch.zeros_like(x) if ctx.needs_input_grad[0] else None
+            return (dx, None, None, None, *[gr.to(d) for gr, d in zip(grads, ctx.param_dtypes)])
+        g = g.to(ctx.dt).contiguous()
+        lib = _lib.load()
+        wa = _widths_array(widths)
+        parts = torch.empty(lib.maloq_radial_bwd_partials_floats(code, nh, wa, E), dtype=torch.float32, device=dev)
+        n_hid = sum(widths[i + 1] * (widths[i] + 3) for i in range(nh))
+        gh = torch.empty(n_hid, dtype=torch.float32, device=dev)
+        dwo = torch.empty(cout, cH, dtype=torch.float32, device=dev)
+        dbo = torch.empty(cout, dtype=torch.float32, device=dev)
+        dx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
+        _lib.call("maloq_radial_bwd", code, nh, wa, _lib.ptr(x), E,
+                  _ptr_array([h[0] for h in hid]), _ptr_array([h[1] for h in hid]),
+                  _ptr_array([h[2] for h in hid]), _ptr_array([h[3] for h in hid]), float(ctx.eps),
+                  _lib.ptr(wpack), _lib.ptr(g), _lib.ptr(save), _lib.ptr(dx), _lib.ptr(parts),
+                  _lib.ptr(gh), _lib.ptr(dwo), _lib.ptr(dbo), _lib.stream_of(dev))
+        grads = []
+        off = 0
+        for i in range(nh):
+            c, ci = widths[i + 1], widths[i]
+            grads.append(gh[off: off + c * ci].view(c, ci))
+            off += c * ci
+            for _ in range(3):  # bias, LayerNorm weight, LayerNorm bias
+                grads.append(gh[off: off + c])
+                off += c
+        grads += [dwo, dbo]
+        grads = [gr.to(d) for gr, d in zip(grads, ctx.param_dtypes)]
+        return (dx, None, None, None, *grads)

@@ -74,3 +74,18 @@ def gaussian_smearing(dist, start, stop, num, width=1.0):
     coeff = -0.5 / (width * (offset[1] - offset[0])).item() ** 2
     d = dist.reshape(-1, 1).to(torch.float64) - offset.reshape(1, -1)
     return torch.exp(coeff * d ** 2)
+
+
+def radial_mlp(x, hidden, w_out, b_out, eps=1e-5):
+    """radial.py:115-142 (RadialMLP): per hidden layer (W, b, gamma, beta)
+    z = x W^T + b; LayerNorm over the last axis with the biased variance,
+    (z - mean) / sqrt(var + eps) * gamma + beta; SiLU(a) = a / (1 + exp(-a));
+    then the output Linear.  Written out in fp64 (differentiable by autograd)."""
+    u = x.to(torch.float64)
+    for w, b, g, bt in hidden:
+        z = u @ w.to(torch.float64).T + b.to(torch.float64)
+        mean = z.mean(dim=-1, keepdim=True)
+        var = ((z - mean) ** 2).mean(dim=-1, keepdim=True)
+        a = (z - mean) / torch.sqrt(var + eps) * g.to(torch.float64) + bt.to(torch.float64)
+        u = a / (1.0 + torch.exp(-a))
+    return u @ w_out.to(torch.float64).T + b_out.to(torch.float64)
