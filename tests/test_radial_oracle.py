@@ -85,6 +85,6 @@ def test_library_rejects_unsupported_widths():
     lib = _lib.load()
     ok = (ctypes.c_int * 4)(8, 64, 64, 1536)
     assert lib.maloq_radial_bwd_partials_floats(1, 2, ok, 1000) > 0
-    for bad in [(8, 48, 64, 1536), (8, 64, 64, 1000), (6, 64, 64, 1536), (8, 256, 64, 1536), (4, 128, 128, 384)]:
+    for bad in [(8, 48, 64, 1536), (8, 64, 64, 1000), (6, 64, 64, 1536), (8, 256, 64, 1536), (4, 128, 64, 384)]:
         arr = (ctypes.c_int * 4)(*bad)
         assert lib.maloq_radial_bwd_partials_floats(1, 2, arr, 1000) == -1, bad
