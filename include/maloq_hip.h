@@ -162,7 +162,9 @@ int maloq_message_wigner_floats(int lmax, int mmax);
  * tensors of the backward): y_ws [E, d', c_in] (dtype) receives the rotated,
  * radially scaled SO(2) input rows (m-major), r_ws (nullable, same shape) the
  * unscaled rows, dk_ws [E, maloq_message_wigner_floats] fp32 the kept
- * Wigner-D rows.  Two kernels: a per-edge prep (Wigner rows + rotation) and
+ * Wigner-D rows; gate_ws (gated blocks, nullable) [E, d' + lmax, c_out] (dtype)
+ * the pre-activation rows (kept rows, then the gate rows of degrees 1..lmax)
+ * that the gated backward needs.  Two kernels: a per-edge prep (Wigner rows + rotation) and
  * the SO(2) MFMA GEMM with inverse rotation and segment sum, then a fixup for
  * segments cut by tile boundaries.
  * Replaces Edgewise.forward_node, helm/esen_block.py:146-208 (bmm(wigner),
@@ -173,11 +175,15 @@ int maloq_message_fwd(int dtype, int lmax, int mmax, int gate, const void* x, in
                       const float* eulers, const void* rad, const void* wpack, const float* bias,
                       const float* jd, float* out, int64_t num_nodes, int c_out,
                       const int64_t* seg_ptr, float* partials, void* y_ws, void* r_ws,
-                      float* dk_ws, void* stream);
+                      float* dk_ws, void* gate_ws, void* stream);
 
-/* Input and radial-scale gradients of the (ungated) fused block:
- *   grad_x[n] = sum_{e: src[e]=n} D_e^T rad[e] (*) SO2^T(D_e grad_out[dst[e]]),
- *   grad_rad[e] = SO2^T(D_e grad_out[dst[e]]) (*) R_e   (R_e = D_e x[src[e]]).
+/* Input and radial-scale gradients of the fused block:
+ *   grad_x[n] = sum_{e: src[e]=n} D_e^T rad[e] (*) SO2^T(G_e),
+ *   grad_rad[e] = SO2^T(G_e) (*) R_e   (R_e = D_e x[src[e]]),
+ * with G_e = D_e grad_out[dst[e]] (ungated), or for gate != 0 the gradient
+ * through GateActivation at the pre-activations gate_saved (the forward's
+ * gate_ws): then G_e has d' + lmax rows (the last lmax: dL/dgate), the SO(2)
+ * transpose includes the gate weights, and dz_ws has d' + lmax rows per edge.
  * Edges in src-sorted order: src_sorted non-decreasing, dst_by_src the
  * matching dst, edge_idx the forward (dst-sorted) position of each edge,
  * which indexes dk (forward dk_ws), rad, grad_rad, r_saved (forward r_ws) and
@@ -185,13 +191,13 @@ int maloq_message_fwd(int dtype, int lmax, int mmax, int gate, const void* x, in
  * c_out] (dtype) receives the rotated output-gradient rows (for the weight
  * gradient).
  * Replaces the autograd backward of Edgewise.forward_node (esen_block.py:146-208). */
-int maloq_message_bwd_dx(int dtype, int lmax, int mmax, const float* grad_out, int c_out,
-                         const int32_t* dst_by_src, const int32_t* src_sorted,
+int maloq_message_bwd_dx(int dtype, int lmax, int mmax, int gate, const float* grad_out,
+                         int c_out, const int32_t* dst_by_src, const int32_t* src_sorted,
                          const int32_t* edge_idx, int64_t num_edges, const float* dk,
                          const void* rad, void* grad_rad, const void* r_saved,
                          const void* wpack_t, const float* jd, float* grad_x, int64_t num_nodes,
                          int c_in, const int64_t* seg_ptr_src, float* partials, void* dz_ws,
-                         void* stream);
+                         const void* gate_saved, void* stream);
 
 /* Rows to allocate for the saved SO(2) rows (y_ws of maloq_message_fwd, dz_ws of
  * maloq_message_bwd_dx) so that maloq_message_dw can read them in whole 128-edge
@@ -200,19 +206,23 @@ int maloq_message_bwd_dx(int dtype, int lmax, int mmax, const float* grad_out, i
 int64_t maloq_message_edge_rows(int64_t num_edges);
 
 /* Floats of the split-K partials buffer of maloq_message_dw. */
-int64_t maloq_message_dw_partials_floats(int lmax, int mmax, int c_out, int c_in, int splits);
+int64_t maloq_message_dw_partials_floats(int lmax, int mmax, int gate, int c_out, int c_in,
+                                         int splits);
 
 /* Weight gradients of the SO(2) linear from the saved rows:
  *   dW_0 = sum_e dZ_0(e)^T Y_0(e);  for m >= 1 with C_m = sum_e dZ_m^T Y_m over
  *   the stacked (+m, -m) rows: dWr = C[+,+] + C[-,-], dWi = C[-,+] - C[+,-],
  *   dW_m = [dWr; dWi] in the layout of so2_m_conv[m-1].fc.weight.
+ * For a gated block (gate != 0) dz has d' + lmax rows per edge (the last lmax:
+ * dL/dgate) and dW_0 also holds the gate rows, first: [lmax c_out + (lmax+1) c_out,
+ * (lmax+1) c_in], the gate block being sum_e dG(e)^T Y_0(e).
  * dz [E, d', c_out], y [E, d', c_in] (dtype; for bf16 with maloq_message_edge_rows(E)
  * rows, zero from row E on, channels multiples of 8), dw0 [(lmax+1) c_out, (lmax+1) c_in],
  * dw_m [2 (lmax-m+1) c_out, (lmax-m+1) c_in] fp32.  Split-K over edges,
  * partials summed in split order (deterministic).
  * Replaces the autograd weight gradient of SO2_Convolution
  * (helm/nn/so2_layers.py:139-214, SO2_m_Conv :61-67). */
-int maloq_message_dw(int dtype, int lmax, int mmax, const void* dz, const void* y,
+int maloq_message_dw(int dtype, int lmax, int mmax, int gate, const void* dz, const void* y,
                      int64_t num_edges, int c_out, int c_in, int splits, float* partials,
                      float* dw0, float* dw1, float* dw2, float* dw3, void* stream);
 

@@ -38,12 +38,12 @@ SIGNATURES = {
     "maloq_message_kept_rows": [_i32, _i32],
     "maloq_message_wigner_floats": [_i32, _i32],
     "maloq_message_fwd": [_i32, _i32, _i32, _i32, _p, _i32, _p, _p, _i64, _p, _p, _p, _p, _p, _p,
-                          _i64, _i32, _p, _p, _p, _p, _p, _p],
-    "maloq_message_bwd_dx": [_i32, _i32, _i32, _p, _i32, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p,
-                             _p, _i64, _i32, _p, _p, _p, _p],
+                          _i64, _i32, _p, _p, _p, _p, _p, _p, _p],
+    "maloq_message_bwd_dx": [_i32, _i32, _i32, _i32, _p, _i32, _p, _p, _p, _i64, _p, _p, _p, _p, _p,
+                             _p, _p, _i64, _i32, _p, _p, _p, _p, _p],
     "maloq_message_edge_rows": [_i64],
-    "maloq_message_dw_partials_floats": [_i32, _i32, _i32, _i32, _i32],
-    "maloq_message_dw": [_i32, _i32, _i32, _p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p],
+    "maloq_message_dw_partials_floats": [_i32, _i32, _i32, _i32, _i32, _i32],
+    "maloq_message_dw": [_i32, _i32, _i32, _i32, _p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p],
     "maloq_radial_pack_bytes": [_i32, _i32, _i32],
     "maloq_radial_fwd": [_i32, _i32, _p, _p, _i64, _p, _p, _p, _p, ctypes.c_float, _p, _p, _p, _p, _p, _p],
     "maloq_radial_bwd_partials_floats": [_i32, _i32, _p, _i64],

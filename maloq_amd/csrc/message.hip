@@ -30,6 +30,8 @@ __global__ void message_fixup_kernel(const int64_t* __restrict__ seg_ptr, int64_
 
 // Packed B fragments per output-channel block: for every kernel-input degree
 // li and K step, per output degree lo: g0, [gate], (Wr, Wi) for m <= min(mmax, li, lo).
+// The gate fragment is there for lo >= 1 in the forward and for li >= 1 in the
+// input gradient: the same count either way.
 static int64_t frags_per_cb(int lmax, int mmax, int gate, int c_k, int kc) {
   int64_t total = 0;
   for (int li = 0; li <= lmax; ++li) {
@@ -133,7 +135,7 @@ extern "C" int maloq_message_fwd(int dtype, int lmax, int mmax, int gate, const 
                                  const float* eulers, const void* rad, const void* wpack,
                                  const float* bias, const float* jd, float* out, int64_t num_nodes,
                                  int c_out, const int64_t* seg_ptr, float* partials, void* y_ws,
-                                 void* r_ws, float* dk_ws, void* stream) {
+                                 void* r_ws, float* dk_ws, void* gate_ws, void* stream) {
   int rc = check_common(dtype, lmax, mmax, c_in, c_out, num_edges);
   if (rc) return rc;
   MALOQ_REQUIRE(num_nodes >= 0, "num_nodes < 0");
@@ -155,20 +157,21 @@ extern "C" int maloq_message_fwd(int dtype, int lmax, int mmax, int gate, const 
     a.ntiles = (num_edges + tile_edges(lmax, gate) - 1) / tile_edges(lmax, gate);
     const int kc = dtype == 1 ? BF16::KC : F32::KC;
     a.frags_per_cb = frags_per_cb(lmax, mmax, gate, c_in, kc);
+    a.gsave = gate ? gate_ws : nullptr;
     rc = dispatch(lmax, mmax, dtype, gate, FWD, a, s);
     if (rc) return rc;
   }
   return fixup(seg_ptr, num_nodes, partials, out, d * c_out, tile_edges(lmax, gate), s);
 }
 
-extern "C" int maloq_message_bwd_dx(int dtype, int lmax, int mmax, const float* grad_out,
+extern "C" int maloq_message_bwd_dx(int dtype, int lmax, int mmax, int gate, const float* grad_out,
                                     int c_out, const int32_t* dst_by_src,
                                     const int32_t* src_sorted, const int32_t* edge_idx,
                                     int64_t num_edges, const float* dk, const void* rad,
                                     void* grad_rad, const void* r_saved, const void* wpack_t,
                                     const float* jd, float* grad_x, int64_t num_nodes, int c_in,
                                     const int64_t* seg_ptr_src, float* partials, void* dz_ws,
-                                    void* stream) {
+                                    const void* gate_saved, void* stream) {
   // kernel input channels = c_out (gradient side), output channels = c_in
   int rc = check_common(dtype, lmax, mmax, c_out, c_in, num_edges);
   if (rc) return rc;
@@ -179,10 +182,11 @@ extern "C" int maloq_message_bwd_dx(int dtype, int lmax, int mmax, const float* 
     MALOQ_REQUIRE(grad_out && dst_by_src && src_sorted && edge_idx && dk && partials && dz_ws,
                   "null pointer");
     MALOQ_REQUIRE(rad == nullptr || r_saved != nullptr, "the radial gradient needs the saved rows");
+    MALOQ_REQUIRE(!gate || gate_saved != nullptr, "the gated backward needs the saved pre-activations");
     PrepArgs p{};
     p.x = grad_out; p.gidx = dst_by_src; p.eidx = edge_idx; p.eulers = nullptr; p.rad = nullptr;
     p.jd = jd; p.y = dz_ws; p.r = nullptr; p.dk = const_cast<float*>(dk); p.build_d = 0;
-    p.E = num_edges; p.C = c_out;
+    p.E = num_edges; p.C = c_out; p.gsave = gate ? gate_saved : nullptr;
     rc = prep_dispatch(lmax, mmax, dtype, BWD_DX, p, s);
     if (rc) return rc;
     Args a{};
@@ -190,11 +194,11 @@ extern "C" int maloq_message_bwd_dx(int dtype, int lmax, int mmax, const float* 
     a.rad = rad; a.drad = grad_rad; a.rsave = r_saved;
     a.wpack = static_cast<const char*>(wpack_t); a.bias = nullptr; a.out = grad_x;
     a.part = partials; a.E = num_edges; a.C_k = c_out; a.C_n = c_in; a.n_cb = c_in / CB;
-    a.extra = 0; a.ntiles = (num_edges + tile_edges(lmax, 0) - 1) / tile_edges(lmax, 0);
+    a.extra = 0; a.ntiles = (num_edges + tile_edges(lmax, gate) - 1) / tile_edges(lmax, gate);
     const int kc = dtype == 1 ? BF16::KC : F32::KC;
-    a.frags_per_cb = frags_per_cb(lmax, mmax, 0, c_out, kc);
-    rc = dispatch(lmax, mmax, dtype, 0, BWD_DX, a, s);
+    a.frags_per_cb = frags_per_cb(lmax, mmax, gate, c_out, kc);
+    rc = dispatch(lmax, mmax, dtype, gate, BWD_DX, a, s);
     if (rc) return rc;
   }
-  return fixup(seg_ptr_src, num_nodes, partials, grad_x, d * c_in, tile_edges(lmax, 0), s);
+  return fixup(seg_ptr_src, num_nodes, partials, grad_x, d * c_in, tile_edges(lmax, gate), s);
 }

@@ -38,11 +38,13 @@ constexpr int MAXG = 8;
 constexpr int DW_T = 128;  // output tile edge
 
 struct DwArgs {
-  const void* dz;       // [E, dp, C_out]
-  const void* y;        // [E, dp, C_in]
+  const void* dz;       // [E, dpz, C_out]
+  const void* y;        // [E, dpy, C_in]
   int64_t E;
-  int dp, C_out, C_in, ngroups, splits;
-  int row0[MAXG], rows[MAXG];
+  int dpz, dpy, C_out, C_in, ngroups, splits;
+  // group g: dz rows [row0z, row0z + rowsz) x y rows [row0y, row0y + rowsy)
+  int row0z[MAXG], rowsz[MAXG], row0y[MAXG], rowsy[MAXG];
+  int gate;                  // last group: dL/dgate rows x m = 0 rows
   int ntk[MAXG];             // DW_T-wide tiles along k (= rows * C_in)
   int64_t tile0[MAXG + 1];   // cumulative tile counts
   int64_t goff[MAXG + 1];    // element offset of group g in one split's partials
@@ -99,7 +101,7 @@ __global__ __launch_bounds__(256) void dw_kernel(DwArgs a) {
   while (g + 1 < a.ngroups && t >= a.tile0[g + 1]) ++g;
   const int64_t lt = t - a.tile0[g];
   const int tn = static_cast<int>(lt / a.ntk[g]), tk = static_cast<int>(lt % a.ntk[g]);
-  const int Ng = a.rows[g] * a.C_out, Kg = a.rows[g] * a.C_in;
+  const int Ng = a.rowsz[g] * a.C_out, Kg = a.rowsy[g] * a.C_in;
   const int64_t eb = split * a.e_per_split;
   const int64_t ee = (eb + a.e_per_split) < a.E ? (eb + a.e_per_split) : a.E;
 
@@ -112,8 +114,8 @@ __global__ __launch_bounds__(256) void dw_kernel(DwArgs a) {
   const int lim = op ? Kg : Ng;
   const typename TM::raw* src = reinterpret_cast<const typename TM::raw*>(op ? a.y : a.dz);
   int64_t coladdr = -1;  // element offset of (edge 0, col) or -1 if the block is outside the tile
-  if (col < lim) coladdr = static_cast<int64_t>(a.row0[g] + col / C) * C + col % C;
-  const int64_t estride = static_cast<int64_t>(a.dp) * C;
+  if (col < lim) coladdr = static_cast<int64_t>((op ? a.row0y[g] : a.row0z[g]) + col / C) * C + col % C;
+  const int64_t estride = static_cast<int64_t>(op ? a.dpy : a.dpz) * C;
   // LDS destination: fragment (col tile, k-substep), row = column within the tile
   const int cl = cg * VEC;  // column within the 128 tile
   const int e_in = eg * VEC;
@@ -242,7 +244,7 @@ __global__ __launch_bounds__(256, 1) void dw_tr_kernel(DwArgs a) {
   while (g + 1 < a.ngroups && t >= a.tile0[g + 1]) ++g;
   const int64_t lt = t - a.tile0[g];
   const int tn = static_cast<int>(lt / a.ntk[g]), tk = static_cast<int>(lt % a.ntk[g]);
-  const int Ng = a.rows[g] * a.C_out, Kg = a.rows[g] * a.C_in;
+  const int Ng = a.rowsz[g] * a.C_out, Kg = a.rowsy[g] * a.C_in;
   const int64_t eb = split * a.e_per_split;
   const int64_t epad = (a.E + CHUNK - 1) / CHUNK * CHUNK;
   const int64_t ee = (eb + a.e_per_split) < epad ? (eb + a.e_per_split) : epad;
@@ -251,10 +253,10 @@ __global__ __launch_bounds__(256, 1) void dw_tr_kernel(DwArgs a) {
   // DMA: wave w copies chunks p = (4 w + j) 64 + lane of each operand tile
   // (row r = p / 32, slot p % 32), loading global chunk (slot ^ (r & 7)).
   const uint16_t* za = reinterpret_cast<const uint16_t*>(a.dz) +
-                       static_cast<int64_t>(a.row0[g]) * a.C_out + static_cast<int64_t>(tn) * T;
+                       static_cast<int64_t>(a.row0z[g]) * a.C_out + static_cast<int64_t>(tn) * T;
   const uint16_t* yb = reinterpret_cast<const uint16_t*>(a.y) +
-                       static_cast<int64_t>(a.row0[g]) * a.C_in + static_cast<int64_t>(tk) * T;
-  const int64_t sa_e = static_cast<int64_t>(a.dp) * a.C_out, sb_e = static_cast<int64_t>(a.dp) * a.C_in;
+                       static_cast<int64_t>(a.row0y[g]) * a.C_in + static_cast<int64_t>(tk) * T;
+  const int64_t sa_e = static_cast<int64_t>(a.dpz) * a.C_out, sb_e = static_cast<int64_t>(a.dpy) * a.C_in;
   int dr[4], dc[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -328,13 +330,14 @@ __global__ __launch_bounds__(256, 1) void dw_tr_kernel(DwArgs a) {
 }
 
 // One thread per element of the reference-layout gradients:
-// dW0 [(L+1) C_out, (L+1) C_in], then dW_m [2 (L-m+1) C_out, (L-m+1) C_in].
+// dW0 [(gate ? L : 0) C_out + (L+1) C_out, (L+1) C_in] (gate rows first, as in
+// fc_m0, so2_layers.py:112-115), then dW_m [2 (L-m+1) C_out, (L-m+1) C_in].
 __global__ void dw_reduce_kernel(DwArgs a, int lmax, float* __restrict__ dw0,
                                  float* __restrict__ dw1, float* __restrict__ dw2,
                                  float* __restrict__ dw3) {
   const int g = blockIdx.y;
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t Kg = static_cast<int64_t>(a.rows[g]) * a.C_in;
+  const int64_t Kg = static_cast<int64_t>(a.rowsy[g]) * a.C_in;
   const int64_t stride = a.goff[a.ngroups];
   auto C = [&](int64_t n, int64_t k) {
     const float* p = a.part + a.goff[g] + n * Kg + k;
@@ -342,10 +345,12 @@ __global__ void dw_reduce_kernel(DwArgs a, int lmax, float* __restrict__ dw0,
     for (int sp = 0; sp < a.splits; ++sp) s += p[sp * stride];
     return s;
   };
-  if (g == 0) {
-    const int64_t Ng = static_cast<int64_t>(a.rows[0]) * a.C_out;
+  const bool gate_group = a.gate && g == a.ngroups - 1;
+  if (g == 0 || gate_group) {
+    const int64_t Ng = static_cast<int64_t>(a.rowsz[g]) * a.C_out;
     if (idx >= Ng * Kg) return;
-    dw0[idx] = C(idx / Kg, idx % Kg);
+    float* d = dw0 + ((g == 0 && a.gate) ? static_cast<int64_t>(lmax) * a.C_out * Kg : 0);
+    d[idx] = C(idx / Kg, idx % Kg);
     return;
   }
   const int m = g;
@@ -372,29 +377,41 @@ using namespace maloq::msg;
 
 // tile: output tile edge (128 for dw_kernel, 256 for dw_tr_kernel); gran:
 // split boundaries are multiples of this many edges.
-static int dw_setup(DwArgs& a, int lmax, int mmax, int64_t E, int c_out, int c_in, int splits,
-                    int tile, int gran) {
+// Groups: m = 0 (rows 0..L of both), +-m for m = 1..mmax (stacked), and for a
+// gated block dz's gate rows (after the kept rows) against y's m = 0 rows.
+static int dw_setup(DwArgs& a, int lmax, int mmax, int gate, int64_t E, int c_out, int c_in,
+                    int splits, int tile, int gran) {
   MALOQ_REQUIRE(mmax >= 0 && mmax <= 3 && mmax <= lmax, "mmax out of range for the weight gradient");
   MALOQ_REQUIRE(splits >= 1 && splits <= 64, "splits out of range");
   a.E = E;
   a.C_out = c_out;
   a.C_in = c_in;
-  a.ngroups = mmax + 1;
+  a.gate = gate ? 1 : 0;
+  a.ngroups = mmax + 1 + a.gate;
   a.splits = splits;
   int row = 0;
-  a.tile0[0] = 0;
-  a.goff[0] = 0;
   for (int g = 0; g <= mmax; ++g) {
     const int r = (g == 0) ? (lmax + 1) : 2 * (lmax - g + 1);
-    a.row0[g] = row;
-    a.rows[g] = r;
+    a.row0z[g] = a.row0y[g] = row;
+    a.rowsz[g] = a.rowsy[g] = r;
     row += r;
-    const int64_t Ng = static_cast<int64_t>(r) * c_out, Kg = static_cast<int64_t>(r) * c_in;
+  }
+  a.dpy = row;
+  a.dpz = row + (gate ? lmax : 0);
+  if (gate) {
+    a.row0z[mmax + 1] = row;
+    a.rowsz[mmax + 1] = lmax;
+    a.row0y[mmax + 1] = 0;
+    a.rowsy[mmax + 1] = lmax + 1;
+  }
+  a.tile0[0] = 0;
+  a.goff[0] = 0;
+  for (int g = 0; g < a.ngroups; ++g) {
+    const int64_t Ng = static_cast<int64_t>(a.rowsz[g]) * c_out, Kg = static_cast<int64_t>(a.rowsy[g]) * c_in;
     a.ntk[g] = static_cast<int>((Kg + tile - 1) / tile);
     a.tile0[g + 1] = a.tile0[g] + ((Ng + tile - 1) / tile) * a.ntk[g];
     a.goff[g + 1] = a.goff[g] + Ng * Kg;
   }
-  a.dp = row;
   a.e_per_split = ((E + splits - 1) / splits + gran - 1) / gran * gran;
   return MALOQ_OK;
 }
@@ -408,14 +425,16 @@ extern "C" int64_t maloq_message_edge_rows(int64_t num_edges) {
   return num_edges < 0 ? -1 : dw_rows(num_edges);
 }
 
-extern "C" int64_t maloq_message_dw_partials_floats(int lmax, int mmax, int c_out, int c_in,
+extern "C" int64_t maloq_message_dw_partials_floats(int lmax, int mmax, int gate, int c_out, int c_in,
                                                     int splits) {
   DwArgs a{};
-  if (dw_setup(a, lmax, mmax, 0, c_out, c_in, splits, DW_T, 64)) return -1;
-  return a.goff[a.ngroups] * splits;
+  if (dw_setup(a, lmax, mmax, gate, 0, c_out, c_in, splits, DW_T, 64)) return -1;
+  int64_t n = a.goff[a.ngroups] * splits;
+  // the bf16 kernel's 256-wide tiles give the same group sizes (goff does not depend on the tile)
+  return n;
 }
 
-extern "C" int maloq_message_dw(int dtype, int lmax, int mmax, const void* dz, const void* y,
+extern "C" int maloq_message_dw(int dtype, int lmax, int mmax, int gate, const void* dz, const void* y,
                                 int64_t num_edges, int c_out, int c_in, int splits,
                                 float* partials, float* dw0, float* dw1, float* dw2, float* dw3,
                                 void* stream) {
@@ -423,14 +442,14 @@ extern "C" int maloq_message_dw(int dtype, int lmax, int mmax, const void* dz, c
   MALOQ_REQUIRE(num_edges >= 0, "num_edges < 0");
   MALOQ_REQUIRE(c_out > 0 && c_in > 0, "bad channels");
   DwArgs a{};
-  int rc = dw_setup(a, lmax, mmax, num_edges, c_out, c_in, splits, DW_T, 64);
+  int rc = dw_setup(a, lmax, mmax, gate, num_edges, c_out, c_in, splits, DW_T, 64);
   if (rc) return rc;
   // bf16 rows of at least one tile (a tile ending past a row's last column
   // reads into the next row): the transpose-read kernel; else dw_kernel.
   const bool tr = dtype == 1 && c_out % 8 == 0 && c_in % 8 == 0 &&
-                  static_cast<int64_t>(a.dp) * c_out >= trdw::T && static_cast<int64_t>(a.dp) * c_in >= trdw::T;
+                  static_cast<int64_t>(a.dpz) * c_out >= trdw::T && static_cast<int64_t>(a.dpy) * c_in >= trdw::T;
   if (tr) {
-    rc = dw_setup(a, lmax, mmax, num_edges, c_out, c_in, splits, trdw::T, trdw::CHUNK);
+    rc = dw_setup(a, lmax, mmax, gate, num_edges, c_out, c_in, splits, trdw::T, trdw::CHUNK);
     if (rc) return rc;
   }
   MALOQ_REQUIRE(partials && dw0, "null pointer");
@@ -453,11 +472,11 @@ extern "C" int maloq_message_dw(int dtype, int lmax, int mmax, const void* dz, c
   rc = check_launch("dw_kernel");
   if (rc) return rc;
   int64_t maxel = 0;
-  for (int g = 0; g <= mmax; ++g) {
-    const int64_t el = static_cast<int64_t>(a.rows[g]) * c_out * a.rows[g] * c_in;
+  for (int g = 0; g < a.ngroups; ++g) {
+    const int64_t el = static_cast<int64_t>(a.rowsz[g]) * c_out * a.rowsy[g] * c_in;
     maxel = el > maxel ? el : maxel;
   }
-  hipLaunchKernelGGL(dw_reduce_kernel, dim3(static_cast<unsigned>((maxel + 255) / 256), mmax + 1),
+  hipLaunchKernelGGL(dw_reduce_kernel, dim3(static_cast<unsigned>((maxel + 255) / 256), a.ngroups),
                      dim3(256), 0, s, a, lmax, dw0, dw1, dw2, dw3);
   return check_launch("dw_reduce_kernel");
 }

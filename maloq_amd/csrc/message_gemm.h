@@ -36,23 +36,33 @@
 namespace maloq {
 namespace msg {
 
-template <int L, int M, bool GATE, int NW, int RT>
+// MODE FWD: a gated block has one more output row type per degree l >= 1 (the
+// gate pre-activations); MODE BWD_DX: one more input row type per degree
+// l >= 1 (dL/dgate), whose products with the transposed gate weights add to
+// the m = 0 outputs.
+template <int L, int M, bool GATE, int NW, int RT, int MODE = 0>
 struct GPlan {
   static constexpr int TE = 32 * RT;
   static constexpr int NT = NW * 64;
   static_assert(TE <= 64, "segment masks are 64-bit");
-  static constexpr int gt(int l) { return (GATE && l >= 1) ? 1 : 0; }
+  static constexpr bool BWD = MODE != 0;
+  static constexpr int gt(int l) { return (GATE && !BWD && l >= 1) ? 1 : 0; }   // output gate row
+  static constexpr int gin(int l) { return (GATE && BWD && l >= 1) ? 1 : 0; }   // input gate row
   static constexpr int nq(int l) { return 1 + 2 * cmin(M, l); }
+  static constexpr int nqa(int l) { return nq(l) + gin(l); }  // A row types of input degree l
   static constexpr int ntype(int l) { return nq(l) + gt(l); }
   // accumulator type of row type q of degree l (0: m=0, [1: gate], then +1, -1, +2, ...)
   static constexpr int qtype(int q, int l) { return q == 0 ? 0 : q + gt(l); }
   static constexpr int DP = Plan<L, M, false, 4, 1>::DP;
+  static constexpr int DPA = DP + ((GATE && BWD) ? L : 0);  // A rows per edge
+  // A-source row of input row type q of degree l (gate rows follow the kept rows)
+  static constexpr int arow(int q, int l) { return q < nq(l) ? Plan<L, M, false, 4, 1>::mrow(q, l) : DP + l - 1; }
   static constexpr int mrow(int q, int l) { return Plan<L, M, false, 4, 1>::mrow(q, l); }
   static constexpr int doff(int l) { return Plan<L, M, false, 4, 1>::doff(l); }
   static constexpr int DS = Plan<L, M, false, 4, 1>::DS;
   // B fragments of one K step (kernel-input degree li), grouped by output degree lo:
   // g0, [gate], then (Wr, Wi) for m = 1 .. min(M, li, lo).
-  static constexpr int nbl(int li, int lo) { return 1 + gt(lo) + 2 * cmin(cmin(M, li), lo); }
+  static constexpr int nbl(int li, int lo) { return 1 + gt(lo) + gin(li) + 2 * cmin(cmin(M, li), lo); }
   static constexpr int bbase(int li, int lo) {
     int s = 0;
     for (int k = 0; k < lo; ++k) s += nbl(li, k);
@@ -62,7 +72,7 @@ struct GPlan {
   // MFMAs per row tile and K step summed over li: the schedule's weight of degree lo
   static constexpr int work(int lo) {
     int s = 0;
-    for (int li = 0; li <= L; ++li) s += 1 + gt(lo) + 4 * cmin(cmin(M, li), lo);
+    for (int li = 0; li <= L; ++li) s += 1 + gt(lo) + gin(li) + 4 * cmin(cmin(M, li), lo);
     return s;
   }
   struct Tab {
@@ -121,11 +131,11 @@ struct GPlan {
   static constexpr int WS = PairLayout<L, M>::WS;
   static constexpr int NW4 = (TE * WS / 4 + NT - 1) / NT;  // float4 copies per thread
   // LDS
-  static constexpr int A_BYTES = nq(L) * RT * FRAG;      // one A stage
+  static constexpr int A_BYTES = nqa(L) * RT * FRAG;     // one A stage
   static constexpr int CH = 16;                           // edges per epilogue chunk
   static constexpr int STG_BYTES = NW * CH * 64 * 4;      // epilogue staging
   static constexpr int U_BYTES = (2 * A_BYTES > STG_BYTES) ? 2 * A_BYTES : STG_BYTES;
-  static constexpr int NA = (nq(L) * RT * 64 + NT - 1) / NT;  // A chunks per thread
+  static constexpr int NA = (nqa(L) * RT * 64 + NT - 1) / NT;  // A chunks per thread
 };
 
 // One lane's 16 bytes of an MFMA operand fragment (a native vector, so that
@@ -146,7 +156,7 @@ __device__ __forceinline__ void mfma(f32x16& acc, frag_t a, frag_t b, F32) {
 
 template <int L, int M, bool GATE, int NW, int RT, class TM, int MODE>
 struct Gemm {
-  using P = GPlan<L, M, GATE, NW, RT>;
+  using P = GPlan<L, M, GATE, NW, RT, MODE>;
   static constexpr int TE = P::TE, NT = P::NT, KC = TM::KC;
   static_assert(NW == 4, "the epilogue staging holds two waves per A stage");
   static constexpr int d = (L + 1) * (L + 1);
@@ -175,7 +185,7 @@ struct Gemm {
   // vmcnt accounting exact); lanes of edges beyond the tile read the tile's
   // first edge, whose rows in those accumulator lanes are never stored.
   struct ATab {
-    int frag[NW][P::nq(L) * RT];
+    int frag[NW][P::nqa(L) * RT];
     int count[NW];
   };
   static constexpr ATab make_atab() {
@@ -189,7 +199,7 @@ struct Gemm {
           order[i] = order[j];
           order[j] = x;
         }
-    constexpr int F = P::nq(L) * RT;
+    constexpr int F = P::nqa(L) * RT;
     for (int f = 0; f < F; ++f) {
       int best = order[0];  // fewest staged so far, ties to the lighter wave
       for (int i = 1; i < NW; ++i) {
@@ -211,7 +221,7 @@ struct Gemm {
   template <int W, int k>
   static constexpr int afrag() { return atab.frag[W][k]; }
   template <int W, int k, int LI>
-  static constexpr bool avalid() { return k < atab.count[W] && afrag<W, k>() < P::nq(LI) * RT; }
+  static constexpr bool avalid() { return k < atab.count[W] && afrag<W, k>() < P::nqa(LI) * RT; }
 
   struct AState {
     int64_t ebase[NAW];  // element offset of (edge, row 0, channel half)
@@ -225,7 +235,7 @@ struct Gemm {
       constexpr int rt = afrag<W, k>() % RT;
       const int e = rt * 32 + (lane & 31);
       const int ei = s.eid[e] >= 0 ? s.eid[e] : s.eid[0];
-      st.ebase[k] = static_cast<int64_t>(ei) * P::DP * a.C_k + (lane >> 5) * TM::VEC;
+      st.ebase[k] = static_cast<int64_t>(ei) * P::DPA * a.C_k + (lane >> 5) * TM::VEC;
     });
   }
   // Direct global -> LDS copies of this wave's fragments of step (LI, ks):
@@ -239,7 +249,7 @@ struct Gemm {
         constexpr int q = afrag<W, k>() / RT;
 #if defined(__HIP_DEVICE_COMPILE__)  // the host pass does not know gfx950's 16-byte form
         __builtin_amdgcn_global_load_lds(
-            y + st.ebase[k] + static_cast<int64_t>(P::mrow(q, LI)) * a.C_k + ks * KC,
+            y + st.ebase[k] + static_cast<int64_t>(P::arow(q, LI)) * a.C_k + ks * KC,
             (lds_void*)(stage + afrag<W, k>() * FRAG), 16, 0, 0);
 #endif
       }
@@ -272,10 +282,12 @@ struct Gemm {
       af[rt] = *reinterpret_cast<const frag_t*>(A + (q * RT + rt) * FRAG + lane * 16);
     });
   }
-  // m = 0 (and gate) products of every owned degree.
+  // m = 0 (and gate) products of every owned degree: forward, the gate
+  // outputs from the m = 0 inputs; input gradient, the m = 0 outputs also
+  // from the gate-gradient inputs ag.
   template <int W, int LI>
   static __device__ __forceinline__ void mma_m0(f32x16 (&acc)[P::MSLOT], const frag_t (&a0)[RT],
-                                                const frag_t (&b)[P::NBW]) {
+                                                const frag_t (&ag)[RT], const frag_t (&b)[P::NBW]) {
     static_for<L + 1>([&](auto LO) {
       constexpr int lo = decltype(LO)::value;
       if constexpr (P::tab.owner[lo] == W) {
@@ -285,6 +297,7 @@ struct Gemm {
           constexpr int sb = P::tab.base[lo] + rt * P::ntype(lo);
           mfma(acc[sb], a0[rt], b[bo], TM{});
           if constexpr (P::gt(lo)) mfma(acc[sb + 1], a0[rt], b[bo + 1], TM{});
+          if constexpr (P::gin(LI)) mfma(acc[sb], ag[rt], b[bo + 1], TM{});
         });
       }
     });
@@ -298,7 +311,7 @@ struct Gemm {
     static_for<L + 1>([&](auto LO) {
       constexpr int lo = decltype(LO)::value;
       if constexpr (P::tab.owner[lo] == W && m <= lo) {
-        constexpr int bw = P::wboff(W, LI, lo) + 1 + P::gt(lo) + 2 * (m - 1);
+        constexpr int bw = P::wboff(W, LI, lo) + 1 + P::gt(lo) + P::gin(LI) + 2 * (m - 1);
         const frag_t wr = b[bw], wi = b[bw + 1];
         static_for<RT>([&](auto R) {
           constexpr int rt = decltype(R)::value;
@@ -341,8 +354,9 @@ struct Gemm {
                                                const char* wp, int64_t foff, int ks, int nks,
                                                int lane) {
     __syncthreads();
-    frag_t a0[RT];
+    frag_t a0[RT], ag[RT];
     read_q<0>(a0, rd, lane);
+    if constexpr (P::gin(LI)) read_q<P::nq(LI)>(ag, rd, lane);
     if constexpr (NXT == LI) {
       a_dma<W, LI>(st, wr, a, ks + 1);
       b_load<W, LI>(bn, wp, foff, ks + 1, lane);
@@ -352,7 +366,7 @@ struct Gemm {
     }
     // keep the next step's loads ahead of this step's MFMAs
     __builtin_amdgcn_sched_barrier(0);
-    mma_m0<W, LI>(acc, a0, bc);
+    mma_m0<W, LI>(acc, a0, ag, bc);
     static_for<M>([&](auto MI) {
       constexpr int m = decltype(MI)::value + 1;
       if constexpr (m <= LI) {
@@ -392,20 +406,65 @@ struct Gemm {
   }
 
   template <int lo>
-  static __device__ __forceinline__ void bias_gate(f32x16 (&acc)[P::MSLOT], const Args& a,
-                                                   int col) {
+  static __device__ __forceinline__ void add_bias(f32x16 (&acc)[P::MSLOT], const Args& a, int col) {
     static_for<RT>([&](auto RTI) {
       constexpr int sb = P::tab.base[lo] + decltype(RTI)::value * P::ntype(lo);
-      {  // branch-free: a runtime branch around accumulator updates costs spills
-        const float b0 = a.bias != nullptr ? a.bias[a.extra + lo * a.C_n + col] : 0.f;
+      // branch-free: a runtime branch around accumulator updates costs spills
+      const float b0 = a.bias != nullptr ? a.bias[a.extra + lo * a.C_n + col] : 0.f;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) acc[sb][i] += b0;
-        if constexpr (P::gt(lo)) {
-          const float bg = a.bias != nullptr ? a.bias[(lo - 1) * a.C_n + col] : 0.f;
+      for (int i = 0; i < 16; ++i) acc[sb][i] += b0;
+      if constexpr (P::gt(lo)) {
+        const float bg = a.bias != nullptr ? a.bias[(lo - 1) * a.C_n + col] : 0.f;
 #pragma unroll
-          for (int i = 0; i < 16; ++i) acc[sb + 1][i] += bg;
-        }
+        for (int i = 0; i < 16; ++i) acc[sb + 1][i] += bg;
       }
+    });
+  }
+
+  // Gated forward: the pre-activation rows of degree lo (kept rows and the gate
+  // row) to a.gsave [edge id][d' + L][C_n], each 32 x 32 block transposed
+  // through the wave's LDS tile so that a lane stores 16 channels of one edge.
+  template <int lo>
+  static __device__ __forceinline__ void save_pre(const f32x16 (&acc)[P::MSLOT], const Smem& s,
+                                                  const Args& a, int cb, float* tb, int lane) {
+    const int co = lane & 31, h = lane >> 5;
+    static_for<RT>([&](auto RTI) {
+      constexpr int rt = decltype(RTI)::value;
+      constexpr int sb = P::tab.base[lo] + rt * P::ntype(lo);
+      const int ei = s.eid[rt * 32 + co];
+      typename TM::raw* g = reinterpret_cast<typename TM::raw*>(a.gsave) +
+                            static_cast<int64_t>(ei >= 0 ? ei : 0) * (P::DP + L) * a.C_n + cb * CB + 16 * h;
+      static_for<P::ntype(lo)>([&](auto TI) {
+        constexpr int t = decltype(TI)::value;  // accumulator type: 0, [gate], +1, -1, ...
+        constexpr int row = (P::gt(lo) && t == 1) ? P::DP + lo - 1
+                                                  : P::mrow(t == 0 ? 0 : t - P::gt(lo), lo);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) tb[tsw(8 * (i >> 2) + 4 * h + (i & 3), co)] = acc[sb + t][i];
+        wave_sync();
+        if (ei >= 0) {
+          float v[16];
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const float4 t4 = *reinterpret_cast<const float4*>(tb + tsw(co, 16 * h + 4 * g4));
+            v[4 * g4] = t4.x; v[4 * g4 + 1] = t4.y; v[4 * g4 + 2] = t4.z; v[4 * g4 + 3] = t4.w;
+          }
+          float w8[8];
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) w8[k] = v[8 * half + k];
+            store_vec<TM, 8>(g + static_cast<int64_t>(row) * a.C_n + 8 * half, w8);
+          }
+        }
+        wave_sync();
+      });
+    });
+  }
+
+  template <int lo>
+  static __device__ __forceinline__ void gate_act(f32x16 (&acc)[P::MSLOT]) {
+    static_for<RT>([&](auto RTI) {
+      constexpr int sb = P::tab.base[lo] + decltype(RTI)::value * P::ntype(lo);
       if constexpr (GATE) {
         if constexpr (lo == 0) {
 #pragma unroll
@@ -607,9 +666,15 @@ struct Gemm {
     static_for<L + 1>([&](auto LO) {
       constexpr int lo = decltype(LO)::value;
       if constexpr (P::tab.owner[lo] == W) {
-        if constexpr (MODE == FWD)
-          bias_gate<lo>(acc, a, col);
-        else if constexpr (RAD)
+        if constexpr (MODE == FWD) {
+          add_bias<lo>(acc, a, col);
+          if constexpr (GATE) {
+            if (a.gsave != nullptr)
+              save_pre<lo>(acc, s, a, cb,
+                           reinterpret_cast<float*>((wave < 2 ? st0 : st1) + (wave & 1) * PW), lane);
+            gate_act<lo>(acc);
+          }
+        } else if constexpr (RAD)
           radial<lo>(acc, s, a, cb,
                      reinterpret_cast<float*>((wave < 2 ? st0 : st1) + (wave & 1) * PW), lane);
         rotate_sum<W, lo>(acc, s, a, cb,

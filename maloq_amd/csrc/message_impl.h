@@ -175,6 +175,8 @@ struct Args {
   int extra;              // FWD: leading gate columns of W0 (= L * C_n if gated)
   int64_t ntiles;
   int64_t frags_per_cb;   // packed fragments per output-channel block
+  void* gsave;            // FWD gated: [E_all, d' + L, C_n] (TM raw) pre-activation rows and
+                          // gate rows, nullable; BWD_DX gated: a_src has d' + L rows
 };
 
 template <int L, int M>
@@ -232,6 +234,9 @@ struct PrepArgs {
   int build_d;          // 1: compute and write dk; 0: read dk
   int64_t E;
   int C;
+  const void* gsave;    // gated input gradient: the forward's pre-activation rows
+                        // [E_all, d' + L, C] (TM raw); y then gets d' + L rows per edge:
+                        // dL/dpre of the kept rows, then dL/dgate of degrees 1..L
 };
 
 template <class TX, int V>
@@ -351,6 +356,73 @@ struct Prep {
     }
   }
 
+  // Gated input gradient (GateActivation backward, activation.py:57-77): with
+  // o the rotated output gradient and z the saved pre-activations,
+  //   l = 0:  dpre = o SiLU'(z) = o s (1 + z (1 - s)),  s = sigmoid(z);
+  //   l >= 1: t = tanh(z_gate[l]); dpre_q = o_q t;  dgate[l] = (1 - t^2) sum_q o_q z_q.
+  static __device__ void run_gated_bwd(const Smem& s, const PrepArgs& a, int nvalid, int tid) {
+    constexpr int DG = P::DP + L;  // rows per edge of the saved and written arrays
+    const int nch = a.C / V;
+    for (int u = tid; u < nvalid * nch; u += NT) {
+      const int e = u / nch, c0 = (u - e * nch) * V;
+      const int64_t eid = s.eid[e];
+      const typename TX::raw* xg = reinterpret_cast<const typename TX::raw*>(a.x) +
+                                   static_cast<int64_t>(s.gid[e]) * d * a.C + c0;
+      typename TM::raw* yo = reinterpret_cast<typename TM::raw*>(a.y) + eid * DG * a.C + c0;
+      const typename TM::raw* zs = reinterpret_cast<const typename TM::raw*>(a.gsave) + eid * DG * a.C + c0;
+      static_for<L + 1>([&](auto LI) {
+        constexpr int l = decltype(LI)::value;
+        constexpr int n = 2 * l + 1;
+        float xv[n][V];
+#pragma unroll
+        for (int j = 0; j < n; ++j) load_vec<TX, V>(xg + (l * l + j) * a.C, xv[j]);
+        const float* Dl = s.D + e * WS;
+        float o[P::nq(l)][V];
+#pragma unroll
+        for (int q = 0; q < P::nq(l); ++q)
+#pragma unroll
+          for (int c = 0; c < V; ++c) {
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 0; j < n; ++j) acc = fmaf(Dl[PL::at(l, q, j)], xv[j][c], acc);
+            o[q][c] = acc;
+          }
+        if constexpr (l == 0) {
+          float z[V];
+          load_vec<TM, V>(zs + static_cast<int64_t>(P::mrow(0, 0)) * a.C, z);
+#pragma unroll
+          for (int c = 0; c < V; ++c) {
+            const float sg = 1.0f / (1.0f + expf(-z[c]));
+            o[0][c] *= sg * (1.0f + z[c] * (1.0f - sg));
+          }
+          store_vec<TM, V>(yo + static_cast<int64_t>(P::mrow(0, 0)) * a.C, o[0]);
+        } else {
+          float t[V], dg[V];
+          load_vec<TM, V>(zs + static_cast<int64_t>(P::DP + l - 1) * a.C, t);
+#pragma unroll
+          for (int c = 0; c < V; ++c) {
+            t[c] = tanhf(t[c]);
+            dg[c] = 0.f;
+          }
+#pragma unroll
+          for (int q = 0; q < P::nq(l); ++q) {
+            float z[V];
+            load_vec<TM, V>(zs + static_cast<int64_t>(P::mrow(q, l)) * a.C, z);
+#pragma unroll
+            for (int c = 0; c < V; ++c) {
+              dg[c] = fmaf(o[q][c], z[c], dg[c]);
+              o[q][c] *= t[c];
+            }
+            store_vec<TM, V>(yo + static_cast<int64_t>(P::mrow(q, l)) * a.C, o[q]);
+          }
+#pragma unroll
+          for (int c = 0; c < V; ++c) dg[c] *= (1.0f - t[c] * t[c]);
+          store_vec<TM, V>(yo + static_cast<int64_t>(P::DP + l - 1) * a.C, dg);
+        }
+      });
+    }
+  }
+
   static __device__ void run(const PrepArgs& a) {
     __shared__ Smem s;
     const int tid = threadIdx.x;
@@ -389,6 +461,10 @@ struct Prep {
     }
     const int nch = a.C / V;
     const int64_t rw = rad_width<L, M>(a.C);
+    if (a.gsave != nullptr) {
+      run_gated_bwd(s, a, nvalid, tid);
+      return;
+    }
     for (int u = tid; u < nvalid * nch; u += NT) {
       const int e = u / nch, c0 = (u - e * nch) * V;
       const int64_t eid = s.eid[e];

@@ -54,9 +54,9 @@ int launch_lm(int dtype, int gate, int mode, const Args& a, hipStream_t s) {
       return gate ? launch<L, M, true, BF16, BF16, FWD>(a, s) : launch<L, M, false, BF16, BF16, FWD>(a, s);
     return gate ? launch<L, M, true, F32, F32, FWD>(a, s) : launch<L, M, false, F32, F32, FWD>(a, s);
   }
-  MALOQ_REQUIRE(!gate, "gated backward is not implemented");
-  if (dtype == 1) return launch<L, M, false, BF16, BF16, BWD_DX>(a, s);
-  return launch<L, M, false, F32, F32, BWD_DX>(a, s);
+  if (dtype == 1)
+    return gate ? launch<L, M, true, BF16, BF16, BWD_DX>(a, s) : launch<L, M, false, BF16, BF16, BWD_DX>(a, s);
+  return gate ? launch<L, M, true, F32, F32, BWD_DX>(a, s) : launch<L, M, false, F32, F32, BWD_DX>(a, s);
 }
 
 // Edge prep: mode FWD gathers x (dtype) and applies rad; mode BWD_DX gathers

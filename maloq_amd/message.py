@@ -68,14 +68,17 @@ class MessagePlan:
 
 
 # ------------------------------------------------------------ weight packing
-def _frag_list(lmax, mmax, gate, l_k):
+def _frag_list(lmax, mmax, gate, l_k, gate_in=False):
     """B fragments of one K step at kernel-input degree l_k, grouped by kernel-
     output degree l_n: g0, [gate], then (Wr, Wi) for m = 1 .. min(mmax, l_k, l_n).
-    Wr and Wi are stored once; the kernel forms the complex mix (and -Wi)."""
+    Wr and Wi are stored once; the kernel forms the complex mix (and -Wi).
+    The gate fragment: forward (``gate``) for output degrees l_n >= 1; input
+    gradient (``gate_in``) for input degrees l_k >= 1 (the transposed gate
+    weights act on dL/dgate rows and add to the m = 0 outputs)."""
     out = []
     for l_n in range(lmax + 1):
         out.append(("g0", 0, l_n))
-        if gate and l_n >= 1:
+        if (gate and l_n >= 1) or (gate_in and l_k >= 1):
             out.append(("gate", 0, l_n))
         for m in range(1, min(mmax, l_k, l_n) + 1):
             out += [("wr", m, l_n), ("wi", m, l_n)]
@@ -113,7 +116,7 @@ def _pack_index(dtype_code, lmax, mmax, gate, c_in, c_out, mode):
     per_cb = []  # list over l_k of [cb, ks, frag, element]
     for l_k in range(lmax + 1):
         frags = []
-        for kind, m, l_n in _frag_list(lmax, mmax, gate and mode == 0, l_k):
+        for kind, m, l_n in _frag_list(lmax, mmax, gate and mode == 0, l_k, gate_in=gate and mode == 1):
             if mode == 0:
                 c, co, l_in, l_out = ck, cn, l_k, l_n
             else:
@@ -151,7 +154,7 @@ def pack_weights(w0, wm, lmax, mmax, gate, c_in, c_out, dtype, mode=0):
         flat = torch.cat([w0.reshape(-1)] + [w.reshape(-1) for w in wm[:mmax]]).float()
         assert flat.numel() == total, "weight shapes do not match (lmax, mmax, channels)"
         packed = flat[idx].to(dtype)
-    want = _lib.load().maloq_message_wpack_bytes(code, lmax, mmax, int(bool(gate and mode == 0)),
+    want = _lib.load().maloq_message_wpack_bytes(code, lmax, mmax, int(bool(gate)),
                                                 c_in if mode == 0 else c_out,
                                                 c_out if mode == 0 else c_in)
     assert packed.numel() * packed.element_size() == want, (packed.numel(), want)
@@ -198,7 +201,8 @@ def message_forward(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=False, wp
 
     ``save``: dict that receives the workspaces kept for the backward
     ("y" rotated scaled rows, "r" unscaled rows if ``rad`` is given, "dk" the
-    kept Wigner-D rows), all indexed by dst-sorted edge position."""
+    kept Wigner-D rows, and for a gated block "g" the pre-activation rows
+    [E, d' + lmax, c_out]), all indexed by dst-sorted edge position."""
     dt = x.dtype
     if dt not in DTYPE_CODE:
         raise ValueError(f"unsupported dtype {dt}")
@@ -222,6 +226,8 @@ def message_forward(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=False, wp
     r = torch.empty(max(E, 1), kept_rows(lmax, mmax), c_in, device=dev, dtype=dt) \
         if (save is not None and rad is not None) else None
     dk = torch.empty(max(E, 1), wigner_floats(lmax, mmax), device=dev, dtype=torch.float32)
+    gws = torch.empty(max(E, 1), kept_rows(lmax, mmax) + lmax, c_out, device=dev, dtype=dt) \
+        if (save is not None and gate) else None
     bias = b0.float().contiguous() if b0 is not None else None
     xc = x.contiguous()
     eul = eulers.float().contiguous()
@@ -229,46 +235,51 @@ def message_forward(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=False, wp
               _lib.ptr(plan.src), _lib.ptr(plan.dst), E, _lib.ptr(eul), _lib.ptr(rad),
               _lib.ptr(wpack), _lib.ptr(bias), _lib.ptr(_jd_dev(lmax, dev)), _lib.ptr(out),
               plan.num_nodes, c_out, _lib.ptr(plan.seg_ptr), _lib.ptr(parts), _lib.ptr(y),
-              _lib.ptr(r), _lib.ptr(dk), _lib.stream_of(dev))
+              _lib.ptr(r), _lib.ptr(dk), _lib.ptr(gws), _lib.stream_of(dev))
     if save is not None:
-        save.update(y=y, r=r, dk=dk)
+        save.update(y=y, r=r, dk=dk, g=gws)
     return out
 
 
 def message_backward_dx(grad_out, x_shape, dt, plan, saved, rad, w0, wm, lmax, mmax,
-                        wpack_t=None, need_rad_grad=True):
-    """(grad_x fp32 [N, d, c_in], grad_rad or None, dz [E, d', c_out]) of the
-    ungated block, from the forward's saved workspaces."""
+                        wpack_t=None, need_rad_grad=True, gate=False):
+    """(grad_x fp32 [N, d, c_in], grad_rad or None, dz [E, d' (+ lmax if gated),
+    c_out]) of the block, from the forward's saved workspaces (for a gated
+    block ``saved["g"]``, the pre-activation rows)."""
     N, d, c_in = x_shape
     c_out = grad_out.shape[2]
     dev = grad_out.device
     if wpack_t is None:
-        wpack_t = pack_weights(w0, wm, lmax, mmax, False, c_in, c_out, dt, 1)
+        wpack_t = pack_weights(w0, wm, lmax, mmax, gate, c_in, c_out, dt, 1)
     E = plan.num_edges
     gx = torch.empty(N, d, c_in, device=dev, dtype=torch.float32)
     lib = _lib.load()
-    parts = torch.empty(max(1, lib.maloq_message_partials_floats(lmax, 0, E, c_in)),
+    parts = torch.empty(max(1, lib.maloq_message_partials_floats(lmax, int(gate), E, c_in)),
                         device=dev, dtype=torch.float32)
     grad_rad = None
     if rad is not None:
         rad = rad.to(dt).contiguous()
         if need_rad_grad:
             grad_rad = torch.empty_like(rad)
-    dz = _edge_rows(E, kept_rows(lmax, mmax), c_out, dev, dt)
+    dz = _edge_rows(E, kept_rows(lmax, mmax) + (lmax if gate else 0), c_out, dev, dt)
     g = grad_out.float().contiguous()
-    _lib.call("maloq_message_bwd_dx", DTYPE_CODE[dt], lmax, mmax, _lib.ptr(g), c_out,
+    gs = saved.get("g") if gate else None
+    if gate:
+        assert gs is not None, "the gated backward needs the forward's pre-activation rows"
+    _lib.call("maloq_message_bwd_dx", DTYPE_CODE[dt], lmax, mmax, int(gate), _lib.ptr(g), c_out,
               _lib.ptr(plan.bwd_dst), _lib.ptr(plan.bwd_src), _lib.ptr(plan.bwd_eidx), E,
               _lib.ptr(saved["dk"]), _lib.ptr(rad), _lib.ptr(grad_rad), _lib.ptr(saved.get("r")),
               _lib.ptr(wpack_t), _lib.ptr(_jd_dev(lmax, dev)), _lib.ptr(gx), N, c_in,
-              _lib.ptr(plan.seg_ptr_src), _lib.ptr(parts), _lib.ptr(dz), _lib.stream_of(dev))
+              _lib.ptr(plan.seg_ptr_src), _lib.ptr(parts), _lib.ptr(dz), _lib.ptr(gs), _lib.stream_of(dev))
     return gx, grad_rad, dz
 
 
-def message_weight_grad(dz, y, lmax, mmax, c_out, c_in, splits=None, num_edges=None):
-    """(dW0 [(L+1) c_out, (L+1) c_in], [dW_m [2 (L-m+1) c_out, (L-m+1) c_in]], db0)
-    in fp32 from the saved rows (deterministic split-K over edges).  ``dz`` and
-    ``y`` are the forward/backward workspaces: for bf16 they carry the zeroed
-    padding rows of ``maloq_message_edge_rows(num_edges)``."""
+def message_weight_grad(dz, y, lmax, mmax, c_out, c_in, splits=None, num_edges=None, gate=False):
+    """(dW0 [(L if gated) c_out + (L+1) c_out, (L+1) c_in], [dW_m [2 (L-m+1) c_out,
+    (L-m+1) c_in]], db0) in fp32 from the saved rows (deterministic split-K over
+    edges).  ``dz`` and ``y`` are the forward/backward workspaces: for bf16 they
+    carry the zeroed padding rows of ``maloq_message_edge_rows(num_edges)``; a
+    gated ``dz`` carries the dL/dgate rows after the kept rows."""
     E = int(dz.shape[0] if num_edges is None else num_edges)
     if dz.dtype == torch.bfloat16:
         assert dz.shape[0] >= _lib.load().maloq_message_edge_rows(E) and y.shape[0] == dz.shape[0], \
@@ -285,59 +296,64 @@ def message_weight_grad(dz, y, lmax, mmax, c_out, c_in, splits=None, num_edges=N
                          for r in [lmax + 1] + [2 * (lmax - m + 1) for m in range(1, mmax + 1)])
             splits = max(1, min(16, round(640 / ntiles), E // 1024))
     lib = _lib.load()
-    parts = torch.empty(max(1, lib.maloq_message_dw_partials_floats(lmax, mmax, c_out, c_in, splits)),
+    parts = torch.empty(max(1, lib.maloq_message_dw_partials_floats(lmax, mmax, int(gate), c_out, c_in,
+                                                                    splits)),
                         device=dz.device, dtype=torch.float32)
-    dw0 = torch.empty((lmax + 1) * c_out, (lmax + 1) * c_in, device=dz.device, dtype=torch.float32)
+    extra = lmax * c_out if gate else 0
+    dw0 = torch.empty(extra + (lmax + 1) * c_out, (lmax + 1) * c_in, device=dz.device, dtype=torch.float32)
     dwm = [torch.empty(2 * (lmax - m + 1) * c_out, (lmax - m + 1) * c_in, device=dz.device,
                        dtype=torch.float32) for m in range(1, mmax + 1)]
     ptrs = [_lib.ptr(w) for w in dwm] + [None] * (3 - len(dwm))
-    _lib.call("maloq_message_dw", DTYPE_CODE[dz.dtype], lmax, mmax, _lib.ptr(dz), _lib.ptr(y), E,
+    _lib.call("maloq_message_dw", DTYPE_CODE[dz.dtype], lmax, mmax, int(gate), _lib.ptr(dz), _lib.ptr(y), E,
               c_out, c_in, splits, _lib.ptr(parts), _lib.ptr(dw0), ptrs[0], ptrs[1], ptrs[2],
               _lib.stream_of(dz.device))
     db0 = dz[:E, : lmax + 1, :].float().sum(0).reshape(-1)
+    if gate:
+        kept = kept_rows(lmax, mmax)
+        db0 = torch.cat([dz[:E, kept: kept + lmax, :].float().sum(0).reshape(-1), db0])
     return dw0, dwm, db0
 
 
 class _MessageBlockFn(torch.autograd.Function):
-    """Autograd wrapper: gradients for x, rad, W0, b0, W_m (ungated block)."""
+    """Autograd wrapper: gradients for x, rad, W0, b0, W_m (gated or not)."""
 
     @staticmethod
-    def forward(ctx, x, rad, w0, b0, plan, eulers, lmax, mmax, *wm):
+    def forward(ctx, x, rad, w0, b0, plan, eulers, lmax, mmax, gate, *wm):
         saved = {}
-        out = message_forward(x, plan, eulers, rad, w0, b0, list(wm), lmax, mmax, gate=False, save=saved)
-        ctx.plan, ctx.lmax, ctx.mmax, ctx.has_b0 = plan, lmax, mmax, b0 is not None
+        out = message_forward(x, plan, eulers, rad, w0, b0, list(wm), lmax, mmax, gate=gate, save=saved)
+        ctx.plan, ctx.lmax, ctx.mmax, ctx.gate, ctx.has_b0 = plan, lmax, mmax, gate, b0 is not None
         ctx.x_shape, ctx.dt = tuple(x.shape), x.dtype
         ctx.has_r = saved["r"] is not None
-        ctx.save_for_backward(rad, w0, saved["y"], saved["dk"], saved["r"] if ctx.has_r else None, *wm)
+        ctx.save_for_backward(rad, w0, saved["y"], saved["dk"], saved["r"] if ctx.has_r else None,
+                              saved["g"], *wm)
         return out
 
     @staticmethod
     def backward(ctx, g):
-        rad, w0, y, dk, r, *wm = ctx.saved_tensors
-        plan, lmax, mmax = ctx.plan, ctx.lmax, ctx.mmax
-        gx, grad_rad, dz = message_backward_dx(g, ctx.x_shape, ctx.dt, plan, {"dk": dk, "r": r}, rad, w0,
-                                               wm, lmax, mmax, need_rad_grad=ctx.needs_input_grad[1])
-        need_w = ctx.needs_input_grad[2] or ctx.needs_input_grad[3] or any(ctx.needs_input_grad[8:])
+        rad, w0, y, dk, r, gs, *wm = ctx.saved_tensors
+        plan, lmax, mmax, gate = ctx.plan, ctx.lmax, ctx.mmax, ctx.gate
+        gx, grad_rad, dz = message_backward_dx(g, ctx.x_shape, ctx.dt, plan, {"dk": dk, "r": r, "g": gs}, rad,
+                                               w0, wm, lmax, mmax, need_rad_grad=ctx.needs_input_grad[1],
+                                               gate=gate)
+        need_w = ctx.needs_input_grad[2] or ctx.needs_input_grad[3] or any(ctx.needs_input_grad[9:])
         dw0 = db0 = None
         dwm = [None] * len(wm)
         if need_w and plan.num_edges > 0:
             dw0, dwm, db0 = message_weight_grad(dz, y, lmax, mmax, g.shape[2], ctx.x_shape[2],
-                                                num_edges=plan.num_edges)
+                                                num_edges=plan.num_edges, gate=gate)
             dw0 = dw0.to(w0.dtype)
             dwm = [d.to(w.dtype) for d, w in zip(dwm, wm)]
             db0 = db0 if ctx.has_b0 else None
         elif need_w:
             dw0 = torch.zeros_like(w0)
             dwm = [torch.zeros_like(w) for w in wm]
-            db0 = torch.zeros((lmax + 1) * g.shape[2], device=g.device) if ctx.has_b0 else None
+            nb = (lmax + 1 + (lmax if gate else 0)) * g.shape[2]
+            db0 = torch.zeros(nb, device=g.device) if ctx.has_b0 else None
         return (gx.to(ctx.dt) if ctx.needs_input_grad[0] else None, grad_rad, dw0, db0, None, None,
-                None, None, *dwm)
+                None, None, None, *dwm)
 
 
 def message_block(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=False):
-    """Differentiable fused block.  Gated blocks are forward-only for now."""
-    if gate:
-        if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in [x, rad, w0, b0, *wm]):
-            raise NotImplementedError("the gated fused block has no backward yet")
-        return message_forward(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=True)
-    return _MessageBlockFn.apply(x, rad, w0, b0, plan, eulers, lmax, mmax, *wm[:mmax])
+    """Differentiable fused block (gated with GateActivation, activation.py:12-77,
+    when ``gate``: w0 and b0 then carry the lmax c_out gate rows first)."""
+    return _MessageBlockFn.apply(x, rad, w0, b0, plan, eulers, lmax, mmax, bool(gate), *wm[:mmax])

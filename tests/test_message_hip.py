@@ -143,18 +143,20 @@ def test_config2_scale_against_oracle_subset(device):
 
 @pytest.mark.parametrize("lmax,mmax", [(2, 2), (4, 2), (6, 2)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_backward_matches_oracle_autograd(lmax, mmax, dtype, device):
-    """Gradients of x, rad, W0, b0 and W_m against fp64 autograd through the oracle."""
+@pytest.mark.parametrize("gate", [False, True])
+def test_backward_matches_oracle_autograd(lmax, mmax, dtype, gate, device):
+    """Gradients of x, rad, W0, b0 and W_m against fp64 autograd through the
+    oracle; gated blocks (GateActivation, activation.py:57-77) included."""
     from maloq_amd import message as M
     from maloq_amd.wigner import extract_euler_angles
-    print(f"bwd case lmax={lmax} dtype={dtype}", flush=True)
-    gen = torch.Generator().manual_seed(100 + lmax)
+    print(f"bwd case lmax={lmax} dtype={dtype} gate={gate}", flush=True)
+    gen = torch.Generator().manual_seed(100 + lmax + 7 * int(gate))
     N, E, c_in, c_out = 30, 300, 32, 32
     d = (lmax + 1) ** 2
     q = (lambda t: t.to(dtype).double()) if dtype == torch.bfloat16 else (lambda t: t.float().double())
     x = q(torch.randn(N, d, c_in, generator=gen, dtype=torch.float64))
     ei = _graph(N, E, gen)
-    conv = _conv(lmax, mmax, c_in, c_out, gen, False)
+    conv = _conv(lmax, mmax, c_in, c_out, gen, gate)
     conv = {"w0": q(conv["w0"]), "b0": conv["b0"].float().double(), "wm": [q(w) for w in conv["wm"]], "c_out": c_out}
     rad = q(torch.rand(E, M.rad_width(lmax, mmax, c_in), generator=gen, dtype=torch.float64) + 0.5)
     gout = torch.randn(N, d, c_out, generator=gen, dtype=torch.float64)
@@ -164,14 +166,15 @@ def test_backward_matches_oracle_autograd(lmax, mmax, dtype, device):
     leaves = [x.clone().requires_grad_(), rad.clone().requires_grad_(), conv["w0"].clone().requires_grad_(),
               conv["b0"].clone().requires_grad_()] + [w.clone().requires_grad_() for w in conv["wm"]]
     ref = omsg.message_block(leaves[0], ei, (e64[:, 0], e64[:, 1], e64[:, 2]), orot.load_jd(), lmax, mmax,
-                             {"w0": leaves[2], "b0": leaves[3], "wm": leaves[4:], "c_out": c_out}, rad=leaves[1])
+                             {"w0": leaves[2], "b0": leaves[3], "wm": leaves[4:], "c_out": c_out}, rad=leaves[1],
+                             gate=gate)
     (ref * gout).sum().backward()
     plan = M.MessagePlan(ei.to(device), N)
     dl = [x.to(device=device, dtype=dtype).requires_grad_(),
           plan.sort_edges(rad.to(device=device, dtype=dtype)).requires_grad_(),
           conv["w0"].to(device).float().requires_grad_(), conv["b0"].to(device).float().requires_grad_()] + \
          [w.to(device).float().requires_grad_() for w in conv["wm"]]
-    out = M.message_block(dl[0], plan, plan.sort_edges(eul), dl[1], dl[2], dl[3], dl[4:], lmax, mmax)
+    out = M.message_block(dl[0], plan, plan.sort_edges(eul), dl[1], dl[2], dl[3], dl[4:], lmax, mmax, gate=gate)
     out.backward(gout.float().to(device))
     tol = 1e-4 if dtype == torch.float32 else 3e-2
     inv = torch.empty_like(plan.perm)

@@ -33,8 +33,9 @@ def _decode(dtype_code):
     return fe, k, lane % 32
 
 
-def _model(packed, dtype_code, lmax, mmax, gate, c_k, c_n, rows, mode):
-    """Kernel-order GEMM: rows [E, d', c_k] m-major -> [E, d' (+gate), c_n]."""
+def _model(packed, dtype_code, lmax, mmax, gate, c_k, c_n, rows, mode, grows=None):
+    """Kernel-order GEMM: rows [E, d', c_k] m-major -> [E, d' (+gate), c_n].
+    Transposed gated mode: grows [E, lmax, c_k] are the dL/dgate input rows."""
     fe, k_of, n_of = _decode(dtype_code)
     kc = 16 if dtype_code == 1 else 8
     E = rows.shape[0]
@@ -52,7 +53,7 @@ def _model(packed, dtype_code, lmax, mmax, gate, c_k, c_n, rows, mode):
     pos = 0
     for cb in range(c_n // 32):
         for l_k in range(lmax + 1):
-            flist = M._frag_list(lmax, mmax, gate and mode == 0, l_k)
+            flist = M._frag_list(lmax, mmax, gate and mode == 0, l_k, gate_in=gate and mode == 1)
             for ks in range(c_k // kc):
                 B = {}
                 for kind, m, l_n in flist:
@@ -65,8 +66,10 @@ def _model(packed, dtype_code, lmax, mmax, gate, c_k, c_n, rows, mode):
                 for (kind, m, l_n), blk in B.items():
                     if kind == "g0":
                         out[:, mrow(0, l_n), ns] += rows[:, mrow(0, l_k), cs] @ blk
-                    elif kind == "gate":
+                    elif kind == "gate" and mode == 0:
                         gate_out[:, l_n - 1, ns] += rows[:, mrow(0, l_k), cs] @ blk
+                    elif kind == "gate":
+                        out[:, mrow(0, l_n), ns] += grows[:, l_k - 1, cs] @ blk
                     elif kind == "wr":
                         wr, wi = blk, B[("wi", m, l_n)]
                         ap = rows[:, mrow(2 * m - 1, l_k), cs]
@@ -138,3 +141,25 @@ def test_packed_size_matches_library():
             c_k, c_n = (c_in, c_out) if mode == 0 else (c_out, c_in)
             want = lib.maloq_message_wpack_bytes(code, lmax, mmax, int(gate), c_k, c_n)
             assert idx.size * (2 if code == 1 else 4) == want
+
+
+@pytest.mark.parametrize("dtype_code", [0, 1])
+@pytest.mark.parametrize("lmax,mmax", [(2, 2), (4, 2)])
+def test_transposed_gated_packing_matches_autograd(dtype_code, lmax, mmax):
+    """Input gradient of a gated SO(2) convolution with respect to its input,
+    given dL/dy (kept rows) and dL/dgate: the kernel's transposed walk over the
+    packed gate and SO(2) weights equals fp64 autograd."""
+    gen = torch.Generator().manual_seed(70 + lmax)
+    c_in, c_out, E = 64, 32, 4
+    w0, wm = _weights(lmax, mmax, c_in, c_out, True, gen)
+    idx, total = M._pack_index(dtype_code, lmax, mmax, True, c_in, c_out, 1)
+    packed = torch.cat([w0.reshape(-1)] + [w.reshape(-1) for w in wm]).numpy()[idx]
+    m_size = [lmax - m + 1 for m in range(mmax + 1)]
+    x = torch.randn(E, M.kept_rows(lmax, mmax), c_in, generator=gen, dtype=torch.float64, requires_grad=True)
+    dy = torch.randn(E, M.kept_rows(lmax, mmax), c_out, generator=gen, dtype=torch.float64)
+    dg = torch.randn(E, lmax * c_out, generator=gen, dtype=torch.float64)
+    y, g = oso2.so2_convolution(x, None, w0, None, wm, m_size, c_out, extra=lmax * c_out)
+    ((y * dy).sum() + (g * dg).sum()).backward()
+    got, _ = _model(packed, dtype_code, lmax, mmax, True, c_out, c_in, dy.numpy(), 1,
+                    grows=dg.reshape(E, lmax, c_out).numpy())
+    np.testing.assert_allclose(got, x.grad.numpy(), rtol=0, atol=1e-12)
