@@ -180,7 +180,7 @@ struct Args {
 };
 
 template <int L, int M>
-__device__ __forceinline__ int rad_slot(int q, int l, int c, int C) {
+__host__ __device__ constexpr int rad_slot(int q, int l, int c, int C) {
   // q: row type; m = (q + 1) / 2; slot = sum_{m' < m} (L - m' + 1) C + (l - m) C + c
   const int m = (q + 1) >> 1;
   int off = 0;
@@ -270,6 +270,23 @@ __device__ __forceinline__ void load_vec<F32, 4>(const float* p, float (&o)[4]) 
   o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
 }
 
+// V elements (16 bytes of TM raw) already in registers -> fp32.
+template <class TM, int V>
+__device__ __forceinline__ void unpack_vec(uint4 v, float (&o)[V]);
+template <>
+__device__ __forceinline__ void unpack_vec<BF16, 8>(uint4 v, float (&o)[8]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    o[2 * k] = __uint_as_float(w[k] << 16);
+    o[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+  }
+}
+template <>
+__device__ __forceinline__ void unpack_vec<F32, 4>(uint4 v, float (&o)[4]) {
+  o[0] = __uint_as_float(v.x); o[1] = __uint_as_float(v.y); o[2] = __uint_as_float(v.z); o[3] = __uint_as_float(v.w);
+}
+
 template <class TM, int V>
 __device__ __forceinline__ void store_vec(typename TM::raw* p, const float (&v)[V]);
 template <>
@@ -291,7 +308,7 @@ __device__ __forceinline__ void store_vec<F32, 4>(float* p, const float (&v)[4])
   *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
-template <int L, int M, class TM, class TX>
+template <int L, int M, class TM, class TX, bool GATED = false>
 struct Prep {
   static constexpr int TE = 32;
   static constexpr int NT = 256;
@@ -461,7 +478,7 @@ struct Prep {
     }
     const int nch = a.C / V;
     const int64_t rw = rad_width<L, M>(a.C);
-    if (a.gsave != nullptr) {
+    if constexpr (GATED) {  // its own instantiation: the common path keeps its register budget
       run_gated_bwd(s, a, nvalid, tid);
       return;
     }
@@ -473,6 +490,14 @@ struct Prep {
       typename TM::raw* yo = reinterpret_cast<typename TM::raw*>(a.y) + eid * P::DP * a.C + c0;
       typename TM::raw* ro = a.r ? reinterpret_cast<typename TM::raw*>(a.r) + eid * P::DP * a.C + c0 : nullptr;
       const typename TM::raw* rp = a.rad ? reinterpret_cast<const typename TM::raw*>(a.rad) + eid * rw + c0 : nullptr;
+      // all radial slots of this (edge, channel chunk) in flight at once: one
+      // memory latency per item instead of one per kept row
+      constexpr int NSLOT = rad_slot<L, M>(2 * M, L, 0, 1) + 1;  // sum_m (L - m + 1)
+      uint4 rr[NSLOT];
+      if (rp) {
+#pragma unroll
+        for (int k = 0; k < NSLOT; ++k) rr[k] = *reinterpret_cast<const uint4*>(rp + static_cast<int64_t>(k) * a.C);
+      }
       static_for<L + 1>([&](auto LI) {
         constexpr int l = decltype(LI)::value;
         constexpr int n = 2 * l + 1;
@@ -494,7 +519,7 @@ struct Prep {
           if (ro) store_vec<TM, V>(ro + ro_off, o);
           if (rp) {
             float rv[V];
-            load_vec<TM, V>(rp + rad_slot<L, M>(q, l, 0, a.C), rv);
+            unpack_vec<TM, V>(rr[rad_slot<L, M>(q, l, 0, 1)], rv);
 #pragma unroll
             for (int c = 0; c < V; ++c) o[c] *= rv[c];
           }
@@ -505,9 +530,9 @@ struct Prep {
   }
 };
 
-template <int L, int M, class TM, class TX>
+template <int L, int M, class TM, class TX, bool GATED = false>
 __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
-  Prep<L, M, TM, TX>::run(a);
+  Prep<L, M, TM, TX, GATED>::run(a);
 }
 
 }  // namespace msg

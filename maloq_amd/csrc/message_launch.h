@@ -65,13 +65,20 @@ template <int L, int M>
 int prep_lm(int dtype, int mode, const PrepArgs& a, hipStream_t s) {
   const int64_t grid = (a.E + 31) / 32;
   MALOQ_REQUIRE(grid < (int64_t(1) << 31), "grid too large");
+  const dim3 g(static_cast<unsigned>(grid)), b(256);
+  const bool gated = mode != FWD && a.gsave != nullptr;
   if (dtype == 1) {
     if (mode == FWD)
-      hipLaunchKernelGGL((prep_kernel<L, M, BF16, BF16>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);
+      hipLaunchKernelGGL((prep_kernel<L, M, BF16, BF16>), g, b, 0, s, a);
+    else if (gated)
+      hipLaunchKernelGGL((prep_kernel<L, M, BF16, F32, true>), g, b, 0, s, a);
     else
-      hipLaunchKernelGGL((prep_kernel<L, M, BF16, F32>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);
+      hipLaunchKernelGGL((prep_kernel<L, M, BF16, F32>), g, b, 0, s, a);
   } else {
-    hipLaunchKernelGGL((prep_kernel<L, M, F32, F32>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);
+    if (gated)
+      hipLaunchKernelGGL((prep_kernel<L, M, F32, F32, true>), g, b, 0, s, a);
+    else
+      hipLaunchKernelGGL((prep_kernel<L, M, F32, F32>), g, b, 0, s, a);
   }
   return check_launch("prep_kernel");
 }
