@@ -87,6 +87,9 @@ def message_step(w, backward=True):
     rad = w["radial"](gaussian_rbf(w["dist"], 0.0, 6.0, 8), out_dtype=w["dt"])
     out = M.message_block(w["x"], w["plan"], eul, rad, w["w0"], w["b0"], w["wm"], w["L"], w["M"])
     if backward:
+        # a training step starts from cleared gradients (zero_grad(set_to_none=True))
+        for t in [w["x"], w["w0"], w["b0"], *w["wm"], *w["radial"].parameters()]:
+            t.grad = None
         out.backward(w["gout"])
     return out
 

@@ -143,6 +143,18 @@ int64_t maloq_message_partials_floats(int lmax, int gate, int64_t num_edges, int
  * kernel-input channels c_k, kernel-output channels c_n); -1 if unsupported. */
 int64_t maloq_message_wpack_bytes(int dtype, int lmax, int mmax, int gate, int c_k, int c_n);
 
+/* Weight packing: out[i] = W[idx[i]] converted to the operand type (dtype 0 =
+ * fp32, 1 = bf16, round to nearest even), W being the concatenation of the nsrc
+ * fp32 device arrays srcs[k] of src_sizes[k] elements (fc_m0.weight, then
+ * so2_m_conv[m-1].fc.weight for m = 1..mmax, in the reference's layout).  idx
+ * [n] int64 device array: the fragment order of the kernels, built once per
+ * shape by the host packer (maloq_amd.message._pack_index); n elements make
+ * maloq_message_wpack_bytes(...) bytes.  nsrc <= 4.  Stands in for reading
+ * fc_m0 / so2_m_conv weights at helm/nn/so2_layers.py:161-203 (the kernels
+ * take the weights in fragment order). */
+int maloq_message_pack(int dtype, int nsrc, const float* const* srcs, const int64_t* src_sizes,
+                       const int64_t* idx, int64_t n, void* out, void* stream);
+
 /* Kept rows d' = (lmax+1) + sum_{m=1..mmax} 2 (lmax-m+1) of the m-major layout,
  * and floats per edge of the kept Wigner-D rows (|m| <= mmax) in the kernels'
  * pair-major layout: per degree l, (l+1) column pairs (j, j+1) of the
@@ -225,6 +237,18 @@ int64_t maloq_message_dw_partials_floats(int lmax, int mmax, int gate, int c_out
 int maloq_message_dw(int dtype, int lmax, int mmax, int gate, const void* dz, const void* y,
                      int64_t num_edges, int c_out, int c_in, int splits, float* partials,
                      float* dw0, float* dw1, float* dw2, float* dw3, void* stream);
+
+/* Bias gradient of fc_m0: out[r c + k] = sum_{e < num_edges} rows[e][row0 + r][k]
+ * for r < nrows, k < c, where rows [num_edges, rows_per_edge, c] (dtype 0 =
+ * fp32, 1 = bf16; c a multiple of 4 resp. 8) are the saved dL/dz rows of
+ * maloq_message_bwd_dx.  db0 of fc_m0 is rows [0, lmax+1) (and, gated, the
+ * gate bias rows [d', d'+lmax)).  A fixed-order tree over 64-edge blocks:
+ * deterministic, fp32 sums.  partials: maloq_message_colsum_partials_floats
+ * floats (may be null when that is 0).  Replaces the autograd bias gradient of
+ * fc_m0 (helm/nn/so2_layers.py:161-170). */
+int64_t maloq_message_colsum_partials_floats(int nrows, int c, int64_t num_edges);
+int maloq_message_colsum(int dtype, const void* rows, int rows_per_edge, int row0, int nrows, int c,
+                         int64_t num_edges, float* partials, float* out, void* stream);
 
 /* ------------------------------------------------------------ RadialMLP -- */
 

@@ -44,6 +44,9 @@ SIGNATURES = {
     "maloq_message_edge_rows": [_i64],
     "maloq_message_dw_partials_floats": [_i32, _i32, _i32, _i32, _i32, _i32],
     "maloq_message_dw": [_i32, _i32, _i32, _i32, _p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p],
+    "maloq_message_pack": [_i32, _i32, _p, _p, _p, _i64, _p, _p],
+    "maloq_message_colsum_partials_floats": [_i32, _i32, _i64],
+    "maloq_message_colsum": [_i32, _p, _i32, _i32, _i32, _i32, _i64, _p, _p, _p],
     "maloq_radial_pack_bytes": [_i32, _i32, _i32],
     "maloq_radial_fwd": [_i32, _i32, _p, _p, _i64, _p, _p, _p, _p, ctypes.c_float, _p, _p, _p, _p, _p, _p],
     "maloq_radial_bwd_partials_floats": [_i32, _i32, _p, _i64],
@@ -56,6 +59,7 @@ RESTYPES = {
     "maloq_message_wpack_bytes": ctypes.c_int64,
     "maloq_message_dw_partials_floats": ctypes.c_int64,
     "maloq_message_edge_rows": ctypes.c_int64,
+    "maloq_message_colsum_partials_floats": ctypes.c_int64,
     "maloq_radial_pack_bytes": ctypes.c_int64,
     "maloq_radial_bwd_partials_floats": ctypes.c_int64,
 }

@@ -20,9 +20,11 @@ dst-sorted order (``plan.sort_edges``).
 """
 from __future__ import annotations
 
+import ctypes
 import functools
 
 import numpy as np
+
 import torch
 
 from . import _lib
@@ -150,14 +152,17 @@ def pack_weights(w0, wm, lmax, mmax, gate, c_in, c_out, dtype, mode=0):
         hit = (torch.from_numpy(idx).to(w0.device), total)
         _PACK_DEV[key] = hit
     idx, total = hit
-    with torch.no_grad():
-        flat = torch.cat([w0.reshape(-1)] + [w.reshape(-1) for w in wm[:mmax]]).float()
-        assert flat.numel() == total, "weight shapes do not match (lmax, mmax, channels)"
-        packed = flat[idx].to(dtype)
-    want = _lib.load().maloq_message_wpack_bytes(code, lmax, mmax, int(bool(gate)),
-                                                c_in if mode == 0 else c_out,
-                                                c_out if mode == 0 else c_in)
+    srcs = [w.detach().float().contiguous() for w in [w0] + list(wm[:mmax])]
+    assert sum(t.numel() for t in srcs) == total, "weight shapes do not match (lmax, mmax, channels)"
+    lib = _lib.load()
+    want = lib.maloq_message_wpack_bytes(code, lmax, mmax, int(bool(gate)),
+                                         c_in if mode == 0 else c_out,
+                                         c_out if mode == 0 else c_in)
+    packed = torch.empty(idx.numel(), dtype=dtype, device=w0.device)
     assert packed.numel() * packed.element_size() == want, (packed.numel(), want)
+    _lib.call("maloq_message_pack", code, len(srcs), (ctypes.c_void_p * len(srcs))(*[t.data_ptr() for t in srcs]),
+              (ctypes.c_int64 * len(srcs))(*[t.numel() for t in srcs]), _lib.ptr(idx), idx.numel(),
+              _lib.ptr(packed), _lib.stream_of(w0.device))
     return packed
 
 
@@ -307,10 +312,14 @@ def message_weight_grad(dz, y, lmax, mmax, c_out, c_in, splits=None, num_edges=N
     _lib.call("maloq_message_dw", DTYPE_CODE[dz.dtype], lmax, mmax, int(gate), _lib.ptr(dz), _lib.ptr(y), E,
               c_out, c_in, splits, _lib.ptr(parts), _lib.ptr(dw0), ptrs[0], ptrs[1], ptrs[2],
               _lib.stream_of(dz.device))
-    db0 = dz[:E, : lmax + 1, :].float().sum(0).reshape(-1)
-    if gate:
-        kept = kept_rows(lmax, mmax)
-        db0 = torch.cat([dz[:E, kept: kept + lmax, :].float().sum(0).reshape(-1), db0])
+    db0 = torch.empty(extra + (lmax + 1) * c_out, device=dz.device, dtype=torch.float32)
+    rpe = dz.shape[1]
+    groups = [(0, lmax + 1, extra)] + ([(kept_rows(lmax, mmax), lmax, 0)] if gate else [])
+    cs = torch.empty(max(1, max(lib.maloq_message_colsum_partials_floats(nr, c_out, E) for _, nr, _ in groups)),
+                     device=dz.device, dtype=torch.float32)
+    for row0, nr, at in groups:
+        _lib.call("maloq_message_colsum", DTYPE_CODE[dz.dtype], _lib.ptr(dz), rpe, row0, nr, c_out, E,
+                  _lib.ptr(cs), _lib.ptr(db0[at:]), _lib.stream_of(dz.device))
     return dw0, dwm, db0
 
 
