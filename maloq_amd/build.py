@@ -50,7 +50,10 @@ def build(verbose: bool = True, incremental: bool = False) -> str:
     """Compile every HIP source (``incremental`` reuses objects newer than their
     inputs; the default always recompiles)."""
     os.makedirs(BUILD_DIR, exist_ok=True)
-    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    # the kernel-heavy units (template instantiations of the message block)
+    # start first, then the rest, largest first
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")),
+                  key=lambda f: ("message_l" not in os.path.basename(f), -os.path.getsize(f), f))
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(lambda s: _compile(s, incremental), srcs))
     tmp = OUT + ".tmp"

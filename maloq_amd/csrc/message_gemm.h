@@ -13,8 +13,8 @@
 // inverse rotation runs from its own accumulators and the segment sum stays
 // inside the wave.  The K loop runs over (l_in, KC input channels):
 //   * A (rotated rows): one 1 KB fragment per (row type q of l_in, row tile),
-//     in the exact lane order of the MFMA A operand; loaded from global into
-//     registers one step ahead, stored to a double-buffered LDS stage, one
+//     in the exact lane order of the MFMA A operand, copied global -> LDS by
+//     DMA (global_load_lds) into a ring of three stages, two steps ahead; one
 //     barrier per step.  Every wave reads the fragments it needs from LDS.
 //   * B (weights): each wave loads only the fragments of its own degrees
 //     straight from global memory into registers (16 bytes per lane, fully
@@ -129,12 +129,13 @@ struct GPlan {
   static constexpr int pblk(int l) { return PairLayout<L, M>::pblk(l); }
   static constexpr int woff(int l) { return PairLayout<L, M>::woff(l); }
   static constexpr int WS = PairLayout<L, M>::WS;
-  static constexpr int NW4 = (TE * WS / 4 + NT - 1) / NT;  // float4 copies per thread
+  // Wigner rows in LDS: TE WS / 4 16-byte chunks, copied by DMA in whole
+  // 64-lane instructions (the array is padded to a multiple of 64 chunks)
+  static constexpr int W16 = TE * WS / 4;
+  static constexpr int W16P = (W16 + 63) / 64 * 64;
   // LDS
   static constexpr int A_BYTES = nqa(L) * RT * FRAG;     // one A stage
   static constexpr int CH = 16;                           // edges per epilogue chunk
-  static constexpr int STG_BYTES = NW * CH * 64 * 4;      // epilogue staging
-  static constexpr int U_BYTES = (2 * A_BYTES > STG_BYTES) ? 2 * A_BYTES : STG_BYTES;
   static constexpr int NA = (nqa(L) * RT * 64 + NT - 1) / NT;  // A chunks per thread
 };
 
@@ -162,7 +163,6 @@ struct Gemm {
   static constexpr int d = (L + 1) * (L + 1);
 
   struct Smem {
-    alignas(16) float W[TE * P::WS];
     float* optr[TE];  // destination row block of the segment ending at each edge
     int seg[TE];
     int eid[TE];
@@ -340,32 +340,51 @@ struct Gemm {
     });
   }
 
-  // One K step (LI, ks) of wave W: reads stage rd and B registers bc; the next
-  // step (degree NXT, or none if NXT < 0) gets its A fragments (DMA) into stage
-  // wr and its B fragments into registers bn.  The callers alternate the two
-  // stages and register sets by step parity, every choice static.  The
-  // barrier's vmcnt(0) wait is exactly the previous step's loads; the m = 0
-  // fragments are read before the next DMA is issued, the others from a stage
-  // no DMA targets.
-  template <int W, int LI, int NXT>
-  static __device__ __forceinline__ void kstep(f32x16 (&acc)[P::MSLOT], const frag_t (&bc)[P::NBW],
-                                               frag_t (&bn)[P::NBW], const AState& st,
-                                               const char* rd, char* wr, const Args& a,
-                                               const char* wp, int64_t foff, int ks, int nks,
-                                               int lane) {
-    __syncthreads();
+  // DMA instructions wave W issues for one K step of input degree LI.
+  template <int W, int LI>
+  static constexpr int ndma() {
+    int n = 0;
+    for (int k = 0; k < NAW; ++k)
+      if (k < atab.count[W] && atab.frag[W][k] < P::nqa(LI) * RT) ++n;
+    return n;
+  }
+  template <int I>
+  static __device__ __forceinline__ char* stage(char* s0, char* s1, char* s2) {
+    return I == 0 ? s0 : (I == 1 ? s1 : s2);
+  }
+
+  // One K step of wave W on input degree LI: A fragments from stage RD, B
+  // fragments in bn (loaded by the previous step).  The A stages form a ring of
+  // three, filled by DMA two steps ahead; B is loaded one step ahead.  At entry
+  // the wave's outstanding vector-memory operations are, in issue order, the B
+  // loads of this step and the DMA of the next step (PEND instructions), so
+  // vmcnt(PEND) leaves only the latter in flight, and after the barrier every
+  // wave's DMA of this step has landed.  lgkmcnt(0): the previous step's LDS
+  // reads are complete before any wave refills that stage.  Then: B of the
+  // next step (degree NB, K step ksb, fragment base fb; none if NB < 0) into
+  // bn, DMA of the step after it (degree NA, K step ksa; none if NA < 0) into
+  // stage (RD + 2) % 3, and the MFMAs of this step.
+  template <int W, int LI, int RD, int NB, int NA, int PEND>
+  static __device__ __forceinline__ void kstep(f32x16 (&acc)[P::MSLOT], frag_t (&bn)[P::NBW],
+                                               const AState& st, char* s0, char* s1, char* s2,
+                                               const Args& a, const char* wp, int64_t fb, int ksb,
+                                               int ksa, int lane) {
+    // s_waitcnt as a builtin, so that the compiler's own wait insertion counts it
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((PEND & 15) | (7 << 4) | ((PEND >> 4) << 14));  // vmcnt(PEND) lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    frag_t bc[P::NBW];
+#pragma unroll
+    for (int i = 0; i < P::NBW; ++i) bc[i] = bn[i];
+    if constexpr (NB >= 0) b_load<W, NB>(bn, wp, fb, ksb, lane);
+    if constexpr (NA >= 0) a_dma<W, NA>(st, stage<(RD + 2) % 3>(s0, s1, s2), a, ksa);
+    // keep the next steps' loads ahead of this step's MFMAs
+    __builtin_amdgcn_sched_barrier(0);
+    const char* rd = stage<RD>(s0, s1, s2);
     frag_t a0[RT], ag[RT];
     read_q<0>(a0, rd, lane);
     if constexpr (P::gin(LI)) read_q<P::nq(LI)>(ag, rd, lane);
-    if constexpr (NXT == LI) {
-      a_dma<W, LI>(st, wr, a, ks + 1);
-      b_load<W, LI>(bn, wp, foff, ks + 1, lane);
-    } else if constexpr (NXT >= 0) {
-      a_dma<W, NXT>(st, wr, a, 0);
-      b_load<W, NXT>(bn, wp, foff + static_cast<int64_t>(nks) * P::nbfrag(LI), 0, lane);
-    }
-    // keep the next step's loads ahead of this step's MFMAs
-    __builtin_amdgcn_sched_barrier(0);
     mma_m0<W, LI>(acc, a0, ag, bc);
     static_for<M>([&](auto MI) {
       constexpr int m = decltype(MI)::value + 1;
@@ -378,24 +397,41 @@ struct Gemm {
     });
   }
 
-  // The nks K steps of input degree LI, starting with stage s0 / registers b0;
-  // EVENK: nks is even (else odd), which fixes the parity of the last steps.
-  template <int W, int LI, bool EVENK>
-  static __device__ __forceinline__ void kdegree(f32x16 (&acc)[P::MSLOT], frag_t (&b0)[P::NBW],
-                                                 frag_t (&b1)[P::NBW], const AState& st, char* s0,
-                                                 char* s1, const Args& a, const char* wp,
-                                                 int64_t foff, int nks, int lane) {
+  // The nks K steps of input degree LI.  KR = nks % 3 for nks >= 2 (then the
+  // stage of the degree's first step is (LI nks) % 3 = (LI KR) % 3), KR = 3 for
+  // nks == 1.  Step ks loads B of ks + 1 and DMAs ks + 2, crossing into degree
+  // LI + 1 for the last two steps; the ring position of every step is static.
+  template <int W, int LI, int KR>
+  static __device__ __forceinline__ void kdegree(f32x16 (&acc)[P::MSLOT], frag_t (&bn)[P::NBW],
+                                                 const AState& st, char* s0, char* s1, char* s2,
+                                                 const Args& a, const char* wp, int64_t foff, int nks,
+                                                 int lane) {
     constexpr int NXT = LI < L ? LI + 1 : -1;
-    int ks = 0;
-    for (; ks + 2 < nks; ks += 2) {
-      kstep<W, LI, LI>(acc, b0, b1, st, s0, s1, a, wp, foff, ks, nks, lane);
-      kstep<W, LI, LI>(acc, b1, b0, st, s1, s0, a, wp, foff, ks + 1, nks, lane);
-    }
-    if constexpr (EVENK) {
-      kstep<W, LI, LI>(acc, b0, b1, st, s0, s1, a, wp, foff, ks, nks, lane);
-      kstep<W, LI, NXT>(acc, b1, b0, st, s1, s0, a, wp, foff, ks + 1, nks, lane);
+    constexpr int ND = ndma<W, LI>();
+    if constexpr (KR == 3) {  // one step per degree: B of degree LI + 1, DMA of LI + 2
+      constexpr int NA = LI + 2 <= L ? LI + 2 : -1;
+      constexpr int PEND = NXT >= 0 ? ndma<W, (NXT >= 0 ? NXT : 0)>() : 0;
+      kstep<W, LI, LI % 3, NXT, NA, PEND>(acc, bn, st, s0, s1, s2, a, wp, foff + P::nbfrag(LI), 0, 0, lane);
     } else {
-      kstep<W, LI, NXT>(acc, b0, b1, st, s0, s1, a, wp, foff, ks, nks, lane);
+      constexpr int PH = (LI * KR) % 3;
+      constexpr int REM = (KR + 1) % 3;  // (nks - 2) % 3
+      int ks = 0;
+      for (; ks + 3 <= nks - 2; ks += 3) {
+        kstep<W, LI, PH, LI, LI, ND>(acc, bn, st, s0, s1, s2, a, wp, foff, ks + 1, ks + 2, lane);
+        kstep<W, LI, (PH + 1) % 3, LI, LI, ND>(acc, bn, st, s0, s1, s2, a, wp, foff, ks + 2, ks + 3, lane);
+        kstep<W, LI, (PH + 2) % 3, LI, LI, ND>(acc, bn, st, s0, s1, s2, a, wp, foff, ks + 3, ks + 4, lane);
+      }
+      if constexpr (REM >= 1)
+        kstep<W, LI, PH, LI, LI, ND>(acc, bn, st, s0, s1, s2, a, wp, foff, ks + 1, ks + 2, lane);
+      if constexpr (REM >= 2)
+        kstep<W, LI, (PH + 1) % 3, LI, LI, ND>(acc, bn, st, s0, s1, s2, a, wp, foff, ks + 2, ks + 3, lane);
+      constexpr int PEND_NXT = NXT >= 0 ? ndma<W, (NXT >= 0 ? NXT : 0)>() : 0;
+      const int64_t fnext = foff + static_cast<int64_t>(nks) * P::nbfrag(LI);
+      // ks = nks - 2: B of (LI, nks - 1), DMA of (LI + 1, 0)
+      kstep<W, LI, (PH + REM) % 3, LI, NXT, ND>(acc, bn, st, s0, s1, s2, a, wp, foff, nks - 1, 0, lane);
+      // ks = nks - 1: B of (LI + 1, 0), DMA of (LI + 1, 1)
+      kstep<W, LI, (PH + REM + 1) % 3, NXT, NXT, PEND_NXT>(acc, bn, st, s0, s1, s2, a, wp, fnext, 0, 1,
+                                                            lane);
     }
   }
 
@@ -565,13 +601,13 @@ struct Gemm {
   // then store the sums of the segments that end in the chunk.
   template <int W, int lo>
   static __device__ __forceinline__ void rotate_sum(f32x16 (&acc)[P::MSLOT], Smem& s,
-                                                    const Args& a, int cb, float* buf, int lane,
-                                                    uint64_t endmask) {
+                                                    const float* wsh, const Args& a, int cb,
+                                                    float* buf, int lane, uint64_t endmask) {
     constexpr int n = 2 * lo + 1;
     constexpr int nq = P::nq(lo);
     constexpr int PB = P::pblk(lo);
     const int co = lane & 31, h = lane >> 5;
-    const float* Wl = s.W + P::woff(lo);
+    const float* Wl = wsh + P::woff(lo);
     const uint64_t startmask = (endmask << 1) | 1ull;
     for (int p = 0; p <= lo; ++p) {
       const bool has_col = 2 * p + h < n;
@@ -607,13 +643,16 @@ struct Gemm {
           X[ii] = __uint_as_float(sw[0]);
           Y[ii] = __uint_as_float(sw[1]);
         }
-        // chunk rows in edge order: X[0..3], Y[0..3], X[4..7], Y[4..7]
+        // chunk rows in edge order: X[0..3], Y[0..3], X[4..7], Y[4..7].  The
+        // chunk's segment starts, opaque per chunk: otherwise the compiler
+        // hoists all 64 uniform selects out of the column loop and spills them.
+        uint32_t sm = static_cast<uint32_t>(startmask >> (c * P::CH)) & 0xffffu;
+        asm volatile("" : "+s"(sm));
         static_for<P::CH>([&](auto UI) {
           constexpr int u = decltype(UI)::value;
-          constexpr int e = c * P::CH + u;
           constexpr int k = 4 * (u >> 3) + (u & 3);
           const float val = ((u >> 2) & 1) ? Y[k] : X[k];
-          run = ((startmask >> e) & 1ull) ? val : run + val;
+          run = ((sm >> u) & 1u) ? val : run + val;
           buf[u * 64 + lane] = run;
         });
         wave_sync();
@@ -630,9 +669,10 @@ struct Gemm {
     }
   }
 
-  template <int W, bool EVENK, bool RAD>
-  static __device__ __forceinline__ void body(Smem& s, char* st0, char* st1, const Args& a, int cb,
-                                              int tid, int nvalid) {
+  template <int W, int KR, bool RAD>
+  static __device__ __forceinline__ void body(Smem& s, const float* wsh, char* st0, char* st1, char* st2,
+                                              const Args& a,
+                                              int cb, int tid, int nvalid) {
     const int wave = tid >> 6, lane = tid & 63;
     f32x16 acc[P::MSLOT];
 #pragma unroll
@@ -644,17 +684,20 @@ struct Gemm {
     const char* wp = a.wpack + static_cast<int64_t>(cb) * a.frags_per_cb * FRAG;
     AState st;
     a_init<W>(st, s, a, lane);
-    frag_t b0[P::NBW], b1[P::NBW];
+    frag_t bn[P::NBW];
+    // ring prologue, in the issue order kstep expects: DMA of step 0, B of
+    // step 0, DMA of step 1
     a_dma<W, 0>(st, st0, a, 0);
-    b_load<W, 0>(b0, wp, 0, 0, lane);
+    b_load<W, 0>(bn, wp, 0, 0, lane);
+    if constexpr (KR == 3) {
+      if constexpr (L >= 1) a_dma<W, (L >= 1 ? 1 : 0)>(st, st1, a, 0);
+    } else {
+      a_dma<W, 0>(st, st1, a, 1);
+    }
     int64_t foff = 0;
     static_for<L + 1>([&](auto LIc) {
       constexpr int LI = decltype(LIc)::value;
-      // parity of the degree's first global K step (LI * nks)
-      if constexpr (EVENK || (LI & 1) == 0)
-        kdegree<W, LI, EVENK>(acc, b0, b1, st, st0, st1, a, wp, foff, nks, lane);
-      else
-        kdegree<W, LI, EVENK>(acc, b1, b0, st, st1, st0, a, wp, foff, nks, lane);
+      kdegree<W, LI, KR>(acc, bn, st, st0, st1, st2, a, wp, foff, nks, lane);
       foff += static_cast<int64_t>(nks) * P::nbfrag(LI);
     });
     __syncthreads();  // all A reads done before the stages become epilogue staging
@@ -677,18 +720,22 @@ struct Gemm {
         } else if constexpr (RAD)
           radial<lo>(acc, s, a, cb,
                      reinterpret_cast<float*>((wave < 2 ? st0 : st1) + (wave & 1) * PW), lane);
-        rotate_sum<W, lo>(acc, s, a, cb,
+        rotate_sum<W, lo>(acc, s, wsh, a, cb,
                           reinterpret_cast<float*>((wave < 2 ? st0 : st1) + (wave & 1) * PW),
                           lane, endmask);
       }
     });
   }
 
-  template <bool EVENK, bool RAD>
+  template <int KR, bool RAD>
   static __device__ __forceinline__ void run(const Args& a) {
     __shared__ Smem s;
     __shared__ alignas(16) char st0[SB];
     __shared__ alignas(16) char st1[SB];
+    __shared__ alignas(16) char st2[SB];
+    // Wigner rows of the tile: its own LDS object, so that the compiler can tell
+    // its DMA apart from the accesses to s
+    __shared__ alignas(16) float wsh[P::W16P * 4];
     const int tid = threadIdx.x, wave = tid >> 6;
     // XCD-aware mapping: consecutive workgroup ids go round-robin over the 8
     // XCDs.  The n_cb channel-block workgroups of one edge tile are the
@@ -708,24 +755,6 @@ struct Gemm {
       s.eid[tid] = v ? (a.eidx ? a.eidx[p] : static_cast<int>(p)) : -1;
     }
     __syncthreads();
-    // Wigner rows of the tile's edges (pair layout), all loads in flight at once
-    {
-      constexpr int R4 = P::WS / 4;
-      const float4* dk4 = reinterpret_cast<const float4*>(a.dk);
-      float4 wv[P::NW4];
-#pragma unroll
-      for (int k = 0; k < P::NW4; ++k) {
-        const int i = tid + k * NT;
-        const int e = i / R4, r = i - (i / R4) * R4;
-        wv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (i < TE * R4 && s.eid[e] >= 0) wv[k] = dk4[static_cast<int64_t>(s.eid[e]) * R4 + r];
-      }
-#pragma unroll
-      for (int k = 0; k < P::NW4; ++k) {
-        const int i = tid + k * NT;
-        if (i < TE * R4) reinterpret_cast<float4*>(s.W)[i] = wv[k];
-      }
-    }
     // Segments cut by the tile boundary go to the partials buffer: the tile's
     // first segment (slot 0) if it began in an earlier tile, its last one
     // (slot 1) if it continues into the next tile.
@@ -743,18 +772,40 @@ struct Gemm {
       }
       s.optr[tid] = dst;
     }
+    // Wigner rows of the tile's edges (pair layout): DMA straight into LDS,
+    // issued after every global load whose value the prologue waits for, so it
+    // is in flight with the first K steps; the K loop's waits and barriers
+    // complete it long before the epilogue reads it.  Chunk i = 64 (k NW + w) +
+    // lane is instruction k of wave w; lanes past the tile read an in-bounds row
+    // into the padding; rows of edges past the tile are never stored.
+    {
+      constexpr int R4 = P::WS / 4;
+      const float4* dk4 = reinterpret_cast<const float4*>(a.dk);
+      const int wv = __builtin_amdgcn_readfirstlane(wave), lane = tid & 63;
+      for (int k = 0; k < (P::W16P / 64 + NW - 1) / NW; ++k) {
+        const int blk = k * NW + wv;  // uniform
+        if (blk >= P::W16P / 64) break;
+        const int i = blk * 64 + lane;
+        const int e = i / R4 < TE ? i / R4 : TE - 1;
+        const int ei = s.eid[e] >= 0 ? s.eid[e] : s.eid[0];
+#if defined(__HIP_DEVICE_COMPILE__)
+        __builtin_amdgcn_global_load_lds(dk4 + static_cast<int64_t>(ei) * R4 + (i - (i / R4) * R4),
+                                         (lds_void*)(reinterpret_cast<char*>(wsh) + blk * 1024), 16, 0, 0);
+#endif
+      }
+    }
     static_for<NW>([&](auto WI) {
       constexpr int w = decltype(WI)::value;
-      if (wave == w) body<w, EVENK, RAD>(s, st0, st1, a, cb, tid, nvalid);
+      if (wave == w) body<w, KR, RAD>(s, wsh, st0, st1, st2, a, cb, tid, nvalid);
     });
   }
 };
 
-// EVENK: the number of K steps per input degree (C_k / KC) is even.
+// KR: (C_k / KC) % 3 if C_k / KC >= 2, else 3.
 // RAD (input gradient only): a radial scale is given (its gradient is formed).
-template <int L, int M, bool GATE, int NW, int RT, class TM, int MODE, bool EVENK, bool RAD>
+template <int L, int M, bool GATE, int NW, int RT, class TM, int MODE, int KR, bool RAD>
 __global__ __launch_bounds__(NW * 64, 2) void gemm_kernel(Args a) {
-  Gemm<L, M, GATE, NW, RT, TM, MODE>::template run<EVENK, RAD>(a);
+  Gemm<L, M, GATE, NW, RT, TM, MODE>::template run<KR, RAD>(a);
 }
 
 }  // namespace msg

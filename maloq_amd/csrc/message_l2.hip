@@ -1,8 +1,14 @@
-// Instantiations of the fused message kernel for lmax = 2.
+// Prep kernels and the GEMM dispatch of the fused message block for lmax = 2.
 #include "message_launch.h"
 
 namespace maloq {
 namespace msg {
+
+// GEMM kernels: defined in message_l2_<dtype>_<mode>.hip
+MALOQ_GEMM_INSTANCES(extern, 2, 2, BF16, FWD)
+MALOQ_GEMM_INSTANCES(extern, 2, 2, BF16, BWD_DX)
+MALOQ_GEMM_INSTANCES(extern, 2, 2, F32, FWD)
+MALOQ_GEMM_INSTANCES(extern, 2, 2, F32, BWD_DX)
 
 int launch_l2(int mmax, int dtype, int gate, int mode, const Args& a, hipStream_t s) {
   MALOQ_REQUIRE(mmax == 2, "lmax=2: built for mmax = 2 only, got %d", mmax);

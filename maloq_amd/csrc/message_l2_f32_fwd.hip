@@ -1,0 +1,10 @@
+// Fused message GEMM kernels for lmax = 2, f32, forward.
+#include "message_launch.h"
+
+namespace maloq {
+namespace msg {
+
+MALOQ_GEMM_INSTANCES(, 2, 2, F32, FWD)
+
+}  // namespace msg
+}  // namespace maloq

@@ -1,8 +1,14 @@
-// Instantiations of the fused message kernel for lmax = 4.
+// Prep kernels and the GEMM dispatch of the fused message block for lmax = 4.
 #include "message_launch.h"
 
 namespace maloq {
 namespace msg {
+
+// GEMM kernels: defined in message_l4_<dtype>_<mode>.hip
+MALOQ_GEMM_INSTANCES(extern, 4, 2, BF16, FWD)
+MALOQ_GEMM_INSTANCES(extern, 4, 2, BF16, BWD_DX)
+MALOQ_GEMM_INSTANCES(extern, 4, 2, F32, FWD)
+MALOQ_GEMM_INSTANCES(extern, 4, 2, F32, BWD_DX)
 
 int launch_l4(int mmax, int dtype, int gate, int mode, const Args& a, hipStream_t s) {
   MALOQ_REQUIRE(mmax == 2, "lmax=4: built for mmax = 2 only, got %d", mmax);

@@ -1,0 +1,10 @@
+// Fused message GEMM kernels for lmax = 6, f32, input gradient.
+#include "message_launch.h"
+
+namespace maloq {
+namespace msg {
+
+MALOQ_GEMM_INSTANCES(, 6, 2, F32, BWD_DX)
+
+}  // namespace msg
+}  // namespace maloq

@@ -17,6 +17,15 @@ struct Cfg {
 
 inline int tile_edges(int lmax, int gate) { return (lmax <= 4 && !gate) ? 64 : 32; }
 
+template <int L, int M, bool GATE, class TM, int MODE, int KR>
+void launch_kr(const Args& a, dim3 g, dim3 b, hipStream_t s) {
+  constexpr int NW = Cfg<L, GATE>::NW, RT = Cfg<L, GATE>::RT;
+  if (MODE != FWD && a.rad != nullptr)
+    hipLaunchKernelGGL((gemm_kernel<L, M, GATE, NW, RT, TM, MODE, KR, MODE != FWD>), g, b, 0, s, a);
+  else
+    hipLaunchKernelGGL((gemm_kernel<L, M, GATE, NW, RT, TM, MODE, KR, false>), g, b, 0, s, a);
+}
+
 template <int L, int M, bool GATE, class TM, class TX, int MODE>
 int launch(const Args& a, hipStream_t s) {
   constexpr int NW = Cfg<L, GATE>::NW, RT = Cfg<L, GATE>::RT;
@@ -26,25 +35,24 @@ int launch(const Args& a, hipStream_t s) {
   const int64_t grid = ((a.ntiles + 7) / 8) * 8 * a.n_cb;
   MALOQ_REQUIRE(grid < (int64_t(1) << 31), "grid too large");
   const dim3 g(static_cast<unsigned>(grid)), b(P::NT);
-  const bool even = (a.C_k / TM::KC) % 2 == 0;
-  if constexpr (MODE == FWD) {
-    if (even)
-      hipLaunchKernelGGL((gemm_kernel<L, M, GATE, NW, RT, TM, MODE, true, false>), g, b, 0, s, a);
-    else
-      hipLaunchKernelGGL((gemm_kernel<L, M, GATE, NW, RT, TM, MODE, false, false>), g, b, 0, s, a);
-  } else if (a.rad != nullptr) {
-    if (even)
-      hipLaunchKernelGGL((gemm_kernel<L, M, GATE, NW, RT, TM, MODE, true, true>), g, b, 0, s, a);
-    else
-      hipLaunchKernelGGL((gemm_kernel<L, M, GATE, NW, RT, TM, MODE, false, true>), g, b, 0, s, a);
-  } else {
-    if (even)
-      hipLaunchKernelGGL((gemm_kernel<L, M, GATE, NW, RT, TM, MODE, true, false>), g, b, 0, s, a);
-    else
-      hipLaunchKernelGGL((gemm_kernel<L, M, GATE, NW, RT, TM, MODE, false, false>), g, b, 0, s, a);
+  // the A-stage ring position of each K step is static per nks % 3 (nks >= 2)
+  const int nks = a.C_k / TM::KC;
+  switch (nks >= 2 ? nks % 3 : 3) {
+    case 0: launch_kr<L, M, GATE, TM, MODE, 0>(a, g, b, s); break;
+    case 1: launch_kr<L, M, GATE, TM, MODE, 1>(a, g, b, s); break;
+    case 2: launch_kr<L, M, GATE, TM, MODE, 2>(a, g, b, s); break;
+    default: launch_kr<L, M, GATE, TM, MODE, 3>(a, g, b, s); break;
   }
   return check_launch("gemm_kernel");
 }
+
+// The GEMM instantiations of one (lmax, mmax, dtype, mode), gated and not:
+// defined (KW empty) in their own translation unit each, so the per-lmax
+// kernel sets compile in parallel, and declared (KW extern) where launch_lm
+// dispatches to them.
+#define MALOQ_GEMM_INSTANCES(KW, L, M, TM, MODE)                              \
+  KW template int launch<L, M, false, TM, TM, MODE>(const Args&, hipStream_t); \
+  KW template int launch<L, M, true, TM, TM, MODE>(const Args&, hipStream_t);
 
 // dtype: 0 fp32, 1 bf16; mode: FWD or BWD_DX.
 template <int L, int M>
