@@ -19,8 +19,8 @@
 //
 // Backward:
 //   radial_du_kernel     du_H = G W_o on the MFMA (G = dL/drad rows, read
-//                        once; the K range split over 4 waves with a 4-step
-//                        load ring, partial tiles summed in wave order).
+//                        once; 64 edges per workgroup, the K range split over
+//                        8 waves, partial tiles summed by a fixed tree).
 //   radial_chain_kernel  recomputes the hidden chain of its 64 edges and runs
 //                        it backward on the VALU (SiLU', LayerNorm backward,
 //                        du_{i-1} = W_i^T dz_i), writing per-tile partials of
@@ -496,17 +496,24 @@ __global__ __launch_bounds__(FW_W * 64) void radial_fwd_kernel(Args a) {
 }
 
 // ---------------------------------------------------------------- backward
-// du_H [e][j] = sum_o G[e][o] W_o[o][j] for 32 edges per workgroup.  Wave w
-// of DU_W takes 1/DU_W of the K (output) range for all NNT column tiles; its
-// A (G rows) and B (W_o^T rows) fragments of up to DU_KS steps are all in
-// flight before the first wait, then the MFMAs run; the partial tiles are
-// summed by a fixed three-level tree through LDS (waves w and w + 4, then
-// w and w + 2, then 0 and 1).
-constexpr int DU_W = 8, DU_TE = 32;
+// du_H [e][j] = sum_o G[e][o] W_o[o][j] for du_te<NNT>() = 32 du_rt<NNT>()
+// edges per workgroup (each W_o fragment serves du_rt row tiles: 2 for
+// c_H <= 64, else 1 within the register budget).  Wave w of DU_W takes
+// 1/DU_W of the K (output) range for all DU_RT x NNT tiles; its A (G rows) and
+// B (W_o^T rows) fragments of up to DU_KS steps are all in flight before the
+// first wait, then the MFMAs run; the partial tiles are summed by a fixed
+// three-level tree through LDS (waves w and w + 4, then w and w + 2, then 0
+// and 1).
+constexpr int DU_W = 8;
+template <int NNT>
+__host__ __device__ constexpr int du_rt() { return NNT <= 2 ? 2 : 1; }
+template <int NNT>
+__host__ __device__ constexpr int du_te() { return 32 * du_rt<NNT>(); }
 template <class TM, int NNT>
 __global__ __launch_bounds__(DU_W * 64) void radial_du_kernel(Args a) {
   constexpr int CH = 32 * NNT, KC = TM::KC, VEC = TM::VEC;
-  constexpr int DU_KS = NNT <= 2 ? 12 : 6;  // steps in flight (register budget)
+  constexpr int DU_RT = du_rt<NNT>(), DU_TE = du_te<NNT>();
+  constexpr int DU_KS = 6;  // steps in flight (register budget)
   constexpr int SLOT = DU_TE * pitch(CH);
   __shared__ alignas(16) float red[4 * SLOT];
   using raw = typename TM::raw;
@@ -517,21 +524,28 @@ __global__ __launch_bounds__(DU_W * 64) void radial_du_kernel(Args a) {
   const raw* G = reinterpret_cast<const raw*>(a.grad);
   const raw* wot = reinterpret_cast<const raw*>(a.wot);
   const int nks = cout / KC, ks0 = wave * nks / DU_W, kq = (wave + 1) * nks / DU_W - ks0;
-  int e = lane & 31;
-  e = e < nvalid ? e : nvalid - 1;  // in-bounds rows; results of padded edges are not stored
-  const raw* ga = G + (e0 + e) * cout + (lane >> 5) * VEC + ks0 * KC;
+  const raw* ga[DU_RT];
+#pragma unroll
+  for (int rt = 0; rt < DU_RT; ++rt) {
+    int e = 32 * rt + (lane & 31);
+    e = e < nvalid ? e : nvalid - 1;  // in-bounds rows; results of padded edges are not stored
+    ga[rt] = G + (e0 + e) * cout + (lane >> 5) * VEC + ks0 * KC;
+  }
   const raw* gb = wot + static_cast<int64_t>(lane & 31) * cout + (lane >> 5) * VEC + ks0 * KC;
-  f32x16 acc[NNT];
+  f32x16 acc[DU_RT][NNT];
 #pragma unroll
-  for (int nt = 0; nt < NNT; ++nt)
+  for (int rt = 0; rt < DU_RT; ++rt)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[nt][r] = 0.f;
+    for (int nt = 0; nt < NNT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[rt][nt][r] = 0.f;
   for (int c0 = 0; c0 < kq; c0 += DU_KS) {
-    frag_t fa[DU_KS], fb[DU_KS][NNT];
+    frag_t fa[DU_KS][DU_RT], fb[DU_KS][NNT];
 #pragma unroll
     for (int s = 0; s < DU_KS; ++s) {
       const int st = c0 + s < kq ? c0 + s : kq - 1;  // clamped: every load is unconditional
-      fa[s] = *reinterpret_cast<const frag_t*>(ga + st * KC);
+#pragma unroll
+      for (int rt = 0; rt < DU_RT; ++rt) fa[s][rt] = *reinterpret_cast<const frag_t*>(ga[rt] + st * KC);
 #pragma unroll
       for (int nt = 0; nt < NNT; ++nt)
         fb[s][nt] = *reinterpret_cast<const frag_t*>(gb + static_cast<int64_t>(32 * nt) * cout + st * KC);
@@ -540,20 +554,29 @@ __global__ __launch_bounds__(DU_W * 64) void radial_du_kernel(Args a) {
     for (int s = 0; s < DU_KS; ++s)
       if (c0 + s < kq)
 #pragma unroll
-        for (int nt = 0; nt < NNT; ++nt) mfma(acc[nt], fa[s], fb[s][nt], TM{});
+        for (int rt = 0; rt < DU_RT; ++rt)
+#pragma unroll
+          for (int nt = 0; nt < NNT; ++nt) mfma(acc[rt][nt], fa[s][rt], fb[s][nt], TM{});
   }
-  // lane L, register r -> edge 8 (r/4) + 4 (L/32) + r%4, column 32 nt + L%32
+  // lane L, register r of row tile rt -> edge 32 rt + 8 (r/4) + 4 (L/32) + r%4,
+  // column 32 nt + L%32
   auto put = [&](float* slot) {
 #pragma unroll
-    for (int nt = 0; nt < NNT; ++nt)
+    for (int rt = 0; rt < DU_RT; ++rt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) slot[acc_row(r, lane) * pitch(CH) + 32 * nt + (lane & 31)] = acc[nt][r];
+      for (int nt = 0; nt < NNT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          slot[(32 * rt + acc_row(r, lane)) * pitch(CH) + 32 * nt + (lane & 31)] = acc[rt][nt][r];
   };
   auto add = [&](const float* slot) {
 #pragma unroll
-    for (int nt = 0; nt < NNT; ++nt)
+    for (int rt = 0; rt < DU_RT; ++rt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[nt][r] += slot[acc_row(r, lane) * pitch(CH) + 32 * nt + (lane & 31)];
+      for (int nt = 0; nt < NNT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          acc[rt][nt][r] += slot[(32 * rt + acc_row(r, lane)) * pitch(CH) + 32 * nt + (lane & 31)];
   };
   if (wave >= 4) put(red + (wave - 4) * SLOT);
   __syncthreads();
@@ -567,14 +590,16 @@ __global__ __launch_bounds__(DU_W * 64) void radial_du_kernel(Args a) {
   __syncthreads();
   if (wave == 0) {
     add(red);
-    // lane L writes column 32 nt + L%32 of rows acc_row(r, L)
+    // lane L writes column 32 nt + L%32 of rows 32 rt + acc_row(r, L)
 #pragma unroll
-    for (int nt = 0; nt < NNT; ++nt)
+    for (int rt = 0; rt < DU_RT; ++rt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int ee = acc_row(r, lane);
-        if (ee < nvalid) a.duh[(e0 + ee) * CH + 32 * nt + (lane & 31)] = acc[nt][r];
-      }
+      for (int nt = 0; nt < NNT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int ee = 32 * rt + acc_row(r, lane);
+          if (ee < nvalid) a.duh[(e0 + ee) * CH + 32 * nt + (lane & 31)] = acc[rt][nt][r];
+        }
   }
 }
 
@@ -1155,12 +1180,13 @@ static int launch_fwd(const Args& a, int64_t ntiles, hipStream_t s) {
 template <class TM>
 static int launch_du(const Args& a, int64_t ntiles, hipStream_t s) {
   (void)ntiles;
-  const dim3 grid(static_cast<unsigned>((a.E + DU_TE - 1) / DU_TE)), block(DU_W * 64);
+  const dim3 block(DU_W * 64);
+  auto grid = [&](int te) { return dim3(static_cast<unsigned>((a.E + te - 1) / te)); };
   switch (a.c[a.nh] / 32) {
-    case 1: hipLaunchKernelGGL((radial_du_kernel<TM, 1>), grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL((radial_du_kernel<TM, 2>), grid, block, 0, s, a); break;
-    case 3: hipLaunchKernelGGL((radial_du_kernel<TM, 3>), grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL((radial_du_kernel<TM, 4>), grid, block, 0, s, a); break;
+    case 1: hipLaunchKernelGGL((radial_du_kernel<TM, 1>), grid(du_te<1>()), block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((radial_du_kernel<TM, 2>), grid(du_te<2>()), block, 0, s, a); break;
+    case 3: hipLaunchKernelGGL((radial_du_kernel<TM, 3>), grid(du_te<3>()), block, 0, s, a); break;
+    default: hipLaunchKernelGGL((radial_du_kernel<TM, 4>), grid(du_te<4>()), block, 0, s, a); break;
   }
   return check_launch("radial_du_kernel");
 }
