@@ -5,9 +5,10 @@
 // quarter (4 x 4 MFMA 32x32 tiles, accumulators in AGPRs).  Both operands are
 // copied in their natural [edge][channel] layout straight from global memory
 // into a 4-stage LDS ring (global_load_lds, 16-byte chunks XOR-swizzled by
-// edge row), 32 edges per stage, three stages in flight; MFMA operands (8
-// consecutive edges of one channel per lane) come from ds_read_b64_tr_b16,
-// which transposes 4x4 blocks of 16-bit elements across each 16-lane group.
+// edge row so that the transposed reads are free of bank conflicts), 32 edges
+// per stage, three stages in flight; MFMA operands (8 consecutive edges of one
+// channel per lane) come from ds_read_b64_tr_b16, which transposes 4x4 blocks
+// of 16-bit elements across each 16-lane group.
 // fp32: dw_kernel below (register transposes).
 //
 // With Y_e the rotated, radially scaled input rows and dZ_e the rotated output
@@ -206,21 +207,22 @@ __device__ __forceinline__ v4s16 tr_read(const char* lds) {
 }
 
 // One K step on stage (sa, sb): 2 k-substeps x 4 x 4 MFMAs per wave.
-// la, lb: this lane's byte offsets inside the operand tiles (row, chunk and
-// wave-half part); the per-(ks, r, tile) offsets are compile-time.
+// la[t], lb[t]: this lane's byte offsets inside the operand tiles for column
+// tile t (row, swizzled chunk and wave-half part); the per-(ks, r) offsets are
+// compile-time.
 __device__ __forceinline__ void trdw_step(f32x16 (&acc)[4][4], const char* sa, const char* sb,
-                                          int la, int lb) {
+                                          const int (&la)[4], const int (&lb)[4]) {
   using namespace trdw;
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
     bf16x8 af[4], bfr[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      // chunk (within the 512-byte row) of the tile's 32 columns: 4 t + ..., XOR with 4 r
-      v4s16 a0 = tr_read(sa + la + (ks * 16 + 0) * PITCH + (((t >> 1) * 8 + 4 * ((t & 1) ^ 0)) * 16));
-      v4s16 a1 = tr_read(sa + la + (ks * 16 + 4) * PITCH + (((t >> 1) * 8 + 4 * ((t & 1) ^ 1)) * 16));
-      v4s16 b0 = tr_read(sb + lb + (ks * 16 + 0) * PITCH + (((t >> 1) * 8 + 4 * ((t & 1) ^ 0)) * 16));
-      v4s16 b1 = tr_read(sb + lb + (ks * 16 + 4) * PITCH + (((t >> 1) * 8 + 4 * ((t & 1) ^ 1)) * 16));
+      // rows 16 ks + {0, 4} + (lane part) of column tile t
+      v4s16 a0 = tr_read(sa + la[t] + (ks * 16 + 0) * PITCH);
+      v4s16 a1 = tr_read(sa + la[t] + (ks * 16 + 4) * PITCH);
+      v4s16 b0 = tr_read(sb + lb[t] + (ks * 16 + 0) * PITCH);
+      v4s16 b1 = tr_read(sb + lb[t] + (ks * 16 + 4) * PITCH);
       af[t] = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
       bfr[t] = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
     }
@@ -269,7 +271,7 @@ __global__ __launch_bounds__(256, 1) void dw_tr_kernel(DwArgs a) {
   for (int j = 0; j < 4; ++j) {
     const int p = (wave * 4 + j) * 64 + lane;
     dr[j] = p >> 5;
-    dc[j] = ((p & 31) ^ (dr[j] & 7)) * 8;
+    dc[j] = ((p & 31) ^ ((dr[j] & 3) << 2)) * 8;  // LDS chunk s of row r holds chunk s ^ 4 (r % 4)
   }
   // The copies are issued by inline asm, invisible to the compiler's wait
   // insertion (which would otherwise drain the ring before LDS reads it cannot
@@ -290,11 +292,18 @@ __global__ __launch_bounds__(256, 1) void dw_tr_kernel(DwArgs a) {
     }
   };
   // transposed reads: lane (g16 = lane/16, a = lane%4, kk = lane/4%4) addresses row
-  // 8 (g16/2) + 4 r + kk + 16 ks, column 32 t + 16 (g16%2) + 4 a of its wave's half
+  // 8 (g16/2) + 4 r + kk + 16 ks, column 32 t + 16 (g16%2) + 4 a of its wave's half,
+  // i.e. 16-byte chunk c = 4 t + 2 (g16%2) + a/2, stored at chunk c ^ 4 kk: the 4
+  // rows x 4 chunks of one read land in 16 distinct chunks (no bank conflicts)
   const int g16 = lane >> 4, aa = lane & 3, kk = (lane >> 2) & 3;
-  const int lrow = (8 * (g16 >> 1) + kk) * PITCH + (((2 * (g16 & 1) + (aa >> 1)) ^ kk) * 16) + (aa & 1) * 8;
+  const int lrow = (8 * (g16 >> 1) + kk) * PITCH + (2 * (g16 & 1) + (aa >> 1)) * 16 + (aa & 1) * 8;
   const int wm = wave >> 1, wn = wave & 1;
-  const int la = lrow + wm * 256, lb = lrow + wn * 256;  // the wave's 128-column half = 16 chunks
+  int la[4], lb[4];  // the wave's 128-column half = 16 chunks
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    la[t] = lrow + wm * 256 + 64 * (t ^ kk);
+    lb[t] = lrow + wn * 256 + 64 * (t ^ kk);
+  }
 
   f32x16 acc[4][4];
 #pragma unroll
