@@ -363,6 +363,65 @@ def traffic_from(root, dtype):
     return 0
 
 
+def embed_workload(seed=0):
+    """Config-2 edge-degree embedding (EdgeDegreeEmbedding, node mode): radial
+    rows [E, (L+1) C] fp32, Euler angles, the dst plan, x [N, d, C] fp32."""
+    import numpy as np
+    import torch
+    from maloq_amd import message as M
+    from maloq_amd import synth
+    from maloq_amd.wigner import extract_euler_angles
+
+    dev = torch.device("cuda:0")
+    g = synth.config2_graph()
+    L, C = 4, 128
+    gen = torch.Generator().manual_seed(seed)
+    ei = torch.from_numpy(np.stack([g.src, g.dst])).to(dev)
+    plan = M.MessagePlan(ei, g.num_nodes)
+    vec = torch.from_numpy(g.edge_distance_vec()).float().to(dev)
+    eul = extract_euler_angles(vec, seed=1234)
+    u = torch.randn(g.num_edges, (L + 1) * C, generator=gen).to(dev)
+    x = torch.zeros(g.num_nodes, (L + 1) ** 2, C, device=dev)
+    E, N, d = g.num_edges, g.num_nodes, (L + 1) ** 2
+    nbytes = E * (L + 1) * C * 4 + E * 12 + E * 8 + (N + 1) * 8 + 2 * N * d * C * 4
+    return dict(ei=ei, plan=plan, eul=eul, u=u, x=x, L=L, C=C, E=E, N=N, bytes=nbytes, vec=vec)
+
+
+def embed_call(ew):
+    import torch
+    from maloq_amd.embedding import edge_degree_embed
+    with torch.no_grad():
+        edge_degree_embed(ew["x"], ew["u"], ew["ei"], None, ew["L"], 5.0, "node", eulers=ew["eul"], plan=ew["plan"])
+
+
+def cpu_embed_baseline(ew):
+    """The oracle restatement of EdgeDegreeEmbedding.forward (fp32 torch on the
+    host cores: pad, einsum to_m, bmm(wigner_inv), index_add_) on the whole
+    config-2 graph, median of 3; the dense wigner_inv is built once beforehand
+    (not timed), as the reference receives it."""
+    import torch
+    from oracle import embedding as oemb
+    from oracle import rotation as orot
+    from oracle.so3 import CoefficientMapping
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    L = ew["L"]
+    e = ew["eul"].cpu()
+    winv = orot.eulers_to_wigner((e[:, 0], e[:, 1], e[:, 2]), 0, L, orot.load_jd(torch.float32)).transpose(1, 2)
+    winv = winv.contiguous()
+    mapping = CoefficientMapping(L, 2)
+    mask = CoefficientMapping(L, L).coefficient_idx(L, 2)
+    u, ei, x = ew["u"].cpu(), ew["ei"].cpu(), ew["x"].cpu().zero_()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        oemb.edge_degree_embedding(x, u, ei, winv, mapping, mask, 5.0, "node")
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    return {"value": ew["E"] / t, "unit": "edges/s", "cores": cores, "kind": "port",
+            "sample": f"config 2, whole graph ({ew['E']} edges), fp32 torch CPU, median of 3"}
+
+
 def profile_only(args):
     """Runs one piece of the path --reps times (for rocprofv3 passes)."""
     import torch
@@ -372,6 +431,10 @@ def profile_only(args):
         b = torch.empty_like(a)
         for _ in range(args.reps):
             b.copy_(a)
+    elif args.only == "embed":
+        ew = embed_workload()
+        for _ in range(args.reps):
+            embed_call(ew)
     elif args.only in ("fwd", "step"):
         w = message_workload(args.dtype)
         if args.only == "fwd":
@@ -403,7 +466,7 @@ def main(argv=None):
     ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp32"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-extras", action="store_true", help="headline only")
-    ap.add_argument("--only", choices=["fwd", "step", "basis", "copy"],
+    ap.add_argument("--only", choices=["fwd", "step", "basis", "copy", "embed"],
                     help="profiling mode: run one piece a few times and exit (no JSON line)")
     ap.add_argument("--reps", type=int, default=5, help="launches in --only mode")
     ap.add_argument("--traffic-from", metavar="DIR",
@@ -476,11 +539,31 @@ def main(argv=None):
                          "unit": "GB/s", "frac": bpb * bw["n_blocks"] / tf / PEAK_HBM,
                          "bytes_per_block": bpb, "traffic": load_traffic("fock_to_irreps")},
         }
+        print("[bench] edge-degree embedding (config 2) ...", file=sys.stderr, flush=True)
+        ew = embed_workload()
+        s = torch.cuda.current_stream()
+        embed_call(ew)
+        s.synchronize()
+        a_ev, b_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a_ev.record(s)
+        for _ in range(20):
+            embed_call(ew)
+        b_ev.record(s)
+        b_ev.synchronize()
+        te = a_ev.elapsed_time(b_ev) / 1e3 / 20
+        result["edge_degree_embedding"] = {
+            "metric": "edges/s", "value": ew["E"] / te, "us_per_call": te * 1e6,
+            "config": "config 2 node mode, fp32 radial rows, D from Euler angles",
+            "roofline": {"kernel": "edge_degree_node_kernel<4>", "bound": "hbm",
+                         "achieved": ew["bytes"] / te / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                         "frac": ew["bytes"] / te / PEAK_HBM, "bytes_per_call": ew["bytes"]},
+        }
     if not args.no_cpu:
         print("[bench] CPU baseline ...", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_message_baseline()
         if not args.no_extras:
             result["basis_transform"]["cpu_baseline"] = cpu_basis_baseline(bw)
+            result["edge_degree_embedding"]["cpu_baseline"] = cpu_embed_baseline(ew)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -250,6 +250,44 @@ int64_t maloq_message_colsum_partials_floats(int nrows, int c, int64_t num_edges
 int maloq_message_colsum(int dtype, const void* rows, int rows_per_edge, int row0, int nrows, int c,
                          int64_t num_edges, float* partials, float* out, void* stream);
 
+/* ----------------------------------------------------- edge-degree embedding -- */
+
+/* EdgeDegreeEmbedding.forward (helm/nn/embedding.py:82-141): with u the
+ * RadialMLP output [E, (lmax+1) C] (the m = 0 coefficient of every degree l),
+ *   emb_e[l^2 + j][c] = D^l_e[l][j] u_e[l][c]   (j = 0 .. 2l)
+ * which is the reference's zero padding + einsum(to_m) + bmm(wigner_inv): only
+ * the (l^2 + l)-th column of each block of wigner_inv = D^T meets a non-zero.
+ *
+ * maloq_edge_m0_rows: rows [E, d] fp32, rows[e][l^2 + j] = D^l_e[l][j] (the m = 0
+ * row of each block), from exactly one of wigner_inv [E, d, d] fp32 (the
+ * reference's input) or eulers [E, 3] fp32 (the (alpha, beta, gamma) triple
+ * of maloq_edge_euler) with jd (packed J_l blocks), computing the m = 0 rows
+ * with the dense kernel's recurrence (bit-identical to its D).  lmax 0-6. */
+int maloq_edge_m0_rows(int lmax, int64_t num_edges, const float* wigner_inv, const float* eulers,
+                       const float* jd, float* rows, void* stream);
+
+/* Node mode (edge_out == NULL): x[dst_e] += emb_e / rescale for every edge, in
+ * place, x [num_nodes, d, C]; the embedding is rounded to the dtype of x (as
+ * the reference casts it) and multiplied by 1 / rescale (within one rounding
+ * of the reference's division); edges are visited per node in the order
+ * seg_ptr / perm give (dst-sorted, stable: the order of index_add_), summed in
+ * fp32 on top of x and stored once.  Edge mode: edge_out [E, d, C] = emb_e in
+ * the dtype of x (no rescale), x untouched.  u_dtype / x_dtype: 0 fp32,
+ * 1 bf16; channels 1-256.  Deterministic, no atomics. */
+int maloq_edge_degree_embed(int u_dtype, int x_dtype, int lmax, const void* u, int64_t num_edges,
+                            int channels, const float* rows, const int64_t* seg_ptr, const int64_t* perm,
+                            int64_t num_nodes, float rescale, void* x, void* edge_out, void* stream);
+
+/* Gradient of the embedding with respect to u (the autograd backward of the
+ * reference's einsum + bmm + index_add_):
+ *   grad_u[e][l C + c] = scale sum_j D^l_e[l][j] grad[row_e][l^2 + j][c],
+ * row_e = grad_rows[e] (node mode: the dst of edge e, scale = 1 / rescale) or
+ * e (grad_rows NULL: edge mode, scale 1).  grad [*, d, C] (g_dtype 0 fp32,
+ * 1 bf16), grad_u [E, (lmax+1) C] fp32, rows from maloq_edge_m0_rows. */
+int maloq_edge_degree_embed_bwd(int g_dtype, int lmax, const void* grad, const int64_t* grad_rows,
+                                int64_t num_edges, int channels, const float* rows, float scale, float* grad_u,
+                                void* stream);
+
 /* ------------------------------------------------------------ RadialMLP -- */
 
 /* The radial function of SO2_Convolution: RadialMLP(channels_list)

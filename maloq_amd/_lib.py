@@ -47,6 +47,9 @@ SIGNATURES = {
     "maloq_message_pack": [_i32, _i32, _p, _p, _p, _i64, _p, _p],
     "maloq_message_colsum_partials_floats": [_i32, _i32, _i64],
     "maloq_message_colsum": [_i32, _p, _i32, _i32, _i32, _i32, _i64, _p, _p, _p],
+    "maloq_edge_m0_rows": [_i32, _i64, _p, _p, _p, _p, _p],
+    "maloq_edge_degree_embed": [_i32, _i32, _i32, _p, _i64, _i32, _p, _p, _p, _i64, ctypes.c_float, _p, _p, _p],
+    "maloq_edge_degree_embed_bwd": [_i32, _i32, _p, _p, _i64, _i32, _p, ctypes.c_float, _p, _p],
     "maloq_radial_pack_bytes": [_i32, _i32, _i32],
     "maloq_radial_fwd": [_i32, _i32, _p, _p, _i64, _p, _p, _p, _p, ctypes.c_float, _p, _p, _p, _p, _p, _p],
     "maloq_radial_bwd_partials_floats": [_i32, _i32, _p, _i64],
