@@ -537,6 +537,8 @@ struct Gemm {
     const int64_t rw = rad_width<L, M>(a.C_n);
     const int co = lane & 31, h = lane >> 5;
     const int c0 = cb * CB + h * 16;  // first channel of this lane in row layout
+    constexpr int VEC = TM::VEC;      // channels per 16-byte piece
+    constexpr int NU = 16 / VEC;      // 16-byte pieces per 16 channels
     static_for<RT>([&](auto RTI) {
       constexpr int rt = decltype(RTI)::value;
       constexpr int sb = P::tab.base[lo] + rt * P::ntype(lo);
@@ -549,6 +551,16 @@ struct Gemm {
         constexpr int q0 = m == 0 ? 0 : 2 * m - 1, nqm = m == 0 ? 1 : 2;
         const typename TM::raw* radp = reinterpret_cast<const typename TM::raw*>(a.rad) + eis * rw +
                                        rad_slot<L, M>(q0, lo, c0, a.C_n);
+        // bf16: this lane's 16 channels of the radial slot, and below of each R
+        // row, issued before the LDS round trips that transpose the block (one
+        // memory latency per block rather than one per 4 channels); fp32 (twice
+        // the registers) loads them where they are used
+        constexpr bool PF = sizeof(typename TM::raw) == 2;
+        uint4 rv_u[NU];
+        if constexpr (PF) {
+#pragma unroll
+          for (int k = 0; k < NU; ++k) rv_u[k] = reinterpret_cast<const uint4*>(radp)[k];
+        }
         float dr[16];
 #pragma unroll
         for (int k = 0; k < 16; ++k) dr[k] = 0.f;
@@ -556,22 +568,36 @@ struct Gemm {
           constexpr int q = q0 + decltype(QI)::value;
           constexpr int slot = sb + P::qtype(q, lo);
           __builtin_amdgcn_sched_barrier(0);  // one block at a time (register pressure)
+          uint4 rr_u[NU];
+          if constexpr (PF) {
+#pragma unroll
+            for (int k = 0; k < NU; ++k) rr_u[k] = reinterpret_cast<const uint4*>(rsave + P::mrow(q, lo) * a.C_n)[k];
+          }
           // accumulator layout -> row layout
 #pragma unroll
           for (int i = 0; i < 16; ++i) tb[tsw(8 * (i >> 2) + 4 * h + (i & 3), co)] = acc[slot][i];
           wave_sync();
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {  // 4 channels at a time (register pressure)
-            float rr[4], rv[4];
-            load_vec<TM, 4>(rsave + P::mrow(q, lo) * a.C_n + 4 * g, rr);
-            load_vec<TM, 4>(radp + 4 * g, rv);
-            float4 t4 = *reinterpret_cast<const float4*>(tb + tsw(co, 16 * h + 4 * g));
-            dr[4 * g] = fmaf(t4.x, rr[0], dr[4 * g]);
-            dr[4 * g + 1] = fmaf(t4.y, rr[1], dr[4 * g + 1]);
-            dr[4 * g + 2] = fmaf(t4.z, rr[2], dr[4 * g + 2]);
-            dr[4 * g + 3] = fmaf(t4.w, rr[3], dr[4 * g + 3]);
-            t4.x *= rv[0]; t4.y *= rv[1]; t4.z *= rv[2]; t4.w *= rv[3];
-            *reinterpret_cast<float4*>(tb + tsw(co, 16 * h + 4 * g)) = t4;
+          for (int g = 0; g < NU; ++g) {  // VEC channels at a time
+            float rr[VEC], rv[VEC];
+            if constexpr (PF) {
+              unpack_vec<TM, VEC>(rr_u[g], rr);
+              unpack_vec<TM, VEC>(rv_u[g], rv);
+            } else {
+              unpack_vec<TM, VEC>(reinterpret_cast<const uint4*>(rsave + P::mrow(q, lo) * a.C_n)[g], rr);
+              unpack_vec<TM, VEC>(reinterpret_cast<const uint4*>(radp)[g], rv);
+            }
+#pragma unroll
+            for (int g4 = 0; g4 < VEC / 4; ++g4) {
+              const int cc = VEC * g + 4 * g4;
+              float4 t4 = *reinterpret_cast<const float4*>(tb + tsw(co, 16 * h + cc));
+              dr[cc] = fmaf(t4.x, rr[4 * g4], dr[cc]);
+              dr[cc + 1] = fmaf(t4.y, rr[4 * g4 + 1], dr[cc + 1]);
+              dr[cc + 2] = fmaf(t4.z, rr[4 * g4 + 2], dr[cc + 2]);
+              dr[cc + 3] = fmaf(t4.w, rr[4 * g4 + 3], dr[cc + 3]);
+              t4.x *= rv[4 * g4]; t4.y *= rv[4 * g4 + 1]; t4.z *= rv[4 * g4 + 2]; t4.w *= rv[4 * g4 + 3];
+              *reinterpret_cast<float4*>(tb + tsw(co, 16 * h + cc)) = t4;
+            }
           }
           wave_sync();
 #pragma unroll
