@@ -422,6 +422,53 @@ def cpu_embed_baseline(ew):
             "sample": f"config 2, whole graph ({ew['E']} edges), fp32 torch CPU, median of 3"}
 
 
+def edgewise_flops_per_edge(L, M, c, h):
+    """Algorithmic FLOPs per edge of the two-convolution Edgewise forward:
+    rotation of the 2c-channel message, gated SO(2) 2c -> h (plus the L h gate
+    rows of m = 0), SO(2) h -> c, inverse rotation, segment sum."""
+    rot = sum(min(2 * l + 1, 2 * M + 1) * (2 * l + 1) for l in range(L + 1))
+    m_side = sum(4 * (L - m + 1) ** 2 for m in range(1, M + 1))
+    mac1 = (L + 1) * 2 * c * (2 * L + 1) * h + m_side * 2 * c * h
+    mac2 = (L + 1) ** 2 * h * c + m_side * h * c
+    return 2 * (rot * 2 * c + mac1 + mac2 + rot * c) + (L + 1) ** 2 * c
+
+
+def edgewise_workload(seed=0):
+    """Config-2 graph through Edgewise (message_type "source-target"): x [N, 25,
+    128] bf16, conv1 256 -> 128 gated with radial scales, conv2 128 -> 128."""
+    import torch
+    from maloq_amd import message as M
+    w = message_workload("bf16", seed)
+    dev, L, Mm, C = w["x"].device, w["L"], w["M"], w["C"]
+    H = C
+    gen = torch.Generator().manual_seed(seed + 1)
+
+    def conv(c_in, c_out, extra):
+        k0 = (L + 1) * c_in
+        w0 = (torch.randn((L + 1) * c_out + extra, k0, generator=gen) / math.sqrt(k0)).to(dev)
+        b0 = (torch.randn((L + 1) * c_out + extra, generator=gen) * 0.1).to(dev)
+        wm = [(torch.randn(2 * (L - m + 1) * c_out, (L - m + 1) * c_in, generator=gen)
+               / math.sqrt((L - m + 1) * c_in)).to(dev) for m in range(1, Mm + 1)]
+        return w0, b0, wm
+    c1, c2 = conv(2 * C, H, L * H), conv(H, C, 0)
+    wp1 = M.pack_weights(c1[0], c1[2], L, Mm, True, 2 * C, H, torch.bfloat16, 0)
+    wp2 = M.pack_weights(c2[0], c2[2], L, Mm, False, H, C, torch.bfloat16, 0)
+    with torch.no_grad():
+        from maloq_amd.wigner import extract_euler_angles
+        eul = extract_euler_angles(w["vec"], seed=1234)
+        rad = (torch.rand(w["E"], M.rad_width(L, Mm, 2 * C), generator=gen) + 0.5).to(dev, torch.bfloat16)
+    return dict(x=w["x"].detach(), plan=w["plan"], eul=eul, rad=rad, c1=c1, c2=c2, wp1=wp1, wp2=wp2,
+                L=L, M=Mm, C=C, H=H, E=w["E"])
+
+
+def edgewise_call(ew):
+    import torch
+    from maloq_amd import message as M
+    with torch.no_grad():
+        return M.edgewise_forward(ew["x"], ew["plan"], ew["eul"], ew["rad"], ew["c1"], ew["c2"], ew["L"], ew["M"],
+                                  wpack1=ew["wp1"], wpack2=ew["wp2"])
+
+
 def profile_only(args):
     """Runs one piece of the path --reps times (for rocprofv3 passes)."""
     import torch
@@ -435,6 +482,10 @@ def profile_only(args):
         ew = embed_workload()
         for _ in range(args.reps):
             embed_call(ew)
+    elif args.only == "edgewise":
+        ew = edgewise_workload()
+        for _ in range(args.reps):
+            edgewise_call(ew)
     elif args.only in ("fwd", "step"):
         w = message_workload(args.dtype)
         if args.only == "fwd":
@@ -466,7 +517,7 @@ def main(argv=None):
     ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp32"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-extras", action="store_true", help="headline only")
-    ap.add_argument("--only", choices=["fwd", "step", "basis", "copy", "embed"],
+    ap.add_argument("--only", choices=["fwd", "step", "basis", "copy", "embed", "edgewise"],
                     help="profiling mode: run one piece a few times and exit (no JSON line)")
     ap.add_argument("--reps", type=int, default=5, help="launches in --only mode")
     ap.add_argument("--traffic-from", metavar="DIR",
@@ -558,6 +609,19 @@ def main(argv=None):
                          "achieved": ew["bytes"] / te / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                          "frac": ew["bytes"] / te / PEAK_HBM, "bytes_per_call": ew["bytes"]},
         }
+        print("[bench] Edgewise two convolutions (config 2) ...", file=sys.stderr, flush=True)
+        gw = edgewise_workload()
+        edgewise_call(gw)
+        tg = kernel_time_events(lambda: edgewise_call(gw), 20)
+        fl = edgewise_flops_per_edge(gw["L"], gw["M"], gw["C"], gw["H"]) * gw["E"]
+        result["edgewise_two_conv_fwd"] = {
+            "metric": "edges/s", "value": gw["E"] / tg, "us_per_call": tg * 1e6,
+            "config": "config 2 graph, cat(x[src], x[dst]) 256 -> gated 128 -> 128 channels, bf16, forward",
+            "roofline": {"scope": "whole call (prep, two GEMMs, fixup)", "bound": "mfma",
+                         "achieved": fl / tg / 1e12, "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
+                         "frac": fl / tg / PEAK_BF16, "flops_per_call": fl},
+        }
+        del gw
     if not args.no_cpu:
         print("[bench] CPU baseline ...", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_message_baseline()

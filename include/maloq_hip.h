@@ -189,6 +189,26 @@ int maloq_message_fwd(int dtype, int lmax, int mmax, int gate, const void* x, in
                       const int64_t* seg_ptr, float* partials, void* y_ws, void* r_ws,
                       float* dk_ws, void* gate_ws, void* stream);
 
+/* Two-convolution message block (forward, node output), as Edgewise.forward_node
+ * with message_type "source-target" (helm/esen_block.py:146-208, convolutions
+ * :85-106): per dst-sorted edge e, m_e = cat(x[src[e]], x[dst[e]]) (2 c_x channels),
+ *   z_e = Gate(SO2_1(rad[e] (*) to_m D_e m_e))   (c_hidden channels, edge frame),
+ *   out[n] = sum_{e: dst[e]=n} D_e^T to_m^T SO2_2(z_e)   (c_out channels),
+ * SO2_1 gated (wpack1/bias1 packed as for maloq_message_fwd with gate = 1, input
+ * 2 c_x), SO2_2 without radial scale or gate (wpack2/bias2, input c_hidden).
+ * Workspaces: y_ws [E, d', 2 c_x], z_ws [E, d', c_hidden] (dtype), dk_ws
+ * [E, maloq_message_wigner_floats], partials maloq_message_partials_floats(lmax, 0,
+ * E, c_out) floats; gate_ws (nullable) [E, d' + lmax, c_hidden] receives the
+ * first convolution's pre-activations.  c_x a multiple of 8.  Replaces the
+ * forward of Edgewise.forward_node (esen_block.py:146-208). */
+int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const void* x, int c_x,
+                               const int32_t* src, const int32_t* dst, int64_t num_edges,
+                               const float* eulers, const void* rad, const void* wpack1,
+                               const float* bias1, int c_hidden, const void* wpack2,
+                               const float* bias2, const float* jd, float* out, int64_t num_nodes,
+                               int c_out, const int64_t* seg_ptr, float* partials, void* y_ws,
+                               float* dk_ws, void* gate_ws, void* z_ws, void* stream);
+
 /* Input and radial-scale gradients of the fused block:
  *   grad_x[n] = sum_{e: src[e]=n} D_e^T rad[e] (*) SO2^T(G_e),
  *   grad_rad[e] = SO2^T(G_e) (*) R_e   (R_e = D_e x[src[e]]),

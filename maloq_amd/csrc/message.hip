@@ -164,6 +164,57 @@ extern "C" int maloq_message_fwd(int dtype, int lmax, int mmax, int gate, const 
   return fixup(seg_ptr, num_nodes, partials, out, d * c_out, tile_edges(lmax, gate), s);
 }
 
+extern "C" int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const void* x, int c_x,
+                                          const int32_t* src, const int32_t* dst, int64_t num_edges,
+                                          const float* eulers, const void* rad, const void* wpack1,
+                                          const float* bias1, int c_hidden, const void* wpack2,
+                                          const float* bias2, const float* jd, float* out,
+                                          int64_t num_nodes, int c_out, const int64_t* seg_ptr,
+                                          float* partials, void* y_ws, float* dk_ws, void* gate_ws,
+                                          void* z_ws, void* stream) {
+  MALOQ_REQUIRE(c_x > 0 && c_x % 8 == 0, "node channels must be a positive multiple of 8");
+  int rc = check_common(dtype, lmax, mmax, 2 * c_x, c_hidden, num_edges);
+  if (rc) return rc;
+  rc = check_common(dtype, lmax, mmax, c_hidden, c_out, num_edges);
+  if (rc) return rc;
+  MALOQ_REQUIRE(num_nodes >= 0, "num_nodes < 0");
+  MALOQ_REQUIRE(out && seg_ptr && jd && wpack1 && wpack2, "null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t d = static_cast<int64_t>(lmax + 1) * (lmax + 1);
+  const int kc = dtype == 1 ? BF16::KC : F32::KC;
+  if (num_edges > 0) {
+    MALOQ_REQUIRE(x && src && dst && eulers && partials && y_ws && dk_ws && z_ws, "null pointer");
+    // rotated message rows of cat(x[src], x[dst]) (radial scale applied) and the Wigner rows
+    PrepArgs p{};
+    p.x = x; p.gidx = src; p.gidx2 = dst; p.x_c = c_x; p.eidx = nullptr; p.eulers = eulers;
+    p.rad = rad; p.jd = jd; p.y = y_ws; p.r = nullptr; p.dk = dk_ws; p.build_d = 1;
+    p.E = num_edges; p.C = 2 * c_x;
+    rc = prep_dispatch(lmax, mmax, dtype, FWD, p, s);
+    if (rc) return rc;
+    // first convolution + gate, kept in the edge frame
+    Args a{};
+    a.a_src = y_ws; a.dk = dk_ws; a.seg = dst; a.eidx = nullptr;
+    a.wpack = static_cast<const char*>(wpack1); a.bias = bias1; a.out = out; a.part = partials;
+    a.E = num_edges; a.C_k = 2 * c_x; a.C_n = c_hidden; a.n_cb = c_hidden / CB;
+    a.extra = lmax * c_hidden;
+    a.ntiles = (num_edges + tile_edges(lmax, 1) - 1) / tile_edges(lmax, 1);
+    a.frags_per_cb = frags_per_cb(lmax, mmax, 1, 2 * c_x, kc);
+    a.gsave = gate_ws; a.zout = z_ws;
+    rc = dispatch(lmax, mmax, dtype, 1, FWD_EDGE, a, s);
+    if (rc) return rc;
+    // second convolution, rotation back and segment sum
+    Args b{};
+    b.a_src = z_ws; b.dk = dk_ws; b.seg = dst; b.eidx = nullptr;
+    b.wpack = static_cast<const char*>(wpack2); b.bias = bias2; b.out = out; b.part = partials;
+    b.E = num_edges; b.C_k = c_hidden; b.C_n = c_out; b.n_cb = c_out / CB; b.extra = 0;
+    b.ntiles = (num_edges + tile_edges(lmax, 0) - 1) / tile_edges(lmax, 0);
+    b.frags_per_cb = frags_per_cb(lmax, mmax, 0, c_hidden, kc);
+    rc = dispatch(lmax, mmax, dtype, 0, FWD, b, s);
+    if (rc) return rc;
+  }
+  return fixup(seg_ptr, num_nodes, partials, out, d * c_out, tile_edges(lmax, 0), s);
+}
+
 extern "C" int maloq_message_bwd_dx(int dtype, int lmax, int mmax, int gate, const float* grad_out,
                                     int c_out, const int32_t* dst_by_src,
                                     const int32_t* src_sorted, const int32_t* edge_idx,

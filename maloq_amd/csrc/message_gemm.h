@@ -45,7 +45,7 @@ struct GPlan {
   static constexpr int TE = 32 * RT;
   static constexpr int NT = NW * 64;
   static_assert(TE <= 64, "segment masks are 64-bit");
-  static constexpr bool BWD = MODE != 0;
+  static constexpr bool BWD = MODE == 1;  // BWD_DX
   static constexpr int gt(int l) { return (GATE && !BWD && l >= 1) ? 1 : 0; }   // output gate row
   static constexpr int gin(int l) { return (GATE && BWD && l >= 1) ? 1 : 0; }   // input gate row
   static constexpr int nq(int l) { return 1 + 2 * cmin(M, l); }
@@ -317,7 +317,7 @@ struct Gemm {
           constexpr int rt = decltype(R)::value;
           constexpr int sb = P::tab.base[lo] + rt * P::ntype(lo);
           constexpr int sp = sb + P::qtype(2 * m - 1, lo), sm = sb + P::qtype(2 * m, lo);
-          if constexpr (MODE == FWD) {
+          if constexpr (MODE != BWD_DX) {
             mfma(acc[sm], ap[rt], wi, TM{});
             mfma(acc[sm], am[rt], wr, TM{});
             mfma(acc[sp], ap[rt], wr, TM{});
@@ -331,7 +331,7 @@ struct Gemm {
         static_for<RT>([&](auto R) {
           constexpr int rt = decltype(R)::value;
           constexpr int sb = P::tab.base[lo] + rt * P::ntype(lo);
-          if constexpr (MODE == FWD)
+          if constexpr (MODE != BWD_DX)
             mfma(acc[sb + P::qtype(2 * m - 1, lo)], am[rt], nwi, TM{});
           else
             mfma(acc[sb + P::qtype(2 * m, lo)], ap[rt], nwi, TM{});
@@ -460,18 +460,22 @@ struct Gemm {
   // Gated forward: the pre-activation rows of degree lo (kept rows and the gate
   // row) to a.gsave [edge id][d' + L][C_n], each 32 x 32 block transposed
   // through the wave's LDS tile so that a lane stores 16 channels of one edge.
-  template <int lo>
+  // ZOUT: the activated kept rows (no gate rows) to a.zout [edge id][d'][C_n]
+  // instead (the edge-frame output of FWD_EDGE).
+  template <int lo, bool ZOUT = false>
   static __device__ __forceinline__ void save_pre(const f32x16 (&acc)[P::MSLOT], const Smem& s,
                                                   const Args& a, int cb, float* tb, int lane) {
     const int co = lane & 31, h = lane >> 5;
+    constexpr int RPE = ZOUT ? P::DP : P::DP + L;  // rows per edge of the destination
     static_for<RT>([&](auto RTI) {
       constexpr int rt = decltype(RTI)::value;
       constexpr int sb = P::tab.base[lo] + rt * P::ntype(lo);
       const int ei = s.eid[rt * 32 + co];
-      typename TM::raw* g = reinterpret_cast<typename TM::raw*>(a.gsave) +
-                            static_cast<int64_t>(ei >= 0 ? ei : 0) * (P::DP + L) * a.C_n + cb * CB + 16 * h;
+      typename TM::raw* g = reinterpret_cast<typename TM::raw*>(ZOUT ? a.zout : a.gsave) +
+                            static_cast<int64_t>(ei >= 0 ? ei : 0) * RPE * a.C_n + cb * CB + 16 * h;
       static_for<P::ntype(lo)>([&](auto TI) {
         constexpr int t = decltype(TI)::value;  // accumulator type: 0, [gate], +1, -1, ...
+        if constexpr (ZOUT && P::gt(lo) && t == 1) return;
         constexpr int row = (P::gt(lo) && t == 1) ? P::DP + lo - 1
                                                   : P::mrow(t == 0 ? 0 : t - P::gt(lo), lo);
 #pragma unroll
@@ -735,7 +739,7 @@ struct Gemm {
     static_for<L + 1>([&](auto LO) {
       constexpr int lo = decltype(LO)::value;
       if constexpr (P::tab.owner[lo] == W) {
-        if constexpr (MODE == FWD) {
+        if constexpr (MODE != BWD_DX) {
           add_bias<lo>(acc, a, col);
           if constexpr (GATE) {
             if (a.gsave != nullptr)
@@ -746,9 +750,13 @@ struct Gemm {
         } else if constexpr (RAD)
           radial<lo>(acc, s, a, cb,
                      reinterpret_cast<float*>((wave < 2 ? st0 : st1) + (wave & 1) * PW), lane);
-        rotate_sum<W, lo>(acc, s, wsh, a, cb,
-                          reinterpret_cast<float*>((wave < 2 ? st0 : st1) + (wave & 1) * PW),
-                          lane, endmask);
+        if constexpr (MODE == FWD_EDGE)
+          save_pre<lo, true>(acc, s, a, cb,
+                             reinterpret_cast<float*>((wave < 2 ? st0 : st1) + (wave & 1) * PW), lane);
+        else
+          rotate_sum<W, lo>(acc, s, wsh, a, cb,
+                            reinterpret_cast<float*>((wave < 2 ? st0 : st1) + (wave & 1) * PW),
+                            lane, endmask);
       }
     });
   }
@@ -804,7 +812,8 @@ struct Gemm {
     // complete it long before the epilogue reads it.  Chunk i = 64 (k NW + w) +
     // lane is instruction k of wave w; lanes past the tile read an in-bounds row
     // into the padding; rows of edges past the tile are never stored.
-    {
+    // FWD_EDGE does not rotate back: no rows.
+    if constexpr (MODE != FWD_EDGE) {
       constexpr int R4 = P::WS / 4;
       const float4* dk4 = reinterpret_cast<const float4*>(a.dk);
       const int wv = __builtin_amdgcn_readfirstlane(wave), lane = tid & 63;

@@ -154,7 +154,10 @@ struct PairLayout {
   static constexpr int at(int l, int q, int j) { return woff(l) + (j >> 1) * pblk(l) + 2 * q + (j & 1); }
 };
 
-enum Mode { FWD = 0, BWD_DX = 1 };
+// FWD_EDGE: the forward GEMM whose gated output rows stay in the edge frame
+// (Args::zout) for a second SO(2) convolution, instead of being rotated back
+// and summed per node.
+enum Mode { FWD = 0, BWD_DX = 1, FWD_EDGE = 2 };
 
 struct Args {
   const void* a_src;      // [E_all, d', C_k] (TM raw): rotated rows, m-major, by edge id
@@ -177,6 +180,8 @@ struct Args {
   int64_t frags_per_cb;   // packed fragments per output-channel block
   void* gsave;            // FWD gated: [E_all, d' + L, C_n] (TM raw) pre-activation rows and
                           // gate rows, nullable; BWD_DX gated: a_src has d' + L rows
+  void* zout;             // FWD_EDGE: [E_all, d', C_n] (TM raw) output rows (gated, m-major),
+                          // written in place of the inverse rotation and segment sum
 };
 
 template <int L, int M>
@@ -237,6 +242,9 @@ struct PrepArgs {
   const void* gsave;    // gated input gradient: the forward's pre-activation rows
                         // [E_all, d' + L, C] (TM raw); y then gets d' + L rows per edge:
                         // dL/dpre of the kept rows, then dL/dgate of degrees 1..L
+  const int32_t* gidx2; // nullable: second gather row per edge (concatenated message
+                        // [x[gidx] | x[gidx2]]: channels >= x_c come from x[gidx2])
+  int x_c;              // channels of an x row (0: C)
 };
 
 template <class TX, int V>
@@ -323,6 +331,7 @@ struct Prep {
     alignas(16) float D[TE * WS];
     float eul[TE * 3];
     int gid[TE];
+    int gid2[TE];
     int eid[TE];
     float m2[TE * (2 * L + 1) * (2 * L + 1)];
     float trig[TE * 3 * 2 * (L + 1)];
@@ -452,6 +461,7 @@ struct Prep {
       const int ei = v ? (a.eidx ? a.eidx[p] : static_cast<int>(p)) : -1;
       s.eid[tid] = ei;
       s.gid[tid] = v ? a.gidx[p] : 0;
+      s.gid2[tid] = (v && a.gidx2) ? a.gidx2[p] : 0;
       for (int k = 0; k < 3; ++k)
         s.eul[tid * 3 + k] = (v && a.build_d) ? a.eulers[static_cast<int64_t>(ei) * 3 + k] : 0.f;
     }
@@ -482,11 +492,14 @@ struct Prep {
       run_gated_bwd(s, a, nvalid, tid);
       return;
     }
+    // concatenated message: channels [0, xc) from x[gidx], [xc, C) from x[gidx2]
+    const int xc = a.x_c > 0 ? a.x_c : a.C;
     for (int u = tid; u < nvalid * nch; u += NT) {
       const int e = u / nch, c0 = (u - e * nch) * V;
       const int64_t eid = s.eid[e];
+      const bool hi = c0 >= xc;
       const typename TX::raw* xg = reinterpret_cast<const typename TX::raw*>(a.x) +
-                                   static_cast<int64_t>(s.gid[e]) * d * a.C + c0;
+                                   static_cast<int64_t>(hi ? s.gid2[e] : s.gid[e]) * d * xc + (hi ? c0 - xc : c0);
       typename TM::raw* yo = reinterpret_cast<typename TM::raw*>(a.y) + eid * P::DP * a.C + c0;
       typename TM::raw* ro = a.r ? reinterpret_cast<typename TM::raw*>(a.r) + eid * P::DP * a.C + c0 : nullptr;
       const typename TM::raw* rp = a.rad ? reinterpret_cast<const typename TM::raw*>(a.rad) + eid * rw + c0 : nullptr;
@@ -503,7 +516,7 @@ struct Prep {
         constexpr int n = 2 * l + 1;
         float xv[n][V];
 #pragma unroll
-        for (int j = 0; j < n; ++j) load_vec<TX, V>(xg + (l * l + j) * a.C, xv[j]);
+        for (int j = 0; j < n; ++j) load_vec<TX, V>(xg + (l * l + j) * xc, xv[j]);
         const float* Dl = s.D + e * WS;
 #pragma unroll
         for (int q = 0; q < P::nq(l); ++q) {

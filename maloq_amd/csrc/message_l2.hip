@@ -6,8 +6,10 @@ namespace msg {
 
 // GEMM kernels: defined in message_l2_<dtype>_<mode>.hip
 MALOQ_GEMM_INSTANCES(extern, 2, 2, BF16, FWD)
+MALOQ_GEMM_EDGE_INSTANCES(extern, 2, 2, BF16)
 MALOQ_GEMM_INSTANCES(extern, 2, 2, BF16, BWD_DX)
 MALOQ_GEMM_INSTANCES(extern, 2, 2, F32, FWD)
+MALOQ_GEMM_EDGE_INSTANCES(extern, 2, 2, F32)
 MALOQ_GEMM_INSTANCES(extern, 2, 2, F32, BWD_DX)
 
 int launch_l2(int mmax, int dtype, int gate, int mode, const Args& a, hipStream_t s) {

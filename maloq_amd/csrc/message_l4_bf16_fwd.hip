@@ -5,6 +5,7 @@ namespace maloq {
 namespace msg {
 
 MALOQ_GEMM_INSTANCES(, 4, 2, BF16, FWD)
+MALOQ_GEMM_EDGE_INSTANCES(, 4, 2, BF16)
 
 }  // namespace msg
 }  // namespace maloq

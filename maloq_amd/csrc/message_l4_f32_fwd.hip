@@ -5,6 +5,7 @@ namespace maloq {
 namespace msg {
 
 MALOQ_GEMM_INSTANCES(, 4, 2, F32, FWD)
+MALOQ_GEMM_EDGE_INSTANCES(, 4, 2, F32)
 
 }  // namespace msg
 }  // namespace maloq

@@ -20,8 +20,8 @@ inline int tile_edges(int lmax, int gate) { return (lmax <= 4 && !gate) ? 64 : 3
 template <int L, int M, bool GATE, class TM, int MODE, int KR>
 void launch_kr(const Args& a, dim3 g, dim3 b, hipStream_t s) {
   constexpr int NW = Cfg<L, GATE>::NW, RT = Cfg<L, GATE>::RT;
-  if (MODE != FWD && a.rad != nullptr)
-    hipLaunchKernelGGL((gemm_kernel<L, M, GATE, NW, RT, TM, MODE, KR, MODE != FWD>), g, b, 0, s, a);
+  if (MODE == BWD_DX && a.rad != nullptr)
+    hipLaunchKernelGGL((gemm_kernel<L, M, GATE, NW, RT, TM, MODE, KR, MODE == BWD_DX>), g, b, 0, s, a);
   else
     hipLaunchKernelGGL((gemm_kernel<L, M, GATE, NW, RT, TM, MODE, KR, false>), g, b, 0, s, a);
 }
@@ -53,10 +53,17 @@ int launch(const Args& a, hipStream_t s) {
 #define MALOQ_GEMM_INSTANCES(KW, L, M, TM, MODE)                              \
   KW template int launch<L, M, false, TM, TM, MODE>(const Args&, hipStream_t); \
   KW template int launch<L, M, true, TM, TM, MODE>(const Args&, hipStream_t);
+// The gated edge-frame forward (first convolution of a two-convolution block).
+#define MALOQ_GEMM_EDGE_INSTANCES(KW, L, M, TM) \
+  KW template int launch<L, M, true, TM, TM, FWD_EDGE>(const Args&, hipStream_t);
 
-// dtype: 0 fp32, 1 bf16; mode: FWD or BWD_DX.
+// dtype: 0 fp32, 1 bf16; mode: FWD, BWD_DX or FWD_EDGE (gated only).
 template <int L, int M>
 int launch_lm(int dtype, int gate, int mode, const Args& a, hipStream_t s) {
+  if (mode == FWD_EDGE) {
+    MALOQ_REQUIRE(gate, "the edge-frame forward is built gated only");
+    return dtype == 1 ? launch<L, M, true, BF16, BF16, FWD_EDGE>(a, s) : launch<L, M, true, F32, F32, FWD_EDGE>(a, s);
+  }
   if (mode == FWD) {
     if (dtype == 1)
       return gate ? launch<L, M, true, BF16, BF16, FWD>(a, s) : launch<L, M, false, BF16, BF16, FWD>(a, s);

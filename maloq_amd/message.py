@@ -14,6 +14,10 @@ Host side of ``maloq_message_fwd`` / ``maloq_message_bwd_dx`` (include/maloq_hip
                        inverse rotate -> segment sum (Edgewise.forward_node,
                        esen_block.py:146-208), with input, radial-scale, weight
                        and bias gradients.
+* ``edgewise_forward`` the reference's two-convolution Edgewise (message
+                       cat(x[src], x[dst]) -> rotate -> SO(2) + gate -> SO(2)
+                       in the edge frame -> inverse rotate -> segment sum),
+                       forward only (``maloq_message_edgewise_fwd``).
 
 Edge inputs (Euler triples, radial scales) are expected in the plan's
 dst-sorted order (``plan.sort_edges``).
@@ -243,6 +247,59 @@ def message_forward(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=False, wp
               _lib.ptr(r), _lib.ptr(dk), _lib.ptr(gws), _lib.stream_of(dev))
     if save is not None:
         save.update(y=y, r=r, dk=dk, g=gws)
+    return out
+
+
+def edgewise_forward(x, plan, eulers, rad, conv1, conv2, lmax, mmax, wpack1=None, wpack2=None,
+                     save=None):
+    """Node output [N, d, c_out] fp32 of the two-convolution block
+    ``Edgewise.forward_node`` with message_type "source-target"
+    (esen_block.py:146-208; maloq_message_edgewise_fwd), forward only.
+
+    The message is ``cat(x[src], x[dst])``; ``conv1 = (w0, b0, wm)`` is the
+    gated first SO(2) convolution (input 2 C, w0/b0 carry the lmax c_hidden gate
+    rows first, ``rad`` its radial scales [E, rad_width(lmax, mmax, 2 C)] or
+    None), ``conv2 = (w0, b0, wm)`` the second one (input c_hidden, no radial
+    scale, no gate).  Between the two the rows stay in the edge frame.
+    ``save``: dict that receives "z" (the gated rows [E, d', c_hidden]),
+    "dk" and, gated, "g" (the first convolution's pre-activations)."""
+    dt = x.dtype
+    if dt not in DTYPE_CODE:
+        raise ValueError(f"unsupported dtype {dt}")
+    _lib.require_cuda(x, eulers, conv1[0], conv2[0])
+    N, d, c_x = x.shape
+    assert d == (lmax + 1) ** 2, "x must be [N, (lmax+1)^2, C]"
+    c_hidden = conv1[0].shape[0] // (2 * lmax + 1)
+    c_out = conv2[0].shape[0] // (lmax + 1)
+    if wpack1 is None:
+        wpack1 = pack_weights(conv1[0], conv1[2], lmax, mmax, True, 2 * c_x, c_hidden, dt, 0)
+    if wpack2 is None:
+        wpack2 = pack_weights(conv2[0], conv2[2], lmax, mmax, False, c_hidden, c_out, dt, 0)
+    E = plan.num_edges
+    dev = x.device
+    kr = kept_rows(lmax, mmax)
+    out = torch.empty(plan.num_nodes, d, c_out, device=dev, dtype=torch.float32)
+    lib = _lib.load()
+    parts = torch.empty(max(1, lib.maloq_message_partials_floats(lmax, 0, E, c_out)), device=dev,
+                        dtype=torch.float32)
+    if rad is not None:
+        assert rad.shape == (E, rad_width(lmax, mmax, 2 * c_x)), "rad must be [E, sum_m (lmax-m+1) 2C]"
+        rad = rad.to(dt).contiguous()
+    y = torch.empty(max(E, 1), kr, 2 * c_x, device=dev, dtype=dt)
+    z = torch.empty(max(E, 1), kr, c_hidden, device=dev, dtype=dt)
+    dk = torch.empty(max(E, 1), wigner_floats(lmax, mmax), device=dev, dtype=torch.float32)
+    gws = torch.empty(max(E, 1), kr + lmax, c_hidden, device=dev, dtype=dt) if save is not None else None
+    b1 = conv1[1].float().contiguous() if conv1[1] is not None else None
+    b2 = conv2[1].float().contiguous() if conv2[1] is not None else None
+    xc = x.contiguous()
+    eul = eulers.float().contiguous()
+    _lib.call("maloq_message_edgewise_fwd", DTYPE_CODE[dt], lmax, mmax, _lib.ptr(xc), c_x,
+              _lib.ptr(plan.src), _lib.ptr(plan.dst), E, _lib.ptr(eul), _lib.ptr(rad), _lib.ptr(wpack1),
+              _lib.ptr(b1), c_hidden, _lib.ptr(wpack2), _lib.ptr(b2), _lib.ptr(_jd_dev(lmax, dev)),
+              _lib.ptr(out), plan.num_nodes, c_out, _lib.ptr(plan.seg_ptr), _lib.ptr(parts), _lib.ptr(y),
+              _lib.ptr(dk), _lib.ptr(gws), _lib.ptr(z), _lib.stream_of(dev))
+    if save is not None:
+        save.update(z=z, dk=dk, g=gws)
     return out
 
 

@@ -281,6 +281,69 @@ def test_message_block_is_gamma_invariant(lmax, mmax, gate, Jd):
     assert torch.allclose(outs[0], outs[2], atol=1e-11)
 
 
+def _identity_conv(lmax, mmax, c):
+    """SO(2) weights that map every m-major row to itself (W_r = I, W_i = 0)."""
+    m_size = [lmax - m + 1 for m in range(mmax + 1)]
+    wm = [torch.cat([torch.eye(m_size[m] * c), torch.zeros(m_size[m] * c, m_size[m] * c)]) for m in range(1, mmax + 1)]
+    return {"w0": torch.eye(m_size[0] * c), "b0": None, "wm": wm, "c_out": c}
+
+
+@pytest.mark.parametrize("lmax,mmax", [(2, 2), (4, 2)])
+def test_message_block_second_conv_identity(lmax, mmax, Jd):
+    """An identity second convolution leaves the gated one-convolution block
+    unchanged, and a scaled one scales it (a wrong row order or +-m mix of the
+    second convolution breaks the first; a dropped second convolution the
+    second)."""
+    g = torch.Generator().manual_seed(40 + lmax)
+    N, E, C, H = 7, 25, 3, 4
+    x = torch.randn(N, (lmax + 1) ** 2, C, generator=g)
+    ei = _random_graph(N, E, g)
+    eul = orot.init_edge_rot_euler_angles(torch.randn(E, 3, generator=g), torch.rand(E, generator=g))
+    conv1 = _conv_params(lmax, mmax, C, H, g, extra=lmax * H)
+    one = omsg.message_block(x, ei, eul, Jd, lmax, mmax, conv1, gate=True)
+    two = omsg.message_block(x, ei, eul, Jd, lmax, mmax, conv1, conv2=_identity_conv(lmax, mmax, H), gate=True)
+    assert torch.allclose(one, two, atol=1e-12)
+    ident = _identity_conv(lmax, mmax, H)
+    scaled = {"w0": 3 * ident["w0"], "b0": None, "wm": [3 * w for w in ident["wm"]], "c_out": H}
+    three = omsg.message_block(x, ei, eul, Jd, lmax, mmax, conv1, conv2=scaled, gate=True)
+    assert torch.allclose(three, 3 * one, atol=1e-12)
+
+
+def _half_conv(conv, lmax, mmax, c, half):
+    """conv on 2c concatenated input channels -> the c-channel conv of one half
+    (column l 2c + half c + k of every block)."""
+    m_size = [lmax - m + 1 for m in range(mmax + 1)]
+    cols = lambda n: torch.tensor([l * 2 * c + half * c + k for l in range(n) for k in range(c)])
+    return {"w0": conv["w0"][:, cols(m_size[0])], "b0": conv["b0"],
+            "wm": [w[:, cols(m_size[m])] for m, w in zip(range(1, mmax + 1), conv["wm"])], "c_out": conv["c_out"]}
+
+
+@pytest.mark.parametrize("half", [0, 1])
+def test_message_block_source_target_concat(half, Jd):
+    """cat(x[src], x[dst]) with the weights of one half zeroed is the one-source
+    block of the other half: x[src] on the graph, or x[dst] on the graph with
+    src replaced by dst (swapping the halves breaks both)."""
+    lmax, mmax = 4, 2
+    g = torch.Generator().manual_seed(60 + half)
+    N, E, C, H = 6, 30, 3, 4
+    x = torch.randn(N, (lmax + 1) ** 2, C, generator=g)
+    ei = _random_graph(N, E, g)
+    eul = orot.init_edge_rot_euler_angles(torch.randn(E, 3, generator=g), torch.rand(E, generator=g))
+    conv1 = _conv_params(lmax, mmax, 2 * C, H, g, extra=lmax * H)
+    conv2 = _conv_params(lmax, mmax, H, C, g)
+    m_size = [lmax - m + 1 for m in range(mmax + 1)]
+    z1 = copy.deepcopy(conv1)
+    cols = lambda n: torch.tensor([l * 2 * C + (1 - half) * C + k for l in range(n) for k in range(C)])
+    z1["w0"][:, cols(m_size[0])] = 0
+    for m in range(1, mmax + 1):
+        z1["wm"][m - 1][:, cols(m_size[m])] = 0
+    got = omsg.message_block(x, ei, eul, Jd, lmax, mmax, z1, conv2=conv2, gate=True, concat="source-target")
+    kept = _half_conv(conv1, lmax, mmax, C, half)
+    ei1 = ei if half == 0 else torch.stack([ei[1], ei[1]])
+    want = omsg.message_block(x, ei1, eul, Jd, lmax, mmax, kept, conv2=conv2, gate=True)
+    assert torch.allclose(got, want, atol=1e-12)
+
+
 def test_message_block_global_equivariance_config1(Jd):
     """Config 1 of the benchmark: rotate positions by R and node features by D(R):
     the block's output rotates by D(R)."""
