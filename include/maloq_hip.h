@@ -199,10 +199,14 @@ int maloq_message_fwd(int dtype, int lmax, int mmax, int gate, const void* x, in
  * Workspaces: y_ws [E, d', 2 c_x], z_ws [E, d', c_hidden] (dtype), dk_ws
  * [E, maloq_message_wigner_floats], partials maloq_message_partials_floats(lmax, 0,
  * E, c_out) floats; gate_ws (nullable) [E, d' + lmax, c_hidden] receives the
- * first convolution's pre-activations.  c_x a multiple of 8.  Replaces the
- * forward of Edgewise.forward_node (esen_block.py:146-208). */
+ * first convolution's pre-activations.  c_x a multiple of 8.  seg_id (nullable:
+ * dst) is the output row of each edge, non-decreasing, with seg_ptr its CSR over
+ * num_nodes rows: seg_id[e] = e with seg_ptr[i] = i gives the per-edge rows of
+ * Edgewise.forward_edge (esen_block.py:210-258).  Replaces the forward of
+ * Edgewise.forward_node (esen_block.py:146-208). */
 int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const void* x, int c_x,
-                               const int32_t* src, const int32_t* dst, int64_t num_edges,
+                               const int32_t* src, const int32_t* dst, const int32_t* seg_id,
+                               int64_t num_edges,
                                const float* eulers, const void* rad, const void* wpack1,
                                const float* bias1, int c_hidden, const void* wpack2,
                                const float* bias2, const float* jd, float* out, int64_t num_nodes,

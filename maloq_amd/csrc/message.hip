@@ -165,7 +165,8 @@ extern "C" int maloq_message_fwd(int dtype, int lmax, int mmax, int gate, const 
 }
 
 extern "C" int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const void* x, int c_x,
-                                          const int32_t* src, const int32_t* dst, int64_t num_edges,
+                                          const int32_t* src, const int32_t* dst,
+                                          const int32_t* seg_id, int64_t num_edges,
                                           const float* eulers, const void* rad, const void* wpack1,
                                           const float* bias1, int c_hidden, const void* wpack2,
                                           const float* bias2, const float* jd, float* out,
@@ -184,6 +185,7 @@ extern "C" int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const v
   const int kc = dtype == 1 ? BF16::KC : F32::KC;
   if (num_edges > 0) {
     MALOQ_REQUIRE(x && src && dst && eulers && partials && y_ws && dk_ws && z_ws, "null pointer");
+    const int32_t* seg = seg_id ? seg_id : dst;
     // rotated message rows of cat(x[src], x[dst]) (radial scale applied) and the Wigner rows
     PrepArgs p{};
     p.x = x; p.gidx = src; p.gidx2 = dst; p.x_c = c_x; p.eidx = nullptr; p.eulers = eulers;
@@ -193,7 +195,7 @@ extern "C" int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const v
     if (rc) return rc;
     // first convolution + gate, kept in the edge frame
     Args a{};
-    a.a_src = y_ws; a.dk = dk_ws; a.seg = dst; a.eidx = nullptr;
+    a.a_src = y_ws; a.dk = dk_ws; a.seg = seg; a.eidx = nullptr;
     a.wpack = static_cast<const char*>(wpack1); a.bias = bias1; a.out = out; a.part = partials;
     a.E = num_edges; a.C_k = 2 * c_x; a.C_n = c_hidden; a.n_cb = c_hidden / CB;
     a.extra = lmax * c_hidden;
@@ -204,7 +206,7 @@ extern "C" int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const v
     if (rc) return rc;
     // second convolution, rotation back and segment sum
     Args b{};
-    b.a_src = z_ws; b.dk = dk_ws; b.seg = dst; b.eidx = nullptr;
+    b.a_src = z_ws; b.dk = dk_ws; b.seg = seg; b.eidx = nullptr;
     b.wpack = static_cast<const char*>(wpack2); b.bias = bias2; b.out = out; b.part = partials;
     b.E = num_edges; b.C_k = c_hidden; b.C_n = c_out; b.n_cb = c_out / CB; b.extra = 0;
     b.ntiles = (num_edges + tile_edges(lmax, 0) - 1) / tile_edges(lmax, 0);

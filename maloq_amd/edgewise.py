@@ -1,0 +1,125 @@
+"""Edgewise message block of the eSEN backbone (two SO(2) convolutions) on MI355X.
+
+The reference (src/maloq/helm/esen_block.py:37-258) forms the message
+``cat(x[src], x[dst])``, rotates it into the edge frame, runs
+``so2_conv_1`` (radial scales from ``x_edge``, lmax * hidden extra m = 0
+outputs), ``GateActivation``, ``so2_conv_2`` (internal weights), rotates back
+and sums per destination node (``forward_node``) or returns the per-edge
+messages (``forward_edge``).
+
+Here the whole chain is one C-ABI call, ``maloq_message_edgewise_fwd``: the
+prep kernel gathers both halves of the message and rotates them, the first
+GEMM applies the gate in its epilogue and leaves the rows in the edge frame,
+the second GEMM rotates back and sums per segment.  Forward only: the module
+refuses to run where autograd would need its backward.  Wigner matrices are
+built in the kernels from the Euler angles (``eulers=``, as from
+:func:`maloq_amd.wigner.extract_euler_angles`); the dense ``wigner`` /
+``wigner_inv`` arguments of the reference signature are not read.
+"""
+from __future__ import annotations
+
+import copy
+import math
+
+import torch
+from torch import nn
+
+from . import _lib
+from .message import MessagePlan, edgewise_forward, rad_width
+from .radial import RadialMLP
+
+
+class SO2_m_Conv(nn.Module):
+    """Weights of one order m (so2_layers.py:19-68): ``fc`` [2 (lmax-m+1) c_out,
+    (lmax-m+1) c_in], no bias, initialised scaled by 1/sqrt(2) as there."""
+
+    def __init__(self, m, sphere_channels, m_output_channels, lmax, mmax) -> None:
+        super().__init__()
+        self.m, self.sphere_channels, self.m_output_channels = m, sphere_channels, m_output_channels
+        self.lmax, self.mmax = lmax, mmax
+        assert mmax >= m
+        n = lmax - m + 1
+        self.out_channels_half = m_output_channels * n
+        self.fc = nn.Linear(n * sphere_channels, 2 * self.out_channels_half, bias=False)
+        self.fc.weight.data.mul_(1 / math.sqrt(2))
+
+
+class SO2_Convolution(nn.Module):
+    """Weights of one SO(2) convolution (so2_layers.py:71-214): ``fc_m0``
+    (with the extra m = 0 outputs first), ``so2_m_conv``, and ``rad_func``
+    when the radial scales come from the edge features (internal_weights
+    False).  The arithmetic runs in the fused kernels."""
+
+    def __init__(self, sphere_channels, m_output_channels, lmax, mmax, mappingReduced, internal_weights=True,
+                 edge_channels_list=None, extra_m0_output_channels=None) -> None:
+        super().__init__()
+        self.sphere_channels, self.m_output_channels = sphere_channels, m_output_channels
+        self.lmax, self.mmax, self.mappingReduced = lmax, mmax, mappingReduced
+        self.internal_weights = internal_weights
+        self.edge_channels_list = copy.deepcopy(edge_channels_list)
+        self.extra_m0_output_channels = extra_m0_output_channels
+        n0 = (lmax + 1) * sphere_channels
+        self.fc_m0 = nn.Linear(n0, m_output_channels * (lmax + 1) + (extra_m0_output_channels or 0), bias=True)
+        self.so2_m_conv = nn.ModuleList(
+            [SO2_m_Conv(m, sphere_channels, m_output_channels, lmax, mmax) for m in range(1, mmax + 1)])
+        self.rad_func = None
+        if not internal_weights:
+            assert self.edge_channels_list is not None
+            self.edge_channels_list.append(rad_width(lmax, mmax, sphere_channels))
+            self.rad_func = RadialMLP(self.edge_channels_list)
+
+    def weights(self):
+        return (self.fc_m0.weight, self.fc_m0.bias, [c.fc.weight for c in self.so2_m_conv])
+
+
+class Edgewise(nn.Module):
+    """Drop-in for the reference's Edgewise (esen_block.py:37-258): same
+    constructor arguments and parameter names (``so2_conv_1.*``,
+    ``so2_conv_2.*``).  message_type "source-target" runs; the three-part
+    "source-target-message" is accepted by the constructor only."""
+
+    def __init__(self, sphere_channels, hidden_channels, lmax, mmax, edge_channels_list, mappingReduced, SO3_grid,
+                 cutoff, message_type, act_type="gate", include_edges=True) -> None:
+        super().__init__()
+        self.sphere_channels, self.hidden_channels = sphere_channels, hidden_channels
+        self.lmax, self.mmax = lmax, mmax
+        self.mappingReduced, self.SO3_grid = mappingReduced, SO3_grid
+        self.edge_channels_list = copy.deepcopy(edge_channels_list)
+        self.act_type, self.include_edges = act_type, include_edges
+        if act_type != "gate":
+            raise ValueError(f"Unknown activation type {act_type}")
+        if message_type == "source-target-message":
+            self.concat_size = 3
+        elif message_type == "source-target":
+            self.concat_size = 2
+        else:
+            raise ValueError(f"Unknown message type {message_type}")
+        self.so2_conv_1 = SO2_Convolution(self.concat_size * sphere_channels, hidden_channels, lmax, mmax,
+                                          mappingReduced, internal_weights=False,
+                                          edge_channels_list=self.edge_channels_list,
+                                          extra_m0_output_channels=lmax * hidden_channels)
+        self.so2_conv_2 = SO2_Convolution(hidden_channels, sphere_channels, lmax, mmax, mappingReduced,
+                                          internal_weights=True)
+
+    def forward(self, x, x_message_edge, x_edge, edge_index, wigner, wigner_inv, node_or_edge="node",
+                partition=None, eulers=None, plan=None):
+        """Node sums [N, d, sphere_channels] (node) or per-edge messages
+        [E, d, sphere_channels] (edge), in the dtype of x.  ``eulers`` [E, 3]:
+        the edges' Euler angles in the original edge order; ``plan``: the
+        graph's MessagePlan (built here when not given)."""
+        if partition:
+            raise NotImplementedError("partitioned (multi-GPU) graphs are not supported on one GPU")
+        if self.concat_size != 2:
+            raise NotImplementedError("message_type 'source-target-message' is not built")
+        if eulers is None:
+            raise ValueError("pass eulers=: the kernels build the Wigner rows from the Euler angles")
+        if torch.is_grad_enabled() and (x.requires_grad or x_edge.requires_grad
+                                        or any(p.requires_grad for p in self.parameters())):
+            raise NotImplementedError("the two-convolution backward is not built: run under torch.no_grad()")
+        _lib.require_cuda(x, x_edge, eulers)
+        if plan is None:
+            plan = MessagePlan(edge_index, x.shape[0])
+        rad = self.so2_conv_1.rad_func(plan.sort_edges(x_edge.float()), out_dtype=x.dtype)
+        out = edgewise_forward(x, plan, plan.sort_edges(eulers.float()), rad, self.so2_conv_1.weights(),
+                               self.so2_conv_2.weights(), self.lmax, self.mmax, node_or_edge=node_or_edge)
+        return out.to(x.dtype)

@@ -251,10 +251,13 @@ def message_forward(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=False, wp
 
 
 def edgewise_forward(x, plan, eulers, rad, conv1, conv2, lmax, mmax, wpack1=None, wpack2=None,
-                     save=None):
+                     save=None, node_or_edge="node"):
     """Node output [N, d, c_out] fp32 of the two-convolution block
     ``Edgewise.forward_node`` with message_type "source-target"
     (esen_block.py:146-208; maloq_message_edgewise_fwd), forward only.
+    ``node_or_edge="edge"``: the rotated-back message of every edge instead,
+    [E, d, c_out] in the original edge order (``Edgewise.forward_edge``,
+    esen_block.py:210-258): each edge is its own output row.
 
     The message is ``cat(x[src], x[dst])``; ``conv1 = (w0, b0, wm)`` is the
     gated first SO(2) convolution (input 2 C, w0/b0 carry the lmax c_hidden gate
@@ -278,7 +281,15 @@ def edgewise_forward(x, plan, eulers, rad, conv1, conv2, lmax, mmax, wpack1=None
     E = plan.num_edges
     dev = x.device
     kr = kept_rows(lmax, mmax)
-    out = torch.empty(plan.num_nodes, d, c_out, device=dev, dtype=torch.float32)
+    if node_or_edge not in ("node", "edge"):
+        raise ValueError("node_or_edge must be 'node' or 'edge'")
+    if node_or_edge == "node":
+        rows, seg_id, seg_ptr = plan.num_nodes, None, plan.seg_ptr
+    else:
+        rows = E
+        seg_id = torch.arange(E, device=dev, dtype=torch.int32)
+        seg_ptr = torch.arange(E + 1, device=dev, dtype=torch.int64)
+    out = torch.empty(rows, d, c_out, device=dev, dtype=torch.float32)
     lib = _lib.load()
     parts = torch.empty(max(1, lib.maloq_message_partials_floats(lmax, 0, E, c_out)), device=dev,
                         dtype=torch.float32)
@@ -294,12 +305,16 @@ def edgewise_forward(x, plan, eulers, rad, conv1, conv2, lmax, mmax, wpack1=None
     xc = x.contiguous()
     eul = eulers.float().contiguous()
     _lib.call("maloq_message_edgewise_fwd", DTYPE_CODE[dt], lmax, mmax, _lib.ptr(xc), c_x,
-              _lib.ptr(plan.src), _lib.ptr(plan.dst), E, _lib.ptr(eul), _lib.ptr(rad), _lib.ptr(wpack1),
-              _lib.ptr(b1), c_hidden, _lib.ptr(wpack2), _lib.ptr(b2), _lib.ptr(_jd_dev(lmax, dev)),
-              _lib.ptr(out), plan.num_nodes, c_out, _lib.ptr(plan.seg_ptr), _lib.ptr(parts), _lib.ptr(y),
-              _lib.ptr(dk), _lib.ptr(gws), _lib.ptr(z), _lib.stream_of(dev))
+              _lib.ptr(plan.src), _lib.ptr(plan.dst), _lib.ptr(seg_id), E, _lib.ptr(eul), _lib.ptr(rad),
+              _lib.ptr(wpack1), _lib.ptr(b1), c_hidden, _lib.ptr(wpack2), _lib.ptr(b2),
+              _lib.ptr(_jd_dev(lmax, dev)), _lib.ptr(out), rows, c_out, _lib.ptr(seg_ptr), _lib.ptr(parts),
+              _lib.ptr(y), _lib.ptr(dk), _lib.ptr(gws), _lib.ptr(z), _lib.stream_of(dev))
     if save is not None:
         save.update(z=z, dk=dk, g=gws)
+    if node_or_edge == "edge":
+        per_edge = torch.empty_like(out)
+        per_edge[plan.perm] = out     # dst-sorted position p holds original edge perm[p]
+        return per_edge
     return out
 
 

@@ -1,0 +1,96 @@
+"""The two-convolution Edgewise block (maloq_amd.edgewise, esen_block.py:37-258).
+
+CPU: the module mirrors the reference's constructor, parameter names and
+shapes, and refuses what is not built (backward, CPU tensors, the three-part
+message).  GPU: node and edge modes against the oracle (oracle.message,
+message_block with conv2 and concat "source-target"), with the radial scales
+from the oracle RadialMLP on the module's own weights; fp32 within 1e-5 of
+the output scale."""
+import pytest
+import torch
+
+from oracle import message as omsg
+from oracle import rotation as orot
+
+
+def _module(C=32, H=64, lmax=4, mmax=2, message_type="source-target"):
+    from maloq_amd.edgewise import Edgewise
+    from maloq_amd.so3 import CoefficientMapping
+    torch.manual_seed(0)
+    return Edgewise(C, H, lmax, mmax, [8, 32, 32], CoefficientMapping(lmax, mmax), None, 6.0, message_type)
+
+
+def test_module_mirrors_reference_structure():
+    mod = _module()
+    shapes = {k: tuple(v.shape) for k, v in mod.named_parameters()}
+    # conv1: input 2 C = 64, hidden 64, extra lmax H = 256 gate outputs; rad width 64 (5 + 2 * 4 + 2 * 3)
+    assert shapes["so2_conv_1.fc_m0.weight"] == (5 * 64 + 4 * 64, 5 * 64)
+    assert shapes["so2_conv_1.fc_m0.bias"] == (5 * 64 + 4 * 64,)
+    assert shapes["so2_conv_1.so2_m_conv.0.fc.weight"] == (2 * 4 * 64, 4 * 64)
+    assert shapes["so2_conv_1.so2_m_conv.1.fc.weight"] == (2 * 3 * 64, 3 * 64)
+    assert shapes["so2_conv_1.rad_func.net.6.weight"] == ((5 + 4 + 3) * 64, 32)
+    assert shapes["so2_conv_2.fc_m0.weight"] == (5 * 32, 5 * 64)
+    assert shapes["so2_conv_2.so2_m_conv.1.fc.weight"] == (2 * 3 * 32, 3 * 64)
+    assert not any(k.startswith("so2_conv_2.rad_func") for k in shapes)
+    assert mod.so2_conv_1.edge_channels_list == [8, 32, 32, 12 * 64]
+    assert mod.edge_channels_list == [8, 32, 32]
+    assert mod.concat_size == 2 and _module(message_type="source-target-message").concat_size == 3
+    with pytest.raises(ValueError):
+        _module(message_type="source")
+
+
+def test_module_refuses_what_is_not_built():
+    from maloq_amd import _lib
+    mod = _module(C=8, H=32, lmax=2)
+    N, E = 4, 6
+    x = torch.zeros(N, 9, 8)
+    ei = torch.zeros(2, E, dtype=torch.long)
+    with pytest.raises(NotImplementedError):      # parameters need gradients
+        mod(x, None, torch.zeros(E, 8), ei, None, None, "node", eulers=torch.zeros(E, 3))
+    with torch.no_grad(), pytest.raises((_lib.MaloqHipError, RuntimeError, ValueError)):   # CPU tensors
+        mod(x, None, torch.zeros(E, 8), ei, None, None, "node", eulers=torch.zeros(E, 3))
+    with torch.no_grad(), pytest.raises(NotImplementedError):
+        _module(C=8, H=32, lmax=2, message_type="source-target-message")(
+            x, None, torch.zeros(E, 8), ei, None, None, "node", eulers=torch.zeros(E, 3))
+
+
+def _oracle_conv(c):
+    w0, b0, wm = c.weights()
+    cpu = lambda t: t.detach().double().cpu()
+    return {"w0": cpu(w0), "b0": cpu(b0), "wm": [cpu(w) for w in wm], "c_out": c.m_output_channels}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["node", "edge"])
+@pytest.mark.parametrize("lmax", [2, 4])
+def test_module_forward_matches_oracle(mode, lmax):
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    from maloq_amd.wigner import extract_euler_angles
+    from oracle.so2 import radial_mlp
+    print(f"edgewise module case mode={mode} lmax={lmax}", flush=True)
+    dev = torch.device("cuda:0")
+    C, H, N, E = 32, 64, 23, 300
+    mod = _module(C, H, lmax).to(dev)
+    gen = torch.Generator().manual_seed(lmax)
+    x = torch.randn(N, (lmax + 1) ** 2, C, generator=gen)
+    src = torch.randint(0, N, (E,), generator=gen)
+    dst = torch.randint(0, N - 2, (E,), generator=gen)
+    ei = torch.stack([src, dst])
+    x_edge = torch.randn(E, 8, generator=gen)
+    eul = extract_euler_angles(torch.randn(E, 3, generator=gen).to(dev), seed=5)
+    with torch.no_grad():
+        got = mod(x.to(dev), None, x_edge.to(dev), ei.to(dev), None, None, mode, eulers=eul)
+    rf = mod.so2_conv_1.rad_func
+    lins = [m for m in rf.net if isinstance(m, torch.nn.Linear)]
+    lns = [m for m in rf.net if isinstance(m, torch.nn.LayerNorm)]
+    cpu = lambda t: t.detach().double().cpu()
+    hidden = [(cpu(li.weight), cpu(li.bias), cpu(ln.weight), cpu(ln.bias)) for li, ln in zip(lins[:-1], lns)]
+    rad = radial_mlp(x_edge.double(), hidden, cpu(lins[-1].weight), cpu(lins[-1].bias), lns[0].eps)
+    e64 = eul.double().cpu()
+    ref = omsg.message_block(x.double(), ei, (e64[:, 0], e64[:, 1], e64[:, 2]), orot.load_jd(), lmax, 2,
+                             _oracle_conv(mod.so2_conv_1), rad=rad, conv2=_oracle_conv(mod.so2_conv_2), gate=True,
+                             concat="source-target", reduce=(mode == "node"))
+    assert got.shape == ref.shape
+    scale = ref.abs().max().item()
+    assert (got.double().cpu() - ref).abs().max().item() <= 1e-5 * scale
