@@ -199,7 +199,8 @@ int maloq_message_fwd(int dtype, int lmax, int mmax, int gate, const void* x, in
  * Workspaces: y_ws [E, d', 2 c_x], z_ws [E, d', c_hidden] (dtype), dk_ws
  * [E, maloq_message_wigner_floats], partials maloq_message_partials_floats(lmax, 0,
  * E, c_out) floats; gate_ws (nullable) [E, d' + lmax, c_hidden] receives the
- * first convolution's pre-activations.  c_x a multiple of 8.  seg_id (nullable:
+ * first convolution's pre-activations, r_ws (nullable) [E, d', 2 c_x] the rotated
+ * message rows before the radial scale (both kept for the backward).  c_x a multiple of 8.  seg_id (nullable:
  * dst) is the output row of each edge, non-decreasing, with seg_ptr its CSR over
  * num_nodes rows: seg_id[e] = e with seg_ptr[i] = i gives the per-edge rows of
  * Edgewise.forward_edge (esen_block.py:210-258).  Replaces the forward of
@@ -211,7 +212,37 @@ int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const void* x, int
                                const float* bias1, int c_hidden, const void* wpack2,
                                const float* bias2, const float* jd, float* out, int64_t num_nodes,
                                int c_out, const int64_t* seg_ptr, float* partials, void* y_ws,
-                               float* dk_ws, void* gate_ws, void* z_ws, void* stream);
+                               void* r_ws, float* dk_ws, void* gate_ws, void* z_ws, void* stream);
+
+/* Input and radial-scale gradients of the two-convolution block
+ * (maloq_message_edgewise_fwd), from the forward's workspaces:
+ *   dz2_ws [E, d', c_x]       = D_e grad_out[dst[e]]          (conv2 output gradient),
+ *   dzh_ws [E, d', c_hidden]  = SO2_2^T(dz2)                  (gate output gradient),
+ *   dz1_ws [E, d' + lmax, c_hidden] = GateActivation backward at gate_saved
+ *                               (the forward's gate_ws): dL/dpre, then dL/dgate,
+ *   grad_rad[e] = SO2_1^T(dz1_e) (*) r_saved[e]  (r_saved: the unscaled rotated
+ *                 message rows [E, d', 2 c_x]; both nullable together with rad),
+ *   grad_x_src / grad_x_dst [num_nodes, d, 2 c_x] fp32: D_e^T rad[e] (*) SO2_1^T(dz1_e)
+ *                 summed per source (channels [0, c_x) valid) and per destination
+ *                 (channels [c_x, 2 c_x) valid); grad_x = the sum of the two valid halves.
+ * grad_row (nullable: dst) is the row of grad_out of each edge (e for the
+ * per-edge output of forward_edge, grad_out then [E, d, c_x]).
+ * Edges in the forward's dst-sorted order (dst, seg_ptr); src_sorted / edge_idx /
+ * seg_ptr_src: the same edges sorted by source, edge_idx the dst-sorted position
+ * of each.  wpack1_t / wpack2_t: the two convolutions packed for the transposed
+ * GEMM (conv1 gated).  c_x a multiple of 32.  dz2_ws and dz1_ws feed
+ * maloq_message_dw (conv2: dz2 with the forward's z_ws; conv1: dz1 with y_ws).
+ * Replaces the autograd backward of Edgewise.forward_node (esen_block.py:146-208). */
+int maloq_message_edgewise_bwd_dx(int dtype, int lmax, int mmax, const float* grad_out, int c_x,
+                                  const int32_t* dst, const int32_t* grad_row,
+                                  const int32_t* src_sorted,
+                                  const int32_t* edge_idx, int64_t num_edges, const float* dk,
+                                  const void* rad, void* grad_rad, const void* r_saved,
+                                  const void* gate_saved, const void* wpack1_t, int c_hidden,
+                                  const void* wpack2_t, const float* jd, float* grad_x_src,
+                                  float* grad_x_dst, int64_t num_nodes, const int64_t* seg_ptr,
+                                  const int64_t* seg_ptr_src, float* partials, void* dz2_ws,
+                                  void* dzh_ws, void* dz1_ws, void* stream);
 
 /* Input and radial-scale gradients of the fused block:
  *   grad_x[n] = sum_{e: src[e]=n} D_e^T rad[e] (*) SO2^T(G_e),

@@ -82,6 +82,17 @@ static int prep_dispatch(int lmax, int mmax, int dtype, int mode, const PrepArgs
   MALOQ_REQUIRE(false, "unsupported lmax %d (built: 2, 4, 6 with mmax 2)", lmax);
 }
 
+static int gate_bwd_dispatch(int lmax, int mmax, int dtype, const void* dz, const void* gsave, void* dp,
+                             int64_t E, int C, hipStream_t s) {
+  switch (lmax) {
+    case 2: return gate_bwd_l2(mmax, dtype, dz, gsave, dp, E, C, s);
+    case 4: return gate_bwd_l4(mmax, dtype, dz, gsave, dp, E, C, s);
+    case 6: return gate_bwd_l6(mmax, dtype, dz, gsave, dp, E, C, s);
+    default: break;
+  }
+  MALOQ_REQUIRE(false, "unsupported lmax %d (built: 2, 4, 6 with mmax 2)", lmax);
+}
+
 static int check_common(int dtype, int lmax, int mmax, int c_k, int c_n, int64_t E) {
   MALOQ_REQUIRE(dtype == 0 || dtype == 1, "dtype must be 0 (fp32) or 1 (bf16)");
   MALOQ_REQUIRE(lmax >= 0 && mmax >= 0 && mmax <= lmax, "bad lmax/mmax");
@@ -171,8 +182,8 @@ extern "C" int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const v
                                           const float* bias1, int c_hidden, const void* wpack2,
                                           const float* bias2, const float* jd, float* out,
                                           int64_t num_nodes, int c_out, const int64_t* seg_ptr,
-                                          float* partials, void* y_ws, float* dk_ws, void* gate_ws,
-                                          void* z_ws, void* stream) {
+                                          float* partials, void* y_ws, void* r_ws, float* dk_ws,
+                                          void* gate_ws, void* z_ws, void* stream) {
   MALOQ_REQUIRE(c_x > 0 && c_x % 8 == 0, "node channels must be a positive multiple of 8");
   int rc = check_common(dtype, lmax, mmax, 2 * c_x, c_hidden, num_edges);
   if (rc) return rc;
@@ -189,7 +200,7 @@ extern "C" int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const v
     // rotated message rows of cat(x[src], x[dst]) (radial scale applied) and the Wigner rows
     PrepArgs p{};
     p.x = x; p.gidx = src; p.gidx2 = dst; p.x_c = c_x; p.eidx = nullptr; p.eulers = eulers;
-    p.rad = rad; p.jd = jd; p.y = y_ws; p.r = nullptr; p.dk = dk_ws; p.build_d = 1;
+    p.rad = rad; p.jd = jd; p.y = y_ws; p.r = r_ws; p.dk = dk_ws; p.build_d = 1;
     p.E = num_edges; p.C = 2 * c_x;
     rc = prep_dispatch(lmax, mmax, dtype, FWD, p, s);
     if (rc) return rc;
@@ -215,6 +226,71 @@ extern "C" int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const v
     if (rc) return rc;
   }
   return fixup(seg_ptr, num_nodes, partials, out, d * c_out, tile_edges(lmax, 0), s);
+}
+
+extern "C" int maloq_message_edgewise_bwd_dx(
+    int dtype, int lmax, int mmax, const float* grad_out, int c_x, const int32_t* dst,
+    const int32_t* grad_row, const int32_t* src_sorted, const int32_t* edge_idx, int64_t num_edges, const float* dk,
+    const void* rad, void* grad_rad, const void* r_saved, const void* gate_saved, const void* wpack1_t,
+    int c_hidden, const void* wpack2_t, const float* jd, float* grad_x_src, float* grad_x_dst,
+    int64_t num_nodes, const int64_t* seg_ptr, const int64_t* seg_ptr_src, float* partials,
+    void* dz2_ws, void* dzh_ws, void* dz1_ws, void* stream) {
+  MALOQ_REQUIRE(c_x > 0 && c_x % CB == 0, "node channels must be a positive multiple of %d", CB);
+  int rc = check_common(dtype, lmax, mmax, c_x, c_hidden, num_edges);   // conv2 transposed
+  if (rc) return rc;
+  rc = check_common(dtype, lmax, mmax, c_hidden, 2 * c_x, num_edges);   // conv1 transposed
+  if (rc) return rc;
+  MALOQ_REQUIRE(num_nodes >= 0, "num_nodes < 0");
+  MALOQ_REQUIRE(grad_x_src && grad_x_dst && seg_ptr && seg_ptr_src && jd && wpack1_t && wpack2_t,
+                "null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t d = static_cast<int64_t>(lmax + 1) * (lmax + 1);
+  const int kc = dtype == 1 ? BF16::KC : F32::KC;
+  if (num_edges > 0) {
+    MALOQ_REQUIRE(grad_out && dst && src_sorted && edge_idx && dk && gate_saved && partials && dz2_ws &&
+                  dzh_ws && dz1_ws, "null pointer");
+    MALOQ_REQUIRE(rad == nullptr || r_saved != nullptr, "the radial gradient needs the saved rows");
+    // dL/d(conv2 output) in the edge frame: D_e grad_out[dst[e]]
+    PrepArgs p{};
+    p.x = grad_out; p.gidx = grad_row ? grad_row : dst; p.eidx = nullptr; p.jd = jd; p.y = dz2_ws;
+    p.dk = const_cast<float*>(dk); p.build_d = 0; p.E = num_edges; p.C = c_x;
+    rc = prep_dispatch(lmax, mmax, dtype, BWD_DX, p, s);
+    if (rc) return rc;
+    // conv2 transposed, rows kept in the edge frame: dL/d(gate output)
+    Args b{};
+    b.a_src = dz2_ws; b.dk = dk; b.seg = dst; b.eidx = nullptr;
+    b.wpack = static_cast<const char*>(wpack2_t); b.out = grad_x_src; b.part = partials;
+    b.E = num_edges; b.C_k = c_x; b.C_n = c_hidden; b.n_cb = c_hidden / CB;
+    b.ntiles = (num_edges + tile_edges(lmax, 0) - 1) / tile_edges(lmax, 0);
+    b.frags_per_cb = frags_per_cb(lmax, mmax, 0, c_x, kc);
+    b.zout = dzh_ws;
+    rc = dispatch(lmax, mmax, dtype, 0, BWD_EDGE, b, s);
+    if (rc) return rc;
+    // gate backward: dL/dpre (kept rows) and dL/dgate rows of conv1
+    rc = gate_bwd_dispatch(lmax, mmax, dtype, dzh_ws, gate_saved, dz1_ws, num_edges, c_hidden, s);
+    if (rc) return rc;
+    // conv1 transposed (gated input rows, radial gradient): the x[src] half of the
+    // message channels summed per source, then the x[dst] half per destination
+    for (int half = 0; half < 2; ++half) {
+      Args a{};
+      a.a_src = dz1_ws; a.dk = dk; a.seg = half ? dst : src_sorted; a.eidx = half ? nullptr : edge_idx;
+      a.rad = rad; a.drad = grad_rad; a.rsave = r_saved;
+      a.wpack = static_cast<const char*>(wpack1_t); a.out = half ? grad_x_dst : grad_x_src;
+      a.part = partials; a.E = num_edges; a.C_k = c_hidden; a.C_n = 2 * c_x;
+      a.cb0 = half * (c_x / CB); a.n_cb = c_x / CB;
+      a.ntiles = (num_edges + tile_edges(lmax, 1) - 1) / tile_edges(lmax, 1);
+      a.frags_per_cb = frags_per_cb(lmax, mmax, 1, c_hidden, kc);
+      rc = dispatch(lmax, mmax, dtype, 1, BWD_DX, a, s);
+      if (rc) return rc;
+      rc = fixup(half ? seg_ptr : seg_ptr_src, num_nodes, partials, half ? grad_x_dst : grad_x_src,
+                 d * 2 * c_x, tile_edges(lmax, 1), s);
+      if (rc) return rc;
+    }
+    return MALOQ_OK;
+  }
+  rc = fixup(seg_ptr_src, num_nodes, partials, grad_x_src, d * 2 * c_x, tile_edges(lmax, 1), s);
+  if (rc) return rc;
+  return fixup(seg_ptr, num_nodes, partials, grad_x_dst, d * 2 * c_x, tile_edges(lmax, 1), s);
 }
 
 extern "C" int maloq_message_bwd_dx(int dtype, int lmax, int mmax, int gate, const float* grad_out,

@@ -45,7 +45,7 @@ struct GPlan {
   static constexpr int TE = 32 * RT;
   static constexpr int NT = NW * 64;
   static_assert(TE <= 64, "segment masks are 64-bit");
-  static constexpr bool BWD = MODE == 1;  // BWD_DX
+  static constexpr bool BWD = MODE == 1 || MODE == 3;  // BWD_DX, BWD_EDGE
   static constexpr int gt(int l) { return (GATE && !BWD && l >= 1) ? 1 : 0; }   // output gate row
   static constexpr int gin(int l) { return (GATE && BWD && l >= 1) ? 1 : 0; }   // input gate row
   static constexpr int nq(int l) { return 1 + 2 * cmin(M, l); }
@@ -317,7 +317,7 @@ struct Gemm {
           constexpr int rt = decltype(R)::value;
           constexpr int sb = P::tab.base[lo] + rt * P::ntype(lo);
           constexpr int sp = sb + P::qtype(2 * m - 1, lo), sm = sb + P::qtype(2 * m, lo);
-          if constexpr (MODE != BWD_DX) {
+          if constexpr (!P::BWD) {
             mfma(acc[sm], ap[rt], wi, TM{});
             mfma(acc[sm], am[rt], wr, TM{});
             mfma(acc[sp], ap[rt], wr, TM{});
@@ -331,7 +331,7 @@ struct Gemm {
         static_for<RT>([&](auto R) {
           constexpr int rt = decltype(R)::value;
           constexpr int sb = P::tab.base[lo] + rt * P::ntype(lo);
-          if constexpr (MODE != BWD_DX)
+          if constexpr (!P::BWD)
             mfma(acc[sb + P::qtype(2 * m - 1, lo)], am[rt], nwi, TM{});
           else
             mfma(acc[sb + P::qtype(2 * m, lo)], ap[rt], nwi, TM{});
@@ -739,7 +739,7 @@ struct Gemm {
     static_for<L + 1>([&](auto LO) {
       constexpr int lo = decltype(LO)::value;
       if constexpr (P::tab.owner[lo] == W) {
-        if constexpr (MODE != BWD_DX) {
+        if constexpr (!P::BWD) {
           add_bias<lo>(acc, a, col);
           if constexpr (GATE) {
             if (a.gsave != nullptr)
@@ -750,7 +750,7 @@ struct Gemm {
         } else if constexpr (RAD)
           radial<lo>(acc, s, a, cb,
                      reinterpret_cast<float*>((wave < 2 ? st0 : st1) + (wave & 1) * PW), lane);
-        if constexpr (MODE == FWD_EDGE)
+        if constexpr (MODE == FWD_EDGE || MODE == BWD_EDGE)
           save_pre<lo, true>(acc, s, a, cb,
                              reinterpret_cast<float*>((wave < 2 ? st0 : st1) + (wave & 1) * PW), lane);
         else
@@ -777,7 +777,7 @@ struct Gemm {
     // tile's rows from that XCD's L2 (each XCD holds the weights of all blocks).
     const int64_t bid = blockIdx.x;
     const int64_t slot = bid >> 3;
-    const int cb = static_cast<int>(slot % a.n_cb);
+    const int cb = a.cb0 + static_cast<int>(slot % a.n_cb);
     const int64_t tile = (slot / a.n_cb) * 8 + (bid & 7);
     if (tile >= a.ntiles) return;  // whole workgroup exits together
     const int64_t e0 = tile * TE;
@@ -812,8 +812,8 @@ struct Gemm {
     // complete it long before the epilogue reads it.  Chunk i = 64 (k NW + w) +
     // lane is instruction k of wave w; lanes past the tile read an in-bounds row
     // into the padding; rows of edges past the tile are never stored.
-    // FWD_EDGE does not rotate back: no rows.
-    if constexpr (MODE != FWD_EDGE) {
+    // FWD_EDGE and BWD_EDGE do not rotate back: no rows.
+    if constexpr (MODE != FWD_EDGE && MODE != BWD_EDGE) {
       constexpr int R4 = P::WS / 4;
       const float4* dk4 = reinterpret_cast<const float4*>(a.dk);
       const int wv = __builtin_amdgcn_readfirstlane(wave), lane = tid & 63;

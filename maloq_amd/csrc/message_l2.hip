@@ -8,9 +8,11 @@ namespace msg {
 MALOQ_GEMM_INSTANCES(extern, 2, 2, BF16, FWD)
 MALOQ_GEMM_EDGE_INSTANCES(extern, 2, 2, BF16)
 MALOQ_GEMM_INSTANCES(extern, 2, 2, BF16, BWD_DX)
+MALOQ_GEMM_BWD_EDGE_INSTANCES(extern, 2, 2, BF16)
 MALOQ_GEMM_INSTANCES(extern, 2, 2, F32, FWD)
 MALOQ_GEMM_EDGE_INSTANCES(extern, 2, 2, F32)
 MALOQ_GEMM_INSTANCES(extern, 2, 2, F32, BWD_DX)
+MALOQ_GEMM_BWD_EDGE_INSTANCES(extern, 2, 2, F32)
 
 int launch_l2(int mmax, int dtype, int gate, int mode, const Args& a, hipStream_t s) {
   MALOQ_REQUIRE(mmax == 2, "lmax=2: built for mmax = 2 only, got %d", mmax);
@@ -20,6 +22,11 @@ int launch_l2(int mmax, int dtype, int gate, int mode, const Args& a, hipStream_
 int prep_l2(int mmax, int dtype, int mode, const PrepArgs& a, hipStream_t s) {
   MALOQ_REQUIRE(mmax == 2, "lmax=2: built for mmax = 2 only, got %d", mmax);
   return prep_lm<2, 2>(dtype, mode, a, s);
+}
+
+int gate_bwd_l2(int mmax, int dtype, const void* dz, const void* gsave, void* dp, int64_t E, int C, hipStream_t s) {
+  MALOQ_REQUIRE(mmax == 2, "lmax=2: built for mmax = 2 only, got %d", mmax);
+  return gate_bwd_lm<2, 2>(dtype, dz, gsave, dp, E, C, s);
 }
 
 }  // namespace msg

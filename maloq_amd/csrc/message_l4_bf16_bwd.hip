@@ -5,6 +5,7 @@ namespace maloq {
 namespace msg {
 
 MALOQ_GEMM_INSTANCES(, 4, 2, BF16, BWD_DX)
+MALOQ_GEMM_BWD_EDGE_INSTANCES(, 4, 2, BF16)
 
 }  // namespace msg
 }  // namespace maloq

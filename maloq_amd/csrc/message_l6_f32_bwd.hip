@@ -5,6 +5,7 @@ namespace maloq {
 namespace msg {
 
 MALOQ_GEMM_INSTANCES(, 6, 2, F32, BWD_DX)
+MALOQ_GEMM_BWD_EDGE_INSTANCES(, 6, 2, F32)
 
 }  // namespace msg
 }  // namespace maloq

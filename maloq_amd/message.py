@@ -264,8 +264,11 @@ def edgewise_forward(x, plan, eulers, rad, conv1, conv2, lmax, mmax, wpack1=None
     rows first, ``rad`` its radial scales [E, rad_width(lmax, mmax, 2 C)] or
     None), ``conv2 = (w0, b0, wm)`` the second one (input c_hidden, no radial
     scale, no gate).  Between the two the rows stay in the edge frame.
-    ``save``: dict that receives "z" (the gated rows [E, d', c_hidden]),
-    "dk" and, gated, "g" (the first convolution's pre-activations)."""
+    ``save``: dict that receives the workspaces the backward reads: "y" (the
+    scaled message rows), "r" (unscaled, when ``rad`` is given), "z" (the
+    gated rows [E, d', c_hidden]), "dk" and "g" (the first convolution's
+    pre-activations); "y" and "z" with the zeroed padding rows of
+    ``maloq_message_edge_rows``."""
     dt = x.dtype
     if dt not in DTYPE_CODE:
         raise ValueError(f"unsupported dtype {dt}")
@@ -296,8 +299,14 @@ def edgewise_forward(x, plan, eulers, rad, conv1, conv2, lmax, mmax, wpack1=None
     if rad is not None:
         assert rad.shape == (E, rad_width(lmax, mmax, 2 * c_x)), "rad must be [E, sum_m (lmax-m+1) 2C]"
         rad = rad.to(dt).contiguous()
-    y = torch.empty(max(E, 1), kr, 2 * c_x, device=dev, dtype=dt)
-    z = torch.empty(max(E, 1), kr, c_hidden, device=dev, dtype=dt)
+    if save is not None:
+        y = _edge_rows(E, kr, 2 * c_x, dev, dt)
+        z = _edge_rows(E, kr, c_hidden, dev, dt)
+    else:
+        y = torch.empty(max(E, 1), kr, 2 * c_x, device=dev, dtype=dt)
+        z = torch.empty(max(E, 1), kr, c_hidden, device=dev, dtype=dt)
+    r = torch.empty(max(E, 1), kr, 2 * c_x, device=dev, dtype=dt) \
+        if (save is not None and rad is not None) else None
     dk = torch.empty(max(E, 1), wigner_floats(lmax, mmax), device=dev, dtype=torch.float32)
     gws = torch.empty(max(E, 1), kr + lmax, c_hidden, device=dev, dtype=dt) if save is not None else None
     b1 = conv1[1].float().contiguous() if conv1[1] is not None else None
@@ -308,14 +317,98 @@ def edgewise_forward(x, plan, eulers, rad, conv1, conv2, lmax, mmax, wpack1=None
               _lib.ptr(plan.src), _lib.ptr(plan.dst), _lib.ptr(seg_id), E, _lib.ptr(eul), _lib.ptr(rad),
               _lib.ptr(wpack1), _lib.ptr(b1), c_hidden, _lib.ptr(wpack2), _lib.ptr(b2),
               _lib.ptr(_jd_dev(lmax, dev)), _lib.ptr(out), rows, c_out, _lib.ptr(seg_ptr), _lib.ptr(parts),
-              _lib.ptr(y), _lib.ptr(dk), _lib.ptr(gws), _lib.ptr(z), _lib.stream_of(dev))
+              _lib.ptr(y), _lib.ptr(r), _lib.ptr(dk), _lib.ptr(gws), _lib.ptr(z), _lib.stream_of(dev))
     if save is not None:
-        save.update(z=z, dk=dk, g=gws)
+        save.update(y=y, r=r, z=z, dk=dk, g=gws)
     if node_or_edge == "edge":
         per_edge = torch.empty_like(out)
         per_edge[plan.perm] = out     # dst-sorted position p holds original edge perm[p]
         return per_edge
     return out
+
+
+def edgewise_backward_dx(grad_out, x_shape, dt, plan, saved, rad, conv1, conv2, lmax, mmax,
+                         need_rad_grad=True, node_or_edge="node"):
+    """Input and radial gradients of :func:`edgewise_forward` from its saved
+    workspaces (maloq_message_edgewise_bwd_dx): (grad_x fp32 [N, d, C],
+    grad_rad or None, dz2 [E, d', C] the second convolution's output gradient,
+    dz1 [E, d' + lmax, c_hidden] the first one's (dL/dpre, then dL/dgate)),
+    dz2 and dz1 with the padding rows the weight gradient reads."""
+    N, d, c_x = x_shape
+    c_hidden = conv1[0].shape[0] // (2 * lmax + 1)
+    dev = grad_out.device
+    E = plan.num_edges
+    kr = kept_rows(lmax, mmax)
+    wp1t = pack_weights(conv1[0], conv1[2], lmax, mmax, True, 2 * c_x, c_hidden, dt, 1)
+    wp2t = pack_weights(conv2[0], conv2[2], lmax, mmax, False, c_hidden, c_x, dt, 1)
+    g = grad_out.float().contiguous()
+    grad_row = None
+    if node_or_edge == "edge":
+        g = g[plan.perm].contiguous()       # per-edge gradient rows in dst-sorted order
+        grad_row = torch.arange(E, device=dev, dtype=torch.int32)
+    gxs = torch.empty(N, d, 2 * c_x, device=dev, dtype=torch.float32)
+    gxd = torch.empty(N, d, 2 * c_x, device=dev, dtype=torch.float32)
+    lib = _lib.load()
+    parts = torch.empty(max(1, lib.maloq_message_partials_floats(lmax, 1, E, 2 * c_x)), device=dev,
+                        dtype=torch.float32)
+    grad_rad = None
+    if rad is not None:
+        rad = rad.to(dt).contiguous()
+        if need_rad_grad:
+            grad_rad = torch.empty_like(rad)
+    dz2 = _edge_rows(E, kr, c_x, dev, dt)
+    dzh = torch.empty(max(E, 1), kr, c_hidden, device=dev, dtype=dt)
+    dz1 = _edge_rows(E, kr + lmax, c_hidden, dev, dt)
+    _lib.call("maloq_message_edgewise_bwd_dx", DTYPE_CODE[dt], lmax, mmax, _lib.ptr(g), c_x, _lib.ptr(plan.dst),
+              _lib.ptr(grad_row), _lib.ptr(plan.bwd_src), _lib.ptr(plan.bwd_eidx), E, _lib.ptr(saved["dk"]),
+              _lib.ptr(rad), _lib.ptr(grad_rad), _lib.ptr(saved.get("r")), _lib.ptr(saved["g"]), _lib.ptr(wp1t),
+              c_hidden, _lib.ptr(wp2t), _lib.ptr(_jd_dev(lmax, dev)), _lib.ptr(gxs), _lib.ptr(gxd), N,
+              _lib.ptr(plan.seg_ptr), _lib.ptr(plan.seg_ptr_src), _lib.ptr(parts), _lib.ptr(dz2), _lib.ptr(dzh),
+              _lib.ptr(dz1), _lib.stream_of(dev))
+    gx = gxs[:, :, :c_x] + gxd[:, :, c_x:]
+    return gx, grad_rad, dz2, dz1
+
+
+class _EdgewiseFn(torch.autograd.Function):
+    """Autograd of the two-convolution block: gradients for x, rad and both
+    convolutions' weights and biases."""
+
+    @staticmethod
+    def forward(ctx, x, rad, w01, b01, w02, b02, plan, eulers, lmax, mmax, node_or_edge, *wm):
+        saved = {}
+        wm1, wm2 = list(wm[:mmax]), list(wm[mmax:])
+        out = edgewise_forward(x, plan, eulers, rad, (w01, b01, wm1), (w02, b02, wm2), lmax, mmax, save=saved,
+                               node_or_edge=node_or_edge)
+        ctx.plan, ctx.lmax, ctx.mmax, ctx.mode = plan, lmax, mmax, node_or_edge
+        ctx.x_shape, ctx.dt = tuple(x.shape), x.dtype
+        ctx.has_b = (b01 is not None, b02 is not None)
+        ctx.save_for_backward(rad, w01, w02, saved["y"], saved["r"], saved["z"], saved["dk"], saved["g"], *wm)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        rad, w01, w02, y, r, z, dk, gs, *wm = ctx.saved_tensors
+        plan, lmax, mmax = ctx.plan, ctx.lmax, ctx.mmax
+        wm1, wm2 = list(wm[:mmax]), list(wm[mmax:])
+        gx, grad_rad, dz2, dz1 = edgewise_backward_dx(g, ctx.x_shape, ctx.dt, plan, {"dk": dk, "r": r, "g": gs},
+                                                      rad, (w01, None, wm1), (w02, None, wm2), lmax, mmax,
+                                                      need_rad_grad=ctx.needs_input_grad[1], node_or_edge=ctx.mode)
+        c_x = ctx.x_shape[2]
+        c_hidden = w01.shape[0] // (2 * lmax + 1)
+        E = plan.num_edges
+        dw01, dwm1, db01 = message_weight_grad(dz1, y, lmax, mmax, c_hidden, 2 * c_x, num_edges=E, gate=True)
+        dw02, dwm2, db02 = message_weight_grad(dz2, z, lmax, mmax, c_x, c_hidden, num_edges=E)
+        gxo = gx.to(ctx.dt) if ctx.needs_input_grad[0] else None
+        grad_rad = grad_rad if ctx.needs_input_grad[1] else None
+        return (gxo, grad_rad, dw01, db01 if ctx.has_b[0] else None, dw02, db02 if ctx.has_b[1] else None,
+                None, None, None, None, None, *dwm1, *dwm2)
+
+
+def edgewise_block(x, plan, eulers, rad, conv1, conv2, lmax, mmax, node_or_edge="node"):
+    """Differentiable :func:`edgewise_forward` (gradients for x, rad and the
+    weights and biases of both convolutions)."""
+    return _EdgewiseFn.apply(x, rad, conv1[0], conv1[1], conv2[0], conv2[1], plan, eulers, lmax, mmax, node_or_edge,
+                             *conv1[2][:mmax], *conv2[2][:mmax])
 
 
 def message_backward_dx(grad_out, x_shape, dt, plan, saved, rad, w0, wm, lmax, mmax,

@@ -136,6 +136,58 @@ def test_edgewise_two_conv_matches_oracle(lmax, dtype, use_rad, device):
     assert torch.all(got[-3:] == 0), "nodes without in-edges must be exactly zero"
 
 
+@pytest.mark.parametrize("lmax,dtype,mode", [(2, torch.float32, "node"), (4, torch.float32, "node"),
+                                             (6, torch.float32, "node"), (4, torch.float32, "edge"),
+                                             (4, torch.bfloat16, "node"), (2, torch.bfloat16, "edge")])
+def test_edgewise_gradients_match_oracle_autograd(lmax, dtype, mode, device):
+    """Gradients of the two-convolution block (x, radial scales, both
+    convolutions' weights and biases) against fp64 autograd of the oracle."""
+    from maloq_amd import message as M
+    from maloq_amd.wigner import extract_euler_angles
+    print(f"edgewise grad case lmax={lmax} dtype={dtype} mode={mode}", flush=True)
+    mmax, N, E, C, H = 2, 21, 260, 32, 64
+    gen = torch.Generator().manual_seed(300 + lmax)
+    d = (lmax + 1) ** 2
+    x = torch.randn(N, d, C, generator=gen, dtype=torch.float64)
+    ei = _graph(N, E, gen, star=(lmax == 4))
+    conv1 = _conv(lmax, mmax, 2 * C, H, gen, True)
+    conv2 = _conv(lmax, mmax, H, C, gen, False)
+    rad = torch.rand(E, M.rad_width(lmax, mmax, 2 * C), generator=gen, dtype=torch.float64) + 0.5
+    gout = torch.randn(N if mode == "node" else E, d, C, generator=gen, dtype=torch.float64)
+    eul = extract_euler_angles(torch.randn(E, 3, generator=gen).float().to(device), seed=lmax)
+    q = (lambda t: t.to(dtype).double()) if dtype == torch.bfloat16 else (lambda t: t.float().double())
+    # oracle leaves: the device-visible (quantised) values in fp64
+    leaves = [q(x), q(rad), q(conv1["w0"]), conv1["b0"].float().double(), *[q(w) for w in conv1["wm"]],
+              q(conv2["w0"]), conv2["b0"].float().double(), *[q(w) for w in conv2["wm"]]]
+    leaves = [t.clone().requires_grad_() for t in leaves]
+    xo, ro, w01, b01, w11, w21, w02, b02, w12, w22 = leaves
+    e64 = eul.cpu().double()
+    ref = omsg.message_block(xo, ei, (e64[:, 0], e64[:, 1], e64[:, 2]), orot.load_jd(), lmax, mmax,
+                             {"w0": w01, "b0": b01, "wm": [w11, w21], "c_out": H}, rad=ro,
+                             conv2={"w0": w02, "b0": b02, "wm": [w12, w22], "c_out": C}, gate=True,
+                             concat="source-target", reduce=(mode == "node"))
+    ref.backward(gout)
+    plan = M.MessagePlan(ei.to(device), N)
+    dl = [t.detach().to(device) for t in leaves]
+    dl[0] = dl[0].to(dtype)
+    dl = [t.float().requires_grad_() if i > 0 else t.requires_grad_() for i, t in enumerate(dl)]
+    rad_d = plan.sort_edges(dl[1].detach()).requires_grad_()
+    out = M.edgewise_block(dl[0], plan, plan.sort_edges(eul), rad_d, (dl[2], dl[3], dl[4:6]),
+                           (dl[6], dl[7], dl[8:10]), lmax, mmax, node_or_edge=mode)
+    out.backward(gout.to(device).float())
+    torch.cuda.synchronize()
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    got = {"x": dl[0].grad, "rad": torch.empty_like(rad_d.grad).index_copy_(0, plan.perm, rad_d.grad)}
+    names = ["w01", "b01", "w11", "w21", "w02", "b02", "w12", "w22"]
+    got.update({n: t.grad for n, t in zip(names, dl[2:])})
+    want = {"x": xo.grad, "rad": ro.grad}
+    want.update({n: t.grad for n, t in zip(names, leaves[2:])})
+    for n in want:
+        scale = want[n].abs().max().item()
+        err = (got[n].double().cpu() - want[n]).abs().max().item() / scale
+        assert err < tol, (n, err)
+
+
 def test_forward_empty_graph(device):
     from maloq_amd import message as M
     plan = M.MessagePlan(torch.zeros(2, 0, dtype=torch.long, device=device), 5)
