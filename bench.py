@@ -469,6 +469,31 @@ def edgewise_call(ew):
                                   wpack1=ew["wp1"], wpack2=ew["wp2"])
 
 
+def edgewise_step(ew):
+    """Forward + backward of the two-convolution block (gradients of x, the
+    radial scales and both convolutions' weights and biases), from cleared
+    gradients."""
+    from maloq_amd import message as M
+    if "leaves" not in ew:
+        c1 = tuple(t.detach().clone().requires_grad_() for t in ew["c1"][:2]) + \
+            ([w.detach().clone().requires_grad_() for w in ew["c1"][2]],)
+        c2 = tuple(t.detach().clone().requires_grad_() for t in ew["c2"][:2]) + \
+            ([w.detach().clone().requires_grad_() for w in ew["c2"][2]],)
+        ew["leaves"] = (ew["x"].detach().clone().requires_grad_(), ew["rad"].detach().clone().requires_grad_(), c1, c2)
+        ew["gout"] = torch_randn_like_nodes(ew)
+    x, rad, c1, c2 = ew["leaves"]
+    for t in [x, rad, c1[0], c1[1], *c1[2], c2[0], c2[1], *c2[2]]:
+        t.grad = None
+    out = M.edgewise_block(x, ew["plan"], ew["eul"], rad, c1, c2, ew["L"], ew["M"])
+    out.backward(ew["gout"])
+
+
+def torch_randn_like_nodes(ew):
+    import torch
+    gen = torch.Generator().manual_seed(7)
+    return torch.randn(ew["x"].shape, generator=gen).to(ew["x"].device)
+
+
 def profile_only(args):
     """Runs one piece of the path --reps times (for rocprofv3 passes)."""
     import torch
@@ -486,6 +511,10 @@ def profile_only(args):
         ew = edgewise_workload()
         for _ in range(args.reps):
             edgewise_call(ew)
+    elif args.only == "edgewise-step":
+        ew = edgewise_workload()
+        for _ in range(args.reps):
+            edgewise_step(ew)
     elif args.only in ("fwd", "step"):
         w = message_workload(args.dtype)
         if args.only == "fwd":
@@ -517,7 +546,7 @@ def main(argv=None):
     ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp32"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-extras", action="store_true", help="headline only")
-    ap.add_argument("--only", choices=["fwd", "step", "basis", "copy", "embed", "edgewise"],
+    ap.add_argument("--only", choices=["fwd", "step", "basis", "copy", "embed", "edgewise", "edgewise-step"],
                     help="profiling mode: run one piece a few times and exit (no JSON line)")
     ap.add_argument("--reps", type=int, default=5, help="launches in --only mode")
     ap.add_argument("--traffic-from", metavar="DIR",
@@ -614,9 +643,12 @@ def main(argv=None):
         edgewise_call(gw)
         tg = kernel_time_events(lambda: edgewise_call(gw), 20)
         fl = edgewise_flops_per_edge(gw["L"], gw["M"], gw["C"], gw["H"]) * gw["E"]
+        ts = time_steps(lambda: edgewise_step(gw), 10, 3)
         result["edgewise_two_conv_fwd"] = {
             "metric": "edges/s", "value": gw["E"] / tg, "us_per_call": tg * 1e6,
-            "config": "config 2 graph, cat(x[src], x[dst]) 256 -> gated 128 -> 128 channels, bf16, forward",
+            "fwd_bwd_edges_per_s": gw["E"] / ts, "fwd_bwd_ms": ts * 1e3,
+            "config": "config 2 graph, cat(x[src], x[dst]) 256 -> gated 128 -> 128 channels, bf16; value: forward, "
+                      "fwd_bwd: forward + all gradients",
             "roofline": {"scope": "whole call (prep, two GEMMs, fixup)", "bound": "mfma",
                          "achieved": fl / tg / 1e12, "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
                          "frac": fl / tg / PEAK_BF16, "flops_per_call": fl},

@@ -10,8 +10,10 @@ messages (``forward_edge``).
 Here the whole chain is one C-ABI call, ``maloq_message_edgewise_fwd``: the
 prep kernel gathers both halves of the message and rotates them, the first
 GEMM applies the gate in its epilogue and leaves the rows in the edge frame,
-the second GEMM rotates back and sums per segment.  Forward only: the module
-refuses to run where autograd would need its backward.  Wigner matrices are
+the second GEMM rotates back and sums per segment.  The backward
+(``maloq_message_edgewise_bwd_dx`` plus the weight-gradient kernels) gives
+the gradients of x, of both convolutions' weights and of the radial
+function's parameters (through ``rad_func``).  Wigner matrices are
 built in the kernels from the Euler angles (``eulers=``, as from
 :func:`maloq_amd.wigner.extract_euler_angles`); the dense ``wigner`` /
 ``wigner_inv`` arguments of the reference signature are not read.
@@ -25,7 +27,7 @@ import torch
 from torch import nn
 
 from . import _lib
-from .message import MessagePlan, edgewise_forward, rad_width
+from .message import MessagePlan, edgewise_block, rad_width
 from .radial import RadialMLP
 
 
@@ -113,13 +115,10 @@ class Edgewise(nn.Module):
             raise NotImplementedError("message_type 'source-target-message' is not built")
         if eulers is None:
             raise ValueError("pass eulers=: the kernels build the Wigner rows from the Euler angles")
-        if torch.is_grad_enabled() and (x.requires_grad or x_edge.requires_grad
-                                        or any(p.requires_grad for p in self.parameters())):
-            raise NotImplementedError("the two-convolution backward is not built: run under torch.no_grad()")
         _lib.require_cuda(x, x_edge, eulers)
         if plan is None:
             plan = MessagePlan(edge_index, x.shape[0])
         rad = self.so2_conv_1.rad_func(plan.sort_edges(x_edge.float()), out_dtype=x.dtype)
-        out = edgewise_forward(x, plan, plan.sort_edges(eulers.float()), rad, self.so2_conv_1.weights(),
-                               self.so2_conv_2.weights(), self.lmax, self.mmax, node_or_edge=node_or_edge)
+        out = edgewise_block(x, plan, plan.sort_edges(eulers.float()), rad, self.so2_conv_1.weights(),
+                             self.so2_conv_2.weights(), self.lmax, self.mmax, node_or_edge=node_or_edge)
         return out.to(x.dtype)

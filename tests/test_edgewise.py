@@ -1,11 +1,12 @@
 """The two-convolution Edgewise block (maloq_amd.edgewise, esen_block.py:37-258).
 
 CPU: the module mirrors the reference's constructor, parameter names and
-shapes, and refuses what is not built (backward, CPU tensors, the three-part
-message).  GPU: node and edge modes against the oracle (oracle.message,
-message_block with conv2 and concat "source-target"), with the radial scales
-from the oracle RadialMLP on the module's own weights; fp32 within 1e-5 of
-the output scale."""
+shapes, and refuses what is not built (CPU tensors, the three-part message).
+GPU: node and edge modes against the oracle (oracle.message, message_block
+with conv2 and concat "source-target"), with the radial scales from the
+oracle RadialMLP on the module's own weights, output and the gradients of x,
+x_edge and every parameter (fp64 autograd through the oracle RadialMLP);
+fp32 within 1e-5 of each tensor's scale."""
 import pytest
 import torch
 
@@ -45,8 +46,6 @@ def test_module_refuses_what_is_not_built():
     N, E = 4, 6
     x = torch.zeros(N, 9, 8)
     ei = torch.zeros(2, E, dtype=torch.long)
-    with pytest.raises(NotImplementedError):      # parameters need gradients
-        mod(x, None, torch.zeros(E, 8), ei, None, None, "node", eulers=torch.zeros(E, 3))
     with torch.no_grad(), pytest.raises((_lib.MaloqHipError, RuntimeError, ValueError)):   # CPU tensors
         mod(x, None, torch.zeros(E, 8), ei, None, None, "node", eulers=torch.zeros(E, 3))
     with torch.no_grad(), pytest.raises(NotImplementedError):
@@ -63,7 +62,7 @@ def _oracle_conv(c):
 @pytest.mark.gpu
 @pytest.mark.parametrize("mode", ["node", "edge"])
 @pytest.mark.parametrize("lmax", [2, 4])
-def test_module_forward_matches_oracle(mode, lmax):
+def test_module_forward_and_gradients_match_oracle(mode, lmax):
     if not torch.cuda.is_available():
         pytest.skip("needs a GPU")
     from maloq_amd.wigner import extract_euler_angles
@@ -79,18 +78,33 @@ def test_module_forward_matches_oracle(mode, lmax):
     ei = torch.stack([src, dst])
     x_edge = torch.randn(E, 8, generator=gen)
     eul = extract_euler_angles(torch.randn(E, 3, generator=gen).to(dev), seed=5)
-    with torch.no_grad():
-        got = mod(x.to(dev), None, x_edge.to(dev), ei.to(dev), None, None, mode, eulers=eul)
-    rf = mod.so2_conv_1.rad_func
-    lins = [m for m in rf.net if isinstance(m, torch.nn.Linear)]
-    lns = [m for m in rf.net if isinstance(m, torch.nn.LayerNorm)]
-    cpu = lambda t: t.detach().double().cpu()
-    hidden = [(cpu(li.weight), cpu(li.bias), cpu(ln.weight), cpu(ln.bias)) for li, ln in zip(lins[:-1], lns)]
-    rad = radial_mlp(x_edge.double(), hidden, cpu(lins[-1].weight), cpu(lins[-1].bias), lns[0].eps)
+    xd = x.to(dev).requires_grad_()
+    xe = x_edge.to(dev).requires_grad_()
+    got = mod(xd, None, xe, ei.to(dev), None, None, mode, eulers=eul)
+    gout = torch.randn(got.shape, generator=gen, dtype=torch.float64)
+    got.backward(gout.float().to(dev))
+    # oracle: the module's parameters as fp64 leaves
+    params = {k: v.detach().double().cpu().requires_grad_() for k, v in mod.named_parameters()}
+    rf = "so2_conv_1.rad_func.net."
+    nlin = len([m for m in mod.so2_conv_1.rad_func.net if isinstance(m, torch.nn.Linear)])
+    lin_idx = [i for i, m in enumerate(mod.so2_conv_1.rad_func.net) if isinstance(m, torch.nn.Linear)]
+    ln_idx = [i for i, m in enumerate(mod.so2_conv_1.rad_func.net) if isinstance(m, torch.nn.LayerNorm)]
+    hidden = [(params[f"{rf}{li}.weight"], params[f"{rf}{li}.bias"], params[f"{rf}{ln}.weight"],
+               params[f"{rf}{ln}.bias"]) for li, ln in zip(lin_idx[:-1], ln_idx)]
+    assert len(hidden) == nlin - 1
+    x64, xe64 = x.double().requires_grad_(), x_edge.double().requires_grad_()
+    rad = radial_mlp(xe64, hidden, params[f"{rf}{lin_idx[-1]}.weight"], params[f"{rf}{lin_idx[-1]}.bias"],
+                     mod.so2_conv_1.rad_func.net[ln_idx[0]].eps)
+    conv = lambda p, c: {"w0": params[f"{p}.fc_m0.weight"], "b0": params[f"{p}.fc_m0.bias"],
+                         "wm": [params[f"{p}.so2_m_conv.{i}.fc.weight"] for i in range(2)], "c_out": c}
     e64 = eul.double().cpu()
-    ref = omsg.message_block(x.double(), ei, (e64[:, 0], e64[:, 1], e64[:, 2]), orot.load_jd(), lmax, 2,
-                             _oracle_conv(mod.so2_conv_1), rad=rad, conv2=_oracle_conv(mod.so2_conv_2), gate=True,
+    ref = omsg.message_block(x64, ei, (e64[:, 0], e64[:, 1], e64[:, 2]), orot.load_jd(), lmax, 2,
+                             conv("so2_conv_1", H), rad=rad, conv2=conv("so2_conv_2", C), gate=True,
                              concat="source-target", reduce=(mode == "node"))
+    ref.backward(gout)
     assert got.shape == ref.shape
-    scale = ref.abs().max().item()
-    assert (got.double().cpu() - ref).abs().max().item() <= 1e-5 * scale
+    pairs = [("out", got.detach(), ref.detach()), ("x", xd.grad, x64.grad), ("x_edge", xe.grad, xe64.grad)]
+    pairs += [(k, v.grad, params[k].grad) for k, v in mod.named_parameters()]
+    for name, a, b in pairs:
+        scale = b.abs().max().item()
+        assert (a.double().cpu() - b).abs().max().item() <= 1e-5 * scale, name
