@@ -200,7 +200,10 @@ int maloq_message_fwd(int dtype, int lmax, int mmax, int gate, const void* x, in
  * [E, maloq_message_wigner_floats], partials maloq_message_partials_floats(lmax, 0,
  * E, c_out) floats; gate_ws (nullable) [E, d' + lmax, c_hidden] receives the
  * first convolution's pre-activations, r_ws (nullable) [E, d', 2 c_x] the rotated
- * message rows before the radial scale (both kept for the backward).  c_x a multiple of 8.  seg_id (nullable:
+ * message rows before the radial scale (both kept for the backward).
+ * x_msg (nullable) [*, d, c_x] (dtype) with msg_row [E]: message_type
+ * "source-target-message", m_e = cat(x[src[e]], x[dst[e]], x_msg[msg_row[e]]) of
+ * 3 c_x channels (conv1 input and the workspaces' 2 c_x become 3 c_x).  c_x a multiple of 8.  seg_id (nullable:
  * dst) is the output row of each edge, non-decreasing, with seg_ptr its CSR over
  * num_nodes rows: seg_id[e] = e with seg_ptr[i] = i gives the per-edge rows of
  * Edgewise.forward_edge (esen_block.py:210-258).  Replaces the forward of
@@ -212,7 +215,8 @@ int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const void* x, int
                                const float* bias1, int c_hidden, const void* wpack2,
                                const float* bias2, const float* jd, float* out, int64_t num_nodes,
                                int c_out, const int64_t* seg_ptr, float* partials, void* y_ws,
-                               void* r_ws, float* dk_ws, void* gate_ws, void* z_ws, void* stream);
+                               void* r_ws, float* dk_ws, void* gate_ws, void* z_ws,
+                               const void* x_msg, const int32_t* msg_row, void* stream);
 
 /* Input and radial-scale gradients of the two-convolution block
  * (maloq_message_edgewise_fwd), from the forward's workspaces:
@@ -225,6 +229,10 @@ int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const void* x, int
  *   grad_x_src / grad_x_dst [num_nodes, d, 2 c_x] fp32: D_e^T rad[e] (*) SO2_1^T(dz1_e)
  *                 summed per source (channels [0, c_x) valid) and per destination
  *                 (channels [c_x, 2 c_x) valid); grad_x = the sum of the two valid halves.
+ * grad_x_msg (nullable; then a "source-target-message" block, whose 2 c_x
+ * above read 3 c_x): [E, d, 3 c_x] fp32, per dst-sorted edge position, channels
+ * [2 c_x, 3 c_x) valid: the gradient of that edge's x_msg row; edge_seg [E] =
+ * 0, 1, ..., E - 1.
  * grad_row (nullable: dst) is the row of grad_out of each edge (e for the
  * per-edge output of forward_edge, grad_out then [E, d, c_x]).
  * Edges in the forward's dst-sorted order (dst, seg_ptr); src_sorted / edge_idx /
@@ -242,7 +250,8 @@ int maloq_message_edgewise_bwd_dx(int dtype, int lmax, int mmax, const float* gr
                                   const void* wpack2_t, const float* jd, float* grad_x_src,
                                   float* grad_x_dst, int64_t num_nodes, const int64_t* seg_ptr,
                                   const int64_t* seg_ptr_src, float* partials, void* dz2_ws,
-                                  void* dzh_ws, void* dz1_ws, void* stream);
+                                  void* dzh_ws, void* dz1_ws, const int32_t* edge_seg,
+                                  float* grad_x_msg, void* stream);
 
 /* Input and radial-scale gradients of the fused block:
  *   grad_x[n] = sum_{e: src[e]=n} D_e^T rad[e] (*) SO2^T(G_e),

@@ -183,9 +183,11 @@ extern "C" int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const v
                                           const float* bias2, const float* jd, float* out,
                                           int64_t num_nodes, int c_out, const int64_t* seg_ptr,
                                           float* partials, void* y_ws, void* r_ws, float* dk_ws,
-                                          void* gate_ws, void* z_ws, void* stream) {
+                                          void* gate_ws, void* z_ws, const void* x_msg,
+                                          const int32_t* msg_row, void* stream) {
   MALOQ_REQUIRE(c_x > 0 && c_x % 8 == 0, "node channels must be a positive multiple of 8");
-  int rc = check_common(dtype, lmax, mmax, 2 * c_x, c_hidden, num_edges);
+  const int parts = x_msg ? 3 : 2;   // message parts: x[src], x[dst] [, x_msg[msg_row]]
+  int rc = check_common(dtype, lmax, mmax, parts * c_x, c_hidden, num_edges);
   if (rc) return rc;
   rc = check_common(dtype, lmax, mmax, c_hidden, c_out, num_edges);
   if (rc) return rc;
@@ -196,22 +198,24 @@ extern "C" int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const v
   const int kc = dtype == 1 ? BF16::KC : F32::KC;
   if (num_edges > 0) {
     MALOQ_REQUIRE(x && src && dst && eulers && partials && y_ws && dk_ws && z_ws, "null pointer");
+    MALOQ_REQUIRE(!x_msg || msg_row, "the edge message rows need msg_row");
     const int32_t* seg = seg_id ? seg_id : dst;
     // rotated message rows of cat(x[src], x[dst]) (radial scale applied) and the Wigner rows
     PrepArgs p{};
-    p.x = x; p.gidx = src; p.gidx2 = dst; p.x_c = c_x; p.eidx = nullptr; p.eulers = eulers;
+    p.x = x; p.gidx = src; p.gidx2 = dst; p.x3 = x_msg; p.gidx3 = msg_row; p.x_c = c_x;
+    p.eidx = nullptr; p.eulers = eulers;
     p.rad = rad; p.jd = jd; p.y = y_ws; p.r = r_ws; p.dk = dk_ws; p.build_d = 1;
-    p.E = num_edges; p.C = 2 * c_x;
+    p.E = num_edges; p.C = parts * c_x;
     rc = prep_dispatch(lmax, mmax, dtype, FWD, p, s);
     if (rc) return rc;
     // first convolution + gate, kept in the edge frame
     Args a{};
     a.a_src = y_ws; a.dk = dk_ws; a.seg = seg; a.eidx = nullptr;
     a.wpack = static_cast<const char*>(wpack1); a.bias = bias1; a.out = out; a.part = partials;
-    a.E = num_edges; a.C_k = 2 * c_x; a.C_n = c_hidden; a.n_cb = c_hidden / CB;
+    a.E = num_edges; a.C_k = parts * c_x; a.C_n = c_hidden; a.n_cb = c_hidden / CB;
     a.extra = lmax * c_hidden;
     a.ntiles = (num_edges + tile_edges(lmax, 1) - 1) / tile_edges(lmax, 1);
-    a.frags_per_cb = frags_per_cb(lmax, mmax, 1, 2 * c_x, kc);
+    a.frags_per_cb = frags_per_cb(lmax, mmax, 1, parts * c_x, kc);
     a.gsave = gate_ws; a.zout = z_ws;
     rc = dispatch(lmax, mmax, dtype, 1, FWD_EDGE, a, s);
     if (rc) return rc;
@@ -234,11 +238,12 @@ extern "C" int maloq_message_edgewise_bwd_dx(
     const void* rad, void* grad_rad, const void* r_saved, const void* gate_saved, const void* wpack1_t,
     int c_hidden, const void* wpack2_t, const float* jd, float* grad_x_src, float* grad_x_dst,
     int64_t num_nodes, const int64_t* seg_ptr, const int64_t* seg_ptr_src, float* partials,
-    void* dz2_ws, void* dzh_ws, void* dz1_ws, void* stream) {
+    void* dz2_ws, void* dzh_ws, void* dz1_ws, const int32_t* edge_seg, float* grad_x_msg, void* stream) {
   MALOQ_REQUIRE(c_x > 0 && c_x % CB == 0, "node channels must be a positive multiple of %d", CB);
+  const int parts = grad_x_msg ? 3 : 2;
   int rc = check_common(dtype, lmax, mmax, c_x, c_hidden, num_edges);   // conv2 transposed
   if (rc) return rc;
-  rc = check_common(dtype, lmax, mmax, c_hidden, 2 * c_x, num_edges);   // conv1 transposed
+  rc = check_common(dtype, lmax, mmax, c_hidden, parts * c_x, num_edges);   // conv1 transposed
   if (rc) return rc;
   MALOQ_REQUIRE(num_nodes >= 0, "num_nodes < 0");
   MALOQ_REQUIRE(grad_x_src && grad_x_dst && seg_ptr && seg_ptr_src && jd && wpack1_t && wpack2_t,
@@ -250,6 +255,7 @@ extern "C" int maloq_message_edgewise_bwd_dx(
     MALOQ_REQUIRE(grad_out && dst && src_sorted && edge_idx && dk && gate_saved && partials && dz2_ws &&
                   dzh_ws && dz1_ws, "null pointer");
     MALOQ_REQUIRE(rad == nullptr || r_saved != nullptr, "the radial gradient needs the saved rows");
+    MALOQ_REQUIRE(!grad_x_msg || edge_seg, "the edge message gradient needs edge_seg");
     // dL/d(conv2 output) in the edge frame: D_e grad_out[dst[e]]
     PrepArgs p{};
     p.x = grad_out; p.gidx = grad_row ? grad_row : dst; p.eidx = nullptr; p.jd = jd; p.y = dz2_ws;
@@ -269,28 +275,33 @@ extern "C" int maloq_message_edgewise_bwd_dx(
     // gate backward: dL/dpre (kept rows) and dL/dgate rows of conv1
     rc = gate_bwd_dispatch(lmax, mmax, dtype, dzh_ws, gate_saved, dz1_ws, num_edges, c_hidden, s);
     if (rc) return rc;
-    // conv1 transposed (gated input rows, radial gradient): the x[src] half of the
-    // message channels summed per source, then the x[dst] half per destination
-    for (int half = 0; half < 2; ++half) {
+    // conv1 transposed (gated input rows, radial gradient), one pass per message
+    // part: the x[src] channels summed per source, the x[dst] channels per
+    // destination, the edge message channels kept per edge (its own segment)
+    for (int part = 0; part < parts; ++part) {
       Args a{};
-      a.a_src = dz1_ws; a.dk = dk; a.seg = half ? dst : src_sorted; a.eidx = half ? nullptr : edge_idx;
+      a.a_src = dz1_ws; a.dk = dk; a.seg = part == 0 ? src_sorted : (part == 1 ? dst : edge_seg);
+      a.eidx = part == 0 ? edge_idx : nullptr;
       a.rad = rad; a.drad = grad_rad; a.rsave = r_saved;
-      a.wpack = static_cast<const char*>(wpack1_t); a.out = half ? grad_x_dst : grad_x_src;
-      a.part = partials; a.E = num_edges; a.C_k = c_hidden; a.C_n = 2 * c_x;
-      a.cb0 = half * (c_x / CB); a.n_cb = c_x / CB;
+      a.wpack = static_cast<const char*>(wpack1_t);
+      a.out = part == 0 ? grad_x_src : (part == 1 ? grad_x_dst : grad_x_msg);
+      a.part = partials; a.E = num_edges; a.C_k = c_hidden; a.C_n = parts * c_x;
+      a.cb0 = part * (c_x / CB); a.n_cb = c_x / CB;
       a.ntiles = (num_edges + tile_edges(lmax, 1) - 1) / tile_edges(lmax, 1);
       a.frags_per_cb = frags_per_cb(lmax, mmax, 1, c_hidden, kc);
       rc = dispatch(lmax, mmax, dtype, 1, BWD_DX, a, s);
       if (rc) return rc;
-      rc = fixup(half ? seg_ptr : seg_ptr_src, num_nodes, partials, half ? grad_x_dst : grad_x_src,
-                 d * 2 * c_x, tile_edges(lmax, 1), s);
+      // per-edge rows of the message part: single-edge segments, never cut
+      if (part == 2) continue;
+      rc = fixup(part ? seg_ptr : seg_ptr_src, num_nodes, partials, part ? grad_x_dst : grad_x_src,
+                 d * parts * c_x, tile_edges(lmax, 1), s);
       if (rc) return rc;
     }
     return MALOQ_OK;
   }
-  rc = fixup(seg_ptr_src, num_nodes, partials, grad_x_src, d * 2 * c_x, tile_edges(lmax, 1), s);
+  rc = fixup(seg_ptr_src, num_nodes, partials, grad_x_src, d * parts * c_x, tile_edges(lmax, 1), s);
   if (rc) return rc;
-  return fixup(seg_ptr, num_nodes, partials, grad_x_dst, d * 2 * c_x, tile_edges(lmax, 1), s);
+  return fixup(seg_ptr, num_nodes, partials, grad_x_dst, d * parts * c_x, tile_edges(lmax, 1), s);
 }
 
 extern "C" int maloq_message_bwd_dx(int dtype, int lmax, int mmax, int gate, const float* grad_out,

@@ -246,7 +246,10 @@ struct PrepArgs {
                         // [E_all, d' + L, C] (TM raw); y then gets d' + L rows per edge:
                         // dL/dpre of the kept rows, then dL/dgate of degrees 1..L
   const int32_t* gidx2; // nullable: second gather row per edge (concatenated message
-                        // [x[gidx] | x[gidx2]]: channels >= x_c come from x[gidx2])
+                        // [x[gidx] | x[gidx2] | x3[gidx3]]: channels [x_c, 2 x_c) from
+                        // x[gidx2], [2 x_c, 3 x_c) from x3[gidx3])
+  const void* x3;       // nullable: third source [*, d, x_c] (TX raw), per-edge rows
+  const int32_t* gidx3; // its row per edge
   int x_c;              // channels of an x row (0: C)
 };
 
@@ -335,6 +338,7 @@ struct Prep {
     float eul[TE * 3];
     int gid[TE];
     int gid2[TE];
+    int gid3[TE];
     int eid[TE];
     float m2[TE * (2 * L + 1) * (2 * L + 1)];
     float trig[TE * 3 * 2 * (L + 1)];
@@ -465,6 +469,7 @@ struct Prep {
       s.eid[tid] = ei;
       s.gid[tid] = v ? a.gidx[p] : 0;
       s.gid2[tid] = (v && a.gidx2) ? a.gidx2[p] : 0;
+      s.gid3[tid] = (v && a.gidx3) ? a.gidx3[p] : 0;
       for (int k = 0; k < 3; ++k)
         s.eul[tid * 3 + k] = (v && a.build_d) ? a.eulers[static_cast<int64_t>(ei) * 3 + k] : 0.f;
     }
@@ -495,14 +500,16 @@ struct Prep {
       run_gated_bwd(s, a, nvalid, tid);
       return;
     }
-    // concatenated message: channels [0, xc) from x[gidx], [xc, C) from x[gidx2]
+    // concatenated message: channels [0, xc) from x[gidx], [xc, 2 xc) from
+    // x[gidx2], [2 xc, 3 xc) from x3[gidx3]
     const int xc = a.x_c > 0 ? a.x_c : a.C;
     for (int u = tid; u < nvalid * nch; u += NT) {
       const int e = u / nch, c0 = (u - e * nch) * V;
       const int64_t eid = s.eid[e];
-      const bool hi = c0 >= xc;
-      const typename TX::raw* xg = reinterpret_cast<const typename TX::raw*>(a.x) +
-                                   static_cast<int64_t>(hi ? s.gid2[e] : s.gid[e]) * d * xc + (hi ? c0 - xc : c0);
+      const int part = (c0 >= xc) + (c0 >= 2 * xc);
+      const int g = part == 0 ? s.gid[e] : (part == 1 ? s.gid2[e] : s.gid3[e]);
+      const typename TX::raw* xg = reinterpret_cast<const typename TX::raw*>(part == 2 ? a.x3 : a.x) +
+                                   static_cast<int64_t>(g) * d * xc + (c0 - part * xc);
       typename TM::raw* yo = reinterpret_cast<typename TM::raw*>(a.y) + eid * P::DP * a.C + c0;
       typename TM::raw* ro = a.r ? reinterpret_cast<typename TM::raw*>(a.r) + eid * P::DP * a.C + c0 : nullptr;
       const typename TM::raw* rp = a.rad ? reinterpret_cast<const typename TM::raw*>(a.rad) + eid * rw + c0 : nullptr;

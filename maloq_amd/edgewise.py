@@ -77,8 +77,8 @@ class SO2_Convolution(nn.Module):
 class Edgewise(nn.Module):
     """Drop-in for the reference's Edgewise (esen_block.py:37-258): same
     constructor arguments and parameter names (``so2_conv_1.*``,
-    ``so2_conv_2.*``).  message_type "source-target" runs; the three-part
-    "source-target-message" is accepted by the constructor only."""
+    ``so2_conv_2.*``); message_type "source-target" or "source-target-message"
+    (then ``x_message_edge`` [E, d, sphere_channels] is the third part)."""
 
     def __init__(self, sphere_channels, hidden_channels, lmax, mmax, edge_channels_list, mappingReduced, SO3_grid,
                  cutoff, message_type, act_type="gate", include_edges=True) -> None:
@@ -111,8 +111,8 @@ class Edgewise(nn.Module):
         graph's MessagePlan (built here when not given)."""
         if partition:
             raise NotImplementedError("partitioned (multi-GPU) graphs are not supported on one GPU")
-        if self.concat_size != 2:
-            raise NotImplementedError("message_type 'source-target-message' is not built")
+        if self.concat_size == 3 and x_message_edge is None:
+            raise ValueError("message_type 'source-target-message' needs x_message_edge")
         if eulers is None:
             raise ValueError("pass eulers=: the kernels build the Wigner rows from the Euler angles")
         _lib.require_cuda(x, x_edge, eulers)
@@ -120,5 +120,6 @@ class Edgewise(nn.Module):
             plan = MessagePlan(edge_index, x.shape[0])
         rad = self.so2_conv_1.rad_func(plan.sort_edges(x_edge.float()), out_dtype=x.dtype)
         out = edgewise_block(x, plan, plan.sort_edges(eulers.float()), rad, self.so2_conv_1.weights(),
-                             self.so2_conv_2.weights(), self.lmax, self.mmax, node_or_edge=node_or_edge)
+                             self.so2_conv_2.weights(), self.lmax, self.mmax, node_or_edge=node_or_edge,
+                             x_message_edge=x_message_edge if self.concat_size == 3 else None)
         return out.to(x.dtype)

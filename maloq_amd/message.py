@@ -251,13 +251,16 @@ def message_forward(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=False, wp
 
 
 def edgewise_forward(x, plan, eulers, rad, conv1, conv2, lmax, mmax, wpack1=None, wpack2=None,
-                     save=None, node_or_edge="node"):
+                     save=None, node_or_edge="node", x_message_edge=None):
     """Node output [N, d, c_out] fp32 of the two-convolution block
     ``Edgewise.forward_node`` with message_type "source-target"
     (esen_block.py:146-208; maloq_message_edgewise_fwd), forward only.
     ``node_or_edge="edge"``: the rotated-back message of every edge instead,
     [E, d, c_out] in the original edge order (``Edgewise.forward_edge``,
     esen_block.py:210-258): each edge is its own output row.
+    ``x_message_edge`` [E, d, C] (original edge order): message_type
+    "source-target-message", the message ``cat(x[src], x[dst], x_message_edge)``
+    and conv1's input 3 C.
 
     The message is ``cat(x[src], x[dst])``; ``conv1 = (w0, b0, wm)`` is the
     gated first SO(2) convolution (input 2 C, w0/b0 carry the lmax c_hidden gate
@@ -277,8 +280,13 @@ def edgewise_forward(x, plan, eulers, rad, conv1, conv2, lmax, mmax, wpack1=None
     assert d == (lmax + 1) ** 2, "x must be [N, (lmax+1)^2, C]"
     c_hidden = conv1[0].shape[0] // (2 * lmax + 1)
     c_out = conv2[0].shape[0] // (lmax + 1)
+    npart = 2 if x_message_edge is None else 3
+    xm = None
+    if x_message_edge is not None:
+        assert tuple(x_message_edge.shape) == (plan.num_edges, d, c_x), "x_message_edge must be [E, d, C]"
+        xm = x_message_edge.to(dt).contiguous()
     if wpack1 is None:
-        wpack1 = pack_weights(conv1[0], conv1[2], lmax, mmax, True, 2 * c_x, c_hidden, dt, 0)
+        wpack1 = pack_weights(conv1[0], conv1[2], lmax, mmax, True, npart * c_x, c_hidden, dt, 0)
     if wpack2 is None:
         wpack2 = pack_weights(conv2[0], conv2[2], lmax, mmax, False, c_hidden, c_out, dt, 0)
     E = plan.num_edges
@@ -297,15 +305,15 @@ def edgewise_forward(x, plan, eulers, rad, conv1, conv2, lmax, mmax, wpack1=None
     parts = torch.empty(max(1, lib.maloq_message_partials_floats(lmax, 0, E, c_out)), device=dev,
                         dtype=torch.float32)
     if rad is not None:
-        assert rad.shape == (E, rad_width(lmax, mmax, 2 * c_x)), "rad must be [E, sum_m (lmax-m+1) 2C]"
+        assert rad.shape == (E, rad_width(lmax, mmax, npart * c_x)), "rad must be [E, sum_m (lmax-m+1) npart C]"
         rad = rad.to(dt).contiguous()
     if save is not None:
-        y = _edge_rows(E, kr, 2 * c_x, dev, dt)
+        y = _edge_rows(E, kr, npart * c_x, dev, dt)
         z = _edge_rows(E, kr, c_hidden, dev, dt)
     else:
-        y = torch.empty(max(E, 1), kr, 2 * c_x, device=dev, dtype=dt)
+        y = torch.empty(max(E, 1), kr, npart * c_x, device=dev, dtype=dt)
         z = torch.empty(max(E, 1), kr, c_hidden, device=dev, dtype=dt)
-    r = torch.empty(max(E, 1), kr, 2 * c_x, device=dev, dtype=dt) \
+    r = torch.empty(max(E, 1), kr, npart * c_x, device=dev, dtype=dt) \
         if (save is not None and rad is not None) else None
     dk = torch.empty(max(E, 1), wigner_floats(lmax, mmax), device=dev, dtype=torch.float32)
     gws = torch.empty(max(E, 1), kr + lmax, c_hidden, device=dev, dtype=dt) if save is not None else None
@@ -313,11 +321,13 @@ def edgewise_forward(x, plan, eulers, rad, conv1, conv2, lmax, mmax, wpack1=None
     b2 = conv2[1].float().contiguous() if conv2[1] is not None else None
     xc = x.contiguous()
     eul = eulers.float().contiguous()
+    mrow = plan.perm.int().contiguous() if xm is not None else None   # x_message_edge row per position
     _lib.call("maloq_message_edgewise_fwd", DTYPE_CODE[dt], lmax, mmax, _lib.ptr(xc), c_x,
               _lib.ptr(plan.src), _lib.ptr(plan.dst), _lib.ptr(seg_id), E, _lib.ptr(eul), _lib.ptr(rad),
               _lib.ptr(wpack1), _lib.ptr(b1), c_hidden, _lib.ptr(wpack2), _lib.ptr(b2),
               _lib.ptr(_jd_dev(lmax, dev)), _lib.ptr(out), rows, c_out, _lib.ptr(seg_ptr), _lib.ptr(parts),
-              _lib.ptr(y), _lib.ptr(r), _lib.ptr(dk), _lib.ptr(gws), _lib.ptr(z), _lib.stream_of(dev))
+              _lib.ptr(y), _lib.ptr(r), _lib.ptr(dk), _lib.ptr(gws), _lib.ptr(z), _lib.ptr(xm),
+              _lib.ptr(mrow), _lib.stream_of(dev))
     if save is not None:
         save.update(y=y, r=r, z=z, dk=dk, g=gws)
     if node_or_edge == "edge":
@@ -328,29 +338,33 @@ def edgewise_forward(x, plan, eulers, rad, conv1, conv2, lmax, mmax, wpack1=None
 
 
 def edgewise_backward_dx(grad_out, x_shape, dt, plan, saved, rad, conv1, conv2, lmax, mmax,
-                         need_rad_grad=True, node_or_edge="node"):
+                         need_rad_grad=True, node_or_edge="node", parts=2):
     """Input and radial gradients of :func:`edgewise_forward` from its saved
     workspaces (maloq_message_edgewise_bwd_dx): (grad_x fp32 [N, d, C],
     grad_rad or None, dz2 [E, d', C] the second convolution's output gradient,
     dz1 [E, d' + lmax, c_hidden] the first one's (dL/dpre, then dL/dgate)),
-    dz2 and dz1 with the padding rows the weight gradient reads."""
+    dz2 and dz1 with the padding rows the weight gradient reads; with
+    ``parts=3`` (a "source-target-message" block) also the gradient of
+    x_message_edge [E, d, C] in the original edge order, fifth."""
     N, d, c_x = x_shape
     c_hidden = conv1[0].shape[0] // (2 * lmax + 1)
     dev = grad_out.device
     E = plan.num_edges
     kr = kept_rows(lmax, mmax)
-    wp1t = pack_weights(conv1[0], conv1[2], lmax, mmax, True, 2 * c_x, c_hidden, dt, 1)
+    wp1t = pack_weights(conv1[0], conv1[2], lmax, mmax, True, parts * c_x, c_hidden, dt, 1)
     wp2t = pack_weights(conv2[0], conv2[2], lmax, mmax, False, c_hidden, c_x, dt, 1)
     g = grad_out.float().contiguous()
     grad_row = None
     if node_or_edge == "edge":
         g = g[plan.perm].contiguous()       # per-edge gradient rows in dst-sorted order
         grad_row = torch.arange(E, device=dev, dtype=torch.int32)
-    gxs = torch.empty(N, d, 2 * c_x, device=dev, dtype=torch.float32)
-    gxd = torch.empty(N, d, 2 * c_x, device=dev, dtype=torch.float32)
+    gxs = torch.empty(N, d, parts * c_x, device=dev, dtype=torch.float32)
+    gxd = torch.empty(N, d, parts * c_x, device=dev, dtype=torch.float32)
+    gxm = torch.empty(max(E, 1), d, parts * c_x, device=dev, dtype=torch.float32) if parts == 3 else None
+    edge_seg = torch.arange(E, device=dev, dtype=torch.int32) if parts == 3 else None
     lib = _lib.load()
-    parts = torch.empty(max(1, lib.maloq_message_partials_floats(lmax, 1, E, 2 * c_x)), device=dev,
-                        dtype=torch.float32)
+    pbuf = torch.empty(max(1, lib.maloq_message_partials_floats(lmax, 1, E, parts * c_x)), device=dev,
+                       dtype=torch.float32)
     grad_rad = None
     if rad is not None:
         rad = rad.to(dt).contiguous()
@@ -363,10 +377,14 @@ def edgewise_backward_dx(grad_out, x_shape, dt, plan, saved, rad, conv1, conv2, 
               _lib.ptr(grad_row), _lib.ptr(plan.bwd_src), _lib.ptr(plan.bwd_eidx), E, _lib.ptr(saved["dk"]),
               _lib.ptr(rad), _lib.ptr(grad_rad), _lib.ptr(saved.get("r")), _lib.ptr(saved["g"]), _lib.ptr(wp1t),
               c_hidden, _lib.ptr(wp2t), _lib.ptr(_jd_dev(lmax, dev)), _lib.ptr(gxs), _lib.ptr(gxd), N,
-              _lib.ptr(plan.seg_ptr), _lib.ptr(plan.seg_ptr_src), _lib.ptr(parts), _lib.ptr(dz2), _lib.ptr(dzh),
-              _lib.ptr(dz1), _lib.stream_of(dev))
-    gx = gxs[:, :, :c_x] + gxd[:, :, c_x:]
-    return gx, grad_rad, dz2, dz1
+              _lib.ptr(plan.seg_ptr), _lib.ptr(plan.seg_ptr_src), _lib.ptr(pbuf), _lib.ptr(dz2), _lib.ptr(dzh),
+              _lib.ptr(dz1), _lib.ptr(edge_seg), _lib.ptr(gxm), _lib.stream_of(dev))
+    gx = gxs[:, :, :c_x] + gxd[:, :, c_x:2 * c_x]
+    if parts == 2:
+        return gx, grad_rad, dz2, dz1
+    gm = torch.empty(E, d, c_x, device=dev, dtype=torch.float32)
+    gm[plan.perm] = gxm[:E, :, 2 * c_x:]      # dst-sorted position p holds original edge perm[p]
+    return gx, grad_rad, dz2, dz1, gm
 
 
 class _EdgewiseFn(torch.autograd.Function):
@@ -374,12 +392,13 @@ class _EdgewiseFn(torch.autograd.Function):
     convolutions' weights and biases."""
 
     @staticmethod
-    def forward(ctx, x, rad, w01, b01, w02, b02, plan, eulers, lmax, mmax, node_or_edge, *wm):
+    def forward(ctx, x, rad, w01, b01, w02, b02, xm, plan, eulers, lmax, mmax, node_or_edge, *wm):
         saved = {}
         wm1, wm2 = list(wm[:mmax]), list(wm[mmax:])
         out = edgewise_forward(x, plan, eulers, rad, (w01, b01, wm1), (w02, b02, wm2), lmax, mmax, save=saved,
-                               node_or_edge=node_or_edge)
+                               node_or_edge=node_or_edge, x_message_edge=xm)
         ctx.plan, ctx.lmax, ctx.mmax, ctx.mode = plan, lmax, mmax, node_or_edge
+        ctx.parts, ctx.xm_dtype = (2, None) if xm is None else (3, xm.dtype)
         ctx.x_shape, ctx.dt = tuple(x.shape), x.dtype
         ctx.has_b = (b01 is not None, b02 is not None)
         ctx.save_for_backward(rad, w01, w02, saved["y"], saved["r"], saved["z"], saved["dk"], saved["g"], *wm)
@@ -390,25 +409,28 @@ class _EdgewiseFn(torch.autograd.Function):
         rad, w01, w02, y, r, z, dk, gs, *wm = ctx.saved_tensors
         plan, lmax, mmax = ctx.plan, ctx.lmax, ctx.mmax
         wm1, wm2 = list(wm[:mmax]), list(wm[mmax:])
-        gx, grad_rad, dz2, dz1 = edgewise_backward_dx(g, ctx.x_shape, ctx.dt, plan, {"dk": dk, "r": r, "g": gs},
-                                                      rad, (w01, None, wm1), (w02, None, wm2), lmax, mmax,
-                                                      need_rad_grad=ctx.needs_input_grad[1], node_or_edge=ctx.mode)
+        res = edgewise_backward_dx(g, ctx.x_shape, ctx.dt, plan, {"dk": dk, "r": r, "g": gs}, rad,
+                                   (w01, None, wm1), (w02, None, wm2), lmax, mmax,
+                                   need_rad_grad=ctx.needs_input_grad[1], node_or_edge=ctx.mode, parts=ctx.parts)
+        gx, grad_rad, dz2, dz1 = res[:4]
+        gxm = res[4].to(ctx.xm_dtype) if (ctx.parts == 3 and ctx.needs_input_grad[6]) else None
         c_x = ctx.x_shape[2]
         c_hidden = w01.shape[0] // (2 * lmax + 1)
         E = plan.num_edges
-        dw01, dwm1, db01 = message_weight_grad(dz1, y, lmax, mmax, c_hidden, 2 * c_x, num_edges=E, gate=True)
+        dw01, dwm1, db01 = message_weight_grad(dz1, y, lmax, mmax, c_hidden, ctx.parts * c_x, num_edges=E,
+                                               gate=True)
         dw02, dwm2, db02 = message_weight_grad(dz2, z, lmax, mmax, c_x, c_hidden, num_edges=E)
         gxo = gx.to(ctx.dt) if ctx.needs_input_grad[0] else None
         grad_rad = grad_rad if ctx.needs_input_grad[1] else None
         return (gxo, grad_rad, dw01, db01 if ctx.has_b[0] else None, dw02, db02 if ctx.has_b[1] else None,
-                None, None, None, None, None, *dwm1, *dwm2)
+                gxm, None, None, None, None, None, *dwm1, *dwm2)
 
 
-def edgewise_block(x, plan, eulers, rad, conv1, conv2, lmax, mmax, node_or_edge="node"):
-    """Differentiable :func:`edgewise_forward` (gradients for x, rad and the
-    weights and biases of both convolutions)."""
-    return _EdgewiseFn.apply(x, rad, conv1[0], conv1[1], conv2[0], conv2[1], plan, eulers, lmax, mmax, node_or_edge,
-                             *conv1[2][:mmax], *conv2[2][:mmax])
+def edgewise_block(x, plan, eulers, rad, conv1, conv2, lmax, mmax, node_or_edge="node", x_message_edge=None):
+    """Differentiable :func:`edgewise_forward` (gradients for x, rad,
+    x_message_edge and the weights and biases of both convolutions)."""
+    return _EdgewiseFn.apply(x, rad, conv1[0], conv1[1], conv2[0], conv2[1], x_message_edge, plan, eulers, lmax, mmax,
+                             node_or_edge, *conv1[2][:mmax], *conv2[2][:mmax])
 
 
 def message_backward_dx(grad_out, x_shape, dt, plan, saved, rad, w0, wm, lmax, mmax,

@@ -1,7 +1,7 @@
 """The two-convolution Edgewise block (maloq_amd.edgewise, esen_block.py:37-258).
 
 CPU: the module mirrors the reference's constructor, parameter names and
-shapes, and refuses what is not built (CPU tensors, the three-part message).
+shapes, and refuses CPU tensors and a three-part message without its third part.
 GPU: node and edge modes against the oracle (oracle.message, message_block
 with conv2 and concat "source-target"), with the radial scales from the
 oracle RadialMLP on the module's own weights, output and the gradients of x,
@@ -48,7 +48,7 @@ def test_module_refuses_what_is_not_built():
     ei = torch.zeros(2, E, dtype=torch.long)
     with torch.no_grad(), pytest.raises((_lib.MaloqHipError, RuntimeError, ValueError)):   # CPU tensors
         mod(x, None, torch.zeros(E, 8), ei, None, None, "node", eulers=torch.zeros(E, 3))
-    with torch.no_grad(), pytest.raises(NotImplementedError):
+    with torch.no_grad(), pytest.raises(ValueError):
         _module(C=8, H=32, lmax=2, message_type="source-target-message")(
             x, None, torch.zeros(E, 8), ei, None, None, "node", eulers=torch.zeros(E, 3))
 

@@ -188,6 +188,59 @@ def test_edgewise_gradients_match_oracle_autograd(lmax, dtype, mode, device):
         assert err < tol, (n, err)
 
 
+@pytest.mark.parametrize("dtype,mode", [(torch.float32, "node"), (torch.bfloat16, "node"), (torch.float32, "edge")])
+def test_edgewise_source_target_message(dtype, mode, device):
+    """Three-part message cat(x[src], x[dst], x_message_edge): output and every
+    gradient (x_message_edge included) against fp64 autograd of the oracle."""
+    from maloq_amd import message as M
+    from maloq_amd.wigner import extract_euler_angles
+    print(f"edgewise 3-part case dtype={dtype} mode={mode}", flush=True)
+    lmax, mmax, N, E, C, H = 4, 2, 19, 230, 32, 64
+    gen = torch.Generator().manual_seed(404)
+    d = (lmax + 1) ** 2
+    x = torch.randn(N, d, C, generator=gen, dtype=torch.float64)
+    xm = torch.randn(E, d, C, generator=gen, dtype=torch.float64)
+    ei = _graph(N, E, gen, star=True)
+    conv1 = _conv(lmax, mmax, 3 * C, H, gen, True)
+    conv2 = _conv(lmax, mmax, H, C, gen, False)
+    rad = torch.rand(E, M.rad_width(lmax, mmax, 3 * C), generator=gen, dtype=torch.float64) + 0.5
+    gout = torch.randn(N if mode == "node" else E, d, C, generator=gen, dtype=torch.float64)
+    eul = extract_euler_angles(torch.randn(E, 3, generator=gen).float().to(device), seed=9)
+    q = (lambda t: t.to(dtype).double()) if dtype == torch.bfloat16 else (lambda t: t.float().double())
+    leaves = [q(x), q(xm), q(rad), q(conv1["w0"]), conv1["b0"].float().double(), *[q(w) for w in conv1["wm"]],
+              q(conv2["w0"]), conv2["b0"].float().double(), *[q(w) for w in conv2["wm"]]]
+    leaves = [t.clone().requires_grad_() for t in leaves]
+    xo, xmo, ro, w01, b01, w11, w21, w02, b02, w12, w22 = leaves
+    e64 = eul.cpu().double()
+    ref = omsg.message_block(xo, ei, (e64[:, 0], e64[:, 1], e64[:, 2]), orot.load_jd(), lmax, mmax,
+                             {"w0": w01, "b0": b01, "wm": [w11, w21], "c_out": H}, rad=ro,
+                             conv2={"w0": w02, "b0": b02, "wm": [w12, w22], "c_out": C}, gate=True,
+                             concat="source-target-message", x_message_edge=xmo, reduce=(mode == "node"))
+    ref.backward(gout)
+    plan = M.MessagePlan(ei.to(device), N)
+    dl = [t.detach().to(device) for t in leaves]
+    dl[0], dl[1] = dl[0].to(dtype), dl[1].to(dtype)
+    dl = [(t if i < 2 else t.float()).requires_grad_() for i, t in enumerate(dl)]
+    rad_d = plan.sort_edges(dl[2].detach()).requires_grad_()
+    out = M.edgewise_block(dl[0], plan, plan.sort_edges(eul), rad_d, (dl[3], dl[4], dl[5:7]),
+                           (dl[7], dl[8], dl[9:11]), lmax, mmax, node_or_edge=mode, x_message_edge=dl[1])
+    out.backward(gout.to(device).float())
+    torch.cuda.synchronize()
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    scale = ref.abs().max().item()
+    assert (out.detach().double().cpu() - ref.detach()).abs().max().item() < tol * scale
+    got = {"x": dl[0].grad, "xm": dl[1].grad,
+           "rad": torch.empty_like(rad_d.grad).index_copy_(0, plan.perm, rad_d.grad)}
+    names = ["w01", "b01", "w11", "w21", "w02", "b02", "w12", "w22"]
+    got.update({n: t.grad for n, t in zip(names, dl[3:])})
+    want = {"x": xo.grad, "xm": xmo.grad, "rad": ro.grad}
+    want.update({n: t.grad for n, t in zip(names, leaves[3:])})
+    for n in want:
+        scale = want[n].abs().max().item()
+        err = (got[n].double().cpu() - want[n]).abs().max().item() / scale
+        assert err < tol, (n, err)
+
+
 def test_forward_empty_graph(device):
     from maloq_amd import message as M
     plan = M.MessagePlan(torch.zeros(2, 0, dtype=torch.long, device=device), 5)

@@ -344,6 +344,36 @@ def test_message_block_source_target_concat(half, Jd):
     assert torch.allclose(got, want, atol=1e-12)
 
 
+def test_message_block_source_target_message_concat(Jd):
+    """The third part of cat(x[src], x[dst], x_message_edge): with the weights of
+    the first two parts zeroed, the block is the one-source block on a graph
+    whose edge e has its own source node e carrying x_message_edge[e]."""
+    lmax, mmax = 2, 2
+    g = torch.Generator().manual_seed(70)
+    N, E, C, H = 5, 18, 3, 4
+    x = torch.randn(N, (lmax + 1) ** 2, C, generator=g)
+    xm = torch.randn(E, (lmax + 1) ** 2, C, generator=g)
+    ei = _random_graph(N, E, g)
+    eul = orot.init_edge_rot_euler_angles(torch.randn(E, 3, generator=g), torch.rand(E, generator=g))
+    conv1 = _conv_params(lmax, mmax, 3 * C, H, g, extra=lmax * H)
+    conv2 = _conv_params(lmax, mmax, H, C, g)
+    m_size = [lmax - m + 1 for m in range(mmax + 1)]
+    cols = lambda n, part: torch.tensor([l * 3 * C + part * C + k for l in range(n) for k in range(C)])
+    z1 = copy.deepcopy(conv1)
+    for part in (0, 1):
+        z1["w0"][:, cols(m_size[0], part)] = 0
+        for m in range(1, mmax + 1):
+            z1["wm"][m - 1][:, cols(m_size[m], part)] = 0
+    got = omsg.message_block(x, ei, eul, Jd, lmax, mmax, z1, conv2=conv2, gate=True,
+                             concat="source-target-message", x_message_edge=xm)
+    kept = {"w0": conv1["w0"][:, cols(m_size[0], 2)], "b0": conv1["b0"],
+            "wm": [w[:, cols(m_size[m], 2)] for m, w in zip(range(1, mmax + 1), conv1["wm"])], "c_out": H}
+    ei1 = torch.stack([torch.arange(E), ei[1]])
+    want = omsg.message_block(xm, ei1, eul, Jd, lmax, mmax, kept, conv2=conv2, gate=True)
+    assert torch.allclose(got, want[:N], atol=1e-12)
+    assert torch.all(want[N:] == 0)
+
+
 def test_message_block_global_equivariance_config1(Jd):
     """Config 1 of the benchmark: rotate positions by R and node features by D(R):
     the block's output rotates by D(R)."""
