@@ -8,24 +8,32 @@ namespace maloq {
 namespace msg {
 
 // Node outputs of segments cut by tile boundaries (summed in tile order) and
-// of empty segments (zero).  seg_ptr: CSR of the segment ids over edges.
-__global__ void message_fixup_kernel(const int64_t* __restrict__ seg_ptr, int64_t nseg,
-                                     const float* __restrict__ part, float* __restrict__ out,
-                                     int64_t row_elems, int TE) {
-  const int64_t node = blockIdx.y;
-  const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (node >= nseg || c >= row_elems) return;
+// of empty segments (zero).  seg_ptr: CSR of the segment ids over edges.  A
+// workgroup per node, 16-byte columns (row_elems a multiple of 4); the
+// workgroups of nodes the main kernel wrote in full exit at once.
+__global__ __launch_bounds__(256) void message_fixup_kernel(const int64_t* __restrict__ seg_ptr,
+                                                            const float* __restrict__ part,
+                                                            float* __restrict__ out, int64_t row_elems,
+                                                            int TE) {
+  const int64_t node = blockIdx.x;
   const int64_t s0 = seg_ptr[node], s1 = seg_ptr[node + 1];
-  float* o = out + node * row_elems + c;
+  float4* o = reinterpret_cast<float4*>(out + node * row_elems);
+  const int64_t n4 = row_elems / 4;
   if (s1 == s0) {
-    *o = 0.f;
+    for (int64_t c = threadIdx.x; c < n4; c += blockDim.x) o[c] = make_float4(0.f, 0.f, 0.f, 0.f);
     return;
   }
   const int64_t t0 = s0 / TE, t1 = (s1 - 1) / TE;
   if (t0 == t1) return;  // written by the main kernel
-  float sum = part[((t0 * 2) + ((s0 == t0 * TE) ? 0 : 1)) * row_elems + c];
-  for (int64_t t = t0 + 1; t <= t1; ++t) sum += part[(t * 2) * row_elems + c];
-  *o = sum;
+  const float4* first = reinterpret_cast<const float4*>(part + ((t0 * 2) + ((s0 == t0 * TE) ? 0 : 1)) * row_elems);
+  for (int64_t c = threadIdx.x; c < n4; c += blockDim.x) {
+    float4 sum = first[c];
+    for (int64_t t = t0 + 1; t <= t1; ++t) {
+      const float4 v = reinterpret_cast<const float4*>(part + (t * 2) * row_elems)[c];
+      sum.x += v.x; sum.y += v.y; sum.z += v.z; sum.w += v.w;
+    }
+    o[c] = sum;
+  }
 }
 
 // Packed B fragments per output-channel block: for every kernel-input degree
@@ -49,15 +57,13 @@ static int64_t frags_per_cb(int lmax, int mmax, int gate, int c_k, int kc) {
 static int fixup(const int64_t* seg_ptr, int64_t nseg, const float* part, float* out,
                  int64_t row_elems, int TE, hipStream_t s) {
   if (nseg == 0) return MALOQ_OK;
-  const unsigned gx = static_cast<unsigned>((row_elems + 255) / 256);
-  for (int64_t s0 = 0; s0 < nseg; s0 += 65535) {
-    const int64_t ns = (nseg - s0) < 65535 ? (nseg - s0) : 65535;
-    hipLaunchKernelGGL(message_fixup_kernel, dim3(gx, static_cast<unsigned>(ns)), dim3(256), 0, s,
-                       seg_ptr + s0, ns, part, out + s0 * row_elems, row_elems, TE);
-    int rc = check_launch("message_fixup_kernel");
-    if (rc) return rc;
-  }
-  return MALOQ_OK;
+  MALOQ_REQUIRE(row_elems % 4 == 0, "row width must be a multiple of 4");
+  MALOQ_REQUIRE(((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(part)) & 15) == 0,
+                "output and partials must be 16-byte aligned");
+  MALOQ_REQUIRE(nseg < (int64_t(1) << 31), "too many segments");
+  hipLaunchKernelGGL(message_fixup_kernel, dim3(static_cast<unsigned>(nseg)), dim3(256), 0, s, seg_ptr, part,
+                     out, row_elems, TE);
+  return check_launch("message_fixup_kernel");
 }
 
 static int dispatch(int lmax, int mmax, int dtype, int gate, int mode, const Args& a,

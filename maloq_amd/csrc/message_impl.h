@@ -322,10 +322,14 @@ __device__ __forceinline__ void store_vec<F32, 4>(float* p, const float (&v)[4])
   *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
+// Edges and threads per prep workgroup (the grid is ceil(E / PREP_TE)).
+constexpr int PREP_TE = 16;
+constexpr int PREP_NT = 256;
+
 template <int L, int M, class TM, class TX, bool GATED = false>
 struct Prep {
-  static constexpr int TE = 32;
-  static constexpr int NT = 256;
+  static constexpr int TE = PREP_TE;
+  static constexpr int NT = PREP_NT;
   using P = Plan<L, M, false, 4, 1>;
   using PL = PairLayout<L, M>;
   static constexpr int WS = PL::WS;
@@ -554,7 +558,7 @@ struct Prep {
 };
 
 template <int L, int M, class TM, class TX, bool GATED = false>
-__global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
+__global__ __launch_bounds__(PREP_NT) void prep_kernel(PrepArgs a) {
   Prep<L, M, TM, TX, GATED>::run(a);
 }
 

@@ -103,9 +103,9 @@ int gate_bwd_lm(int dtype, const void* dz, const void* gsave, void* dp, int64_t 
 // fp32 output gradients and writes dtype rows.
 template <int L, int M>
 int prep_lm(int dtype, int mode, const PrepArgs& a, hipStream_t s) {
-  const int64_t grid = (a.E + 31) / 32;
+  const int64_t grid = (a.E + PREP_TE - 1) / PREP_TE;
   MALOQ_REQUIRE(grid < (int64_t(1) << 31), "grid too large");
-  const dim3 g(static_cast<unsigned>(grid)), b(256);
+  const dim3 g(static_cast<unsigned>(grid)), b(PREP_NT);
   const bool gated = mode != FWD && a.gsave != nullptr;
   if (dtype == 1) {
     if (mode == FWD)
