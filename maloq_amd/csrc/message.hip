@@ -293,21 +293,21 @@ extern "C" int maloq_message_edgewise_bwd_dx(
       a.out = part == 0 ? grad_x_src : (part == 1 ? grad_x_dst : grad_x_msg);
       a.part = partials; a.E = num_edges; a.C_k = c_hidden; a.C_n = parts * c_x;
       a.cb0 = part * (c_x / CB); a.n_cb = c_x / CB;
-      a.ntiles = (num_edges + tile_edges(lmax, 1) - 1) / tile_edges(lmax, 1);
+      a.ntiles = (num_edges + tile_edges(lmax, 1, BWD_DX) - 1) / tile_edges(lmax, 1, BWD_DX);
       a.frags_per_cb = frags_per_cb(lmax, mmax, 1, c_hidden, kc);
       rc = dispatch(lmax, mmax, dtype, 1, BWD_DX, a, s);
       if (rc) return rc;
       // per-edge rows of the message part: single-edge segments, never cut
       if (part == 2) continue;
       rc = fixup(part ? seg_ptr : seg_ptr_src, num_nodes, partials, part ? grad_x_dst : grad_x_src,
-                 d * parts * c_x, tile_edges(lmax, 1), s);
+                 d * parts * c_x, tile_edges(lmax, 1, BWD_DX), s);
       if (rc) return rc;
     }
     return MALOQ_OK;
   }
-  rc = fixup(seg_ptr_src, num_nodes, partials, grad_x_src, d * parts * c_x, tile_edges(lmax, 1), s);
+  rc = fixup(seg_ptr_src, num_nodes, partials, grad_x_src, d * parts * c_x, tile_edges(lmax, 1, BWD_DX), s);
   if (rc) return rc;
-  return fixup(seg_ptr, num_nodes, partials, grad_x_dst, d * parts * c_x, tile_edges(lmax, 1), s);
+  return fixup(seg_ptr, num_nodes, partials, grad_x_dst, d * parts * c_x, tile_edges(lmax, 1, BWD_DX), s);
 }
 
 extern "C" int maloq_message_bwd_dx(int dtype, int lmax, int mmax, int gate, const float* grad_out,
@@ -340,11 +340,11 @@ extern "C" int maloq_message_bwd_dx(int dtype, int lmax, int mmax, int gate, con
     a.rad = rad; a.drad = grad_rad; a.rsave = r_saved;
     a.wpack = static_cast<const char*>(wpack_t); a.bias = nullptr; a.out = grad_x;
     a.part = partials; a.E = num_edges; a.C_k = c_out; a.C_n = c_in; a.n_cb = c_in / CB;
-    a.extra = 0; a.ntiles = (num_edges + tile_edges(lmax, gate) - 1) / tile_edges(lmax, gate);
+    a.extra = 0; a.ntiles = (num_edges + tile_edges(lmax, gate, BWD_DX) - 1) / tile_edges(lmax, gate, BWD_DX);
     const int kc = dtype == 1 ? BF16::KC : F32::KC;
     a.frags_per_cb = frags_per_cb(lmax, mmax, gate, c_out, kc);
     rc = dispatch(lmax, mmax, dtype, gate, BWD_DX, a, s);
     if (rc) return rc;
   }
-  return fixup(seg_ptr_src, num_nodes, partials, grad_x, d * c_in, tile_edges(lmax, gate), s);
+  return fixup(seg_ptr_src, num_nodes, partials, grad_x, d * c_in, tile_edges(lmax, gate, BWD_DX), s);
 }

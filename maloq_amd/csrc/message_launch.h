@@ -9,17 +9,21 @@ namespace msg {
 // lmax <= 4 without gate: 4 waves x 64 edges; gated or lmax > 4: 4 waves x
 // 32 edges, so a wave's accumulators and operand registers stay within the
 // 256 registers of two resident workgroups per CU.
-template <int L, bool GATE>
+template <int L, bool GATE, int MODE = FWD>
 struct Cfg {
   static constexpr int NW = 4;
-  static constexpr int RT = (L <= 4 && !GATE) ? 2 : 1;
+  // the gated input gradient has no extra accumulators (its gate rows are an
+  // extra input row type), so it keeps the 64-edge tiles
+  static constexpr int RT = (L <= 4 && (!GATE || MODE == BWD_DX)) ? 2 : 1;
 };
 
-inline int tile_edges(int lmax, int gate) { return (lmax <= 4 && !gate) ? 64 : 32; }
+inline int tile_edges(int lmax, int gate, int mode = FWD) {
+  return (lmax <= 4 && (!gate || mode == BWD_DX)) ? 64 : 32;
+}
 
 template <int L, int M, bool GATE, class TM, int MODE, int KR>
 void launch_kr(const Args& a, dim3 g, dim3 b, hipStream_t s) {
-  constexpr int NW = Cfg<L, GATE>::NW, RT = Cfg<L, GATE>::RT;
+  constexpr int NW = Cfg<L, GATE, MODE>::NW, RT = Cfg<L, GATE, MODE>::RT;
   if (MODE == BWD_DX && a.rad != nullptr)
     hipLaunchKernelGGL((gemm_kernel<L, M, GATE, NW, RT, TM, MODE, KR, MODE == BWD_DX>), g, b, 0, s, a);
   else
@@ -28,7 +32,7 @@ void launch_kr(const Args& a, dim3 g, dim3 b, hipStream_t s) {
 
 template <int L, int M, bool GATE, class TM, class TX, int MODE>
 int launch(const Args& a, hipStream_t s) {
-  constexpr int NW = Cfg<L, GATE>::NW, RT = Cfg<L, GATE>::RT;
+  constexpr int NW = Cfg<L, GATE, MODE>::NW, RT = Cfg<L, GATE, MODE>::RT;
   using P = GPlan<L, M, GATE, NW, RT>;
   // Must match the workgroup -> (tile, channel block) mapping of Gemm::run:
   // tiles in groups of 8 (one per XCD), n_cb workgroups per tile.
