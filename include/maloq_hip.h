@@ -221,9 +221,9 @@ int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const void* x, int
 /* Input and radial-scale gradients of the two-convolution block
  * (maloq_message_edgewise_fwd), from the forward's workspaces:
  *   dz2_ws [E, d', c_x]       = D_e grad_out[dst[e]]          (conv2 output gradient),
- *   dzh_ws [E, d', c_hidden]  = SO2_2^T(dz2)                  (gate output gradient),
- *   dz1_ws [E, d' + lmax, c_hidden] = GateActivation backward at gate_saved
- *                               (the forward's gate_ws): dL/dpre, then dL/dgate,
+ *   dz1_ws [E, d' + lmax, c_hidden] = GateActivation backward of SO2_2^T(dz2) at
+ *                               gate_saved (the forward's gate_ws): dL/dpre, then
+ *                               dL/dgate (formed in the transposed GEMM's epilogue),
  *   grad_rad[e] = SO2_1^T(dz1_e) (*) r_saved[e]  (r_saved: the unscaled rotated
  *                 message rows [E, d', 2 c_x]; both nullable together with rad),
  *   grad_x_src / grad_x_dst [num_nodes, d, 2 c_x] fp32: D_e^T rad[e] (*) SO2_1^T(dz1_e)
@@ -250,7 +250,7 @@ int maloq_message_edgewise_bwd_dx(int dtype, int lmax, int mmax, const float* gr
                                   const void* wpack2_t, const float* jd, float* grad_x_src,
                                   float* grad_x_dst, int64_t num_nodes, const int64_t* seg_ptr,
                                   const int64_t* seg_ptr_src, float* partials, void* dz2_ws,
-                                  void* dzh_ws, void* dz1_ws, const int32_t* edge_seg,
+                                  void* dz1_ws, const int32_t* edge_seg,
                                   float* grad_x_msg, void* stream);
 
 /* Input and radial-scale gradients of the fused block:

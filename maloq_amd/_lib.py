@@ -42,7 +42,7 @@ SIGNATURES = {
     "maloq_message_edgewise_fwd": [_i32, _i32, _i32, _p, _i32, _p, _p, _p, _i64, _p, _p, _p, _p, _i32, _p, _p,
                                    _p, _p, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p],
     "maloq_message_edgewise_bwd_dx": [_i32, _i32, _i32, _p, _i32, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p,
-                                      _i32, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p],
+                                      _i32, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p],
     "maloq_message_bwd_dx": [_i32, _i32, _i32, _i32, _p, _i32, _p, _p, _p, _i64, _p, _p, _p, _p, _p,
                              _p, _p, _i64, _i32, _p, _p, _p, _p, _p],
     "maloq_message_edge_rows": [_i64],

@@ -88,17 +88,6 @@ static int prep_dispatch(int lmax, int mmax, int dtype, int mode, const PrepArgs
   MALOQ_REQUIRE(false, "unsupported lmax %d (built: 2, 4, 6 with mmax 2)", lmax);
 }
 
-static int gate_bwd_dispatch(int lmax, int mmax, int dtype, const void* dz, const void* gsave, void* dp,
-                             int64_t E, int C, hipStream_t s) {
-  switch (lmax) {
-    case 2: return gate_bwd_l2(mmax, dtype, dz, gsave, dp, E, C, s);
-    case 4: return gate_bwd_l4(mmax, dtype, dz, gsave, dp, E, C, s);
-    case 6: return gate_bwd_l6(mmax, dtype, dz, gsave, dp, E, C, s);
-    default: break;
-  }
-  MALOQ_REQUIRE(false, "unsupported lmax %d (built: 2, 4, 6 with mmax 2)", lmax);
-}
-
 static int check_common(int dtype, int lmax, int mmax, int c_k, int c_n, int64_t E) {
   MALOQ_REQUIRE(dtype == 0 || dtype == 1, "dtype must be 0 (fp32) or 1 (bf16)");
   MALOQ_REQUIRE(lmax >= 0 && mmax >= 0 && mmax <= lmax, "bad lmax/mmax");
@@ -244,7 +233,7 @@ extern "C" int maloq_message_edgewise_bwd_dx(
     const void* rad, void* grad_rad, const void* r_saved, const void* gate_saved, const void* wpack1_t,
     int c_hidden, const void* wpack2_t, const float* jd, float* grad_x_src, float* grad_x_dst,
     int64_t num_nodes, const int64_t* seg_ptr, const int64_t* seg_ptr_src, float* partials,
-    void* dz2_ws, void* dzh_ws, void* dz1_ws, const int32_t* edge_seg, float* grad_x_msg, void* stream) {
+    void* dz2_ws, void* dz1_ws, const int32_t* edge_seg, float* grad_x_msg, void* stream) {
   MALOQ_REQUIRE(c_x > 0 && c_x % CB == 0, "node channels must be a positive multiple of %d", CB);
   const int parts = grad_x_msg ? 3 : 2;
   int rc = check_common(dtype, lmax, mmax, c_x, c_hidden, num_edges);   // conv2 transposed
@@ -259,7 +248,7 @@ extern "C" int maloq_message_edgewise_bwd_dx(
   const int kc = dtype == 1 ? BF16::KC : F32::KC;
   if (num_edges > 0) {
     MALOQ_REQUIRE(grad_out && dst && src_sorted && edge_idx && dk && gate_saved && partials && dz2_ws &&
-                  dzh_ws && dz1_ws, "null pointer");
+                  dz1_ws, "null pointer");
     MALOQ_REQUIRE(rad == nullptr || r_saved != nullptr, "the radial gradient needs the saved rows");
     MALOQ_REQUIRE(!grad_x_msg || edge_seg, "the edge message gradient needs edge_seg");
     // dL/d(conv2 output) in the edge frame: D_e grad_out[dst[e]]
@@ -268,18 +257,16 @@ extern "C" int maloq_message_edgewise_bwd_dx(
     p.dk = const_cast<float*>(dk); p.build_d = 0; p.E = num_edges; p.C = c_x;
     rc = prep_dispatch(lmax, mmax, dtype, BWD_DX, p, s);
     if (rc) return rc;
-    // conv2 transposed, rows kept in the edge frame: dL/d(gate output)
+    // conv2 transposed, rows kept in the edge frame and passed through the gate
+    // backward: dL/dpre (kept rows) and dL/dgate rows of conv1
     Args b{};
     b.a_src = dz2_ws; b.dk = dk; b.seg = dst; b.eidx = nullptr;
     b.wpack = static_cast<const char*>(wpack2_t); b.out = grad_x_src; b.part = partials;
     b.E = num_edges; b.C_k = c_x; b.C_n = c_hidden; b.n_cb = c_hidden / CB;
     b.ntiles = (num_edges + tile_edges(lmax, 0) - 1) / tile_edges(lmax, 0);
     b.frags_per_cb = frags_per_cb(lmax, mmax, 0, c_x, kc);
-    b.zout = dzh_ws;
+    b.zout = dz1_ws; b.gsave = const_cast<void*>(gate_saved);
     rc = dispatch(lmax, mmax, dtype, 0, BWD_EDGE, b, s);
-    if (rc) return rc;
-    // gate backward: dL/dpre (kept rows) and dL/dgate rows of conv1
-    rc = gate_bwd_dispatch(lmax, mmax, dtype, dzh_ws, gate_saved, dz1_ws, num_edges, c_hidden, s);
     if (rc) return rc;
     // conv1 transposed (gated input rows, radial gradient), one pass per message
     // part: the x[src] channels summed per source, the x[dst] channels per

@@ -501,6 +501,92 @@ struct Gemm {
     });
   }
 
+  // BWD_EDGE with a.gsave: the GateActivation backward (activation.py:57-77)
+  // fused into the edge-frame store.  acc holds o = dL/d(gate output) of degree
+  // lo; after the transpose through LDS a lane holds 16 channels of one edge,
+  // reads the saved pre-activations z of the same row (and the gate row) and
+  // writes to a.zout [edge id][d' + L][C_n]:
+  //   lo = 0:  dpre = o s (1 + z (1 - s)),  s = sigmoid(z);
+  //   lo >= 1: t = tanh(z_gate); dpre_q = o_q t;  dgate = (1 - t^2) sum_q o_q z_q.
+  template <int lo>
+  static __device__ __forceinline__ void store_gate_bwd(const f32x16 (&acc)[P::MSLOT], const Smem& s,
+                                                        const Args& a, int cb, float* tb, int lane) {
+    constexpr int DG = P::DP + L;
+    const int co = lane & 31, h = lane >> 5;
+    static_for<RT>([&](auto RTI) {
+      constexpr int rt = decltype(RTI)::value;
+      constexpr int sb = P::tab.base[lo] + rt * P::ntype(lo);
+      const int ei = s.eid[rt * 32 + co];
+      const int64_t base = static_cast<int64_t>(ei >= 0 ? ei : 0) * DG * a.C_n + cb * CB + 16 * h;
+      typename TM::raw* g = reinterpret_cast<typename TM::raw*>(a.zout) + base;
+      const typename TM::raw* zs = reinterpret_cast<const typename TM::raw*>(a.gsave) + base;
+      float tg[16], dg[16];
+      if constexpr (lo > 0) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          tg[k] = 0.f;
+          dg[k] = 0.f;
+        }
+        if (ei >= 0) {
+          float t8[8];
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            load_vec<TM, 8>(zs + static_cast<int64_t>(P::DP + lo - 1) * a.C_n + 8 * half, t8);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) tg[8 * half + k] = tanhf(t8[k]);
+          }
+        }
+      }
+      static_for<P::ntype(lo)>([&](auto TI) {
+        constexpr int t = decltype(TI)::value;
+        constexpr int row = P::mrow(t, lo);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) tb[tsw(8 * (i >> 2) + 4 * h + (i & 3), co)] = acc[sb + t][i];
+        wave_sync();
+        if (ei >= 0) {
+          float v[16];
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const float4 t4 = *reinterpret_cast<const float4*>(tb + tsw(co, 16 * h + 4 * g4));
+            v[4 * g4] = t4.x; v[4 * g4 + 1] = t4.y; v[4 * g4 + 2] = t4.z; v[4 * g4 + 3] = t4.w;
+          }
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            float z8[8], w8[8];
+            load_vec<TM, 8>(zs + static_cast<int64_t>(row) * a.C_n + 8 * half, z8);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+              const float o = v[8 * half + k], z = z8[k];
+              if constexpr (lo == 0) {
+                const float sg = 1.0f / (1.0f + expf(-z));
+                w8[k] = o * (sg * (1.0f + z * (1.0f - sg)));
+              } else {
+                dg[8 * half + k] = fmaf(o, z, dg[8 * half + k]);
+                w8[k] = o * tg[8 * half + k];
+              }
+            }
+            store_vec<TM, 8>(g + static_cast<int64_t>(row) * a.C_n + 8 * half, w8);
+          }
+        }
+        wave_sync();
+      });
+      if constexpr (lo > 0) {
+        if (ei >= 0) {
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            float w8[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+              const float tv = tg[8 * half + k];
+              w8[k] = dg[8 * half + k] * (1.0f - tv * tv);
+            }
+            store_vec<TM, 8>(g + static_cast<int64_t>(P::DP + lo - 1) * a.C_n + 8 * half, w8);
+          }
+        }
+      }
+    });
+  }
+
   template <int lo>
   static __device__ __forceinline__ void gate_act(f32x16 (&acc)[P::MSLOT]) {
     static_for<RT>([&](auto RTI) {
@@ -750,7 +836,10 @@ struct Gemm {
         } else if constexpr (RAD)
           radial<lo>(acc, s, a, cb,
                      reinterpret_cast<float*>((wave < 2 ? st0 : st1) + (wave & 1) * PW), lane);
-        if constexpr (MODE == FWD_EDGE || MODE == BWD_EDGE)
+        if constexpr (MODE == BWD_EDGE)
+          store_gate_bwd<lo>(acc, s, a, cb,
+                             reinterpret_cast<float*>((wave < 2 ? st0 : st1) + (wave & 1) * PW), lane);
+        else if constexpr (MODE == FWD_EDGE)
           save_pre<lo, true>(acc, s, a, cb,
                              reinterpret_cast<float*>((wave < 2 ? st0 : st1) + (wave & 1) * PW), lane);
         else

@@ -156,9 +156,9 @@ struct PairLayout {
 
 // FWD_EDGE: the forward GEMM whose gated output rows stay in the edge frame
 // (Args::zout) for a second SO(2) convolution, instead of being rotated back
-// and summed per node.  BWD_EDGE: the transposed GEMM with its output rows
-// kept in the edge frame the same way (the input gradient of that second
-// convolution).
+// and summed per node.  BWD_EDGE: the transposed GEMM of that second
+// convolution with its output rows kept in the edge frame and passed through
+// the gate backward (the gradient at the first convolution's output).
 enum Mode { FWD = 0, BWD_DX = 1, FWD_EDGE = 2, BWD_EDGE = 3 };
 
 struct Args {
@@ -182,8 +182,10 @@ struct Args {
   int64_t frags_per_cb;   // packed fragments per output-channel block
   void* gsave;            // FWD gated: [E_all, d' + L, C_n] (TM raw) pre-activation rows and
                           // gate rows, nullable; BWD_DX gated: a_src has d' + L rows
-  void* zout;             // FWD_EDGE / BWD_EDGE: [E_all, d', C_n] (TM raw) output rows
-                          // (m-major), written in place of the inverse rotation and segment sum
+  void* zout;             // FWD_EDGE: [E_all, d', C_n] (TM raw) output rows (m-major), written
+                          // in place of the inverse rotation and segment sum; BWD_EDGE:
+                          // [E_all, d' + L, C_n], the gate backward of those rows at the
+                          // pre-activations in gsave ([E_all, d' + L, C_n])
   int cb0;                // first output channel block (the grid covers n_cb blocks from it)
 };
 
@@ -560,66 +562,6 @@ struct Prep {
 template <int L, int M, class TM, class TX, bool GATED = false>
 __global__ __launch_bounds__(PREP_NT) void prep_kernel(PrepArgs a) {
   Prep<L, M, TM, TX, GATED>::run(a);
-}
-
-// GateActivation backward (activation.py:57-77) on edge-frame rows: o = dz
-// [E, d', C] (the output gradient of the gate), z = the saved pre-activations
-// [E, d' + L, C]; writes dp [E, d' + L, C]:
-//   l = 0:  dpre = o s (1 + z (1 - s)),  s = sigmoid(z);
-//   l >= 1: t = tanh(z_gate[l]); dpre_q = o_q t;  dgate[l] = (1 - t^2) sum_q o_q z_q.
-// A thread per (edge, 16-byte channel chunk).
-template <int L, int M, class TM>
-__global__ __launch_bounds__(256) void gate_bwd_rows_kernel(const void* dz, const void* gsave, void* dp,
-                                                            int64_t E, int C) {
-  using P = Plan<L, M, false, 4, 1>;
-  constexpr int V = TM::VEC;
-  constexpr int DG = P::DP + L;
-  using raw = typename TM::raw;
-  const int nch = C / V;
-  const int64_t u = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (u >= E * nch) return;
-  const int64_t e = u / nch;
-  const int c0 = static_cast<int>(u - e * nch) * V;
-  const raw* os = reinterpret_cast<const raw*>(dz) + e * P::DP * C + c0;
-  const raw* zs = reinterpret_cast<const raw*>(gsave) + e * DG * C + c0;
-  raw* yo = reinterpret_cast<raw*>(dp) + e * DG * C + c0;
-  static_for<L + 1>([&](auto LI) {
-    constexpr int l = decltype(LI)::value;
-    if constexpr (l == 0) {
-      float o[V], z[V];
-      load_vec<TM, V>(os + static_cast<int64_t>(P::mrow(0, 0)) * C, o);
-      load_vec<TM, V>(zs + static_cast<int64_t>(P::mrow(0, 0)) * C, z);
-#pragma unroll
-      for (int c = 0; c < V; ++c) {
-        const float sg = 1.0f / (1.0f + expf(-z[c]));
-        o[c] *= sg * (1.0f + z[c] * (1.0f - sg));
-      }
-      store_vec<TM, V>(yo + static_cast<int64_t>(P::mrow(0, 0)) * C, o);
-    } else {
-      float t[V], dg[V];
-      load_vec<TM, V>(zs + static_cast<int64_t>(P::DP + l - 1) * C, t);
-#pragma unroll
-      for (int c = 0; c < V; ++c) {
-        t[c] = tanhf(t[c]);
-        dg[c] = 0.f;
-      }
-#pragma unroll
-      for (int q = 0; q < P::nq(l); ++q) {
-        float o[V], z[V];
-        load_vec<TM, V>(os + static_cast<int64_t>(P::mrow(q, l)) * C, o);
-        load_vec<TM, V>(zs + static_cast<int64_t>(P::mrow(q, l)) * C, z);
-#pragma unroll
-        for (int c = 0; c < V; ++c) {
-          dg[c] = fmaf(o[c], z[c], dg[c]);
-          o[c] *= t[c];
-        }
-        store_vec<TM, V>(yo + static_cast<int64_t>(P::mrow(q, l)) * C, o);
-      }
-#pragma unroll
-      for (int c = 0; c < V; ++c) dg[c] *= (1.0f - t[c] * t[c]);
-      store_vec<TM, V>(yo + static_cast<int64_t>(P::DP + l - 1) * C, dg);
-    }
-  });
 }
 
 }  // namespace msg

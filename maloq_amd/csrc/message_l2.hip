@@ -24,10 +24,5 @@ int prep_l2(int mmax, int dtype, int mode, const PrepArgs& a, hipStream_t s) {
   return prep_lm<2, 2>(dtype, mode, a, s);
 }
 
-int gate_bwd_l2(int mmax, int dtype, const void* dz, const void* gsave, void* dp, int64_t E, int C, hipStream_t s) {
-  MALOQ_REQUIRE(mmax == 2, "lmax=2: built for mmax = 2 only, got %d", mmax);
-  return gate_bwd_lm<2, 2>(dtype, dz, gsave, dp, E, C, s);
-}
-
 }  // namespace msg
 }  // namespace maloq

@@ -24,10 +24,5 @@ int prep_l4(int mmax, int dtype, int mode, const PrepArgs& a, hipStream_t s) {
   return prep_lm<4, 2>(dtype, mode, a, s);
 }
 
-int gate_bwd_l4(int mmax, int dtype, const void* dz, const void* gsave, void* dp, int64_t E, int C, hipStream_t s) {
-  MALOQ_REQUIRE(mmax == 2, "lmax=4: built for mmax = 2 only, got %d", mmax);
-  return gate_bwd_lm<4, 2>(dtype, dz, gsave, dp, E, C, s);
-}
-
 }  // namespace msg
 }  // namespace maloq

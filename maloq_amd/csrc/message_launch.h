@@ -72,7 +72,8 @@ int launch_lm(int dtype, int gate, int mode, const Args& a, hipStream_t s) {
     return dtype == 1 ? launch<L, M, true, BF16, BF16, FWD_EDGE>(a, s) : launch<L, M, true, F32, F32, FWD_EDGE>(a, s);
   }
   if (mode == BWD_EDGE) {
-    MALOQ_REQUIRE(!gate && a.rad == nullptr, "the edge-frame input gradient is built ungated, without radial");
+    MALOQ_REQUIRE(!gate && a.rad == nullptr && a.gsave != nullptr,
+                  "the edge-frame input gradient is built ungated, without radial, with the gate backward");
     return dtype == 1 ? launch<L, M, false, BF16, BF16, BWD_EDGE>(a, s)
                       : launch<L, M, false, F32, F32, BWD_EDGE>(a, s);
   }
@@ -84,23 +85,6 @@ int launch_lm(int dtype, int gate, int mode, const Args& a, hipStream_t s) {
   if (dtype == 1)
     return gate ? launch<L, M, true, BF16, BF16, BWD_DX>(a, s) : launch<L, M, false, BF16, BF16, BWD_DX>(a, s);
   return gate ? launch<L, M, true, F32, F32, BWD_DX>(a, s) : launch<L, M, false, F32, F32, BWD_DX>(a, s);
-}
-
-// Gate backward on edge-frame rows (gate_bwd_rows_kernel).
-template <int L, int M>
-int gate_bwd_lm(int dtype, const void* dz, const void* gsave, void* dp, int64_t E, int C, hipStream_t s) {
-  const int v = dtype == 1 ? BF16::VEC : F32::VEC;
-  MALOQ_REQUIRE(C % v == 0, "channels must be a multiple of %d", v);
-  const int64_t grid = (E * (C / v) + 255) / 256;
-  if (grid == 0) return MALOQ_OK;
-  MALOQ_REQUIRE(grid < (int64_t(1) << 31), "grid too large");
-  if (dtype == 1)
-    hipLaunchKernelGGL((gate_bwd_rows_kernel<L, M, BF16>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, dz,
-                       gsave, dp, E, C);
-  else
-    hipLaunchKernelGGL((gate_bwd_rows_kernel<L, M, F32>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, dz,
-                       gsave, dp, E, C);
-  return check_launch("gate_bwd_rows_kernel");
 }
 
 // Edge prep: mode FWD gathers x (dtype) and applies rad; mode BWD_DX gathers
@@ -133,9 +117,6 @@ int launch_l6(int mmax, int dtype, int gate, int mode, const Args& a, hipStream_
 int prep_l2(int mmax, int dtype, int mode, const PrepArgs& a, hipStream_t s);
 int prep_l4(int mmax, int dtype, int mode, const PrepArgs& a, hipStream_t s);
 int prep_l6(int mmax, int dtype, int mode, const PrepArgs& a, hipStream_t s);
-int gate_bwd_l2(int mmax, int dtype, const void* dz, const void* gsave, void* dp, int64_t E, int C, hipStream_t s);
-int gate_bwd_l4(int mmax, int dtype, const void* dz, const void* gsave, void* dp, int64_t E, int C, hipStream_t s);
-int gate_bwd_l6(int mmax, int dtype, const void* dz, const void* gsave, void* dp, int64_t E, int C, hipStream_t s);
 
 }  // namespace msg
 }  // namespace maloq

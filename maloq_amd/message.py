@@ -371,13 +371,12 @@ def edgewise_backward_dx(grad_out, x_shape, dt, plan, saved, rad, conv1, conv2, 
         if need_rad_grad:
             grad_rad = torch.empty_like(rad)
     dz2 = _edge_rows(E, kr, c_x, dev, dt)
-    dzh = torch.empty(max(E, 1), kr, c_hidden, device=dev, dtype=dt)
     dz1 = _edge_rows(E, kr + lmax, c_hidden, dev, dt)
     _lib.call("maloq_message_edgewise_bwd_dx", DTYPE_CODE[dt], lmax, mmax, _lib.ptr(g), c_x, _lib.ptr(plan.dst),
               _lib.ptr(grad_row), _lib.ptr(plan.bwd_src), _lib.ptr(plan.bwd_eidx), E, _lib.ptr(saved["dk"]),
               _lib.ptr(rad), _lib.ptr(grad_rad), _lib.ptr(saved.get("r")), _lib.ptr(saved["g"]), _lib.ptr(wp1t),
               c_hidden, _lib.ptr(wp2t), _lib.ptr(_jd_dev(lmax, dev)), _lib.ptr(gxs), _lib.ptr(gxd), N,
-              _lib.ptr(plan.seg_ptr), _lib.ptr(plan.seg_ptr_src), _lib.ptr(pbuf), _lib.ptr(dz2), _lib.ptr(dzh),
+              _lib.ptr(plan.seg_ptr), _lib.ptr(plan.seg_ptr_src), _lib.ptr(pbuf), _lib.ptr(dz2),
               _lib.ptr(dz1), _lib.ptr(edge_seg), _lib.ptr(gxm), _lib.stream_of(dev))
     gx = gxs[:, :, :c_x] + gxd[:, :, c_x:2 * c_x]
     if parts == 2:
