@@ -147,26 +147,41 @@ _PACK_DEV: dict = {}
 
 
 def pack_weights(w0, wm, lmax, mmax, gate, c_in, c_out, dtype, mode=0):
-    """Packed B fragments (raw bytes on the weights' device) for the kernels."""
+    """Packed B fragments (raw bytes on the weights' device) for the kernels.
+    ``mode="both"``: the forward (0) and transposed (1) packings from one
+    launch, returned as the pair (wpack, wpack_t)."""
     code = DTYPE_CODE[dtype]
-    key = (code, lmax, mmax, bool(gate), c_in, c_out, mode, str(w0.device))
-    hit = _PACK_DEV.get(key)
-    if hit is None:
-        idx, total = _pack_index(code, lmax, mmax, bool(gate), c_in, c_out, mode)
-        hit = (torch.from_numpy(idx).to(w0.device), total)
-        _PACK_DEV[key] = hit
-    idx, total = hit
+    if mode == "both":
+        key = (code, lmax, mmax, bool(gate), c_in, c_out, "both", str(w0.device))
+        hit = _PACK_DEV.get(key)
+        if hit is None:
+            i0, total = _pack_index(code, lmax, mmax, bool(gate), c_in, c_out, 0)
+            i1, _ = _pack_index(code, lmax, mmax, bool(gate), c_in, c_out, 1)
+            hit = (torch.from_numpy(np.concatenate([i0, i1])).to(w0.device), total, i0.size)
+            _PACK_DEV[key] = hit
+        idx, total, n0 = hit
+    else:
+        key = (code, lmax, mmax, bool(gate), c_in, c_out, mode, str(w0.device))
+        hit = _PACK_DEV.get(key)
+        if hit is None:
+            idx, total = _pack_index(code, lmax, mmax, bool(gate), c_in, c_out, mode)
+            hit = (torch.from_numpy(idx).to(w0.device), total)
+            _PACK_DEV[key] = hit
+        idx, total = hit
     srcs = [w.detach().float().contiguous() for w in [w0] + list(wm[:mmax])]
     assert sum(t.numel() for t in srcs) == total, "weight shapes do not match (lmax, mmax, channels)"
     lib = _lib.load()
     want = lib.maloq_message_wpack_bytes(code, lmax, mmax, int(bool(gate)),
-                                         c_in if mode == 0 else c_out,
-                                         c_out if mode == 0 else c_in)
+                                         c_in if mode != 1 else c_out,
+                                         c_out if mode != 1 else c_in)
+    want_t = lib.maloq_message_wpack_bytes(code, lmax, mmax, int(bool(gate)), c_out, c_in) if mode == "both" else 0
     packed = torch.empty(idx.numel(), dtype=dtype, device=w0.device)
-    assert packed.numel() * packed.element_size() == want, (packed.numel(), want)
+    assert packed.numel() * packed.element_size() == want + want_t, (packed.numel(), want, want_t)
     _lib.call("maloq_message_pack", code, len(srcs), (ctypes.c_void_p * len(srcs))(*[t.data_ptr() for t in srcs]),
               (ctypes.c_int64 * len(srcs))(*[t.numel() for t in srcs]), _lib.ptr(idx), idx.numel(),
               _lib.ptr(packed), _lib.stream_of(w0.device))
+    if mode == "both":
+        return packed[:n0], packed[n0:]
     return packed
 
 
@@ -338,7 +353,7 @@ def edgewise_forward(x, plan, eulers, rad, conv1, conv2, lmax, mmax, wpack1=None
 
 
 def edgewise_backward_dx(grad_out, x_shape, dt, plan, saved, rad, conv1, conv2, lmax, mmax,
-                         need_rad_grad=True, node_or_edge="node", parts=2):
+                         need_rad_grad=True, node_or_edge="node", parts=2, wpack1_t=None, wpack2_t=None):
     """Input and radial gradients of :func:`edgewise_forward` from its saved
     workspaces (maloq_message_edgewise_bwd_dx): (grad_x fp32 [N, d, C],
     grad_rad or None, dz2 [E, d', C] the second convolution's output gradient,
@@ -351,8 +366,9 @@ def edgewise_backward_dx(grad_out, x_shape, dt, plan, saved, rad, conv1, conv2, 
     dev = grad_out.device
     E = plan.num_edges
     kr = kept_rows(lmax, mmax)
-    wp1t = pack_weights(conv1[0], conv1[2], lmax, mmax, True, parts * c_x, c_hidden, dt, 1)
-    wp2t = pack_weights(conv2[0], conv2[2], lmax, mmax, False, c_hidden, c_x, dt, 1)
+    wp1t = wpack1_t if wpack1_t is not None else \
+        pack_weights(conv1[0], conv1[2], lmax, mmax, True, parts * c_x, c_hidden, dt, 1)
+    wp2t = wpack2_t if wpack2_t is not None else pack_weights(conv2[0], conv2[2], lmax, mmax, False, c_hidden, c_x, dt, 1)
     g = grad_out.float().contiguous()
     grad_row = None
     if node_or_edge == "edge":
@@ -394,8 +410,17 @@ class _EdgewiseFn(torch.autograd.Function):
     def forward(ctx, x, rad, w01, b01, w02, b02, xm, plan, eulers, lmax, mmax, node_or_edge, *wm):
         saved = {}
         wm1, wm2 = list(wm[:mmax]), list(wm[mmax:])
-        out = edgewise_forward(x, plan, eulers, rad, (w01, b01, wm1), (w02, b02, wm2), lmax, mmax, save=saved,
-                               node_or_edge=node_or_edge, x_message_edge=xm)
+        npart = 2 if xm is None else 3
+        c_x, c_hidden = x.shape[2], w01.shape[0] // (2 * lmax + 1)
+        # both packings of each convolution from one launch when a backward will
+        # run; the transposed ones wait for it
+        mode = "both" if any(ctx.needs_input_grad) else 0
+        p1 = pack_weights(w01, wm1, lmax, mmax, True, npart * c_x, c_hidden, x.dtype, mode)
+        p2 = pack_weights(w02, wm2, lmax, mmax, False, c_hidden, c_x, x.dtype, mode)
+        (wp1, wp1t), (wp2, wp2t) = (p1, p2) if mode == "both" else ((p1, None), (p2, None))
+        ctx.wpack_t = (wp1t, wp2t)
+        out = edgewise_forward(x, plan, eulers, rad, (w01, b01, wm1), (w02, b02, wm2), lmax, mmax, wpack1=wp1,
+                               wpack2=wp2, save=saved, node_or_edge=node_or_edge, x_message_edge=xm)
         ctx.plan, ctx.lmax, ctx.mmax, ctx.mode = plan, lmax, mmax, node_or_edge
         ctx.parts, ctx.xm_dtype = (2, None) if xm is None else (3, xm.dtype)
         ctx.x_shape, ctx.dt = tuple(x.shape), x.dtype
@@ -410,7 +435,9 @@ class _EdgewiseFn(torch.autograd.Function):
         wm1, wm2 = list(wm[:mmax]), list(wm[mmax:])
         res = edgewise_backward_dx(g, ctx.x_shape, ctx.dt, plan, {"dk": dk, "r": r, "g": gs}, rad,
                                    (w01, None, wm1), (w02, None, wm2), lmax, mmax,
-                                   need_rad_grad=ctx.needs_input_grad[1], node_or_edge=ctx.mode, parts=ctx.parts)
+                                   need_rad_grad=ctx.needs_input_grad[1], node_or_edge=ctx.mode, parts=ctx.parts,
+                                   wpack1_t=ctx.wpack_t[0], wpack2_t=ctx.wpack_t[1])
+        ctx.wpack_t = None
         gx, grad_rad, dz2, dz1 = res[:4]
         gxm = res[4].to(ctx.xm_dtype) if (ctx.parts == 3 and ctx.needs_input_grad[6]) else None
         c_x = ctx.x_shape[2]
@@ -515,7 +542,14 @@ class _MessageBlockFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, rad, w0, b0, plan, eulers, lmax, mmax, gate, *wm):
         saved = {}
-        out = message_forward(x, plan, eulers, rad, w0, b0, list(wm), lmax, mmax, gate=gate, save=saved)
+        # both packings from one launch when a backward will run: the transposed
+        # one is kept for it
+        c_out = w0.shape[0] // (lmax + 1 + (lmax if gate else 0))
+        if any(ctx.needs_input_grad):
+            wp, ctx.wpack_t = pack_weights(w0, wm, lmax, mmax, gate, x.shape[2], c_out, x.dtype, "both")
+        else:
+            wp, ctx.wpack_t = pack_weights(w0, wm, lmax, mmax, gate, x.shape[2], c_out, x.dtype, 0), None
+        out = message_forward(x, plan, eulers, rad, w0, b0, list(wm), lmax, mmax, gate=gate, wpack=wp, save=saved)
         ctx.plan, ctx.lmax, ctx.mmax, ctx.gate, ctx.has_b0 = plan, lmax, mmax, gate, b0 is not None
         ctx.x_shape, ctx.dt = tuple(x.shape), x.dtype
         ctx.has_r = saved["r"] is not None
@@ -528,8 +562,9 @@ class _MessageBlockFn(torch.autograd.Function):
         rad, w0, y, dk, r, gs, *wm = ctx.saved_tensors
         plan, lmax, mmax, gate = ctx.plan, ctx.lmax, ctx.mmax, ctx.gate
         gx, grad_rad, dz = message_backward_dx(g, ctx.x_shape, ctx.dt, plan, {"dk": dk, "r": r, "g": gs}, rad,
-                                               w0, wm, lmax, mmax, need_rad_grad=ctx.needs_input_grad[1],
-                                               gate=gate)
+                                               w0, wm, lmax, mmax, wpack_t=ctx.wpack_t,
+                                               need_rad_grad=ctx.needs_input_grad[1], gate=gate)
+        ctx.wpack_t = None
         need_w = ctx.needs_input_grad[2] or ctx.needs_input_grad[3] or any(ctx.needs_input_grad[9:])
         dw0 = db0 = None
         dwm = [None] * len(wm)
