@@ -54,6 +54,23 @@ def _colsum(rows, row0, nrows, E):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("gate", [False, True])
+def test_pack_both_equals_the_two_packings(gate, dtype, device):
+    """mode "both" (one launch) gives bit-for-bit the forward and transposed
+    packings of two separate launches, each slice 16-byte aligned."""
+    lmax, mmax, c_in, c_out = 4, 2, 64, 32
+    gen = torch.Generator().manual_seed(5 + int(gate))
+    extra = lmax * c_out if gate else 0
+    w0 = torch.randn((lmax + 1) * c_out + extra, (lmax + 1) * c_in, generator=gen).to(device)
+    wm = [torch.randn(2 * (lmax - m + 1) * c_out, (lmax - m + 1) * c_in, generator=gen).to(device)
+          for m in range(1, mmax + 1)]
+    a, b = M.pack_weights(w0, wm, lmax, mmax, gate, c_in, c_out, dtype, "both")
+    assert torch.equal(a, M.pack_weights(w0, wm, lmax, mmax, gate, c_in, c_out, dtype, 0))
+    assert torch.equal(b, M.pack_weights(w0, wm, lmax, mmax, gate, c_in, c_out, dtype, 1))
+    assert a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("E", [0, 1, 63, 64, 65, 1000, 4097, 300001])
 def test_colsum_matches_fp64(E, dtype, device):
     print(f"colsum case E={E} dtype={dtype}", flush=True)
