@@ -443,9 +443,26 @@ class _EdgewiseFn(torch.autograd.Function):
         c_x = ctx.x_shape[2]
         c_hidden = w01.shape[0] // (2 * lmax + 1)
         E = plan.num_edges
-        dw01, dwm1, db01 = message_weight_grad(dz1, y, lmax, mmax, c_hidden, ctx.parts * c_x, num_edges=E,
-                                               gate=True)
-        dw02, dwm2, db02 = message_weight_grad(dz2, z, lmax, mmax, c_x, c_hidden, num_edges=E)
+        nig = ctx.needs_input_grad
+        dw01 = db01 = dw02 = db02 = None
+        dwm1, dwm2 = [None] * mmax, [None] * mmax
+        if nig[2] or nig[3] or any(nig[12:12 + mmax]):
+            if E > 0:
+                dw01, dwm1, db01 = message_weight_grad(dz1, y, lmax, mmax, c_hidden, ctx.parts * c_x, num_edges=E,
+                                                       gate=True)
+            else:
+                dw01, dwm1 = torch.zeros_like(w01, dtype=torch.float32), [torch.zeros_like(w, dtype=torch.float32)
+                                                                          for w in wm1]
+                db01 = torch.zeros(w01.shape[0], device=w01.device)
+            dw01, dwm1 = dw01.to(w01.dtype), [d.to(w.dtype) for d, w in zip(dwm1, wm1)]
+        if nig[4] or nig[5] or any(nig[12 + mmax:]):
+            if E > 0:
+                dw02, dwm2, db02 = message_weight_grad(dz2, z, lmax, mmax, c_x, c_hidden, num_edges=E)
+            else:
+                dw02, dwm2 = torch.zeros_like(w02, dtype=torch.float32), [torch.zeros_like(w, dtype=torch.float32)
+                                                                          for w in wm2]
+                db02 = torch.zeros(w02.shape[0], device=w02.device)
+            dw02, dwm2 = dw02.to(w02.dtype), [d.to(w.dtype) for d, w in zip(dwm2, wm2)]
         gxo = gx.to(ctx.dt) if ctx.needs_input_grad[0] else None
         grad_rad = grad_rad if ctx.needs_input_grad[1] else None
         return (gxo, grad_rad, dw01, db01 if ctx.has_b[0] else None, dw02, db02 if ctx.has_b[1] else None,

@@ -241,6 +241,27 @@ def test_edgewise_source_target_message(dtype, mode, device):
         assert err < tol, (n, err)
 
 
+def test_edgewise_empty_graph(device):
+    """No edges: node sums are zero, gradients of x and of every weight are zero."""
+    from maloq_amd import message as M
+    lmax, mmax, N, C, H = 2, 2, 4, 32, 64
+    gen = torch.Generator().manual_seed(1)
+    plan = M.MessagePlan(torch.zeros(2, 0, dtype=torch.long, device=device), N)
+    c1 = _conv(lmax, mmax, 2 * C, H, gen, True)
+    c2 = _conv(lmax, mmax, H, C, gen, False)
+    dv = lambda c: (c["w0"].float().to(device).requires_grad_(), c["b0"].float().to(device).requires_grad_(),
+                    [w.float().to(device).requires_grad_() for w in c["wm"]])
+    conv1, conv2 = dv(c1), dv(c2)
+    x = torch.randn(N, 9, C, device=device, requires_grad=True)
+    rad = torch.zeros(0, M.rad_width(lmax, mmax, 2 * C), device=device, requires_grad=True)
+    out = M.edgewise_block(x, plan, torch.zeros(0, 3, device=device), rad, conv1, conv2, lmax, mmax)
+    assert out.shape == (N, 9, C) and torch.all(out == 0)
+    out.backward(torch.ones_like(out))
+    assert torch.all(x.grad == 0)
+    for t in [conv1[0], conv1[1], *conv1[2], conv2[0], conv2[1], *conv2[2]]:
+        assert t.grad is not None and torch.all(t.grad == 0)
+
+
 def test_forward_empty_graph(device):
     from maloq_amd import message as M
     plan = M.MessagePlan(torch.zeros(2, 0, dtype=torch.long, device=device), 5)
