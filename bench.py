@@ -644,7 +644,7 @@ def main(argv=None):
         tg = kernel_time_events(lambda: edgewise_call(gw), 20)
         fl = edgewise_flops_per_edge(gw["L"], gw["M"], gw["C"], gw["H"]) * gw["E"]
         ts = time_steps(lambda: edgewise_step(gw), 10, 3)
-        result["edgewise_two_conv_fwd"] = {
+        result["edgewise_two_conv"] = {
             "metric": "edges/s", "value": gw["E"] / tg, "us_per_call": tg * 1e6,
             "fwd_bwd_edges_per_s": gw["E"] / ts, "fwd_bwd_ms": ts * 1e3,
             "config": "config 2 graph, cat(x[src], x[dst]) 256 -> gated 128 -> 128 channels, bf16; value: forward, "
