@@ -238,7 +238,8 @@ int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const void* x, int
  * Edges in the forward's dst-sorted order (dst, seg_ptr); src_sorted / edge_idx /
  * seg_ptr_src: the same edges sorted by source, edge_idx the dst-sorted position
  * of each.  wpack1_t / wpack2_t: the two convolutions packed for the transposed
- * GEMM (conv1 gated).  c_x a multiple of 32.  dz2_ws and dz1_ws feed
+ * GEMM (conv1 gated).  c_x a multiple of 32.  partials: maloq_message_partials_floats(lmax,
+ * 1, E, 2 c_x) floats (3 c_x with grad_x_msg).  dz2_ws and dz1_ws feed
  * maloq_message_dw (conv2: dz2 with the forward's z_ws; conv1: dz1 with y_ws).
  * Replaces the autograd backward of Edgewise.forward_node (esen_block.py:146-208). */
 int maloq_message_edgewise_bwd_dx(int dtype, int lmax, int mmax, const float* grad_out, int c_x,
