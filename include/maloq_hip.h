@@ -17,7 +17,7 @@
 
 #include <stdint.h>
 
-#define MALOQ_ABI_VERSION 1
+#define MALOQ_ABI_VERSION 2
 
 #ifdef __cplusplus
 extern "C" {
@@ -52,6 +52,20 @@ int maloq_edge_vec_to_wigner(const float* edge_vec, int64_t num_edges, uint64_t 
 int maloq_wigner_from_euler(const float* eulers, int64_t num_edges, int lmax,
                             const float* jd_packed, float* wigner, float* wigner_inv,
                             int write_zeros, void* stream);
+
+/* Rotation of irreps rows into or out of the edge frame, per edge:
+ *   out[e] = D_e x[g(e)]    (inverse == 0),   out[e] = D_e^T x[g(e)]   (inverse != 0),
+ * g(e) = gather[e] (nullable: e), x [*, d, c], out [E, d, c], d = (lmax+1)^2,
+ * 0 <= lmax <= 8, c a multiple of 4; x_dtype / out_dtype 0 fp32, 1 bf16 (fp32
+ * arithmetic).  D_e from exactly one of eulers [E, 3] (the (alpha, beta, gamma)
+ * triple of maloq_edge_euler, with jd_packed; bit-identical blocks to
+ * maloq_wigner_from_euler) or wigner [E, d, d] fp32 (its diagonal blocks; the
+ * reference's Wigner matrices are zero elsewhere).
+ * Replaces torch.bmm(wigner, x_message) / torch.bmm(wigner_inv, x_message),
+ * helm/esen_block.py:181,191 and helm/esen_osh.py:1218,1228,1318,1328. */
+int maloq_rotate(int x_dtype, int out_dtype, int lmax, const void* x, int c, const int32_t* gather,
+                 int64_t num_edges, const float* eulers, const float* wigner, const float* jd_packed,
+                 int inverse, void* out, void* stream);
 
 /* ------------------------------------------------------ basis transform -- */
 
@@ -149,7 +163,7 @@ int64_t maloq_message_wpack_bytes(int dtype, int lmax, int mmax, int gate, int c
  * so2_m_conv[m-1].fc.weight for m = 1..mmax, in the reference's layout).  idx
  * [n] int64 device array: the fragment order of the kernels, built once per
  * shape by the host packer (maloq_amd.message._pack_index); n elements make
- * maloq_message_wpack_bytes(...) bytes.  nsrc <= 4.  Stands in for reading
+ * maloq_message_wpack_bytes(...) bytes.  nsrc <= 8.  Stands in for reading
  * fc_m0 / so2_m_conv weights at helm/nn/so2_layers.py:161-203 (the kernels
  * take the weights in fragment order). */
 int maloq_message_pack(int dtype, int nsrc, const float* const* srcs, const int64_t* src_sizes,
@@ -162,9 +176,28 @@ int maloq_message_pack(int dtype, int nsrc, const float* const* srcs, const int6
 int maloq_message_kept_rows(int lmax, int mmax);
 int maloq_message_wigner_floats(int lmax, int mmax);
 
+/* 1 if the message-block kernels are built for (lmax, mmax), else 0: (2, 2),
+ * (4, 2), (4, 4), (6, 2), (6, 6).  The reference builds its models with
+ * mmax = lmax (train_utils/training_workflow.py:510-511); mmax = 2 is the
+ * benchmark's truncation.  Lets a host layer reject a shape at construction
+ * (as SO2_Convolution would build it, helm/nn/so2_layers.py:71-130). */
+int maloq_message_supported(int lmax, int mmax);
+
+/* Kept Wigner rows (|m| <= mmax) of a caller's dense wigner [E, d, d] fp32 (the
+ * reference's argument, esen_block.py:118-121) in the kernels' pair-major
+ * layout: dk [E, maloq_message_wigner_floats(lmax, mmax)], dk[p] from
+ * wigner[perm[p]] (perm nullable: p).  With eulers == NULL the message
+ * forwards below read their dk_ws as so filled instead of building the rows
+ * from Euler angles.  Replaces the row selection of bmm(wigner, x_message) +
+ * einsum(to_m), helm/esen_block.py:181-184. */
+int maloq_message_wigner_rows(int lmax, int mmax, const float* wigner, const int64_t* perm,
+                              int64_t num_edges, float* dk, void* stream);
+
 /* Fused message block, forward:
  *   out[n] = sum_{e: dst[e]=n} D_e^T SO2(D_e x[src[e]] (*) rad[e]) [gate],
- * with D_e the kept rows |m| <= mmax of the Wigner-D of eulers[e].
+ * with D_e the kept rows |m| <= mmax of the Wigner-D of eulers[e] (eulers NULL: of the
+ * rows dk_ws already holds, see maloq_message_wigner_rows; likewise for
+ * maloq_message_edgewise_fwd).
  * Edges must be sorted by dst (non-decreasing); per-edge arrays (eulers, rad)
  * follow that order.  x [N_src, d, c_in] (fp32 or bf16 per dtype), rad
  * [E, sum_m (lmax-m+1) c_in] (nullable), wpack from the host packer, bias
@@ -226,20 +259,19 @@ int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const void* x, int
  *                               dL/dgate (formed in the transposed GEMM's epilogue),
  *   grad_rad[e] = SO2_1^T(dz1_e) (*) r_saved[e]  (r_saved: the unscaled rotated
  *                 message rows [E, d', 2 c_x]; both nullable together with rad),
- *   grad_x_src / grad_x_dst [num_nodes, d, 2 c_x] fp32: D_e^T rad[e] (*) SO2_1^T(dz1_e)
- *                 summed per source (channels [0, c_x) valid) and per destination
- *                 (channels [c_x, 2 c_x) valid); grad_x = the sum of the two valid halves.
+ *   grad_x_src / grad_x_dst [num_nodes, d, c_x] fp32: D_e^T rad[e] (*) SO2_1^T(dz1_e)
+ *                 restricted to the x[src] channels and summed per source, resp. to the
+ *                 x[dst] channels and summed per destination; grad_x = their sum.
  * grad_x_msg (nullable; then a "source-target-message" block, whose 2 c_x
- * above read 3 c_x): [E, d, 3 c_x] fp32, per dst-sorted edge position, channels
- * [2 c_x, 3 c_x) valid: the gradient of that edge's x_msg row; edge_seg [E] =
- * 0, 1, ..., E - 1.
+ * above read 3 c_x): [E, d, c_x] fp32, per dst-sorted edge position: the
+ * gradient of that edge's x_msg row; edge_seg [E] = 0, 1, ..., E - 1.
  * grad_row (nullable: dst) is the row of grad_out of each edge (e for the
  * per-edge output of forward_edge, grad_out then [E, d, c_x]).
  * Edges in the forward's dst-sorted order (dst, seg_ptr); src_sorted / edge_idx /
  * seg_ptr_src: the same edges sorted by source, edge_idx the dst-sorted position
  * of each.  wpack1_t / wpack2_t: the two convolutions packed for the transposed
  * GEMM (conv1 gated).  c_x a multiple of 32.  partials: maloq_message_partials_floats(lmax,
- * 1, E, 2 c_x) floats (3 c_x with grad_x_msg).  dz2_ws and dz1_ws feed
+ * 1, E, c_x) floats.  dz2_ws and dz1_ws feed
  * maloq_message_dw (conv2: dz2 with the forward's z_ws; conv1: dz1 with y_ws).
  * Replaces the autograd backward of Edgewise.forward_node (esen_block.py:146-208). */
 int maloq_message_edgewise_bwd_dx(int dtype, int lmax, int mmax, const float* grad_out, int c_x,
@@ -295,13 +327,14 @@ int64_t maloq_message_dw_partials_floats(int lmax, int mmax, int gate, int c_out
  * (lmax+1) c_in], the gate block being sum_e dG(e)^T Y_0(e).
  * dz [E, d', c_out], y [E, d', c_in] (dtype; for bf16 with maloq_message_edge_rows(E)
  * rows, zero from row E on, channels multiples of 8), dw0 [(lmax+1) c_out, (lmax+1) c_in],
- * dw_m [2 (lmax-m+1) c_out, (lmax-m+1) c_in] fp32.  Split-K over edges,
+ * dwm: host array of mmax device pointers (mmax <= 6), dwm[m - 1] = dW_m
+ * [2 (lmax-m+1) c_out, (lmax-m+1) c_in] fp32.  Split-K over edges,
  * partials summed in split order (deterministic).
  * Replaces the autograd weight gradient of SO2_Convolution
  * (helm/nn/so2_layers.py:139-214, SO2_m_Conv :61-67). */
 int maloq_message_dw(int dtype, int lmax, int mmax, int gate, const void* dz, const void* y,
                      int64_t num_edges, int c_out, int c_in, int splits, float* partials,
-                     float* dw0, float* dw1, float* dw2, float* dw3, void* stream);
+                     float* dw0, float* const* dwm, void* stream);
 
 /* Bias gradient of fc_m0: out[r c + k] = sum_{e < num_edges} rows[e][row0 + r][k]
  * for r < nrows, k < c, where rows [num_edges, rows_per_edge, c] (dtype 0 =

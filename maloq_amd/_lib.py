@@ -27,6 +27,7 @@ SIGNATURES = {
     "maloq_edge_euler": [_p, _i64, _u64, _p, _p],
     "maloq_edge_vec_to_wigner": [_p, _i64, _u64, _i32, _p, _p, _p, _p, _i32, _p],
     "maloq_wigner_from_euler": [_p, _i64, _i32, _p, _p, _p, _i32, _p],
+    "maloq_rotate": [_i32, _i32, _i32, _p, _i32, _p, _i64, _p, _p, _p, _i32, _p, _p],
     "maloq_label_transform": [_p, _p, _p, _p, _i64, _i32, _i32, _p, _p, _p, _p],
     "maloq_basis_row_meta": [_i64, _p, _p, _p, _p, _p, _i64, _p, _i32, _p, _p],
     "maloq_fock_to_irreps": [_p, _i64, _p, _i64, _p, _i32, _p, _p, _p, _i32, _i32, _p, _p, _p, _p],
@@ -47,7 +48,9 @@ SIGNATURES = {
                              _p, _p, _i64, _i32, _p, _p, _p, _p, _p],
     "maloq_message_edge_rows": [_i64],
     "maloq_message_dw_partials_floats": [_i32, _i32, _i32, _i32, _i32, _i32],
-    "maloq_message_dw": [_i32, _i32, _i32, _i32, _p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p],
+    "maloq_message_dw": [_i32, _i32, _i32, _i32, _p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p],
+    "maloq_message_supported": [_i32, _i32],
+    "maloq_message_wigner_rows": [_i32, _i32, _p, _p, _i64, _p, _p],
     "maloq_message_pack": [_i32, _i32, _p, _p, _p, _i64, _p, _p],
     "maloq_message_colsum_partials_floats": [_i32, _i32, _i64],
     "maloq_message_colsum": [_i32, _p, _i32, _i32, _i32, _i32, _i64, _p, _p, _p],

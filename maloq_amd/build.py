@@ -9,6 +9,7 @@ from __future__ import annotations
 import concurrent.futures as cf
 import glob
 import os
+import re
 import subprocess
 import sys
 
@@ -29,10 +30,24 @@ FLAGS = [
 ]
 
 
+_INCLUDE = re.compile(r'^\s*#\s*include\s+"([^"]+)"', re.M)
+
+
+def _deps(path: str, seen: set) -> set:
+    """The file and every project header it includes, transitively."""
+    path = os.path.normpath(path)
+    if path in seen or not os.path.exists(path):
+        return seen
+    seen.add(path)
+    with open(path, encoding="utf-8", errors="replace") as f:
+        for inc in _INCLUDE.findall(f.read()):
+            _deps(os.path.join(os.path.dirname(path), inc), seen)
+    return seen
+
+
 def _deps_mtime(src: str) -> float:
-    """Newest mtime among the source and the headers of csrc/ (coarse but safe)."""
-    hdrs = glob.glob(os.path.join(CSRC, "*.h")) + glob.glob(os.path.join(HERE, "..", "include", "*.h"))
-    return max([os.path.getmtime(src)] + [os.path.getmtime(h) for h in hdrs])
+    """Newest mtime among the source and the headers it includes."""
+    return max(os.path.getmtime(p) for p in _deps(src, set()))
 
 
 def _compile(src: str, incremental: bool = False) -> str:

@@ -68,8 +68,8 @@ __device__ __forceinline__ void m0_row_euler(const float* sJ, float b, float c, 
   float cb[l + 1], sb[l + 1], cc[l + 1], sc[l + 1];
 #pragma unroll
   for (int m = 0; m <= l; ++m) {
-    sincosf(static_cast<float>(m) * b, &sb[m], &cb[m]);
-    sincosf(static_cast<float>(m) * c, &sc[m], &cc[m]);
+    sincos_m(m, b, &sb[m], &cb[m]);
+    sincos_m(m, c, &sc[m], &cc[m]);
   }
   const float* J = sJ + jd_offset(l);
   float acc[n], m2[n];

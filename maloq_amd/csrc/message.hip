@@ -74,7 +74,7 @@ static int dispatch(int lmax, int mmax, int dtype, int gate, int mode, const Arg
     case 6: return launch_l6(mmax, dtype, gate, mode, a, s);
     default: break;
   }
-  MALOQ_REQUIRE(false, "unsupported lmax %d (built: 2, 4, 6 with mmax 2)", lmax);
+  MALOQ_REQUIRE(false, "unsupported lmax %d (built: (lmax, mmax) in (2, 2), (4, 2), (4, 4), (6, 2), (6, 6))", lmax);
 }
 
 static int prep_dispatch(int lmax, int mmax, int dtype, int mode, const PrepArgs& a,
@@ -85,7 +85,7 @@ static int prep_dispatch(int lmax, int mmax, int dtype, int mode, const PrepArgs
     case 6: return prep_l6(mmax, dtype, mode, a, s);
     default: break;
   }
-  MALOQ_REQUIRE(false, "unsupported lmax %d (built: 2, 4, 6 with mmax 2)", lmax);
+  MALOQ_REQUIRE(false, "unsupported lmax %d (built: (lmax, mmax) in (2, 2), (4, 2), (4, 4), (6, 2), (6, 6))", lmax);
 }
 
 static int check_common(int dtype, int lmax, int mmax, int c_k, int c_n, int64_t E) {
@@ -123,9 +123,13 @@ extern "C" int maloq_message_kept_rows(int lmax, int mmax) { return kept_rows(lm
 
 extern "C" int maloq_message_wigner_floats(int lmax, int mmax) { return wigner_floats(lmax, mmax); }
 
+extern "C" int maloq_message_supported(int lmax, int mmax) {
+  return (lmax == 2 && mmax == 2) || ((lmax == 4 || lmax == 6) && (mmax == 2 || mmax == lmax)) ? 1 : 0;
+}
+
 extern "C" int64_t maloq_message_partials_floats(int lmax, int gate, int64_t num_edges, int c_out) {
   const int64_t d = static_cast<int64_t>(lmax + 1) * (lmax + 1);
-  const int64_t te = tile_edges(lmax, gate);
+  const int64_t te = MIN_TILE_EDGES;  // sized for the smallest tile of any instantiation
   return ((num_edges + te - 1) / te) * 2 * d * c_out;
 }
 
@@ -149,10 +153,11 @@ extern "C" int maloq_message_fwd(int dtype, int lmax, int mmax, int gate, const 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t d = static_cast<int64_t>(lmax + 1) * (lmax + 1);
   if (num_edges > 0) {
-    MALOQ_REQUIRE(x && src && dst && eulers && partials && y_ws && dk_ws, "null pointer");
+    MALOQ_REQUIRE(x && src && dst && partials && y_ws && dk_ws, "null pointer");
     PrepArgs p{};
     p.x = x; p.gidx = src; p.eidx = nullptr; p.eulers = eulers; p.rad = rad; p.jd = jd;
-    p.y = y_ws; p.r = r_ws; p.dk = dk_ws; p.build_d = 1; p.E = num_edges; p.C = c_in;
+    // without Euler triples dk_ws already holds the kept Wigner rows (maloq_message_wigner_rows)
+    p.y = y_ws; p.r = r_ws; p.dk = dk_ws; p.build_d = eulers != nullptr; p.E = num_edges; p.C = c_in;
     rc = prep_dispatch(lmax, mmax, dtype, FWD, p, s);
     if (rc) return rc;
     Args a{};
@@ -160,14 +165,14 @@ extern "C" int maloq_message_fwd(int dtype, int lmax, int mmax, int gate, const 
     a.wpack = static_cast<const char*>(wpack); a.bias = bias; a.out = out;
     a.part = partials; a.E = num_edges; a.C_k = c_in; a.C_n = c_out; a.n_cb = c_out / CB;
     a.extra = gate ? lmax * c_out : 0;
-    a.ntiles = (num_edges + tile_edges(lmax, gate) - 1) / tile_edges(lmax, gate);
+    a.ntiles = (num_edges + tile_edges(lmax, mmax, gate) - 1) / tile_edges(lmax, mmax, gate);
     const int kc = dtype == 1 ? BF16::KC : F32::KC;
     a.frags_per_cb = frags_per_cb(lmax, mmax, gate, c_in, kc);
     a.gsave = gate ? gate_ws : nullptr;
     rc = dispatch(lmax, mmax, dtype, gate, FWD, a, s);
     if (rc) return rc;
   }
-  return fixup(seg_ptr, num_nodes, partials, out, d * c_out, tile_edges(lmax, gate), s);
+  return fixup(seg_ptr, num_nodes, partials, out, d * c_out, tile_edges(lmax, mmax, gate), s);
 }
 
 extern "C" int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const void* x, int c_x,
@@ -192,14 +197,14 @@ extern "C" int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const v
   const int64_t d = static_cast<int64_t>(lmax + 1) * (lmax + 1);
   const int kc = dtype == 1 ? BF16::KC : F32::KC;
   if (num_edges > 0) {
-    MALOQ_REQUIRE(x && src && dst && eulers && partials && y_ws && dk_ws && z_ws, "null pointer");
+    MALOQ_REQUIRE(x && src && dst && partials && y_ws && dk_ws && z_ws, "null pointer");
     MALOQ_REQUIRE(!x_msg || msg_row, "the edge message rows need msg_row");
     const int32_t* seg = seg_id ? seg_id : dst;
     // rotated message rows of cat(x[src], x[dst]) (radial scale applied) and the Wigner rows
     PrepArgs p{};
     p.x = x; p.gidx = src; p.gidx2 = dst; p.x3 = x_msg; p.gidx3 = msg_row; p.x_c = c_x;
     p.eidx = nullptr; p.eulers = eulers;
-    p.rad = rad; p.jd = jd; p.y = y_ws; p.r = r_ws; p.dk = dk_ws; p.build_d = 1;
+    p.rad = rad; p.jd = jd; p.y = y_ws; p.r = r_ws; p.dk = dk_ws; p.build_d = eulers != nullptr;
     p.E = num_edges; p.C = parts * c_x;
     rc = prep_dispatch(lmax, mmax, dtype, FWD, p, s);
     if (rc) return rc;
@@ -209,7 +214,7 @@ extern "C" int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const v
     a.wpack = static_cast<const char*>(wpack1); a.bias = bias1; a.out = out; a.part = partials;
     a.E = num_edges; a.C_k = parts * c_x; a.C_n = c_hidden; a.n_cb = c_hidden / CB;
     a.extra = lmax * c_hidden;
-    a.ntiles = (num_edges + tile_edges(lmax, 1) - 1) / tile_edges(lmax, 1);
+    a.ntiles = (num_edges + tile_edges(lmax, mmax, 1) - 1) / tile_edges(lmax, mmax, 1);
     a.frags_per_cb = frags_per_cb(lmax, mmax, 1, parts * c_x, kc);
     a.gsave = gate_ws; a.zout = z_ws;
     rc = dispatch(lmax, mmax, dtype, 1, FWD_EDGE, a, s);
@@ -219,12 +224,12 @@ extern "C" int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const v
     b.a_src = z_ws; b.dk = dk_ws; b.seg = seg; b.eidx = nullptr;
     b.wpack = static_cast<const char*>(wpack2); b.bias = bias2; b.out = out; b.part = partials;
     b.E = num_edges; b.C_k = c_hidden; b.C_n = c_out; b.n_cb = c_out / CB; b.extra = 0;
-    b.ntiles = (num_edges + tile_edges(lmax, 0) - 1) / tile_edges(lmax, 0);
+    b.ntiles = (num_edges + tile_edges(lmax, mmax, 0) - 1) / tile_edges(lmax, mmax, 0);
     b.frags_per_cb = frags_per_cb(lmax, mmax, 0, c_hidden, kc);
     rc = dispatch(lmax, mmax, dtype, 0, FWD, b, s);
     if (rc) return rc;
   }
-  return fixup(seg_ptr, num_nodes, partials, out, d * c_out, tile_edges(lmax, 0), s);
+  return fixup(seg_ptr, num_nodes, partials, out, d * c_out, tile_edges(lmax, mmax, 0), s);
 }
 
 extern "C" int maloq_message_edgewise_bwd_dx(
@@ -263,7 +268,7 @@ extern "C" int maloq_message_edgewise_bwd_dx(
     b.a_src = dz2_ws; b.dk = dk; b.seg = dst; b.eidx = nullptr;
     b.wpack = static_cast<const char*>(wpack2_t); b.out = grad_x_src; b.part = partials;
     b.E = num_edges; b.C_k = c_x; b.C_n = c_hidden; b.n_cb = c_hidden / CB;
-    b.ntiles = (num_edges + tile_edges(lmax, 0) - 1) / tile_edges(lmax, 0);
+    b.ntiles = (num_edges + tile_edges(lmax, mmax, 0) - 1) / tile_edges(lmax, mmax, 0);
     b.frags_per_cb = frags_per_cb(lmax, mmax, 0, c_x, kc);
     b.zout = dz1_ws; b.gsave = const_cast<void*>(gate_saved);
     rc = dispatch(lmax, mmax, dtype, 0, BWD_EDGE, b, s);
@@ -280,21 +285,22 @@ extern "C" int maloq_message_edgewise_bwd_dx(
       a.out = part == 0 ? grad_x_src : (part == 1 ? grad_x_dst : grad_x_msg);
       a.part = partials; a.E = num_edges; a.C_k = c_hidden; a.C_n = parts * c_x;
       a.cb0 = part * (c_x / CB); a.n_cb = c_x / CB;
-      a.ntiles = (num_edges + tile_edges(lmax, 1, BWD_DX) - 1) / tile_edges(lmax, 1, BWD_DX);
+      a.ow = c_x;   // each part's gradient is its own [*, d, c_x] array
+      a.ntiles = (num_edges + tile_edges(lmax, mmax, 1, BWD_DX) - 1) / tile_edges(lmax, mmax, 1, BWD_DX);
       a.frags_per_cb = frags_per_cb(lmax, mmax, 1, c_hidden, kc);
       rc = dispatch(lmax, mmax, dtype, 1, BWD_DX, a, s);
       if (rc) return rc;
       // per-edge rows of the message part: single-edge segments, never cut
       if (part == 2) continue;
       rc = fixup(part ? seg_ptr : seg_ptr_src, num_nodes, partials, part ? grad_x_dst : grad_x_src,
-                 d * parts * c_x, tile_edges(lmax, 1, BWD_DX), s);
+                 d * c_x, tile_edges(lmax, mmax, 1, BWD_DX), s);
       if (rc) return rc;
     }
     return MALOQ_OK;
   }
-  rc = fixup(seg_ptr_src, num_nodes, partials, grad_x_src, d * parts * c_x, tile_edges(lmax, 1, BWD_DX), s);
+  rc = fixup(seg_ptr_src, num_nodes, partials, grad_x_src, d * c_x, tile_edges(lmax, mmax, 1, BWD_DX), s);
   if (rc) return rc;
-  return fixup(seg_ptr, num_nodes, partials, grad_x_dst, d * parts * c_x, tile_edges(lmax, 1, BWD_DX), s);
+  return fixup(seg_ptr, num_nodes, partials, grad_x_dst, d * c_x, tile_edges(lmax, mmax, 1, BWD_DX), s);
 }
 
 extern "C" int maloq_message_bwd_dx(int dtype, int lmax, int mmax, int gate, const float* grad_out,
@@ -327,11 +333,11 @@ extern "C" int maloq_message_bwd_dx(int dtype, int lmax, int mmax, int gate, con
     a.rad = rad; a.drad = grad_rad; a.rsave = r_saved;
     a.wpack = static_cast<const char*>(wpack_t); a.bias = nullptr; a.out = grad_x;
     a.part = partials; a.E = num_edges; a.C_k = c_out; a.C_n = c_in; a.n_cb = c_in / CB;
-    a.extra = 0; a.ntiles = (num_edges + tile_edges(lmax, gate, BWD_DX) - 1) / tile_edges(lmax, gate, BWD_DX);
+    a.extra = 0; a.ntiles = (num_edges + tile_edges(lmax, mmax, gate, BWD_DX) - 1) / tile_edges(lmax, mmax, gate, BWD_DX);
     const int kc = dtype == 1 ? BF16::KC : F32::KC;
     a.frags_per_cb = frags_per_cb(lmax, mmax, gate, c_out, kc);
     rc = dispatch(lmax, mmax, dtype, gate, BWD_DX, a, s);
     if (rc) return rc;
   }
-  return fixup(seg_ptr_src, num_nodes, partials, grad_x, d * c_in, tile_edges(lmax, gate, BWD_DX), s);
+  return fixup(seg_ptr_src, num_nodes, partials, grad_x, d * c_in, tile_edges(lmax, mmax, gate, BWD_DX), s);
 }

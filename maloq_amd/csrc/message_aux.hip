@@ -4,14 +4,16 @@
 //     GEMM kernels and converted to the operand type in one launch;
 //   * bias gradient: column sums over edges of chosen rows of the saved
 //     output-gradient rows (dL/db0 of fc_m0), split over edge ranges and
-//     summed in a fixed order (deterministic, no atomics).
-#include "common.h"
+//     summed in a fixed order (deterministic, no atomics);
+//   * kept Wigner rows from a caller's dense [E, d, d] wigner, in the pair
+//     layout the fused kernels read (PairLayout in message_impl.h).
+#include "message_impl.h"
 #include "../../include/maloq_hip.h"
 
 namespace maloq {
 namespace aux {
 
-constexpr int MAXSRC = 4;
+constexpr int MAXSRC = 8;  // fc_m0 and so2_m_conv[m - 1] for m <= 7
 
 struct PackArgs {
   const float* src[MAXSRC];
@@ -107,6 +109,43 @@ __global__ __launch_bounds__(CS_TX * CS_TY) void colsum_kernel(const void* __res
 
 static int64_t cs_blocks(int64_t rows) { return rows <= CS_RB ? 1 : (rows + CS_RB - 1) / CS_RB; }
 
+// dk[p][k] for k in the pair layout of (L, M): D(q, j) of degree l is
+// wigner[e][l^2 + i(q)][l^2 + j] with i(0) = l, i(2m - 1) = l + m, i(2m) = l - m
+// (the m-major row types), e = perm[p] (or p); padding entries are zero.
+template <int L, int M>
+__global__ void wigner_rows_kernel(const float* __restrict__ wigner, const int64_t* __restrict__ perm,
+                                   int64_t E, float* __restrict__ dk) {
+  using PL = msg::PairLayout<L, M>;
+  constexpr int WS = PL::WS, d = (L + 1) * (L + 1);
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= E * WS) return;
+  const int64_t p = idx / WS;
+  const int k = static_cast<int>(idx - p * WS);
+  int l = 0;
+  while (l < L && k >= PL::woff(l + 1)) ++l;
+  const int r = k - PL::woff(l), pb = PL::pblk(l);
+  const int pair = r / pb, s = r - pair * pb;
+  const int q = s >> 1, j = 2 * pair + (s & 1);
+  float v = 0.f;
+  if (q < PL::nq(l) && j <= 2 * l) {
+    const int m = (q + 1) >> 1;
+    const int i = q == 0 ? l : ((q & 1) ? l + m : l - m);
+    const int64_t e = perm != nullptr ? perm[p] : p;
+    v = wigner[(e * d + l * l + i) * d + l * l + j];
+  }
+  dk[idx] = v;
+}
+
+template <int L, int M>
+int wigner_rows(const float* wigner, const int64_t* perm, int64_t E, float* dk, hipStream_t s) {
+  const int64_t n = E * msg::PairLayout<L, M>::WS;
+  const int64_t grid = (n + 255) / 256;
+  MALOQ_REQUIRE(grid < (int64_t(1) << 31), "grid too large");
+  hipLaunchKernelGGL((wigner_rows_kernel<L, M>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, wigner, perm,
+                     E, dk);
+  return check_launch("wigner_rows_kernel");
+}
+
 }  // namespace aux
 }  // namespace maloq
 
@@ -186,5 +225,21 @@ extern "C" int maloq_message_colsum(int dtype, const void* rows, int rows_per_ed
     stride = n;
     nr = sb;
     bf = false;
+  }
+}
+
+extern "C" int maloq_message_wigner_rows(int lmax, int mmax, const float* wigner, const int64_t* perm,
+                                         int64_t num_edges, float* dk, void* stream) {
+  MALOQ_REQUIRE(maloq_message_supported(lmax, mmax), "no message kernels for lmax %d, mmax %d", lmax, mmax);
+  MALOQ_REQUIRE(num_edges >= 0, "num_edges < 0");
+  if (num_edges == 0) return MALOQ_OK;
+  MALOQ_REQUIRE(wigner && dk, "null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (lmax * 10 + mmax) {
+    case 22: return aux::wigner_rows<2, 2>(wigner, perm, num_edges, dk, s);
+    case 42: return aux::wigner_rows<4, 2>(wigner, perm, num_edges, dk, s);
+    case 44: return aux::wigner_rows<4, 4>(wigner, perm, num_edges, dk, s);
+    case 62: return aux::wigner_rows<6, 2>(wigner, perm, num_edges, dk, s);
+    default: return aux::wigner_rows<6, 6>(wigner, perm, num_edges, dk, s);
   }
 }

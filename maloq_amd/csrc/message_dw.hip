@@ -348,9 +348,12 @@ __global__ __launch_bounds__(256, 1) void dw_tr_kernel(DwArgs a) {
 // One thread per element of the reference-layout gradients:
 // dW0 [(gate ? L : 0) C_out + (L+1) C_out, (L+1) C_in] (gate rows first, as in
 // fc_m0, so2_layers.py:112-115), then dW_m [2 (L-m+1) C_out, (L-m+1) C_in].
-__global__ void dw_reduce_kernel(DwArgs a, int lmax, float* __restrict__ dw0,
-                                 float* __restrict__ dw1, float* __restrict__ dw2,
-                                 float* __restrict__ dw3) {
+// Destinations of the m >= 1 gradients (a kernel argument by value).
+struct DwOut {
+  float* m[MAXG];
+};
+
+__global__ void dw_reduce_kernel(DwArgs a, int lmax, float* __restrict__ dw0, DwOut dwm) {
   const int g = blockIdx.y;
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t Kg = static_cast<int64_t>(a.rowsy[g]) * a.C_in;
@@ -381,7 +384,7 @@ __global__ void dw_reduce_kernel(DwArgs a, int lmax, float* __restrict__ dw0,
     const int64_t ko = r - ho;
     v = C(ho + ko, ki) - C(ko, ki_n + ki);
   }
-  float* dst = m == 1 ? dw1 : (m == 2 ? dw2 : dw3);
+  float* dst = dwm.m[m - 1];
   dst[idx] = v;
 }
 
@@ -397,7 +400,7 @@ using namespace maloq::msg;
 // gated block dz's gate rows (after the kept rows) against y's m = 0 rows.
 static int dw_setup(DwArgs& a, int lmax, int mmax, int gate, int64_t E, int c_out, int c_in,
                     int splits, int tile, int gran) {
-  MALOQ_REQUIRE(mmax >= 0 && mmax <= 3 && mmax <= lmax, "mmax out of range for the weight gradient");
+  MALOQ_REQUIRE(mmax >= 0 && mmax + 2 <= MAXG && mmax <= lmax, "mmax out of range for the weight gradient");
   MALOQ_REQUIRE(splits >= 1 && splits <= 64, "splits out of range");
   a.E = E;
   a.C_out = c_out;
@@ -452,7 +455,7 @@ extern "C" int64_t maloq_message_dw_partials_floats(int lmax, int mmax, int gate
 
 extern "C" int maloq_message_dw(int dtype, int lmax, int mmax, int gate, const void* dz, const void* y,
                                 int64_t num_edges, int c_out, int c_in, int splits,
-                                float* partials, float* dw0, float* dw1, float* dw2, float* dw3,
+                                float* partials, float* dw0, float* const* dwm,
                                 void* stream) {
   MALOQ_REQUIRE(dtype == 0 || dtype == 1, "dtype must be 0 (fp32) or 1 (bf16)");
   MALOQ_REQUIRE(num_edges >= 0, "num_edges < 0");
@@ -469,9 +472,12 @@ extern "C" int maloq_message_dw(int dtype, int lmax, int mmax, int gate, const v
     if (rc) return rc;
   }
   MALOQ_REQUIRE(partials && dw0, "null pointer");
-  MALOQ_REQUIRE(mmax < 1 || dw1, "dw1 is null");
-  MALOQ_REQUIRE(mmax < 2 || dw2, "dw2 is null");
-  MALOQ_REQUIRE(mmax < 3 || dw3, "dw3 is null");
+  DwOut outm{};
+  MALOQ_REQUIRE(mmax == 0 || dwm, "dwm is null");
+  for (int m = 1; m <= mmax; ++m) {
+    MALOQ_REQUIRE(dwm[m - 1], "dwm[%d] is null", m - 1);
+    outm.m[m - 1] = dwm[m - 1];
+  }
   MALOQ_REQUIRE(num_edges == 0 || (dz && y), "null pointer");
   a.dz = dz;
   a.y = y;
@@ -494,6 +500,6 @@ extern "C" int maloq_message_dw(int dtype, int lmax, int mmax, int gate, const v
     maxel = el > maxel ? el : maxel;
   }
   hipLaunchKernelGGL(dw_reduce_kernel, dim3(static_cast<unsigned>((maxel + 255) / 256), a.ngroups),
-                     dim3(256), 0, s, a, lmax, dw0, dw1, dw2, dw3);
+                     dim3(256), 0, s, a, lmax, dw0, outm);
   return check_launch("dw_reduce_kernel");
 }

@@ -727,7 +727,9 @@ struct Gemm {
     const uint64_t startmask = (endmask << 1) | 1ull;
     for (int p = 0; p <= lo; ++p) {
       const bool has_col = 2 * p + h < n;
-      const int64_t colo = static_cast<int64_t>(lo * lo + 2 * p + h) * a.C_n + cb * CB + co;
+      const int ow = a.ow > 0 ? a.ow : a.C_n;
+      const int ocb = a.ow > 0 ? cb - a.cb0 : cb;
+      const int64_t colo = static_cast<int64_t>(lo * lo + 2 * p + h) * ow + ocb * CB + co;
       float run = 0.f;
       static_for<2 * RT>([&](auto CI) {
         constexpr int c = decltype(CI)::value;
@@ -885,13 +887,14 @@ struct Gemm {
     const bool lp = (e0 + nvalid < a.E) && (a.seg[e0 + nvalid] == a.seg[e0 + nvalid - 1]);
     if (tid < TE) {
       float* dst = nullptr;
+      const int64_t ow = a.ow > 0 ? a.ow : a.C_n;
       if (tid < nvalid) {
         const int sg = s.seg[tid];
         const bool first = sg == s.seg[0], last = sg == s.seg[nvalid - 1];
         if ((first && fp) || (last && lp))
-          dst = a.part + (tile * 2 + (first ? 0 : 1)) * d * a.C_n;
+          dst = a.part + (tile * 2 + (first ? 0 : 1)) * d * ow;
         else
-          dst = a.out + static_cast<int64_t>(sg) * d * a.C_n;
+          dst = a.out + static_cast<int64_t>(sg) * d * ow;
       }
       s.optr[tid] = dst;
     }
@@ -927,8 +930,9 @@ struct Gemm {
 
 // KR: (C_k / KC) % 3 if C_k / KC >= 2, else 3.
 // RAD (input gradient only): a radial scale is given (its gradient is formed).
-template <int L, int M, bool GATE, int NW, int RT, class TM, int MODE, int KR, bool RAD>
-__global__ __launch_bounds__(NW * 64, 2) void gemm_kernel(Args a) {
+// MINB: resident workgroups per CU the register allocation targets.
+template <int L, int M, bool GATE, int NW, int RT, class TM, int MODE, int KR, bool RAD, int MINB>
+__global__ __launch_bounds__(NW * 64, MINB) void gemm_kernel(Args a) {
   Gemm<L, M, GATE, NW, RT, TM, MODE>::template run<KR, RAD>(a);
 }
 

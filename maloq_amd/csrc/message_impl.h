@@ -187,6 +187,8 @@ struct Args {
                           // [E_all, d' + L, C_n], the gate backward of those rows at the
                           // pre-activations in gsave ([E_all, d' + L, C_n])
   int cb0;                // first output channel block (the grid covers n_cb blocks from it)
+  int ow;                 // channels per row of out / part (0: C_n); output channel block cb
+                          // lands at channel (cb - cb0) CB of its row when ow != 0
 };
 
 template <int L, int M>
@@ -355,7 +357,7 @@ struct Prep {
       const int e = q / (3 * (L + 1)), r = q % (3 * (L + 1));
       const int ang = r / (L + 1), m = r % (L + 1);
       float sn, cs;
-      sincosf(static_cast<float>(m) * s.eul[e * 3 + ang], &sn, &cs);
+      sincos_m(m, s.eul[e * 3 + ang], &sn, &cs);
       s.trig[(e * 3 + ang) * 2 * (L + 1) + m] = cs;
       s.trig[(e * 3 + ang) * 2 * (L + 1) + (L + 1) + m] = sn;
     }

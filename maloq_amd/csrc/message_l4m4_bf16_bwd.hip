@@ -1,0 +1,11 @@
+// Fused message GEMM kernels for lmax = mmax = 4, bf16, input gradient.
+#include "message_launch.h"
+
+namespace maloq {
+namespace msg {
+
+MALOQ_GEMM_INSTANCES(, 4, 4, BF16, BWD_DX)
+MALOQ_GEMM_BWD_EDGE_INSTANCES(, 4, 4, BF16)
+
+}  // namespace msg
+}  // namespace maloq

@@ -1,0 +1,11 @@
+// Fused message GEMM kernels for lmax = mmax = 6, bf16, forward.
+#include "message_launch.h"
+
+namespace maloq {
+namespace msg {
+
+MALOQ_GEMM_INSTANCES(, 6, 6, BF16, FWD)
+MALOQ_GEMM_EDGE_INSTANCES(, 6, 6, BF16)
+
+}  // namespace msg
+}  // namespace maloq

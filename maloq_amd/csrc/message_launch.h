@@ -5,34 +5,47 @@
 namespace maloq {
 namespace msg {
 
-// Waves per workgroup and 32-edge row tiles per workgroup for each lmax:
-// lmax <= 4 without gate: 4 waves x 64 edges; gated or lmax > 4: 4 waves x
-// 32 edges, so a wave's accumulators and operand registers stay within the
-// 256 registers of two resident workgroups per CU.
-template <int L, bool GATE, int MODE = FWD>
+// Waves per workgroup, 32-edge row tiles per workgroup and resident
+// workgroups per CU (the launch bound) for each shape:
+//   mmax < lmax, lmax <= 4 without gate: 4 waves x 64 edges, two workgroups
+//     per CU (256 registers per lane);
+//   gated, or lmax > 4: 4 waves x 32 edges (the gated input gradient has no
+//     extra accumulators -- its gate rows are an extra input row type -- so it
+//     keeps the 64-edge tiles at lmax <= 4);
+//   mmax = lmax (every output degree keeps all 2l + 1 row types, d' = d):
+//     32-edge tiles; at lmax > 4, or gated with an accumulating forward (the
+//     gate rows are extra accumulators), one workgroup per CU, so a wave has
+//     512 registers (accumulators in AGPRs) instead of spilling.
+template <int L, int M, bool GATE, int MODE = FWD>
 struct Cfg {
   static constexpr int NW = 4;
-  // the gated input gradient has no extra accumulators (its gate rows are an
-  // extra input row type), so it keeps the 64-edge tiles
-  static constexpr int RT = (L <= 4 && (!GATE || MODE == BWD_DX)) ? 2 : 1;
+  static constexpr bool FULL = M == L && L > 2;
+  static constexpr int RT = FULL ? 1 : ((L <= 4 && (!GATE || MODE == BWD_DX)) ? 2 : 1);
+  static constexpr int MINB = (FULL && (L > 4 || (GATE && (MODE == FWD || MODE == FWD_EDGE)))) ? 1 : 2;
 };
 
-inline int tile_edges(int lmax, int gate, int mode = FWD) {
+inline int tile_edges(int lmax, int mmax, int gate, int mode = FWD) {
+  if (mmax == lmax && lmax > 2) return 32;
   return (lmax <= 4 && (!gate || mode == BWD_DX)) ? 64 : 32;
 }
+// Every instantiation's tile has a multiple of 32 edges: partial-segment
+// buffers sized for 32-edge tiles fit them all.
+constexpr int MIN_TILE_EDGES = 32;
 
 template <int L, int M, bool GATE, class TM, int MODE, int KR>
 void launch_kr(const Args& a, dim3 g, dim3 b, hipStream_t s) {
-  constexpr int NW = Cfg<L, GATE, MODE>::NW, RT = Cfg<L, GATE, MODE>::RT;
+  using C = Cfg<L, M, GATE, MODE>;
   if (MODE == BWD_DX && a.rad != nullptr)
-    hipLaunchKernelGGL((gemm_kernel<L, M, GATE, NW, RT, TM, MODE, KR, MODE == BWD_DX>), g, b, 0, s, a);
+    hipLaunchKernelGGL((gemm_kernel<L, M, GATE, C::NW, C::RT, TM, MODE, KR, MODE == BWD_DX, C::MINB>), g, b, 0, s,
+                       a);
   else
-    hipLaunchKernelGGL((gemm_kernel<L, M, GATE, NW, RT, TM, MODE, KR, false>), g, b, 0, s, a);
+    hipLaunchKernelGGL((gemm_kernel<L, M, GATE, C::NW, C::RT, TM, MODE, KR, false, C::MINB>), g, b, 0, s, a);
 }
 
 template <int L, int M, bool GATE, class TM, class TX, int MODE>
 int launch(const Args& a, hipStream_t s) {
-  constexpr int NW = Cfg<L, GATE, MODE>::NW, RT = Cfg<L, GATE, MODE>::RT;
+  constexpr int NW = Cfg<L, M, GATE, MODE>::NW, RT = Cfg<L, M, GATE, MODE>::RT;
+  MALOQ_REQUIRE(tile_edges(L, M, GATE, MODE) == 32 * RT, "tile size mismatch");
   using P = GPlan<L, M, GATE, NW, RT>;
   // Must match the workgroup -> (tile, channel block) mapping of Gemm::run:
   // tiles in groups of 8 (one per XCD), n_cb workgroups per tile.

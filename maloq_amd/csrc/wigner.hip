@@ -69,7 +69,7 @@ __global__ __launch_bounds__(256) void wigner_dense_kernel(
     for (int q = row; q < 3 * (L + 1); q += d) {
       const int ang = q / (L + 1), m = q - ang * (L + 1);
       float s, c;
-      sincosf(static_cast<float>(m) * sAng[el][ang], &s, &c);
+      sincos_m(m, sAng[el][ang], &s, &c);
       sTrig[el][ang][0][m] = c;
       sTrig[el][ang][1][m] = s;
     }

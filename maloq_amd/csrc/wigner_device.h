@@ -61,6 +61,18 @@ __host__ __device__ constexpr int jd_offset(int l) {
   return s;
 }
 
+// sin and cos of m t, the product and the trigonometry in fp64 and then
+// rounded: the fp32 product m t alone would carry an error of up to
+// |m t| 2^-24, which frequency m turns into O(1e-6) errors of D at l >= 5.
+// Every kernel that builds Wigner blocks uses this, so their blocks agree bit
+// for bit.
+__device__ __forceinline__ void sincos_m(int m, float t, float* s, float* c) {
+  double sd, cd;
+  sincos(static_cast<double>(m) * static_cast<double>(t), &sd, &cd);
+  *s = static_cast<float>(sd);
+  *c = static_cast<float>(cd);
+}
+
 // cos / sin of (l - i) * t from a table of cos(m t), sin(m t), m = 0..L.
 __device__ __forceinline__ float xcos(const float* tc, int f) { return tc[f < 0 ? -f : f]; }
 __device__ __forceinline__ float xsin(const float* ts, int f) {

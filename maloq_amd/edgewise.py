@@ -13,10 +13,14 @@ GEMM applies the gate in its epilogue and leaves the rows in the edge frame,
 the second GEMM rotates back and sums per segment.  The backward
 (``maloq_message_edgewise_bwd_dx`` plus the weight-gradient kernels) gives
 the gradients of x, of both convolutions' weights and of the radial
-function's parameters (through ``rad_func``).  Wigner matrices are
-built in the kernels from the Euler angles (``eulers=``, as from
-:func:`maloq_amd.wigner.extract_euler_angles`); the dense ``wigner`` /
-``wigner_inv`` arguments of the reference signature are not read.
+function's parameters (through ``rad_func``).  The Wigner rows come from the
+reference's own dense ``wigner`` argument (its kept rows gathered once per
+call, ``maloq_message_wigner_rows``; ``wigner_inv``, its transpose, is not
+read) or, with ``eulers=`` (as from
+:func:`maloq_amd.wigner.extract_euler_angles`), are built inside the prep
+kernel with no dense [E, d, d] in HBM.  Built for (lmax, mmax) in (2, 2),
+(4, 2), (4, 4), (6, 2), (6, 6); the reference's models use mmax = lmax
+(training_workflow.py:510-511).
 """
 from __future__ import annotations
 
@@ -90,6 +94,13 @@ class Edgewise(nn.Module):
         self.act_type, self.include_edges = act_type, include_edges
         if act_type != "gate":
             raise ValueError(f"Unknown activation type {act_type}")
+        # Refuse at construction what the kernels are not built for (instead of
+        # a C-ABI error at the first forward).
+        if not _lib.load().maloq_message_supported(lmax, mmax):
+            raise ValueError(f"no message kernels for lmax={lmax}, mmax={mmax} "
+                             "(built: (2, 2), (4, 2), (4, 4), (6, 2), (6, 6))")
+        if sphere_channels % 32 or hidden_channels % 32:
+            raise ValueError("sphere_channels and hidden_channels must be multiples of 32")
         if message_type == "source-target-message":
             self.concat_size = 3
         elif message_type == "source-target":
@@ -113,13 +124,17 @@ class Edgewise(nn.Module):
             raise NotImplementedError("partitioned (multi-GPU) graphs are not supported on one GPU")
         if self.concat_size == 3 and x_message_edge is None:
             raise ValueError("message_type 'source-target-message' needs x_message_edge")
-        if eulers is None:
-            raise ValueError("pass eulers=: the kernels build the Wigner rows from the Euler angles")
-        _lib.require_cuda(x, x_edge, eulers)
+        if eulers is None and wigner is None:
+            raise ValueError("pass the reference's dense wigner [E, d, d] or eulers= [E, 3]")
+        _lib.require_cuda(x, x_edge, eulers, wigner)
         if plan is None:
             plan = MessagePlan(edge_index, x.shape[0])
         rad = self.so2_conv_1.rad_func(plan.sort_edges(x_edge.float()), out_dtype=x.dtype)
-        out = edgewise_block(x, plan, plan.sort_edges(eulers.float()), rad, self.so2_conv_1.weights(),
-                             self.so2_conv_2.weights(), self.lmax, self.mmax, node_or_edge=node_or_edge,
-                             x_message_edge=x_message_edge if self.concat_size == 3 else None)
+        # The kept rows of the dense wigner are gathered in-kernel; wigner_inv is
+        # its transpose (esen_osh.py:294) and is not read.
+        out = edgewise_block(x, plan, plan.sort_edges(eulers.float()) if eulers is not None else None, rad,
+                             self.so2_conv_1.weights(), self.so2_conv_2.weights(), self.lmax, self.mmax,
+                             node_or_edge=node_or_edge,
+                             x_message_edge=x_message_edge if self.concat_size == 3 else None,
+                             wigner=wigner if eulers is None else None)
         return out.to(x.dtype)

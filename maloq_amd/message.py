@@ -54,10 +54,24 @@ class MessagePlan:
     """
 
     def __init__(self, edge_index: torch.Tensor, num_nodes: int):
+        if edge_index.dim() != 2 or edge_index.shape[0] != 2:
+            raise ValueError(f"edge_index must be [2, E], got {tuple(edge_index.shape)}")
         src, dst = edge_index[0].long(), edge_index[1].long()
         self.num_nodes = int(num_nodes)
         self.num_edges = int(src.shape[0])
         self.device = src.device
+        if self.num_nodes < 0:
+            raise ValueError("num_nodes < 0")
+        if self.num_edges >= 2**31 - 1 or self.num_nodes >= 2**31 - 1:
+            raise ValueError("the kernels index edges and nodes with int32")
+        # The kernels gather x[src] and write out[dst] without bounds checks, so
+        # every index must name a node (index_add_ and indexing raise on the
+        # reference path).  One host sync, as the bincount below needs anyway.
+        if self.num_edges > 0:
+            lo = torch.minimum(src.min(), dst.min()).item()
+            hi = torch.maximum(src.max(), dst.max()).item()
+            if lo < 0 or hi >= self.num_nodes:
+                raise ValueError(f"edge_index holds node ids in [{lo}, {hi}], outside [0, {self.num_nodes})")
         self.perm = torch.sort(dst, stable=True).indices
         src_s, dst_s = src[self.perm], dst[self.perm]
         self.src = src_s.int().contiguous()
@@ -219,8 +233,36 @@ def wigner_floats(lmax, mmax):
     return sum((l + 1) * ((2 * (1 + 2 * min(mmax, l)) + 3) // 4 * 4) for l in range(lmax + 1))
 
 
+def _wigner_rows(wigner, plan, lmax, mmax):
+    """Kept Wigner rows [E, wigner_floats] in the plan's dst-sorted order from a
+    dense wigner [E, d, d] in the original edge order (maloq_message_wigner_rows)."""
+    E, d = plan.num_edges, (lmax + 1) ** 2
+    if tuple(wigner.shape) != (E, d, d):
+        raise ValueError(f"wigner must be [E, {d}, {d}], got {tuple(wigner.shape)}")
+    _lib.require_cuda(wigner)
+    w = wigner.float().contiguous()
+    dk = torch.empty(max(E, 1), wigner_floats(lmax, mmax), device=w.device, dtype=torch.float32)
+    _lib.call("maloq_message_wigner_rows", lmax, mmax, _lib.ptr(w), _lib.ptr(plan.perm), E, _lib.ptr(dk),
+              _lib.stream_of(w.device))
+    return dk
+
+
+def _edge_frames(eulers, wigner, plan, lmax, mmax, dev):
+    """(eulers or None, dk workspace): from the Euler triples (dst-sorted; the
+    prep kernel builds the rows) or from a dense wigner (original order)."""
+    if (eulers is None) == (wigner is None):
+        raise ValueError("give exactly one of eulers and wigner")
+    if wigner is not None:
+        return None, _wigner_rows(wigner, plan, lmax, mmax)
+    E = plan.num_edges
+    if tuple(eulers.shape) != (E, 3):
+        raise ValueError("eulers must be [E, 3] (dst-sorted)")
+    dk = torch.empty(max(E, 1), wigner_floats(lmax, mmax), device=dev, dtype=torch.float32)
+    return eulers.float().contiguous(), dk
+
+
 def message_forward(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=False, wpack=None,
-                    save=None):
+                    save=None, wigner=None):
     """Node output [N, d, c_out] fp32 of the fused block (no autograd).
 
     ``save``: dict that receives the workspaces kept for the backward
@@ -231,6 +273,8 @@ def message_forward(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=False, wp
     if dt not in DTYPE_CODE:
         raise ValueError(f"unsupported dtype {dt}")
     _lib.require_cuda(x, eulers, w0)
+    if not _lib.load().maloq_message_supported(lmax, mmax):
+        raise ValueError(f"no message kernels for lmax={lmax}, mmax={mmax}")
     N, d, c_in = x.shape
     assert d == (lmax + 1) ** 2, "x must be [N, (lmax+1)^2, C]"
     n0 = w0.shape[0]
@@ -249,12 +293,11 @@ def message_forward(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=False, wp
     y = _edge_rows(E, kept_rows(lmax, mmax), c_in, dev, dt)
     r = torch.empty(max(E, 1), kept_rows(lmax, mmax), c_in, device=dev, dtype=dt) \
         if (save is not None and rad is not None) else None
-    dk = torch.empty(max(E, 1), wigner_floats(lmax, mmax), device=dev, dtype=torch.float32)
+    eul, dk = _edge_frames(eulers, wigner, plan, lmax, mmax, dev)
     gws = torch.empty(max(E, 1), kept_rows(lmax, mmax) + lmax, c_out, device=dev, dtype=dt) \
         if (save is not None and gate) else None
     bias = b0.float().contiguous() if b0 is not None else None
     xc = x.contiguous()
-    eul = eulers.float().contiguous()
     _lib.call("maloq_message_fwd", DTYPE_CODE[dt], lmax, mmax, int(gate), _lib.ptr(xc), c_in,
               _lib.ptr(plan.src), _lib.ptr(plan.dst), E, _lib.ptr(eul), _lib.ptr(rad),
               _lib.ptr(wpack), _lib.ptr(bias), _lib.ptr(_jd_dev(lmax, dev)), _lib.ptr(out),
@@ -266,7 +309,7 @@ def message_forward(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=False, wp
 
 
 def edgewise_forward(x, plan, eulers, rad, conv1, conv2, lmax, mmax, wpack1=None, wpack2=None,
-                     save=None, node_or_edge="node", x_message_edge=None):
+                     save=None, node_or_edge="node", x_message_edge=None, wigner=None):
     """Node output [N, d, c_out] fp32 of the two-convolution block
     ``Edgewise.forward_node`` with message_type "source-target"
     (esen_block.py:146-208; maloq_message_edgewise_fwd), forward only.
@@ -291,6 +334,8 @@ def edgewise_forward(x, plan, eulers, rad, conv1, conv2, lmax, mmax, wpack1=None
     if dt not in DTYPE_CODE:
         raise ValueError(f"unsupported dtype {dt}")
     _lib.require_cuda(x, eulers, conv1[0], conv2[0])
+    if not _lib.load().maloq_message_supported(lmax, mmax):
+        raise ValueError(f"no message kernels for lmax={lmax}, mmax={mmax}")
     N, d, c_x = x.shape
     assert d == (lmax + 1) ** 2, "x must be [N, (lmax+1)^2, C]"
     c_hidden = conv1[0].shape[0] // (2 * lmax + 1)
@@ -330,12 +375,11 @@ def edgewise_forward(x, plan, eulers, rad, conv1, conv2, lmax, mmax, wpack1=None
         z = torch.empty(max(E, 1), kr, c_hidden, device=dev, dtype=dt)
     r = torch.empty(max(E, 1), kr, npart * c_x, device=dev, dtype=dt) \
         if (save is not None and rad is not None) else None
-    dk = torch.empty(max(E, 1), wigner_floats(lmax, mmax), device=dev, dtype=torch.float32)
+    eul, dk = _edge_frames(eulers, wigner, plan, lmax, mmax, dev)
     gws = torch.empty(max(E, 1), kr + lmax, c_hidden, device=dev, dtype=dt) if save is not None else None
     b1 = conv1[1].float().contiguous() if conv1[1] is not None else None
     b2 = conv2[1].float().contiguous() if conv2[1] is not None else None
     xc = x.contiguous()
-    eul = eulers.float().contiguous()
     mrow = plan.perm.int().contiguous() if xm is not None else None   # x_message_edge row per position
     _lib.call("maloq_message_edgewise_fwd", DTYPE_CODE[dt], lmax, mmax, _lib.ptr(xc), c_x,
               _lib.ptr(plan.src), _lib.ptr(plan.dst), _lib.ptr(seg_id), E, _lib.ptr(eul), _lib.ptr(rad),
@@ -374,12 +418,12 @@ def edgewise_backward_dx(grad_out, x_shape, dt, plan, saved, rad, conv1, conv2, 
     if node_or_edge == "edge":
         g = g[plan.perm].contiguous()       # per-edge gradient rows in dst-sorted order
         grad_row = torch.arange(E, device=dev, dtype=torch.int32)
-    gxs = torch.empty(N, d, parts * c_x, device=dev, dtype=torch.float32)
-    gxd = torch.empty(N, d, parts * c_x, device=dev, dtype=torch.float32)
-    gxm = torch.empty(max(E, 1), d, parts * c_x, device=dev, dtype=torch.float32) if parts == 3 else None
+    gxs = torch.empty(N, d, c_x, device=dev, dtype=torch.float32)
+    gxd = torch.empty(N, d, c_x, device=dev, dtype=torch.float32)
+    gxm = torch.empty(max(E, 1), d, c_x, device=dev, dtype=torch.float32) if parts == 3 else None
     edge_seg = torch.arange(E, device=dev, dtype=torch.int32) if parts == 3 else None
     lib = _lib.load()
-    pbuf = torch.empty(max(1, lib.maloq_message_partials_floats(lmax, 1, E, parts * c_x)), device=dev,
+    pbuf = torch.empty(max(1, lib.maloq_message_partials_floats(lmax, 1, E, c_x)), device=dev,
                        dtype=torch.float32)
     grad_rad = None
     if rad is not None:
@@ -394,11 +438,11 @@ def edgewise_backward_dx(grad_out, x_shape, dt, plan, saved, rad, conv1, conv2, 
               c_hidden, _lib.ptr(wp2t), _lib.ptr(_jd_dev(lmax, dev)), _lib.ptr(gxs), _lib.ptr(gxd), N,
               _lib.ptr(plan.seg_ptr), _lib.ptr(plan.seg_ptr_src), _lib.ptr(pbuf), _lib.ptr(dz2),
               _lib.ptr(dz1), _lib.ptr(edge_seg), _lib.ptr(gxm), _lib.stream_of(dev))
-    gx = gxs[:, :, :c_x] + gxd[:, :, c_x:2 * c_x]
+    gx = gxs.add_(gxd)
     if parts == 2:
         return gx, grad_rad, dz2, dz1
     gm = torch.empty(E, d, c_x, device=dev, dtype=torch.float32)
-    gm[plan.perm] = gxm[:E, :, 2 * c_x:]      # dst-sorted position p holds original edge perm[p]
+    gm[plan.perm] = gxm[:E]      # dst-sorted position p holds original edge perm[p]
     return gx, grad_rad, dz2, dz1, gm
 
 
@@ -407,7 +451,7 @@ class _EdgewiseFn(torch.autograd.Function):
     convolutions' weights and biases."""
 
     @staticmethod
-    def forward(ctx, x, rad, w01, b01, w02, b02, xm, plan, eulers, lmax, mmax, node_or_edge, *wm):
+    def forward(ctx, x, rad, w01, b01, w02, b02, xm, plan, frames, lmax, mmax, node_or_edge, *wm):
         saved = {}
         wm1, wm2 = list(wm[:mmax]), list(wm[mmax:])
         npart = 2 if xm is None else 3
@@ -419,8 +463,8 @@ class _EdgewiseFn(torch.autograd.Function):
         p2 = pack_weights(w02, wm2, lmax, mmax, False, c_hidden, c_x, x.dtype, mode)
         (wp1, wp1t), (wp2, wp2t) = (p1, p2) if mode == "both" else ((p1, None), (p2, None))
         ctx.wpack_t = (wp1t, wp2t)
-        out = edgewise_forward(x, plan, eulers, rad, (w01, b01, wm1), (w02, b02, wm2), lmax, mmax, wpack1=wp1,
-                               wpack2=wp2, save=saved, node_or_edge=node_or_edge, x_message_edge=xm)
+        out = edgewise_forward(x, plan, frames[0], rad, (w01, b01, wm1), (w02, b02, wm2), lmax, mmax, wpack1=wp1,
+                               wpack2=wp2, save=saved, node_or_edge=node_or_edge, x_message_edge=xm, wigner=frames[1])
         ctx.plan, ctx.lmax, ctx.mmax, ctx.mode = plan, lmax, mmax, node_or_edge
         ctx.parts, ctx.xm_dtype = (2, None) if xm is None else (3, xm.dtype)
         ctx.x_shape, ctx.dt = tuple(x.shape), x.dtype
@@ -469,10 +513,12 @@ class _EdgewiseFn(torch.autograd.Function):
                 gxm, None, None, None, None, None, *dwm1, *dwm2)
 
 
-def edgewise_block(x, plan, eulers, rad, conv1, conv2, lmax, mmax, node_or_edge="node", x_message_edge=None):
+def edgewise_block(x, plan, eulers, rad, conv1, conv2, lmax, mmax, node_or_edge="node", x_message_edge=None,
+                   wigner=None):
     """Differentiable :func:`edgewise_forward` (gradients for x, rad,
     x_message_edge and the weights and biases of both convolutions)."""
-    return _EdgewiseFn.apply(x, rad, conv1[0], conv1[1], conv2[0], conv2[1], x_message_edge, plan, eulers, lmax, mmax,
+    return _EdgewiseFn.apply(x, rad, conv1[0], conv1[1], conv2[0], conv2[1], x_message_edge, plan, (eulers, wigner),
+                             lmax, mmax,
                              node_or_edge, *conv1[2][:mmax], *conv2[2][:mmax])
 
 
@@ -538,10 +584,9 @@ def message_weight_grad(dz, y, lmax, mmax, c_out, c_in, splits=None, num_edges=N
     dw0 = torch.empty(extra + (lmax + 1) * c_out, (lmax + 1) * c_in, device=dz.device, dtype=torch.float32)
     dwm = [torch.empty(2 * (lmax - m + 1) * c_out, (lmax - m + 1) * c_in, device=dz.device,
                        dtype=torch.float32) for m in range(1, mmax + 1)]
-    ptrs = [_lib.ptr(w) for w in dwm] + [None] * (3 - len(dwm))
+    ptrs = (ctypes.c_void_p * max(1, mmax))(*[_lib.ptr(w) for w in dwm])
     _lib.call("maloq_message_dw", DTYPE_CODE[dz.dtype], lmax, mmax, int(gate), _lib.ptr(dz), _lib.ptr(y), E,
-              c_out, c_in, splits, _lib.ptr(parts), _lib.ptr(dw0), ptrs[0], ptrs[1], ptrs[2],
-              _lib.stream_of(dz.device))
+              c_out, c_in, splits, _lib.ptr(parts), _lib.ptr(dw0), ptrs, _lib.stream_of(dz.device))
     db0 = torch.empty(extra + (lmax + 1) * c_out, device=dz.device, dtype=torch.float32)
     rpe = dz.shape[1]
     groups = [(0, lmax + 1, extra)] + ([(kept_rows(lmax, mmax), lmax, 0)] if gate else [])
@@ -557,7 +602,7 @@ class _MessageBlockFn(torch.autograd.Function):
     """Autograd wrapper: gradients for x, rad, W0, b0, W_m (gated or not)."""
 
     @staticmethod
-    def forward(ctx, x, rad, w0, b0, plan, eulers, lmax, mmax, gate, *wm):
+    def forward(ctx, x, rad, w0, b0, plan, frames, lmax, mmax, gate, *wm):
         saved = {}
         # both packings from one launch when a backward will run: the transposed
         # one is kept for it
@@ -566,7 +611,8 @@ class _MessageBlockFn(torch.autograd.Function):
             wp, ctx.wpack_t = pack_weights(w0, wm, lmax, mmax, gate, x.shape[2], c_out, x.dtype, "both")
         else:
             wp, ctx.wpack_t = pack_weights(w0, wm, lmax, mmax, gate, x.shape[2], c_out, x.dtype, 0), None
-        out = message_forward(x, plan, eulers, rad, w0, b0, list(wm), lmax, mmax, gate=gate, wpack=wp, save=saved)
+        out = message_forward(x, plan, frames[0], rad, w0, b0, list(wm), lmax, mmax, gate=gate, wpack=wp, save=saved,
+                              wigner=frames[1])
         ctx.plan, ctx.lmax, ctx.mmax, ctx.gate, ctx.has_b0 = plan, lmax, mmax, gate, b0 is not None
         ctx.x_shape, ctx.dt = tuple(x.shape), x.dtype
         ctx.has_r = saved["r"] is not None
@@ -600,7 +646,7 @@ class _MessageBlockFn(torch.autograd.Function):
                 None, None, None, *dwm)
 
 
-def message_block(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=False):
+def message_block(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=False, wigner=None):
     """Differentiable fused block (gated with GateActivation, activation.py:12-77,
     when ``gate``: w0 and b0 then carry the lmax c_out gate rows first)."""
-    return _MessageBlockFn.apply(x, rad, w0, b0, plan, eulers, lmax, mmax, bool(gate), *wm[:mmax])
+    return _MessageBlockFn.apply(x, rad, w0, b0, plan, (eulers, wigner), lmax, mmax, bool(gate), *wm[:mmax])

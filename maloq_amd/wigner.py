@@ -33,10 +33,12 @@ def _packed_jd(Jd, lmax: int, device) -> torch.Tensor:
         return _JD_CACHE[key]
     if len(Jd) <= lmax:
         raise ValueError(f"Jd has {len(Jd)} entries, need {lmax + 1}")
-    key = ("list", lmax, str(device), tuple(int(j.data_ptr()) if torch.is_tensor(j) else id(j) for j in Jd[: lmax + 1]))
+    # keyed by content: the J_l are tiny, and a content key cannot be fooled by
+    # a freed list whose storage is reused at the same addresses
+    mats = [np.asarray(j.detach().cpu().double() if torch.is_tensor(j) else j, dtype=np.float64) for j in Jd[: lmax + 1]]
+    key = ("list", lmax, str(device), b"".join(np.ascontiguousarray(m).tobytes() for m in mats))
     hit = _JD_CACHE.get(key)
     if hit is None:
-        mats = [np.asarray(j.detach().cpu().double() if torch.is_tensor(j) else j, dtype=np.float64) for j in Jd[: lmax + 1]]
         hit = torch.from_numpy(pack_jd(mats, lmax)).to(device)
         if len(_JD_CACHE) > 64:
             _JD_CACHE.clear()

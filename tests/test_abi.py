@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     missing = [s for s in declared_symbols() if not hasattr(lib, s)]
     assert not missing, missing
     lib.maloq_abi_version.restype = ctypes.c_int
-    assert lib.maloq_abi_version() == 1
+    assert lib.maloq_abi_version() == 2
 
 
 def test_ctypes_signatures_cover_header():
@@ -40,3 +40,17 @@ def test_error_path_without_gpu():
     from maloq_amd import _lib
     with pytest.raises(_lib.MaloqHipError, match="lmax must be 0-8"):
         _lib.call("maloq_wigner_from_euler", None, 0, 9, None, None, None, 1, None)
+
+
+def test_supported_shapes_and_rotate_validation_without_gpu():
+    """Shape queries and the rotation's argument checks run on the host."""
+    from maloq_amd import _lib
+    lib = _lib.load()
+    built = {(l, m) for l in range(9) for m in range(l + 1) if lib.maloq_message_supported(l, m)}
+    assert built == {(2, 2), (4, 2), (4, 4), (6, 2), (6, 6)}
+    with pytest.raises(_lib.MaloqHipError, match="lmax must be 0-8"):
+        _lib.call("maloq_rotate", 0, 0, 9, None, 4, None, 1, None, None, None, 0, None, None)
+    with pytest.raises(_lib.MaloqHipError, match="multiple of 4"):
+        _lib.call("maloq_rotate", 0, 0, 2, None, 6, None, 1, None, None, None, 0, None, None)
+    with pytest.raises(_lib.MaloqHipError, match="no message kernels"):
+        _lib.call("maloq_message_wigner_rows", 4, 3, None, None, 1, None, None)

@@ -428,3 +428,49 @@ def test_so2_convolution_brute_force():
             row += 2 * ms
             off_r += ms * C
     assert torch.allclose(got, ref, atol=1e-12)
+
+
+# ------------------------------------------------------------------- gate
+def _m_major_degrees(lmax, mmax):
+    """Degree l of every m-major row, from the ordering rule alone
+    (so3.py:52-64): m = 0 rows l = 0..L, then for m = 1..M the +m rows
+    l = m..L followed by the -m rows l = m..L."""
+    ls = list(range(lmax + 1))
+    for m in range(1, mmax + 1):
+        ls += list(range(m, lmax + 1)) * 2
+    return ls
+
+
+@pytest.mark.parametrize("lmax,mmax", [(1, 1), (2, 2), (4, 2), (4, 4), (6, 2), (6, 6)])
+def test_gate_expand_index_closed_form(lmax, mmax):
+    """GateActivation(outer_dim='m') (activation.py:39-47, fed by
+    esen_block.py:66-75): the m-major row r >= 1 takes tanh(g[l(r) - 1])."""
+    want = torch.tensor(_m_major_degrees(lmax, mmax)[1:]) - 1
+    got = oso2.gate_expand_index(OMapping(lmax, mmax))
+    assert torch.equal(got, want)
+    # the product's kept-row count agrees with the same rule
+    assert [l for l, _ in pso3.kept_rows(lmax, mmax)] == _m_major_degrees(lmax, mmax)
+
+
+def test_gate_activation_brute_force():
+    """Per-element loops of activation.py:57-77 against the vectorised oracle:
+    SiLU on row 0, row r >= 1 times tanh of the gate of its own degree."""
+    lmax, mmax, H, E = 4, 2, 3, 5
+    g = torch.Generator().manual_seed(3)
+    rows = _m_major_degrees(lmax, mmax)
+    x = torch.randn(E, len(rows), H, generator=g)
+    gate = torch.randn(E, lmax * H, generator=g)
+    got = oso2.gate_activation_m(gate, x, oso2.gate_expand_index(OMapping(lmax, mmax)), lmax)
+    ref = torch.empty_like(x)
+    for e in range(E):
+        for c in range(H):
+            z = x[e, 0, c]
+            ref[e, 0, c] = z / (1 + math.exp(-z))
+            for r in range(1, len(rows)):
+                ref[e, r, c] = x[e, r, c] * math.tanh(gate[e, (rows[r] - 1) * H + c])
+    assert torch.allclose(got, ref, atol=1e-12)
+    # a plausible slip, gating row r by the gate of its m instead of its l, fails
+    bad = x.clone()
+    for r in range(1, len(rows)):
+        bad[:, r] = x[:, r] * torch.tanh(gate[:, (min(r, lmax) - 1) * H:(min(r, lmax)) * H])
+    assert not torch.allclose(got[:, 1:], bad[:, 1:], atol=1e-6)

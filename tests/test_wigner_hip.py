@@ -4,8 +4,9 @@ Mirrors every case of the reference's tests/test_wigner_backend.py (per-L
 blocks at the extracted angles, both-path checks, seed determinism, edge
 cases) and adds oracle parity in fp64, the edge-frame alignment and the
 config-2 size.  Tolerances: D entries are O(1); fp32 kernels agree with the
-fp64 oracle evaluated at the same angles within 1e-5 absolute for l <= 4 and
-5e-5 for l <= 8 (frequency l amplifies the fp32 angle rounding).
+fp64 oracle evaluated at the same angles within 1e-5 absolute for l <= 6 and
+3e-5 for l = 7, 8 (the trigonometry is evaluated in fp64 from the fp32 angles;
+the fp32 products of the J recurrence grow with the block size).
 """
 import numpy as np
 import pytest
@@ -38,7 +39,7 @@ def _vecs(n, device, seed=42):
 
 
 def _tol(l):
-    return 1e-5 if l <= 4 else 5e-5
+    return 1e-5 if l <= 6 else 3e-5
 
 
 class TestNumericalCorrectness:
@@ -54,6 +55,7 @@ class TestNumericalCorrectness:
             sz = 2 * l + 1
             ref = orot.wigner_D(l, e[:, 0], e[:, 1], e[:, 2], jd64)
             err = (w[:, start:start + sz, start:start + sz] - ref).abs().max().item()
+            print(f"L={l} lmax={lmax} n={num_edges} err={err:.2e}")
             assert err < _tol(l), f"L={l} lmax={lmax} n={num_edges} err={err}"
             start += sz
         # off-diagonal blocks are exactly zero
