@@ -222,6 +222,28 @@ int maloq_message_fwd(int dtype, int lmax, int mmax, int gate, const void* x, in
                       const int64_t* seg_ptr, float* partials, void* y_ws, void* r_ws,
                       float* dk_ws, void* gate_ws, void* stream);
 
+/* Bytes of the device array behind maloq_message_fwd_noalloc (per GPU). */
+#define MALOQ_NOALLOC_SCRATCH_BYTES (64ll << 20)
+
+/* maloq_message_fwd without allocation: no counterpart in the reference; for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments and
+ * result as maloq_message_fwd minus its workspaces (partials, y_ws, r_ws,
+ * dk_ws, gate_ws), which come from one file-scope device array of
+ * MALOQ_NOALLOC_SCRATCH_BYTES per GPU; eulers must be given (no dense-wigner
+ * rows).  The workspace is partials + E d' c_in s + E WS 4 bytes, each part
+ * rounded up to 256 (d' = maloq_message_kept_rows, WS =
+ * maloq_message_wigner_floats, s = 2 for bf16, 4 for fp32); a call that needs
+ * more is refused with an error (about 10 k edges at lmax 4, mmax 2, C 128,
+ * bf16).  Nothing is saved for a backward.  Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU (other streams, other threads)
+ * race and must be serialised by the caller. */
+int maloq_message_fwd_noalloc(int dtype, int lmax, int mmax, int gate, const void* x, int c_in,
+                              const int32_t* src, const int32_t* dst, int64_t num_edges,
+                              const float* eulers, const void* rad, const void* wpack, const float* bias,
+                              const float* jd, float* out, int64_t num_nodes, int c_out,
+                              const int64_t* seg_ptr, void* stream);
+
 /* Two-convolution message block (forward, node output), as Edgewise.forward_node
  * with message_type "source-target" (helm/esen_block.py:146-208, convolutions
  * :85-106): per dst-sorted edge e, m_e = cat(x[src[e]], x[dst[e]]) (2 c_x channels),

@@ -50,6 +50,8 @@ SIGNATURES = {
     "maloq_message_dw_partials_floats": [_i32, _i32, _i32, _i32, _i32, _i32],
     "maloq_message_dw": [_i32, _i32, _i32, _i32, _p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p],
     "maloq_message_supported": [_i32, _i32],
+    "maloq_message_fwd_noalloc": [_i32, _i32, _i32, _i32, _p, _i32, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i64,
+                                  _i32, _p, _p],
     "maloq_message_wigner_rows": [_i32, _i32, _p, _p, _i64, _p, _p],
     "maloq_message_pack": [_i32, _i32, _p, _p, _p, _i64, _p, _p],
     "maloq_message_colsum_partials_floats": [_i32, _i32, _i64],

@@ -1,6 +1,8 @@
 // C ABI of the fused message block (forward and input gradient) and the
 // partial-segment fixup.  The kernels themselves are in message_impl.h and
 // are instantiated per lmax in message_l{2,4,6}.hip.
+#include <mutex>
+
 #include "message_launch.h"
 #include "../../include/maloq_hip.h"
 
@@ -173,6 +175,65 @@ extern "C" int maloq_message_fwd(int dtype, int lmax, int mmax, int gate, const 
     if (rc) return rc;
   }
   return fixup(seg_ptr, num_nodes, partials, out, d * c_out, tile_edges(lmax, mmax, gate), s);
+}
+
+// ------------------------------------------------- forward without allocation
+// Workspace of maloq_message_fwd_noalloc: one file-scope device array per GPU
+// (each device that loads the library holds its own copy until the process
+// ends).  In host code the name `scratch` is only a stand-in symbol; its device
+// address is looked up once per device with hipGetSymbolAddress and only that
+// address is ever passed to a kernel.
+static __device__ __align__(256) unsigned char scratch[MALOQ_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_ptr(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  MALOQ_REQUIRE(e == hipSuccess, "hipGetDevice: %s", hipGetErrorString(e));
+  MALOQ_REQUIRE(dev >= 0 && dev < kMaxDevices, "device id %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    MALOQ_REQUIRE(e == hipSuccess && p != nullptr, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MALOQ_OK;
+}
+
+int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
+}  // namespace
+
+extern "C" int maloq_message_fwd_noalloc(int dtype, int lmax, int mmax, int gate, const void* x, int c_in,
+                                         const int32_t* src, const int32_t* dst, int64_t num_edges,
+                                         const float* eulers, const void* rad, const void* wpack,
+                                         const float* bias, const float* jd, float* out, int64_t num_nodes,
+                                         int c_out, const int64_t* seg_ptr, void* stream) {
+  int rc = check_common(dtype, lmax, mmax, c_in, c_out, num_edges);
+  if (rc) return rc;
+  MALOQ_REQUIRE(maloq_message_supported(lmax, mmax), "no message kernels for lmax %d, mmax %d", lmax, mmax);
+  MALOQ_REQUIRE(eulers != nullptr || num_edges == 0, "the no-allocation forward builds D from eulers");
+  // workspace layout: partials | rotated rows y [E, d', c_in] | kept Wigner rows [E, WS]
+  const int64_t part_b = align256(maloq_message_partials_floats(lmax, gate, num_edges, c_out) * 4);
+  const int64_t y_b = align256(num_edges * kept_rows(lmax, mmax) * c_in * (dtype == 1 ? 2 : 4));
+  const int64_t dk_b = align256(num_edges * wigner_floats(lmax, mmax) * 4);
+  const int64_t need = part_b + y_b + dk_b;
+  MALOQ_REQUIRE(need <= static_cast<int64_t>(MALOQ_NOALLOC_SCRATCH_BYTES),
+                "maloq_message_fwd_noalloc: %lld edges need %lld bytes of workspace, the scratch array holds %lld",
+                static_cast<long long>(num_edges), static_cast<long long>(need),
+                static_cast<long long>(MALOQ_NOALLOC_SCRATCH_BYTES));
+  void* base = nullptr;
+  rc = scratch_ptr(&base);
+  if (rc) return rc;
+  char* b = static_cast<char*>(base);
+  return maloq_message_fwd(dtype, lmax, mmax, gate, x, c_in, src, dst, num_edges, eulers, rad, wpack, bias, jd, out,
+                           num_nodes, c_out, seg_ptr, reinterpret_cast<float*>(b), b + part_b, nullptr,
+                           reinterpret_cast<float*>(b + part_b + y_b), nullptr, stream);
 }
 
 extern "C" int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const void* x, int c_x,
