@@ -6,14 +6,20 @@ atoms, ~30k directed edges, lmax 4, mmax 2, 128 channels, 8 Gaussian RBFs).
 A step is one fused message block, forward and backward, with inputs already
 resident in HBM: per-edge Euler angles + Wigner-D, the radial MLP (fused HIP), the
 fused rotate -> SO(2) -> inverse-rotate -> segment-sum kernel, and its input,
-radial and weight gradients.  `value` is edges per second.
+radial and weight gradients.  `value` is edges per second, in fp32 by default
+(the reference's path computes in fp32, esen_osh.py:277-281).
 
 The JSON line also carries the roofline of the dominant kernel (the fused
 forward launch, MFMA-bound), the CPU baseline (the build's own CPU
-restatement of the reference's PyTorch path, timed on a bounded sample) and
-the basis-transform throughput (config 3, H-blocks/s) with its HBM roofline.
+restatement of the reference's PyTorch path, timed on a bounded sample), and
+one object per other configuration of the benchmark, each with its own
+throughput, roofline and CPU baseline: config 2 in the other precision,
+config 1 (rotation round trip, HBM-bound), configs 4 and 5 (fused block,
+bf16), config 3 and config 5's basis transforms (H-blocks/s, with and without
+the per-structure row plan), the edge-degree embedding and the
+two-convolution Edgewise block.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--dtype bf16|fp32]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--dtype fp32|bf16]
 """
 from __future__ import annotations
 
@@ -49,17 +55,32 @@ def gaussian_rbf(dist, start, stop, num):
     return torch.exp(coeff * (dist.view(-1, 1) - offset.view(1, -1)) ** 2)
 
 
-def message_workload(dtype_name, seed=0):
-    """Tensors of config 2 on cuda:0."""
+# message-block legs: (graph loader, lmax, mmax, channels, gated, RBF cutoff)
+MESSAGE_CONFIGS = {
+    "config2": ("config2_graph", 4, 2, 128, False, 6.0),
+    "config4": ("config4_graph", 6, 2, 128, True, 8.0),
+    "config5": ("config5_graph", 4, 2, 256, False, 6.0),
+}
+_GRAPHS: dict = {}
+
+
+def _graph(name):
+    from maloq_amd import synth
+    if name not in _GRAPHS:
+        _GRAPHS[name] = getattr(synth, name)()
+    return _GRAPHS[name]
+
+
+def message_workload(dtype_name, seed=0, cfg="config2"):
+    """Tensors of a message-block configuration on cuda:0 (default config 2)."""
     import numpy as np
     import torch
     from maloq_amd import message as M
-    from maloq_amd import synth
 
     dev = torch.device("cuda:0")
     dt = {"bf16": torch.bfloat16, "fp32": torch.float32}[dtype_name]
-    g = synth.config2_graph()
-    L, Mm, C = 4, 2, 128
+    gname, L, Mm, C, gate, cutoff = MESSAGE_CONFIGS[cfg]
+    g = _graph(gname)
     gen = torch.Generator().manual_seed(seed)
     N, E = g.num_nodes, g.num_edges
     plan = M.MessagePlan(torch.from_numpy(np.stack([g.src, g.dst])).to(dev), N)
@@ -67,8 +88,9 @@ def message_workload(dtype_name, seed=0):
     dist = vec.norm(dim=1)
     x = torch.randn(N, (L + 1) ** 2, C, generator=gen).to(device=dev, dtype=dt).requires_grad_()
     k0 = (L + 1) * C
-    w0 = (torch.randn((L + 1) * C, k0, generator=gen) / math.sqrt(k0)).to(dev).requires_grad_()
-    b0 = torch.zeros((L + 1) * C, device=dev, requires_grad=True)
+    extra = L * C if gate else 0
+    w0 = (torch.randn((L + 1) * C + extra, k0, generator=gen) / math.sqrt(k0)).to(dev).requires_grad_()
+    b0 = torch.zeros((L + 1) * C + extra, device=dev, requires_grad=True)
     wm = []
     for m in range(1, Mm + 1):
         k = (L - m + 1) * C
@@ -77,15 +99,15 @@ def message_workload(dtype_name, seed=0):
     radial = make_radial(8, 64, M.rad_width(L, Mm, C), dev)
     gout = torch.randn(N, (L + 1) ** 2, C, generator=gen).to(dev)
     return dict(graph=g, plan=plan, vec=vec, dist=dist, x=x, w0=w0, b0=b0, wm=wm, radial=radial,
-                gout=gout, L=L, M=Mm, C=C, dt=dt, N=N, E=E)
+                gout=gout, L=L, M=Mm, C=C, dt=dt, N=N, E=E, gate=gate, cutoff=cutoff, cfg=cfg)
 
 
 def message_step(w, backward=True):
     from maloq_amd import message as M
     from maloq_amd.wigner import extract_euler_angles
     eul = extract_euler_angles(w["vec"], seed=1234)
-    rad = w["radial"](gaussian_rbf(w["dist"], 0.0, 6.0, 8), out_dtype=w["dt"])
-    out = M.message_block(w["x"], w["plan"], eul, rad, w["w0"], w["b0"], w["wm"], w["L"], w["M"])
+    rad = w["radial"](gaussian_rbf(w["dist"], 0.0, w["cutoff"], 8), out_dtype=w["dt"])
+    out = M.message_block(w["x"], w["plan"], eul, rad, w["w0"], w["b0"], w["wm"], w["L"], w["M"], gate=w["gate"])
     if backward:
         # a training step starts from cleared gradients (zero_grad(set_to_none=True))
         for t in [w["x"], w["w0"], w["b0"], *w["wm"], *w["radial"].parameters()]:
@@ -128,12 +150,17 @@ def fused_forward_launch_time(w, reps=20):
     from maloq_amd.wigner import extract_euler_angles
     with torch.no_grad():
         eul = extract_euler_angles(w["vec"], seed=1234)
-        rad = w["radial"](gaussian_rbf(w["dist"], 0.0, 6.0, 8), out_dtype=w["dt"])
+        rad = w["radial"](gaussian_rbf(w["dist"], 0.0, w["cutoff"], 8), out_dtype=w["dt"])
         x = w["x"].detach()
-        wpack = M.pack_weights(w["w0"], w["wm"], w["L"], w["M"], False, w["C"], w["C"], w["dt"], 0)
+        wpack = M.pack_weights(w["w0"], w["wm"], w["L"], w["M"], w["gate"], w["C"], w["C"], w["dt"], 0)
         f = lambda: M.message_forward(x, w["plan"], eul, rad, w["w0"], w["b0"], w["wm"], w["L"], w["M"],
-                                      wpack=wpack)
+                                      gate=w["gate"], wpack=wpack)
         return kernel_time_events(f, reps)
+
+
+def gated_flops_extra(L, c_in, c_out):
+    """FLOPs per edge of the gate rows (L c_out extra m = 0 outputs) and the gate itself."""
+    return 2 * (L + 1) * c_in * L * c_out + ((L + 1) ** 2 - 1) * c_out
 
 
 # ---------------------------------------------------------- basis transform
@@ -206,26 +233,30 @@ def basis_timing(bw, reps=50):
 
 
 # ---------------------------------------------------------------- CPU legs
-def cpu_message_baseline(budget_s=15.0):
-    """The build's CPU restatement of the reference path (bmm(wigner), einsum
-    to_m, SO2_Convolution, einsum, bmm(wigner_inv), index_add_), fp32 torch on
-    the host cores, forward + backward, on the first molecules of config 2."""
+def cpu_message_baseline(budget_s=15.0, cfg="config2"):
+    """The build's CPU restatement of the reference path (RadialMLP,
+    bmm(wigner), einsum to_m, SO2_Convolution [+ GateActivation], einsum,
+    bmm(wigner_inv), index_add_), fp32 torch on the host cores, forward +
+    backward, on the in-edges of the first nodes of the configuration (whole
+    molecules for configs 2 and 4), sized to about ``budget_s`` of CPU work."""
     import numpy as np
     import torch
     from oracle import message as omsg
     from oracle import rotation as orot
-    from maloq_amd import synth
+    from maloq_amd import message as M
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    g = synth.config2_graph()
-    L, Mm, C = 4, 2, 128
+    gname, L, Mm, C, gate, cutoff = MESSAGE_CONFIGS[cfg]
+    g = _graph(gname)
     gen = torch.Generator().manual_seed(0)
     Jd = orot.load_jd(torch.float32)
-    conv = {"w0": torch.randn(5 * C, 5 * C, generator=gen) / math.sqrt(5 * C),
-            "b0": torch.zeros(5 * C),
+    k0 = (L + 1) * C
+    extra = L * C if gate else 0
+    conv = {"w0": torch.randn(k0 + extra, k0, generator=gen) / math.sqrt(k0),
+            "b0": torch.zeros(k0 + extra),
             "wm": [torch.randn(2 * (L - m + 1) * C, (L - m + 1) * C, generator=gen) / math.sqrt((L - m + 1) * C)
-                   for m in (1, 2)], "c_out": C}
+                   for m in range(1, Mm + 1)], "c_out": C}
     for k in ("w0", "b0"):
         conv[k].requires_grad_()
     for wmm in conv["wm"]:
@@ -234,31 +265,33 @@ def cpu_message_baseline(budget_s=15.0):
     torch.manual_seed(0)
     radial = torch.nn.Sequential(torch.nn.Linear(8, 64), torch.nn.LayerNorm(64), torch.nn.SiLU(),
                                  torch.nn.Linear(64, 64), torch.nn.LayerNorm(64), torch.nn.SiLU(),
-                                 torch.nn.Linear(64, 1536))
+                                 torch.nn.Linear(64, M.rad_width(L, Mm, C)))
+    x_all = torch.randn(g.num_nodes, (L + 1) ** 2, C, generator=gen)
+    # node counts: whole molecules where the graph has them
+    unit = int(np.sum(g.mol == 0)) if g.mol.max() > 0 else 10
 
-    def run(nmol):
-        sel = np.isin(g.mol[g.dst], np.arange(nmol))
-        nodes = np.nonzero(np.isin(g.mol, np.arange(nmol)))[0]
+    def run(n_nodes):
+        sel = g.dst < n_nodes
         ei = torch.from_numpy(np.stack([g.src[sel], g.dst[sel]]))
         vec = torch.from_numpy(g.edge_distance_vec()[sel]).float()
-        x = torch.randn(len(nodes), 25, C, generator=gen).requires_grad_()
+        x = x_all.clone().requires_grad_()
         t0 = time.perf_counter()
-        rad = radial(gaussian_rbf(vec.norm(dim=1), 0.0, 6.0, 8))
+        rad = radial(gaussian_rbf(vec.norm(dim=1), 0.0, cutoff, 8))
         eul = orot.init_edge_rot_euler_angles(vec, torch.rand(len(vec), generator=gen))
-        out = omsg.message_block(x, ei, eul, Jd, L, Mm, conv, rad=rad)
+        out = omsg.message_block(x, ei, eul, Jd, L, Mm, conv, rad=rad, gate=gate)
         out.backward(torch.ones_like(out))
         return time.perf_counter() - t0, int(sel.sum())
 
-    run(1)  # warm-up
-    t1, e1 = run(1)
-    nmol = max(1, min(32, int(budget_s / 5 / max(t1, 1e-3))))
+    run(unit)  # warm-up
+    t1, _ = run(unit)
+    n = max(1, min(g.num_nodes // unit, int(budget_s / 5 / max(t1, 1e-3)))) * unit
     times = []
     for _ in range(5):
-        t, e = run(nmol)
+        t, e = run(n)
         times.append(t)
     t = sorted(times)[len(times) // 2]
     return {"value": e / t, "unit": "edges/s", "cores": cores, "kind": "port",
-            "sample": f"config 2, first {nmol} molecule(s) ({e} edges), fp32 torch CPU, fwd+bwd, median of 5",
+            "sample": f"{cfg}, in-edges of the first {n} nodes ({e} edges), fp32 torch CPU, fwd+bwd, median of 5",
             "threads": torch.get_num_threads(), "cpu": _cpu_model()}
 
 
@@ -289,6 +322,248 @@ def cpu_basis_baseline(bw, budget_s=8.0):
             break
     return {"value": total_blocks / total_t, "unit": "H-blocks/s", "cores": cores, "kind": "port",
             "sample": f"config 3, {m + 1} molecule(s) ({total_blocks} blocks), numpy gather + fp32 matmul"}
+
+
+# ------------------------------------------------------- config 1: rotation
+def rotation_leg(cpu=True):
+    """Config 1 (12 atoms, lmax 2, C 32, fp32): x[src] rotated into the edge
+    frame and back (two maloq_rotate launches), single launches and a batch of
+    round trips captured in one HIP graph; the identity and global-rotation
+    errors; and the same kernel at config-2 scale (36 804 edges, lmax 4,
+    C 128), where it is HBM-bound, for its roofline."""
+    import numpy as np
+    import torch
+    from maloq_amd import _lib
+    from maloq_amd import message as M
+    from maloq_amd.rotate import rotate
+    from maloq_amd.wigner import extract_euler_angles
+    dev = torch.device("cuda:0")
+    lib = _lib.load()
+    out = {"metric": "edges/s (rotate in + rotate out)"}
+
+    def raw(xdt, odt, L, x, C, gather, E, eul, inv, y):
+        rc = lib.maloq_rotate(xdt, odt, L, x.data_ptr(), C, gather.data_ptr() if gather is not None else None, E,
+                              eul.data_ptr(), None, M._jd_dev(L, dev).data_ptr(), inv, y.data_ptr(),
+                              torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, lib.maloq_last_error()
+
+    g = _graph("config1_graph")
+    L, C, E = 2, 32, g.num_edges
+    gen = torch.Generator().manual_seed(0)
+    x = torch.randn(g.num_nodes, 9, C, generator=gen).to(dev)
+    vec = torch.from_numpy(g.edge_distance_vec()).float().to(dev)
+    eul = extract_euler_angles(vec, seed=0)
+    src = torch.from_numpy(g.src).to(device=dev, dtype=torch.int32)
+    y = torch.empty(E, 9, C, device=dev)
+    z = torch.empty(E, 9, C, device=dev)
+
+    def rt():
+        raw(0, 0, L, x, C, src, E, eul, 0, y)
+        raw(0, 0, L, y, C, None, E, eul, 1, z)
+    t1 = kernel_time_events(rt, 200)
+    nb = 50
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        rt()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            for _ in range(nb):
+                rt()
+    torch.cuda.current_stream().wait_stream(s)
+    tg = kernel_time_events(graph.replay, 20) / nb
+    torch.cuda.synchronize()
+    ident = ((z - x[src.long()]).abs().max() / x.abs().max()).item()
+    out.update({"config": f"config 1: 12 atoms, {E} directed edges (5 A cutoff), lmax 2, 32 channels, fp32",
+                "value": E / tg, "edges": E, "us_per_round_trip_single_launches": t1 * 1e6,
+                "us_per_round_trip_hip_graph": tg * 1e6, "identity_rel_err": ident})
+    # equivariance: m = 0 rows of the edge frame are unchanged by a global rotation
+    a, b, c = 0.3, 1.1, -0.7
+    from oracle import rotation as orot
+    tt = lambda v: torch.tensor([v], dtype=torch.float64)
+    R = torch.from_numpy(_yxy(a, b, c))
+    Dfull = torch.block_diag(*[orot.wigner_D(l, tt(a), tt(b), tt(c), orot.load_jd())[0] for l in range(3)])
+    xr = torch.einsum("ij,njc->nic", Dfull, x.cpu().double()).float().to(dev)
+    eul_r = extract_euler_angles((torch.from_numpy(g.edge_distance_vec()) @ R.T).float().to(dev), seed=0)
+    y0 = rotate(x, L, eulers=eul, gather=src.long())
+    y1 = rotate(xr, L, eulers=eul_r, gather=src.long())
+    m0 = [l * l + l for l in range(3)]
+    out["equivariance_rel_err_m0_rows"] = ((y1[:, m0] - y0[:, m0]).abs().max() / y0.abs().max()).item()
+    # the kernel at config-2 scale: HBM roofline
+    g2 = _graph("config2_graph")
+    L2, C2, E2 = 4, 128, g2.num_edges
+    d2 = 25
+    eul2 = extract_euler_angles(torch.from_numpy(g2.edge_distance_vec()).float().to(dev), seed=0)
+    src2 = torch.from_numpy(g2.src).to(device=dev, dtype=torch.int32)
+    scale = {}
+    for name, code, dt in (("fp32", 0, torch.float32), ("bf16", 1, torch.bfloat16)):
+        x2 = torch.randn(g2.num_nodes, d2, C2, generator=gen).to(device=dev, dtype=dt)
+        y2 = torch.empty(E2, d2, C2, device=dev, dtype=dt)
+        z2 = torch.empty(E2, d2, C2, device=dev, dtype=dt)
+        es = 2 if code else 4
+        t_in = kernel_time_events(lambda: raw(code, code, L2, x2, C2, src2, E2, eul2, 0, y2), 20)
+        t_out = kernel_time_events(lambda: raw(code, code, L2, y2, C2, None, E2, eul2, 1, z2), 20)
+        b_in = E2 * (2 * d2 * C2 * es + 12 + 4)
+        b_out = E2 * (2 * d2 * C2 * es + 12)
+        scale[name] = {"rotate_in_us": t_in * 1e6, "rotate_out_us": t_out * 1e6,
+                       "edges_per_s_round_trip": E2 / (t_in + t_out),
+                       "roofline": {"kernel": "rotate_kernel<4> (rotate in, gather of x[src])", "bound": "hbm",
+                                    "achieved": b_in / t_in / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                                    "frac": b_in / t_in / PEAK_HBM, "bytes_per_edge": b_in / E2},
+                       "rotate_out_hbm_frac": b_out / t_out / PEAK_HBM}
+    out["config2_scale"] = scale
+    if cpu:
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        e = eul.cpu()
+        xs = x.cpu()
+        Jd = orot.load_jd(torch.float32)
+        srcl = src.long().cpu()
+
+        def cpu_rt():
+            w = orot.eulers_to_wigner((e[:, 0], e[:, 1], e[:, 2]), 0, L, Jd)
+            yy = torch.bmm(w, xs[srcl])
+            return torch.bmm(w.transpose(1, 2), yy)
+        cpu_rt()
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 3.0:
+            cpu_rt()
+            reps += 1
+        out["cpu_baseline"] = {"value": E * reps / (time.perf_counter() - t0), "unit": "edges/s", "cores": cores,
+                               "kind": "port", "sample": f"config 1, whole graph ({E} edges), eulers_to_wigner + "
+                                                         f"bmm + bmm^T, fp32 torch CPU, {reps} repetitions"}
+    return out
+
+
+def _yxy(a, b, c):
+    ca, sa, cb, sb, cc, sc = math.cos(a), math.sin(a), math.cos(b), math.sin(b), math.cos(c), math.sin(c)
+    import numpy as np
+    Ry = lambda co, si: np.array([[co, 0, si], [0, 1, 0], [-si, 0, co]])
+    Rx = np.array([[1, 0, 0], [0, cb, -sb], [0, sb, cb]])
+    return Ry(ca, sa) @ Rx @ Ry(cc, sc)
+
+
+# --------------------------------------------- config 5: block-sparse basis
+SIO2_BASIS = {14: [0, 0, 1, 1, 2], 8: [0, 0, 1, 1, 2]}
+
+
+def sparse_basis_workload():
+    """Config 5's 2s2p1d (T = 169) block list over the 2000-atom cell: every atom
+    pair within 6 A plus the on-site blocks, N(0, 1) exp(-r / 2), on-site - 10."""
+    import numpy as np
+    import torch
+    from maloq_amd import synth
+    from maloq_amd import tensor_decomp as ptd
+    from maloq_amd.basis_transform import HipE3TensorDecomp
+    from oracle import matrix2labels as om2l
+    dev = torch.device("cuda:0")
+    g = _graph("config5_graph")
+    t = ptd.BasisTables(SIO2_BASIS)
+    base = ptd.e3TensorDecomp(t.req_output_irreps, t.out_js_list, torch.float32, device_torch=dev)
+    hip = HipE3TensorDecomp(base)
+    rows, cols = synth.atom_pair_rows(g.src, g.dst, g.num_nodes)
+    off = np.concatenate([[0], np.cumsum(t.orbitals_per_atom(g.Z))]).astype(np.int32)
+    bdo = om2l.block_data_offsets(off, rows, cols)
+    rng = np.random.default_rng(0)
+    data = rng.standard_normal(int(bdo[-1])).astype(np.float32)
+    r = np.linalg.norm(g.vec, axis=1)
+    n_e = len(g.src)
+    sizes = np.diff(bdo)
+    data *= np.repeat(np.concatenate([np.exp(-r / 2), np.ones(len(rows) - n_e)]).astype(np.float32), sizes)
+    for k in range(n_e, len(rows)):
+        i = rows[k]
+        n = off[i + 1] - off[i]
+        blk = data[bdo[k]:bdo[k + 1]].reshape(n, n)
+        blk -= 10.0 * np.eye(n, dtype=np.float32)
+    return dict(tables=t, hip=hip, Z=g.Z.astype(np.int32), off=off, rows=rows.astype(np.int32),
+                cols=cols.astype(np.int32), bdo=torch.from_numpy(bdo).to(dev), bdo_np=bdo,
+                data=torch.from_numpy(data).to(dev), data_np=data, n_blocks=len(rows),
+                block_bytes=4 * int(bdo[-1]), T=base.in_slices[-1])
+
+
+def cpu_sparse_basis_baseline(sw, budget_s=8.0):
+    """The restated K13 gather (numpy_single_matrix2label over the block list) +
+    get_net_out as an fp32 matmul, on whole-cell row chunks until the budget."""
+    import numpy as np
+    import torch
+    from oracle import matrix2labels as om2l
+    from oracle import tensor_decomp as otd
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    t = sw["tables"]
+    o = otd.E3TensorDecomp(t.out_js_list, dtype=torch.float32)
+    n = sw["n_blocks"]
+    step = 4096
+    done, tot = 0, 0.0
+    while done < n and tot < budget_s:
+        sl = slice(done, min(n, done + step))
+        rows, cols = sw["rows"][sl], sw["cols"][sl]
+        bdo = sw["bdo_np"][sl.start:sl.stop + 1] - sw["bdo_np"][sl.start]
+        data = sw["data_np"][sw["bdo_np"][sl.start]:sw["bdo_np"][sl.stop]]
+        t0 = time.perf_counter()
+        lab = np.zeros((len(rows), sw["T"]), np.float32)
+        om2l.single_matrix2label_sparse(t.orbital_template, sw["off"], sw["Z"], rows, cols, data, bdo, lab, True)
+        o.get_net_out(torch.from_numpy(lab))
+        tot += time.perf_counter() - t0
+        done = sl.stop
+    return {"value": done / tot, "unit": "H-blocks/s", "cores": cores, "kind": "port",
+            "sample": f"config 5, {done} of {n} blocks, numpy block-list gather + fp32 matmul"}
+
+
+def sparse_basis_leg(sw, reps=30):
+    import torch
+    hip, t = sw["hip"], sw["tables"]
+    dev = sw["data"].device
+    import numpy as np
+    dev_args = tuple(torch.as_tensor(np.asarray(a, np.int32), device=dev)
+                     for a in (sw["off"], sw["Z"], sw["rows"], sw["cols"]))
+    make = lambda: hip.make_plan(sw["data"], *dev_args, t.orbital_template, block_data_offsets=sw["bdo"])
+    plan = make()
+    tplan = kernel_time_events(make, max(1, reps // 5))
+    irr = hip.fock_to_irreps(sw["data"], *dev_args, t.orbital_template, block_data_offsets=sw["bdo"], plan=plan)
+    tf = kernel_time_events(lambda: hip.fock_to_irreps(sw["data"], *dev_args, t.orbital_template,
+                                                       block_data_offsets=sw["bdo"], plan=plan), reps)
+    back = torch.zeros_like(sw["data"])
+    ti = kernel_time_events(lambda: hip.irreps_to_fock(irr, back, *dev_args, t.orbital_template,
+                                                       block_data_offsets=sw["bdo"], plan=plan), reps)
+    rt = ((back - sw["data"]).abs().max() / sw["data"].abs().max()).item()
+    nb = sw["n_blocks"]
+    bpb = (sw["block_bytes"] + 4 * sw["T"] * nb) / nb
+    return {"metric": "H-blocks/s", "fwd": nb / tf, "inv": nb / ti, "fwd_with_plan": nb / (tf + tplan),
+            "inv_with_plan": nb / (ti + tplan), "plan_ms": tplan * 1e3, "blocks": nb, "T": sw["T"],
+            "round_trip_rel_err": rt,
+            "roofline": {"kernel": "transform_kernel<FOCK,ROWS> (block list)", "bound": "hbm",
+                         "achieved": bpb * nb / tf / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                         "frac": bpb * nb / tf / PEAK_HBM, "bytes_per_block": bpb}}
+
+
+def message_leg(cfg, dtype, steps, warmup, cpu=True):
+    """fwd+bwd of the fused block on configuration ``cfg``: edges/s, the fused
+    forward launch's MFMA roofline, and the CPU baseline."""
+    import torch
+    w = message_workload(dtype, cfg=cfg)
+    t_step = time_steps(lambda: message_step(w, True), steps, warmup)
+    t_fwd = time_steps(lambda: message_step(w, False), steps, warmup)
+    t_launch = fused_forward_launch_time(w, reps=10)
+    L, Mm, C, E = w["L"], w["M"], w["C"], w["E"]
+    f_edge = fused_flops_per_edge(L, Mm, C, C) + (gated_flops_extra(L, C, C) if w["gate"] else 0)
+    peak = PEAK_BF16 if dtype == "bf16" else PEAK_FP32
+    gname = MESSAGE_CONFIGS[cfg][0]
+    res = {"metric": "edges/s (fused block fwd+bwd)", "value": E / t_step, "ms_per_step": t_step * 1e3,
+           "fwd_edges_per_s": E / t_fwd, "dtype": dtype,
+           "config": {"workload": f"{cfg} fused message block fwd+bwd{' (gated)' if w['gate'] else ''}",
+                      "graph": gname, "edges": E, "nodes": w["N"], "lmax": L, "mmax": Mm, "channels": C,
+                      "gate": w["gate"], "rbf_cutoff_A": w["cutoff"]},
+           "roofline": {"kernel": f"maloq_message_fwd: prep + gemm_kernel<{L},{Mm}> + fixup", "bound": "mfma",
+                        "achieved": f_edge * E / t_launch / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
+                        "frac": f_edge * E / t_launch / peak, "flops_per_edge": f_edge,
+                        "launch_ms": t_launch * 1e3}}
+    del w
+    torch.cuda.empty_cache()
+    if cpu:
+        res["cpu_baseline"] = cpu_message_baseline(budget_s=12.0, cfg=cfg)
+    return res
 
 
 def _cpu_model():
@@ -515,8 +790,13 @@ def profile_only(args):
         ew = edgewise_workload()
         for _ in range(args.reps):
             edgewise_step(ew)
+    elif args.only == "rotate":
+        rotation_leg(cpu=False)
+    elif args.only == "basis5":
+        sw = sparse_basis_workload()
+        sparse_basis_leg(sw, reps=args.reps)
     elif args.only in ("fwd", "step"):
-        w = message_workload(args.dtype)
+        w = message_workload(args.dtype, cfg=args.cfg)
         if args.only == "fwd":
             fused_forward_launch_time(w, reps=args.reps)
         else:
@@ -543,11 +823,15 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp32"])
+    ap.add_argument("--dtype", default="fp32", choices=["bf16", "fp32"],
+                    help="precision of the headline (the reference computes in fp32)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-extras", action="store_true", help="headline only")
-    ap.add_argument("--only", choices=["fwd", "step", "basis", "copy", "embed", "edgewise", "edgewise-step"],
+    ap.add_argument("--only", choices=["fwd", "step", "basis", "copy", "embed", "edgewise", "edgewise-step",
+                                       "rotate", "basis5"],
                     help="profiling mode: run one piece a few times and exit (no JSON line)")
+    ap.add_argument("--cfg", default="config2", choices=sorted(MESSAGE_CONFIGS),
+                    help="message-block configuration of --only fwd / step")
     ap.add_argument("--reps", type=int, default=5, help="launches in --only mode")
     ap.add_argument("--traffic-from", metavar="DIR",
                     help="write profiles/traffic.json from rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE runs in DIR")
@@ -600,25 +884,34 @@ def main(argv=None):
     }
     del w
     torch.cuda.empty_cache()
+    other = "bf16" if args.dtype == "fp32" else "fp32"
     if not args.no_extras:
-        if args.dtype == "bf16":
-            w32 = message_workload("fp32")
-            t32 = time_steps(lambda: message_step(w32, True), max(3, args.steps // 4), 2)
-            result["fp32_fwd_bwd_edges_per_s"] = w32["E"] / t32
-            tl32 = fused_forward_launch_time(w32, reps=5)
-            result["fp32_fwd_roofline_frac"] = f_edge * w32["E"] / tl32 / PEAK_FP32
-            del w32
+        # the same configuration in the other precision (the reference computes in fp32)
+        print(f"[bench] config 2 in {other} ...", file=sys.stderr, flush=True)
+        result[f"config2_{other}"] = message_leg("config2", other, max(5, args.steps // 2), 3, cpu=False)
+        print("[bench] config 1 rotation ...", file=sys.stderr, flush=True)
+        result["config1_rotation"] = rotation_leg(cpu=not args.no_cpu)
+        for cfg in ("config4", "config5"):
+            print(f"[bench] {cfg} fused block (bf16) ...", file=sys.stderr, flush=True)
+            result[cfg] = message_leg(cfg, "bf16", max(5, args.steps // 2), 3, cpu=not args.no_cpu)
         print("[bench] basis transform (config 3) ...", file=sys.stderr, flush=True)
         bw = basis_workload()
         tf, ti, rt, tplan = basis_timing(bw)
         bpb = (bw["block_bytes"] + 4 * bw["T"] * bw["n_blocks"]) / bw["n_blocks"]
         result["basis_transform"] = {
             "metric": "H-blocks/s", "fwd": bw["n_blocks"] / tf, "inv": bw["n_blocks"] / ti,
+            "fwd_with_plan": bw["n_blocks"] / (tf + tplan), "inv_with_plan": bw["n_blocks"] / (ti + tplan),
             "blocks": bw["n_blocks"], "round_trip_rel_err": rt, "plan_ms": tplan * 1e3,
             "roofline": {"bound": "hbm", "achieved": bpb * bw["n_blocks"] / tf / 1e9, "peak": PEAK_HBM / 1e9,
                          "unit": "GB/s", "frac": bpb * bw["n_blocks"] / tf / PEAK_HBM,
                          "bytes_per_block": bpb, "traffic": load_traffic("fock_to_irreps")},
         }
+        print("[bench] basis transform (config 5, block list) ...", file=sys.stderr, flush=True)
+        sw = sparse_basis_workload()
+        result["config5_basis_transform"] = sparse_basis_leg(sw)
+        if not args.no_cpu:
+            result["config5_basis_transform"]["cpu_baseline"] = cpu_sparse_basis_baseline(sw)
+        del sw
         print("[bench] edge-degree embedding (config 2) ...", file=sys.stderr, flush=True)
         ew = embed_workload()
         s = torch.cuda.current_stream()
