@@ -148,6 +148,45 @@ int maloq_matrix2label(float* fock, int64_t ld, const int64_t* data_offsets,
                        const int32_t* tmpl_ptr, const int32_t* tmpl, float* target,
                        int64_t target_ld, int forward, void* stream);
 
+/* ------------------------------------------- label-side caller hooks -- */
+
+/* labels[r][cols[k]] += sign * means[atomic_numbers[r]][k] for r < num_rows,
+ * k < ncols (labels row stride ld, means [max Z + 1, ncols] fp32, every Z of
+ * the rows inside the table).  sign = -1: the l = 0 shift of the node labels,
+ * Fock_Targets.scale_shift_node_blocks (fock_utils/fock_targets_batched.py:1093-1115,
+ * applied at :444-453); sign = +1: its undo, unscale_shift_node_blocks with
+ * shift only (:1157-1183, called from train_utils/splittrainer.py:537-541). */
+int maloq_label_scalar_shift(float* labels, int64_t ld, int64_t num_rows, const int32_t* atomic_numbers,
+                             const float* means, const int32_t* cols, int ncols, float sign, void* stream);
+
+/* Label padding mask: mask[r][c] = cover[pair_kind[Z[rows[r]]*100 + Z[cols[r]]]][c]
+ * (0 where the pair kind is -1), mask [num_rows, t] uint8, cover [kinds, t]
+ * uint8 (1 on the output columns of every template entry of the kind), Z < 100.
+ * Replaces Fock_Targets.create_label_unpadding_mask,
+ * fock_utils/fock_targets_batched.py:1012-1080 (a Python loop per row there). */
+int maloq_label_mask(const int32_t* rows, const int32_t* cols, const int32_t* atomic_numbers,
+                     const int32_t* pair_kind, const uint8_t* cover, int t, int64_t num_rows, uint8_t* mask,
+                     void* stream);
+
+/* out[i][j] = sign[i] sign[j] H[src[i]][src[j]] for i, j < n (src a
+ * permutation of 0..n-1, sign +-1; out must not alias H): the per-shell
+ * m-reordering with reflections S H S^T of sort_by_m,
+ * fock_utils/utils_orca_out.py:402-465, with (src, sign) from the host. */
+int maloq_signed_permute(const float* H, int64_t n, int64_t ld_in, const int32_t* src, const float* sign,
+                         float* out, int64_t ld_out, void* stream);
+
+/* A SparseBlockMatrix (block b: rows of atom block_rows[b], columns of atom
+ * block_cols[b], row-major at data[block_data_offsets[b]]) into CSR arrays:
+ * indptr [n + 1] and block_col_offsets [num_blocks] (the columns of the blocks
+ * left of b in its block row, blocks of a row atom ordered by column atom)
+ * from the host; csr_data / csr_indices [nnz] written here, column indices
+ * ascending within each row.  Replaces the COO build of
+ * sparse_block_matrix_to_scipy_csr, fock_utils/matrix2labels_kernels.py:16-42. */
+int maloq_blocks_to_csr(const float* data, const int64_t* block_data_offsets, const int32_t* block_rows,
+                        const int32_t* block_cols, const int32_t* fock_block_offsets,
+                        const int64_t* block_col_offsets, const int64_t* indptr, int64_t num_blocks,
+                        float* csr_data, int64_t* csr_indices, void* stream);
+
 /* -------------------------------------------------- fused message block -- */
 
 /* Floats of the partial-segment buffer the message entry points need. */

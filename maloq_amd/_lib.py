@@ -34,6 +34,10 @@ SIGNATURES = {
     "maloq_irreps_to_fock": [_p, _p, _p, _i64, _p, _i64, _p, _i32, _p, _i32, _i32, _p, _p, _p, _p],
     "maloq_matrix2label": [_p, _i64, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _i64, _i32, _p],
     "maloq_segment_sum": [_p, _p, _p, _i64, _i64, _p, _p],
+    "maloq_label_scalar_shift": [_p, _i64, _i64, _p, _p, _p, _i32, ctypes.c_float, _p],
+    "maloq_label_mask": [_p, _p, _p, _p, _p, _i32, _i64, _p, _p],
+    "maloq_signed_permute": [_p, _i64, _i64, _p, _p, _p, _i64, _p],
+    "maloq_blocks_to_csr": [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p],
     "maloq_message_partials_floats": [_i32, _i32, _i64, _i32],
     "maloq_message_wpack_bytes": [_i32, _i32, _i32, _i32, _i32, _i32],
     "maloq_message_kept_rows": [_i32, _i32],
@@ -103,15 +107,21 @@ def load():
 
 
 def call(name: str, *args) -> None:
+    """Call entry point ``name``; a tensor argument is passed as its device
+    pointer and, being held by ``args``, stays allocated until the call has
+    enqueued its kernels."""
     lib = load()
-    rc = getattr(lib, name)(*args)
+    rc = getattr(lib, name)(*(a.data_ptr() if isinstance(a, torch.Tensor) else a for a in args))
     if rc != 0:
         msg = lib.maloq_last_error().decode(errors="replace")
         raise MaloqHipError(f"{name} failed ({rc}): {msg}")
 
 
 def ptr(t) -> int | None:
-    """Device pointer of a tensor (None for None)."""
+    """Device pointer of a tensor (None for None).  The caller must keep the
+    tensor referenced until the kernels reading it are enqueued: the pointer of
+    a temporary is released to the caching allocator as soon as this returns,
+    and the next allocation of that size receives the same block."""
     if t is None:
         return None
     return t.data_ptr()

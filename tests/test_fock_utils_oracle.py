@@ -1,0 +1,105 @@
+"""Pins of the label-side hook restatements (oracle/fock_utils.py) and of the
+product's host tables, CPU only.
+
+* scale-shift: undo(shift(x)) = x; the shift moves exactly the scalar columns
+  by the reference's nablaDFT means (tests/golden/scale_shifts_nabladft.npz);
+* sort_by_m: the l = 1 block goes from ORCA's (p0, p+1, p-1) = (z, x, y) to
+  e3nn's (y, z, x); both directions are inverse; S is orthogonal; the product's
+  (src, sign) tables reproduce the restated loop;
+* padding mask: True exactly on the label columns the template gather writes;
+* CSR export: the dense form equals the assembled block list.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fock_utils as ofu
+from oracle import matrix2labels as om2l
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _nabla():
+    z = np.load(os.path.join(GOLDEN, "scale_shifts_nabladft.npz"))
+    means = {int(Z): z["means"][k].tolist() for k, Z in enumerate(z["Z"])}
+    return means, z["scalar_irrep_indices"].tolist()
+
+
+def test_scale_shift_round_trip_and_columns():
+    means, idx = _nabla()
+    Zs = [1, 6, 8, 7, 6, 16]
+    x = torch.randn(len(Zs), 1000, dtype=torch.float64, generator=torch.Generator().manual_seed(0))
+    y = ofu.scale_shift_node_blocks(x, Zs, means, idx)
+    other = [c for c in range(1000) if c not in set(idx)]
+    assert torch.equal(y[:, other], x[:, other])
+    for r, z in enumerate(Zs):
+        assert torch.allclose(x[r, idx] - y[r, idx], torch.tensor(means[z], dtype=torch.float64))
+    assert torch.allclose(ofu.unscale_shift_node_blocks(y, Zs, means, idx), x, atol=1e-12)
+    # the carbon core s-s mean is the large negative one-centre value (-10.32 Ha)
+    assert means[6][0] < -10 and means[1][0] < 0
+
+
+BASIS = {1: [0, 0, 1], 6: [0, 0, 0, 1, 1, 2], 8: [0, 0, 0, 1, 1, 2], 16: [0, 0, 0, 1, 1, 2, 3]}
+
+
+def _ham(Z, seed):
+    n = sum(sum(2 * (l % 10) + 1 for l in BASIS[z]) for z in Z)
+    a = np.random.default_rng(seed).standard_normal((n, n))
+    return a + a.T
+
+
+def test_sort_by_m_p_order_and_inverse():
+    Z = [6]
+    n = 14
+    # C: s s s p p d; the first p shell starts at 3
+    H = np.zeros((n, n))
+    H[3:6, 3:6] = np.diag([10.0, 20.0, 30.0])          # ORCA (pz, px, py)
+    e = ofu.sort_by_m(H, BASIS, Z, "orca_to_e3nn")
+    assert np.allclose(np.diag(e[3:6, 3:6]), [30.0, 10.0, 20.0])   # e3nn (y, z, x)
+    for fwd, back in (("orca_to_e3nn", "e3nn_to_orca"), ("e3nn_to_pyscf", "pyscf_to_e3nn")):
+        Z2 = [8, 1, 16, 6]
+        H2 = _ham(Z2, 1)
+        assert np.allclose(ofu.sort_by_m(ofu.sort_by_m(H2, BASIS, Z2, fwd), BASIS, Z2, back), H2, atol=1e-12)
+        # similarity by an orthogonal matrix: the spectrum is kept
+        assert np.allclose(np.linalg.eigvalsh(ofu.sort_by_m(H2, BASIS, Z2, fwd)), np.linalg.eigvalsh(H2))
+
+
+@pytest.mark.parametrize("direction", ["orca_to_e3nn", "e3nn_to_orca", "e3nn_to_pyscf", "pyscf_to_e3nn"])
+def test_m_order_tables_match_oracle(direction):
+    from maloq_amd.fock_utils import m_order_permutation
+    Z = [8, 1, 16, 6, 1]
+    H = _ham(Z, 2)
+    src, sign = m_order_permutation(BASIS, Z, direction)
+    got = sign[:, None] * sign[None, :] * H[np.ix_(src, src)]
+    assert np.array_equal(got, ofu.sort_by_m(H, BASIS, Z, direction))
+
+
+def test_padding_mask_matches_gather_coverage():
+    from maloq_amd import tensor_decomp as ptd
+    t = ptd.BasisTables({1: [0, 0, 1], 6: [0, 0, 0, 1, 1, 2], 8: [0, 0, 0, 1, 1, 2]})
+    T = int(t.orbital_starts[-1])
+    Z = np.array([6, 1, 8, 1, 6])
+    src = np.array([0, 1, 2, 3, 4, 0, 2])
+    dst = np.array([1, 0, 4, 2, 0, 3, 3])
+    em, nm = ofu.create_label_unpadding_mask(t.orbital_template, Z, src, dst, T)
+    off = np.concatenate([[0], np.cumsum(t.orbitals_per_atom(Z))]).astype(np.int32)
+    rows = np.concatenate([src, np.arange(5)]).astype(np.int32)
+    cols = np.concatenate([dst, np.arange(5)]).astype(np.int32)
+    lab = np.zeros((len(rows), T), np.float32)
+    om2l.single_matrix2label(t.orbital_template, off, Z, rows, cols, np.ones((off[-1], off[-1]), np.float32), lab, True)
+    assert np.array_equal(torch.cat([em, nm]).numpy(), lab != 0)
+
+
+def test_csr_export_assembles_blocks():
+    off = np.array([0, 3, 5, 9], np.int64)
+    rows = np.array([0, 1, 0, 2, 2, 1])
+    cols = np.array([1, 1, 0, 2, 0, 2])
+    bdo = om2l.block_data_offsets(off, rows, cols)
+    data = np.arange(1, bdo[-1] + 1, dtype=np.float32)
+    A = ofu.sparse_block_matrix_to_scipy_csr(data, bdo, rows, cols, off).toarray()
+    D = np.zeros((9, 9), np.float32)
+    for b, (i, j) in enumerate(zip(rows, cols)):
+        D[off[i]:off[i + 1], off[j]:off[j + 1]] = data[bdo[b]:bdo[b + 1]].reshape(off[i + 1] - off[i], -1)
+    assert np.array_equal(A, D)
