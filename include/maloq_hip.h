@@ -73,8 +73,15 @@ int maloq_rotate(int x_dtype, int out_dtype, int lmax, const void* x, int c, con
  * is block diagonal: CG block b (one shell pair l1 x l2) maps the n = (2l1+1)(2l2+1)
  * columns col0 .. col0+n-1 of an unsorted label row to the same columns of the
  * unsorted irreps row (and back).
- *   blocks [nblocks, 3] = (n, col0, woff); the block matrix is w[woff + j*n + k]
- *     (output column j, input column k), n in {1,3,5,7,9,15,21,25,35,49} (l <= 3);
+ *   blocks [nblocks, 4] = (n, col0, woff, program); the block matrix is
+ *     w[woff + j*n + k] (output column j, input column k), n in
+ *     {1,3,5,7,9,15,21,25,35,49} (l <= 3); program >= 0 names the compiled CG
+ *     program (maloq_basis_cg_block) whose matrix equals that block exactly,
+ *     which the kernels then run instead of reading w; -1 for none.  The
+ *     program depends on the direction (w_fwd / w_inv / w_adj), so each
+ *     direction has its own blocks table;
+ *   w      the block matrices; NULL is allowed when every block of the table
+ *     has a program (the kernels then carry no dense path at all);
  *   sched  [5 + nblocks]: sched[0..4] are offsets into sched + 5 of the block ids
  *     each of the 4 waves of a workgroup contracts (sched[4] = nblocks);
  *   t      row width, at most 1279 (one 32-row tile of fp32 in LDS).
@@ -100,8 +107,8 @@ int maloq_label_transform(const float* in, const int32_t* perm_in, float* out,
  *          columns, row-major (SparseBlockMatrix, matrix2labels_kernels.py:43-48);
  * kind = pair_kind[Z_i*100 + Z_j] (-1: no template, the row is all zero), n_i, n_j <= 255,
  * n_i * n_j <= maxe.  row_meta: [num_rows, 4] int32, 16-byte aligned.  The transforms
- * below take the plan in any row order (the host orders it by kind); entry p of the
- * plan reads and writes row r = plan[p].z.  Replaces the per-call index lists of
+ * below take the plan in any row order; entry p of the plan reads and writes
+ * row r = plan[p].z.  Replaces the per-call index lists of
  * cupy_single_matrix2label (matrix2labels_kernels.py:978-994). */
 int maloq_basis_row_meta(int64_t ld, const int64_t* data_offsets,
                          const int32_t* fock_block_offsets, const int32_t* atomic_numbers,
@@ -135,6 +142,15 @@ int maloq_irreps_to_fock(const float* irreps, const int32_t* perm_in, float* foc
                          int maxe, const uint32_t* kind_blocks, int t, int nblocks,
                          const int32_t* blocks, const float* w, const int32_t* sched,
                          void* stream);
+
+/* The dense n x n matrix (row-major, output column x input column) of compiled
+ * CG program p = dir * 16 + l1 * 4 + l2 (dir 0: get_net_out, the
+ * decomposition's wms_H block; 1: get_H, its wms block; 2: get_H's adjoint,
+ * wms transposed), n = (2 l1 + 1)(2 l2 + 1), written to host memory w.  No GPU
+ * work: the host compares its tables with these to fill the program column of
+ * blocks.  The matrices restate e3TensorDecomp's blocks for one shell pair,
+ * fock_utils/utils_tensor_decomp.py:85-99. */
+int maloq_basis_cg_block(int program, float* w, int n);
 
 /* Plain Fock <-> label copy (no CG), dense or block-sparse storage as above.
  * forward != 0: label[r, out0 + k] = block(r)[r0 + k/w, c0 + k%w];

@@ -29,6 +29,7 @@ SIGNATURES = {
     "maloq_wigner_from_euler": [_p, _i64, _i32, _p, _p, _p, _i32, _p],
     "maloq_rotate": [_i32, _i32, _i32, _p, _i32, _p, _i64, _p, _p, _p, _i32, _p, _p],
     "maloq_label_transform": [_p, _p, _p, _p, _i64, _i32, _i32, _p, _p, _p, _p],
+    "maloq_basis_cg_block": [_i32, _p, _i32],
     "maloq_basis_row_meta": [_i64, _p, _p, _p, _p, _p, _i64, _p, _i32, _p, _p],
     "maloq_fock_to_irreps": [_p, _i64, _p, _i64, _p, _i32, _p, _p, _p, _i32, _i32, _p, _p, _p, _p],
     "maloq_irreps_to_fock": [_p, _p, _p, _i64, _p, _i64, _p, _i32, _p, _i32, _i32, _p, _p, _p, _p],

@@ -39,16 +39,16 @@ _SUPPORTED_N = frozenset((2 * a + 1) * (2 * b + 1) for a in range(4) for b in ra
 _WAVES = 4  # waves per workgroup of the transform kernel
 
 
-def _wave_schedule(sizes):
+def _wave_schedule(costs):
     """Longest-processing-time split of the CG blocks over the 4 waves of a
-    workgroup (cost n^2 FMAs + 2n LDS accesses per row).  Layout: 5 offsets,
-    then the block ids of wave 0, wave 1, ..."""
+    workgroup (``costs[b]``: FMAs + LDS accesses per row of block b).
+    Layout: 5 offsets, then the block ids of wave 0, wave 1, ..."""
     load = [0] * _WAVES
     lists = [[] for _ in range(_WAVES)]
-    for b in sorted(range(len(sizes)), key=lambda i: (-sizes[i], i)):
+    for b in sorted(range(len(costs)), key=lambda i: (-costs[i], i)):
         w = min(range(_WAVES), key=lambda k: (load[k], k))
         lists[w].append(b)
-        load[w] += sizes[b] * sizes[b] + 2 * sizes[b]
+        load[w] += costs[b]
     offs = np.cumsum([0] + [len(x) for x in lists])
     return np.concatenate([offs, np.concatenate([np.array(x, np.int64) for x in lists])]).astype(np.int32)
 
@@ -61,7 +61,11 @@ def cg_block_tables(decomp_obj):
       [output column][input column], of get_net_out (W[t][h] = wms_H[b] as
       [n, n], utils_tensor_decomp.py:118), get_H (W[h][t] = wms[b] as [n, n],
       :117) and the transpose of get_H's block (its adjoint);
-    * ``sched``: the per-wave block lists (_wave_schedule).
+    * ``programs`` [3, nblocks]: per direction (fwd, inv, adj) the compiled CG
+      program of libmaloq_hip.so whose matrix equals the block's exactly, or -1
+      (the kernels then read the weights);
+    * ``sched``: the per-wave block lists (_wave_schedule), costed by the
+      nonzeros a compiled program computes or n^2 for a dense block.
     """
     ins, hs = decomp_obj.in_slices, decomp_obj.H_slices
     if list(map(int, ins)) != list(map(int, hs)):
@@ -77,8 +81,35 @@ def cg_block_tables(decomp_obj):
         blocks.append((n, int(ins[b]), woff))
         w_fwd.append(fwd.reshape(-1)); w_inv.append(inv.reshape(-1)); w_adj.append(inv.T.reshape(-1))
         woff += n * n
-    return {"blocks": np.array(blocks, np.int32), "sched": _wave_schedule([n for n, _, _ in blocks]),
-            "w_fwd": np.concatenate(w_fwd), "w_inv": np.concatenate(w_inv), "w_adj": np.concatenate(w_adj)}
+    w = [np.concatenate(w_fwd), np.concatenate(w_inv), np.concatenate(w_adj)]
+    programs = _match_cg_programs(decomp_obj.out_js_list, blocks, w)
+    costs = []
+    for b, (n, _, woff) in enumerate(blocks):
+        fma = int(np.count_nonzero(w[0][woff:woff + n * n])) if (programs[:, b] >= 0).all() else n * n
+        costs.append(fma + 2 * n)
+    return {"blocks": np.array(blocks, np.int32), "programs": programs, "sched": _wave_schedule(costs),
+            "w_fwd": w[0], "w_inv": w[1], "w_adj": w[2]}
+
+
+def _match_cg_programs(out_js_list, blocks, w):
+    """[3, nblocks] int32: for direction d (0 fwd, 1 inv, 2 adj) and block b of
+    shell pair (l1, l2), the program d * 16 + l1 * 4 + l2 if its compiled
+    matrix (maloq_basis_cg_block) equals the block's fp32 matrix entry for
+    entry, else -1."""
+    lib = _lib.load()
+    compiled = {}
+    out = np.full((3, len(blocks)), -1, np.int32)
+    for b, (n, _, woff) in enumerate(blocks):
+        l1, l2 = (int(v) % 10 for v in out_js_list[b])
+        for d in range(3):
+            p = d * 16 + l1 * 4 + l2
+            if p not in compiled:
+                m = np.empty(n * n, np.float32)
+                compiled[p] = m if lib.maloq_basis_cg_block(p, m.ctypes.data, n) == 0 else None
+            ref = compiled[p]
+            if ref is not None and ref.shape[0] == n * n and np.array_equal(ref, w[d][woff:woff + n * n].astype(np.float32)):
+                out[d, b] = p
+    return out
 
 
 def template_slot_tables(orbital_template, h_slices):
@@ -131,9 +162,9 @@ def template_slot_tables(orbital_template, h_slices):
 class BasisPlan:
     """Row plan of the Fock-side transforms for one structure: per atom pair the
     block base, its original row index, element-pair kind and shape
-    (maloq_basis_row_meta), ordered by kind so that the 32-row tiles of the
-    transform hold one or a few element pairs.  Build it once per (index lists,
-    storage) and pass it to fock_to_irreps / irreps_to_fock."""
+    (maloq_basis_row_meta), in row order.  One small kernel builds it; build it
+    once per (index lists, storage) to reuse it across fock_to_irreps /
+    irreps_to_fock calls."""
 
     def __init__(self, meta, num_rows, ld, template_key):
         self.meta, self.num_rows, self.ld, self.template_key = meta, num_rows, ld, template_key
@@ -168,10 +199,19 @@ class HipE3TensorDecomp:
             self.sort_perm = torch.argmax(decomp_obj.sort(eye.to(decomp_obj.device)).cpu(), dim=0).numpy()
         tabs = cg_block_tables(decomp_obj)
         dev = self.device
-        self._blocks = _i32(tabs["blocks"].reshape(-1), dev)
+        # one blocks table per direction: (n, col0, woff, compiled program or -1)
+        self._blocks_fwd, self._blocks_inv, self._blocks_adj = (
+            _i32(np.concatenate([tabs["blocks"], tabs["programs"][d][:, None]], axis=1).reshape(-1), dev)
+            for d in range(3))
+        self.cg_programs = tabs["programs"]
         self._sched = _i32(tabs["sched"], dev)
         f32 = lambda a: torch.as_tensor(a.astype(np.float32), device=dev)
         self._w_fwd, self._w_inv, self._w_adj = f32(tabs["w_fwd"]), f32(tabs["w_inv"]), f32(tabs["w_adj"])
+        # the weights the kernels read: none in a direction where every block
+        # runs a compiled program (the kernel variant without the dense loops)
+        self._wk_fwd, self._wk_inv, self._wk_adj = (
+            None if (self.cg_programs[d] >= 0).all() else w for d, w in enumerate(
+                (self._w_fwd, self._w_inv, self._w_adj)))
         self._perm = _i32(self.sort_perm, dev) if self.sort_perm is not None else None
         self.block_n2 = np.array([(2 * (l2 % 10) + 1) for _, l2 in decomp_obj.out_js_list], np.int32)
         self._templates = {}
@@ -188,28 +228,28 @@ class HipE3TensorDecomp:
         if x.dim() != 2 or x.shape[1] != width:
             raise ValueError(f"expected [R, {width}], got {tuple(x.shape)}")
 
-    def _transform(self, x, w, perm_in=None, perm_out=None):
+    def _transform(self, x, blocks, w, perm_in=None, perm_out=None):
         x = x.contiguous()
         out = torch.empty_like(x)
         _lib.call("maloq_label_transform", _lib.ptr(x), _lib.ptr(perm_in), _lib.ptr(out), _lib.ptr(perm_out),
-                  x.shape[0], x.shape[1], self.num_blocks, _lib.ptr(self._blocks), _lib.ptr(w),
+                  x.shape[0], x.shape[1], self.num_blocks, _lib.ptr(blocks), _lib.ptr(w),
                   _lib.ptr(self._sched), _lib.stream_of(x.device))
         return out
 
     def _get_H_impl(self, net_out):
         self._check(net_out, self.total_in_dim)
-        return self._transform(net_out, self._w_inv, perm_in=self._perm)
+        return self._transform(net_out, self._blocks_inv, self._wk_inv, perm_in=self._perm)
 
     def _get_H_adjoint(self, grad):
         self._check(grad, self.total_h_dim)
-        return self._transform(grad, self._w_adj, perm_out=self._perm)
+        return self._transform(grad, self._blocks_adj, self._wk_adj, perm_out=self._perm)
 
     def get_H(self, net_out):
         return _GetH.apply(net_out, self)
 
     def get_net_out(self, H):
         self._check(H, self.total_h_dim)
-        return self._transform(H, self._w_fwd, perm_out=self._perm)
+        return self._transform(H, self._blocks_fwd, self._wk_fwd, perm_out=self._perm)
 
     # ------------------------------------------------ fused Fock <-> irreps
     def _template_tables(self, orbital_template):
@@ -247,9 +287,6 @@ class HipE3TensorDecomp:
         _lib.call("maloq_basis_row_meta", ld, _lib.ptr(bdo), _lib.ptr(off), _lib.ptr(Z), _lib.ptr(r_),
                   _lib.ptr(c_), R, _lib.ptr(tabs["pair_kind"]), tabs["maxe"], _lib.ptr(meta),
                   _lib.stream_of(dev))
-        if R > 1:
-            kind = torch.bitwise_and(meta[:R, 3], 0xFFFF)
-            meta = meta[:R][torch.argsort(kind, stable=True)].contiguous()
         return BasisPlan(meta, R, ld, id(orbital_template))
 
     def _plan_for(self, plan, fock, fock_block_offsets, atomic_numbers, rows, cols, orbital_template,
@@ -276,8 +313,8 @@ class HipE3TensorDecomp:
         out = torch.empty(plan.num_rows, self.total_in_dim, device=fock.device, dtype=torch.float32)
         _lib.call("maloq_fock_to_irreps", _lib.ptr(fock), plan.ld, _lib.ptr(plan.meta), plan.num_rows,
                   _lib.ptr(tabs["raw"]), tabs["maxe"], _lib.ptr(tabs["kind_blocks"]), _lib.ptr(out),
-                  _lib.ptr(self._perm), self.total_in_dim, self.num_blocks, _lib.ptr(self._blocks),
-                  _lib.ptr(self._w_fwd), _lib.ptr(self._sched), _lib.stream_of(fock.device))
+                  _lib.ptr(self._perm), self.total_in_dim, self.num_blocks, _lib.ptr(self._blocks_fwd),
+                  _lib.ptr(self._wk_fwd), _lib.ptr(self._sched), _lib.stream_of(fock.device))
         return out
 
     def irreps_to_fock(self, net_out, fock, fock_block_offsets, atomic_numbers, rows, cols,
@@ -293,8 +330,8 @@ class HipE3TensorDecomp:
         net_out = net_out.contiguous()
         _lib.call("maloq_irreps_to_fock", _lib.ptr(net_out), _lib.ptr(self._perm), _lib.ptr(fock), plan.ld,
                   _lib.ptr(plan.meta), plan.num_rows, _lib.ptr(tabs["raw"]), tabs["maxe"],
-                  _lib.ptr(tabs["kind_blocks"]), self.total_in_dim, self.num_blocks, _lib.ptr(self._blocks),
-                  _lib.ptr(self._w_inv), _lib.ptr(self._sched), _lib.stream_of(fock.device))
+                  _lib.ptr(tabs["kind_blocks"]), self.total_in_dim, self.num_blocks, _lib.ptr(self._blocks_inv),
+                  _lib.ptr(self._wk_inv), _lib.ptr(self._sched), _lib.stream_of(fock.device))
         return fock
 
 

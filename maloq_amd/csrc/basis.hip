@@ -14,23 +14,26 @@
 //      element dropped into its label column through a per-element-pair table;
 //   2. contract: each of the 4 waves takes a fixed list of CG blocks (longest-
 //      processing-time balanced on the host); lane = row, so the n x n block
-//      matrix is the same for all 64 lanes and is read with scalar loads, and
-//      every FMA takes its weight from an SGPR.  A block that no row of the
-//      tile has (an element pair without that shell pair) is skipped;
+//      matrix is the same for all 64 lanes.  A block whose matrix is one of
+//      the compiled CG programs (cg_blocks.h: its exact zeros skipped, its
+//      weights literals, about a fifth of the dense FMAs and no weight loads)
+//      runs that program; any other block runs the dense n x n loop with its
+//      weights read into SGPRs.  A block that no row of the tile has (an
+//      element pair without that shell pair) is skipped;
 //   3. store: coalesced rows (through the sort permutation) or the atom-pair
 //      blocks again in memory order (every Fock entry written by exactly one
 //      (row, column): deterministic, no atomics).
 //
 // Fock-side calls run on a row plan: maloq_basis_row_meta describes every row
 // (block base, original row index, element-pair kind, block shape) once per
-// structure, and the host orders the plan by kind so that tiles hold one or a
-// few element pairs and the block skip in phase 2 takes effect.
+// structure, in row order.
 //
 // Reference semantics: e3TensorDecomp.get_H / get_net_out
 // (fock_utils/utils_tensor_decomp.py:154-169), the Triton kernels K6/K8
 // (basis_transform_triton_backend.py:853-1008) and the CuPy gather/scatter
 // K12/K13 (matrix2labels_kernels.py:547-800).
 #include "common.h"
+#include "cg_blocks.h"
 #include "../../include/maloq_hip.h"
 
 namespace maloq {
@@ -66,7 +69,7 @@ struct Args {
   const uint32_t* kind_blocks;  // [kinds, 2]: CG blocks present for the kind (bit b), or null
   // CG tables
   int nblocks;
-  const int32_t* blocks;    // [nblocks, 3]: n, first column, weight offset
+  const int32_t* blocks;    // [nblocks, 4]: n, first column, weight offset, CG program or -1
   const float* w;
   const int32_t* sched;     // [kWaves + 1] offsets into sched + kWaves + 1 of block ids
 };
@@ -265,7 +268,10 @@ __device__ __forceinline__ void contract(float* row, const float* __restrict__ W
   }
 }
 
-template <bool SKIP>
+// DENSE: the tables may hold blocks without a compiled program (read from
+// a.w); otherwise every block has one and the dense loops (and their
+// registers) are compiled out.
+template <bool SKIP, bool DENSE>
 __device__ __forceinline__ void contract_tile(const Args& a, const Smem& s, float* tile) {
   const int wave = uniform(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -286,9 +292,15 @@ __device__ __forceinline__ void contract_tile(const Args& a, const Smem& s, floa
       const bool mine = ((b < 32 ? have0 >> b : have1 >> (b - 32)) & 1u) != 0;
       if (__builtin_amdgcn_ballot_w64(mine) == 0) continue;  // no row of the tile has block b
     }
-    const int n = uniform(a.blocks[3 * b]);
-    const int c0 = uniform(a.blocks[3 * b + 1]);
-    const float* W = a.w + uniform(a.blocks[3 * b + 2]);
+    const int n = uniform(a.blocks[4 * b]);
+    const int c0 = uniform(a.blocks[4 * b + 1]);
+    const int prog = uniform(a.blocks[4 * b + 3]);
+    if (prog >= 0) {
+      cg::run(prog, row + c0);
+      continue;
+    }
+    if constexpr (!DENSE) continue;  // excluded by the host (w == NULL only with every program set)
+    const float* W = a.w + uniform(a.blocks[4 * b + 2]);
     switch (n) {  // (2 l1 + 1)(2 l2 + 1) for l1, l2 <= 3
       case 1: contract<1>(row + c0, W); break;
       case 3: contract<3>(row + c0, W); break;
@@ -305,9 +317,19 @@ __device__ __forceinline__ void contract_tile(const Args& a, const Smem& s, floa
   }
 }
 
-// IN/OUT: the two sides; PLAN: rows come from the row plan (Fock-side calls).
-template <int IN, int OUT>
-__global__ __launch_bounds__(kThreads) void transform_kernel(Args a) {
+// Waves per SIMD each variant is compiled for.  Programs only: registers
+// capped as far as they go without spills (the 25 KB tile of a 196-column row
+// allows six workgroups per CU).  With the dense loops the compiler's own
+// choice is faster (the 49 x 49 loop needs its registers).
+template <int IN, int OUT, bool DENSE>
+struct MinWaves {
+  static constexpr int value = DENSE ? 1 : (IN == ROWS ? (OUT == ROWS ? 6 : 5) : 4);
+};
+
+// IN/OUT: the two sides; PLAN: rows come from the row plan (Fock-side calls);
+// DENSE: see contract_tile.
+template <int IN, int OUT, bool DENSE>
+__global__ __launch_bounds__(kThreads, (MinWaves<IN, OUT, DENSE>::value)) void transform_kernel(Args a) {
   constexpr bool PLAN = IN == FOCK || OUT == FOCK;
   extern __shared__ float tile[];  // [kRows][tp]
   __shared__ Smem s;
@@ -320,9 +342,9 @@ __global__ __launch_bounds__(kThreads) void transform_kernel(Args a) {
   load_tile<IN, PLAN>(a, s, tile, r0, nrows);
   __syncthreads();
   if (PLAN && a.kind_blocks != nullptr)
-    contract_tile<true>(a, s, tile);
+    contract_tile<true, DENSE>(a, s, tile);
   else
-    contract_tile<false>(a, s, tile);
+    contract_tile<false, DENSE>(a, s, tile);
   __syncthreads();
   store_tile<OUT, PLAN>(a, s, tile, r0, nrows);
 }
@@ -380,7 +402,7 @@ namespace {
 
 int check_tables(int t, int nblocks, const int32_t* blocks, const float* w, const int32_t* sched) {
   MALOQ_REQUIRE(t > 0 && nblocks > 0, "bad sizes (t=%d, nblocks=%d)", t, nblocks);
-  MALOQ_REQUIRE(blocks && w && sched, "null CG table");
+  MALOQ_REQUIRE(blocks && sched, "null CG table");  // w may be NULL: every block has a program
   const int tp = t | 1;
   MALOQ_REQUIRE(static_cast<int64_t>(bt::kRows) * tp * 4 <= bt::kMaxTileBytes,
                 "label width %d too large for one LDS tile", t);
@@ -422,8 +444,12 @@ template <int IN, int OUT>
 int launch_transform(const bt::Args& a, void* stream, const char* name) {
   const int64_t groups = (a.R + bt::kRows - 1) / bt::kRows;
   const size_t shm = static_cast<size_t>(bt::kRows) * a.tp * sizeof(float);
-  hipLaunchKernelGGL((bt::transform_kernel<IN, OUT>), dim3(static_cast<unsigned>(groups)),
-                     dim3(kThreads), shm, static_cast<hipStream_t>(stream), a);
+  if (a.w != nullptr)
+    hipLaunchKernelGGL((bt::transform_kernel<IN, OUT, true>), dim3(static_cast<unsigned>(groups)),
+                       dim3(kThreads), shm, static_cast<hipStream_t>(stream), a);
+  else
+    hipLaunchKernelGGL((bt::transform_kernel<IN, OUT, false>), dim3(static_cast<unsigned>(groups)),
+                       dim3(kThreads), shm, static_cast<hipStream_t>(stream), a);
   return check_launch(name);
 }
 
@@ -500,6 +526,17 @@ extern "C" int maloq_irreps_to_fock(const float* irreps, const int32_t* perm_in,
   a.in = irreps;
   a.perm_in = perm_in;
   return launch_transform<bt::ROWS, bt::FOCK>(a, stream, "irreps -> fock");
+}
+
+extern "C" int maloq_basis_cg_block(int program, float* w, int n) {
+  MALOQ_REQUIRE(program >= 0 && program < cg::kPrograms, "CG program %d outside 0..%d", program,
+                cg::kPrograms - 1);
+  const int l1 = (program >> 2) & 3, l2 = program & 3;
+  const int size = (2 * l1 + 1) * (2 * l2 + 1);
+  MALOQ_REQUIRE(w != nullptr && n == size, "CG program %d is %d x %d (got n = %d)", program, size, size, n);
+  for (int i = 0; i < size * size; ++i) w[i] = 0.f;
+  for (int e = cg::kFirst[program]; e < cg::kFirst[program + 1]; ++e) w[cg::kRow[e] * size + cg::kCol[e]] = cg::kVal[e];
+  return MALOQ_OK;
 }
 
 extern "C" int maloq_matrix2label(float* fock, int64_t ld, const int64_t* data_offsets,

@@ -103,7 +103,7 @@ def _(msg, perm, seg_ptr, num_segments):
 
 # --------------------------------------------------------- basis transform
 @custom_op("maloq_hip::label_transform", mutates_args=())
-def label_transform(x: Tensor, blocks: Tensor, w: Tensor, sched: Tensor, perm_in: Optional[Tensor],
+def label_transform(x: Tensor, blocks: Tensor, w: Optional[Tensor], sched: Tensor, perm_in: Optional[Tensor],
                     perm_out: Optional[Tensor], num_blocks: int) -> Tensor:
     _lib.require_cuda(x)
     xc = x.contiguous()
@@ -123,7 +123,7 @@ def get_net_out(decomp, H: Tensor) -> Tensor:
     """``e3TensorDecomp.get_net_out`` (utils_tensor_decomp.py:163-169) as the op,
     with the tables of a :class:`maloq_amd.basis_transform.HipE3TensorDecomp`."""
     decomp._check(H, decomp.total_h_dim)
-    return label_transform(H, decomp._blocks, decomp._w_fwd, decomp._sched, None, decomp._perm, decomp.num_blocks)
+    return label_transform(H, decomp._blocks_fwd, decomp._wk_fwd, decomp._sched, None, decomp._perm, decomp.num_blocks)
 
 
 def get_H(decomp, net_out: Tensor) -> Tensor:
@@ -137,13 +137,13 @@ class _GetHOp(torch.autograd.Function):
     @staticmethod
     def forward(ctx, net_out, decomp):
         ctx.decomp = decomp
-        return label_transform(net_out, decomp._blocks, decomp._w_inv, decomp._sched, decomp._perm, None,
+        return label_transform(net_out, decomp._blocks_inv, decomp._wk_inv, decomp._sched, decomp._perm, None,
                                decomp.num_blocks)
 
     @staticmethod
     def backward(ctx, g):
         d = ctx.decomp
-        return label_transform(g.contiguous(), d._blocks, d._w_adj, d._sched, None, d._perm, d.num_blocks), None
+        return label_transform(g.contiguous(), d._blocks_adj, d._wk_adj, d._sched, None, d._perm, d.num_blocks), None
 
 
 # ----------------------------------------------------------- message block
