@@ -96,8 +96,13 @@ __global__ __launch_bounds__(256) void dw_kernel(DwArgs a) {
   __shared__ alignas(16) char smem[2 * Cfg::STAGE];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t ntiles = a.tile0[a.ngroups];
-  const int64_t split = blockIdx.x / ntiles;
-  const int64_t t = blockIdx.x % ntiles;
+  // XCD-aware order, as in dw_tr_kernel: the tiles of one split (which read
+  // the same dZ and Y rows) run on one XCD and share its L2
+  const int64_t per = gridDim.x >> 3;
+  const int64_t wid = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (wid >= ntiles * a.splits) return;  // whole workgroup, before any barrier
+  const int64_t split = wid / ntiles;
+  const int64_t t = wid % ntiles;
   int g = 0;
   while (g + 1 < a.ngroups && t >= a.tile0[g + 1]) ++g;
   const int64_t lt = t - a.tile0[g];
@@ -483,8 +488,8 @@ extern "C" int maloq_message_dw(int dtype, int lmax, int mmax, int gate, const v
   a.y = y;
   a.part = partials;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // dw_tr_kernel maps workgroups to work items per XCD (grid a multiple of 8)
-  const int64_t grid = tr ? (a.tile0[a.ngroups] * splits + 7) / 8 * 8 : a.tile0[a.ngroups] * splits;
+  // both kernels map workgroups to work items per XCD (grid a multiple of 8)
+  const int64_t grid = (a.tile0[a.ngroups] * splits + 7) / 8 * 8;
   MALOQ_REQUIRE(grid < (int64_t(1) << 31), "grid too large");
   if (tr)
     hipLaunchKernelGGL(dw_tr_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);

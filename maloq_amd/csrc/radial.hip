@@ -851,6 +851,7 @@ __device__ __forceinline__ v4s16 tr_read(const char* lds) {
 
 constexpr int DO_T = 128;   // outputs per workgroup tile
 constexpr int DO_KE = 32;   // edges per step
+constexpr int DO_KB = 8;    // fp32: two-edge MFMA steps per register batch
 
 template <class TM>
 __global__ __launch_bounds__(NT) void radial_dwo_kernel(Args a);
@@ -964,8 +965,9 @@ __global__ __launch_bounds__(NT) void radial_dwo_kernel<BF16>(Args a) {
   }
 }
 
-template <>
-__global__ __launch_bounds__(NT) void radial_dwo_kernel<F32>(Args a) {
+// fp32, NNT = c_H / 32 column tiles of u_H.
+template <int NNT>
+__global__ __launch_bounds__(NT) void radial_dwo_f32_kernel(Args a) {
   // 32x32x2 fp32 MFMA: lane i supplies A[o = i%32][edge i/32] and B[edge i/32][j = i%32],
   // both straight from the natural rows
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -979,8 +981,7 @@ __global__ __launch_bounds__(NT) void radial_dwo_kernel<F32>(Args a) {
   const int64_t ee = (eb + a.e_per_split) < a.E ? (eb + a.e_per_split) : a.E;
   const float* G = reinterpret_cast<const float*>(a.grad);
   const float* U = reinterpret_cast<const float*>(a.save);
-  constexpr int NNT = MAXC / 32;
-  const int nnt = cH / 32;
+  constexpr int nnt = NNT;
   f32x16 acc[NNT], accb;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
@@ -989,17 +990,39 @@ __global__ __launch_bounds__(NT) void radial_dwo_kernel<F32>(Args a) {
     for (int nt = 0; nt < NNT; ++nt) acc[nt][r] = 0.f;
   }
   const int h = lane >> 5;
-  for (int64_t e = eb; e < ee; e += 2) {
-    const int64_t er = e + h;
-    const bool ok = er < ee;
-    const float av = ok ? G[er * cout + o] : 0.f;
-    accb = __builtin_amdgcn_mfma_f32_32x32x2f32(av, 1.0f, accb, 0, 0, 0);
+  // DO_KB two-edge MFMA steps per batch; the loads of the next batch are in
+  // flight while the MFMAs of this one run (two register buffers)
+  float av[2][DO_KB], bv[2][DO_KB][NNT];
+  auto load = [&](int buf, int64_t e0) {
 #pragma unroll
-    for (int nt = 0; nt < NNT; ++nt)
-      if (nt < nnt) {
-        const float bv = ok ? U[er * cH + 32 * nt + (lane & 31)] : 0.f;
-        acc[nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc[nt], 0, 0, 0);
-      }
+    for (int k = 0; k < DO_KB; ++k) {
+      const int64_t er = e0 + 2 * k + h;
+      const bool ok = er < ee;
+      av[buf][k] = ok ? G[er * cout + o] : 0.f;
+#pragma unroll
+      for (int nt = 0; nt < NNT; ++nt)
+        bv[buf][k][nt] = (ok && nt < nnt) ? U[er * cH + 32 * nt + (lane & 31)] : 0.f;
+    }
+  };
+  auto step = [&](int buf) {
+#pragma unroll
+    for (int k = 0; k < DO_KB; ++k) {
+      accb = __builtin_amdgcn_mfma_f32_32x32x2f32(av[buf][k], 1.0f, accb, 0, 0, 0);
+#pragma unroll
+      for (int nt = 0; nt < NNT; ++nt)
+        if (nt < nnt) acc[nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[buf][k], bv[buf][k][nt], acc[nt], 0, 0, 0);
+    }
+  };
+  constexpr int64_t BE = 2 * DO_KB;  // edges per batch
+  const int64_t nb = ee > eb ? (ee - eb + BE - 1) / BE : 0;
+  if (nb > 0) load(0, eb);
+  for (int64_t b = 0; b < nb; b += 2) {
+    if (b + 1 < nb) load(1, eb + (b + 1) * BE);
+    step(0);
+    if (b + 1 < nb) {
+      if (b + 2 < nb) load(0, eb + (b + 2) * BE);
+      step(1);
+    }
   }
   float* part = a.part + split * a.pstride;
   const int ob = ot * DO_T + 32 * wave;
@@ -1323,7 +1346,12 @@ extern "C" int maloq_radial_bwd(int dtype, int nhidden, const int* widths, const
   if (dtype == 1)
     hipLaunchKernelGGL(radial_dwo_kernel<BF16>, dim3(static_cast<unsigned>(not_ * splits)), dim3(NT), 0, s, a);
   else
-    hipLaunchKernelGGL(radial_dwo_kernel<F32>, dim3(static_cast<unsigned>(not_ * splits)), dim3(NT), 0, s, a);
+    switch (a.c[a.nh] / 32) {
+      case 1: hipLaunchKernelGGL(radial_dwo_f32_kernel<1>, dim3(static_cast<unsigned>(not_ * splits)), dim3(NT), 0, s, a); break;
+      case 2: hipLaunchKernelGGL(radial_dwo_f32_kernel<2>, dim3(static_cast<unsigned>(not_ * splits)), dim3(NT), 0, s, a); break;
+      case 3: hipLaunchKernelGGL(radial_dwo_f32_kernel<3>, dim3(static_cast<unsigned>(not_ * splits)), dim3(NT), 0, s, a); break;
+      default: hipLaunchKernelGGL(radial_dwo_f32_kernel<4>, dim3(static_cast<unsigned>(not_ * splits)), dim3(NT), 0, s, a); break;
+    }
   rc = check_launch("radial_dwo_kernel");
   if (rc) return rc;
   return reduce(partials, po, splits, po, partials + splits * po, grad_out_weight,

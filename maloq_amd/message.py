@@ -572,10 +572,15 @@ def message_weight_grad(dz, y, lmax, mmax, c_out, c_in, splits=None, num_edges=N
                          for r in [lmax + 1] + [2 * (lmax - m + 1) for m in range(1, mmax + 1)])
             splits = max(1, min(64, 256 // ntiles, -(-E // 128)))
         else:
-            # about 640 workgroups of 128 x 128 output tiles, >= 1024 edges per split
+            # 128 x 128 output tiles: the split count that balances the
+            # workgroups over the compute units (the busiest CU runs
+            # ceil(tiles * splits / CUs) of them, each 1 / splits of the edges),
+            # at most three per CU, >= 1024 edges per split
             ntiles = sum(-(-r * c_out // 128) * -(-r * c_in // 128)
                          for r in [lmax + 1] + [2 * (lmax - m + 1) for m in range(1, mmax + 1)])
-            splits = max(1, min(16, round(640 / ntiles), E // 1024))
+            cus = torch.cuda.get_device_properties(dz.device).multi_processor_count
+            cands = [s for s in range(1, 17) if ntiles * s <= 3 * cus and s <= max(1, E // 1024)] or [1]
+            splits = min(cands, key=lambda s: (-(-ntiles * s // cus) / s, -s))
     lib = _lib.load()
     parts = torch.empty(max(1, lib.maloq_message_dw_partials_floats(lmax, mmax, int(gate), c_out, c_in,
                                                                     splits)),

@@ -55,7 +55,7 @@ def _close(got, ref, tol, what):
 
 
 CASES = [((8, 64, 64, 1536), 1000), ((8, 32, 192), 37), ((16, 64, 32, 64, 256), 130), ((8, 64, 64, 1536), 64),
-         ((4, 128, 384), 200)]
+         ((4, 128, 384), 200), ((8, 96, 256), 333)]
 
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
