@@ -13,15 +13,17 @@ namespace msg {
 //     extra accumulators -- its gate rows are an extra input row type -- so it
 //     keeps the 64-edge tiles at lmax <= 4);
 //   mmax = lmax (every output degree keeps all 2l + 1 row types, d' = d):
-//     32-edge tiles; at lmax > 4, or gated with an accumulating forward (the
-//     gate rows are extra accumulators), one workgroup per CU, so a wave has
-//     512 registers (accumulators in AGPRs) instead of spilling.
+//     32-edge tiles;
+//   one workgroup per CU, so that a wave has 512 registers (accumulators in
+//     AGPRs) instead of spilling: every lmax > 4 kernel (at two per CU the
+//     lmax-6 kernels spilled 128-916 bytes per lane), and at mmax = lmax the
+//     gated accumulating forwards (the gate rows are extra accumulators).
 template <int L, int M, bool GATE, int MODE = FWD>
 struct Cfg {
   static constexpr int NW = 4;
   static constexpr bool FULL = M == L && L > 2;
   static constexpr int RT = FULL ? 1 : ((L <= 4 && (!GATE || MODE == BWD_DX)) ? 2 : 1);
-  static constexpr int MINB = (FULL && (L > 4 || (GATE && (MODE == FWD || MODE == FWD_EDGE)))) ? 1 : 2;
+  static constexpr int MINB = (L > 4 || (FULL && GATE && (MODE == FWD || MODE == FWD_EDGE))) ? 1 : 2;
 };
 
 inline int tile_edges(int lmax, int mmax, int gate, int mode = FWD) {
