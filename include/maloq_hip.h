@@ -164,6 +164,37 @@ int maloq_matrix2label(float* fock, int64_t ld, const int64_t* data_offsets,
                        const int32_t* tmpl_ptr, const int32_t* tmpl, float* target,
                        int64_t target_ld, int forward, void* stream);
 
+/* ------------------------------------------------ Fock irreps head -- */
+
+/* The gated nonlinearity of Fock_Irreps_Head.process (helm/esen_osh.py:986-1005)
+ * on backbone features x [R, d, c] (d = (lmax+1)^2, l-major rows, fp32) and the
+ * scalar linear's output scalars [R, c + lmax c]:
+ *   out[r, 0, k] = scalars[r, k];
+ *   out[r, l^2 + m, k] = cst sigmoid(scalars[r, c + (l-1) c + k]) x[r, l^2 + m, k], l >= 1
+ * (cst: the normalisation of e3nn's Gate activation).  out [R, d, c].  Replaces
+ * lin_scalars' split + Gate (e3nn.nn.Gate with sigmoid gates) of the reference. */
+int maloq_irreps_gate_fwd(const float* x, int64_t num_rows, int lmax, int c, const float* scalars, float cst,
+                          float* out, void* stream);
+
+/* Its gradient: grad_x [R, d, c] (row 0 is set to zero: x's l = 0 reaches the
+ * output only through the scalar linear) and grad_scalars [R, c + lmax c]. */
+int maloq_irreps_gate_bwd(const float* x, int64_t num_rows, int lmax, int c, const float* scalars, float cst,
+                          const float* grad_out, float* grad_x, float* grad_scalars, void* stream);
+
+/* out[r, k] = src[k] >= 0 ? sign[k] in[r, src[k]] : 0 for k < t (row strides
+ * ld_in, ld_out): the head's output permutation to label order
+ * (x_out[:, output_permutation], esen_osh.py:909-914, 948-953) and, with the parity
+ * multipliers as signs, expand_reduced_node (:1055-1064). */
+int maloq_gather_columns(const float* in, int64_t ld_in, int64_t num_rows, const int32_t* src, const float* sign,
+                         int t, float* out, int64_t ld_out, void* stream);
+
+/* The gradient of that gather: grad_in[r, s] = sum over k in [ptr[s], ptr[s+1])
+ * of sign[k] grad_out[r, cols[k]] (the output columns that read input column s,
+ * CSR by input column, summed in a fixed order). */
+int maloq_scatter_columns(const float* grad_out, int64_t ld_out, int64_t num_rows, const int32_t* ptr,
+                          const int32_t* cols, const float* sign, int s, float* grad_in, int64_t ld_in,
+                          void* stream);
+
 /* ------------------------------------------- label-side caller hooks -- */
 
 /* labels[r][cols[k]] += sign * means[atomic_numbers[r]][k] for r < num_rows,

@@ -1,0 +1,302 @@
+"""Fock_Irreps_Head on the GPU: node and edge embeddings -> irreps labels.
+
+The reference's output head (helm/esen_osh.py:522-1064) maps the backbone's
+[rows, (lmax+1)^2, C] features to the label irreps of every orbital pair:
+``stack_irreps`` regroups the features by degree, ``process`` applies
+
+    s = Linear(C x 0e -> (C + L C) x 0e)(x_l=0)            (lin_scalars_learnable)
+    g = [s[:C], Gate(sigmoid(s[C:]), x_l>=1)]                (e3nn Gate)
+    y_l = Linear(C x le -> mul_l x le)(g_l),  l = 0..L       (lin_out_layers)
+
+and the l-sorted result is permuted to the labels' irreps order (and, with
+reduce_node, expanded from the node-reduced irreps by index and parity sign).
+
+Here the features stay in the backbone's l-major layout (no stacked copy):
+the scalar and per-l linears are plain GEMMs on the library (torch.matmul ->
+hipBLASLt); the gate is ``maloq_irreps_gate_fwd`` / ``_bwd``; and one
+``maloq_gather_columns`` does the per-l transpose to e3nn's channel-major
+layout, the output permutation and the node expansion together (its gradient
+is the fixed-order ``maloq_scatter_columns``).  Parameter names follow the
+reference (e3nn Linear's flat ``weight`` [mul_in * mul_out] and ``bias``), so
+state dicts load.  reduce_edge is not carried (it raises).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+from torch import nn
+
+from . import _lib
+
+
+def _normalize2mom_sigmoid():
+    """e3nn's normalize2mom constant for sigmoid: E[sigmoid(z)^2]^-1/2 over 10^6
+    float64 N(0, 1) draws of a CPU generator seeded 0 (as e3nn computes it)."""
+    gen = torch.Generator(device="cpu").manual_seed(0)
+    z = torch.randn(1_000_000, generator=gen, dtype=torch.float64)
+    cst = torch.sigmoid(z).pow(2).mean().pow(-0.5).item()
+    return 1.0 if abs(cst - 1.0) < 1e-4 else cst
+
+
+_CST = None
+
+
+def _cst():
+    global _CST
+    if _CST is None:
+        _CST = _normalize2mom_sigmoid()
+    return _CST
+
+
+def _irreps_ls(irreps):
+    """The degree of every 1x le entry of an irreps (string "1x0e+1x1e+...",
+    an e3nn / maloq_amd Irreps, or (mul, (l, p)) pairs), mul expanded."""
+    if isinstance(irreps, str):
+        out = []
+        for term in irreps.replace(" ", "").split("+"):
+            if not term:
+                continue
+            mul, ir = term.split("x") if "x" in term else ("1", term)
+            out += [int(ir[:-1])] * int(mul)
+        return out
+    out = []
+    for mul, ir in irreps:
+        l = ir.l if hasattr(ir, "l") else int(ir[0])
+        out += [int(l)] * int(mul)
+    return out
+
+
+def _product_ls(l1, l2, kind="all"):
+    l3s = range(abs(l1 - l2), l1 + l2 + 1)
+    if kind == "even":
+        return [l for l in l3s if l % 2 == 0]
+    if kind == "odd":
+        return [l for l in l3s if l % 2 == 1]
+    return list(l3s)
+
+
+def _nodereduced_ls(ls_list, intra):
+    """make_irreps_nodereduced (esen_osh.py:697-722): upper-triangle shell pairs,
+    and on the diagonal the even irreps only with reduce_node_intra."""
+    out = []
+    for i, li in enumerate(ls_list):
+        for j, lj in enumerate(ls_list):
+            if i == j:
+                out += _product_ls(li, lj, "even" if intra else "all")
+            elif i < j:
+                out += _product_ls(li, lj)
+    return out
+
+
+def _expand_tables(ls_list, intra):
+    """get_reduced_to_all_indices / get_parity_multiplier (irreps_utils.py:163-211):
+    label column -> node-reduced column (-1: zero) and its sign."""
+    red, idx = {}, 0
+    for i, li in enumerate(ls_list):
+        for j, lj in enumerate(ls_list):
+            if i <= j:
+                for l in _product_ls(li, lj, "even" if (i == j and intra) else "all"):
+                    red[(i, j, l)] = idx
+                    idx += 2 * l + 1
+    src, sign = [], []
+    for i, li in enumerate(ls_list):
+        for j, lj in enumerate(ls_list):
+            for l in _product_ls(li, lj):
+                n = 2 * l + 1
+                key = (i, j, l) if i <= j else (j, i, l)
+                if key not in red:  # odd self-interaction irreps removed by reduce_node_intra
+                    src += [-1] * n
+                    sign += [0.0] * n
+                    continue
+                flip = i > j and ((l % 2 == 0) if (li + lj) % 2 == 1 else (l % 2 == 1))
+                src += range(red[key], red[key] + n)
+                sign += [-1.0 if flip else 1.0] * n
+    return np.asarray(src, np.int64), np.asarray(sign, np.float32)
+
+
+def _label_to_z(ls, lmax):
+    """For irreps entries 1x l e in the order ``ls`` (the labels'), the column of
+    the GEMM output buffer Z each label column reads: Z holds per degree l the
+    block [2l+1, mul_l] (m-major, straight from the GEMM), and the k-th entry of
+    degree l (in label order) is copy k -- the l-sorted order of get_output_permutation
+    (esen_osh.py:833-880)."""
+    mul = [sum(1 for l in ls if l == k) for k in range(lmax + 1)]
+    zoff = np.concatenate([[0], np.cumsum([(2 * l + 1) * mul[l] for l in range(lmax + 1)])])
+    seen = [0] * (lmax + 1)
+    cols = []
+    for l in ls:
+        v = seen[l]
+        seen[l] += 1
+        cols += [int(zoff[l] + m * mul[l] + v) for m in range(2 * l + 1)]
+    return np.asarray(cols, np.int64), mul, int(zoff[-1])
+
+
+class _ColumnMap:
+    """Device tables of a signed column gather out[:, t] = sign[t] Z[:, src[t]]
+    and the CSR of its transpose (for the fixed-order gradient)."""
+
+    def __init__(self, src, sign, width, device):
+        src = np.asarray(src, np.int64)
+        sign = np.asarray(sign, np.float32)
+        self.t, self.width = len(src), int(width)
+        self.src = torch.as_tensor(src.astype(np.int32), device=device)
+        self.sign = torch.as_tensor(sign, device=device)
+        keep = np.nonzero((src >= 0) & (sign != 0))[0]
+        order = keep[np.argsort(src[keep], kind="stable")]
+        counts = np.bincount(src[order], minlength=self.width) if len(order) else np.zeros(self.width, np.int64)
+        self.ptr = torch.as_tensor(np.concatenate([[0], np.cumsum(counts)]).astype(np.int32), device=device)
+        self.cols = torch.as_tensor(order.astype(np.int32), device=device)
+        self.csign = torch.as_tensor(sign[order], device=device)
+
+
+class _Gather(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, z, cmap):
+        z = z.contiguous()
+        out = torch.empty(z.shape[0], cmap.t, device=z.device, dtype=torch.float32)
+        _lib.call("maloq_gather_columns", z, z.shape[1], z.shape[0], cmap.src, cmap.sign, cmap.t, out, cmap.t,
+                  _lib.stream_of(z.device))
+        ctx.cmap = cmap
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        cmap = ctx.cmap
+        g = g.contiguous()
+        dz = torch.empty(g.shape[0], cmap.width, device=g.device, dtype=torch.float32)
+        _lib.call("maloq_scatter_columns", g, cmap.t, g.shape[0], cmap.ptr, cmap.cols, cmap.csign, cmap.width, dz,
+                  cmap.width, _lib.stream_of(g.device))
+        return dz, None
+
+
+class _GateFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, s, lmax, cst):
+        out = torch.empty_like(x)
+        _lib.call("maloq_irreps_gate_fwd", x, x.shape[0], lmax, x.shape[2], s, cst, out, _lib.stream_of(x.device))
+        ctx.save_for_backward(x, s)
+        ctx.lmax, ctx.cst = lmax, cst
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        x, s = ctx.saved_tensors
+        g = g.contiguous()
+        dx, ds = torch.empty_like(x), torch.empty_like(s)
+        _lib.call("maloq_irreps_gate_bwd", x, x.shape[0], ctx.lmax, x.shape[2], s, ctx.cst, g, dx, ds,
+                  _lib.stream_of(x.device))
+        return dx, ds, None, None
+
+
+class E3Linear(nn.Module):
+    """e3nn.o3.Linear for mul_in x le -> mul_out x le (one path): ``weight`` flat
+    [mul_in * mul_out] (viewed [mul_in, mul_out], N(0, 1) init), output divided
+    by sqrt(mul_in); ``bias`` [mul_out] (zeros) on scalar outputs, empty else."""
+
+    def __init__(self, mul_in, mul_out, l, biases=True):
+        super().__init__()
+        self.mul_in, self.mul_out, self.l = mul_in, mul_out, l
+        self.weight = nn.Parameter(torch.randn(mul_in * mul_out))
+        self.bias = nn.Parameter(torch.zeros(mul_out if (biases and l == 0) else 0))
+
+    def matrix(self):
+        return self.weight.view(self.mul_in, self.mul_out) / math.sqrt(self.mul_in)
+
+
+class _GateModule(nn.Module):
+    """Placeholder for the reference's e3nn Gate (no parameters); the gate runs
+    in ``maloq_irreps_gate_fwd``."""
+
+
+class Fock_Irreps_Head(nn.Module):
+    """esen_osh.py:522-1064 (reduce_edge=False).  forward(emb, batch) ->
+    (node_outputs [spins, N, T], edge_outputs [spins, E, T]) from
+    emb["node_embeddings"] [N, (lmax+1)^2, C] and emb["edge_embeddings"]."""
+
+    def __init__(self, irreps_in, irreps_out, lmax, sphere_channels, reduce_edge=False, ls_list=None,
+                 open_shell=False, reduce_node=False, reduce_node_intra=False, orbital_basis=None):
+        super().__init__()
+        if reduce_edge:
+            raise NotImplementedError("reduce_edge is not carried by the HIP output head")
+        C, L = int(sphere_channels), int(lmax)
+        self.sphere_channels, self.lmax = C, L
+        self.reduce_node, self.reduce_node_intra, self.reduce_edge = reduce_node, reduce_node_intra, False
+        self.irreps_out = irreps_out
+        self.ls_list = None if ls_list is None else [int(l) % 10 for l in ls_list]
+        self.num_spins = 2 if open_shell else 1
+        self._ls_out = _irreps_ls(irreps_out)
+        if max(self._ls_out) > L:
+            raise ValueError(f"irreps_out reaches l = {max(self._ls_out)} > lmax = {L}")
+        in_ls = _irreps_ls(irreps_in)
+        if sorted(set(in_ls)) != list(range(L + 1)) or any(in_ls.count(l) != C for l in range(L + 1)):
+            raise ValueError("irreps_in must be sphere_channels x le for l = 0..lmax")
+        if reduce_node:
+            if self.ls_list is None:
+                raise ValueError("reduce_node needs ls_list")
+            self._ls_node = _nodereduced_ls(self.ls_list, reduce_node_intra)
+        self.lin_scalars_learnable = nn.ModuleList([E3Linear(C, C + L * C, 0) for _ in range(self.num_spins)])
+        self.gate = nn.ModuleList([_GateModule() for _ in range(self.num_spins)])
+
+        def layers(ls):
+            mul = [sum(1 for x in ls if x == l) for l in range(L + 1)]
+            return nn.ModuleList([nn.ModuleList([E3Linear(C, mul[l], l) for l in range(L + 1)])
+                                  for _ in range(self.num_spins)])
+        if reduce_node:
+            self.node_lin_out_layers = layers(self._ls_node)
+            self.edge_lin_out_layers = layers(self._ls_out)
+        else:
+            self.lin_out_layers = layers(self._ls_out)
+        self._maps = {}
+
+    # ---------------------------------------------------------------- tables
+    def _column_map(self, stream, device):
+        key = (stream, str(device))
+        if key not in self._maps:
+            if stream == "node" and self.reduce_node:
+                zcol, _, width = _label_to_z(self._ls_node, self.lmax)
+                red_src, sign = _expand_tables(self.ls_list, self.reduce_node_intra)
+                src = np.where(red_src >= 0, zcol[np.maximum(red_src, 0)], -1)
+            else:
+                src, _, width = _label_to_z(self._ls_out, self.lmax)
+                sign = np.ones(len(src), np.float32)
+            if len(src) != sum(2 * l + 1 for l in self._ls_out):
+                raise ValueError("the reduced node irreps do not expand to irreps_out (ls_list mismatch)")
+            self._maps[key] = _ColumnMap(src, sign, width, device)
+        return self._maps[key]
+
+    # ---------------------------------------------------------------- compute
+    def _process(self, x, lin_layers, spin, stream):
+        """s = lin_scalars(x_0), gate, per-l linear into Z [rows, sum_l (2l+1) mul_l]
+        (m-major per degree), then the label gather."""
+        _lib.require_cuda(x)
+        if x.dtype != torch.float32 or x.dim() != 3 or x.shape[1] != (self.lmax + 1) ** 2 \
+                or x.shape[2] != self.sphere_channels:
+            raise ValueError(f"embeddings must be float32 [rows, {(self.lmax + 1) ** 2}, {self.sphere_channels}]")
+        x = x.contiguous()
+        ls = self.lin_scalars_learnable[spin]
+        s = torch.addmm(ls.bias, x[:, 0, :], ls.matrix())
+        g = _GateFn.apply(x, s.contiguous(), self.lmax, _cst())
+        zs = []
+        for l, lin in enumerate(lin_layers):
+            if lin.mul_out == 0:
+                continue
+            y = torch.matmul(g[:, l * l:(l + 1) ** 2, :], lin.matrix())   # [rows, 2l+1, mul_l]
+            if l == 0 and lin.bias.numel():
+                y = y + lin.bias
+            zs.append(y.reshape(x.shape[0], -1))
+        z = torch.cat(zs, dim=1)
+        return _Gather.apply(z, self._column_map(stream, x.device))
+
+    def forward(self, emb, batch=None):
+        node_x, edge_x = emb["node_embeddings"], emb["edge_embeddings"]
+        node_out, edge_out = [], []
+        for spin in range(self.num_spins):
+            if self.reduce_node:
+                node_out.append(self._process(node_x, self.node_lin_out_layers[spin], spin, "node"))
+                edge_out.append(self._process(edge_x, self.edge_lin_out_layers[spin], spin, "edge"))
+            else:
+                node_out.append(self._process(node_x, self.lin_out_layers[spin], spin, "common"))
+                edge_out.append(self._process(edge_x, self.lin_out_layers[spin], spin, "common"))
+        return torch.stack(node_out), torch.stack(edge_out)
