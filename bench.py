@@ -769,6 +769,38 @@ def torch_randn_like_nodes(ew):
     return torch.randn(ew["x"].shape, generator=gen).to(ew["x"].device)
 
 
+def library_gemm_ceiling(dtypes=("bf16", "fp32"), reps=20):
+    """The SO(2) per-m GEMMs of each message configuration as plain library
+    GEMMs (torch.matmul -> hipBLASLt), no rotation or scatter: Y_m [E, k] x
+    W_m [k, k] with k = (L+1) C for m = 0 and 2 (L-m+1) C for m > 0 (the +-m
+    complex mix as one real GEMM) -- the same FLOPs as the fused kernel's SO(2)
+    part.  The achievable rate of the library on these shapes."""
+    import torch
+    dev = torch.device("cuda:0")
+    out = {}
+    for cfg, (gname, L, M, C, gate, _) in MESSAGE_CONFIGS.items():
+        E = _graph(gname).src.shape[0]
+        for dtn in dtypes:
+            dt = torch.bfloat16 if dtn == "bf16" else torch.float32
+            gen = torch.Generator(device="cpu").manual_seed(0)
+            parts, tot_f, tot_t = {}, 0.0, 0.0
+            for m in range(M + 1):
+                k = (L - m + 1) * C * (1 if m == 0 else 2)
+                kn = k + (L * C if (m == 0 and gate) else 0)   # gated: the gate outputs ride on m = 0
+                y = torch.randn(E, k, generator=gen).to(dev, dt)
+                w = torch.randn(k, kn, generator=gen).to(dev, dt)
+                tm = kernel_time_events(lambda y=y, w=w: torch.matmul(y, w), reps)
+                fl = 2.0 * E * k * kn
+                parts[f"m{m}"] = {"shape": [E, k, kn], "us": tm * 1e6, "tflops": fl / tm / 1e12}
+                tot_f += fl
+                tot_t += tm
+                del y, w
+            peak = PEAK_BF16 if dtn == "bf16" else PEAK_FP32
+            out[f"{cfg}_{dtn}"] = {"us": tot_t * 1e6, "tflops": tot_f / tot_t / 1e12,
+                                   "frac_of_peak": tot_f / tot_t / peak, "per_m": parts}
+    return out
+
+
 def profile_only(args):
     """Runs one piece of the path --reps times (for rocprofv3 passes)."""
     import torch
@@ -792,6 +824,8 @@ def profile_only(args):
             edgewise_step(ew)
     elif args.only == "rotate":
         rotation_leg(cpu=False)
+    elif args.only == "ceiling":
+        print(json.dumps(library_gemm_ceiling()), flush=True)
     elif args.only == "basis5":
         sw = sparse_basis_workload()
         sparse_basis_leg(sw, reps=args.reps)
@@ -828,7 +862,7 @@ def main(argv=None):
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-extras", action="store_true", help="headline only")
     ap.add_argument("--only", choices=["fwd", "step", "basis", "copy", "embed", "edgewise", "edgewise-step",
-                                       "rotate", "basis5"],
+                                       "rotate", "basis5", "ceiling"],
                     help="profiling mode: run one piece a few times and exit (no JSON line)")
     ap.add_argument("--cfg", default="config2", choices=sorted(MESSAGE_CONFIGS),
                     help="message-block configuration of --only fwd / step")
@@ -947,6 +981,8 @@ def main(argv=None):
                          "frac": fl / tg / PEAK_BF16, "flops_per_call": fl},
         }
         del gw
+        print("[bench] library GEMM ceiling of the SO(2) shapes ...", file=sys.stderr, flush=True)
+        result["library_gemm_ceiling"] = library_gemm_ceiling(("bf16",))
     if not args.no_cpu:
         print("[bench] CPU baseline ...", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_message_baseline()
