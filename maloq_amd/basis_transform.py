@@ -197,6 +197,10 @@ class HipE3TensorDecomp:
             # a reference e3TensorDecomp: read the permutation off its sort module
             eye = torch.eye(int(decomp_obj.in_slices[-1]), dtype=torch.float64)
             self.sort_perm = torch.argmax(decomp_obj.sort(eye.to(decomp_obj.device)).cpu(), dim=0).numpy()
+        if self.sort_perm is not None and not np.array_equal(np.sort(np.asarray(self.sort_perm)),
+                                                             np.arange(self.total_in_dim)):
+            # the kernels read and write every label column exactly once through it
+            raise ValueError("sort_perm must be a permutation of the label columns")
         tabs = cg_block_tables(decomp_obj)
         dev = self.device
         # one blocks table per direction: (n, col0, woff, compiled program or -1)
