@@ -4,6 +4,7 @@
 // kernel arguments, and the per-edge prep kernel (Wigner rows + rotation into
 // the edge frame).  The SO(2) GEMM with its inverse-rotation / segment-sum
 // epilogue is in message_gemm.h.
+#include <type_traits>
 #include <utility>
 
 #include "common.h"
@@ -325,6 +326,30 @@ template <>
 __device__ __forceinline__ void store_vec<F32, 4>(float* p, const float (&v)[4]) {
   *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
 }
+template <>
+__device__ __forceinline__ void store_vec<BF16, 4>(uint16_t* p, const float (&v)[4]) {
+  uint2 w;
+  w.x = f32_to_bf16(v[0]) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
+  w.y = f32_to_bf16(v[2]) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
+  *reinterpret_cast<uint2*>(p) = w;
+}
+
+// V elements of TM raw as one register vector (16 bytes, or 8 for 4 bf16).
+template <class TM, int V>
+struct RawVec {
+  using type = uint4;
+  static __device__ __forceinline__ void unpack(type v, float (&o)[V]) { unpack_vec<TM, V>(v, o); }
+};
+template <>
+struct RawVec<BF16, 4> {
+  using type = uint2;
+  static __device__ __forceinline__ void unpack(uint2 v, float (&o)[4]) {
+    o[0] = __uint_as_float(v.x << 16);
+    o[1] = __uint_as_float(v.x & 0xffff0000u);
+    o[2] = __uint_as_float(v.y << 16);
+    o[3] = __uint_as_float(v.y & 0xffff0000u);
+  }
+};
 
 // Edges and threads per prep workgroup (the grid is ceil(E / PREP_TE)).
 constexpr int PREP_TE = 16;
@@ -338,7 +363,10 @@ struct Prep {
   using PL = PairLayout<L, M>;
   static constexpr int WS = PL::WS;
   static constexpr int d = (L + 1) * (L + 1);
-  static constexpr int V = TM::VEC;
+  // channels per item: one 16-byte vector, or 4 bf16 where 8 channels of the
+  // widest degree's rows and outputs spill (lmax > 4 or mmax > 2)
+  static constexpr int V = (std::is_same_v<TM, BF16> && (L > 4 || M > 2)) ? 4 : TM::VEC;
+  using RV = RawVec<TM, V>;
 
   struct Smem {
     float J[jd_size(L)];
@@ -522,16 +550,29 @@ struct Prep {
       typename TM::raw* ro = a.r ? reinterpret_cast<typename TM::raw*>(a.r) + eid * P::DP * a.C + c0 : nullptr;
       const typename TM::raw* rp = a.rad ? reinterpret_cast<const typename TM::raw*>(a.rad) + eid * rw + c0 : nullptr;
       // all radial slots of this (edge, channel chunk) in flight at once: one
-      // memory latency per item instead of one per kept row
+      // memory latency per item instead of one per kept row.  Where holding
+      // them all beside the largest degree's x rows would not fit the register
+      // budget (and spilled: bf16 at lmax 6, mmax = lmax), each degree loads
+      // its own min(mmax, l) + 1 slots with its x rows instead.
       constexpr int NSLOT = rad_slot<L, M>(2 * M, L, 0, 1) + 1;  // sum_m (L - m + 1)
-      uint4 rr[NSLOT];
-      if (rp) {
+      constexpr bool ALL = NSLOT * 4 + (2 * L + 1) * V <= 120;
+      typename RV::type rr[ALL ? NSLOT : 1];
+      if (ALL && rp) {
 #pragma unroll
-        for (int k = 0; k < NSLOT; ++k) rr[k] = *reinterpret_cast<const uint4*>(rp + static_cast<int64_t>(k) * a.C);
+        for (int k = 0; k < NSLOT; ++k)
+          rr[k] = *reinterpret_cast<const typename RV::type*>(rp + static_cast<int64_t>(k) * a.C);
       }
       static_for<L + 1>([&](auto LI) {
         constexpr int l = decltype(LI)::value;
         constexpr int n = 2 * l + 1;
+        constexpr int NM = cmin(M, l) + 1;
+        typename RV::type rl[ALL ? 1 : NM];  // this degree's slots, by m
+        if (!ALL && rp) {
+#pragma unroll
+          for (int m = 0; m < (ALL ? 1 : NM); ++m)
+            rl[m] = *reinterpret_cast<const typename RV::type*>(
+                rp + static_cast<int64_t>(rad_slot<L, M>(2 * m, l, 0, 1)) * a.C);
+        }
         float xv[n][V];
 #pragma unroll
         for (int j = 0; j < n; ++j) load_vec<TX, V>(xg + (l * l + j) * xc, xv[j]);
@@ -550,7 +591,10 @@ struct Prep {
           if (ro) store_vec<TM, V>(ro + ro_off, o);
           if (rp) {
             float rv[V];
-            unpack_vec<TM, V>(rr[rad_slot<L, M>(q, l, 0, 1)], rv);
+            if constexpr (ALL)
+              RV::unpack(rr[rad_slot<L, M>(q, l, 0, 1)], rv);
+            else
+              RV::unpack(rl[(q + 1) >> 1], rv);
 #pragma unroll
             for (int c = 0; c < V; ++c) o[c] *= rv[c];
           }
