@@ -363,9 +363,10 @@ struct Prep {
   using PL = PairLayout<L, M>;
   static constexpr int WS = PL::WS;
   static constexpr int d = (L + 1) * (L + 1);
-  // channels per item: one 16-byte vector, or 4 bf16 where 8 channels of the
-  // widest degree's rows and outputs spill (lmax > 4 or mmax > 2)
-  static constexpr int V = (std::is_same_v<TM, BF16> && (L > 4 || M > 2)) ? 4 : TM::VEC;
+  // channels per item: 4 (16 bytes of fp32, 8 of bf16).  Eight bf16 channels
+  // per item spilled at lmax > 4 or mmax > 2 and ran 12 % slower at lmax 4
+  // (fewer resident waves).
+  static constexpr int V = std::is_same_v<TM, BF16> ? 4 : TM::VEC;
   using RV = RawVec<TM, V>;
 
   struct Smem {
