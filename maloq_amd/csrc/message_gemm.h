@@ -159,7 +159,6 @@ template <int L, int M, bool GATE, int NW, int RT, class TM, int MODE>
 struct Gemm {
   using P = GPlan<L, M, GATE, NW, RT, MODE>;
   static constexpr int TE = P::TE, NT = P::NT, KC = TM::KC;
-  static_assert(NW == 4, "the epilogue staging holds two waves per A stage");
   static constexpr int d = (L + 1) * (L + 1);
 
   struct Smem {
@@ -167,12 +166,18 @@ struct Gemm {
     int seg[TE];
     int eid[TE];
   };
-  // A stages (two distinct LDS objects, so the compiler can tell a stage being
-  // filled by DMA from the one being read); after the K loop they hold the
-  // epilogue's per-wave staging (two waves per stage).
+  // A stages (three distinct LDS objects, so the compiler can tell a stage
+  // being filled by DMA from the one being read); after the K loop they hold
+  // the epilogue's per-wave staging, WPS waves per stage (2 of 4 waves: st0
+  // and st1; 3 of 8 waves: all three).
   // per-wave epilogue staging: the 16-edge scan chunk or the 32 x 36 transpose tile
   static constexpr int PW = (P::CH * 64 > 32 * 36 ? P::CH * 64 : 32 * 36) * 4;
-  static constexpr int SB = (P::A_BYTES > 2 * PW) ? P::A_BYTES : 2 * PW;
+  static constexpr int WPS = (NW + 2) / 3;
+  static constexpr int SB = (P::A_BYTES > WPS * PW) ? P::A_BYTES : WPS * PW;
+  static __device__ __forceinline__ float* wave_staging(int wave, char* st0, char* st1, char* st2) {
+    const int k = wave / WPS;
+    return reinterpret_cast<float*>((k == 0 ? st0 : (k == 1 ? st1 : st2)) + (wave - k * WPS) * PW);
+  }
   typedef __attribute__((address_space(3))) void lds_void;
 
   // ------------------------------------------------------------ A operand
@@ -832,21 +837,21 @@ struct Gemm {
           if constexpr (GATE) {
             if (a.gsave != nullptr)
               save_pre<lo>(acc, s, a, cb,
-                           reinterpret_cast<float*>((wave < 2 ? st0 : st1) + (wave & 1) * PW), lane);
+                           wave_staging(wave, st0, st1, st2), lane);
             gate_act<lo>(acc);
           }
         } else if constexpr (RAD)
           radial<lo>(acc, s, a, cb,
-                     reinterpret_cast<float*>((wave < 2 ? st0 : st1) + (wave & 1) * PW), lane);
+                     wave_staging(wave, st0, st1, st2), lane);
         if constexpr (MODE == BWD_EDGE)
           store_gate_bwd<lo>(acc, s, a, cb,
-                             reinterpret_cast<float*>((wave < 2 ? st0 : st1) + (wave & 1) * PW), lane);
+                             wave_staging(wave, st0, st1, st2), lane);
         else if constexpr (MODE == FWD_EDGE)
           save_pre<lo, true>(acc, s, a, cb,
-                             reinterpret_cast<float*>((wave < 2 ? st0 : st1) + (wave & 1) * PW), lane);
+                             wave_staging(wave, st0, st1, st2), lane);
         else
           rotate_sum<W, lo>(acc, s, wsh, a, cb,
-                            reinterpret_cast<float*>((wave < 2 ? st0 : st1) + (wave & 1) * PW),
+                            wave_staging(wave, st0, st1, st2),
                             lane, endmask);
       }
     });

@@ -9,19 +9,26 @@ namespace msg {
 // workgroups per CU (the launch bound) for each shape:
 //   mmax < lmax, lmax <= 4 without gate: 4 waves x 64 edges, two workgroups
 //     per CU (256 registers per lane);
-//   gated, or lmax > 4: 4 waves x 32 edges (the gated input gradient has no
-//     extra accumulators -- its gate rows are an extra input row type -- so it
+//   gated, or lmax > 4: 32 edges (the gated input gradient has no extra
+//     accumulators -- its gate rows are an extra input row type -- so it
 //     keeps the 64-edge tiles at lmax <= 4);
 //   mmax = lmax (every output degree keeps all 2l + 1 row types, d' = d):
 //     32-edge tiles;
-//   one workgroup per CU, so that a wave has 512 registers (accumulators in
-//     AGPRs) instead of spilling: every lmax > 4 kernel (at two per CU the
-//     lmax-6 kernels spilled 128-916 bytes per lane), and at mmax = lmax the
-//     gated accumulating forwards (the gate rows are extra accumulators).
+//   one workgroup per CU: every lmax > 4 kernel (at two 4-wave workgroups per
+//     CU the lmax-6 kernels spilled 128-916 bytes per lane), and at mmax =
+//     lmax the gated accumulating forwards (the gate rows are extra
+//     accumulators).  At lmax > 4 with mmax < lmax that workgroup has 8 waves:
+//     a wave owns at most one output degree, fits 256 registers, and shares
+//     its SIMD with a second wave (13-14 % faster at lmax 6 than 4 waves with
+//     512 registers each); the other one-per-CU shapes keep 4 waves with
+//     their accumulators in AGPRs.
 template <int L, int M, bool GATE, int MODE = FWD>
 struct Cfg {
-  static constexpr int NW = 4;
   static constexpr bool FULL = M == L && L > 2;
+  // lmax > 4 with mmax < lmax: 8 waves, so a wave owns at most one degree and
+  // two waves share a SIMD (the one-workgroup-per-CU kernel otherwise has a
+  // single wave per SIMD to hide its latencies)
+  static constexpr int NW = (L > 4 && !FULL) ? 8 : 4;
   static constexpr int RT = FULL ? 1 : ((L <= 4 && (!GATE || MODE == BWD_DX)) ? 2 : 1);
   static constexpr int MINB = (L > 4 || (FULL && GATE && (MODE == FWD || MODE == FWD_EDGE))) ? 1 : 2;
 };
