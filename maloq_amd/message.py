@@ -566,19 +566,22 @@ def message_weight_grad(dz, y, lmax, mmax, c_out, c_in, splits=None, num_edges=N
         assert dz.shape[0] >= _lib.load().maloq_message_edge_rows(E) and y.shape[0] == dz.shape[0], \
             "bf16 weight gradient needs the padded workspaces"
     if splits is None:
+        # the kernel's groups (rows of dz, rows of y): m = 0, the stacked +-m of
+        # m = 1 .. mmax, and for a gated block its gate rows against y's m = 0 rows
+        groups = ([(lmax + 1, lmax + 1)] + [(2 * (lmax - m + 1),) * 2 for m in range(1, mmax + 1)]
+                  + ([(lmax, lmax + 1)] if gate else []))
+        cus = torch.cuda.get_device_properties(dz.device).multi_processor_count
         if dz.dtype == torch.bfloat16:
-            # 256 x 256 tiles, one workgroup per CU: about one wave of 256 workgroups
-            ntiles = sum(-(-r * c_out // 256) * -(-r * c_in // 256)
-                         for r in [lmax + 1] + [2 * (lmax - m + 1) for m in range(1, mmax + 1)])
-            splits = max(1, min(64, 256 // ntiles, -(-E // 128)))
+            # 256 x 256 tiles, one workgroup per CU: the most splits that keep
+            # every workgroup in one round
+            ntiles = sum(-(-rz * c_out // 256) * -(-ry * c_in // 256) for rz, ry in groups)
+            splits = max(1, min(64, cus // ntiles, -(-E // 128)))
         else:
             # 128 x 128 output tiles: the split count that balances the
             # workgroups over the compute units (the busiest CU runs
             # ceil(tiles * splits / CUs) of them, each 1 / splits of the edges),
             # at most three per CU, >= 1024 edges per split
-            ntiles = sum(-(-r * c_out // 128) * -(-r * c_in // 128)
-                         for r in [lmax + 1] + [2 * (lmax - m + 1) for m in range(1, mmax + 1)])
-            cus = torch.cuda.get_device_properties(dz.device).multi_processor_count
+            ntiles = sum(-(-rz * c_out // 128) * -(-ry * c_in // 128) for rz, ry in groups)
             cands = [s for s in range(1, 17) if ntiles * s <= 3 * cus and s <= max(1, E // 1024)] or [1]
             splits = min(cands, key=lambda s: (-(-ntiles * s // cus) / s, -s))
     lib = _lib.load()
