@@ -170,21 +170,24 @@ int maloq_matrix2label(float* fock, int64_t ld, const int64_t* data_offsets,
  * on backbone features x [R, d, c] (d = (lmax+1)^2, l-major rows, fp32) and the
  * scalar linear's output scalars [R, c + lmax c]:
  *   out[r, 0, k] = scalars[r, k];
- *   out[r, l^2 + m, k] = cst sigmoid(scalars[r, c + (l-1) c + k]) x[r, l^2 + m, k], l >= 1
- * (cst: the normalisation of e3nn's Gate activation).  out [R, d, c].  Replaces
- * lin_scalars' split + Gate (e3nn.nn.Gate with sigmoid gates) of the reference. */
+ *   out[r, l^2 + m, k] = cst f(scalars[r, c + (l-1) c + k]) x[r, l^2 + m, k], l >= 1
+ * with f = sigmoid (act 0) or, with reduce_edge (gates on |scalars|, tanh, so
+ * odd data stay odd: :625-629, 994-995), f(z) = tanh(|z|) (act 1); cst: the
+ * normalisation of e3nn's Gate activation.  out [R, d, c].  Replaces lin_scalars'
+ * split + Gate (e3nn.nn.Gate) of the reference. */
 int maloq_irreps_gate_fwd(const float* x, int64_t num_rows, int lmax, int c, const float* scalars, float cst,
-                          float* out, void* stream);
+                          int act, float* out, void* stream);
 
 /* Its gradient: grad_x [R, d, c] (row 0 is set to zero: x's l = 0 reaches the
  * output only through the scalar linear) and grad_scalars [R, c + lmax c]. */
 int maloq_irreps_gate_bwd(const float* x, int64_t num_rows, int lmax, int c, const float* scalars, float cst,
-                          const float* grad_out, float* grad_x, float* grad_scalars, void* stream);
+                          int act, const float* grad_out, float* grad_x, float* grad_scalars, void* stream);
 
 /* out[r, k] = src[k] >= 0 ? sign[k] in[r, src[k]] : 0 for k < t (row strides
  * ld_in, ld_out): the head's output permutation to label order
- * (x_out[:, output_permutation], esen_osh.py:909-914, 948-953) and, with the parity
- * multipliers as signs, expand_reduced_node (:1055-1064). */
+ * (x_out[:, output_permutation], esen_osh.py:909-914, 948-953), with the parity
+ * multipliers as signs expand_reduced_node (:1055-1064), and with reduce_edge the
+ * alpha and beta terms of the edge-pair remix (:915-937). */
 int maloq_gather_columns(const float* in, int64_t ld_in, int64_t num_rows, const int32_t* src, const float* sign,
                          int t, float* out, int64_t ld_out, void* stream);
 

@@ -30,8 +30,8 @@ SIGNATURES = {
     "maloq_rotate": [_i32, _i32, _i32, _p, _i32, _p, _i64, _p, _p, _p, _i32, _p, _p],
     "maloq_label_transform": [_p, _p, _p, _p, _i64, _i32, _i32, _p, _p, _p, _p],
     "maloq_basis_cg_block": [_i32, _p, _i32],
-    "maloq_irreps_gate_fwd": [_p, _i64, _i32, _i32, _p, ctypes.c_float, _p, _p],
-    "maloq_irreps_gate_bwd": [_p, _i64, _i32, _i32, _p, ctypes.c_float, _p, _p, _p, _p],
+    "maloq_irreps_gate_fwd": [_p, _i64, _i32, _i32, _p, ctypes.c_float, _i32, _p, _p],
+    "maloq_irreps_gate_bwd": [_p, _i64, _i32, _i32, _p, ctypes.c_float, _i32, _p, _p, _p, _p],
     "maloq_gather_columns": [_p, _i64, _i64, _p, _p, _i32, _p, _i64, _p],
     "maloq_scatter_columns": [_p, _i64, _i64, _p, _p, _p, _i32, _p, _i64, _p],
     "maloq_basis_row_meta": [_i64, _p, _p, _p, _p, _p, _i64, _p, _i32, _p, _p],

@@ -10,6 +10,9 @@
 //   g[b, 0, c]        = s[b, c]                                   (transformed l = 0)
 //   g[b, l^2 + m, c]  = cst sigmoid(s[b, C + (l-1) C + c]) x[b, l^2 + m, c]   (l >= 1)
 // (e3nn's Gate with normalised activation: cst = E[sigmoid(z)^2]^-1/2, z ~ N(0,1)).
+// With reduce_edge the gate must keep odd data odd: the activation is then
+// cst tanh(|s|) (e3nn's Gate with tanh gates on |gating scalars|, :994-995),
+// selected by act = 1; act = 0 is cst sigmoid(s).
 // The labels are then out[r, t] = sign[t] in[r, src[t]] (0 where src[t] < 0),
 // and the gradient of that gather is a fixed-order sum over the columns that
 // read each input column (CSR), so it is deterministic without atomics.
@@ -21,9 +24,17 @@ namespace ih {
 
 __device__ __forceinline__ float sigmoidf(float z) { return 1.0f / (1.0f + expf(-z)); }
 
+// The gate activation f(z) and f'(z): sigmoid (act 0), or tanh(|z|) (act 1)
+// with d|z|/dz = sign(z), 0 at z = 0 (as torch's abs).
+__device__ __forceinline__ float gate_act(int act, float z) { return act ? tanhf(fabsf(z)) : sigmoidf(z); }
+__device__ __forceinline__ float gate_dact(int act, float z, float f) {
+  if (act) return (1.0f - f * f) * (z > 0.f ? 1.0f : (z < 0.f ? -1.0f : 0.f));
+  return f * (1.0f - f);
+}
+
 // One thread per (b, row, channel); consecutive threads take consecutive channels.
 __global__ void gate_fwd_kernel(const float* __restrict__ x, int64_t B, int L, int C, const float* __restrict__ s,
-                                float cst, float* __restrict__ g) {
+                                float cst, int act, float* __restrict__ g) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int d = (L + 1) * (L + 1);
   if (i >= B * d * C) return;
@@ -37,16 +48,16 @@ __global__ void gate_fwd_kernel(const float* __restrict__ x, int64_t B, int L, i
   }
   int l = 1;  // degree of row j: l^2 <= j < (l+1)^2
   while ((l + 1) * (l + 1) <= j) ++l;
-  g[i] = cst * sigmoidf(sb[C + (l - 1) * C + c]) * x[i];
+  g[i] = cst * gate_act(act, sb[C + (l - 1) * C + c]) * x[i];
 }
 
 // One thread per (b, channel): the d rows of that channel.
 //   dx[b, l^2 + m, c]           = go g_l          (l >= 1; row 0 untouched: x's l = 0
 //                                                 only feeds the scalar linear)
 //   ds[b, c]                    = go[b, 0, c]
-//   ds[b, C + (l-1) C + c]      = cst s'(z) sum_m go[b, l^2 + m, c] x[b, l^2 + m, c]
+//   ds[b, C + (l-1) C + c]      = cst f'(z) sum_m go[b, l^2 + m, c] x[b, l^2 + m, c]
 __global__ void gate_bwd_kernel(const float* __restrict__ x, int64_t B, int L, int C, const float* __restrict__ s,
-                                float cst, const float* __restrict__ go, float* __restrict__ dx,
+                                float cst, int act, const float* __restrict__ go, float* __restrict__ dx,
                                 float* __restrict__ ds) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= B * C) return;
@@ -61,7 +72,7 @@ __global__ void gate_bwd_kernel(const float* __restrict__ x, int64_t B, int L, i
   dx[rb] = 0.f;
   for (int l = 1; l <= L; ++l) {
     const float z = sb[C + (l - 1) * C + c];
-    const float sg = sigmoidf(z);
+    const float sg = gate_act(act, z);
     const float gl = cst * sg;
     float acc = 0.f;
     for (int m = 0; m < 2 * l + 1; ++m) {
@@ -70,7 +81,7 @@ __global__ void gate_bwd_kernel(const float* __restrict__ x, int64_t B, int L, i
       acc = fmaf(gv, x[k], acc);
       dx[k] = gv * gl;
     }
-    dsb[C + (l - 1) * C + c] = acc * cst * sg * (1.0f - sg);
+    dsb[C + (l - 1) * C + c] = acc * cst * gate_dact(act, z, sg);
   }
 }
 
@@ -112,27 +123,30 @@ int grid_of(int64_t n, unsigned* g) {
 using namespace maloq;
 
 extern "C" int maloq_irreps_gate_fwd(const float* x, int64_t num_rows, int lmax, int c, const float* scalars, float cst,
-                                     float* out, void* stream) {
+                                     int act, float* out, void* stream) {
   MALOQ_REQUIRE(num_rows >= 0 && lmax >= 0 && lmax <= 8 && c > 0, "bad sizes");
+  MALOQ_REQUIRE(act == 0 || act == 1, "act must be 0 (sigmoid) or 1 (tanh of |z|)");
   if (num_rows == 0) return MALOQ_OK;
   MALOQ_REQUIRE(x && scalars && out && out != x, "null or aliased pointer");
   const int d = (lmax + 1) * (lmax + 1);
   unsigned g;
   if (ih::grid_of(num_rows * d * c, &g)) return MALOQ_EINVAL;
   hipLaunchKernelGGL(ih::gate_fwd_kernel, dim3(g), dim3(256), 0, static_cast<hipStream_t>(stream), x, num_rows, lmax,
-                     c, scalars, cst, out);
+                     c, scalars, cst, act, out);
   return check_launch("gate_fwd_kernel");
 }
 
 extern "C" int maloq_irreps_gate_bwd(const float* x, int64_t num_rows, int lmax, int c, const float* scalars, float cst,
-                                     const float* grad_out, float* grad_x, float* grad_scalars, void* stream) {
+                                     int act, const float* grad_out, float* grad_x, float* grad_scalars,
+                                     void* stream) {
   MALOQ_REQUIRE(num_rows >= 0 && lmax >= 0 && lmax <= 8 && c > 0, "bad sizes");
+  MALOQ_REQUIRE(act == 0 || act == 1, "act must be 0 (sigmoid) or 1 (tanh of |z|)");
   if (num_rows == 0) return MALOQ_OK;
   MALOQ_REQUIRE(x && scalars && grad_out && grad_x && grad_scalars, "null pointer");
   unsigned g;
   if (ih::grid_of(num_rows * c, &g)) return MALOQ_EINVAL;
   hipLaunchKernelGGL(ih::gate_bwd_kernel, dim3(g), dim3(256), 0, static_cast<hipStream_t>(stream), x, num_rows, lmax,
-                     c, scalars, cst, grad_out, grad_x, grad_scalars);
+                     c, scalars, cst, act, grad_out, grad_x, grad_scalars);
   return check_launch("gate_bwd_kernel");
 }
 

@@ -18,7 +18,15 @@ hipBLASLt); the gate is ``maloq_irreps_gate_fwd`` / ``_bwd``; and one
 layout, the output permutation and the node expansion together (its gradient
 is the fixed-order ``maloq_scatter_columns``).  Parameter names follow the
 reference (e3nn Linear's flat ``weight`` [mul_in * mul_out] and ``bias``), so
-state dicts load.  reduce_edge is not carried (it raises).
+state dicts load.
+
+With reduce_edge (esen_osh.py:570-575, 894-944, 1090-1130) every edge pair
+(i -> j, j -> i) is processed once as alpha = x_ij + x_ji and beta = x_ij - x_ji
+(gates cst tanh(|s|), no biases but the node layers'), and the labels of both
+directions are rebuilt as A + B and A - B, where A and B are two signed column
+gathers of the alpha and beta GEMM outputs that carry the reference's
+output permutations, the Vpa +- Vpb remix of the off-diagonal shell pairs, the
+subspace remix and the parity flips.
 """
 from __future__ import annotations
 
@@ -31,23 +39,23 @@ from torch import nn
 from . import _lib
 
 
-def _normalize2mom_sigmoid():
-    """e3nn's normalize2mom constant for sigmoid: E[sigmoid(z)^2]^-1/2 over 10^6
-    float64 N(0, 1) draws of a CPU generator seeded 0 (as e3nn computes it)."""
+def _normalize2mom(act):
+    """e3nn's normalize2mom constant: E[act(z)^2]^-1/2 over 10^6 float64 N(0, 1)
+    draws of a CPU generator seeded 0 (as e3nn computes it)."""
     gen = torch.Generator(device="cpu").manual_seed(0)
     z = torch.randn(1_000_000, generator=gen, dtype=torch.float64)
-    cst = torch.sigmoid(z).pow(2).mean().pow(-0.5).item()
+    cst = act(z).pow(2).mean().pow(-0.5).item()
     return 1.0 if abs(cst - 1.0) < 1e-4 else cst
 
 
-_CST = None
+_CST = {}
 
 
-def _cst():
-    global _CST
-    if _CST is None:
-        _CST = _normalize2mom_sigmoid()
-    return _CST
+def _cst(act):
+    """act 0: sigmoid gates; act 1: tanh gates (reduce_edge)."""
+    if act not in _CST:
+        _CST[act] = _normalize2mom(torch.tanh if act else torch.sigmoid)
+    return _CST[act]
 
 
 def _irreps_ls(irreps):
@@ -133,6 +141,111 @@ def _label_to_z(ls, lmax):
     return np.asarray(cols, np.int64), mul, int(zoff[-1])
 
 
+def _edgereduced(ls_list):
+    """make_irreps_edgereduced (esen_osh.py:733-835): the alpha (symmetric) and
+    beta (antisymmetric) irreps, the parity-flip label columns, and the paired
+    columns of the off-diagonal shell pairs: alpha (i, j) with beta (j, i), i < j."""
+    alpha, beta, flips = [], [], []
+    pos = 0
+    ablk, bblk = {}, {}
+    at = bt = 0
+    for i, li in enumerate(ls_list):
+        for j, lj in enumerate(ls_list):
+            prod = _product_ls(li, lj)
+            dim = sum(2 * l + 1 for l in prod)
+            if i == j:
+                ev, od = _product_ls(li, lj, "even"), _product_ls(li, lj, "odd")
+                alpha += ev
+                beta += od
+                at += sum(2 * l + 1 for l in ev)
+                bt += sum(2 * l + 1 for l in od)
+                pos += dim
+            elif i < j:
+                alpha += prod
+                ablk[(i, j)] = range(at, at + dim)
+                at += dim
+                for l in prod:
+                    if (l + li + lj) % 2 == 1:   # odd l of an even pair, even l of an odd pair
+                        flips += range(pos, pos + 2 * l + 1)
+                    pos += 2 * l + 1
+            else:
+                beta += prod
+                bblk[(i, j)] = range(bt, bt + dim)
+                bt += dim
+                pos += dim
+    off_a = [k for (i, j), r in ablk.items() for k in r]
+    off_b = [k for (i, j) in ablk for k in bblk[(j, i)]]
+    return alpha, beta, set(flips), off_a, off_b
+
+
+def _remix(ls_a, ls_b, ls_list):
+    """get_subspace_remix_permutation (irreps_utils.py:46-103): label column ->
+    column of cat(alpha, beta) (alpha: even irreps of diagonal pairs and the
+    upper pairs; beta: odd irreps of diagonal pairs and the lower pairs, in order)."""
+    def starts(ls, base):
+        out, cur = [], base
+        for l in ls:
+            out.append(cur)
+            cur += 2 * l + 1
+        return out
+    sa, sb = starts(ls_a, 0), starts(ls_b, sum(2 * l + 1 for l in ls_a))
+    perm, ia, ib = [], 0, 0
+    for i, li in enumerate(ls_list):
+        for j, lj in enumerate(ls_list):
+            for l in _product_ls(li, lj):
+                if i < j or (i == j and l % 2 == 0):
+                    perm += range(sa[ia], sa[ia] + 2 * l + 1)
+                    ia += 1
+                else:
+                    perm += range(sb[ib], sb[ib] + 2 * l + 1)
+                    ib += 1
+    return perm
+
+
+def _edge_pair_maps(ls_list, lmax):
+    """Column gathers of the reduce_edge edge labels: for label column t,
+    label = A[t] + B[t] on the canonical edge and A[t] - B[t] on its reverse,
+    A[t] = sa[t] Za[:, ca[t]], B[t] = sb[t] Zb[:, cb[t]] (Za, Zb: the alpha and
+    beta GEMM outputs).  Follows half_edges_to_full, the output permutations,
+    the Vpa +- Vpb remix, the subspace remix and the parity flips
+    (esen_osh.py:918-937)."""
+    ls_a, ls_b, flips, off_a, off_b = _edgereduced(ls_list)
+    za, _, wa = _label_to_z(ls_a, lmax)
+    zb, _, wb = _label_to_z(ls_b, lmax)
+    da = sum(2 * l + 1 for l in ls_a)
+    pos_a = {k: n for n, k in enumerate(off_a)}
+    pos_b = {k: n for n, k in enumerate(off_b)}
+    remix = _remix(ls_a, ls_b, ls_list)
+    ca, sa, cb, sb = [], [], [], []
+    for t, c in enumerate(remix):
+        f = -1.0 if t in flips else 1.0
+        if c < da:
+            ka, kb, beta_sign = c, (off_b[pos_a[c]] if c in pos_a else None), 1.0
+        else:
+            kb = c - da
+            ka, beta_sign = (off_a[pos_b[kb]] if kb in pos_b else None), (-1.0 if kb in pos_b else 1.0)
+        ca.append(int(za[ka]) if ka is not None else -1)
+        sa.append(f if ka is not None else 0.0)
+        cb.append(int(zb[kb]) if kb is not None else -1)
+        sb.append(f * beta_sign if kb is not None else 0.0)
+    return (ca, sa, wa), (cb, sb, wb), ls_a, ls_b
+
+
+def _reverse_edges(edge_index):
+    """create_half_antisym_edge_pairs (esen_osh.py:1090-1110): the reverse of
+    every edge and the canonical half (index below its reverse's); every edge
+    must have its reverse."""
+    src, dst = edge_index[0].long(), edge_index[1].long()
+    k = int(edge_index.max()) + 1 if edge_index.numel() else 1
+    perm_orig = torch.sort(src * k + dst)[1]
+    perm_flip = torch.sort(dst * k + src)[1]
+    rev = perm_flip[torch.argsort(perm_orig)]
+    if not bool(((src[rev] == dst) & (dst[rev] == src)).all()):
+        raise ValueError("reduce_edge needs every edge (i, j) to come with its reverse (j, i)")
+    half = torch.nonzero(torch.arange(src.numel(), device=src.device) < rev)[:, 0]
+    return rev, half
+
+
 class _ColumnMap:
     """Device tables of a signed column gather out[:, t] = sign[t] Z[:, src[t]]
     and the CSR of its transpose (for the fixed-order gradient)."""
@@ -173,11 +286,13 @@ class _Gather(torch.autograd.Function):
 
 class _GateFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, s, lmax, cst):
+    def forward(ctx, x, s, lmax, act):
         out = torch.empty_like(x)
-        _lib.call("maloq_irreps_gate_fwd", x, x.shape[0], lmax, x.shape[2], s, cst, out, _lib.stream_of(x.device))
+        cst = _cst(act)
+        _lib.call("maloq_irreps_gate_fwd", x, x.shape[0], lmax, x.shape[2], s, cst, act, out,
+                  _lib.stream_of(x.device))
         ctx.save_for_backward(x, s)
-        ctx.lmax, ctx.cst = lmax, cst
+        ctx.lmax, ctx.act = lmax, act
         return out
 
     @staticmethod
@@ -185,8 +300,8 @@ class _GateFn(torch.autograd.Function):
         x, s = ctx.saved_tensors
         g = g.contiguous()
         dx, ds = torch.empty_like(x), torch.empty_like(s)
-        _lib.call("maloq_irreps_gate_bwd", x, x.shape[0], ctx.lmax, x.shape[2], s, ctx.cst, g, dx, ds,
-                  _lib.stream_of(x.device))
+        _lib.call("maloq_irreps_gate_bwd", x, x.shape[0], ctx.lmax, x.shape[2], s, _cst(ctx.act), ctx.act, g, dx,
+                  ds, _lib.stream_of(x.device))
         return dx, ds, None, None
 
 
@@ -211,18 +326,21 @@ class _GateModule(nn.Module):
 
 
 class Fock_Irreps_Head(nn.Module):
-    """esen_osh.py:522-1064 (reduce_edge=False).  forward(emb, batch) ->
-    (node_outputs [spins, N, T], edge_outputs [spins, E, T]) from
-    emb["node_embeddings"] [N, (lmax+1)^2, C] and emb["edge_embeddings"]."""
+    """esen_osh.py:522-1064.  forward(emb, batch) -> (node_outputs [spins, N, T],
+    edge_outputs [spins, E, T]) from emb["node_embeddings"] [N, (lmax+1)^2, C]
+    and emb["edge_embeddings"]; with reduce_edge, batch.edge_index [2, E] (every
+    edge with its reverse)."""
 
     def __init__(self, irreps_in, irreps_out, lmax, sphere_channels, reduce_edge=False, ls_list=None,
                  open_shell=False, reduce_node=False, reduce_node_intra=False, orbital_basis=None):
         super().__init__()
-        if reduce_edge:
-            raise NotImplementedError("reduce_edge is not carried by the HIP output head")
+        if reduce_edge and not reduce_node:
+            raise NotImplementedError("The case of not reducing node irreps but reducing edge irreps is "
+                                      "currently not implemented")
         C, L = int(sphere_channels), int(lmax)
         self.sphere_channels, self.lmax = C, L
-        self.reduce_node, self.reduce_node_intra, self.reduce_edge = reduce_node, reduce_node_intra, False
+        self.reduce_node, self.reduce_node_intra, self.reduce_edge = reduce_node, reduce_node_intra, bool(reduce_edge)
+        self._act = 1 if reduce_edge else 0
         self.irreps_out = irreps_out
         self.ls_list = None if ls_list is None else [int(l) % 10 for l in ls_list]
         self.num_spins = 2 if open_shell else 1
@@ -236,14 +354,24 @@ class Fock_Irreps_Head(nn.Module):
             if self.ls_list is None:
                 raise ValueError("reduce_node needs ls_list")
             self._ls_node = _nodereduced_ls(self.ls_list, reduce_node_intra)
-        self.lin_scalars_learnable = nn.ModuleList([E3Linear(C, C + L * C, 0) for _ in range(self.num_spins)])
+        # with reduce_edge the scalar linear and the edge layers carry no bias
+        # (odd data must stay odd: not_antisym, esen_osh.py:570-575, 622)
+        self.lin_scalars_learnable = nn.ModuleList([E3Linear(C, C + L * C, 0, biases=not reduce_edge)
+                                                    for _ in range(self.num_spins)])
         self.gate = nn.ModuleList([_GateModule() for _ in range(self.num_spins)])
 
-        def layers(ls):
+        def layers(ls, biases=True):
             mul = [sum(1 for x in ls if x == l) for l in range(L + 1)]
-            return nn.ModuleList([nn.ModuleList([E3Linear(C, mul[l], l) for l in range(L + 1)])
+            return nn.ModuleList([nn.ModuleList([E3Linear(C, mul[l], l, biases=biases) for l in range(L + 1)])
                                   for _ in range(self.num_spins)])
-        if reduce_node:
+        if reduce_edge:
+            (self._map_a, self._map_b, ls_a, ls_b) = _edge_pair_maps(self.ls_list, L)
+            if len(self._map_a[0]) != sum(2 * l + 1 for l in self._ls_out):
+                raise ValueError("the edge-pair irreps do not rebuild irreps_out (ls_list mismatch)")
+            self.node_lin_out_layers = layers(self._ls_node)
+            self.edge_lin_out_layers = nn.ModuleDict({"alpha": layers(ls_a, biases=False),
+                                                      "beta": layers(ls_b, biases=False)})
+        elif reduce_node:
             self.node_lin_out_layers = layers(self._ls_node)
             self.edge_lin_out_layers = layers(self._ls_out)
         else:
@@ -266,18 +394,24 @@ class Fock_Irreps_Head(nn.Module):
             self._maps[key] = _ColumnMap(src, sign, width, device)
         return self._maps[key]
 
+    def _pair_maps(self, device):
+        key = ("pairs", str(device))
+        if key not in self._maps:
+            self._maps[key] = tuple(_ColumnMap(c, s, w, device) for c, s, w in (self._map_a, self._map_b))
+        return self._maps[key]
+
     # ---------------------------------------------------------------- compute
-    def _process(self, x, lin_layers, spin, stream):
+    def _z(self, x, lin_layers, spin):
         """s = lin_scalars(x_0), gate, per-l linear into Z [rows, sum_l (2l+1) mul_l]
-        (m-major per degree), then the label gather."""
+        (m-major per degree)."""
         _lib.require_cuda(x)
         if x.dtype != torch.float32 or x.dim() != 3 or x.shape[1] != (self.lmax + 1) ** 2 \
                 or x.shape[2] != self.sphere_channels:
             raise ValueError(f"embeddings must be float32 [rows, {(self.lmax + 1) ** 2}, {self.sphere_channels}]")
         x = x.contiguous()
         ls = self.lin_scalars_learnable[spin]
-        s = torch.addmm(ls.bias, x[:, 0, :], ls.matrix())
-        g = _GateFn.apply(x, s.contiguous(), self.lmax, _cst())
+        s = torch.addmm(ls.bias, x[:, 0, :], ls.matrix()) if ls.bias.numel() else x[:, 0, :] @ ls.matrix()
+        g = _GateFn.apply(x, s.contiguous(), self.lmax, self._act)
         zs = []
         for l, lin in enumerate(lin_layers):
             if lin.mul_out == 0:
@@ -286,14 +420,34 @@ class Fock_Irreps_Head(nn.Module):
             if l == 0 and lin.bias.numel():
                 y = y + lin.bias
             zs.append(y.reshape(x.shape[0], -1))
-        z = torch.cat(zs, dim=1)
-        return _Gather.apply(z, self._column_map(stream, x.device))
+        return torch.cat(zs, dim=1)
+
+    def _process(self, x, lin_layers, spin, stream):
+        """Z, then the label gather."""
+        return _Gather.apply(self._z(x, lin_layers, spin), self._column_map(stream, x.device))
+
+    def _edge_pairs(self, edge_x, edge_index, spin):
+        """reduce_edge: alpha / beta of the canonical half, both directions' labels."""
+        rev, half = edge_index
+        xh, xr = edge_x[half], edge_x[rev[half]]
+        za = self._z(xh + xr, self.edge_lin_out_layers["alpha"][spin], spin)
+        zb = self._z(xh - xr, self.edge_lin_out_layers["beta"][spin], spin)
+        ma, mb = self._pair_maps(edge_x.device)
+        a, b = _Gather.apply(za, ma), _Gather.apply(zb, mb)
+        out = torch.zeros(edge_x.shape[0], a.shape[1], device=a.device, dtype=a.dtype)
+        return out.index_put((half,), a + b).index_put((rev[half],), a - b)
 
     def forward(self, emb, batch=None):
         node_x, edge_x = emb["node_embeddings"], emb["edge_embeddings"]
+        if self.reduce_edge:
+            ei = batch["edge_index"] if isinstance(batch, dict) else batch.edge_index
+            pairs = _reverse_edges(ei.squeeze(0).reshape(2, -1).to(edge_x.device))
         node_out, edge_out = [], []
         for spin in range(self.num_spins):
-            if self.reduce_node:
+            if self.reduce_edge:
+                node_out.append(self._process(node_x, self.node_lin_out_layers[spin], spin, "node"))
+                edge_out.append(self._edge_pairs(edge_x, pairs, spin))
+            elif self.reduce_node:
                 node_out.append(self._process(node_x, self.node_lin_out_layers[spin], spin, "node"))
                 edge_out.append(self._process(edge_x, self.edge_lin_out_layers[spin], spin, "edge"))
             else:

@@ -20,4 +20,9 @@ Parity pins (what each restated function is checked against):
                     an import of e3nn could pin it; e3nn is absent).
 * matrix2labels.* : exact copy semantics, forward/inverse identity on covered
                     entries.
+* irreps_head.*   : node expansion against the CG labels of symmetric on-site
+                    blocks, edge pairs against the CG labels of transposed
+                    blocks, stable l-sort permutation, SO(3) equivariance.  The
+                    e3nn Gate normalisation constants (sigmoid, tanh): parity
+                    unpinned (e3nn's own code is absent).
 """
