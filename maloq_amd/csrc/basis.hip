@@ -47,7 +47,10 @@ namespace bt {
 // hides more load latency than the idle upper half-wave of phase 2 costs.
 constexpr int kRows = 32;            // rows per workgroup
 constexpr int kWaves = kThreads / 64;
-constexpr int kPassRows = kRows / kWaves;  // rows per wave per load pass (x 4 chunks of 64)
+// rows per wave per load pass (x 4 chunks of 64): half a wave's 8 rows, 16
+// loads in flight per lane.  All 8 in one pass held 98 VGPRs (4 workgroups per
+// CU instead of 6) and ran 20-25 % slower.
+constexpr int kPassRows = kRows / kWaves / 2;
 constexpr int kMaxTileBytes = 160 * 1024;
 constexpr int kMaxSkipBlocks = 64;   // blocks covered by the per-kind presence masks
 
@@ -271,12 +274,21 @@ __device__ __forceinline__ void contract(float* row, const float* __restrict__ W
 // DENSE: the tables may hold blocks without a compiled program (read from
 // a.w); otherwise every block has one and the dense loops (and their
 // registers) are compiled out.
+// The CG tables are read through the constant address space: uniform
+// addresses there become scalar loads (no vector load plus readfirstlane).
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(4))) T* konst(const T* p) {
+  return (const __attribute__((address_space(4))) T*)(p);
+}
+
 template <bool SKIP, bool DENSE>
 __device__ __forceinline__ void contract_tile(const Args& a, const Smem& s, float* tile) {
   const int wave = uniform(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const int beg = uniform(a.sched[wave]), end = uniform(a.sched[wave + 1]);
-  const int32_t* ids = a.sched + kWaves + 1;
+  const auto* sched = konst(a.sched);
+  const auto* blk = konst(a.blocks);
+  const int beg = uniform(sched[wave]), end = uniform(sched[wave + 1]);
+  const auto* ids = sched + kWaves + 1;
   // lane = row; with 32 rows the upper half-wave repeats the lower one (same
   // reads, same values written)
   float* row = tile + (lane % kRows) * a.tp;
@@ -286,22 +298,29 @@ __device__ __forceinline__ void contract_tile(const Args& a, const Smem& s, floa
     have0 = kind >= 0 ? a.kind_blocks[2 * kind] : 0u;
     have1 = kind >= 0 ? a.kind_blocks[2 * kind + 1] : 0u;
   }
+  // block ids two ahead, block entries one ahead: the scalar loads of the next
+  // blocks are in flight while the current block's program runs
+  int b0 = beg < end ? ids[beg] : 0;
+  int b1 = beg + 1 < end ? ids[beg + 1] : 0;
+  int en = 0, ec = 0, ew = 0, ep = -1;
+  if (beg < end) { en = blk[4 * b0]; ec = blk[4 * b0 + 1]; ew = blk[4 * b0 + 2]; ep = blk[4 * b0 + 3]; }
   for (int p = beg; p < end; ++p) {
-    const int b = uniform(ids[p]);
+    const int b = uniform(b0);
+    const int n = uniform(en), c0 = uniform(ec), woff = uniform(ew), prog = uniform(ep);
+    if (p + 1 < end) { en = blk[4 * b1]; ec = blk[4 * b1 + 1]; ew = blk[4 * b1 + 2]; ep = blk[4 * b1 + 3]; }
+    b0 = b1;
+    if (p + 2 < end) b1 = ids[p + 2];
     if constexpr (SKIP) {
       const bool mine = ((b < 32 ? have0 >> b : have1 >> (b - 32)) & 1u) != 0;
       if (__builtin_amdgcn_ballot_w64(mine) == 0) continue;  // no row of the tile has block b
     }
-    const int n = uniform(a.blocks[4 * b]);
-    const int c0 = uniform(a.blocks[4 * b + 1]);
-    const int prog = uniform(a.blocks[4 * b + 3]);
     if (prog >= 0) {
       cg::run(prog, row + c0);
       continue;
     }
     if constexpr (!DENSE) continue;  // excluded by the host (w == NULL only with every program set)
-    const float* W = a.w + uniform(a.blocks[4 * b + 2]);
-    switch (n) {  // (2 l1 + 1)(2 l2 + 1) for l1, l2 <= 3
+    const float* W = a.w + woff;
+    switch (n) {
       case 1: contract<1>(row + c0, W); break;
       case 3: contract<3>(row + c0, W); break;
       case 5: contract<5>(row + c0, W); break;
