@@ -23,6 +23,8 @@
 //   3. store: coalesced rows (through the sort permutation) or the atom-pair
 //      blocks again in memory order (every Fock entry written by exactly one
 //      (row, column): deterministic, no atomics).
+// Label / irreps rows whose width is a multiple of 4 are loaded and stored 16
+// bytes (4 consecutive columns) per lane.
 //
 // Fock-side calls run on a row plan: maloq_basis_row_meta describes every row
 // (block base, original row index, element-pair kind, block shape) once per
@@ -151,6 +153,34 @@ __device__ __forceinline__ void load_tile(const Args& a, const Smem& s, float* t
                                           int nrows) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if constexpr (SIDE == ROWS) {
+    if ((a.t & 3) == 0) {
+      // rows of 16-byte aligned width: each lane loads 4 consecutive columns
+      for (int c4 = 4 * lane; c4 < a.t; c4 += 256) {
+        int dc[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) dc[k] = a.perm_in ? a.perm_in[c4 + k] : c4 + k;
+        for (int i0 = 0; i0 < kRows / kWaves; i0 += kPassRows) {
+          float4 v[kPassRows];
+#pragma unroll
+          for (int i = 0; i < kPassRows; ++i) {
+            const int g = wave + kWaves * (i0 + i);
+            v[i] = *reinterpret_cast<const float4*>(a.in + (g < nrows ? row_of<PLAN>(s, r0, g) : r0) * a.t + c4);
+          }
+#pragma unroll
+          for (int i = 0; i < kPassRows; ++i) {
+            const int g = wave + kWaves * (i0 + i);
+            if (g < nrows) {
+              float* tr = tile + g * a.tp;
+              tr[dc[0]] = v[i].x;
+              tr[dc[1]] = v[i].y;
+              tr[dc[2]] = v[i].z;
+              tr[dc[3]] = v[i].w;
+            }
+          }
+        }
+      }
+      return;
+    }
     // wave w copies rows w, w + 4, ... in passes of kPassRows rows x 256
     // columns (coalesced along the row), all loads of a pass in flight
     for (int c0 = 0; c0 < a.t; c0 += 256) {
@@ -217,6 +247,20 @@ __device__ __forceinline__ void store_tile(const Args& a, const Smem& s, const f
                                            int64_t r0, int nrows) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if constexpr (SIDE == ROWS) {
+    if ((a.t & 3) == 0) {
+      // rows of 16-byte aligned width: each lane stores 4 consecutive columns
+      for (int c4 = 4 * lane; c4 < a.t; c4 += 256) {
+        int sc[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) sc[k] = a.perm_out ? a.perm_out[c4 + k] : c4 + k;
+        for (int g = wave; g < nrows; g += kWaves) {
+          const float* tr = tile + g * a.tp;
+          *reinterpret_cast<float4*>(a.out + row_of<PLAN>(s, r0, g) * a.t + c4) =
+              make_float4(tr[sc[0]], tr[sc[1]], tr[sc[2]], tr[sc[3]]);
+        }
+      }
+      return;
+    }
     for (int c = lane; c < a.t; c += 64) {
       const int sc = a.perm_out ? a.perm_out[c] : c;
       for (int g = wave; g < nrows; g += kWaves)
