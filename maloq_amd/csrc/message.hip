@@ -275,7 +275,7 @@ extern "C" int maloq_message_edgewise_fwd(int dtype, int lmax, int mmax, const v
     a.wpack = static_cast<const char*>(wpack1); a.bias = bias1; a.out = out; a.part = partials;
     a.E = num_edges; a.C_k = parts * c_x; a.C_n = c_hidden; a.n_cb = c_hidden / CB;
     a.extra = lmax * c_hidden;
-    a.ntiles = (num_edges + tile_edges(lmax, mmax, 1) - 1) / tile_edges(lmax, mmax, 1);
+    a.ntiles = (num_edges + tile_edges(lmax, mmax, 1, FWD_EDGE) - 1) / tile_edges(lmax, mmax, 1, FWD_EDGE);
     a.frags_per_cb = frags_per_cb(lmax, mmax, 1, parts * c_x, kc);
     a.gsave = gate_ws; a.zout = z_ws;
     rc = dispatch(lmax, mmax, dtype, 1, FWD_EDGE, a, s);
