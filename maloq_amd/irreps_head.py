@@ -419,7 +419,7 @@ class Fock_Irreps_Head(nn.Module):
             y = torch.matmul(g[:, l * l:(l + 1) ** 2, :], lin.matrix())   # [rows, 2l+1, mul_l]
             if l == 0 and lin.bias.numel():
                 y = y + lin.bias
-            zs.append(y.reshape(x.shape[0], -1))
+            zs.append(y.reshape(x.shape[0], (2 * l + 1) * lin.mul_out))
         return torch.cat(zs, dim=1)
 
     def _process(self, x, lin_layers, spin, stream):

@@ -197,3 +197,8 @@ def test_reduce_edge_needs_reverse_edges():
     x = torch.randn(3, (lmax + 1) ** 2, C).cuda()
     with pytest.raises(ValueError):
         mod({"node_embeddings": x, "edge_embeddings": torch.randn(3, (lmax + 1) ** 2, C).cuda()}, {"edge_index": ei})
+    # no edges at all: empty edge labels, node labels as usual
+    T = sum(2 * l + 1 for l in oh.all_ls(t.ls_list))
+    n, e = mod({"node_embeddings": x, "edge_embeddings": torch.zeros(0, (lmax + 1) ** 2, C).cuda()},
+               {"edge_index": torch.zeros(2, 0, dtype=torch.int64).cuda()})
+    assert n.shape == (1, 3, T) and e.shape == (1, 0, T)
