@@ -83,8 +83,9 @@ int maloq_rotate(int x_dtype, int out_dtype, int lmax, const void* x, int c, con
  *   w      the block matrices; NULL is allowed when every block of the table
  *     has a program (the kernels then carry no dense path at all);
  *   sched  [5 + nblocks]: sched[0..4] are offsets into sched + 5 of the block ids
- *     each of the 4 waves of a workgroup contracts (sched[4] = nblocks);
- *   t      row width, at most 1279 (one 32-row tile of fp32 in LDS).
+ *     of 4 lists (sched[4] = nblocks); each wave of a workgroup contracts one
+ *     list (4 waves) or every other block of one (8 waves);
+ *   t      row width, at most 1271 (one 32-row tile of fp32 in LDS).
  * Sorted irreps rows use perm (sorted column j <-> unsorted column perm[j]). */
 
 /* Label/irreps rows -> rows, [R, t] -> [R, t]:

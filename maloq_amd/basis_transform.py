@@ -36,13 +36,15 @@ def _i32(a, device):
 
 # (2 l1 + 1)(2 l2 + 1) for l1, l2 <= 3: the block sizes the kernel is built for
 _SUPPORTED_N = frozenset((2 * a + 1) * (2 * b + 1) for a in range(4) for b in range(4))
-_WAVES = 4  # waves per workgroup of the transform kernel
+_WAVES = 4  # block lists of the transform kernel's schedule
 
 
 def _wave_schedule(costs):
-    """Longest-processing-time split of the CG blocks over the 4 waves of a
-    workgroup (``costs[b]``: FMAs + LDS accesses per row of block b).
-    Layout: 5 offsets, then the block ids of wave 0, wave 1, ..."""
+    """Longest-processing-time split of the CG blocks into 4 lists, each in
+    descending cost order (``costs[b]``: FMAs + LDS accesses per row of block
+    b).  A 4-wave workgroup runs one list per wave, an 8-wave one every other
+    block of a list per wave.  Layout: 5 offsets, then the block ids of list 0,
+    list 1, ..."""
     load = [0] * _WAVES
     lists = [[] for _ in range(_WAVES)]
     for b in sorted(range(len(costs)), key=lambda i: (-costs[i], i)):

@@ -6,15 +6,16 @@
 // label and irreps sides of a block occupy the same columns, so a block can be
 // contracted in place.
 //
-// One workgroup owns 32 rows (atom pairs) and works in three phases over a
-// [32, t] fp32 tile in LDS (odd row pitch: lane-per-row reads are bank-conflict
-// free):
+// One workgroup owns TR = 32 or 64 rows (atom pairs), TR / 8 waves, and works in
+// three phases over a [TR, t] fp32 tile in LDS (odd row pitch: lane-per-row
+// reads are bank-conflict free):
 //   1. load: label/irreps rows with coalesced row copies, or the atom-pair
 //      blocks of the Fock matrix walked in memory order (coalesced), every
 //      element dropped into its label column through a per-element-pair table;
-//   2. contract: each of the 4 waves takes a fixed list of CG blocks (longest-
-//      processing-time balanced on the host); lane = row, so the n x n block
-//      matrix is the same for all 64 lanes.  A block whose matrix is one of
+//   2. contract: the CG blocks are split into 4 lists on the host (longest-
+//      processing-time balanced); with 4 waves each wave runs one list, with 8
+//      every other block of one list.  Lane = row, so the n x n block matrix is
+//      the same for all 64 lanes.  A block whose matrix is one of
 //      the compiled CG programs (cg_blocks.h: its exact zeros skipped, its
 //      weights literals, about a fifth of the dense FMAs and no weight loads)
 //      runs that program; any other block runs the dense n x n loop with its
@@ -45,14 +46,18 @@ constexpr int kMaxElements = 100;
 
 namespace bt {
 
-// 32 rows per workgroup: a 25 KB tile lets six workgroups share a CU, which
-// hides more load latency than the idle upper half-wave of phase 2 costs.
-constexpr int kRows = 32;            // rows per workgroup
-constexpr int kWaves = kThreads / 64;
+// Tile rows TR: 64 (8 waves, every lane a row in phase 2) where the LDS tile
+// still lets as many waves share a CU as 32-row tiles would; otherwise 32 (4
+// waves, the upper half-wave repeats the lower one in phase 2).  Each wave
+// loads and stores 8 rows.
+constexpr int kRowsPerWave = 8;
+constexpr int kNarrowRows = 32, kWideRows = 64;
+constexpr int kSchedLists = 4;       // CG block lists of the host schedule
+__host__ __device__ constexpr int waves_of(int tr) { return tr / kRowsPerWave; }
 // rows per wave per load pass (x 4 chunks of 64): half a wave's 8 rows, 16
 // loads in flight per lane.  All 8 in one pass held 98 VGPRs (4 workgroups per
 // CU instead of 6) and ran 20-25 % slower.
-constexpr int kPassRows = kRows / kWaves / 2;
+constexpr int kPassRows = kRowsPerWave / 2;
 constexpr int kMaxTileBytes = 160 * 1024;
 constexpr int kMaxSkipBlocks = 64;   // blocks covered by the per-kind presence masks
 
@@ -76,16 +81,17 @@ struct Args {
   int nblocks;
   const int32_t* blocks;    // [nblocks, 4]: n, first column, weight offset, CG program or -1
   const float* w;
-  const int32_t* sched;     // [kWaves + 1] offsets into sched + kWaves + 1 of block ids
+  const int32_t* sched;     // [kSchedLists + 1] offsets into sched + kSchedLists + 1 of block ids
 };
 
+template <int TR>
 struct Smem {
-  int64_t base[kRows];
-  int64_t row[kRows];  // original row index
-  int kind[kRows];
-  int ne[kRows];       // elements of the atom-pair block (n_i * n_j)
-  int nj[kRows];
-  float rnj[kRows];    // 1 / n_j
+  int64_t base[TR];
+  int64_t row[TR];  // original row index
+  int kind[TR];
+  int ne[TR];       // elements of the atom-pair block (n_i * n_j)
+  int nj[TR];
+  float rnj[TR];    // 1 / n_j
 };
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -109,9 +115,10 @@ __global__ __launch_bounds__(kThreads) void row_meta_kernel(
                       static_cast<int>(r), (kind + 1) | ((ni & 255) << 16) | ((nj & 255) << 24));
 }
 
-__device__ __forceinline__ void load_meta(const Args& a, Smem& s, int64_t r0, int nrows) {
+template <int TR>
+__device__ __forceinline__ void load_meta(const Args& a, Smem<TR>& s, int64_t r0, int nrows) {
   const int g = threadIdx.x;
-  if (g >= kRows) return;
+  if (g >= TR) return;
   if (g >= nrows) {
     s.kind[g] = -1;
     s.ne[g] = 0;
@@ -132,7 +139,8 @@ __device__ __forceinline__ void load_meta(const Args& a, Smem& s, int64_t r0, in
 // base.  a = floor((q + 1/2) / n_j) in fp32 is exact: the quotient's distance to
 // the nearest integer is >= 1/(2 n_j) >= 2^-9, far above the rounding error
 // for q < 2^16.
-__device__ __forceinline__ int elem_offset(const Args& a, const Smem& s, int g, int q) {
+template <int TR>
+__device__ __forceinline__ int elem_offset(const Args& a, const Smem<TR>& s, int g, int q) {
   if (a.ld == 0) return q;  // block list: n_i x n_j row-major
   const int nj = s.nj[g];
   const int ar = static_cast<int>((static_cast<float>(q) + 0.5f) * s.rnj[g]);
@@ -140,17 +148,18 @@ __device__ __forceinline__ int elem_offset(const Args& a, const Smem& s, int g, 
 }
 
 // Original row index of tile row g.
-template <bool PLAN>
-__device__ __forceinline__ int64_t row_of(const Smem& s, int64_t r0, int g) {
+template <bool PLAN, int TR>
+__device__ __forceinline__ int64_t row_of(const Smem<TR>& s, int64_t r0, int g) {
   if constexpr (PLAN)
     return s.row[g];
   else
     return r0 + g;
 }
 
-template <int SIDE, bool PLAN>
-__device__ __forceinline__ void load_tile(const Args& a, const Smem& s, float* tile, int64_t r0,
+template <int SIDE, bool PLAN, int TR>
+__device__ __forceinline__ void load_tile(const Args& a, const Smem<TR>& s, float* tile, int64_t r0,
                                           int nrows) {
+  constexpr int NW = waves_of(TR);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if constexpr (SIDE == ROWS) {
     if ((a.t & 3) == 0) {
@@ -159,16 +168,16 @@ __device__ __forceinline__ void load_tile(const Args& a, const Smem& s, float* t
         int dc[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) dc[k] = a.perm_in ? a.perm_in[c4 + k] : c4 + k;
-        for (int i0 = 0; i0 < kRows / kWaves; i0 += kPassRows) {
+        for (int i0 = 0; i0 < kRowsPerWave; i0 += kPassRows) {
           float4 v[kPassRows];
 #pragma unroll
           for (int i = 0; i < kPassRows; ++i) {
-            const int g = wave + kWaves * (i0 + i);
+            const int g = wave + NW * (i0 + i);
             v[i] = *reinterpret_cast<const float4*>(a.in + (g < nrows ? row_of<PLAN>(s, r0, g) : r0) * a.t + c4);
           }
 #pragma unroll
           for (int i = 0; i < kPassRows; ++i) {
-            const int g = wave + kWaves * (i0 + i);
+            const int g = wave + NW * (i0 + i);
             if (g < nrows) {
               float* tr = tile + g * a.tp;
               tr[dc[0]] = v[i].x;
@@ -181,7 +190,7 @@ __device__ __forceinline__ void load_tile(const Args& a, const Smem& s, float* t
       }
       return;
     }
-    // wave w copies rows w, w + 4, ... in passes of kPassRows rows x 256
+    // wave w copies rows w, w + NW, ... in passes of kPassRows rows x 256
     // columns (coalesced along the row), all loads of a pass in flight
     for (int c0 = 0; c0 < a.t; c0 += 256) {
       int dc[4];
@@ -190,13 +199,13 @@ __device__ __forceinline__ void load_tile(const Args& a, const Smem& s, float* t
         const int c = c0 + ch * 64 + lane;
         dc[ch] = c < a.t ? (a.perm_in ? a.perm_in[c] : c) : -1;
       }
-      for (int i0 = 0; i0 < kRows / kWaves; i0 += kPassRows) {
+      for (int i0 = 0; i0 < kRowsPerWave; i0 += kPassRows) {
         float v[kPassRows][4];
 #pragma unroll
         for (int i = 0; i < kPassRows; ++i)
 #pragma unroll
           for (int ch = 0; ch < 4; ++ch) {
-            const int g = wave + kWaves * (i0 + i), c = c0 + ch * 64 + lane;
+            const int g = wave + NW * (i0 + i), c = c0 + ch * 64 + lane;
             const bool ok = g < nrows && c < a.t;
             const float x = a.in[ok ? row_of<PLAN>(s, r0, g) * a.t + c : 0];
             v[i][ch] = ok ? x : 0.f;
@@ -205,27 +214,27 @@ __device__ __forceinline__ void load_tile(const Args& a, const Smem& s, float* t
         for (int i = 0; i < kPassRows; ++i)
 #pragma unroll
           for (int ch = 0; ch < 4; ++ch) {
-            const int g = wave + kWaves * (i0 + i);
+            const int g = wave + NW * (i0 + i);
             if (g < nrows && dc[ch] >= 0) tile[g * a.tp + dc[ch]] = v[i][ch];
           }
       }
     }
   } else {
     // Zero the tile (label columns the element pair lacks stay zero), then
-    // wave w walks the atom-pair blocks of rows w, w + 4, ... in memory order
+    // wave w walks the atom-pair blocks of rows w, w + NW, ... in memory order
     // (coalesced), passes of kPassRows rows x 256 elements, and drops every
     // element into its label column.
-    for (int i = threadIdx.x; i < kRows * a.tp; i += kThreads) tile[i] = 0.f;
+    for (int i = threadIdx.x; i < TR * a.tp; i += NW * 64) tile[i] = 0.f;
     __syncthreads();
     for (int q0 = 0; q0 < a.maxe; q0 += 256) {
-      for (int i0 = 0; i0 < kRows / kWaves; i0 += kPassRows) {
+      for (int i0 = 0; i0 < kRowsPerWave; i0 += kPassRows) {
         float v[kPassRows][4];
         int dst[kPassRows][4];
 #pragma unroll
         for (int i = 0; i < kPassRows; ++i)
 #pragma unroll
           for (int ch = 0; ch < 4; ++ch) {
-            const int g = wave + kWaves * (i0 + i), q = q0 + ch * 64 + lane;
+            const int g = wave + NW * (i0 + i), q = q0 + ch * 64 + lane;
             const bool ok = q < s.ne[g];
             const int col = ok ? a.raw_slot[s.kind[g] * a.maxe + q] : -1;
             const float x = a.fock[ok ? s.base[g] + elem_offset(a, s, g, q) : 0];
@@ -242,9 +251,10 @@ __device__ __forceinline__ void load_tile(const Args& a, const Smem& s, float* t
   }
 }
 
-template <int SIDE, bool PLAN>
-__device__ __forceinline__ void store_tile(const Args& a, const Smem& s, const float* tile,
+template <int SIDE, bool PLAN, int TR>
+__device__ __forceinline__ void store_tile(const Args& a, const Smem<TR>& s, const float* tile,
                                            int64_t r0, int nrows) {
+  constexpr int NW = waves_of(TR);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if constexpr (SIDE == ROWS) {
     if ((a.t & 3) == 0) {
@@ -253,7 +263,7 @@ __device__ __forceinline__ void store_tile(const Args& a, const Smem& s, const f
         int sc[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) sc[k] = a.perm_out ? a.perm_out[c4 + k] : c4 + k;
-        for (int g = wave; g < nrows; g += kWaves) {
+        for (int g = wave; g < nrows; g += NW) {
           const float* tr = tile + g * a.tp;
           *reinterpret_cast<float4*>(a.out + row_of<PLAN>(s, r0, g) * a.t + c4) =
               make_float4(tr[sc[0]], tr[sc[1]], tr[sc[2]], tr[sc[3]]);
@@ -263,26 +273,26 @@ __device__ __forceinline__ void store_tile(const Args& a, const Smem& s, const f
     }
     for (int c = lane; c < a.t; c += 64) {
       const int sc = a.perm_out ? a.perm_out[c] : c;
-      for (int g = wave; g < nrows; g += kWaves)
+      for (int g = wave; g < nrows; g += NW)
         a.out[row_of<PLAN>(s, r0, g) * a.t + c] = tile[g * a.tp + sc];
     }
   } else {
     // every element of every atom-pair block a label column covers, in memory order
     for (int q0 = 0; q0 < a.maxe; q0 += 256) {
-      for (int i0 = 0; i0 < kRows / kWaves; i0 += kPassRows) {
+      for (int i0 = 0; i0 < kRowsPerWave; i0 += kPassRows) {
         int col[kPassRows][4];
 #pragma unroll
         for (int i = 0; i < kPassRows; ++i)
 #pragma unroll
           for (int ch = 0; ch < 4; ++ch) {
-            const int g = wave + kWaves * (i0 + i), q = q0 + ch * 64 + lane;
+            const int g = wave + NW * (i0 + i), q = q0 + ch * 64 + lane;
             col[i][ch] = q < s.ne[g] ? a.raw_slot[s.kind[g] * a.maxe + q] : -1;
           }
 #pragma unroll
         for (int i = 0; i < kPassRows; ++i)
 #pragma unroll
           for (int ch = 0; ch < 4; ++ch) {
-            const int g = wave + kWaves * (i0 + i), q = q0 + ch * 64 + lane;
+            const int g = wave + NW * (i0 + i), q = q0 + ch * 64 + lane;
             if (col[i][ch] >= 0)
               a.fock[s.base[g] + elem_offset(a, s, g, q)] = tile[g * a.tp + col[i][ch]];
           }
@@ -325,35 +335,40 @@ __device__ __forceinline__ const __attribute__((address_space(4))) T* konst(cons
   return (const __attribute__((address_space(4))) T*)(p);
 }
 
-template <bool SKIP, bool DENSE>
-__device__ __forceinline__ void contract_tile(const Args& a, const Smem& s, float* tile) {
+template <bool SKIP, bool DENSE, int TR>
+__device__ __forceinline__ void contract_tile(const Args& a, const Smem<TR>& s, float* tile) {
+  // wave w runs list w % 4 of the schedule: all of it with 4 waves, the
+  // entries w / 4, w / 4 + 2, ... with 8 (each list is in descending cost
+  // order, so the two halves cost about the same)
+  constexpr int STEP = waves_of(TR) / kSchedLists;
   const int wave = uniform(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const auto* sched = konst(a.sched);
   const auto* blk = konst(a.blocks);
-  const int beg = uniform(sched[wave]), end = uniform(sched[wave + 1]);
-  const auto* ids = sched + kWaves + 1;
+  const int list = wave % kSchedLists;
+  const int beg = uniform(sched[list] + wave / kSchedLists), end = uniform(sched[list + 1]);
+  const auto* ids = sched + kSchedLists + 1;
   // lane = row; with 32 rows the upper half-wave repeats the lower one (same
   // reads, same values written)
-  float* row = tile + (lane % kRows) * a.tp;
+  float* row = tile + (lane % TR) * a.tp;
   uint32_t have0 = 0xffffffffu, have1 = 0xffffffffu;  // CG blocks this lane's row has
   if constexpr (SKIP) {
-    const int kind = s.kind[lane % kRows];
+    const int kind = s.kind[lane % TR];
     have0 = kind >= 0 ? a.kind_blocks[2 * kind] : 0u;
     have1 = kind >= 0 ? a.kind_blocks[2 * kind + 1] : 0u;
   }
   // block ids two ahead, block entries one ahead: the scalar loads of the next
   // blocks are in flight while the current block's program runs
   int b0 = beg < end ? ids[beg] : 0;
-  int b1 = beg + 1 < end ? ids[beg + 1] : 0;
+  int b1 = beg + STEP < end ? ids[beg + STEP] : 0;
   int en = 0, ec = 0, ew = 0, ep = -1;
   if (beg < end) { en = blk[4 * b0]; ec = blk[4 * b0 + 1]; ew = blk[4 * b0 + 2]; ep = blk[4 * b0 + 3]; }
-  for (int p = beg; p < end; ++p) {
+  for (int p = beg; p < end; p += STEP) {
     const int b = uniform(b0);
     const int n = uniform(en), c0 = uniform(ec), woff = uniform(ew), prog = uniform(ep);
-    if (p + 1 < end) { en = blk[4 * b1]; ec = blk[4 * b1 + 1]; ew = blk[4 * b1 + 2]; ep = blk[4 * b1 + 3]; }
+    if (p + STEP < end) { en = blk[4 * b1]; ec = blk[4 * b1 + 1]; ew = blk[4 * b1 + 2]; ep = blk[4 * b1 + 3]; }
     b0 = b1;
-    if (p + 2 < end) b1 = ids[p + 2];
+    if (p + 2 * STEP < end) b1 = ids[p + 2 * STEP];
     if constexpr (SKIP) {
       const bool mine = ((b < 32 ? have0 >> b : have1 >> (b - 32)) & 1u) != 0;
       if (__builtin_amdgcn_ballot_w64(mine) == 0) continue;  // no row of the tile has block b
@@ -382,22 +397,23 @@ __device__ __forceinline__ void contract_tile(const Args& a, const Smem& s, floa
 
 // Waves per SIMD each variant is compiled for.  Programs only: registers
 // capped as far as they go without spills (the 25 KB tile of a 196-column row
-// allows six workgroups per CU).  With the dense loops the compiler's own
-// choice is faster (the 49 x 49 loop needs its registers).
+// allows six 4-wave workgroups per CU, its 50 KB 64-row tile three 8-wave
+// ones).  With the dense loops the compiler's own choice is faster (the
+// 49 x 49 loop needs its registers).
 template <int IN, int OUT, bool DENSE>
 struct MinWaves {
   static constexpr int value = DENSE ? 1 : (IN == ROWS ? (OUT == ROWS ? 6 : 5) : 4);
 };
 
 // IN/OUT: the two sides; PLAN: rows come from the row plan (Fock-side calls);
-// DENSE: see contract_tile.
-template <int IN, int OUT, bool DENSE>
-__global__ __launch_bounds__(kThreads, (MinWaves<IN, OUT, DENSE>::value)) void transform_kernel(Args a) {
+// DENSE: see contract_tile; TR: tile rows.
+template <int IN, int OUT, bool DENSE, int TR>
+__global__ __launch_bounds__(waves_of(TR) * 64, (MinWaves<IN, OUT, DENSE>::value)) void transform_kernel(Args a) {
   constexpr bool PLAN = IN == FOCK || OUT == FOCK;
-  extern __shared__ float tile[];  // [kRows][tp]
-  __shared__ Smem s;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kRows;
-  const int nrows = static_cast<int>((a.R - r0) < kRows ? (a.R - r0) : kRows);
+  extern __shared__ float tile[];  // [TR][tp]
+  __shared__ Smem<TR> s;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * TR;
+  const int nrows = static_cast<int>((a.R - r0) < TR ? (a.R - r0) : TR);
   if constexpr (PLAN) {
     load_meta(a, s, r0, nrows);
     __syncthreads();
@@ -467,7 +483,8 @@ int check_tables(int t, int nblocks, const int32_t* blocks, const float* w, cons
   MALOQ_REQUIRE(t > 0 && nblocks > 0, "bad sizes (t=%d, nblocks=%d)", t, nblocks);
   MALOQ_REQUIRE(blocks && sched, "null CG table");  // w may be NULL: every block has a program
   const int tp = t | 1;
-  MALOQ_REQUIRE(static_cast<int64_t>(bt::kRows) * tp * 4 <= bt::kMaxTileBytes,
+  // a 32-row tile and its row descriptors (32 bytes a row) in one CU's LDS
+  MALOQ_REQUIRE(static_cast<int64_t>(bt::kNarrowRows) * (tp * 4 + 32) <= bt::kMaxTileBytes,
                 "label width %d too large for one LDS tile", t);
   return MALOQ_OK;
 }
@@ -503,17 +520,36 @@ int set_fock_side(bt::Args& a, float* fock, int64_t ld, const int32_t* row_meta,
   return MALOQ_OK;
 }
 
+// Waves of TR-row workgroups that fit on one CU by LDS (tile + Smem), at most
+// 24 (the register budget of the program-only variants).
+int resident_waves(int tr, int tp) {
+  const int64_t lds = static_cast<int64_t>(tr) * tp * 4 + static_cast<int64_t>(tr) * 32;
+  const int nw = bt::waves_of(tr);
+  int64_t wgs = bt::kMaxTileBytes / lds;
+  if (wgs * nw > 24) wgs = 24 / nw;
+  return static_cast<int>(wgs * nw);
+}
+
+template <int IN, int OUT, int TR>
+int launch_tiles(const bt::Args& a, void* stream, const char* name) {
+  const int64_t groups = (a.R + TR - 1) / TR;
+  const size_t shm = static_cast<size_t>(TR) * a.tp * sizeof(float);
+  const dim3 grid(static_cast<unsigned>(groups)), block(bt::waves_of(TR) * 64);
+  if (a.w != nullptr)
+    hipLaunchKernelGGL((bt::transform_kernel<IN, OUT, true, TR>), grid, block, shm,
+                       static_cast<hipStream_t>(stream), a);
+  else
+    hipLaunchKernelGGL((bt::transform_kernel<IN, OUT, false, TR>), grid, block, shm,
+                       static_cast<hipStream_t>(stream), a);
+  return check_launch(name);
+}
+
+// 64-row tiles wherever they keep as many waves resident as 32-row tiles.
 template <int IN, int OUT>
 int launch_transform(const bt::Args& a, void* stream, const char* name) {
-  const int64_t groups = (a.R + bt::kRows - 1) / bt::kRows;
-  const size_t shm = static_cast<size_t>(bt::kRows) * a.tp * sizeof(float);
-  if (a.w != nullptr)
-    hipLaunchKernelGGL((bt::transform_kernel<IN, OUT, true>), dim3(static_cast<unsigned>(groups)),
-                       dim3(kThreads), shm, static_cast<hipStream_t>(stream), a);
-  else
-    hipLaunchKernelGGL((bt::transform_kernel<IN, OUT, false>), dim3(static_cast<unsigned>(groups)),
-                       dim3(kThreads), shm, static_cast<hipStream_t>(stream), a);
-  return check_launch(name);
+  if (resident_waves(bt::kWideRows, a.tp) >= resident_waves(bt::kNarrowRows, a.tp))
+    return launch_tiles<IN, OUT, bt::kWideRows>(a, stream, name);
+  return launch_tiles<IN, OUT, bt::kNarrowRows>(a, stream, name);
 }
 
 }  // namespace
