@@ -224,7 +224,12 @@ __device__ __forceinline__ void load_tile(const Args& a, const Smem<TR>& s, floa
     // wave w walks the atom-pair blocks of rows w, w + NW, ... in memory order
     // (coalesced), passes of kPassRows rows x 256 elements, and drops every
     // element into its label column.
-    for (int i = threadIdx.x; i < TR * a.tp; i += NW * 64) tile[i] = 0.f;
+    {
+      const int n = TR * a.tp, n4 = n >> 2;
+      float4* t4 = reinterpret_cast<float4*>(tile);
+      for (int i = threadIdx.x; i < n4; i += NW * 64) t4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (threadIdx.x < (n & 3)) tile[4 * n4 + threadIdx.x] = 0.f;
+    }
     __syncthreads();
     for (int q0 = 0; q0 < a.maxe; q0 += 256) {
       for (int i0 = 0; i0 < kRowsPerWave; i0 += kPassRows) {
@@ -410,7 +415,7 @@ struct MinWaves {
 template <int IN, int OUT, bool DENSE, int TR>
 __global__ __launch_bounds__(waves_of(TR) * 64, (MinWaves<IN, OUT, DENSE>::value)) void transform_kernel(Args a) {
   constexpr bool PLAN = IN == FOCK || OUT == FOCK;
-  extern __shared__ float tile[];  // [TR][tp]
+  extern __shared__ __attribute__((aligned(16))) float tile[];  // [TR][tp]
   __shared__ Smem<TR> s;
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * TR;
   const int nrows = static_cast<int>((a.R - r0) < TR ? (a.R - r0) : TR);
