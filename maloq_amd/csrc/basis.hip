@@ -95,6 +95,11 @@ struct Smem {
 };
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
 
 // Row plan entry r: int4 (base lo, base hi, r, (kind + 1) | n_i << 16 | n_j << 24).
 __global__ __launch_bounds__(kThreads) void row_meta_kernel(
@@ -120,6 +125,7 @@ __device__ __forceinline__ void load_meta(const Args& a, Smem<TR>& s, int64_t r0
   const int g = threadIdx.x;
   if (g >= TR) return;
   if (g >= nrows) {
+    s.base[g] = 0;
     s.kind[g] = -1;
     s.ne[g] = 0;
     s.row[g] = -1;
@@ -282,7 +288,12 @@ __device__ __forceinline__ void store_tile(const Args& a, const Smem<TR>& s, con
         a.out[row_of<PLAN>(s, r0, g) * a.t + c] = tile[g * a.tp + sc];
     }
   } else {
-    // every element of every atom-pair block a label column covers, in memory order
+    // every element of every atom-pair block a label column covers, in memory
+    // order.  A row's block base and table row are the same for the whole
+    // wave (scalar registers); the per-element addresses are offsets from
+    // them.  Past a block's end the table read is of element 0 (in bounds;
+    // rows past the tile's end have kind 0's row and base 0) and nothing is
+    // stored.
     for (int q0 = 0; q0 < a.maxe; q0 += 256) {
       for (int i0 = 0; i0 < kRowsPerWave; i0 += kPassRows) {
         int col[kPassRows][4];
@@ -291,15 +302,18 @@ __device__ __forceinline__ void store_tile(const Args& a, const Smem<TR>& s, con
 #pragma unroll
           for (int ch = 0; ch < 4; ++ch) {
             const int g = wave + NW * (i0 + i), q = q0 + ch * 64 + lane;
-            col[i][ch] = q < s.ne[g] ? a.raw_slot[s.kind[g] * a.maxe + q] : -1;
+            const bool ok = q < uniform(s.ne[g]);
+            const int32_t* slot = a.raw_slot + uniform(s.kind[g] > 0 ? s.kind[g] : 0) * a.maxe;
+            const int c = slot[ok ? q : 0];
+            col[i][ch] = ok ? c : -1;
           }
 #pragma unroll
         for (int i = 0; i < kPassRows; ++i)
 #pragma unroll
           for (int ch = 0; ch < 4; ++ch) {
             const int g = wave + NW * (i0 + i), q = q0 + ch * 64 + lane;
-            if (col[i][ch] >= 0)
-              a.fock[s.base[g] + elem_offset(a, s, g, q)] = tile[g * a.tp + col[i][ch]];
+            float* blk = a.fock + uniform64(s.base[g]);
+            if (col[i][ch] >= 0) blk[elem_offset(a, s, g, q)] = tile[g * a.tp + col[i][ch]];
           }
       }
     }
