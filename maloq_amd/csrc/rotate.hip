@@ -13,10 +13,13 @@
 // (2l+1) x (2l+1) blocks are touched: sum_l (2l+1)^2 MACs per channel instead
 // of the d^2 of a dense bmm.
 //
-// A workgroup takes EPB = 256 / d edges: phase 1 puts their D blocks in LDS
-// (one thread per (edge, row), as the dense Wigner kernel); phase 2 runs one
-// thread per (edge, 4 channels), reading each degree's 2l+1 input rows as
+// A workgroup takes epb <= EPB = 256 / d edges: phase 1 puts their D blocks in
+// LDS (one thread per (edge, row), as the dense Wigner kernel); phase 2 runs
+// one thread per (edge, 4 channels), reading each degree's 2l+1 input rows as
 // 16-byte (fp32) or 8-byte (bf16) vectors and writing the 2l+1 output rows.
+// epb = min(EPB, 256 / (C / 4)): phase 2 is then one round of the 256 threads
+// (C = 128, d = 25: 8 edges x 32 channel quads) instead of a full round and a
+// quarter-wave tail.
 // HBM-bound: d C (s_in + s_out) bytes per edge plus 12 (Euler triple).
 #include "common.h"
 #include "wigner_device.h"
@@ -34,6 +37,7 @@ struct Args {
   const float* wigner;    // [E, d, d] or null
   const float* jd;        // packed J_0..J_L (with eulers)
   int inverse;
+  int epb;                // edges per workgroup (<= Shape::EPB)
   void* out;              // [E, d, C]
 };
 
@@ -75,8 +79,8 @@ __global__ __launch_bounds__(256) void rotate_kernel(Args a) {
   __shared__ float sM2[EPB][JSZ];
   __shared__ float sD[EPB][JSZ];
   const int t = threadIdx.x;
-  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * EPB;
-  const int nvalid = static_cast<int>((a.E - e0) < EPB ? (a.E - e0) : EPB);
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * a.epb;
+  const int nvalid = static_cast<int>((a.E - e0) < a.epb ? (a.E - e0) : a.epb);
 
   // ---- phase 1: the D blocks of the workgroup's edges
   const int el = t / d, row = t - (t / d) * d;
@@ -160,8 +164,10 @@ struct BF16T {
 };
 
 template <int L>
-int launch(int x_dtype, int out_dtype, const Args& a, hipStream_t s) {
-  const int64_t grid = (a.E + Shape<L>::EPB - 1) / Shape<L>::EPB;
+int launch(int x_dtype, int out_dtype, Args a, hipStream_t s) {
+  const int by_channels = 256 / (a.C / 4);
+  a.epb = by_channels < 1 ? 1 : (by_channels < Shape<L>::EPB ? by_channels : Shape<L>::EPB);
+  const int64_t grid = (a.E + a.epb - 1) / a.epb;
   MALOQ_REQUIRE(grid < (int64_t(1) << 31), "grid too large");
   const dim3 g(static_cast<unsigned>(grid)), b(256);
   if (x_dtype == 0 && out_dtype == 0) hipLaunchKernelGGL((rotate_kernel<L, F32T, F32T>), g, b, 0, s, a);
