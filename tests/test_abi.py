@@ -54,3 +54,17 @@ def test_supported_shapes_and_rotate_validation_without_gpu():
         _lib.call("maloq_rotate", 0, 0, 2, None, 6, None, 1, None, None, None, 0, None, None)
     with pytest.raises(_lib.MaloqHipError, match="no message kernels"):
         _lib.call("maloq_message_wigner_rows", 4, 3, None, None, 1, None, None)
+
+
+def test_label_width_limit_without_gpu():
+    """A 32-row fp32 tile of the label width and its 32-byte row descriptors
+    must fit one CU's 160 KB of LDS: 1271 is the widest row accepted (checked on
+    the host; zero rows launch nothing)."""
+    import numpy as np
+    from maloq_amd import _lib
+    blocks = np.array([[1, 0, 0, 0]], dtype=np.int32)
+    sched = np.array([0, 1, 1, 1, 1, 0], dtype=np.int32)
+    bp, sp = blocks.ctypes.data, sched.ctypes.data
+    _lib.call("maloq_label_transform", None, None, None, None, 0, 1271, 1, bp, None, sp, None)
+    with pytest.raises(_lib.MaloqHipError, match="label width 1272 too large"):
+        _lib.call("maloq_label_transform", None, None, None, None, 0, 1272, 1, bp, None, sp, None)
