@@ -361,10 +361,14 @@ __device__ __forceinline__ void hidden_layer(int c, const float* prm, int cin, c
 
 // ---------------------------------------------------------------- forward
 // Persistent: each workgroup (FW_W waves) stages the hidden parameters and the
-// output bias once and keeps the W_o fragments of its waves' output tiles in
-// registers (wave w owns a contiguous range of 32-output tiles), then loops
-// over 64-edge tiles.  The output loop has no loads, so its stores are never
-// waited on.  Results go through a per-wave LDS block of 64 edges x 128 bytes
+// output bias once, then works through an equal share of the (64-edge tile,
+// 128-byte output group) units, in order: for each tile its share touches it
+// runs the hidden chain, then its waves split the tile's groups of that share
+// (contiguous ranges of 32-output tiles, W_o fragments loaded in chunks of
+// MAXT tiles as they are used).  Equal shares of units rather than whole
+// tiles: 575 tiles on 256 CUs would give some CUs three tiles against an
+// average of 2.25.  Only the workgroup holding a tile's first group saves
+// u_H.  The output loop has no loads, so its stores are never waited on.  Results go through a per-wave LDS block of 64 edges x 128 bytes
 // of outputs and leave as whole 128-byte row segments (16 bytes per lane,
 // eight lanes per row): stores in the accumulator's lane order (16 bytes per
 // row per instruction) reach less than half the HBM write rate.
@@ -391,11 +395,11 @@ __global__ __launch_bounds__(FW_W * 64) void radial_fwd_kernel(Args a) {
   char* stg = reinterpret_cast<char*>(buf1 + TE * pitch(cmax)) + wave * TE * FW_SP;  // this wave's block
   stage_vec<NTH>(a.bo, cout, bo, tid);
   stage_params<NTH>(a, prm, tid);
-  // this wave's output tiles [tw0, tw0 + ntw) and their W_o fragments (chunks of MAXT tiles)
+  // this wave's output tiles [tw0, tw0 + ntw) of the current edge tile and
+  // their W_o fragments (chunks of MAXT tiles)
   constexpr int GT = 64 / (sizeof(raw) * 16);  // tiles per 128-byte group: 2 (bf16) or 1 (fp32)
   const int not_ = cout / 32, ngrp = not_ / GT;
-  const int gw0 = wave * ngrp / FW_W, gw1 = (wave + 1) * ngrp / FW_W;
-  const int tw0 = gw0 * GT, ntw = (gw1 - gw0) * GT;
+  int tw0 = 0, ntw = 0;
   const raw* wo = reinterpret_cast<const raw*>(a.wo);
   const raw* wlane = wo + static_cast<int64_t>(lane & 31) * CH + (lane >> 5) * VEC;
   frag_t af[MAXT][NK];
@@ -409,11 +413,21 @@ __global__ __launch_bounds__(FW_W * 64) void radial_fwd_kernel(Args a) {
         af[t][kc] = *reinterpret_cast<const frag_t*>(wlane + static_cast<int64_t>(ot) * 32 * CH + kc * KC);
     }
   };
-  const bool one_chunk = ntw <= MAXT;
-  if (one_chunk) load_chunk(0);
   __syncthreads();
   raw* out = reinterpret_cast<raw*>(a.out);
-  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+  // this workgroup's units [u0, u1) of ntiles x ngrp
+  const int64_t units = ntiles * ngrp;
+  const int64_t u0 = static_cast<int64_t>(blockIdx.x) * units / gridDim.x;
+  const int64_t u1 = static_cast<int64_t>(blockIdx.x + 1) * units / gridDim.x;
+  if (u0 >= u1) return;  // whole workgroup
+  for (int64_t tile = u0 / ngrp; tile * ngrp < u1; ++tile) {
+    const int glo = static_cast<int>(u0 > tile * ngrp ? u0 - tile * ngrp : 0);
+    const int ghi = static_cast<int>(u1 - tile * ngrp < ngrp ? u1 - tile * ngrp : ngrp);
+    {
+      const int n = ghi - glo, gw0 = glo + wave * n / FW_W, gw1 = glo + (wave + 1) * n / FW_W;
+      tw0 = gw0 * GT;
+      ntw = (gw1 - gw0) * GT;
+    }
     const int64_t e0 = tile * TE;
     const int nvalid = static_cast<int>((a.E - e0) < TE ? (a.E - e0) : TE);
     stage_rows<NTH>(a.x, e0, nvalid, a.c[0], act0, tid);
@@ -432,7 +446,7 @@ __global__ __launch_bounds__(FW_W * 64) void radial_fwd_kernel(Args a) {
     const float* uH = ain;  // [TE][pitch(CH)]
     // saved u_H rows (TM raw) for the weight gradient: the CH / VEC 16-byte
     // pieces of each row round-robin over the waves
-    if (a.save != nullptr && lane < nvalid) {
+    if (a.save != nullptr && glo == 0 && lane < nvalid) {
       raw* sv = reinterpret_cast<raw*>(a.save) + (e0 + lane) * CH;
       for (int f = wave; f < CH / VEC; f += FW_W)
         *reinterpret_cast<frag_t*>(sv + f * VEC) = pack_frag(uH + lane * pitch(CH) + f * VEC, TM{});
@@ -445,7 +459,7 @@ __global__ __launch_bounds__(FW_W * 64) void radial_fwd_kernel(Args a) {
       for (int kc = 0; kc < NK; ++kc)
         bf[nt][kc] = pack_frag(uH + (32 * nt + (lane & 31)) * pitch(CH) + kc * KC + (lane >> 5) * VEC, TM{});
     for (int t0 = 0; t0 < ntw; t0 += MAXT) {
-      if (!one_chunk) load_chunk(t0);
+      load_chunk(t0);
 #pragma unroll
       for (int t = 0; t < MAXT; ++t) {
         if (t0 + t >= ntw) break;
