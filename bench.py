@@ -229,7 +229,13 @@ def basis_timing(bw, reps=50):
     inv = kernel_time_events(lambda: hip.irreps_to_fock(out, back, *dev_args, t.orbital_template,
                                                         block_data_offsets=bw["bdo"], plan=plan), reps)
     rt = ((back - bw["data"]).abs().max() / bw["data"].abs().max()).item()
-    return fwd, inv, rt, plan_s
+    # without a plan: one launch each, the rows described from the pair list
+    # inside the kernel (a structure transformed once)
+    fwd_pl = kernel_time_events(lambda: hip.fock_to_irreps(bw["data"], *dev_args, t.orbital_template,
+                                                           block_data_offsets=bw["bdo"]), reps)
+    inv_pl = kernel_time_events(lambda: hip.irreps_to_fock(out, back, *dev_args, t.orbital_template,
+                                                           block_data_offsets=bw["bdo"]), reps)
+    return fwd, inv, rt, plan_s, fwd_pl, inv_pl
 
 
 # ---------------------------------------------------------------- CPU legs
@@ -528,10 +534,15 @@ def sparse_basis_leg(sw, reps=30):
     ti = kernel_time_events(lambda: hip.irreps_to_fock(irr, back, *dev_args, t.orbital_template,
                                                        block_data_offsets=sw["bdo"], plan=plan), reps)
     rt = ((back - sw["data"]).abs().max() / sw["data"].abs().max()).item()
+    tfp = kernel_time_events(lambda: hip.fock_to_irreps(sw["data"], *dev_args, t.orbital_template,
+                                                        block_data_offsets=sw["bdo"]), reps)
+    tip = kernel_time_events(lambda: hip.irreps_to_fock(irr, back, *dev_args, t.orbital_template,
+                                                        block_data_offsets=sw["bdo"]), reps)
     nb = sw["n_blocks"]
     bpb = (sw["block_bytes"] + 4 * sw["T"] * nb) / nb
     return {"metric": "H-blocks/s", "fwd": nb / tf, "inv": nb / ti, "fwd_with_plan": nb / (tf + tplan),
-            "inv_with_plan": nb / (ti + tplan), "plan_ms": tplan * 1e3, "blocks": nb, "T": sw["T"],
+            "inv_with_plan": nb / (ti + tplan), "fwd_pair_list": nb / tfp, "inv_pair_list": nb / tip,
+            "plan_ms": tplan * 1e3, "blocks": nb, "T": sw["T"],
             "round_trip_rel_err": rt,
             "roofline": {"kernel": "transform_kernel<FOCK,ROWS> (block list)", "bound": "hbm",
                          "achieved": bpb * nb / tf / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
@@ -930,11 +941,12 @@ def main(argv=None):
             result[cfg] = message_leg(cfg, "bf16", max(5, args.steps // 2), 3, cpu=not args.no_cpu)
         print("[bench] basis transform (config 3) ...", file=sys.stderr, flush=True)
         bw = basis_workload()
-        tf, ti, rt, tplan = basis_timing(bw)
+        tf, ti, rt, tplan, tfp, tip = basis_timing(bw)
         bpb = (bw["block_bytes"] + 4 * bw["T"] * bw["n_blocks"]) / bw["n_blocks"]
         result["basis_transform"] = {
             "metric": "H-blocks/s", "fwd": bw["n_blocks"] / tf, "inv": bw["n_blocks"] / ti,
             "fwd_with_plan": bw["n_blocks"] / (tf + tplan), "inv_with_plan": bw["n_blocks"] / (ti + tplan),
+            "fwd_pair_list": bw["n_blocks"] / tfp, "inv_pair_list": bw["n_blocks"] / tip,
             "blocks": bw["n_blocks"], "round_trip_rel_err": rt, "plan_ms": tplan * 1e3,
             "roofline": {"bound": "hbm", "achieved": bpb * bw["n_blocks"] / tf / 1e9, "peak": PEAK_HBM / 1e9,
                          "unit": "GB/s", "frac": bpb * bw["n_blocks"] / tf / PEAK_HBM,

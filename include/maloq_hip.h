@@ -144,6 +144,30 @@ int maloq_irreps_to_fock(const float* irreps, const int32_t* perm_in, float* foc
                          const int32_t* blocks, const float* w, const int32_t* sched,
                          void* stream);
 
+/* The two fused transforms above for a one-off pair list, without a row plan:
+ * each workgroup describes its own rows exactly as maloq_basis_row_meta would
+ * (the same ld / data_offsets / fock_block_offsets / atomic_numbers / rows /
+ * cols / pair_kind / maxe arguments), so a single call does the work of
+ * maloq_basis_row_meta + maloq_fock_to_irreps (or maloq_irreps_to_fock) with
+ * identical results.  For block-list storage ld is ignored.  Replaces the same
+ * reference calls as those two; a caller that transforms one structure once
+ * (make_targets per molecule and spin, fock_targets_batched.py:426-441) needs
+ * no plan. */
+int maloq_fock_to_irreps_pairs(const float* fock, int64_t ld, const int64_t* data_offsets,
+                               const int32_t* fock_block_offsets, const int32_t* atomic_numbers,
+                               const int32_t* rows, const int32_t* cols, int64_t num_rows,
+                               const int32_t* pair_kind, const int32_t* raw_slot, int maxe,
+                               const uint32_t* kind_blocks, float* out, const int32_t* perm_out,
+                               int t, int nblocks, const int32_t* blocks, const float* w,
+                               const int32_t* sched, void* stream);
+int maloq_irreps_to_fock_pairs(const float* irreps, const int32_t* perm_in, float* fock, int64_t ld,
+                               const int64_t* data_offsets, const int32_t* fock_block_offsets,
+                               const int32_t* atomic_numbers, const int32_t* rows, const int32_t* cols,
+                               int64_t num_rows, const int32_t* pair_kind, const int32_t* raw_slot,
+                               int maxe, const uint32_t* kind_blocks, int t, int nblocks,
+                               const int32_t* blocks, const float* w, const int32_t* sched,
+                               void* stream);
+
 /* The dense n x n matrix (row-major, output column x input column) of compiled
  * CG program p = dir * 16 + l1 * 4 + l2 (dir 0: get_net_out, the
  * decomposition's wms_H block; 1: get_H, its wms block; 2: get_H's adjoint,

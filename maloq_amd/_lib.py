@@ -37,6 +37,10 @@ SIGNATURES = {
     "maloq_basis_row_meta": [_i64, _p, _p, _p, _p, _p, _i64, _p, _i32, _p, _p],
     "maloq_fock_to_irreps": [_p, _i64, _p, _i64, _p, _i32, _p, _p, _p, _i32, _i32, _p, _p, _p, _p],
     "maloq_irreps_to_fock": [_p, _p, _p, _i64, _p, _i64, _p, _i32, _p, _i32, _i32, _p, _p, _p, _p],
+    "maloq_fock_to_irreps_pairs": [_p, _i64, _p, _p, _p, _p, _p, _i64, _p, _p, _i32, _p, _p, _p, _i32, _i32, _p,
+                                   _p, _p, _p],
+    "maloq_irreps_to_fock_pairs": [_p, _p, _p, _i64, _p, _p, _p, _p, _p, _i64, _p, _p, _i32, _p, _i32, _i32, _p,
+                                   _p, _p, _p],
     "maloq_matrix2label": [_p, _i64, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _i64, _i32, _p],
     "maloq_segment_sum": [_p, _p, _p, _i64, _i64, _p, _p],
     "maloq_label_scalar_shift": [_p, _i64, _i64, _p, _p, _p, _i32, ctypes.c_float, _p],

@@ -277,7 +277,8 @@ class HipE3TensorDecomp:
             if fock.dim() != 2 or fock.stride(1) != 1:
                 raise ValueError("dense Fock matrix must be 2-D with unit column stride")
             return fock.stride(0), None
-        return 0, sparse_offsets.to(torch.int64).contiguous()
+        # on the Fock matrix's device: the kernels read it there
+        return 0, torch.as_tensor(sparse_offsets).to(device=fock.device, dtype=torch.int64).contiguous()
 
     def make_plan(self, fock, fock_block_offsets, atomic_numbers, rows, cols, orbital_template,
                   block_data_offsets=None):
@@ -307,15 +308,39 @@ class HipE3TensorDecomp:
             raise ValueError("plan was built for another Fock storage or template")
         return plan
 
+    def _pairs(self, fock, fock_block_offsets, atomic_numbers, rows, cols, block_data_offsets):
+        """Device arguments of the plan-less entry points (the pair list itself)."""
+        if fock.dtype != torch.float32:
+            raise ValueError("Unsupported dtype for the Fock matrix; only float32 is supported.")
+        dev = fock.device
+        off, Z, r_, c_ = (_i32(x, dev) for x in (fock_block_offsets, atomic_numbers, rows, cols))
+        if r_.shape != c_.shape:
+            raise ValueError("rows and cols must have the same length")
+        ld, bdo = self._storage(fock, block_data_offsets)
+        return ld, bdo, off, Z, r_, c_
+
     def fock_to_irreps(self, fock, fock_block_offsets, atomic_numbers, rows, cols, orbital_template,
                        block_data_offsets=None, plan=None):
         """Labels in the irreps basis for every atom pair (rows[r], cols[r]):
-        gather by template + get_net_out in one launch (plus the row plan if
-        none is given)."""
+        gather by template + get_net_out in one launch.  Without a plan the
+        kernel describes the rows from the pair list itself (one launch, no
+        plan); with one (make_plan, for a structure transformed many times) it
+        reads the plan."""
         _lib.require_cuda(fock)
+        tabs = self._template_tables(orbital_template)
+        if plan is None:
+            ld, bdo, off, Z, r_, c_ = self._pairs(fock, fock_block_offsets, atomic_numbers, rows, cols,
+                                                 block_data_offsets)
+            R = int(r_.shape[0])
+            out = torch.empty(R, self.total_in_dim, device=fock.device, dtype=torch.float32)
+            _lib.call("maloq_fock_to_irreps_pairs", _lib.ptr(fock), ld, _lib.ptr(bdo), _lib.ptr(off), _lib.ptr(Z),
+                      _lib.ptr(r_), _lib.ptr(c_), R, _lib.ptr(tabs["pair_kind"]), _lib.ptr(tabs["raw"]),
+                      tabs["maxe"], _lib.ptr(tabs["kind_blocks"]), _lib.ptr(out), _lib.ptr(self._perm),
+                      self.total_in_dim, self.num_blocks, _lib.ptr(self._blocks_fwd), _lib.ptr(self._wk_fwd),
+                      _lib.ptr(self._sched), _lib.stream_of(fock.device))
+            return out
         plan = self._plan_for(plan, fock, fock_block_offsets, atomic_numbers, rows, cols, orbital_template,
                               block_data_offsets)
-        tabs = self._template_tables(orbital_template)
         out = torch.empty(plan.num_rows, self.total_in_dim, device=fock.device, dtype=torch.float32)
         _lib.call("maloq_fock_to_irreps", _lib.ptr(fock), plan.ld, _lib.ptr(plan.meta), plan.num_rows,
                   _lib.ptr(tabs["raw"]), tabs["maxe"], _lib.ptr(tabs["kind_blocks"]), _lib.ptr(out),
@@ -325,15 +350,29 @@ class HipE3TensorDecomp:
 
     def irreps_to_fock(self, net_out, fock, fock_block_offsets, atomic_numbers, rows, cols,
                        orbital_template, block_data_offsets=None, plan=None):
-        """get_H per row, scattered into ``fock`` (in place) at the template's entries."""
+        """get_H per row, scattered into ``fock`` (in place) at the template's
+        entries (without a plan: one launch from the pair list, as
+        fock_to_irreps)."""
         self._check(net_out, self.total_in_dim)
         _lib.require_cuda(fock)
+        tabs = self._template_tables(orbital_template)
+        net_out = net_out.contiguous()
+        if plan is None:
+            ld, bdo, off, Z, r_, c_ = self._pairs(fock, fock_block_offsets, atomic_numbers, rows, cols,
+                                                 block_data_offsets)
+            R = int(r_.shape[0])
+            if R != net_out.shape[0]:
+                raise ValueError("net_out rows must match the atom-pair list")
+            _lib.call("maloq_irreps_to_fock_pairs", _lib.ptr(net_out), _lib.ptr(self._perm), _lib.ptr(fock), ld,
+                      _lib.ptr(bdo), _lib.ptr(off), _lib.ptr(Z), _lib.ptr(r_), _lib.ptr(c_), R,
+                      _lib.ptr(tabs["pair_kind"]), _lib.ptr(tabs["raw"]), tabs["maxe"], _lib.ptr(tabs["kind_blocks"]),
+                      self.total_in_dim, self.num_blocks, _lib.ptr(self._blocks_inv), _lib.ptr(self._wk_inv),
+                      _lib.ptr(self._sched), _lib.stream_of(fock.device))
+            return fock
         plan = self._plan_for(plan, fock, fock_block_offsets, atomic_numbers, rows, cols, orbital_template,
                               block_data_offsets)
         if plan.num_rows != net_out.shape[0]:
             raise ValueError("net_out rows must match the atom-pair list")
-        tabs = self._template_tables(orbital_template)
-        net_out = net_out.contiguous()
         _lib.call("maloq_irreps_to_fock", _lib.ptr(net_out), _lib.ptr(self._perm), _lib.ptr(fock), plan.ld,
                   _lib.ptr(plan.meta), plan.num_rows, _lib.ptr(tabs["raw"]), tabs["maxe"],
                   _lib.ptr(tabs["kind_blocks"]), self.total_in_dim, self.num_blocks, _lib.ptr(self._blocks_inv),

@@ -29,7 +29,9 @@
 //
 // Fock-side calls run on a row plan: maloq_basis_row_meta describes every row
 // (block base, original row index, element-pair kind, block shape) once per
-// structure, in row order.
+// structure, in row order.  The *_pairs entry points take the pair list
+// instead: each workgroup describes its own rows the same way (one launch, no
+// plan; the same bits).
 //
 // Reference semantics: e3TensorDecomp.get_H / get_net_out
 // (fock_utils/utils_tensor_decomp.py:154-169), the Triton kernels K6/K8
@@ -73,7 +75,14 @@ struct Args {
   // Fock side
   float* fock;
   int64_t ld;               // dense row stride, or 0 for block-list storage
-  const int4* meta;         // [R] row plan (maloq_basis_row_meta), processing order
+  const int4* meta;         // [R] row plan (maloq_basis_row_meta), processing order, or
+                            // null: the kernel describes its rows itself from the pair list
+  const int64_t* data_offsets;  // pair list (meta null): block-list bases, or null (dense)
+  const int32_t* off;           //   [atoms + 1] first orbital of each atom
+  const int32_t* Z;             //   [atoms] atomic numbers
+  const int32_t* rows;          //   [R] atom i of pair r
+  const int32_t* cols;          //   [R] atom j of pair r
+  const int32_t* pair_kind;     //   [100 * 100] element-pair kind, or -1
   const int32_t* raw_slot;  // [kinds, maxe]: label column of block element q, or -1
   int maxe;                 // row length of raw_slot (largest n_i * n_j)
   const uint32_t* kind_blocks;  // [kinds, 2]: CG blocks present for the kind (bit b), or null
@@ -101,14 +110,12 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
   return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-// Row plan entry r: int4 (base lo, base hi, r, (kind + 1) | n_i << 16 | n_j << 24).
-__global__ __launch_bounds__(kThreads) void row_meta_kernel(
-    int64_t R, int64_t ld, const int64_t* __restrict__ data_offsets,
-    const int32_t* __restrict__ off, const int32_t* __restrict__ Z,
-    const int32_t* __restrict__ rows, const int32_t* __restrict__ cols,
-    const int32_t* __restrict__ pair_kind, int maxe, int4* __restrict__ meta) {
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  if (r >= R) return;
+// Row plan entry of pair r: int4 (base lo, base hi, r, (kind + 1) | n_i << 16 |
+// n_j << 24).
+__device__ __forceinline__ int4 describe_row(int64_t r, int64_t ld, const int64_t* __restrict__ data_offsets,
+                                             const int32_t* __restrict__ off, const int32_t* __restrict__ Z,
+                                             const int32_t* __restrict__ rows, const int32_t* __restrict__ cols,
+                                             const int32_t* __restrict__ pair_kind, int maxe) {
   const int i = rows[r], j = cols[r];
   const int oi = off[i], oj = off[j];
   const int ni = off[i + 1] - oi, nj = off[j + 1] - oj;
@@ -116,11 +123,21 @@ __global__ __launch_bounds__(kThreads) void row_meta_kernel(
   int kind = pair_kind[Z[i] * kMaxElements + Z[j]];
   // a block larger than the template's rows cannot be one of its element pairs
   if (ni > 255 || nj > 255 || ni * nj > maxe) kind = -1;
-  meta[r] = make_int4(static_cast<int>(base & 0xffffffff), static_cast<int>(base >> 32),
-                      static_cast<int>(r), (kind + 1) | ((ni & 255) << 16) | ((nj & 255) << 24));
+  return make_int4(static_cast<int>(base & 0xffffffff), static_cast<int>(base >> 32), static_cast<int>(r),
+                   (kind + 1) | ((ni & 255) << 16) | ((nj & 255) << 24));
 }
 
-template <int TR>
+__global__ __launch_bounds__(kThreads) void row_meta_kernel(
+    int64_t R, int64_t ld, const int64_t* __restrict__ data_offsets,
+    const int32_t* __restrict__ off, const int32_t* __restrict__ Z,
+    const int32_t* __restrict__ rows, const int32_t* __restrict__ cols,
+    const int32_t* __restrict__ pair_kind, int maxe, int4* __restrict__ meta) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (r >= R) return;
+  meta[r] = describe_row(r, ld, data_offsets, off, Z, rows, cols, pair_kind, maxe);
+}
+
+template <int TR, bool PAIRS>
 __device__ __forceinline__ void load_meta(const Args& a, Smem<TR>& s, int64_t r0, int nrows) {
   const int g = threadIdx.x;
   if (g >= TR) return;
@@ -131,7 +148,13 @@ __device__ __forceinline__ void load_meta(const Args& a, Smem<TR>& s, int64_t r0
     s.row[g] = -1;
     return;
   }
-  const int4 m = a.meta[r0 + g];
+  // from the plan, or (PAIRS) described here from the pair list: the plan's
+  // entry r is the description of pair r
+  int4 m;
+  if constexpr (PAIRS)
+    m = describe_row(r0 + g, a.ld, a.data_offsets, a.off, a.Z, a.rows, a.cols, a.pair_kind, a.maxe);
+  else
+    m = a.meta[r0 + g];
   s.base[g] = static_cast<int64_t>(static_cast<uint32_t>(m.x)) | (static_cast<int64_t>(m.y) << 32);
   s.row[g] = static_cast<uint32_t>(m.z);
   const int kind = (m.w & 0xffff) - 1, ni = (m.w >> 16) & 255, nj = (m.w >> 24) & 255;
@@ -425,8 +448,9 @@ struct MinWaves {
 };
 
 // IN/OUT: the two sides; PLAN: rows come from the row plan (Fock-side calls);
-// DENSE: see contract_tile; TR: tile rows.
-template <int IN, int OUT, bool DENSE, int TR>
+// DENSE: see contract_tile; TR: tile rows; PAIRS: Fock side without a plan
+// (its own instantiation: describing rows costs the plan path no registers).
+template <int IN, int OUT, bool DENSE, int TR, bool PAIRS = false>
 __global__ __launch_bounds__(waves_of(TR) * 64, (MinWaves<IN, OUT, DENSE>::value)) void transform_kernel(Args a) {
   constexpr bool PLAN = IN == FOCK || OUT == FOCK;
   extern __shared__ __attribute__((aligned(16))) float tile[];  // [TR][tp]
@@ -434,7 +458,7 @@ __global__ __launch_bounds__(waves_of(TR) * 64, (MinWaves<IN, OUT, DENSE>::value
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * TR;
   const int nrows = static_cast<int>((a.R - r0) < TR ? (a.R - r0) : TR);
   if constexpr (PLAN) {
-    load_meta(a, s, r0, nrows);
+    load_meta<TR, PAIRS>(a, s, r0, nrows);
     __syncthreads();
   }
   load_tile<IN, PLAN>(a, s, tile, r0, nrows);
@@ -539,6 +563,33 @@ int set_fock_side(bt::Args& a, float* fock, int64_t ld, const int32_t* row_meta,
   return MALOQ_OK;
 }
 
+// Fock side given as the pair list itself (no row plan): the kernel describes
+// each tile's rows as maloq_basis_row_meta would.
+int set_fock_pairs(bt::Args& a, float* fock, int64_t ld, const int64_t* data_offsets, const int32_t* off,
+                   const int32_t* Z, const int32_t* rows, const int32_t* cols, int64_t num_rows,
+                   const int32_t* pair_kind, const int32_t* raw_slot, int maxe, const uint32_t* kind_blocks) {
+  MALOQ_REQUIRE(num_rows < (int64_t(1) << 31), "bad number of rows");
+  MALOQ_REQUIRE(fock && off && Z && rows && cols && pair_kind && raw_slot, "null pointer");
+  MALOQ_REQUIRE(data_offsets || (ld > 0 && ld < (int64_t(1) << 24)), "dense Fock row stride %lld out of range",
+                static_cast<long long>(ld));
+  MALOQ_REQUIRE(maxe > 0 && maxe <= 65535, "raw_slot row length %d out of range", maxe);
+  MALOQ_REQUIRE(kind_blocks == nullptr || a.nblocks <= bt::kMaxSkipBlocks,
+                "block presence masks cover at most %d CG blocks", bt::kMaxSkipBlocks);
+  a.fock = fock;
+  a.ld = data_offsets ? 0 : ld;
+  a.meta = nullptr;
+  a.data_offsets = data_offsets;
+  a.off = off;
+  a.Z = Z;
+  a.rows = rows;
+  a.cols = cols;
+  a.pair_kind = pair_kind;
+  a.raw_slot = raw_slot;
+  a.maxe = maxe;
+  a.kind_blocks = kind_blocks;
+  return MALOQ_OK;
+}
+
 // Waves of TR-row workgroups that fit on one CU by LDS (tile + Smem), at most
 // 24 (the register budget of the program-only variants).
 int resident_waves(int tr, int tp) {
@@ -549,26 +600,26 @@ int resident_waves(int tr, int tp) {
   return static_cast<int>(wgs * nw);
 }
 
-template <int IN, int OUT, int TR>
+template <int IN, int OUT, int TR, bool PAIRS>
 int launch_tiles(const bt::Args& a, void* stream, const char* name) {
   const int64_t groups = (a.R + TR - 1) / TR;
   const size_t shm = static_cast<size_t>(TR) * a.tp * sizeof(float);
   const dim3 grid(static_cast<unsigned>(groups)), block(bt::waves_of(TR) * 64);
   if (a.w != nullptr)
-    hipLaunchKernelGGL((bt::transform_kernel<IN, OUT, true, TR>), grid, block, shm,
+    hipLaunchKernelGGL((bt::transform_kernel<IN, OUT, true, TR, PAIRS>), grid, block, shm,
                        static_cast<hipStream_t>(stream), a);
   else
-    hipLaunchKernelGGL((bt::transform_kernel<IN, OUT, false, TR>), grid, block, shm,
+    hipLaunchKernelGGL((bt::transform_kernel<IN, OUT, false, TR, PAIRS>), grid, block, shm,
                        static_cast<hipStream_t>(stream), a);
   return check_launch(name);
 }
 
 // 64-row tiles wherever they keep as many waves resident as 32-row tiles.
-template <int IN, int OUT>
+template <int IN, int OUT, bool PAIRS = false>
 int launch_transform(const bt::Args& a, void* stream, const char* name) {
   if (resident_waves(bt::kWideRows, a.tp) >= resident_waves(bt::kNarrowRows, a.tp))
-    return launch_tiles<IN, OUT, bt::kWideRows>(a, stream, name);
-  return launch_tiles<IN, OUT, bt::kNarrowRows>(a, stream, name);
+    return launch_tiles<IN, OUT, bt::kWideRows, PAIRS>(a, stream, name);
+  return launch_tiles<IN, OUT, bt::kNarrowRows, PAIRS>(a, stream, name);
 }
 
 }  // namespace
@@ -644,6 +695,46 @@ extern "C" int maloq_irreps_to_fock(const float* irreps, const int32_t* perm_in,
   a.in = irreps;
   a.perm_in = perm_in;
   return launch_transform<bt::ROWS, bt::FOCK>(a, stream, "irreps -> fock");
+}
+
+extern "C" int maloq_fock_to_irreps_pairs(const float* fock, int64_t ld, const int64_t* data_offsets,
+                                          const int32_t* fock_block_offsets, const int32_t* atomic_numbers,
+                                          const int32_t* rows, const int32_t* cols, int64_t num_rows,
+                                          const int32_t* pair_kind, const int32_t* raw_slot, int maxe,
+                                          const uint32_t* kind_blocks, float* out, const int32_t* perm_out,
+                                          int t, int nblocks, const int32_t* blocks, const float* w,
+                                          const int32_t* sched, void* stream) {
+  MALOQ_REQUIRE(num_rows >= 0, "bad sizes");
+  if (int rc = check_tables(t, nblocks, blocks, w, sched)) return rc;
+  if (num_rows == 0) return MALOQ_OK;
+  MALOQ_REQUIRE(out, "null pointer");
+  bt::Args a = base_args(num_rows, t, nblocks, blocks, w, sched);
+  if (int rc = set_fock_pairs(a, const_cast<float*>(fock), ld, data_offsets, fock_block_offsets, atomic_numbers,
+                              rows, cols, num_rows, pair_kind, raw_slot, maxe, kind_blocks))
+    return rc;
+  a.out = out;
+  a.perm_out = perm_out;
+  return launch_transform<bt::FOCK, bt::ROWS, true>(a, stream, "fock -> irreps (pair list)");
+}
+
+extern "C" int maloq_irreps_to_fock_pairs(const float* irreps, const int32_t* perm_in, float* fock, int64_t ld,
+                                          const int64_t* data_offsets, const int32_t* fock_block_offsets,
+                                          const int32_t* atomic_numbers, const int32_t* rows,
+                                          const int32_t* cols, int64_t num_rows, const int32_t* pair_kind,
+                                          const int32_t* raw_slot, int maxe, const uint32_t* kind_blocks,
+                                          int t, int nblocks, const int32_t* blocks, const float* w,
+                                          const int32_t* sched, void* stream) {
+  MALOQ_REQUIRE(num_rows >= 0, "bad sizes");
+  if (int rc = check_tables(t, nblocks, blocks, w, sched)) return rc;
+  if (num_rows == 0) return MALOQ_OK;
+  MALOQ_REQUIRE(irreps, "null pointer");
+  bt::Args a = base_args(num_rows, t, nblocks, blocks, w, sched);
+  if (int rc = set_fock_pairs(a, fock, ld, data_offsets, fock_block_offsets, atomic_numbers, rows, cols, num_rows,
+                              pair_kind, raw_slot, maxe, kind_blocks))
+    return rc;
+  a.in = irreps;
+  a.perm_in = perm_in;
+  return launch_transform<bt::ROWS, bt::FOCK, true>(a, stream, "irreps -> fock (pair list)");
 }
 
 extern "C" int maloq_basis_cg_block(int program, float* w, int n) {

@@ -277,3 +277,44 @@ def test_row_plan_reuse_and_mismatch(device):
     wide = torch.zeros(H.shape[0], H.shape[1] + 3, device=device)[:, :H.shape[1]]  # other row stride
     with pytest.raises(ValueError):
         hip.fock_to_irreps(wide, off, z, rows, cols, t.orbital_template, plan=plan)
+
+
+def test_pair_list_calls_equal_planned_calls(device):
+    """Without a plan the fused transforms describe their rows from the pair
+    list inside the kernel (maloq_fock_to_irreps_pairs /
+    maloq_irreps_to_fock_pairs): the same bits as with a prebuilt plan, both
+    directions, block-list and dense storage; block offsets given on the host
+    are moved to the device."""
+    from maloq_amd.basis_transform import HipE3TensorDecomp
+    from maloq_amd.synth import sio2_cell, radius_graph, atom_pair_rows
+    t, base, ora = _tables(SIO2)
+    hip = HipE3TensorDecomp(base)
+    Z, pos, L = sio2_cell(n_atoms=150, seed=3, iters=200)
+    src, dst, vec = radius_graph(pos, 5.0, cell=L)
+    rows, cols = atom_pair_rows(src, dst, len(Z))
+    off = np.concatenate([[0], np.cumsum(t.orbitals_per_atom(Z))]).astype(np.int32)
+    bdo = om2l.block_data_offsets(off, rows, cols)
+    data = np.random.default_rng(1).standard_normal(int(bdo[-1])).astype(np.float32)
+    dd = torch.from_numpy(data).to(device)
+    bd = torch.from_numpy(bdo).to(device)
+    plan = hip.make_plan(dd, off, Z, rows, cols, t.orbital_template, block_data_offsets=bd)
+    a = hip.fock_to_irreps(dd, off, Z, rows, cols, t.orbital_template, block_data_offsets=bd, plan=plan)
+    for offsets in (bd, bdo, torch.from_numpy(bdo)):  # device tensor, numpy, host tensor
+        b = hip.fock_to_irreps(dd, off, Z, rows, cols, t.orbital_template, block_data_offsets=offsets)
+        assert torch.equal(a, b)
+    back_a, back_b = torch.zeros_like(dd), torch.zeros_like(dd)
+    hip.irreps_to_fock(a, back_a, off, Z, rows, cols, t.orbital_template, block_data_offsets=bd, plan=plan)
+    hip.irreps_to_fock(a, back_b, off, Z, rows, cols, t.orbital_template, block_data_offsets=bdo)
+    assert torch.equal(back_a, back_b)
+    assert np.abs(back_b.cpu().numpy() - data).max() / np.abs(data).max() < 1e-6
+    # dense storage, the inverse direction (the forward is compared in the test above)
+    t3, base3, _ = _tables(CFG3)
+    hip3 = HipE3TensorDecomp(base3)
+    z, H, off3, r3, c3 = _molecules(1, t3, seed0=41)[0]
+    Hd = torch.from_numpy(H).to(device)
+    plan3 = hip3.make_plan(Hd, off3, z, r3, c3, t3.orbital_template)
+    irr = hip3.fock_to_irreps(Hd, off3, z, r3, c3, t3.orbital_template)
+    H_a, H_b = torch.zeros_like(Hd), torch.zeros_like(Hd)
+    hip3.irreps_to_fock(irr, H_a, off3, z, r3, c3, t3.orbital_template, plan=plan3)
+    hip3.irreps_to_fock(irr, H_b, off3, z, r3, c3, t3.orbital_template)
+    assert torch.equal(H_a, H_b)
