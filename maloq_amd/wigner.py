@@ -22,6 +22,7 @@ from . import _lib
 from .so3 import jd_matrices, pack_jd
 
 _JD_CACHE: dict = {}
+_JD_IDENT: dict = {}  # (tensor ids, versions) -> (packed tables, the tensors)
 
 
 def _packed_jd(Jd, lmax: int, device) -> torch.Tensor:
@@ -33,9 +34,19 @@ def _packed_jd(Jd, lmax: int, device) -> torch.Tensor:
         return _JD_CACHE[key]
     if len(Jd) <= lmax:
         raise ValueError(f"Jd has {len(Jd)} entries, need {lmax + 1}")
+    js = list(Jd[: lmax + 1])
+    # fast path, no host copy (for device-resident J_l that would be a sync per
+    # call): the same tensor objects, unmodified.  The entry holds the tensors
+    # themselves, so their ids cannot be reused by other objects meanwhile.
+    ident = None
+    if all(torch.is_tensor(j) for j in js):
+        ident = ("ident", lmax, str(device), tuple((id(j), j._version) for j in js))
+        hit = _JD_IDENT.get(ident)
+        if hit is not None:
+            return hit[0]
     # keyed by content: the J_l are tiny, and a content key cannot be fooled by
     # a freed list whose storage is reused at the same addresses
-    mats = [np.asarray(j.detach().cpu().double() if torch.is_tensor(j) else j, dtype=np.float64) for j in Jd[: lmax + 1]]
+    mats = [np.asarray(j.detach().cpu().double() if torch.is_tensor(j) else j, dtype=np.float64) for j in js]
     key = ("list", lmax, str(device), b"".join(np.ascontiguousarray(m).tobytes() for m in mats))
     hit = _JD_CACHE.get(key)
     if hit is None:
@@ -43,6 +54,10 @@ def _packed_jd(Jd, lmax: int, device) -> torch.Tensor:
         if len(_JD_CACHE) > 64:
             _JD_CACHE.clear()
         _JD_CACHE[key] = hit
+    if ident is not None:
+        if len(_JD_IDENT) > 64:
+            _JD_IDENT.clear()
+        _JD_IDENT[ident] = (hit, js)
     return hit
 
 
