@@ -49,6 +49,27 @@ def test_rotate_matches_oracle(lmax, dtype, device):
         assert err < tol, f"inverse={inv} err {err}"
 
 
+@pytest.mark.parametrize("lmax", [2, 4])
+@pytest.mark.parametrize("C", [4, 1024])
+def test_rotate_channel_widths(lmax, C, device):
+    """Edges per workgroup follow the width: min(256 / d, 256 / (C / 4)), so
+    C = 4 packs 256 / d edges and C = 1024 one edge per workgroup."""
+    from maloq_amd.rotate import rotate
+    from maloq_amd.wigner import extract_euler_angles
+    print(f"rotate widths lmax={lmax} C={C}", flush=True)
+    gen = torch.Generator().manual_seed(C + lmax)
+    d, N, E = (lmax + 1) ** 2, 11, 97
+    x = torch.randn(N, d, C, generator=gen, dtype=torch.float64)
+    src = torch.randint(0, N, (E,), generator=gen)
+    eul = extract_euler_angles(torch.randn(E, 3, generator=gen).to(device), seed=C)
+    Dm = _ref_blocks(eul, lmax)
+    xd, sd = x.to(device=device, dtype=torch.float32), src.to(device)
+    for inv in (False, True):
+        ref = torch.bmm(Dm.transpose(1, 2) if inv else Dm, x.float().double()[src])
+        got = rotate(xd, lmax, eulers=eul, gather=sd, inverse=inv, out_dtype=torch.float32).cpu().double()
+        assert (got - ref).abs().max().item() / ref.abs().max().item() < 1e-5, inv
+
+
 @pytest.mark.parametrize("lmax", [2, 4, 6])
 def test_rotate_dense_wigner_equals_euler_path(lmax, device):
     """The dense-wigner input (the reference's argument) gives bit-identical rows
