@@ -48,10 +48,20 @@ def make_radial(n_rbf, hidden, out, device):
     return RadialMLP([n_rbf, hidden, hidden, out]).to(device)
 
 
+_RBF: dict = {}
+
+
 def gaussian_rbf(dist, start, stop, num):
+    """Gaussian smearing of the edge lengths.  The offsets and the coefficient
+    are made once per (start, stop, num, device), as a smearing module makes
+    them at construction: reading the coefficient back from the device on every
+    step would stall the step on the GPU."""
     import torch
-    offset = torch.linspace(start, stop, num, device=dist.device)
-    coeff = -0.5 / (offset[1] - offset[0]).item() ** 2
+    key = (start, stop, num, str(dist.device))
+    if key not in _RBF:
+        off = torch.linspace(start, stop, num)  # host tensor: no device read
+        _RBF[key] = (off.to(dist.device), -0.5 / (off[1] - off[0]).item() ** 2)
+    offset, coeff = _RBF[key]
     return torch.exp(coeff * (dist.view(-1, 1) - offset.view(1, -1)) ** 2)
 
 
