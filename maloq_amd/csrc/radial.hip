@@ -996,13 +996,16 @@ __global__ __launch_bounds__(NT) void radial_dwo_f32_kernel(Args a) {
   const float* G = reinterpret_cast<const float*>(a.grad);
   const float* U = reinterpret_cast<const float*>(a.save);
   constexpr int nnt = NNT;
-  f32x16 acc[NNT], accb;
+  f32x16 acc[NNT];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    accb[r] = 0.f;
+  for (int r = 0; r < 16; ++r)
 #pragma unroll
     for (int nt = 0; nt < NNT; ++nt) acc[nt][r] = 0.f;
-  }
+  // db_o on the VALU: this lane's running sum of G[e][o] over its half of the
+  // edges (even edges for lanes 0-31, odd for 32-63), the halves added at the
+  // end.  (An MFMA against a ones column would spend a third of the kernel's
+  // MFMA issue on a column sum.)
+  float colsum = 0.f;
   const int h = lane >> 5;
   // DO_KB two-edge MFMA steps per batch; the loads of the next batch are in
   // flight while the MFMAs of this one run (two register buffers)
@@ -1021,7 +1024,7 @@ __global__ __launch_bounds__(NT) void radial_dwo_f32_kernel(Args a) {
   auto step = [&](int buf) {
 #pragma unroll
     for (int k = 0; k < DO_KB; ++k) {
-      accb = __builtin_amdgcn_mfma_f32_32x32x2f32(av[buf][k], 1.0f, accb, 0, 0, 0);
+      colsum += av[buf][k];
 #pragma unroll
       for (int nt = 0; nt < NNT; ++nt)
         if (nt < nnt) acc[nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[buf][k], bv[buf][k][nt], acc[nt], 0, 0, 0);
@@ -1046,8 +1049,10 @@ __global__ __launch_bounds__(NT) void radial_dwo_f32_kernel(Args a) {
 #pragma unroll
     for (int nt = 0; nt < NNT; ++nt)
       if (nt < nnt) part[static_cast<int64_t>(oo) * cH + 32 * nt + (lane & 31)] = acc[nt][r];
-    if ((lane & 31) == 0) part[static_cast<int64_t>(cout) * cH + oo] = accb[r];
   }
+  // lanes L and L + 32 hold the two halves of output ob + L % 32
+  const float other = __shfl_xor(colsum, 32);
+  if (h == 0) part[static_cast<int64_t>(cout) * cH + o] = colsum + other;
 }
 
 // Fixed-order sums of nparts partial vectors (stride floats apart).  First
