@@ -34,6 +34,28 @@ def _i32(a, device):
     return torch.as_tensor(np.ascontiguousarray(np.asarray(a, dtype=np.int32)), device=device)
 
 
+def _check_pairs_on_host(off, Z, rows, cols):
+    """Range checks of the atom-pair structure where it is still on the host
+    (numpy or CPU tensors, as the per-molecule callers hold it): the kernels
+    index with these values unchecked.  Device tensors are the caller's
+    responsibility (checking them would read them back, a sync per call)."""
+    arrs = (off, Z, rows, cols)
+    if any(torch.is_tensor(a) and a.is_cuda for a in arrs):
+        return
+    off, Z, rows, cols = (np.asarray(a.numpy() if torch.is_tensor(a) else a).reshape(-1) for a in arrs)
+    natoms = off.shape[0] - 1
+    if natoms < 0 or Z.shape[0] < natoms:
+        raise ValueError("fock_block_offsets must have one entry per atom plus one, and atomic_numbers one per atom")
+    if natoms > 0 and (np.any(np.diff(off) < 0) or off[0] < 0):
+        raise ValueError("fock_block_offsets must be non-decreasing from >= 0")
+    if rows.shape != cols.shape:
+        raise ValueError("rows and cols must have the same length")
+    if rows.size and (min(rows.min(), cols.min()) < 0 or max(rows.max(), cols.max()) >= natoms):
+        raise IndexError("atom-pair index outside 0..num_atoms-1")
+    if natoms and (Z[:natoms].min() < 0 or Z[:natoms].max() >= MAX_ELEMENTS):
+        raise ValueError(f"atomic numbers must lie in 0..{MAX_ELEMENTS - 1}")
+
+
 # (2 l1 + 1)(2 l2 + 1) for l1, l2 <= 3: the block sizes the kernel is built for
 _SUPPORTED_N = frozenset((2 * a + 1) * (2 * b + 1) for a in range(4) for b in range(4))
 _WAVES = 4  # block lists of the transform kernel's schedule
@@ -285,6 +307,7 @@ class HipE3TensorDecomp:
         """BasisPlan for the atom pairs (rows[r], cols[r]) of ``fock`` (dense, or
         the block list of ``block_data_offsets``)."""
         _lib.require_cuda(fock)
+        _check_pairs_on_host(fock_block_offsets, atomic_numbers, rows, cols)
         dev = fock.device
         tabs = self._template_tables(orbital_template)
         off, Z, r_, c_ = (_i32(x, dev) for x in (fock_block_offsets, atomic_numbers, rows, cols))
@@ -312,6 +335,7 @@ class HipE3TensorDecomp:
         """Device arguments of the plan-less entry points (the pair list itself)."""
         if fock.dtype != torch.float32:
             raise ValueError("Unsupported dtype for the Fock matrix; only float32 is supported.")
+        _check_pairs_on_host(fock_block_offsets, atomic_numbers, rows, cols)
         dev = fock.device
         off, Z, r_, c_ = (_i32(x, dev) for x in (fock_block_offsets, atomic_numbers, rows, cols))
         if r_.shape != c_.shape:

@@ -368,10 +368,11 @@ __device__ __forceinline__ void hidden_layer(int c, const float* prm, int cin, c
 // MAXT tiles as they are used).  Equal shares of units rather than whole
 // tiles: 575 tiles on 256 CUs would give some CUs three tiles against an
 // average of 2.25.  Only the workgroup holding a tile's first group saves
-// u_H.  The output loop has no loads, so its stores are never waited on.  Results go through a per-wave LDS block of 64 edges x 128 bytes
-// of outputs and leave as whole 128-byte row segments (16 bytes per lane,
-// eight lanes per row): stores in the accumulator's lane order (16 bytes per
-// row per instruction) reach less than half the HBM write rate.
+// u_H.  The output loop has no loads, so its stores are never waited on.
+// Results go through a per-wave LDS block of 64 edges x 128 bytes of outputs
+// and leave as whole 128-byte row segments (16 bytes per lane, eight lanes per
+// row): stores in the accumulator's lane order (16 bytes per row per
+// instruction) reach less than half the HBM write rate.
 constexpr int FW_W = 8;
 constexpr int FW_SP = 128 + 16;  // bytes per staged row (the pad spreads rows over the banks)
 template <class TM, int NNT>

@@ -144,3 +144,27 @@ def test_unsupported_block_size_rejected():
     t, base, ora = _setup({1: [0, 4]})   # a g shell: 9 x 9 = 81 > 49
     with pytest.raises(ValueError):
         cg_block_tables(base)
+
+
+def test_pair_structure_checked_on_host():
+    """Index arrays given on the host are range-checked before any launch (the
+    kernels index with them unchecked)."""
+    import numpy as np
+    import pytest
+    import torch
+    from maloq_amd.basis_transform import _check_pairs_on_host
+    off = np.array([0, 5, 19, 33], np.int32)
+    Z = np.array([1, 6, 8], np.int32)
+    rows, cols = np.array([0, 1, 2, 2]), np.array([0, 2, 1, 2])
+    _check_pairs_on_host(off, Z, rows, cols)
+    _check_pairs_on_host(torch.from_numpy(off), torch.from_numpy(Z), torch.from_numpy(rows), torch.from_numpy(cols))
+    with pytest.raises(IndexError):
+        _check_pairs_on_host(off, Z, rows, np.array([0, 3, 1, 2]))
+    with pytest.raises(IndexError):
+        _check_pairs_on_host(off, Z, np.array([-1, 1, 2, 2]), cols)
+    with pytest.raises(ValueError):
+        _check_pairs_on_host(off, np.array([1, 6, 100], np.int32), rows, cols)
+    with pytest.raises(ValueError):
+        _check_pairs_on_host(np.array([0, 5, 4, 33], np.int32), Z, rows, cols)
+    with pytest.raises(ValueError):
+        _check_pairs_on_host(off, Z, rows, cols[:3])
