@@ -16,6 +16,7 @@ import numpy as np
 import torch
 
 from . import _lib
+from .basis_transform import _check_pairs_on_host
 from .tensor_decomp import MAX_ELEMENTS
 
 
@@ -68,6 +69,7 @@ def hip_single_matrix2label(orbital_templates, fock_block_offsets, idx_to_atomic
     _lib.require_cuda(fock_matrix, target)
     if fock_matrix.dim() != 2 or fock_matrix.stride(1) != 1 or target.stride(1) != 1:
         raise ValueError("fock_matrix and target must be 2-D with unit column stride")
+    _check_pairs_on_host(fock_block_offsets, idx_to_atomic_number, fock_block_rows, fock_block_cols)
     dev = target.device
     tptr, tent = pack_orbital_template(orbital_templates, dev)
     rows = _dev_i32(fock_block_rows, dev)
@@ -97,6 +99,7 @@ def hip_single_matrix2label_sparse(orbital_templates, fock_block_offsets, idx_to
     if target.dtype != torch.float32:
         raise AssertionError("sparse kernel only implements fp32")
     _lib.require_cuda(target)
+    _check_pairs_on_host(fock_block_offsets, idx_to_atomic_number, fock_block_rows, fock_block_cols)
     dev = target.device
     rows = _dev_i32(fock_block_rows, dev)
     cols = _dev_i32(fock_block_cols, dev)
