@@ -175,11 +175,20 @@ def gated_flops_extra(L, c_in, c_out):
 
 # ---------------------------------------------------------- basis transform
 CFG3_BASIS = {1: [0, 0, 1], 6: [0, 0, 0, 1, 1, 2], 7: [0, 0, 0, 1, 1, 2], 8: [0, 0, 0, 1, 1, 2]}
+# def2-TZVPD shells (src/maloq/fock_utils/basis_sets.py:28) of H/C/N/O, plus Ga
+# (4 d shells) and I (2 f shells): the template then has the 64 orbitals of the
+# whole dictionary, 4096 label columns, as the OMol loader builds it from every
+# element (dataset_utils/get_loader.py:106-107); the molecules are H/C/N/O.
+TZVPD_BASIS = {1: [0, 0, 0, 1, 1], 6: [0, 0, 0, 0, 0, 1, 1, 1, 2, 2, 3, 0, 2],
+               7: [0, 0, 0, 0, 0, 1, 1, 1, 2, 2, 3, 0, 2], 8: [0, 0, 0, 0, 0, 1, 1, 1, 2, 2, 3, 0, 1, 2],
+               31: [0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 2, 2, 2, 2, 3, 0, 2],
+               53: [0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 2, 2, 2, 3, 3, 0, 1, 2]}
 
 
-def basis_workload():
+def basis_workload(basis=None):
     """Config 3 as one block list (all on-site + off-site < 8 A blocks of 64
-    molecules), so the whole batch is one launch."""
+    molecules), so the whole batch is one launch; ``basis`` (default: config 3's
+    def2-SVP-like one) gives the orbitals and the label template."""
     import numpy as np
     import torch
     from maloq_amd import synth
@@ -187,7 +196,7 @@ def basis_workload():
     from maloq_amd.basis_transform import HipE3TensorDecomp
 
     dev = torch.device("cuda:0")
-    t = ptd.BasisTables(CFG3_BASIS)
+    t = ptd.BasisTables(basis or CFG3_BASIS)
     base = ptd.e3TensorDecomp(t.req_output_irreps, t.out_js_list, torch.float32, device_torch=dev)
     hip = HipE3TensorDecomp(base)
     Zs, offs, rows, cols, data = [], [0], [], [], []
@@ -246,6 +255,31 @@ def basis_timing(bw, reps=50):
     inv_pl = kernel_time_events(lambda: hip.irreps_to_fock(out, back, *dev_args, t.orbital_template,
                                                            block_data_offsets=bw["bdo"]), reps)
     return fwd, inv, rt, plan_s, fwd_pl, inv_pl
+
+
+def wide_basis_leg(reps=20, cpu=True):
+    """Config 3's molecules under the def2-TZVPD template (4096-column label
+    rows, several column groups per row tile): H-blocks/s both directions, with
+    a prebuilt plan and from the pair list, HBM roofline of the forward."""
+    import torch
+    bw = basis_workload(TZVPD_BASIS)
+    tf, ti, rt, tplan, tfp, tip = basis_timing(bw, reps)
+    nb = bw["n_blocks"]
+    bpb = (bw["block_bytes"] + 4 * bw["T"] * nb) / nb
+    out = {"metric": "H-blocks/s", "fwd": nb / tf, "inv": nb / ti, "fwd_with_plan": nb / (tf + tplan),
+           "inv_with_plan": nb / (ti + tplan), "fwd_pair_list": nb / tfp, "inv_pair_list": nb / tip,
+           "blocks": nb, "T": int(bw["T"]), "column_groups": bw["hip"].ngroups, "round_trip_rel_err": rt,
+           "plan_ms": tplan * 1e3, "config": "config 3 molecules (64 x 30-50 atoms, H/C/N/O), def2-TZVPD "
+                                             "template (4096 columns), block list",
+           "roofline": {"kernel": "transform_kernel<FOCK,ROWS> (block list, column groups)", "bound": "hbm",
+                        "achieved": bpb * nb / tf / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                        "frac": bpb * nb / tf / PEAK_HBM, "bytes_per_block": bpb,
+                        "traffic": load_traffic("fock_to_irreps_tzvpd")}}
+    if cpu:
+        out["cpu_baseline"] = cpu_basis_baseline(bw, budget_s=10.0)
+    del bw
+    torch.cuda.empty_cache()
+    return out
 
 
 # ---------------------------------------------------------------- CPU legs
@@ -329,7 +363,7 @@ def cpu_basis_baseline(bw, budget_s=8.0):
         src, dst, _ = synth.radius_graph(p, 8.0)
         r, c = synth.atom_pair_rows(src, dst, len(z))
         t0 = time.perf_counter()
-        lab = np.zeros((len(r), 196), np.float32)
+        lab = np.zeros((len(r), int(bw["T"])), np.float32)
         om2l.single_matrix2label(t.orbital_template, off, z, r, c, H, lab, True)
         o.get_net_out(torch.from_numpy(lab))
         total_t += time.perf_counter() - t0
@@ -337,7 +371,8 @@ def cpu_basis_baseline(bw, budget_s=8.0):
         if total_t > budget_s:
             break
     return {"value": total_blocks / total_t, "unit": "H-blocks/s", "cores": cores, "kind": "port",
-            "sample": f"config 3, {m + 1} molecule(s) ({total_blocks} blocks), numpy gather + fp32 matmul"}
+            "sample": f"config 3 molecules, {m + 1} molecule(s) ({total_blocks} blocks), T = {int(bw['T'])}, "
+                      f"numpy gather + fp32 matmul"}
 
 
 # ------------------------------------------------------- config 1: rotation
@@ -850,6 +885,8 @@ def profile_only(args):
     elif args.only == "basis5":
         sw = sparse_basis_workload()
         sparse_basis_leg(sw, reps=args.reps)
+    elif args.only == "basis-tzvpd":
+        print(json.dumps(wide_basis_leg(reps=args.reps, cpu=False)), flush=True)
     elif args.only in ("fwd", "step"):
         w = message_workload(args.dtype, cfg=args.cfg)
         if args.only == "fwd":
@@ -883,7 +920,7 @@ def main(argv=None):
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-extras", action="store_true", help="headline only")
     ap.add_argument("--only", choices=["fwd", "step", "basis", "copy", "embed", "edgewise", "edgewise-step",
-                                       "rotate", "basis5", "ceiling"],
+                                       "rotate", "basis5", "basis-tzvpd", "ceiling"],
                     help="profiling mode: run one piece a few times and exit (no JSON line)")
     ap.add_argument("--cfg", default="config2", choices=sorted(MESSAGE_CONFIGS),
                     help="message-block configuration of --only fwd / step")
@@ -968,6 +1005,8 @@ def main(argv=None):
         if not args.no_cpu:
             result["config5_basis_transform"]["cpu_baseline"] = cpu_sparse_basis_baseline(sw)
         del sw
+        print("[bench] basis transform (config 3 molecules, def2-TZVPD template) ...", file=sys.stderr, flush=True)
+        result["def2_tzvpd_basis_transform"] = wide_basis_leg(cpu=not args.no_cpu)
         print("[bench] edge-degree embedding (config 2) ...", file=sys.stderr, flush=True)
         ew = embed_workload()
         s = torch.cuda.current_stream()

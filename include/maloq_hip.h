@@ -17,7 +17,7 @@
 
 #include <stdint.h>
 
-#define MALOQ_ABI_VERSION 2
+#define MALOQ_ABI_VERSION 3
 
 #ifdef __cplusplus
 extern "C" {
@@ -82,11 +82,21 @@ int maloq_rotate(int x_dtype, int out_dtype, int lmax, const void* x, int c, con
  *     direction has its own blocks table;
  *   w      the block matrices; NULL is allowed when every block of the table
  *     has a program (the kernels then carry no dense path at all);
- *   sched  [5 + nblocks]: sched[0..4] are offsets into sched + 5 of the block ids
- *     of 4 lists (sched[4] = nblocks); each wave of a workgroup contracts one
- *     list (4 waves) or every other block of one (8 waves);
- *   t      row width, at most 1271 (one 32-row tile of fp32 in LDS).
- * Sorted irreps rows use perm (sorted column j <-> unsorted column perm[j]). */
+ *   sched  column groups and per-wave block lists.  The unsorted row is split
+ *     into ngroups groups of consecutive CG blocks (at most 64 blocks and
+ *     group_cols columns each; one group of t columns when the row fits one
+ *     LDS tile).  sched[0] = ngroups; sched[1 + 4g .. 4 + 4g] = (first column,
+ *     width, first block, offset o_g) of group g; sched[o_g .. o_g + 4] are
+ *     offsets into sched + o_g + 5 of the (global) block ids of the group's 4
+ *     lists; each wave of a workgroup contracts one list (4 waves) or every
+ *     other block of one (8 waves);
+ *   t      row width (any; the widest group, group_cols, must fit a 32-row
+ *     fp32 LDS tile: group_cols <= 1269);
+ *   ngroups, group_cols  as in sched; the grid is (row tiles) x (groups).
+ * Sorted irreps rows use perm (sorted column j <-> unsorted column perm[j]),
+ * only with ngroups = 1 (rows of several groups are permuted by a separate
+ * maloq_gather_columns).  Replaces the label-width-agnostic grid of the
+ * reference's Triton backend, basis_transform_triton_backend.py:1255-1438. */
 
 /* Label/irreps rows -> rows, [R, t] -> [R, t]:
  *   out[r, j] = Y[r, perm_out ? perm_out[j] : j],  Y = blockdiag(W) X,
@@ -99,17 +109,18 @@ int maloq_rotate(int x_dtype, int out_dtype, int lmax, const void* x, int c, con
 int maloq_label_transform(const float* in, const int32_t* perm_in, float* out,
                           const int32_t* perm_out, int64_t num_rows, int t, int nblocks,
                           const int32_t* blocks, const float* w, const int32_t* sched,
-                          void* stream);
+                          int ngroups, int group_cols, void* stream);
 
 /* Row plan of the Fock-side transforms, int4 per atom pair r (i = rows[r],
  * j = cols[r]): (base lo, base hi, r, (kind + 1) | n_i << 16 | n_j << 24), where
- *   dense  (data_offsets == NULL): the block starts at fock[off[i]*ld + off[j]], row stride ld;
+ *   dense  (data_offsets == NULL): the block starts at fock[off[i]*ld + off[j]], row stride
+ *          ld < 2^23;
  *   sparse (data_offsets != NULL): block r at fock[data_offsets[r]], n_j = off[j+1]-off[j]
  *          columns, row-major (SparseBlockMatrix, matrix2labels_kernels.py:43-48);
  * kind = pair_kind[Z_i*100 + Z_j] (-1: no template, the row is all zero), n_i, n_j <= 255,
- * n_i * n_j <= maxe.  row_meta: [num_rows, 4] int32, 16-byte aligned.  The transforms
- * below take the plan in any row order; entry p of the plan reads and writes
- * row r = plan[p].z.  Replaces the per-call index lists of
+ * n_i * n_j <= maxe (the template's largest block).  row_meta: [num_rows, 4] int32,
+ * 16-byte aligned.  The transforms below take the plan in any row order; entry p of
+ * the plan reads and writes row r = plan[p].z.  Replaces the per-call index lists of
  * cupy_single_matrix2label (matrix2labels_kernels.py:978-994). */
 int maloq_basis_row_meta(int64_t ld, const int64_t* data_offsets,
                          const int32_t* fock_block_offsets, const int32_t* atomic_numbers,
@@ -119,18 +130,25 @@ int maloq_basis_row_meta(int64_t ld, const int64_t* data_offsets,
 /* Fused Fock -> irreps over a row plan: gather every atom-pair block into its
  * label row, then get_net_out; out [R, t] in original row order.
  * ld: the dense row stride, 0 for block-list storage (as in the plan).
- * raw_slot [kinds, maxe]: element q = a*n_j + b of a block of that kind goes to label
- * column raw_slot[kind*maxe + q], or nowhere if -1; label columns no element reaches
- * are zero.  kind_blocks [kinds, 2] (or NULL): bit b set if the kind has CG block b
- * (nblocks <= 64); blocks that no row of a 32-row tile has are skipped.
+ * slots: the template's elements per (column group, element-pair kind), as a
+ *   rectangle of the atom-pair block: slots[0] = kinds K, slots[1] = ngroups,
+ *   slots[2 + g] = the largest rectangle (nr * nc) of group g,
+ *   slots[2 + ngroups + g*K + k] = r0 | nr << 8 | c0 << 16 | nc << 24 (block rows
+ *   r0 .. r0+nr-1, columns c0 .. c0+nc-1; nr = 0 for none; a rectangle outside a
+ *   row's actual block is skipped), slots[2 + ngroups + ngroups*K + g*K + k] = the
+ *   offset in slots of its column table: nr*nc entries, row-major, each the
+ *   column of group g (label column = the group's first column + it) that the
+ *   element goes to, or -1.  Label columns no element reaches are zero.
+ * kind_blocks [ngroups*K, 2] (or NULL): bit i set if the kind has the group's
+ * i-th CG block; blocks that no row of a tile has are skipped.
  * Replaces cupy_single_matrix2label(forward=True) + get_net_out,
  * fock_utils/matrix2labels_kernels.py:946-1036 (K12) / :1038-1115 (K13) and
  * fock_targets_batched.py:426-441. */
 int maloq_fock_to_irreps(const float* fock, int64_t ld, const int32_t* row_meta,
-                         int64_t num_rows, const int32_t* raw_slot, int maxe,
+                         int64_t num_rows, const int32_t* slots, int maxe,
                          const uint32_t* kind_blocks, float* out, const int32_t* perm_out,
                          int t, int nblocks, const int32_t* blocks, const float* w,
-                         const int32_t* sched, void* stream);
+                         const int32_t* sched, int ngroups, int group_cols, void* stream);
 
 /* Fused irreps -> Fock over a row plan: get_H per row, then scatter the label
  * columns that the row's element pair has into its atom-pair block (tables as
@@ -139,10 +157,10 @@ int maloq_fock_to_irreps(const float* fock, int64_t ld, const int32_t* row_meta,
  * Replaces get_H + cupy_single_matrix2label(forward=False),
  * train_utils/splittrainer.py:546-597 over matrix2labels_kernels.py:946-1036. */
 int maloq_irreps_to_fock(const float* irreps, const int32_t* perm_in, float* fock, int64_t ld,
-                         const int32_t* row_meta, int64_t num_rows, const int32_t* raw_slot,
+                         const int32_t* row_meta, int64_t num_rows, const int32_t* slots,
                          int maxe, const uint32_t* kind_blocks, int t, int nblocks,
                          const int32_t* blocks, const float* w, const int32_t* sched,
-                         void* stream);
+                         int ngroups, int group_cols, void* stream);
 
 /* The two fused transforms above for a one-off pair list, without a row plan:
  * each workgroup describes its own rows exactly as maloq_basis_row_meta would
@@ -156,17 +174,17 @@ int maloq_irreps_to_fock(const float* irreps, const int32_t* perm_in, float* foc
 int maloq_fock_to_irreps_pairs(const float* fock, int64_t ld, const int64_t* data_offsets,
                                const int32_t* fock_block_offsets, const int32_t* atomic_numbers,
                                const int32_t* rows, const int32_t* cols, int64_t num_rows,
-                               const int32_t* pair_kind, const int32_t* raw_slot, int maxe,
+                               const int32_t* pair_kind, const int32_t* slots, int maxe,
                                const uint32_t* kind_blocks, float* out, const int32_t* perm_out,
                                int t, int nblocks, const int32_t* blocks, const float* w,
-                               const int32_t* sched, void* stream);
+                               const int32_t* sched, int ngroups, int group_cols, void* stream);
 int maloq_irreps_to_fock_pairs(const float* irreps, const int32_t* perm_in, float* fock, int64_t ld,
                                const int64_t* data_offsets, const int32_t* fock_block_offsets,
                                const int32_t* atomic_numbers, const int32_t* rows, const int32_t* cols,
-                               int64_t num_rows, const int32_t* pair_kind, const int32_t* raw_slot,
+                               int64_t num_rows, const int32_t* pair_kind, const int32_t* slots,
                                int maxe, const uint32_t* kind_blocks, int t, int nblocks,
                                const int32_t* blocks, const float* w, const int32_t* sched,
-                               void* stream);
+                               int ngroups, int group_cols, void* stream);
 
 /* The dense n x n matrix (row-major, output column x input column) of compiled
  * CG program p = dir * 16 + l1 * 4 + l2 (dir 0: get_net_out, the

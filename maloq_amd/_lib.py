@@ -28,19 +28,19 @@ SIGNATURES = {
     "maloq_edge_vec_to_wigner": [_p, _i64, _u64, _i32, _p, _p, _p, _p, _i32, _p],
     "maloq_wigner_from_euler": [_p, _i64, _i32, _p, _p, _p, _i32, _p],
     "maloq_rotate": [_i32, _i32, _i32, _p, _i32, _p, _i64, _p, _p, _p, _i32, _p, _p],
-    "maloq_label_transform": [_p, _p, _p, _p, _i64, _i32, _i32, _p, _p, _p, _p],
+    "maloq_label_transform": [_p, _p, _p, _p, _i64, _i32, _i32, _p, _p, _p, _i32, _i32, _p],
     "maloq_basis_cg_block": [_i32, _p, _i32],
     "maloq_irreps_gate_fwd": [_p, _i64, _i32, _i32, _p, ctypes.c_float, _i32, _p, _p],
     "maloq_irreps_gate_bwd": [_p, _i64, _i32, _i32, _p, ctypes.c_float, _i32, _p, _p, _p, _p],
     "maloq_gather_columns": [_p, _i64, _i64, _p, _p, _i32, _p, _i64, _p],
     "maloq_scatter_columns": [_p, _i64, _i64, _p, _p, _p, _i32, _p, _i64, _p],
     "maloq_basis_row_meta": [_i64, _p, _p, _p, _p, _p, _i64, _p, _i32, _p, _p],
-    "maloq_fock_to_irreps": [_p, _i64, _p, _i64, _p, _i32, _p, _p, _p, _i32, _i32, _p, _p, _p, _p],
-    "maloq_irreps_to_fock": [_p, _p, _p, _i64, _p, _i64, _p, _i32, _p, _i32, _i32, _p, _p, _p, _p],
+    "maloq_fock_to_irreps": [_p, _i64, _p, _i64, _p, _i32, _p, _p, _p, _i32, _i32, _p, _p, _p, _i32, _i32, _p],
+    "maloq_irreps_to_fock": [_p, _p, _p, _i64, _p, _i64, _p, _i32, _p, _i32, _i32, _p, _p, _p, _i32, _i32, _p],
     "maloq_fock_to_irreps_pairs": [_p, _i64, _p, _p, _p, _p, _p, _i64, _p, _p, _i32, _p, _p, _p, _i32, _i32, _p,
-                                   _p, _p, _p],
+                                   _p, _p, _i32, _i32, _p],
     "maloq_irreps_to_fock_pairs": [_p, _p, _p, _i64, _p, _p, _p, _p, _p, _i64, _p, _p, _i32, _p, _i32, _i32, _p,
-                                   _p, _p, _p],
+                                   _p, _p, _i32, _i32, _p],
     "maloq_matrix2label": [_p, _i64, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _i64, _i32, _p],
     "maloq_segment_sum": [_p, _p, _p, _i64, _i64, _p, _p],
     "maloq_label_scalar_shift": [_p, _i64, _i64, _p, _p, _p, _i32, ctypes.c_float, _p],

@@ -104,26 +104,50 @@ def _(msg, perm, seg_ptr, num_segments):
 # --------------------------------------------------------- basis transform
 @custom_op("maloq_hip::label_transform", mutates_args=())
 def label_transform(x: Tensor, blocks: Tensor, w: Optional[Tensor], sched: Tensor, perm_in: Optional[Tensor],
-                    perm_out: Optional[Tensor], num_blocks: int) -> Tensor:
+                    perm_out: Optional[Tensor], num_blocks: int, ngroups: int, group_cols: int,
+                    perm_inv: Optional[Tensor]) -> Tensor:
+    """Rows of several column groups (``ngroups`` > 1) are permuted by a
+    separate column gather: the input through ``perm_inv`` (the inverse of
+    ``perm_in``), the output through ``perm_out``."""
     _lib.require_cuda(x)
     xc = x.contiguous()
+    pre = ngroups > 1 and perm_in is not None
+    post = ngroups > 1 and perm_out is not None
+    if pre or post:
+        ones = torch.ones(xc.shape[1], device=xc.device, dtype=torch.float32)
+
+    def gather(y, src):
+        o = torch.empty_like(y)
+        _lib.call("maloq_gather_columns", _lib.ptr(y), y.shape[1], y.shape[0], _lib.ptr(src), _lib.ptr(ones),
+                  y.shape[1], _lib.ptr(o), o.shape[1], _lib.stream_of(y.device))
+        return o
+
+    if pre:
+        if perm_inv is None:
+            raise ValueError("rows of several column groups need the inverse input permutation")
+        xc = gather(xc, perm_inv)
     out = torch.empty_like(xc)
-    _lib.call("maloq_label_transform", _lib.ptr(xc), _lib.ptr(perm_in), _lib.ptr(out), _lib.ptr(perm_out),
-              xc.shape[0], xc.shape[1], num_blocks, _lib.ptr(blocks), _lib.ptr(w), _lib.ptr(sched),
-              _lib.stream_of(x.device))
-    return out
+    _lib.call("maloq_label_transform", _lib.ptr(xc), _lib.ptr(None if pre else perm_in), _lib.ptr(out),
+              _lib.ptr(None if post else perm_out), xc.shape[0], xc.shape[1], num_blocks, _lib.ptr(blocks),
+              _lib.ptr(w), _lib.ptr(sched), ngroups, group_cols, _lib.stream_of(x.device))
+    return gather(out, perm_out) if post else out
 
 
 @register_fake("maloq_hip::label_transform")
-def _(x, blocks, w, sched, perm_in, perm_out, num_blocks):
+def _(x, blocks, w, sched, perm_in, perm_out, num_blocks, ngroups, group_cols, perm_inv):
     return torch.empty_like(x)
+
+
+def _layout(d):
+    return d.num_blocks, d.ngroups, d.group_cols, getattr(d, "_perm_inv", None)
 
 
 def get_net_out(decomp, H: Tensor) -> Tensor:
     """``e3TensorDecomp.get_net_out`` (utils_tensor_decomp.py:163-169) as the op,
     with the tables of a :class:`maloq_amd.basis_transform.HipE3TensorDecomp`."""
     decomp._check(H, decomp.total_h_dim)
-    return label_transform(H, decomp._blocks_fwd, decomp._wk_fwd, decomp._sched, None, decomp._perm, decomp.num_blocks)
+    return label_transform(H, decomp._blocks_fwd, decomp._wk_fwd, decomp._sched, None, decomp._perm,
+                           *_layout(decomp))
 
 
 def get_H(decomp, net_out: Tensor) -> Tensor:
@@ -138,12 +162,13 @@ class _GetHOp(torch.autograd.Function):
     def forward(ctx, net_out, decomp):
         ctx.decomp = decomp
         return label_transform(net_out, decomp._blocks_inv, decomp._wk_inv, decomp._sched, decomp._perm, None,
-                               decomp.num_blocks)
+                               *_layout(decomp))
 
     @staticmethod
     def backward(ctx, g):
         d = ctx.decomp
-        return label_transform(g.contiguous(), d._blocks_adj, d._wk_adj, d._sched, None, d._perm, d.num_blocks), None
+        return label_transform(g.contiguous(), d._blocks_adj, d._wk_adj, d._sched, None, d._perm,
+                               *_layout(d)), None
 
 
 # ----------------------------------------------------------- message block

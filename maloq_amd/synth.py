@@ -16,7 +16,7 @@ from dataclasses import dataclass
 
 import numpy as np
 
-SYMBOL_Z = {"H": 1, "C": 6, "N": 7, "O": 8, "F": 9, "Si": 14, "S": 16}
+SYMBOL_Z = {"H": 1, "C": 6, "N": 7, "O": 8, "F": 9, "Si": 14, "S": 16, "Ga": 31, "I": 53}
 
 
 @dataclass

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     missing = [s for s in declared_symbols() if not hasattr(lib, s)]
     assert not missing, missing
     lib.maloq_abi_version.restype = ctypes.c_int
-    assert lib.maloq_abi_version() == 2
+    assert lib.maloq_abi_version() == 3
 
 
 def test_ctypes_signatures_cover_header():
@@ -57,14 +57,23 @@ def test_supported_shapes_and_rotate_validation_without_gpu():
 
 
 def test_label_width_limit_without_gpu():
-    """A 32-row fp32 tile of the label width and its 32-byte row descriptors
-    must fit one CU's 160 KB of LDS: 1271 is the widest row accepted (checked on
-    the host; zero rows launch nothing)."""
+    """A 32-row fp32 tile of the widest column group and its 40-byte row
+    descriptors must fit one CU's 160 KB of LDS: 1269 columns is the widest
+    group accepted.  Wider rows are split into groups (any width, 0 rows launch
+    nothing); a column permutation needs one group (checked on the host)."""
     import numpy as np
     from maloq_amd import _lib
     blocks = np.array([[1, 0, 0, 0]], dtype=np.int32)
-    sched = np.array([0, 1, 1, 1, 1, 0], dtype=np.int32)
+    sched = np.array([1, 0, 1, 0, 5, 0, 1, 1, 1, 1, 0], dtype=np.int32)
     bp, sp = blocks.ctypes.data, sched.ctypes.data
-    _lib.call("maloq_label_transform", None, None, None, None, 0, 1271, 1, bp, None, sp, None)
-    with pytest.raises(_lib.MaloqHipError, match="label width 1272 too large"):
-        _lib.call("maloq_label_transform", None, None, None, None, 0, 1272, 1, bp, None, sp, None)
+    _lib.call("maloq_label_transform", None, None, None, None, 0, 1269, 1, bp, None, sp, 1, 1269, None)
+    with pytest.raises(_lib.MaloqHipError, match="column group of 1270 columns too wide"):
+        _lib.call("maloq_label_transform", None, None, None, None, 0, 1270, 1, bp, None, sp, 1, 1270, None)
+    # 4096 columns as 21 groups of at most 204 (400 blocks)
+    _lib.call("maloq_label_transform", None, None, None, None, 0, 4096, 400, bp, None, sp, 21, 204, None)
+    with pytest.raises(_lib.MaloqHipError, match="does not fit the row width"):
+        _lib.call("maloq_label_transform", None, None, None, None, 0, 4096, 400, bp, None, sp, 1, 204, None)
+    with pytest.raises(_lib.MaloqHipError, match="needs rows of one column group"):
+        _lib.call("maloq_label_transform", None, sp, None, None, 0, 4096, 400, bp, None, sp, 21, 204, None)
+    with pytest.raises(_lib.MaloqHipError, match="column groups 401 outside"):
+        _lib.call("maloq_label_transform", None, None, None, None, 0, 4096, 400, bp, None, sp, 401, 204, None)

@@ -19,6 +19,13 @@ pytestmark = pytest.mark.gpu
 CFG3 = {1: [0, 0, 1], 6: [0, 0, 0, 1, 1, 2], 7: [0, 0, 0, 1, 1, 2], 8: [0, 0, 0, 1, 1, 2]}
 MOCK = {1: [0], 6: [0, 0, 1], 8: [0, 0, 1]}
 SIO2 = {14: [0, 0, 1, 1, 2], 8: [0, 0, 1, 1, 2]}
+# def2-TZVPD shells (src/maloq/fock_utils/basis_sets.py:28): H/C/N/O rows are 1600
+# columns wide; with Ga and I the template has the whole dictionary's 64 orbitals
+# (4096 columns, 400 CG blocks), as get_loader.py:106-107 builds it for OMol.
+TZVPD_HCNO = {1: [0, 0, 0, 1, 1], 6: [0, 0, 0, 0, 0, 1, 1, 1, 2, 2, 3, 0, 2],
+              7: [0, 0, 0, 0, 0, 1, 1, 1, 2, 2, 3, 0, 2], 8: [0, 0, 0, 0, 0, 1, 1, 1, 2, 2, 3, 0, 1, 2]}
+TZVPD = {**TZVPD_HCNO, 31: [0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 2, 2, 2, 2, 3, 0, 2],
+         53: [0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 2, 2, 2, 3, 3, 0, 1, 2]}
 
 
 def _tables(basis, if_sort=False):
@@ -100,14 +107,19 @@ def test_sparse_block_list_bit_exact(device):
         assert np.array_equal(back.data.cpu().numpy()[covered], data[covered])
 
 
-@pytest.mark.parametrize("basis,if_sort", [(MOCK, True), (MOCK, False), (CFG3, False), (SIO2, False)])
+@pytest.mark.parametrize("basis,if_sort", [(MOCK, True), (MOCK, False), (CFG3, False), (SIO2, False),
+                                           (TZVPD_HCNO, False), (TZVPD_HCNO, True), (TZVPD, False)])
 def test_label_transforms_match_oracle(basis, if_sort, device):
+    """get_net_out / get_H against the dense fp64 oracle; the def2-TZVPD rows
+    (1600 and 4096 columns) run as several column groups, sorted ones through
+    the separate column permutation."""
     from maloq_amd.basis_transform import HipE3TensorDecomp
     t, base, ora = _tables(basis, if_sort)
     hip = HipE3TensorDecomp(base)
     T = ora.H_slices[-1]
+    assert (hip.ngroups > 1) == (T > 204)
     g = torch.Generator().manual_seed(0)
-    for R in (0, 1, 77, 1000):
+    for R in ((0, 1, 77, 1000) if T <= 204 else (0, 1, 77, 300)):
         Hh = torch.randn(R, T, generator=g)
         x = torch.randn(R, ora.in_slices[-1], generator=g)
         got = hip.get_net_out(Hh.float().to(device)).cpu().double()
@@ -140,14 +152,18 @@ def test_reference_mock_triton_case(device):
     assert torch.allclose(hip.get_H(x), y_ref, atol=1e-4, rtol=1e-4)
 
 
-def test_get_H_backward_is_adjoint(device):
+@pytest.mark.parametrize("basis,if_sort", [(CFG3, False), (TZVPD, False), (TZVPD_HCNO, True)])
+def test_get_H_backward_is_adjoint(basis, if_sort, device):
     from maloq_amd.basis_transform import HipE3TensorDecomp
-    t, base, ora = _tables(CFG3)
+    t, base, ora = _tables(basis, if_sort)
     hip = HipE3TensorDecomp(base)
-    x = torch.randn(300, 196, device=device, requires_grad=True)
-    gH = torch.randn(300, 196, device=device)
+    T = int(ora.H_slices[-1])
+    x = torch.randn(300, T, device=device, requires_grad=True)
+    gH = torch.randn(300, T, device=device)
     hip.get_H(x).backward(gH)
-    ref = gH.cpu().double() @ ora.W_global.T
+    ref = gH.cpu().double() @ ora.W_global.T  # gradient wrt the unsorted rows get_H multiplies
+    if if_sort:
+        ref = ora.sort(ref)  # get_H un-sorts its input first, so the gradient is sorted back
     assert (x.grad.cpu().double() - ref).abs().max() / ref.abs().max() < 1e-5
 
 
@@ -167,7 +183,7 @@ def test_compiled_programs_equal_dense_blocks(basis, device):
     def rows(blocks, w, perm_in, perm_out):
         out = torch.empty_like(x)
         _lib.call("maloq_label_transform", x, perm_in, out, perm_out, x.shape[0], T, hip.num_blocks, blocks, w,
-                  hip._sched, _lib.stream_of(device))
+                  hip._sched, *hip._layout(), _lib.stream_of(device))
         return out
 
     for blocks, w, pin, pout in ((hip._blocks_fwd, hip._w_fwd, None, hip._perm),
@@ -318,3 +334,80 @@ def test_pair_list_calls_equal_planned_calls(device):
     hip3.irreps_to_fock(irr, H_a, off3, z, r3, c3, t3.orbital_template, plan=plan3)
     hip3.irreps_to_fock(irr, H_b, off3, z, r3, c3, t3.orbital_template)
     assert torch.equal(H_a, H_b)
+
+
+def _wide_molecule(t, elements, seed, n=12):
+    from maloq_amd.synth import sphere_molecule, radius_graph, dense_hamiltonian, atom_pair_rows
+    z, p = sphere_molecule(n, elements, [1.0] * len(elements), seed=seed)
+    H, off = dense_hamiltonian(z, p, t.orbitals_per_atom(z), seed=seed + 1)
+    src, dst, _ = radius_graph(p, 8.0)
+    rows, cols = atom_pair_rows(src, dst, n)
+    return z, H, off, rows, cols
+
+
+@pytest.mark.parametrize("basis,elements", [(TZVPD_HCNO, ["H", "C", "N", "O"]), (TZVPD, ["H", "C", "N", "O"]),
+                                            (TZVPD, ["H", "C", "O", "Ga", "I"])])
+def test_wide_fused_fock_transforms(basis, elements, device):
+    """def2-TZVPD widths, dense and block-list storage, with and without a row
+    plan.  The gather and the scatter are bit-exact: fock_to_irreps(F) equals
+    get_net_out of the oracle's gathered labels bit for bit (the same CG
+    programs on the same tile), and irreps_to_fock(x) equals the oracle's
+    scatter of get_H(x).  Against the fp64 oracle: 1e-5; round trip: 1e-6."""
+    from maloq_amd.basis_transform import HipE3TensorDecomp
+    t, base, ora = _tables(basis)
+    hip = HipE3TensorDecomp(base)
+    T = hip.total_in_dim
+    assert hip.ngroups > 1
+    for seed in (0, 1):
+        z, H, off, rows, cols = _wide_molecule(t, elements, 50 + seed)
+        lab = _oracle_labels(t, z, H, off, rows, cols, T)
+        Hd = torch.from_numpy(H).to(device)
+        want = hip.get_net_out(torch.from_numpy(lab).to(device))
+        ref = ora.get_net_out(torch.from_numpy(lab).double())
+        bdo = om2l.block_data_offsets(off, rows, cols)
+        data = np.concatenate([H[off[i]:off[i + 1], off[j]:off[j + 1]].reshape(-1) for i, j in zip(rows, cols)])
+        dd = torch.from_numpy(data).to(device)
+        plan = hip.make_plan(Hd, off, z, rows, cols, t.orbital_template)
+        for got in (hip.fock_to_irreps(Hd, off, z, rows, cols, t.orbital_template),
+                    hip.fock_to_irreps(Hd, off, z, rows, cols, t.orbital_template, plan=plan),
+                    hip.fock_to_irreps(dd, off, z, rows, cols, t.orbital_template, block_data_offsets=bdo)):
+            assert torch.equal(got, want)
+            assert (got.cpu().double() - ref).abs().max() / ref.abs().max() < 1e-5
+        # inverse: scatter into zeros, compare with the oracle scatter of get_H
+        Hx = hip.get_H(want).cpu().numpy()
+        H_ref = np.zeros_like(H)
+        om2l.single_matrix2label(t.orbital_template, off, z, rows, cols, H_ref, Hx.copy(), False)
+        H2 = torch.zeros_like(Hd)
+        hip.irreps_to_fock(want, H2, off, z, rows, cols, t.orbital_template)
+        assert np.array_equal(H2.cpu().numpy(), H_ref)
+        H3 = torch.zeros_like(Hd)
+        hip.irreps_to_fock(want, H3, off, z, rows, cols, t.orbital_template, plan=plan)
+        assert torch.equal(H2, H3)
+        back = torch.zeros_like(dd)
+        hip.irreps_to_fock(want, back, off, z, rows, cols, t.orbital_template, block_data_offsets=bdo)
+        assert np.abs(back.cpu().numpy() - data).max() / np.abs(data).max() < 1e-6
+        mask = np.zeros(H.shape, bool)
+        for i, j in zip(rows, cols):
+            mask[off[i]:off[i + 1], off[j]:off[j + 1]] = True
+        assert np.abs(H2.cpu().numpy() - H)[mask].max() / np.abs(H).max() < 1e-6
+        assert np.all(H2.cpu().numpy()[~mask] == 0)
+
+
+def test_wide_sorted_fock_transforms(device):
+    """Sorted irreps rows wider than one column group: the fused transforms
+    permute in a separate column gather, and give the sorted rows of the
+    unsorted decomposition exactly."""
+    from maloq_amd.basis_transform import HipE3TensorDecomp
+    t, base_s, _ = _tables(TZVPD_HCNO, if_sort=True)
+    _, base_u, _ = _tables(TZVPD_HCNO)
+    hs, hu = HipE3TensorDecomp(base_s), HipE3TensorDecomp(base_u)
+    z, H, off, rows, cols = _wide_molecule(t, ["H", "C", "N", "O"], 60)
+    Hd = torch.from_numpy(H).to(device)
+    perm = torch.as_tensor(np.asarray(hs.sort_perm), device=device)
+    a = hs.fock_to_irreps(Hd, off, z, rows, cols, t.orbital_template)
+    b = hu.fock_to_irreps(Hd, off, z, rows, cols, t.orbital_template)
+    assert torch.equal(a, b[:, perm])
+    Ha, Hb = torch.zeros_like(Hd), torch.zeros_like(Hd)
+    hs.irreps_to_fock(a, Ha, off, z, rows, cols, t.orbital_template)
+    hu.irreps_to_fock(b, Hb, off, z, rows, cols, t.orbital_template)
+    assert torch.equal(Ha, Hb)

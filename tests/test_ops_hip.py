@@ -87,13 +87,21 @@ def test_message_block_op_matches_module_path(device):
 
 
 @pytest.mark.gpu
-def test_label_transform_op_matches_decomp(device):
+@pytest.mark.parametrize("basis,if_sort", [({1: [0, 0, 1], 6: [0, 0, 0, 1, 1, 2]}, False),
+                                           ({1: [0, 0, 0, 1, 1], 8: [0, 0, 0, 0, 0, 1, 1, 1, 2, 2, 3, 0, 1, 2]},
+                                            True)])
+def test_label_transform_op_matches_decomp(basis, if_sort, device):
+    """The op equals the decomposition's methods bit for bit, forward and
+    gradient, for one column group and for sorted rows of several groups (the
+    def2-TZVPD H/O width, 1600 columns); opcheck covers its schema and fake."""
     from maloq_amd import ops
     from maloq_amd import tensor_decomp as ptd
     from maloq_amd.basis_transform import HipE3TensorDecomp
-    t = ptd.BasisTables({1: [0, 0, 1], 6: [0, 0, 0, 1, 1, 2]})
-    hip = HipE3TensorDecomp(ptd.e3TensorDecomp(t.req_output_irreps, t.out_js_list, torch.float32,
+    t = ptd.BasisTables(basis)
+    irreps = t.simplified_irreps if if_sort else t.req_output_irreps
+    hip = HipE3TensorDecomp(ptd.e3TensorDecomp(irreps, t.out_js_list, torch.float32, if_sort=if_sort,
                                                device_torch=device))
+    assert (hip.ngroups > 1) == if_sort
     gen = torch.Generator().manual_seed(3)
     H = torch.randn(77, hip.total_h_dim, generator=gen).to(device)
     assert torch.equal(ops.get_net_out(hip, H), hip.get_net_out(H))
@@ -105,3 +113,5 @@ def test_label_transform_op_matches_decomp(device):
     a.backward(g)
     b.backward(g)
     assert torch.equal(y.grad, y2.grad)
+    torch.library.opcheck(ops.label_transform, (H, hip._blocks_fwd, hip._wk_fwd, hip._sched, None, hip._perm)
+                          + ops._layout(hip), test_utils=("test_schema", "test_faketensor"))
