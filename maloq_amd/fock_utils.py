@@ -43,13 +43,23 @@ class ScaleShift:
     def __init__(self, scale_shift_data, device, spin_string=""):
         means = scale_shift_data["element_scalar_means" + spin_string]
         idx = [int(i) for i in scale_shift_data["scalar_irrep_indices"]]
+        if len(set(idx)) != len(idx):
+            # one writer per label element: the kernel updates each (row, column) once
+            raise ValueError("scalar_irrep_indices must not repeat a column")
+        if min(idx, default=0) < 0:
+            raise ValueError("scalar_irrep_indices must be non-negative")
         if isinstance(means, dict):
             max_z = max(int(z) for z in means)
             table = np.zeros((max_z + 1, len(idx)), np.float32)
             for z, v in means.items():
-                table[int(z)] = np.asarray(v, dtype=np.float32)
+                v = np.asarray(v, dtype=np.float32).reshape(-1)
+                if v.shape[0] != len(idx):
+                    raise ValueError(f"element {z}: {v.shape[0]} means for {len(idx)} scalar columns")
+                table[int(z)] = v
         else:
             table = np.asarray(torch.as_tensor(means).float().cpu().numpy(), np.float32)
+            if table.ndim != 2 or table.shape[1] != len(idx):
+                raise ValueError(f"means table must be [max Z + 1, {len(idx)}], got {tuple(table.shape)}")
         self.device = torch.device(device)
         self.means = torch.from_numpy(table).to(self.device)
         self.cols = _i32(idx, self.device)
@@ -246,7 +256,10 @@ def sparse_block_matrix_to_csr_arrays(sparse_matrix):
         raise IndexError("a block's data runs outside the data array")
     # columns of the blocks left of each block in its block row (blocks of one
     # row atom in column-atom order)
-    order = torch.argsort(rows * (off.shape[0]) + cols)
+    keys = rows * (off.shape[0]) + cols
+    order = torch.argsort(keys)
+    if nb > 1 and bool((keys[order][1:] == keys[order][:-1]).any()):
+        raise ValueError("blocks overlap: a (row atom, column atom) pair appears twice")
     ro, njo = rows[order], nj[order]
     run = torch.cumsum(njo, 0) - njo
     first = torch.zeros_like(run)
@@ -263,8 +276,6 @@ def sparse_block_matrix_to_csr_arrays(sparse_matrix):
     indptr = torch.zeros(n + 1, dtype=torch.int64, device=dev)
     indptr[1:] = torch.cumsum(atom_len[atom_of_row], 0)
     nnz = int(indptr[-1].item())
-    if nnz != int((ni * nj).sum().item()):
-        raise ValueError("blocks overlap: a (row atom, column atom) pair appears twice")
     csr_data = torch.empty(nnz, dtype=torch.float32, device=dev)
     csr_idx = torch.empty(nnz, dtype=torch.int64, device=dev)
     data_d = data.float().contiguous()                 # alive across the launch

@@ -14,10 +14,18 @@ Parity pins (what each restated function is checked against):
 * so2.*, message.*: brute force on tiny inputs, gamma invariance of the block,
                     global SO(3) equivariance, fp64 scatter sums.
 * tensor_decomp.* : CG invariance under the Jd-based D, unit norm, cyclic
-                    symmetry, exact round trip, (0,l,l)/(l,l,0) sign pinned by the
-                    reference's element_scale_shifts data (l=0 label means).
-                    Sign of CG tensors with l1+l2+l3 odd: parity unpinned (only
-                    an import of e3nn could pin it; e3nn is absent).
+                    symmetry, exact round trip.  These fix each CG tensor only
+                    up to one sign per cyclic class (l1, l2, l3).  Data pins:
+                    the (l,l,0) class (with (0,l,l), (l,0,l)) for l <= 2 by the
+                    reference's nablaDFT l = 0 label means, for l = 3 by its
+                    OMol on-site f-f means (tests/golden/scale_shifts_*.npz);
+                    the 4096-column irreps layout by the OMol scalar columns.
+                    The sign of every other class, i.e. every coupling with
+                    l1, l2, l3 all > 0 ((1,1,1), (1,1,2), (2,2,2), (1,2,3), ...):
+                    parity unpinned.  Only e3nn.o3.wigner_3j, which the
+                    reference calls (utils_tensor_decomp.py:93-94) and which is
+                    absent here, could pin it; the restatement follows e3nn's
+                    published construction.
 * matrix2labels.* : exact copy semantics, forward/inverse identity on covered
                     entries.
 * irreps_head.*   : node expansion against the CG labels of symmetric on-site

@@ -7,9 +7,10 @@ subgraph of the subset's in-edges) and through size-independent properties.
 * config 4: 8 x 150 atoms (8 A cutoff), lmax 6, mmax 2, C 128, gated, bf16:
   forward and backward on a node subset, and bitwise run-to-run determinism of
   the whole graph's forward and gradients;
-* config 5: 2000-atom periodic SiO2 cell (6 A cutoff), lmax 4, C 256, bf16:
-  forward on a node subset; the 2s2p1d block-sparse basis transform on the
-  whole cell: gather bit-exact against the oracle, round trip within 1e-6.
+* config 5: 2000-atom periodic SiO2 cell (6 A cutoff), lmax 4, C 256: bf16
+  forward, and fp32 / bf16 forward and backward, on a node subset; the 2s2p1d
+  block-sparse basis transform on the whole cell: gather bit-exact against
+  the oracle, round trip within 1e-6.
 
 Bars: fp32 within 1e-5 of the output (or gradient) scale, bf16 within 2e-2,
 the oracle evaluated on the bf16-rounded inputs and weights.
@@ -139,6 +140,16 @@ def test_config4_gated_lmax6_fwd_bwd(cfg4, device):
 def test_config5_c256_forward(cfg5, device):
     print("config 5 lmax=4 C=256 bf16", flush=True)
     _subset_check(cfg5, np.arange(0, 2000, 200), 4, 2, 256, torch.bfloat16, False, device, backward=False, seed=5)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_config5_c256_fwd_bwd(cfg5, dtype, device):
+    """The timed config-5 step at its width (C = 256) on the whole 2000-atom
+    cell: the forward rows and every gradient (x, the radial rows, the m = 0
+    weights and bias, the m > 0 weights) of a loss on a node subset, against
+    the fp64 oracle on the subset's in-edges."""
+    print(f"config 5 lmax=4 C=256 fwd+bwd dtype={dtype}", flush=True)
+    _subset_check(cfg5, np.arange(7, 2000, 250), 4, 2, 256, dtype, False, device, backward=True, seed=6)
 
 
 def test_config5_block_sparse_transform_full_cell(cfg5, device):

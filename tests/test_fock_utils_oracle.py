@@ -103,3 +103,19 @@ def test_csr_export_assembles_blocks():
     for b, (i, j) in enumerate(zip(rows, cols)):
         D[off[i]:off[i + 1], off[j]:off[j + 1]] = data[bdo[b]:bdo[b + 1]].reshape(off[i + 1] - off[i], -1)
     assert np.array_equal(A, D)
+
+
+def test_scale_shift_tables_validated():
+    """A means table of the wrong width and a repeated scalar column are refused
+    when the ScaleShift is built (the kernel indexes means[Z * ncols + k] and
+    updates each (row, column) from one thread)."""
+    from maloq_amd.fock_utils import ScaleShift
+    ok = {"element_scalar_means": {1: [0.5, 1.0], 6: [2.0, 3.0]}, "scalar_irrep_indices": [0, 3]}
+    ScaleShift(ok, "cpu")
+    with pytest.raises(ValueError, match="must not repeat"):
+        ScaleShift({**ok, "scalar_irrep_indices": [3, 3]}, "cpu")
+    with pytest.raises(ValueError, match="2 scalar columns"):
+        ScaleShift({**ok, "element_scalar_means": {1: [0.5], 6: [2.0, 3.0]}}, "cpu")
+    with pytest.raises(ValueError, match="must be"):
+        ScaleShift({**ok, "element_scalar_means": torch.zeros(7, 3)}, "cpu")
+    ScaleShift({**ok, "element_scalar_means": torch.zeros(7, 2)}, "cpu")

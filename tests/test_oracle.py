@@ -143,6 +143,62 @@ def test_cg_scalar_coupling_signs(l):
     assert np.abs(otd.wigner_3j(l, l, 0).numpy()[:, :, 0] - e).max() < 1e-14
 
 
+# def2-TZVPD shells (src/maloq/fock_utils/basis_sets.py:28) of H/C/N/O plus Ga (4 d shells) and
+# I (2 f shells): the same template as the whole dictionary (64 orbitals, 4096 columns).
+TZVPD = {1: [0, 0, 0, 1, 1], 6: [0, 0, 0, 0, 0, 1, 1, 1, 2, 2, 3, 0, 2],
+         7: [0, 0, 0, 0, 0, 1, 1, 1, 2, 2, 3, 0, 2], 8: [0, 0, 0, 0, 0, 1, 1, 1, 2, 2, 3, 0, 1, 2],
+         31: [0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 2, 2, 2, 2, 3, 0, 2],
+         53: [0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 2, 2, 2, 3, 3, 0, 1, 2]}
+
+
+def _omol_scale_shifts():
+    import os
+    return np.load(os.path.join(os.path.dirname(__file__), "golden", "scale_shifts_omol.npz"))
+
+
+def test_omol_scalar_columns_are_the_l0_irreps_at_4096_columns():
+    """The reference's OMol scale-shift data (element_scale_shifts_omol_csh_58k.pt,
+    def2-TZVPD over the whole dictionary) names its 114 scalar label columns: they
+    are exactly the l3 = 0 irreps of the shell pairs l1 = l2 (diffuse shells
+    included) in the restated decomposition's 4096-column layout."""
+    d = _omol_scale_shifts()
+    t, ls, js, sl, full = otd.make_output_irreps(copy.deepcopy(TZVPD))
+    o = otd.E3TensorDecomp(js)
+    assert int(o.in_slices[-1]) == 4096 and len(js) == 400
+    scal = [int(o.in_slices[b]) for b, (l1, l2) in enumerate(js) if l1 % 10 == l2 % 10]
+    assert scal == d["scalar_irrep_indices"].tolist()
+    # and each is the irrep l3 = 0 of its block: the first of l3 = |l1 - l2| ..
+    col_l = [l for l in o.irreps_ls for _ in range(2 * l + 1)]
+    assert len(col_l) == 4096 and all(col_l[c] == 0 for c in scal)
+    assert sum(1 for l in col_l if l == 0) == len(scal)
+
+
+def test_cg_ff_scalar_sign_pinned_by_omol_means():
+    """(3,3,0): tight f polarisation functions have positive diagonal Fock
+    elements, and the reference's OMol data gives every element with an f shell
+    a positive on-site f-f scalar label mean (B .. F at 6 to 46 standard
+    deviations: C 6.5 +- 0.4, O 13.6 +- 0.4).  With the restated coupling, an f-f block of positive trace maps to
+    a positive scalar label (+trace / sqrt 7); a flipped (3,3,0) sign would make
+    every such mean negative."""
+    d = _omol_scale_shifts()
+    t, ls, js, sl, full = otd.make_output_irreps(copy.deepcopy(TZVPD))
+    o = otd.E3TensorDecomp(js)
+    ff = [b for b, (l1, l2) in enumerate(js) if l1 % 10 == 3 and l2 % 10 == 3]
+    b = ff[0]  # f0 - f0
+    col = list(d["scalar_irrep_indices"]).index(int(o.in_slices[b]))
+    with_f = [k for k, Z in enumerate(d["Z"]) if not (d["means"][k, col] == 0.0 and d["stds"][k, col] == 1.0)]
+    assert len(with_f) >= 40 and 6 in d["Z"][with_f] and 8 in d["Z"][with_f]
+    assert np.all(d["means"][with_f, col] > 0)  # all 47 elements with an f shell
+    light = [k for k in with_f if 5 <= d["Z"][k] <= 9]  # B .. F: 6 to 46 standard deviations
+    assert len(light) == 5 and np.all(d["means"][light, col] > 6 * d["stds"][light, col])
+    H = torch.zeros(1, int(o.H_slices[-1]), dtype=torch.float64)
+    n = int(o.H_slices[b + 1] - o.H_slices[b])
+    H[0, int(o.H_slices[b]):int(o.H_slices[b + 1])] = torch.eye(7, dtype=torch.float64).reshape(-1)  # F_ff = I
+    assert n == 49
+    lab = o.get_net_out(H)
+    assert abs(lab[0, int(o.in_slices[b])].item() - 7 / math.sqrt(7)) < 1e-12
+
+
 BASES = {
     "mock": {1: [0], 6: [0, 0, 1], 8: [0, 0, 1]},
     "def2svp_qm7": {9: [0, 0, 0, 1, 1, 2], 8: [0, 0, 0, 1, 1, 2], 7: [0, 0, 0, 1, 1, 2], 6: [0, 0, 0, 1, 1, 2], 1: [0, 0, 1]},
