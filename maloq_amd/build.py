@@ -72,7 +72,12 @@ def build(verbose: bool = True, incremental: bool = False) -> str:
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(lambda s: _compile(s, incremental), srcs))
     tmp = OUT + ".tmp"
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]
+    # -Bsymbolic: the library's calls to its own functions (the per-shape launch
+    # templates, kernel stubs) bind inside it.  Without it they go through the
+    # PLT, and a second build loaded into the same process (a copy with other
+    # tile sizes, another version) would run the first build's definitions with
+    # its own sizes.
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,-Bsymbolic", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")

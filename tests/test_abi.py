@@ -77,3 +77,53 @@ def test_label_width_limit_without_gpu():
         _lib.call("maloq_label_transform", None, sp, None, None, 0, 4096, 400, bp, None, sp, 21, 204, None)
     with pytest.raises(_lib.MaloqHipError, match="column groups 401 outside"):
         _lib.call("maloq_label_transform", None, None, None, None, 0, 4096, 400, bp, None, sp, 401, 204, None)
+
+
+def test_library_binds_its_own_functions():
+    """The library is linked with -Bsymbolic: its calls to its own C++
+    functions (the per-shape launch templates, kernel stubs) are bound inside
+    it, with no PLT slot a second build loaded into the same process could
+    take over."""
+    import shutil
+    import subprocess
+    readelf = shutil.which("readelf")
+    if readelf is None:
+        pytest.skip("readelf is not installed")
+    dyn = subprocess.run([readelf, "-dW", LIB], capture_output=True, text=True, check=True).stdout
+    assert "SYMBOLIC" in dyn
+    rel = subprocess.run([readelf, "-rW", LIB], capture_output=True, text=True, check=True).stdout
+    own = [ln for ln in rel.splitlines() if "JUMP_SLOT" in ln and "_ZN5maloq" in ln]
+    assert not own, own[:3]
+
+
+def test_second_build_in_one_process_runs_its_own_templates(tmp_path):
+    """Why the library binds its own functions.  Two builds that explicitly
+    instantiate the same launch template with different tile sizes, both loaded
+    with RTLD_GLOBAL as maloq_amd/_lib.py loads the library: without
+    -Bsymbolic the second build's entry point runs the first build's template
+    (it would size the grid for one tile and launch the other's kernel); with
+    it, its own."""
+    import shutil
+    import subprocess
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("g++ is not installed")
+    (tmp_path / "t.h").write_text("template <int MODE> int launch(int e);\nextern template int launch<0>(int);\n")
+    for te in (64, 32):
+        (tmp_path / f"i{te}.cpp").write_text(
+            '#include "t.h"\ntemplate <int MODE> int launch(int e) { return (e + %d - 1) / %d * 1000 + %d; }\n'
+            "template int launch<0>(int);\n" % (te, te, te))
+        (tmp_path / f"e{te}.cpp").write_text('#include "t.h"\nextern "C" int entry(int e) { return launch<0>(e); }\n')
+
+    def build(te, name, flags):
+        out = str(tmp_path / name)
+        subprocess.run([gxx, "-O2", "-fPIC", "-shared", *flags, str(tmp_path / f"i{te}.cpp"),
+                        str(tmp_path / f"e{te}.cpp"), "-o", out], check=True)
+        return ctypes.CDLL(out, mode=ctypes.RTLD_GLOBAL)
+
+    first = build(64, "first.so", [])
+    plain = build(32, "plain.so", [])
+    symbolic = build(32, "symbolic.so", ["-Wl,-Bsymbolic"])
+    assert first.entry(100) == 2064        # 2 tiles of 64 edges
+    assert plain.entry(100) == 2064        # the 32-edge build ran the 64-edge template
+    assert symbolic.entry(100) == 4032     # 4 tiles of 32 edges: its own
