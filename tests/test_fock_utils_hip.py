@@ -121,7 +121,8 @@ def test_csr_export_matches_scipy(device):
     assert np.array_equal(got.data, want.data)
     # a (row atom, column atom) pair listed twice is refused before any launch
     dup = SparseBlockMatrix(data=sbm.data,
-                            block_data_offsets=torch.cat([sbm.block_data_offsets, sbm.block_data_offsets[:1]]),
+                            block_data_offsets=torch.cat([sbm.block_data_offsets[:-1], sbm.block_data_offsets[:1],
+                                                          sbm.block_data_offsets[-1:]]),
                             fock_block_rows=torch.cat([sbm.fock_block_rows, sbm.fock_block_rows[:1]]),
                             fock_block_cols=torch.cat([sbm.fock_block_cols, sbm.fock_block_cols[:1]]),
                             fock_block_offsets=sbm.fock_block_offsets)
