@@ -639,6 +639,8 @@ TRAFFIC_GROUPS = {
     "fock_to_irreps": r"maloq::bt::transform_kernel",
 }
 COPY_BYTES = 4 * 64 * 1024 * 1024        # the --only copy kernel: this many bytes read, as many written
+PMC_GEMM = ("SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "SQ_INSTS_MFMA", "SQ_INSTS_VALU_MFMA_MOPS_BF16",
+            "SQ_INSTS_VALU_MFMA_MOPS_F32", "SQ_INSTS_LDS", "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE")
 
 
 def load_traffic(name):
@@ -691,6 +693,93 @@ def traffic_from(root, dtype):
     with open(TRAFFIC_JSON, "w") as f:
         json.dump(prev, f, indent=1, sort_keys=True)
     print(json.dumps(out))
+    return 0
+
+
+COUNTER_PIECES = (("step_config2_fp32", "config 2, fp32, training step"),
+                  ("step_config2_bf16", "config 2, bf16, training step"),
+                  ("step_config4_bf16", "config 4 (lmax 6, gated), bf16, training step"),
+                  ("step_config5_bf16", "config 5 (C 256), bf16, training step"),
+                  ("edgewise_step_bf16", "Edgewise two convolutions, config 2, bf16, fwd+bwd"))
+SIMDS = 1024  # 256 CUs x 4 SIMDs
+
+
+def _kernel_label(name):
+    """Short label of a message-block kernel from its demangled name, or None."""
+    import re
+    m = re.search(r"gemm_kernel<(\d+), (\d+), (true|false), (\d+), (\d+), maloq::msg::(\w+), (\d+), (\d+), "
+                  r"(true|false), (\d+)>", name)
+    if m:
+        L, M, gate, nw, rt, tm, mode, kr, rad, minb = m.groups()
+        modes = {"0": "FWD", "1": "BWD_DX", "2": "FWD_EDGE", "3": "BWD_EDGE"}
+        return (f"gemm {modes[mode]} L{L} M{M}{' gated' if gate == 'true' else ''} {tm} "
+                f"({32 * int(rt)}-edge tiles, {nw} waves{', radial grad' if rad == 'true' else ''})")
+    for k in ("dw_tr_kernel", "dw_kernel", "dw_reduce_kernel", "prep_kernel", "radial_fwd", "radial_du",
+              "radial_chain", "radial_dwo"):
+        if k in name:
+            return k + ("<BF16>" if "BF16" in name and k == "dw_kernel" else "<F32>" if k == "dw_kernel" else "")
+    return None
+
+
+def counters_from(root):
+    """Writes profiles/gemm_counters.md from rocprofv3 --pmc runs under `root`:
+    <root>/<piece>/run_counter_collection.csv for the COUNTER_PIECES (counters
+    SQ_VALU_MFMA_BUSY_CYCLES, GRBM_GUI_ACTIVE, SQ_INSTS_MFMA,
+    SQ_INSTS_VALU_MFMA_MOPS_BF16 / _F32, SQ_INSTS_LDS, SQ_LDS_BANK_CONFLICT,
+    SQ_LDS_IDX_ACTIVE).  Per kernel the median dispatch: MFMA busy = busy
+    cycles over (SIMDs x the dispatch's cycles, from GRBM_GUI_ACTIVE per XCD
+    and its duration), MFMA TFLOP/s executed (MOPS x 512 over the duration),
+    LDS bank-conflict cycles per LDS-active cycle."""
+    import csv
+    import statistics
+    rows = ["| workload | kernel | dispatch µs | MFMA busy | MFMA TFLOP/s executed | MFMA instr. | LDS instr. | "
+            "LDS bank conflicts / LDS active cycles |", "|---|---|---|---|---|---|---|---|"]
+    for piece, what in COUNTER_PIECES:
+        path = os.path.join(root, piece, "run_counter_collection.csv")
+        if not os.path.exists(path):
+            continue
+        per = {}  # (label, dispatch) -> {counter: value, "dur": ns}
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                label = _kernel_label(r["Kernel_Name"])
+                if label is None:
+                    continue
+                d = per.setdefault((label, r["Dispatch_Id"]), {})
+                d[r["Counter_Name"]] = float(r["Counter_Value"])
+                d["dur"] = float(r["End_Timestamp"]) - float(r["Start_Timestamp"])
+        by = {}
+        for (label, _), d in per.items():
+            by.setdefault(label, []).append(d)
+        for label in sorted(by):
+            ds = by[label]
+            med = lambda k: statistics.median(x.get(k, 0.0) for x in ds)
+            dur = med("dur")
+            grbm = med("GRBM_GUI_ACTIVE")
+            xcds = max(1, round(grbm / (dur * 2.4))) if dur > 0 else 1  # GRBM summed over XCDs at ~2.4 GHz
+            cycles = grbm / xcds
+            busy = med("SQ_VALU_MFMA_BUSY_CYCLES") / (SIMDS * cycles) if cycles else 0.0
+            mops = med("SQ_INSTS_VALU_MFMA_MOPS_BF16") + med("SQ_INSTS_VALU_MFMA_MOPS_F32")
+            tflops = mops * 512 / (dur * 1e-9) / 1e12 if dur else 0.0
+            conf = med("SQ_LDS_BANK_CONFLICT") / max(med("SQ_LDS_IDX_ACTIVE"), 1.0)
+            rows.append(f"| {what} | {label} | {dur / 1e3:.1f} | {100 * busy:.1f} % | {tflops:.1f} | "
+                        f"{med('SQ_INSTS_MFMA'):.3g} | {med('SQ_INSTS_LDS'):.3g} | {conf:.3f} |")
+    out = os.path.join(os.path.dirname(TRAFFIC_JSON), "gemm_counters.md")
+    with open(out, "w") as f:
+        f.write("# MFMA and LDS counters of the message-block kernels (rocprofv3 --pmc, median dispatch)\n\n")
+        f.write("Commands (GPU box, repo root, one counter pass per workload):\n\n")
+        for piece, what in COUNTER_PIECES:
+            only = "edgewise-step" if piece.startswith("edgewise") else "step"
+            dt = piece.rsplit("_", 1)[1]
+            cfg = "" if only != "step" else f" --cfg {piece.split('_')[1]}"
+            f.write(f"    timeout -s KILL 90 rocprofv3 --pmc {' '.join(PMC_GEMM)} --output-format csv "
+                    f"-d <root>/{piece} -o run -- python bench.py --only {only} --dtype {dt}{cfg} --reps 2\n")
+        f.write(f"    python bench.py --counters-from <root>\n\n")
+        f.write("MFMA busy: SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x the dispatch's cycles); the cycles are "
+                "GRBM_GUI_ACTIVE per XCD (the counter is summed over the XCDs).  MFMA TFLOP/s executed: "
+                "(SQ_INSTS_VALU_MFMA_MOPS_BF16 + _F32) x 512 / dispatch time (peaks: bf16 2500, fp32 157.3).  "
+                "Durations are those of the counter run (kernels serialised).\n\n")
+        f.write("\n".join(rows) + "\n")
+    print(open(out).read())
     return 0
 
 
@@ -890,7 +979,13 @@ def profile_only(args):
     elif args.only in ("fwd", "step"):
         w = message_workload(args.dtype, cfg=args.cfg)
         if args.only == "fwd":
-            fused_forward_launch_time(w, reps=args.reps)
+            # the bench times the forward after its training steps: warm the GPU
+            # the same way, so that a profile of this mode matches the headline
+            for _ in range(20):
+                message_step(w, True)
+            t = fused_forward_launch_time(w, reps=args.reps)
+            print(json.dumps({"fused_forward_launch_us": t * 1e6, "cfg": args.cfg, "dtype": args.dtype,
+                              "reps": args.reps}), flush=True)
         else:
             for _ in range(args.reps):
                 message_step(w, True)
@@ -927,9 +1022,13 @@ def main(argv=None):
     ap.add_argument("--reps", type=int, default=5, help="launches in --only mode")
     ap.add_argument("--traffic-from", metavar="DIR",
                     help="write profiles/traffic.json from rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE runs in DIR")
+    ap.add_argument("--counters-from", metavar="DIR",
+                    help="write profiles/gemm_counters.md from rocprofv3 --pmc MFMA/LDS counter runs in DIR")
     args = ap.parse_args(argv)
     if args.traffic_from:
         return traffic_from(args.traffic_from, args.dtype)
+    if args.counters_from:
+        return counters_from(args.counters_from)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(the hot path runs on a single MI355X; multi-GPU sharding is design-only)", file=sys.stderr)
