@@ -31,7 +31,7 @@ import torch
 from torch import nn
 
 from . import _lib
-from .message import MessagePlan, edgewise_block, rad_width
+from .message import edgewise_block, plan_for, rad_width
 from .radial import RadialMLP
 
 
@@ -119,7 +119,7 @@ class Edgewise(nn.Module):
         """Node sums [N, d, sphere_channels] (node) or per-edge messages
         [E, d, sphere_channels] (edge), in the dtype of x.  ``eulers`` [E, 3]:
         the edges' Euler angles in the original edge order; ``plan``: the
-        graph's MessagePlan (built here when not given)."""
+        graph's MessagePlan (the cached plan of edge_index when not given)."""
         if partition:
             raise NotImplementedError("partitioned (multi-GPU) graphs are not supported on one GPU")
         if self.concat_size == 3 and x_message_edge is None:
@@ -128,7 +128,7 @@ class Edgewise(nn.Module):
             raise ValueError("pass the reference's dense wigner [E, d, d] or eulers= [E, 3]")
         _lib.require_cuda(x, x_edge, eulers, wigner)
         if plan is None:
-            plan = MessagePlan(edge_index, x.shape[0])
+            plan = plan_for(edge_index, x.shape[0])
         rad = self.so2_conv_1.rad_func(plan.sort_edges(x_edge.float()), out_dtype=x.dtype)
         # The kept rows of the dense wigner are gathered in-kernel; wigner_inv is
         # its transpose (esen_osh.py:294) and is not read.

@@ -25,7 +25,7 @@ import torch
 from torch import nn
 
 from . import _lib
-from .message import MessagePlan, _jd_dev
+from .message import _jd_dev, plan_for
 from .radial import RadialMLP
 
 DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1}
@@ -93,7 +93,7 @@ def edge_degree_embed(x, u, edge_index, wigner_inv, lmax, rescale_factor, node_o
             raise ValueError(f"eulers must be [{E}, 3]")
     node = node_or_edge == "node"
     if node and plan is None:
-        plan = MessagePlan(edge_index, x.shape[0])
+        plan = plan_for(edge_index, x.shape[0])
     rows = _m0_rows(wigner_inv, eul, lmax, E, u.device)
     need = torch.is_grad_enabled() and (u.requires_grad or (node and x.requires_grad))
     if not need:

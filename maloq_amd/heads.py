@@ -26,7 +26,7 @@ from torch import nn
 
 from . import _lib
 from .edgewise import SO2_Convolution
-from .message import MessagePlan, edgewise_block
+from .message import CB, edgewise_block, plan_for
 from .so3 import CoefficientMapping
 
 
@@ -77,14 +77,16 @@ class _HeadBase(nn.Module):
         nodes = emb["node_embeddings"]
         x_edge = emb["x_edge"]
         if plan is None:
-            plan = MessagePlan(edge_index, nodes.shape[0])
+            plan = plan_for(edge_index, nodes.shape[0])
         wigner = emb.get("wigner") if eulers is None else None
         rad = self.so2_conv_1.rad_func(plan.sort_edges(x_edge.float()), out_dtype=nodes.dtype)
-        C = self.sphere_channels
-        if self.out_channels == C:
+        # the kernels write output channels in blocks of 32: a head with fewer
+        # (the force head's one) pads its conv2 to one block, not to sphere_channels
+        pad = -(-self.out_channels // CB) * CB
+        if self.out_channels == pad:
             conv2 = self.so2_conv_2.weights()
         else:
-            conv2 = _pad_out_channels(self.so2_conv_2, self.lmax, self.mmax, self.out_channels, C)
+            conv2 = _pad_out_channels(self.so2_conv_2, self.lmax, self.mmax, self.out_channels, pad)
         out = edgewise_block(nodes, plan, plan.sort_edges(eulers.float()) if eulers is not None else None, rad,
                              self.so2_conv_1.weights(), conv2, self.lmax, self.mmax, wigner=wigner)
         return out[:, :, :self.out_channels]

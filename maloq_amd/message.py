@@ -24,8 +24,10 @@ dst-sorted order (``plan.sort_edges``).
 """
 from __future__ import annotations
 
+import collections
 import ctypes
 import functools
+import weakref
 
 import numpy as np
 
@@ -85,6 +87,50 @@ class MessagePlan:
 
     def sort_edges(self, t: torch.Tensor) -> torch.Tensor:
         return t[self.perm].contiguous()
+
+
+class _PlanCache:
+    """MessagePlans of the most recent graphs, keyed on the ``edge_index``
+    tensor itself: the same tensor object (alive, with the same storage,
+    shape, device and version counter) and the same ``num_nodes`` give the
+    same plan.  The reference backbone hands one ``graph_dict["edge_index"]``
+    to every layer and block (helm/esen_osh.py:438-463), so its sorts and host
+    syncs then run once per graph instead of once per call.  An in-place
+    change of the tensor bumps its version counter and builds a new plan."""
+
+    def __init__(self, size=8):
+        self.size = size
+        self._entries = collections.OrderedDict()
+        self.built = 0  # plans built (misses), for tests and benchmarks
+
+    def get(self, edge_index: torch.Tensor, num_nodes: int) -> MessagePlan:
+        key = (id(edge_index), edge_index.data_ptr(), tuple(edge_index.shape), str(edge_index.device),
+               edge_index._version, int(num_nodes))
+        hit = self._entries.get(key)
+        if hit is not None and hit[0]() is edge_index:
+            self._entries.move_to_end(key)
+            return hit[1]
+        plan = MessagePlan(edge_index, num_nodes)
+        self.built += 1
+        self._entries[key] = (weakref.ref(edge_index), plan)
+        while len(self._entries) > self.size:
+            self._entries.popitem(last=False)
+        return plan
+
+    def clear(self):
+        self._entries.clear()
+
+
+_PLANS = _PlanCache()
+
+
+def plan_for(edge_index: torch.Tensor, num_nodes: int) -> MessagePlan:
+    """The cached MessagePlan of this graph (see _PlanCache)."""
+    return _PLANS.get(edge_index, num_nodes)
+
+
+def clear_plan_cache():
+    _PLANS.clear()
 
 
 # ------------------------------------------------------------ weight packing
