@@ -908,6 +908,132 @@ def edgewise_step(ew):
     out.backward(ew["gout"])
 
 
+REF_LAYERS = 4
+
+
+def reference_backbone_workload(dtype_name, seed=0):
+    """The reference's layer loop (helm/esen_osh.py:438-463) on the config-2
+    graph: REF_LAYERS Edgewise modules at its model shape (lmax = mmax = 4,
+    sphere and hidden channels 128, radial [384, 128, 128], training_workflow.py:
+    508-511, run_QM7.py:66-67), called with its signature: the dense wigner and
+    wigner_inv [E, 25, 25] and one edge_index tensor, no plan (the modules find
+    the graph's plan in the cache)."""
+    import numpy as np
+    import torch
+    from maloq_amd.edgewise import Edgewise
+    from maloq_amd.so3 import CoefficientMapping
+    from maloq_amd.wigner import extract_euler_angles, wigner_from_eulers
+    dev = torch.device("cuda:0")
+    dt = {"bf16": torch.bfloat16, "fp32": torch.float32}[dtype_name]
+    g = _graph("config2_graph")
+    L = Mm = 4
+    C = H = 128
+    torch.manual_seed(seed)
+    mods = [Edgewise(C, H, L, Mm, [384, 128, 128], CoefficientMapping(L, Mm), None, 6.0, "source-target").to(dev)
+            for _ in range(REF_LAYERS)]
+    gen = torch.Generator().manual_seed(seed)
+    ei = torch.from_numpy(np.stack([g.src, g.dst])).to(dev)
+    vec = torch.from_numpy(g.edge_distance_vec()).float().to(dev)
+    with torch.no_grad():
+        wig = wigner_from_eulers(extract_euler_angles(vec, seed=3), None, L)
+        wig_inv = wig.transpose(1, 2).contiguous()
+    x = torch.randn(g.num_nodes, (L + 1) ** 2, C, generator=gen).to(dev, dt).requires_grad_()
+    x_edge = torch.randn(g.num_edges, 384, generator=gen).to(dev).requires_grad_()
+    return dict(mods=mods, ei=ei, wig=wig, wig_inv=wig_inv, x=x, x_edge=x_edge, L=L, M=Mm, C=C, H=H,
+                E=g.num_edges, N=g.num_nodes, dt=dt)
+
+
+def reference_backbone_pass(rw, backward=True, cached=True):
+    """The layer loop: x <- x + Edgewise_i(x), then the gradient of a fixed
+    linear loss wrt x, x_edge and every module parameter.  cached=False drops
+    the plan cache before each layer (the plan built per call, as without it)."""
+    import torch
+    from maloq_amd import message as M
+    x = rw["x"]
+    for t in [rw["x"], rw["x_edge"], *[p for m in rw["mods"] for p in m.parameters()]]:
+        t.grad = None
+    with torch.set_grad_enabled(backward):
+        h = x
+        for mod in rw["mods"]:
+            if not cached:
+                M.clear_plan_cache()
+            h = h + mod(h, None, rw["x_edge"], rw["ei"], rw["wig"], rw["wig_inv"], "node").to(h.dtype)
+        if backward:
+            h.float().sum().backward()
+    return h
+
+
+def reference_backbone_leg(dtype_name, steps=5, warmup=2, cpu=True):
+    import torch
+    from maloq_amd import message as M
+    rw = reference_backbone_workload(dtype_name)
+    M.clear_plan_cache()
+    built0 = M._PLANS.built
+    reference_backbone_pass(rw, True)
+    plans_per_pass = M._PLANS.built - built0
+    t_step = time_steps(lambda: reference_backbone_pass(rw, True), steps, warmup)
+    t_fwd = time_steps(lambda: reference_backbone_pass(rw, False), steps, warmup)
+    t_fwd_nc = time_steps(lambda: reference_backbone_pass(rw, False, cached=False), steps, warmup)
+    E, n = rw["E"], REF_LAYERS
+    fl = edgewise_flops_per_edge(rw["L"], rw["M"], rw["C"], rw["H"]) * E * n
+    peak = PEAK_BF16 if dtype_name == "bf16" else PEAK_FP32
+    out = {"metric": "edges/s per layer", "fwd_bwd": E * n / t_step, "fwd": E * n / t_fwd,
+           "fwd_without_plan_cache": E * n / t_fwd_nc, "ms_per_pass_fwd_bwd": t_step * 1e3,
+           "ms_per_pass_fwd": t_fwd * 1e3, "ms_per_pass_fwd_without_plan_cache": t_fwd_nc * 1e3,
+           "plans_built_per_pass": plans_per_pass, "layers": n, "dtype": dtype_name,
+           "config": "config-2 graph (36 804 edges), Edgewise x4 at the reference's model shape: lmax = mmax = 4, "
+                     "C = H = 128, radial [384, 128, 128], dense wigner / wigner_inv, no plan= (reference call)",
+           "roofline": {"scope": "whole forward pass (radial MLPs, Wigner-row gathers, prep, both GEMMs, fixups)",
+                        "bound": "mfma", "achieved": fl / t_fwd / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
+                        "frac": fl / t_fwd / peak, "flops_per_pass": fl}}
+    if cpu:
+        out["cpu_baseline"] = cpu_reference_backbone_baseline(rw)
+    del rw
+    torch.cuda.empty_cache()
+    return out
+
+
+def cpu_reference_backbone_baseline(rw, budget_s=10.0):
+    """The oracle's two-convolution Edgewise (oracle.message.message_block with
+    conv2, concat source-target, fp32 torch on the host cores), one layer forward
+    + backward, on the in-edges of the graph's first nodes, against the module's
+    own weights (radial scales precomputed: the layer's SO(2) work)."""
+    import numpy as np
+    import torch
+    from oracle import message as omsg
+    from oracle import rotation as orot
+    from maloq_amd import message as M
+    from maloq_amd.wigner import extract_euler_angles
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    mod = rw["mods"][0]
+    L, Mm, C, H = rw["L"], rw["M"], rw["C"], rw["H"]
+    g = _graph("config2_graph")
+    sel = torch.from_numpy(g.mol[g.dst] == 0)  # the first molecule's in-edges
+    ei = torch.from_numpy(np.stack([g.src, g.dst]))[:, sel]
+    vec = torch.from_numpy(g.edge_distance_vec()).float()[sel]
+    eul = extract_euler_angles(vec.to("cuda:0"), seed=3).cpu()
+    cpu = lambda t: t.detach().float().cpu()
+    conv = lambda c, co: {"w0": cpu(c.fc_m0.weight).requires_grad_(), "b0": cpu(c.fc_m0.bias).requires_grad_(),
+                          "wm": [cpu(m.fc.weight).requires_grad_() for m in c.so2_m_conv], "c_out": co}
+    c1, c2 = conv(mod.so2_conv_1, H), conv(mod.so2_conv_2, C)
+    x = torch.randn(g.num_nodes, (L + 1) ** 2, C).requires_grad_()
+    rad = (torch.rand(ei.shape[1], M.rad_width(L, Mm, 2 * C)) + 0.5).requires_grad_()
+    jd = orot.load_jd()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 2:
+        t0 = time.perf_counter()
+        out = omsg.message_block(x, ei, (eul[:, 0], eul[:, 1], eul[:, 2]), jd, L, Mm, c1, rad=rad, conv2=c2,
+                                 gate=True, concat="source-target")
+        out.sum().backward()
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[len(times) // 2]
+    return {"value": ei.shape[1] / t, "unit": "edges/s per layer", "cores": cores, "kind": "port",
+            "sample": f"one layer fwd+bwd on the {ei.shape[1]} in-edges of the first molecule (config 2), fp32 "
+                      f"torch, median of {len(times)}"}
+
+
 def torch_randn_like_nodes(ew):
     import torch
     gen = torch.Generator().manual_seed(7)
@@ -974,6 +1100,10 @@ def profile_only(args):
     elif args.only == "basis5":
         sw = sparse_basis_workload()
         sparse_basis_leg(sw, reps=args.reps)
+    elif args.only == "ref-backbone":
+        rw = reference_backbone_workload(args.dtype)
+        for _ in range(args.reps):
+            reference_backbone_pass(rw, True)
     elif args.only == "basis-tzvpd":
         print(json.dumps(wide_basis_leg(reps=args.reps, cpu=False)), flush=True)
     elif args.only in ("fwd", "step"):
@@ -1015,7 +1145,7 @@ def main(argv=None):
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-extras", action="store_true", help="headline only")
     ap.add_argument("--only", choices=["fwd", "step", "basis", "copy", "embed", "edgewise", "edgewise-step",
-                                       "rotate", "basis5", "basis-tzvpd", "ceiling"],
+                                       "rotate", "basis5", "basis-tzvpd", "ref-backbone", "ceiling"],
                     help="profiling mode: run one piece a few times and exit (no JSON line)")
     ap.add_argument("--cfg", default="config2", choices=sorted(MESSAGE_CONFIGS),
                     help="message-block configuration of --only fwd / step")
@@ -1141,6 +1271,10 @@ def main(argv=None):
                          "frac": fl / tg / PEAK_BF16, "flops_per_call": fl},
         }
         del gw
+        for dtn in ("fp32", "bf16"):
+            print(f"[bench] reference layer loop (Edgewise x{REF_LAYERS}, lmax = mmax = 4, {dtn}) ...",
+                  file=sys.stderr, flush=True)
+            result[f"reference_backbone_{dtn}"] = reference_backbone_leg(dtn, cpu=(dtn == "fp32" and not args.no_cpu))
         print("[bench] library GEMM ceiling of the SO(2) shapes ...", file=sys.stderr, flush=True)
         result["library_gemm_ceiling"] = library_gemm_ceiling(("bf16",))
     if not args.no_cpu:
