@@ -273,30 +273,67 @@ __device__ __forceinline__ bool strided_pass(const Smem<TR>& s, int wave, int i0
   return uniform(any) != 0;
 }
 
+// A tile row's rectangle, read once per pass into scalar registers (the row is
+// the same for the whole wave).
+struct RowRect {
+  int64_t base;
+  int cnt, nc, rs, lo;
+  float rnc;
+};
+
+template <int TR>
+__device__ __forceinline__ RowRect row_rect(const Smem<TR>& s, int g) {
+  RowRect r;
+  r.base = uniform64(s.base[g]);
+  r.cnt = uniform(s.cnt[g]);
+  r.nc = uniform(s.nc[g]);
+  r.rs = uniform(s.rs[g]);
+  r.lo = uniform(s.lo[g]);
+  r.rnc = __int_as_float(uniform(__float_as_int(s.rnc[g])));
+  return r;
+}
+
+// Offset of element k of a rectangle from its base (see elem_offset).
+template <bool STRIDED>
+__device__ __forceinline__ int rect_offset(const RowRect& r, int k) {
+  if constexpr (!STRIDED) return k;
+  const int i = static_cast<int>((static_cast<float>(k) + 0.5f) * r.rnc);
+  return i * r.rs + (k - i * r.nc);
+}
+
 // One gather pass: kPassRows rows x 256 rectangle elements, all loads in
-// flight, then dropped into their tile columns.  !STRIDED: every row's
-// rectangle is contiguous (element k at base + k).
+// flight, then dropped into their tile columns.  Every load is issued
+// unconditionally (lanes past a rectangle's end read its first table entry
+// and fock[0], both in bounds), so no branch stands between them.  !STRIDED: every row's rectangle is contiguous (element k at base + k).
 template <int NW, bool STRIDED, int TR>
 __device__ __forceinline__ void gather_pass(const Args& a, const Smem<TR>& s, float* tile, int wave, int lane,
                                             int k0, int i0) {
   float v[kPassRows][4];
-  int dst[kPassRows][4];
+  int col[kPassRows][4];
 #pragma unroll
-  for (int i = 0; i < kPassRows; ++i)
+  for (int i = 0; i < kPassRows; ++i) {
+    const int g = wave + NW * (i0 + i);
+    const RowRect r = row_rect(s, g);
+    const int32_t* slot = a.slots + r.lo;
+    const float* blk = a.fock + r.base;
 #pragma unroll
     for (int ch = 0; ch < 4; ++ch) {
-      const int g = wave + NW * (i0 + i), k = k0 + ch * 64 + lane;
-      const bool ok = k < s.cnt[g];
-      const int col = ok ? a.slots[s.lo[g] + k] : -1;
-      const int off = STRIDED ? elem_offset(s, g, k) : k;
-      v[i][ch] = a.fock[ok ? s.base[g] + off : 0];
-      dst[i][ch] = col >= 0 ? g * a.tp + col : -1;
+      const int k = k0 + ch * 64 + lane;
+      const bool ok = k < r.cnt;
+      const int c = slot[ok ? k : 0];
+      // lanes past the rectangle read fock[0] (a block base may lie past the
+      // matrix when its atom has no orbitals)
+      v[i][ch] = *(ok ? blk + rect_offset<STRIDED>(r, k) : a.fock);
+      col[i][ch] = ok ? c : -1;
     }
+  }
 #pragma unroll
-  for (int i = 0; i < kPassRows; ++i)
+  for (int i = 0; i < kPassRows; ++i) {
+    const int g = wave + NW * (i0 + i);
 #pragma unroll
     for (int ch = 0; ch < 4; ++ch)
-      if (dst[i][ch] >= 0) tile[dst[i][ch]] = v[i][ch];
+      if (col[i][ch] >= 0) tile[g * a.tp + col[i][ch]] = v[i][ch];
+  }
 }
 
 // One scatter pass (the inverse of gather_pass).
@@ -305,24 +342,28 @@ __device__ __forceinline__ void scatter_pass(const Args& a, const Smem<TR>& s, c
                                              int lane, int k0, int i0) {
   int col[kPassRows][4];
 #pragma unroll
-  for (int i = 0; i < kPassRows; ++i)
+  for (int i = 0; i < kPassRows; ++i) {
+    const RowRect r = row_rect(s, wave + NW * (i0 + i));
+    const int32_t* slot = a.slots + r.lo;
 #pragma unroll
     for (int ch = 0; ch < 4; ++ch) {
-      const int g = wave + NW * (i0 + i), k = k0 + ch * 64 + lane;
-      const bool ok = k < uniform(s.cnt[g]);
-      const int32_t* slot = a.slots + uniform(s.lo[g]);
+      const int k = k0 + ch * 64 + lane;
+      const bool ok = k < r.cnt;
       const int c = slot[ok ? k : 0];
       col[i][ch] = ok ? c : -1;
     }
+  }
 #pragma unroll
-  for (int i = 0; i < kPassRows; ++i)
+  for (int i = 0; i < kPassRows; ++i) {
+    const int g = wave + NW * (i0 + i);
+    const RowRect r = row_rect(s, g);
+    float* blk = a.fock + r.base;
 #pragma unroll
     for (int ch = 0; ch < 4; ++ch) {
-      const int g = wave + NW * (i0 + i), k = k0 + ch * 64 + lane;
-      float* blk = a.fock + uniform64(s.base[g]);
-      const int off = STRIDED ? elem_offset(s, g, k) : k;
-      if (col[i][ch] >= 0) blk[off] = tile[g * a.tp + col[i][ch]];
+      const int k = k0 + ch * 64 + lane;
+      if (col[i][ch] >= 0) blk[rect_offset<STRIDED>(r, k)] = tile[g * a.tp + col[i][ch]];
     }
+  }
 }
 
 template <int SIDE, bool PLAN, int TR>

@@ -192,7 +192,7 @@ def _(x, rad, w0, b0, wm, src, dst, seg_ptr, eulers, lmax, mmax, gate):
     E = src.shape[0]
     c_out = w0.shape[0] // (lmax + 1 + (lmax if gate else 0))
     kr = M.kept_rows(lmax, mmax)
-    rows = (E + 127) // 128 * 128 + 1
+    rows = int(_lib.load().maloq_message_edge_rows(E))  # the saved rows' padding, as the forward allocates them
     out = x.new_empty(N, d, c_out, dtype=torch.float32)
     y = x.new_empty(rows, kr, c_in)
     r = x.new_empty(max(E, 1), kr, c_in) if rad is not None else x.new_empty(0)

@@ -34,6 +34,21 @@ def test_opcheck(device):
     seg = torch.cat([torch.zeros(1, dtype=torch.int64, device=device),
                      torch.cumsum(torch.bincount(gather, minlength=9), 0)])
     torch.library.opcheck(ops.segment_sum, (msg, perm, seg, 9), test_utils=("test_schema", "test_faketensor"))
+    # the fused block's forward: its fake gives the saved rows the library's padding
+    from maloq_amd import message as M
+    L, C, E, N = 2, 32, 50, 9
+    ei = torch.stack([torch.randint(0, N, (E,), generator=gen), gather.cpu()]).to(device)
+    plan = M.MessagePlan(ei, N)
+    xm = torch.randn(N, (L + 1) ** 2, C, generator=gen).to(device)
+    w0 = torch.randn((L + 1) * C + L * C, (L + 1) * C, generator=gen).to(device)
+    b0 = torch.randn((L + 1) * C + L * C, generator=gen).to(device)
+    wm = [torch.randn(2 * (L - m + 1) * C, (L - m + 1) * C, generator=gen).to(device) for m in (1, 2)]
+    rad = torch.rand(E, M.rad_width(L, L, C), generator=gen).to(device)
+    for gate in (False, True):
+        w0g, b0g = (w0, b0) if gate else (w0[:(L + 1) * C], b0[:(L + 1) * C])
+        torch.library.opcheck(ops.message_block_fwd,
+                              (xm, rad, w0g, b0g, wm, plan.src, plan.dst, plan.seg_ptr, plan.sort_edges(eul), L, L,
+                               gate), test_utils=("test_schema", "test_faketensor"))
 
 
 @pytest.mark.gpu
