@@ -22,6 +22,10 @@ void set_error(const char* fmt, ...);
 // Returns MALOQ_EHIP (and records the message) if the last launch failed.
 int check_launch(const char* what);
 
+// Compute units of the current device (queried once per device; 256 if the
+// query fails).
+int device_cus();
+
 __device__ __forceinline__ float bf16_to_f32(uint16_t v) {
   return __uint_as_float(static_cast<uint32_t>(v) << 16);
 }

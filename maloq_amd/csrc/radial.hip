@@ -1142,15 +1142,8 @@ static int dwo_splits(const Args& a) {
 static int64_t ntiles_of(int64_t E) { return (E + TE - 1) / TE; }
 // Workgroups of the persistent kernels: one per compute unit, at most one per tile.
 static int persistent_grid(int64_t ntiles) {
-  static int cus[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev] = n;
-  }
-  return static_cast<int>(ntiles < cus[dev] ? ntiles : cus[dev]);
+  const int cus = device_cus();
+  return static_cast<int>(ntiles < cus ? ntiles : cus);
 }
 static int rgroups(int64_t nparts) { return static_cast<int>((nparts + RGROUP - 1) / RGROUP); }
 
