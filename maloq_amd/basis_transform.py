@@ -436,6 +436,7 @@ class HipE3TensorDecomp:
             None if (self.cg_programs[d] >= 0).all() else w for d, w in enumerate(
                 (self._w_fwd, self._w_inv, self._w_adj)))
         self._perm = _i32(self.sort_perm, dev) if self.sort_perm is not None else None
+        self._perm_inv = None
         if self._perm is not None and self.ngroups > 1:
             # rows of several column groups are permuted by a separate column
             # gather: sorted <- unsorted (perm) and unsorted <- sorted (inverse)
@@ -474,15 +475,13 @@ class HipE3TensorDecomp:
         return None, None, perm_in is not None, perm_out is not None
 
     def _transform(self, x, blocks, w, perm_in=None, perm_out=None):
-        x = x.contiguous()
-        perm_in, perm_out, pre, post = self._split_perms(perm_in, perm_out)
-        if pre:
-            x = self._permute(x, self._perm_inv)
-        out = torch.empty_like(x)
-        _lib.call("maloq_label_transform", _lib.ptr(x), _lib.ptr(perm_in), _lib.ptr(out), _lib.ptr(perm_out),
-                  x.shape[0], x.shape[1], self.num_blocks, _lib.ptr(blocks), _lib.ptr(w),
-                  _lib.ptr(self._sched), *self._layout(), _lib.stream_of(x.device))
-        return self._permute(out, self._perm) if post else out
+        """The registered operator maloq_hip::label_transform (the C++
+        extension): for rows of several column groups it un-sorts the input
+        through the inverse permutation and sorts the output after the kernel."""
+        from .ops import label_transform
+        with torch.no_grad():  # differentiable through _GetH only, like the tables it is given
+            return label_transform(x, blocks, w, self._sched, perm_in, perm_out, self.num_blocks, self.ngroups,
+                                   self.group_cols, self._perm_inv)
 
     def _get_H_impl(self, net_out):
         self._check(net_out, self.total_in_dim)

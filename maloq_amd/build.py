@@ -1,8 +1,9 @@
-"""Builds libmaloq_hip.so (all HIP kernels + the C ABI) in-tree for gfx950.
+"""Builds libmaloq_hip.so (all HIP kernels + the C ABI) in-tree for gfx950,
+then the PyTorch operator layer _maloq_torch.so (a C++ extension over it).
 
 Usage: python -m maloq_amd.build   (or __graft_entry__.build()).
-Each .hip file is compiled to an object in parallel, then linked; the result
-is maloq_amd/libmaloq_hip.so next to this file.
+Each .hip file is compiled to an object in parallel, then linked; the results
+are maloq_amd/libmaloq_hip.so and maloq_amd/_maloq_torch.so next to this file.
 """
 from __future__ import annotations
 
@@ -18,6 +19,11 @@ CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libmaloq_hip.so")
 BUILD_DIR = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+# The PyTorch operator layer (torch_ops.cpp): a C++ extension built with g++
+# against torch's headers, linking libmaloq_hip.so.
+TORCH_SRC = os.path.join(CSRC, "torch_ops.cpp")
+TORCH_EXT = os.path.join(HERE, "_maloq_torch.so")
+CXX = os.environ.get("CXX", "g++")
 
 FLAGS = [
     "--offload-arch=gfx950",
@@ -87,6 +93,32 @@ def build(verbose: bool = True, incremental: bool = False) -> str:
     return OUT
 
 
+def build_torch_ext(verbose: bool = True, incremental: bool = False) -> str:
+    """Compile the operator layer into maloq_amd/_maloq_torch.so (after the
+    HIP library, which it links)."""
+    if incremental and os.path.exists(TORCH_EXT) and os.path.getmtime(TORCH_EXT) >= _deps_mtime(TORCH_SRC):
+        return TORCH_EXT
+    import torch
+
+    tdir = os.path.dirname(torch.__file__)
+    inc = [os.path.join(tdir, "include"), os.path.join(tdir, "include", "torch", "csrc", "api", "include")]
+    libdir = os.path.join(tdir, "lib")
+    tmp = TORCH_EXT + ".tmp"
+    cmd = [CXX, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wno-unused-function",
+           "-D__HIP_PLATFORM_AMD__", "-DUSE_ROCM", f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+           *[f"-I{p}" for p in inc], "-I/opt/rocm/include", TORCH_SRC, "-o", tmp,
+           f"-L{HERE}", "-lmaloq_hip", f"-L{libdir}", "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch_hip", "-ltorch",
+           "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{libdir}"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"torch extension build failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, TORCH_EXT)
+    if verbose:
+        print(f"built {TORCH_EXT}", flush=True)
+    return TORCH_EXT
+
+
 if __name__ == "__main__":
     build(incremental="--incremental" in sys.argv)
+    build_torch_ext(incremental="--incremental" in sys.argv)
     sys.exit(0)

@@ -1,18 +1,19 @@
-"""PyTorch custom ops (namespace ``maloq_hip``) over the C ABI.
+"""PyTorch custom ops (namespace ``maloq_hip``) of the HIP path.
 
-The reference's hot path is PyTorch code, so its replacement is exposed to
-PyTorch's dispatcher as registered operators rather than opaque Python calls:
-``torch.compile`` and other graph capture see them as single ops with known
-output shapes (each has a fake implementation), and autograd goes through the
-registered backward formulas.  Each op enqueues HIP kernels of
-``libmaloq_hip.so`` on the current stream; there is no CPU implementation.
+The operators are defined and implemented in C++ (``csrc/torch_ops.cpp``,
+built into ``_maloq_torch.so``, a thin extension over ``libmaloq_hip.so``):
+each checks its arguments, allocates its outputs and calls the C ABI on the
+current HIP stream; there is no CPU implementation.  This module loads the
+extension and registers, from Python, each operator's fake (meta)
+implementation, so that ``torch.compile`` and other graph capture see single
+ops with known output shapes, and the autograd formulas.
 
     maloq_hip::edge_euler(edge_vec, seed)                 extract_euler_angles
     maloq_hip::wigner_from_euler(eulers, lmax, inverse)   eulers_to_wigner (dense D or D^T)
     maloq_hip::rotate(x, eulers, gather?, lmax, inverse)  bmm(wigner, x[src]) / bmm(wigner_inv, z)
     maloq_hip::segment_sum(msg, perm, seg_ptr, n)         index_add_ in a fixed order
     maloq_hip::label_transform(x, ..)                     get_net_out / get_H on label rows
-    maloq_hip::message_block(x, rad?, w0, b0?, wm, plan tensors, eulers, lmax, mmax, gate)
+    maloq_hip::message_block_fwd(x, rad?, w0, b0?, wm, plan tensors, eulers, lmax, mmax, gate)
                                                           Edgewise.forward_node with one convolution
 
 Reference interfaces: helm/triton_kernels/wigner_fused.py:383-486,
@@ -21,33 +22,38 @@ fock_utils/utils_tensor_decomp.py:154-169.
 """
 from __future__ import annotations
 
-from typing import List, Optional
+import os
 
 import torch
 from torch import Tensor
-from torch.library import custom_op, register_fake
+from torch.library import register_autograd, register_fake
 
 from . import _lib
 from . import message as M
 from .rotate import _scatter_rows, rotate as _rotate
 
+EXT_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_maloq_torch.so")
+
+
+def _load_extension():
+    if not os.path.exists(EXT_PATH):
+        raise _lib.MaloqHipError(f"{EXT_PATH} is missing: build it with `python -m maloq_amd.build` "
+                                 "(the operators have no Python implementation)")
+    _lib.load()  # the HIP library the extension links, loaded once
+    torch.ops.load_library(EXT_PATH)
+
+
+_load_extension()
+_ops = torch.ops.maloq_hip
 
 # ------------------------------------------------------------------ Wigner
-@custom_op("maloq_hip::edge_euler", mutates_args=())
-def edge_euler(edge_vec: Tensor, seed: int) -> Tensor:
-    from .wigner import extract_euler_angles
-    return extract_euler_angles(edge_vec, seed)
+edge_euler = _ops.edge_euler
+wigner_from_euler = _ops.wigner_from_euler
 
 
 @register_fake("maloq_hip::edge_euler")
 def _(edge_vec, seed):
     return edge_vec.new_empty(edge_vec.shape[0], 3)
-
-
-@custom_op("maloq_hip::wigner_from_euler", mutates_args=())
-def wigner_from_euler(eulers: Tensor, lmax: int, inverse: bool) -> Tensor:
-    from .wigner import wigner_from_eulers
-    return wigner_from_eulers(eulers, None, lmax, inverse=inverse)
 
 
 @register_fake("maloq_hip::wigner_from_euler")
@@ -57,9 +63,7 @@ def _(eulers, lmax, inverse):
 
 
 # ---------------------------------------------------------------- rotation
-@custom_op("maloq_hip::rotate", mutates_args=())
-def rotate(x: Tensor, eulers: Tensor, gather: Optional[Tensor], lmax: int, inverse: bool) -> Tensor:
-    return _rotate(x, lmax, eulers=eulers, gather=gather, inverse=inverse)
+rotate = _ops.rotate
 
 
 @register_fake("maloq_hip::rotate")
@@ -80,20 +84,11 @@ def _rotate_backward(ctx, grad):
     return gx.to(ctx.x_dtype), None, None, None, None
 
 
-rotate.register_autograd(_rotate_backward, setup_context=_rotate_setup)
+register_autograd("maloq_hip::rotate", _rotate_backward, setup_context=_rotate_setup)
 
 
 # ------------------------------------------------------------ segment sum
-@custom_op("maloq_hip::segment_sum", mutates_args=())
-def segment_sum(msg: Tensor, perm: Tensor, seg_ptr: Tensor, num_segments: int) -> Tensor:
-    _lib.require_cuda(msg, perm, seg_ptr)
-    m = msg.float().contiguous()
-    out = torch.empty((num_segments,) + tuple(msg.shape[1:]), device=msg.device, dtype=torch.float32)
-    width = m[0].numel() if m.shape[0] > 0 else int(torch.tensor(msg.shape[1:]).prod())
-    perm_d, seg_d = perm.long().contiguous(), seg_ptr.long().contiguous()   # alive across the launch
-    _lib.call("maloq_segment_sum", _lib.ptr(m), _lib.ptr(perm_d), _lib.ptr(seg_d), num_segments, width,
-              _lib.ptr(out), _lib.stream_of(msg.device))
-    return out
+segment_sum = _ops.segment_sum
 
 
 @register_fake("maloq_hip::segment_sum")
@@ -102,35 +97,7 @@ def _(msg, perm, seg_ptr, num_segments):
 
 
 # --------------------------------------------------------- basis transform
-@custom_op("maloq_hip::label_transform", mutates_args=())
-def label_transform(x: Tensor, blocks: Tensor, w: Optional[Tensor], sched: Tensor, perm_in: Optional[Tensor],
-                    perm_out: Optional[Tensor], num_blocks: int, ngroups: int, group_cols: int,
-                    perm_inv: Optional[Tensor]) -> Tensor:
-    """Rows of several column groups (``ngroups`` > 1) are permuted by a
-    separate column gather: the input through ``perm_inv`` (the inverse of
-    ``perm_in``), the output through ``perm_out``."""
-    _lib.require_cuda(x)
-    xc = x.contiguous()
-    pre = ngroups > 1 and perm_in is not None
-    post = ngroups > 1 and perm_out is not None
-    if pre or post:
-        ones = torch.ones(xc.shape[1], device=xc.device, dtype=torch.float32)
-
-    def gather(y, src):
-        o = torch.empty_like(y)
-        _lib.call("maloq_gather_columns", _lib.ptr(y), y.shape[1], y.shape[0], _lib.ptr(src), _lib.ptr(ones),
-                  y.shape[1], _lib.ptr(o), o.shape[1], _lib.stream_of(y.device))
-        return o
-
-    if pre:
-        if perm_inv is None:
-            raise ValueError("rows of several column groups need the inverse input permutation")
-        xc = gather(xc, perm_inv)
-    out = torch.empty_like(xc)
-    _lib.call("maloq_label_transform", _lib.ptr(xc), _lib.ptr(None if pre else perm_in), _lib.ptr(out),
-              _lib.ptr(None if post else perm_out), xc.shape[0], xc.shape[1], num_blocks, _lib.ptr(blocks),
-              _lib.ptr(w), _lib.ptr(sched), ngroups, group_cols, _lib.stream_of(x.device))
-    return gather(out, perm_out) if post else out
+label_transform = _ops.label_transform
 
 
 @register_fake("maloq_hip::label_transform")
@@ -172,18 +139,9 @@ class _GetHOp(torch.autograd.Function):
 
 
 # ----------------------------------------------------------- message block
-@custom_op("maloq_hip::message_block_fwd", mutates_args=())
-def message_block_fwd(x: Tensor, rad: Optional[Tensor], w0: Tensor, b0: Optional[Tensor], wm: List[Tensor],
-                      src: Tensor, dst: Tensor, seg_ptr: Tensor, eulers: Tensor, lmax: int, mmax: int,
-                      gate: bool) -> List[Tensor]:
-    """Node output and the workspaces the backward reads: [out, y, r, dk, g]
-    (r empty without radial scales, g empty ungated)."""
-    plan = _PlanView(src, dst, seg_ptr, x.shape[0])
-    saved = {}
-    out = M.message_forward(x, plan, eulers, rad, w0, b0, list(wm), lmax, mmax, gate=gate, save=saved)
-    empty = x.new_empty(0)
-    return [out, saved["y"], saved["r"] if saved["r"] is not None else empty, saved["dk"],
-            saved["g"] if saved["g"] is not None else empty]
+# Node output and the workspaces the backward reads: [out, y, r, dk, g]
+# (r empty without radial scales, g empty ungated).
+message_block_fwd = _ops.message_block_fwd
 
 
 @register_fake("maloq_hip::message_block_fwd")
@@ -199,15 +157,6 @@ def _(x, rad, w0, b0, wm, src, dst, seg_ptr, eulers, lmax, mmax, gate):
     dk = x.new_empty(max(E, 1), M.wigner_floats(lmax, mmax), dtype=torch.float32)
     g = x.new_empty(max(E, 1), kr + lmax, c_out) if gate else x.new_empty(0)
     return [out, y, r, dk, g]
-
-
-class _PlanView:
-    """The tensors of a MessagePlan the forward kernels read."""
-
-    def __init__(self, src, dst, seg_ptr, num_nodes):
-        self.src, self.dst, self.seg_ptr = src, dst, seg_ptr
-        self.num_nodes, self.num_edges = int(seg_ptr.shape[0]) - 1, int(src.shape[0])
-        self.perm = None
 
 
 def message_block(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=False):
