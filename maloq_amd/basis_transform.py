@@ -393,6 +393,12 @@ class _GetH(torch.autograd.Function):
         return ctx.obj._get_H_adjoint(grad.contiguous()), None
 
 
+def _ops():
+    """The C++ operators (maloq_amd.ops loads the extension on first use)."""
+    from . import ops
+    return ops
+
+
 class HipE3TensorDecomp:
     """``group_cols``: the widest column group of the kernels' tiles (rows wider
     than that are split into groups of whole CG blocks; one group when the row
@@ -478,10 +484,9 @@ class HipE3TensorDecomp:
         """The registered operator maloq_hip::label_transform (the C++
         extension): for rows of several column groups it un-sorts the input
         through the inverse permutation and sorts the output after the kernel."""
-        from .ops import label_transform
         with torch.no_grad():  # differentiable through _GetH only, like the tables it is given
-            return label_transform(x, blocks, w, self._sched, perm_in, perm_out, self.num_blocks, self.ngroups,
-                                   self.group_cols, self._perm_inv)
+            return _ops().label_transform(x, blocks, w, self._sched, perm_in, perm_out, self.num_blocks,
+                                          self.ngroups, self.group_cols, self._perm_inv)
 
     def _get_H_impl(self, net_out):
         self._check(net_out, self.total_in_dim)
@@ -531,10 +536,7 @@ class HipE3TensorDecomp:
         off, Z, r_, c_ = (_i32(x, dev) for x in (fock_block_offsets, atomic_numbers, rows, cols))
         ld, bdo = self._storage(fock, block_data_offsets)
         R = int(r_.shape[0])
-        meta = torch.empty(max(R, 1), 4, device=dev, dtype=torch.int32)
-        _lib.call("maloq_basis_row_meta", ld, _lib.ptr(bdo), _lib.ptr(off), _lib.ptr(Z), _lib.ptr(r_),
-                  _lib.ptr(c_), R, _lib.ptr(tabs["pair_kind"]), tabs["maxe"], _lib.ptr(meta),
-                  _lib.stream_of(dev))
+        meta = _ops().basis_row_meta(ld, bdo, off, Z, r_, c_, tabs["pair_kind"], tabs["maxe"])
         return BasisPlan(meta, R, ld, id(orbital_template))
 
     def _plan_for(self, plan, fock, fock_block_offsets, atomic_numbers, rows, cols, orbital_template,
@@ -574,22 +576,18 @@ class HipE3TensorDecomp:
         if plan is None:
             ld, bdo, off, Z, r_, c_ = self._pairs(fock, fock_block_offsets, atomic_numbers, rows, cols,
                                                  block_data_offsets)
-            R = int(r_.shape[0])
-            out = torch.empty(R, self.total_in_dim, device=fock.device, dtype=torch.float32)
-            _lib.call("maloq_fock_to_irreps_pairs", _lib.ptr(fock), ld, _lib.ptr(bdo), _lib.ptr(off), _lib.ptr(Z),
-                      _lib.ptr(r_), _lib.ptr(c_), R, _lib.ptr(tabs["pair_kind"]), _lib.ptr(tabs["slots"]),
-                      tabs["maxe"], _lib.ptr(tabs["kind_blocks"]), _lib.ptr(out), _lib.ptr(perm_out),
-                      self.total_in_dim, self.num_blocks, _lib.ptr(self._blocks_fwd), _lib.ptr(self._wk_fwd),
-                      _lib.ptr(self._sched), *self._layout(), _lib.stream_of(fock.device))
+            meta, R = None, int(r_.shape[0])
         else:
             plan = self._plan_for(plan, fock, fock_block_offsets, atomic_numbers, rows, cols, orbital_template,
                                   block_data_offsets)
-            out = torch.empty(plan.num_rows, self.total_in_dim, device=fock.device, dtype=torch.float32)
-            _lib.call("maloq_fock_to_irreps", _lib.ptr(fock), plan.ld, _lib.ptr(plan.meta), plan.num_rows,
-                      _lib.ptr(tabs["slots"]), tabs["maxe"], _lib.ptr(tabs["kind_blocks"]), _lib.ptr(out),
-                      _lib.ptr(perm_out), self.total_in_dim, self.num_blocks, _lib.ptr(self._blocks_fwd),
-                      _lib.ptr(self._wk_fwd), _lib.ptr(self._sched), *self._layout(), _lib.stream_of(fock.device))
-        return self._permute(out, self._perm) if post else out
+            ld, bdo, off, Z, r_, c_ = plan.ld, None, None, None, None, None
+            meta, R = plan.meta, plan.num_rows
+        with torch.no_grad():
+            return _ops().fock_to_irreps(fock, ld, bdo, off, Z, r_, c_, meta, R, tabs["pair_kind"],
+                                         tabs["slots"], tabs["maxe"], tabs["kind_blocks"], perm_out,
+                                         self.total_in_dim, self.num_blocks, self._blocks_fwd, self._wk_fwd,
+                                         self._sched, self.ngroups, self.group_cols,
+                                         self._perm if post else None)
 
     def irreps_to_fock(self, net_out, fock, fock_block_offsets, atomic_numbers, rows, cols,
                        orbital_template, block_data_offsets=None, plan=None):
@@ -599,30 +597,23 @@ class HipE3TensorDecomp:
         self._check(net_out, self.total_in_dim)
         _lib.require_cuda(fock)
         tabs = self._template_tables(orbital_template)
-        net_out = net_out.contiguous()
         perm_in, _, pre, _ = self._split_perms(self._perm, None)
-        if pre:
-            net_out = self._permute(net_out, self._perm_inv)
         if plan is None:
             ld, bdo, off, Z, r_, c_ = self._pairs(fock, fock_block_offsets, atomic_numbers, rows, cols,
                                                  block_data_offsets)
-            R = int(r_.shape[0])
-            if R != net_out.shape[0]:
-                raise ValueError("net_out rows must match the atom-pair list")
-            _lib.call("maloq_irreps_to_fock_pairs", _lib.ptr(net_out), _lib.ptr(perm_in), _lib.ptr(fock), ld,
-                      _lib.ptr(bdo), _lib.ptr(off), _lib.ptr(Z), _lib.ptr(r_), _lib.ptr(c_), R,
-                      _lib.ptr(tabs["pair_kind"]), _lib.ptr(tabs["slots"]), tabs["maxe"],
-                      _lib.ptr(tabs["kind_blocks"]), self.total_in_dim, self.num_blocks, _lib.ptr(self._blocks_inv),
-                      _lib.ptr(self._wk_inv), _lib.ptr(self._sched), *self._layout(), _lib.stream_of(fock.device))
-            return fock
-        plan = self._plan_for(plan, fock, fock_block_offsets, atomic_numbers, rows, cols, orbital_template,
-                              block_data_offsets)
-        if plan.num_rows != net_out.shape[0]:
+            meta, R = None, int(r_.shape[0])
+        else:
+            plan = self._plan_for(plan, fock, fock_block_offsets, atomic_numbers, rows, cols, orbital_template,
+                                  block_data_offsets)
+            ld, bdo, off, Z, r_, c_ = plan.ld, None, None, None, None, None
+            meta, R = plan.meta, plan.num_rows
+        if R != net_out.shape[0]:
             raise ValueError("net_out rows must match the atom-pair list")
-        _lib.call("maloq_irreps_to_fock", _lib.ptr(net_out), _lib.ptr(perm_in), _lib.ptr(fock), plan.ld,
-                  _lib.ptr(plan.meta), plan.num_rows, _lib.ptr(tabs["slots"]), tabs["maxe"],
-                  _lib.ptr(tabs["kind_blocks"]), self.total_in_dim, self.num_blocks, _lib.ptr(self._blocks_inv),
-                  _lib.ptr(self._wk_inv), _lib.ptr(self._sched), *self._layout(), _lib.stream_of(fock.device))
+        with torch.no_grad():
+            _ops().irreps_to_fock(net_out, fock, ld, bdo, off, Z, r_, c_, meta, R, tabs["pair_kind"], tabs["slots"],
+                                  tabs["maxe"], tabs["kind_blocks"], perm_in, self.total_in_dim, self.num_blocks,
+                                  self._blocks_inv, self._wk_inv, self._sched, self.ngroups, self.group_cols,
+                                  self._perm_inv if pre else None)
         return fock
 
 

@@ -15,13 +15,21 @@
 //   label_transform(x, ...)                      get_net_out / get_H, utils_tensor_decomp.py:154-169
 //   message_block_fwd(x, rad?, w0, b0?, wm, ...) Edgewise.forward_node with one SO(2)
 //                                                convolution, esen_block.py:146-208
+//   message_block_bwd(grad_out, ...)             its autograd backward (so2_layers.py:139-214)
+//   basis_row_meta(...)                          the row plan of the fused Fock transforms
+//   fock_to_irreps(fock, ...)                    matrix2label + get_net_out,
+//                                                fock_targets_batched.py:335-464
+//   irreps_to_fock(net_out, fock!, ...)          get_H + label2matrix (in place),
+//                                                splittrainer.py:1172-1233
 // Private helpers (CPU): _jd_table(), _pack_index(...) expose the tables the
 // operators build, for tests.
 #include <ATen/ATen.h>
+#include <ATen/hip/HIPContextLight.h>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <map>
 #include <mutex>
@@ -386,6 +394,287 @@ std::vector<at::Tensor> message_block_fwd(const at::Tensor& x, const c10::option
   return {out, y, r, dk, g};
 }
 
+// Saved rows of the bf16 weight gradient: rows past E are zero (it reads whole
+// 128-edge chunks).
+at::Tensor edge_rows(int64_t E, int64_t rows, int64_t c, const at::TensorOptions& opt) {
+  const int64_t n = maloq_message_edge_rows(E);
+  at::Tensor t = at::empty({n, rows, c}, opt);
+  if (n > E) t.narrow(0, E, n - E).zero_();
+  return t;
+}
+
+at::Tensor pack_weights(int code, int64_t lmax, int64_t mmax, bool gate, int64_t c_in, int64_t c_out, int mode,
+                        const at::Tensor& w0, at::TensorList wm, at::ScalarType dt) {
+  int64_t total = 0;
+  const at::Tensor& idx = pack_index_on(code, static_cast<int>(lmax), static_cast<int>(mmax), gate,
+                                        static_cast<int>(c_in), static_cast<int>(c_out), mode, w0.device(), &total);
+  std::vector<at::Tensor> srcs{w0.detach().to(at::kFloat).contiguous()};
+  for (int64_t m = 0; m < mmax; ++m) srcs.push_back(wm[m].detach().to(at::kFloat).contiguous());
+  int64_t have = 0;
+  std::vector<const float*> sp;
+  std::vector<int64_t> sn;
+  for (const auto& t : srcs) {
+    have += t.numel();
+    sp.push_back(t.data_ptr<float>());
+    sn.push_back(t.numel());
+  }
+  TORCH_CHECK_VALUE(have == total, "weight shapes do not match (lmax, mmax, channels)");
+  const int64_t c_k = mode == 0 ? c_in : c_out, c_n = mode == 0 ? c_out : c_in;
+  const int64_t want = maloq_message_wpack_bytes(code, static_cast<int>(lmax), static_cast<int>(mmax), gate,
+                                                 static_cast<int>(c_k), static_cast<int>(c_n));
+  at::Tensor wpack = at::empty({idx.numel()}, w0.options().dtype(dt));
+  TORCH_CHECK(wpack.numel() * wpack.element_size() == want, "packed weight size mismatch");
+  check_rc(maloq_message_pack(code, static_cast<int>(sp.size()), sp.data(), sn.data(), idx.data_ptr<int64_t>(),
+                              idx.numel(), wpack.data_ptr(), stream_of(w0)),
+           "maloq_message_pack");
+  return wpack;
+}
+
+// Split-K count of the weight gradient over the edges (deterministic: the
+// partials are summed in split order).  bf16: 256 x 256 output tiles, one
+// workgroup per CU, the most splits that keep every workgroup in one round;
+// fp32: 128 x 128 tiles, the count that balances the workgroups over the CUs
+// (at most three per CU, >= 1024 edges per split).
+int dw_splits(bool bf16, int64_t lmax, int64_t mmax, bool gate, int64_t c_out, int64_t c_in, int64_t E, int cus) {
+  std::vector<std::pair<int64_t, int64_t>> groups{{lmax + 1, lmax + 1}};
+  for (int64_t m = 1; m <= mmax; ++m) groups.emplace_back(2 * (lmax - m + 1), 2 * (lmax - m + 1));
+  if (gate) groups.emplace_back(lmax, lmax + 1);
+  auto cdiv = [](int64_t a, int64_t b) { return (a + b - 1) / b; };
+  int64_t ntiles = 0;
+  const int64_t tile = bf16 ? 256 : 128;
+  for (const auto& g : groups) ntiles += cdiv(g.first * c_out, tile) * cdiv(g.second * c_in, tile);
+  if (bf16) return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>({64, cus / ntiles, cdiv(E, 128)})));
+  int best = 1;
+  double best_cost = 0;
+  bool have = false;
+  for (int s = 1; s <= 16; ++s) {
+    if (ntiles * s > 3 * cus || s > std::max<int64_t>(1, E / 1024)) continue;
+    const double cost = static_cast<double>(cdiv(ntiles * s, cus)) / s;
+    // ties go to the larger split count
+    if (!have || cost < best_cost || (cost == best_cost && s > best)) {
+      best = s;
+      best_cost = cost;
+      have = true;
+    }
+  }
+  return best;
+}
+
+// Gradients of message_block_fwd from its saved rows: [grad_x fp32 [N, d, c_in],
+// grad_rad (empty unless asked), dW0, db0, dW_1 .. dW_mmax] (fp32).  The
+// graph arrives as the plan's source-sorted arrays: bwd_src, bwd_dst,
+// bwd_eidx (dst-sorted position of each source-sorted edge), seg_ptr_src.
+std::vector<at::Tensor> message_block_bwd(const at::Tensor& grad_out, const c10::optional<at::Tensor>& rad,
+                                          const at::Tensor& w0, at::TensorList wm, const at::Tensor& bwd_src,
+                                          const at::Tensor& bwd_dst, const at::Tensor& bwd_eidx,
+                                          const at::Tensor& seg_ptr_src, const at::Tensor& y, const at::Tensor& dk,
+                                          const c10::optional<at::Tensor>& r, const c10::optional<at::Tensor>& g,
+                                          int64_t num_nodes, int64_t c_in, int64_t lmax, int64_t mmax, bool gate,
+                                          bool need_rad_grad) {
+  const auto dt = y.scalar_type();
+  const int code = dtype_code(dt);
+  require_gpu(grad_out, "grad_out");
+  require_gpu(y, "y");
+  require_gpu(dk, "dk");
+  TORCH_CHECK_VALUE(maloq_message_supported(static_cast<int>(lmax), static_cast<int>(mmax)),
+                    "no message kernels for lmax=", lmax, ", mmax=", mmax);
+  const int64_t d = (lmax + 1) * (lmax + 1);
+  TORCH_CHECK_VALUE(grad_out.dim() == 3 && grad_out.size(1) == d, "grad_out must be [N, (lmax+1)^2, c_out]");
+  TORCH_CHECK_VALUE(bwd_src.scalar_type() == at::kInt && bwd_dst.scalar_type() == at::kInt &&
+                        bwd_eidx.scalar_type() == at::kInt && seg_ptr_src.scalar_type() == at::kLong,
+                    "the plan's source-sorted arrays must be int32 and seg_ptr_src int64");
+  TORCH_CHECK_VALUE(static_cast<int64_t>(wm.size()) >= mmax, "wm needs mmax weights");
+  TORCH_CHECK_VALUE(!gate || (g.has_value() && g->numel() > 0),
+                    "the gated backward needs the forward's pre-activation rows");
+  const c10::DeviceGuard guard(grad_out.device());
+  const int64_t c_out = grad_out.size(2), E = bwd_src.size(0);
+  const int kr = maloq_message_kept_rows(static_cast<int>(lmax), static_cast<int>(mmax));
+  const auto opt32 = grad_out.options().dtype(at::kFloat);
+  void* st = stream_of(grad_out);
+  // input gradient (and the radial gradient)
+  const at::Tensor wpack_t = pack_weights(code, lmax, mmax, gate, c_in, c_out, 1, w0, wm, dt);
+  at::Tensor gx = at::empty({num_nodes, d, c_in}, opt32);
+  const int64_t pf = maloq_message_partials_floats(static_cast<int>(lmax), gate ? 1 : 0, E, static_cast<int>(c_in));
+  at::Tensor parts = at::empty({pf > 1 ? pf : 1}, opt32);
+  at::Tensor radc, grad_rad = at::empty({0}, opt32);
+  if (rad.has_value()) {
+    radc = rad->to(dt).contiguous();
+    if (need_rad_grad) grad_rad = at::empty_like(radc);
+  }
+  at::Tensor dz = edge_rows(E, kr + (gate ? lmax : 0), c_out, y.options());
+  const at::Tensor gq = grad_out.to(at::kFloat).contiguous();
+  const bool has_r = r.has_value() && r->numel() > 0;
+  check_rc(maloq_message_bwd_dx(code, static_cast<int>(lmax), static_cast<int>(mmax), gate ? 1 : 0,
+                                gq.data_ptr<float>(), static_cast<int>(c_out), bwd_dst.data_ptr<int32_t>(),
+                                bwd_src.data_ptr<int32_t>(), bwd_eidx.data_ptr<int32_t>(), E, dk.data_ptr<float>(),
+                                radc.defined() ? radc.data_ptr() : nullptr,
+                                grad_rad.numel() ? grad_rad.data_ptr() : nullptr, has_r ? r->data_ptr() : nullptr,
+                                wpack_t.data_ptr(), jd_on(grad_out.device()), gx.data_ptr<float>(), num_nodes,
+                                static_cast<int>(c_in), seg_ptr_src.data_ptr<int64_t>(), parts.data_ptr<float>(),
+                                dz.data_ptr(), gate ? g->data_ptr() : nullptr, st),
+           "maloq_message_bwd_dx");
+  // weight and bias gradients
+  const int64_t extra = gate ? lmax * c_out : 0;
+  at::Tensor dw0, db0;
+  std::vector<at::Tensor> dwm;
+  if (E == 0) {
+    dw0 = at::zeros({extra + (lmax + 1) * c_out, (lmax + 1) * c_in}, opt32);
+    for (int64_t m = 1; m <= mmax; ++m) dwm.push_back(at::zeros({2 * (lmax - m + 1) * c_out, (lmax - m + 1) * c_in}, opt32));
+    db0 = at::zeros({extra + (lmax + 1) * c_out}, opt32);
+  } else {
+    if (dt == at::kBFloat16)
+      TORCH_CHECK(dz.size(0) >= maloq_message_edge_rows(E) && y.size(0) == dz.size(0),
+                  "bf16 weight gradient needs the padded workspaces");
+    const int cus = at::cuda::getDeviceProperties(grad_out.device().index())->multiProcessorCount;
+    const int splits = dw_splits(dt == at::kBFloat16, lmax, mmax, gate, c_out, c_in, E, cus);
+    const int64_t dp = maloq_message_dw_partials_floats(static_cast<int>(lmax), static_cast<int>(mmax), gate ? 1 : 0,
+                                                        static_cast<int>(c_out), static_cast<int>(c_in), splits);
+    at::Tensor dparts = at::empty({dp > 1 ? dp : 1}, opt32);
+    dw0 = at::empty({extra + (lmax + 1) * c_out, (lmax + 1) * c_in}, opt32);
+    std::vector<float*> dptr;
+    for (int64_t m = 1; m <= mmax; ++m) {
+      dwm.push_back(at::empty({2 * (lmax - m + 1) * c_out, (lmax - m + 1) * c_in}, opt32));
+      dptr.push_back(dwm.back().data_ptr<float>());
+    }
+    if (dptr.empty()) dptr.push_back(nullptr);
+    check_rc(maloq_message_dw(code, static_cast<int>(lmax), static_cast<int>(mmax), gate ? 1 : 0, dz.data_ptr(),
+                              y.data_ptr(), E, static_cast<int>(c_out), static_cast<int>(c_in), splits,
+                              dparts.data_ptr<float>(), dw0.data_ptr<float>(), dptr.data(), st),
+             "maloq_message_dw");
+    db0 = at::empty({extra + (lmax + 1) * c_out}, opt32);
+    const int rpe = static_cast<int>(dz.size(1));
+    // (first row, rows, output offset): the m = 0 rows, then a gated block's gate rows
+    std::vector<std::tuple<int, int, int64_t>> groups{{0, static_cast<int>(lmax + 1), extra}};
+    if (gate) groups.emplace_back(kr, static_cast<int>(lmax), 0);
+    int64_t cs_n = 1;
+    for (const auto& gr : groups)
+      cs_n = std::max(cs_n, maloq_message_colsum_partials_floats(std::get<1>(gr), static_cast<int>(c_out), E));
+    at::Tensor cs = at::empty({cs_n}, opt32);
+    for (const auto& gr : groups)
+      check_rc(maloq_message_colsum(code, dz.data_ptr(), rpe, std::get<0>(gr), std::get<1>(gr), static_cast<int>(c_out),
+                                    E, cs.data_ptr<float>(), db0.data_ptr<float>() + std::get<2>(gr), st),
+               "maloq_message_colsum");
+  }
+  std::vector<at::Tensor> res{gx, grad_rad, dw0, db0};
+  for (auto& t : dwm) res.push_back(t);
+  return res;
+}
+
+// ------------------------------------------------ fused Fock <-> irreps
+// The tables (pair_kind, slots, kind_blocks, blocks, w, sched) are those of a
+// basis_transform.HipE3TensorDecomp; ld > 0: dense Fock rows of stride ld (the
+// tensor's own row stride, unit column stride), ld = 0: block-list storage
+// with block_data_offsets.
+at::Tensor basis_row_meta(int64_t ld, const c10::optional<at::Tensor>& bdo, const at::Tensor& off,
+                          const at::Tensor& Z, const at::Tensor& rows, const at::Tensor& cols,
+                          const at::Tensor& pair_kind, int64_t maxe) {
+  require_gpu(rows, "rows");
+  const c10::DeviceGuard guard(rows.device());
+  const int64_t R = rows.size(0);
+  at::Tensor meta = at::empty({R > 1 ? R : 1, 4}, rows.options().dtype(at::kInt));
+  check_rc(maloq_basis_row_meta(ld, cptr<int64_t>(bdo), off.data_ptr<int32_t>(), Z.data_ptr<int32_t>(),
+                                rows.data_ptr<int32_t>(), cols.data_ptr<int32_t>(), R, pair_kind.data_ptr<int32_t>(),
+                                static_cast<int>(maxe), meta.data_ptr<int32_t>(), stream_of(rows)),
+           "maloq_basis_row_meta");
+  return meta;
+}
+
+// One launch: from the row plan `meta` (num_rows rows) or, without one, from
+// the pair list (off, Z, rows, cols, block_data_offsets).  perm_post: rows of
+// several column groups are sorted by a separate column gather afterwards.
+at::Tensor fock_to_irreps(const at::Tensor& fock, int64_t ld, const c10::optional<at::Tensor>& bdo,
+                          const c10::optional<at::Tensor>& off, const c10::optional<at::Tensor>& Z,
+                          const c10::optional<at::Tensor>& rows, const c10::optional<at::Tensor>& cols,
+                          const c10::optional<at::Tensor>& meta, int64_t num_rows, const at::Tensor& pair_kind,
+                          const at::Tensor& slots, int64_t maxe, const at::Tensor& kind_blocks,
+                          const c10::optional<at::Tensor>& perm_out, int64_t t, int64_t num_blocks,
+                          const at::Tensor& blocks, const c10::optional<at::Tensor>& w, const at::Tensor& sched,
+                          int64_t ngroups, int64_t group_cols, const c10::optional<at::Tensor>& perm_post) {
+  require_gpu(fock, "fock");
+  TORCH_CHECK_VALUE(fock.scalar_type() == at::kFloat,
+                    "Unsupported dtype for the Fock matrix; only float32 is supported.");
+  const c10::DeviceGuard guard(fock.device());
+  void* st = stream_of(fock);
+  at::Tensor out = at::empty({num_rows, t}, fock.options());
+  const auto* kb = static_cast<const uint32_t*>(kind_blocks.data_ptr());
+  if (meta.has_value()) {
+    check_rc(maloq_fock_to_irreps(fock.data_ptr<float>(), ld, meta->data_ptr<int32_t>(), num_rows,
+                                  slots.data_ptr<int32_t>(), static_cast<int>(maxe), kb, out.data_ptr<float>(),
+                                  cptr<int32_t>(perm_out), static_cast<int>(t), static_cast<int>(num_blocks),
+                                  blocks.data_ptr<int32_t>(), cptr<float>(w), sched.data_ptr<int32_t>(),
+                                  static_cast<int>(ngroups), static_cast<int>(group_cols), st),
+             "maloq_fock_to_irreps");
+  } else {
+    TORCH_CHECK_VALUE(off.has_value() && Z.has_value() && rows.has_value() && cols.has_value(),
+                      "fock_to_irreps needs a row plan or the pair list");
+    check_rc(maloq_fock_to_irreps_pairs(fock.data_ptr<float>(), ld, cptr<int64_t>(bdo), off->data_ptr<int32_t>(),
+                                        Z->data_ptr<int32_t>(), rows->data_ptr<int32_t>(), cols->data_ptr<int32_t>(),
+                                        num_rows, pair_kind.data_ptr<int32_t>(), slots.data_ptr<int32_t>(),
+                                        static_cast<int>(maxe), kb, out.data_ptr<float>(), cptr<int32_t>(perm_out),
+                                        static_cast<int>(t), static_cast<int>(num_blocks), blocks.data_ptr<int32_t>(),
+                                        cptr<float>(w), sched.data_ptr<int32_t>(), static_cast<int>(ngroups),
+                                        static_cast<int>(group_cols), st),
+             "maloq_fock_to_irreps_pairs");
+  }
+  if (!perm_post.has_value()) return out;
+  at::Tensor ones = at::ones({t}, fock.options());
+  at::Tensor sorted = at::empty_like(out);
+  check_rc(maloq_gather_columns(out.data_ptr<float>(), t, num_rows, perm_post->data_ptr<int32_t>(),
+                                ones.data_ptr<float>(), static_cast<int>(t), sorted.data_ptr<float>(), t, st),
+           "maloq_gather_columns");
+  return sorted;
+}
+
+// get_H per row, scattered into fock in place (the template's entries only).
+// perm_pre: rows of several column groups are un-sorted by a column gather first.
+void irreps_to_fock(const at::Tensor& net_out, const at::Tensor& fock, int64_t ld,
+                    const c10::optional<at::Tensor>& bdo, const c10::optional<at::Tensor>& off,
+                    const c10::optional<at::Tensor>& Z, const c10::optional<at::Tensor>& rows,
+                    const c10::optional<at::Tensor>& cols, const c10::optional<at::Tensor>& meta,
+                    int64_t num_rows, const at::Tensor& pair_kind, const at::Tensor& slots, int64_t maxe,
+                    const at::Tensor& kind_blocks, const c10::optional<at::Tensor>& perm_in, int64_t t,
+                    int64_t num_blocks, const at::Tensor& blocks, const c10::optional<at::Tensor>& w,
+                    const at::Tensor& sched, int64_t ngroups, int64_t group_cols,
+                    const c10::optional<at::Tensor>& perm_pre) {
+  require_gpu(fock, "fock");
+  require_gpu(net_out, "net_out");
+  TORCH_CHECK_VALUE(fock.scalar_type() == at::kFloat && net_out.scalar_type() == at::kFloat,
+                    "the Fock matrix and the irreps rows must be float32");
+  TORCH_CHECK_VALUE(net_out.dim() == 2 && net_out.size(0) == num_rows && net_out.size(1) == t,
+                    "net_out rows must match the atom-pair list");
+  const c10::DeviceGuard guard(fock.device());
+  void* st = stream_of(fock);
+  at::Tensor x = net_out.contiguous();
+  if (perm_pre.has_value()) {
+    at::Tensor ones = at::ones({t}, fock.options());
+    at::Tensor u = at::empty_like(x);
+    check_rc(maloq_gather_columns(x.data_ptr<float>(), t, num_rows, perm_pre->data_ptr<int32_t>(),
+                                  ones.data_ptr<float>(), static_cast<int>(t), u.data_ptr<float>(), t, st),
+             "maloq_gather_columns");
+    x = u;
+  }
+  const auto* kb = static_cast<const uint32_t*>(kind_blocks.data_ptr());
+  if (meta.has_value()) {
+    check_rc(maloq_irreps_to_fock(x.data_ptr<float>(), cptr<int32_t>(perm_in), fock.data_ptr<float>(), ld,
+                                  meta->data_ptr<int32_t>(), num_rows, slots.data_ptr<int32_t>(),
+                                  static_cast<int>(maxe), kb, static_cast<int>(t), static_cast<int>(num_blocks),
+                                  blocks.data_ptr<int32_t>(), cptr<float>(w), sched.data_ptr<int32_t>(),
+                                  static_cast<int>(ngroups), static_cast<int>(group_cols), st),
+             "maloq_irreps_to_fock");
+  } else {
+    TORCH_CHECK_VALUE(off.has_value() && Z.has_value() && rows.has_value() && cols.has_value(),
+                      "irreps_to_fock needs a row plan or the pair list");
+    check_rc(maloq_irreps_to_fock_pairs(x.data_ptr<float>(), cptr<int32_t>(perm_in), fock.data_ptr<float>(), ld,
+                                        cptr<int64_t>(bdo), off->data_ptr<int32_t>(), Z->data_ptr<int32_t>(),
+                                        rows->data_ptr<int32_t>(), cols->data_ptr<int32_t>(), num_rows,
+                                        pair_kind.data_ptr<int32_t>(), slots.data_ptr<int32_t>(),
+                                        static_cast<int>(maxe), kb, static_cast<int>(t), static_cast<int>(num_blocks),
+                                        blocks.data_ptr<int32_t>(), cptr<float>(w), sched.data_ptr<int32_t>(),
+                                        static_cast<int>(ngroups), static_cast<int>(group_cols), st),
+             "maloq_irreps_to_fock_pairs");
+  }
+}
+
 // ------------------------------------------------------- test-only helpers
 at::Tensor jd_table() {
   return at::from_blob(const_cast<float*>(maloq::kJdTable), {maloq::kJdFloats}, at::kFloat).clone();
@@ -411,6 +700,19 @@ TORCH_LIBRARY(maloq_hip, m) {
         "int num_blocks, int ngroups, int group_cols, Tensor? perm_inv) -> Tensor");
   m.def("message_block_fwd(Tensor x, Tensor? rad, Tensor w0, Tensor? b0, Tensor[] wm, Tensor src, Tensor dst, "
         "Tensor seg_ptr, Tensor eulers, int lmax, int mmax, bool gate) -> Tensor[]");
+  m.def("message_block_bwd(Tensor grad_out, Tensor? rad, Tensor w0, Tensor[] wm, Tensor bwd_src, "
+        "Tensor bwd_dst, Tensor bwd_eidx, Tensor seg_ptr_src, Tensor y, Tensor dk, Tensor? r, Tensor? g, "
+        "int num_nodes, int c_in, int lmax, int mmax, bool gate, bool need_rad_grad) -> Tensor[]");
+  m.def("basis_row_meta(int ld, Tensor? block_data_offsets, Tensor off, Tensor Z, Tensor rows, Tensor cols, "
+        "Tensor pair_kind, int maxe) -> Tensor");
+  m.def("fock_to_irreps(Tensor fock, int ld, Tensor? block_data_offsets, Tensor? off, Tensor? Z, Tensor? rows, "
+        "Tensor? cols, Tensor? meta, int num_rows, Tensor pair_kind, Tensor slots, int maxe, Tensor kind_blocks, "
+        "Tensor? perm_out, int t, int num_blocks, Tensor blocks, Tensor? w, Tensor sched, int ngroups, "
+        "int group_cols, Tensor? perm_post) -> Tensor");
+  m.def("irreps_to_fock(Tensor net_out, Tensor(a!) fock, int ld, Tensor? block_data_offsets, Tensor? off, "
+        "Tensor? Z, Tensor? rows, Tensor? cols, Tensor? meta, int num_rows, Tensor pair_kind, Tensor slots, "
+        "int maxe, Tensor kind_blocks, Tensor? perm_in, int t, int num_blocks, Tensor blocks, Tensor? w, "
+        "Tensor sched, int ngroups, int group_cols, Tensor? perm_pre) -> ()");
   m.def("_jd_table() -> Tensor", &jd_table);
   m.def("_pack_index(int dtype_code, int lmax, int mmax, bool gate, int c_in, int c_out, int mode) -> Tensor",
         &pack_index_cpu);
@@ -423,4 +725,8 @@ TORCH_LIBRARY_IMPL(maloq_hip, CUDA, m) {
   m.impl("segment_sum", &segment_sum);
   m.impl("label_transform", &label_transform);
   m.impl("message_block_fwd", &message_block_fwd);
+  m.impl("message_block_bwd", &message_block_bwd);
+  m.impl("basis_row_meta", &basis_row_meta);
+  m.impl("fock_to_irreps", &fock_to_irreps);
+  m.impl("irreps_to_fock", &irreps_to_fock);
 }

@@ -159,10 +159,28 @@ def _(x, rad, w0, b0, wm, src, dst, seg_ptr, eulers, lmax, mmax, gate):
     return [out, y, r, dk, g]
 
 
+message_block_bwd = _ops.message_block_bwd
+
+
+@register_fake("maloq_hip::message_block_bwd")
+def _(grad_out, rad, w0, wm, bwd_src, bwd_dst, bwd_eidx, seg_ptr_src, y, dk, r, g, num_nodes, c_in, lmax, mmax,
+      gate, need_rad_grad):
+    d = (lmax + 1) ** 2
+    c_out = grad_out.shape[2]
+    f32 = dict(dtype=torch.float32)
+    extra = lmax * c_out if gate else 0
+    gx = grad_out.new_empty(num_nodes, d, c_in, **f32)
+    grad_rad = rad.new_empty(rad.shape, dtype=y.dtype) if (rad is not None and need_rad_grad) \
+        else grad_out.new_empty(0, **f32)
+    dw0 = grad_out.new_empty(extra + (lmax + 1) * c_out, (lmax + 1) * c_in, **f32)
+    db0 = grad_out.new_empty(extra + (lmax + 1) * c_out, **f32)
+    dwm = [grad_out.new_empty(2 * (lmax - m + 1) * c_out, (lmax - m + 1) * c_in, **f32) for m in range(1, mmax + 1)]
+    return [gx, grad_rad, dw0, db0] + dwm
+
+
 def message_block(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=False):
-    """The fused block through the registered op (forward) and
-    :func:`maloq_amd.message.message_backward_dx` / ``message_weight_grad``
-    (backward): same results as :func:`maloq_amd.message.message_block`."""
+    """The fused block through the registered operators (message_block_fwd,
+    message_block_bwd): same results as :func:`maloq_amd.message.message_block`."""
     return _MessageOp.apply(x, rad, w0, b0, plan, eulers, lmax, mmax, bool(gate), *wm[:mmax])
 
 
@@ -180,16 +198,32 @@ class _MessageOp(torch.autograd.Function):
     def backward(ctx, gout):
         rad, w0, y, dk, r, g, *wm = ctx.saved_tensors
         plan, lmax, mmax, gate = ctx.plan, ctx.lmax, ctx.mmax, ctx.gate
-        gx, grad_rad, dz = M.message_backward_dx(gout, ctx.x_shape, ctx.dt, plan, {"dk": dk, "r": r, "g": g}, rad,
-                                                 w0, wm, lmax, mmax, need_rad_grad=ctx.needs_input_grad[1],
-                                                 gate=gate)
-        dw0 = db0 = None
-        dwm = [None] * len(wm)
-        if plan.num_edges > 0:
-            dw0, dwm, db0 = M.message_weight_grad(dz, y, lmax, mmax, gout.shape[2], ctx.x_shape[2],
-                                                  num_edges=plan.num_edges, gate=gate)
-        else:
-            dw0, dwm = torch.zeros_like(w0), [torch.zeros_like(w) for w in wm]
-            db0 = torch.zeros(w0.shape[0], device=w0.device)
-        return (gx.to(ctx.dt), grad_rad, dw0.to(w0.dtype), db0 if ctx.has_b0 else None, None, None, None, None,
-                None, *[d.to(w.dtype) for d, w in zip(dwm, wm)])
+        need_rad = rad is not None and ctx.needs_input_grad[1]
+        gx, grad_rad, dw0, db0, *dwm = message_block_bwd(
+            gout, rad, w0, list(wm), plan.bwd_src, plan.bwd_dst, plan.bwd_eidx, plan.seg_ptr_src, y, dk, r, g,
+            ctx.x_shape[0], ctx.x_shape[2], lmax, mmax, gate, need_rad)
+        return (gx.to(ctx.dt), grad_rad if need_rad else None, dw0.to(w0.dtype), db0 if ctx.has_b0 else None,
+                None, None, None, None, None, *[d.to(w.dtype) for d, w in zip(dwm, wm)])
+
+
+# ------------------------------------------------- fused Fock <-> irreps
+basis_row_meta = _ops.basis_row_meta
+fock_to_irreps = _ops.fock_to_irreps
+irreps_to_fock = _ops.irreps_to_fock
+
+
+@register_fake("maloq_hip::basis_row_meta")
+def _(ld, block_data_offsets, off, Z, rows, cols, pair_kind, maxe):
+    return rows.new_empty(max(rows.shape[0], 1), 4, dtype=torch.int32)
+
+
+@register_fake("maloq_hip::fock_to_irreps")
+def _(fock, ld, block_data_offsets, off, Z, rows, cols, meta, num_rows, pair_kind, slots, maxe, kind_blocks,
+      perm_out, t, num_blocks, blocks, w, sched, ngroups, group_cols, perm_post):
+    return fock.new_empty(num_rows, t)
+
+
+@register_fake("maloq_hip::irreps_to_fock")
+def _(net_out, fock, ld, block_data_offsets, off, Z, rows, cols, meta, num_rows, pair_kind, slots, maxe,
+      kind_blocks, perm_in, t, num_blocks, blocks, w, sched, ngroups, group_cols, perm_pre):
+    return None

@@ -13,7 +13,7 @@ import torch
 def test_ops_are_registered():
     import maloq_amd.ops  # noqa: F401
     for name in ("edge_euler", "wigner_from_euler", "rotate", "segment_sum", "label_transform",
-                 "message_block_fwd"):
+                 "message_block_fwd", "message_block_bwd", "basis_row_meta", "fock_to_irreps", "irreps_to_fock"):
         assert hasattr(torch.ops.maloq_hip, name), name
 
 
@@ -46,9 +46,14 @@ def test_opcheck(device):
     rad = torch.rand(E, M.rad_width(L, L, C), generator=gen).to(device)
     for gate in (False, True):
         w0g, b0g = (w0, b0) if gate else (w0[:(L + 1) * C], b0[:(L + 1) * C])
-        torch.library.opcheck(ops.message_block_fwd,
-                              (xm, rad, w0g, b0g, wm, plan.src, plan.dst, plan.seg_ptr, plan.sort_edges(eul), L, L,
-                               gate), test_utils=("test_schema", "test_faketensor"))
+        args = (xm, rad, w0g, b0g, wm, plan.src, plan.dst, plan.seg_ptr, plan.sort_edges(eul), L, L, gate)
+        torch.library.opcheck(ops.message_block_fwd, args, test_utils=("test_schema", "test_faketensor"))
+        out, y, r, dk, g = ops.message_block_fwd(*args)
+        gout = torch.randn(out.shape, generator=gen).to(device)
+        torch.library.opcheck(ops.message_block_bwd,
+                              (gout, rad, w0g, wm, plan.bwd_src, plan.bwd_dst, plan.bwd_eidx, plan.seg_ptr_src, y,
+                               dk, r, g if gate else None, N, C, L, L, gate, True),
+                              test_utils=("test_schema", "test_faketensor"))
 
 
 @pytest.mark.gpu
@@ -130,3 +135,45 @@ def test_label_transform_op_matches_decomp(basis, if_sort, device):
     assert torch.equal(y.grad, y2.grad)
     torch.library.opcheck(ops.label_transform, (H, hip._blocks_fwd, hip._wk_fwd, hip._sched, None, hip._perm)
                           + ops._layout(hip), test_utils=("test_schema", "test_faketensor"))
+
+
+@pytest.mark.gpu
+def test_fused_fock_ops_opcheck(device):
+    """Schema and fake implementations of the fused Fock operators, on the
+    arguments HipE3TensorDecomp passes (a SiO2 block list, with and without a
+    row plan); the in-place irreps_to_fock is checked as a mutating op."""
+    from maloq_amd import ops
+    from maloq_amd import tensor_decomp as ptd
+    from maloq_amd.basis_transform import HipE3TensorDecomp
+    from maloq_amd.synth import atom_pair_rows, radius_graph, sio2_cell
+    from oracle import matrix2labels as om2l
+    t = ptd.BasisTables({8: [0, 0, 1, 1, 2], 14: [0, 0, 1, 1, 2]})
+    hip = HipE3TensorDecomp(ptd.e3TensorDecomp(t.req_output_irreps, t.out_js_list, torch.float32,
+                                               device_torch=device))
+    Z, pos, L = sio2_cell(n_atoms=30, seed=2, iters=50)
+    src, dst, _ = radius_graph(pos, 5.0, cell=L)
+    rows, cols = atom_pair_rows(src, dst, len(Z))
+    off = np.concatenate([[0], np.cumsum(t.orbitals_per_atom(Z))]).astype(np.int32)
+    bdo = om2l.block_data_offsets(off, rows, cols)
+    gen = torch.Generator().manual_seed(4)
+    data = torch.randn(int(bdo[-1]), generator=gen).to(device)
+    bd = torch.from_numpy(bdo).to(device)
+    dev_i32 = lambda a: torch.as_tensor(np.asarray(a, np.int32), device=device)
+    o, z, r, c = (dev_i32(a) for a in (off, Z, rows, cols))
+    tabs = hip._template_tables(t.orbital_template)
+    R = len(rows)
+    torch.library.opcheck(ops.basis_row_meta, (0, bd, o, z, r, c, tabs["pair_kind"], tabs["maxe"]),
+                          test_utils=("test_schema", "test_faketensor"))
+    meta = ops.basis_row_meta(0, bd, o, z, r, c, tabs["pair_kind"], tabs["maxe"])
+    common = (tabs["pair_kind"], tabs["slots"], tabs["maxe"], tabs["kind_blocks"])
+    tail = (hip.num_blocks, hip._blocks_fwd, hip._wk_fwd, hip._sched, hip.ngroups, hip.group_cols, None)
+    for m in (None, meta):
+        pairs = (bd, o, z, r, c) if m is None else (None, None, None, None, None)
+        torch.library.opcheck(ops.fock_to_irreps, (data, 0) + pairs + (m, R) + common + (None, hip.total_in_dim)
+                              + tail, test_utils=("test_schema", "test_faketensor"))
+    lab = hip.fock_to_irreps(data, off, Z, rows, cols, t.orbital_template, block_data_offsets=bd)
+    back = torch.zeros_like(data)
+    torch.library.opcheck(ops.irreps_to_fock, (lab, back, 0, bd, o, z, r, c, None, R) + common
+                          + (None, hip.total_in_dim, hip.num_blocks, hip._blocks_inv, hip._wk_inv, hip._sched,
+                             hip.ngroups, hip.group_cols, None),
+                          test_utils=("test_schema", "test_faketensor"))
