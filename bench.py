@@ -1081,6 +1081,25 @@ def profile_only(args):
         b = torch.empty_like(a)
         for _ in range(args.reps):
             b.copy_(a)
+    elif args.only == "hbm":
+        # the practical HBM ceiling of the box: torch's device copy (read +
+        # write), fill (write) and sum (read) over one fp32 [E, d, C] array of
+        # config 2 (471 MB), event-timed
+        import json
+        n = 36804 * 25 * 128
+        a = torch.ones(n, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+            b.fill_(1.0)
+            a.sum()
+        torch.cuda.synchronize()
+        nb = 4 * n
+        tc = kernel_time_events(lambda: b.copy_(a), args.reps)
+        tf = kernel_time_events(lambda: b.fill_(2.0), args.reps)
+        ts = kernel_time_events(lambda: a.sum(), args.reps)
+        print(json.dumps({"bytes_per_array": nb, "copy_TBps": 2 * nb / tc / 1e12, "fill_TBps": nb / tf / 1e12,
+                          "sum_TBps": nb / ts / 1e12, "copy_us": tc * 1e6, "peak_TBps": 8.0}), flush=True)
     elif args.only == "embed":
         ew = embed_workload()
         for _ in range(args.reps):
@@ -1144,7 +1163,7 @@ def main(argv=None):
                     help="precision of the headline (the reference computes in fp32)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-extras", action="store_true", help="headline only")
-    ap.add_argument("--only", choices=["fwd", "step", "basis", "copy", "embed", "edgewise", "edgewise-step",
+    ap.add_argument("--only", choices=["fwd", "step", "basis", "copy", "hbm", "embed", "edgewise", "edgewise-step",
                                        "rotate", "basis5", "basis-tzvpd", "ref-backbone", "ceiling"],
                     help="profiling mode: run one piece a few times and exit (no JSON line)")
     ap.add_argument("--cfg", default="config2", choices=sorted(MESSAGE_CONFIGS),

@@ -31,6 +31,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <initializer_list>
 #include <map>
 #include <mutex>
 #include <string>
@@ -63,10 +64,22 @@ int dtype_code(at::ScalarType s) {
   return -1;
 }
 
+// Device pointer of an optional tensor of element type T (null if absent);
+// a tensor of another dtype is refused rather than reinterpreted.
 template <class T>
 const T* cptr(const c10::optional<at::Tensor>& t) {
-  return t.has_value() ? static_cast<const T*>(t->data_ptr()) : nullptr;
+  return t.has_value() ? t->data_ptr<T>() : nullptr;
 }
+
+// Every given tensor on the device of `ref` (the kernels take raw pointers).
+void same_device(const at::Tensor& ref, std::initializer_list<c10::optional<at::Tensor>> ts) {
+  for (const auto& t : ts)
+    TORCH_CHECK_VALUE(!t.has_value() || t->device() == ref.device(), "all tensors must be on ", ref.device(),
+                      ", got one on ", t->device());
+}
+
+// 1-D length of an index tensor (or -1 if absent).
+int64_t len(const c10::optional<at::Tensor>& t) { return t.has_value() ? t->numel() : -1; }
 
 // Packed J_0 .. J_8 on the device (the table of every lmax <= 8 is its prefix),
 // uploaded once per device and kept for the life of the process (never freed:
@@ -218,6 +231,7 @@ at::Tensor rotate(const at::Tensor& x, const at::Tensor& eulers, const c10::opti
   require_gpu(x, "x");
   require_gpu(eulers, "eulers");
   if (gather.has_value()) require_gpu(*gather, "gather");
+  same_device(x, {eulers, gather});
   const c10::DeviceGuard guard(x.device());
   const int64_t E = eulers.size(0);
   TORCH_CHECK_VALUE(eulers.dim() == 2 && eulers.size(1) == 3, "eulers must be [E, 3]");
@@ -251,6 +265,9 @@ at::Tensor segment_sum(const at::Tensor& msg, const at::Tensor& perm, const at::
   require_gpu(perm, "perm");
   require_gpu(seg_ptr, "seg_ptr");
   TORCH_CHECK_VALUE(msg.dim() >= 1 && num_segments >= 0, "msg must have a leading edge dimension");
+  TORCH_CHECK_VALUE(perm.numel() == msg.size(0), "perm must hold one entry per message row");
+  TORCH_CHECK_VALUE(seg_ptr.numel() == num_segments + 1, "seg_ptr must hold num_segments + 1 offsets");
+  same_device(msg, {perm, seg_ptr});
   const c10::DeviceGuard guard(msg.device());
   const at::Tensor m = msg.to(at::kFloat).contiguous();
   std::vector<int64_t> shape{num_segments};
@@ -278,6 +295,10 @@ at::Tensor label_transform(const at::Tensor& x, const at::Tensor& blocks, const 
   require_gpu(x, "x");
   TORCH_CHECK_VALUE(x.dim() == 2, "label rows must be [R, t]");
   TORCH_CHECK_VALUE(x.scalar_type() == at::kFloat, "label rows must be float32");
+  same_device(x, {blocks, w, sched, perm_in, perm_out, perm_inv});
+  TORCH_CHECK_VALUE(blocks.numel() == 4 * num_blocks, "blocks must be [num_blocks, 4]");
+  for (const auto* p : {&perm_in, &perm_out, &perm_inv})
+    TORCH_CHECK_VALUE(len(*p) < 0 || len(*p) == x.size(1), "column permutations must have one entry per column");
   const c10::DeviceGuard guard(x.device());
   at::Tensor xc = x.contiguous();
   const bool pre = ngroups > 1 && perm_in.has_value();
@@ -327,6 +348,9 @@ std::vector<at::Tensor> message_block_fwd(const at::Tensor& x, const c10::option
                         seg_ptr.scalar_type() == at::kLong,
                     "the plan's src/dst must be int32 and seg_ptr int64");
   TORCH_CHECK_VALUE(static_cast<int64_t>(wm.size()) >= mmax, "wm needs mmax weights");
+  TORCH_CHECK_VALUE(dst.numel() == src.numel() && seg_ptr.numel() >= 1, "src and dst must have one entry per edge");
+  same_device(x, {rad, w0, b0, src, dst, seg_ptr, eulers});
+  for (int64_t m = 0; m < mmax; ++m) same_device(x, {wm[m]});
   const c10::DeviceGuard guard(x.device());
   const int64_t c_in = x.size(2), n0 = w0.size(0);
   const int64_t c_out = n0 / (lmax + 1 + (gate ? lmax : 0));
@@ -486,6 +510,13 @@ std::vector<at::Tensor> message_block_bwd(const at::Tensor& grad_out, const c10:
   TORCH_CHECK_VALUE(static_cast<int64_t>(wm.size()) >= mmax, "wm needs mmax weights");
   TORCH_CHECK_VALUE(!gate || (g.has_value() && g->numel() > 0),
                     "the gated backward needs the forward's pre-activation rows");
+  TORCH_CHECK_VALUE(bwd_dst.numel() == bwd_src.numel() && bwd_eidx.numel() == bwd_src.numel(),
+                    "the source-sorted arrays must have one entry per edge");
+  TORCH_CHECK_VALUE(seg_ptr_src.numel() == num_nodes + 1, "seg_ptr_src must hold num_nodes + 1 offsets");
+  TORCH_CHECK_VALUE(y.dim() == 3 && y.size(0) >= bwd_src.numel() && dk.size(0) >= bwd_src.numel(),
+                    "the saved rows must cover every edge");
+  same_device(grad_out, {rad, w0, bwd_src, bwd_dst, bwd_eidx, seg_ptr_src, y, dk, r, g});
+  for (int64_t m = 0; m < mmax; ++m) same_device(grad_out, {wm[m]});
   const c10::DeviceGuard guard(grad_out.device());
   const int64_t c_out = grad_out.size(2), E = bwd_src.size(0);
   const int kr = maloq_message_kept_rows(static_cast<int>(lmax), static_cast<int>(mmax));
@@ -569,6 +600,9 @@ at::Tensor basis_row_meta(int64_t ld, const c10::optional<at::Tensor>& bdo, cons
                           const at::Tensor& Z, const at::Tensor& rows, const at::Tensor& cols,
                           const at::Tensor& pair_kind, int64_t maxe) {
   require_gpu(rows, "rows");
+  TORCH_CHECK_VALUE(cols.numel() == rows.numel(), "rows and cols must have the same length");
+  TORCH_CHECK_VALUE(len(bdo) < 0 || len(bdo) >= rows.numel(), "block_data_offsets must cover every pair");
+  same_device(rows, {bdo, off, Z, cols, pair_kind});
   const c10::DeviceGuard guard(rows.device());
   const int64_t R = rows.size(0);
   at::Tensor meta = at::empty({R > 1 ? R : 1, 4}, rows.options().dtype(at::kInt));
@@ -577,6 +611,28 @@ at::Tensor basis_row_meta(int64_t ld, const c10::optional<at::Tensor>& bdo, cons
                                 static_cast<int>(maxe), meta.data_ptr<int32_t>(), stream_of(rows)),
            "maloq_basis_row_meta");
   return meta;
+}
+
+// Shapes a fused Fock call relies on: the row plan (or the pair list) covers
+// num_rows rows; the CG block table has num_blocks entries; every tensor on
+// the Fock matrix's device.
+void check_fock_args(const at::Tensor& fock, const c10::optional<at::Tensor>& bdo,
+                     const c10::optional<at::Tensor>& off, const c10::optional<at::Tensor>& Z,
+                     const c10::optional<at::Tensor>& rows, const c10::optional<at::Tensor>& cols,
+                     const c10::optional<at::Tensor>& meta, int64_t num_rows, int64_t t, const at::Tensor& blocks,
+                     int64_t num_blocks, std::initializer_list<c10::optional<at::Tensor>> tables) {
+  TORCH_CHECK_VALUE(num_rows >= 0 && t > 0, "bad row count or width");
+  TORCH_CHECK_VALUE(blocks.numel() == 4 * num_blocks, "blocks must be [num_blocks, 4]");
+  if (meta.has_value()) {
+    TORCH_CHECK_VALUE(meta->dim() == 2 && meta->size(1) == 4 && meta->size(0) >= num_rows,
+                      "the row plan must hold num_rows [4] entries");
+  } else if (rows.has_value() && cols.has_value()) {
+    TORCH_CHECK_VALUE(rows->numel() == num_rows && cols->numel() == num_rows,
+                      "rows and cols must hold num_rows entries");
+    TORCH_CHECK_VALUE(len(bdo) < 0 || len(bdo) >= num_rows, "block_data_offsets must cover every pair");
+  }
+  same_device(fock, {bdo, off, Z, rows, cols, meta, blocks});
+  same_device(fock, tables);
 }
 
 // One launch: from the row plan `meta` (num_rows rows) or, without one, from
@@ -593,10 +649,14 @@ at::Tensor fock_to_irreps(const at::Tensor& fock, int64_t ld, const c10::optiona
   require_gpu(fock, "fock");
   TORCH_CHECK_VALUE(fock.scalar_type() == at::kFloat,
                     "Unsupported dtype for the Fock matrix; only float32 is supported.");
+  check_fock_args(fock, bdo, off, Z, rows, cols, meta, num_rows, t, blocks, num_blocks,
+                  {pair_kind, slots, kind_blocks, perm_out, w, sched, perm_post});
+  TORCH_CHECK_VALUE(len(perm_out) < 0 || len(perm_out) == t, "perm_out must have one entry per column");
+  TORCH_CHECK_VALUE(len(perm_post) < 0 || len(perm_post) == t, "perm_post must have one entry per column");
   const c10::DeviceGuard guard(fock.device());
   void* st = stream_of(fock);
   at::Tensor out = at::empty({num_rows, t}, fock.options());
-  const auto* kb = static_cast<const uint32_t*>(kind_blocks.data_ptr());
+  const auto* kb = reinterpret_cast<const uint32_t*>(kind_blocks.data_ptr<int32_t>());
   if (meta.has_value()) {
     check_rc(maloq_fock_to_irreps(fock.data_ptr<float>(), ld, meta->data_ptr<int32_t>(), num_rows,
                                   slots.data_ptr<int32_t>(), static_cast<int>(maxe), kb, out.data_ptr<float>(),
@@ -642,6 +702,10 @@ void irreps_to_fock(const at::Tensor& net_out, const at::Tensor& fock, int64_t l
                     "the Fock matrix and the irreps rows must be float32");
   TORCH_CHECK_VALUE(net_out.dim() == 2 && net_out.size(0) == num_rows && net_out.size(1) == t,
                     "net_out rows must match the atom-pair list");
+  check_fock_args(fock, bdo, off, Z, rows, cols, meta, num_rows, t, blocks, num_blocks,
+                  {net_out, pair_kind, slots, kind_blocks, perm_in, w, sched, perm_pre});
+  TORCH_CHECK_VALUE(len(perm_in) < 0 || len(perm_in) == t, "perm_in must have one entry per column");
+  TORCH_CHECK_VALUE(len(perm_pre) < 0 || len(perm_pre) == t, "perm_pre must have one entry per column");
   const c10::DeviceGuard guard(fock.device());
   void* st = stream_of(fock);
   at::Tensor x = net_out.contiguous();
@@ -653,7 +717,7 @@ void irreps_to_fock(const at::Tensor& net_out, const at::Tensor& fock, int64_t l
              "maloq_gather_columns");
     x = u;
   }
-  const auto* kb = static_cast<const uint32_t*>(kind_blocks.data_ptr());
+  const auto* kb = reinterpret_cast<const uint32_t*>(kind_blocks.data_ptr<int32_t>());
   if (meta.has_value()) {
     check_rc(maloq_irreps_to_fock(x.data_ptr<float>(), cptr<int32_t>(perm_in), fock.data_ptr<float>(), ld,
                                   meta->data_ptr<int32_t>(), num_rows, slots.data_ptr<int32_t>(),

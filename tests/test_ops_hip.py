@@ -177,3 +177,33 @@ def test_fused_fock_ops_opcheck(device):
                           + (None, hip.total_in_dim, hip.num_blocks, hip._blocks_inv, hip._wk_inv, hip._sched,
                              hip.ngroups, hip.group_cols, None),
                           test_utils=("test_schema", "test_faketensor"))
+
+
+@pytest.mark.gpu
+def test_operators_refuse_inconsistent_arguments(device):
+    """The operators take raw device pointers into the kernels, so shapes that
+    would read or write past a buffer are refused on the host (ValueError)
+    before any launch."""
+    from maloq_amd import ops
+    msg = torch.zeros(10, 4, device=device)
+    perm = torch.arange(10, device=device)
+    with pytest.raises(ValueError, match="seg_ptr"):
+        ops.segment_sum(msg, perm, torch.zeros(3, dtype=torch.int64, device=device), 5)
+    with pytest.raises(ValueError, match="perm"):
+        ops.segment_sum(msg, perm[:4], torch.zeros(6, dtype=torch.int64, device=device), 5)
+    x = torch.zeros(3, 25, device=device)
+    blocks = torch.zeros(2, 4, dtype=torch.int32, device=device)
+    sched = torch.zeros(8, dtype=torch.int32, device=device)
+    with pytest.raises(ValueError, match="column permutations"):
+        ops.label_transform(x, blocks, None, sched, torch.zeros(24, dtype=torch.int32, device=device), None,
+                            2, 1, 25, None)
+    with pytest.raises(ValueError, match="blocks"):
+        ops.label_transform(x, blocks, None, sched, None, None, 3, 1, 25, None)
+    fock = torch.zeros(100, device=device)
+    i32 = torch.zeros(4, dtype=torch.int32, device=device)
+    meta = torch.zeros(2, 4, dtype=torch.int32, device=device)
+    with pytest.raises(ValueError, match="row plan"):
+        ops.fock_to_irreps(fock, 0, None, None, None, None, None, meta, 5, i32, i32, 1, i32, None, 25, 2, blocks,
+                           None, sched, 1, 25, None)
+    with pytest.raises(ValueError, match="rows and cols"):
+        ops.basis_row_meta(0, None, i32, i32, i32, i32[:2], i32, 1)
