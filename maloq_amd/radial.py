@@ -95,7 +95,9 @@ def radial_mlp(inputs: torch.Tensor, mod: RadialMLP, out_dtype: torch.dtype | No
     :func:`fused_supported`) run as Linear (a plain library GEMM) ->
     LayerNorm -> SiLU in torch, as the reference's own module does; the rest,
     when any is left, are the fused kernels, which hand the gradient of their
-    input to autograd."""
+    input to autograd.  When no hidden layer is left for them, the output
+    Linear runs as a library GEMM in the output dtype (bf16 operands, fp32
+    accumulation for a bf16 block), like the fused kernels' output layer."""
     dt = out_dtype or torch.float32
     if dt not in DTYPE_CODE:
         raise ValueError(f"unsupported output dtype {dt}")
@@ -109,6 +111,10 @@ def radial_mlp(inputs: torch.Tensor, mod: RadialMLP, out_dtype: torch.dtype | No
         inputs = F.silu(F.layer_norm(F.linear(inputs.float(), w1, b1), (widths[1],), g1, bt1, eps))
         widths, params = widths[1:], params[4:]
     if len(widths) < 3:    # no hidden layer left: the output Linear alone
+        if dt == torch.bfloat16:
+            # in the message dtype with fp32 accumulation, as the fused kernels
+            # run their output layer (hidden layers stay fp32)
+            return F.linear(inputs.to(dt), params[0].to(dt), params[1].to(dt))
         return F.linear(inputs, params[0], params[1]).to(dt)
     return _RadialFn.apply(inputs, dt, widths, eps, *params)
 

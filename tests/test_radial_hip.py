@@ -58,7 +58,10 @@ def _close(got, ref, tol, what):
 # equal shares of (tile, output group) units split tiles between workgroups
 # (only the one holding a tile's first group saves its hidden rows)
 CASES = [((8, 64, 64, 1536), 1000), ((8, 32, 192), 37), ((16, 64, 32, 64, 256), 130), ((8, 64, 64, 1536), 64),
-         ((4, 128, 384), 200), ((8, 96, 256), 333), ((8, 64, 64, 1536), 20000)]
+         ((4, 128, 384), 200), ((8, 96, 256), 333), ((8, 64, 64, 1536), 20000),
+         # the reference models' widths (esen_osh.py:189-192) at lmax = mmax = 4 and 2 C = 256
+         # conv1 input channels: wider than the fused kernels, so every layer is a library GEMM
+         ((384, 128, 128, 3840), 150)]
 
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
