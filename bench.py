@@ -67,6 +67,7 @@ def gaussian_rbf(dist, start, stop, num):
 
 # message-block legs: (graph loader, lmax, mmax, channels, gated, RBF cutoff)
 MESSAGE_CONFIGS = {
+    "config1": ("config1_graph", 2, 2, 32, False, 5.0),
     "config2": ("config2_graph", 4, 2, 128, False, 6.0),
     "config4": ("config4_graph", 6, 2, 128, True, 8.0),
     "config5": ("config5_graph", 4, 2, 256, False, 6.0),
@@ -112,12 +113,19 @@ def message_workload(dtype_name, seed=0, cfg="config2"):
                 gout=gout, L=L, M=Mm, C=C, dt=dt, N=N, E=E, gate=gate, cutoff=cutoff, cfg=cfg)
 
 
-def message_step(w, backward=True):
+def message_step(w, backward=True, ops=True):
+    """One training step of the fused block: Euler angles, radial MLP, the
+    block (through the module path, or with ``ops`` through the registered
+    C++ operators maloq_hip::message_block_fwd / _bwd; same kernels and bits)."""
     from maloq_amd import message as M
     from maloq_amd.wigner import extract_euler_angles
+    block = M.message_block
+    if ops:
+        from maloq_amd import ops as O
+        block = O.message_block
     eul = extract_euler_angles(w["vec"], seed=1234)
     rad = w["radial"](gaussian_rbf(w["dist"], 0.0, w["cutoff"], 8), out_dtype=w["dt"])
-    out = M.message_block(w["x"], w["plan"], eul, rad, w["w0"], w["b0"], w["wm"], w["L"], w["M"], gate=w["gate"])
+    out = block(w["x"], w["plan"], eul, rad, w["w0"], w["b0"], w["wm"], w["L"], w["M"], gate=w["gate"])
     if backward:
         # a training step starts from cleared gradients (zero_grad(set_to_none=True))
         for t in [w["x"], w["w0"], w["b0"], *w["wm"], *w["radial"].parameters()]:
@@ -1050,6 +1058,8 @@ def library_gemm_ceiling(dtypes=("bf16", "fp32"), reps=20):
     dev = torch.device("cuda:0")
     out = {}
     for cfg, (gname, L, M, C, gate, _) in MESSAGE_CONFIGS.items():
+        if cfg == "config1":   # the host-overhead case only
+            continue
         E = _graph(gname).src.shape[0]
         for dtn in dtypes:
             dt = torch.bfloat16 if dtn == "bf16" else torch.float32
@@ -1081,6 +1091,18 @@ def profile_only(args):
         b = torch.empty_like(a)
         for _ in range(args.reps):
             b.copy_(a)
+    elif args.only == "host":
+        # wall time per training step through the module path and through the
+        # registered operators: config 1 (132 edges) is bound by the host's
+        # enqueue, config 2 by the GPU
+        import json
+        res = {}
+        for cfg in ("config1", "config2"):
+            w = message_workload(args.dtype, cfg=cfg)
+            for name, use_ops in (("module", False), ("ops", True)):
+                t = time_steps(lambda: message_step(w, ops=use_ops), max(args.reps, 20), 5)
+                res[f"{cfg}_{name}_us_per_step"] = t * 1e6
+        print(json.dumps(res), flush=True)
     elif args.only == "hbm":
         # the practical HBM ceiling of the box: torch's device copy (read +
         # write), fill (write) and sum (read) over one fp32 [E, d, C] array of
@@ -1163,7 +1185,7 @@ def main(argv=None):
                     help="precision of the headline (the reference computes in fp32)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-extras", action="store_true", help="headline only")
-    ap.add_argument("--only", choices=["fwd", "step", "basis", "copy", "hbm", "embed", "edgewise", "edgewise-step",
+    ap.add_argument("--only", choices=["fwd", "step", "basis", "copy", "hbm", "host", "embed", "edgewise", "edgewise-step",
                                        "rotate", "basis5", "basis-tzvpd", "ref-backbone", "ceiling"],
                     help="profiling mode: run one piece a few times and exit (no JSON line)")
     ap.add_argument("--cfg", default="config2", choices=sorted(MESSAGE_CONFIGS),
