@@ -919,7 +919,7 @@ def edgewise_step(ew):
 REF_LAYERS = 4
 
 
-def reference_backbone_workload(dtype_name, seed=0):
+def reference_backbone_workload(dtype_name, seed=0, lmax=4, layers=None):
     """The reference's layer loop (helm/esen_osh.py:438-463) on the config-2
     graph: REF_LAYERS Edgewise modules at its model shape (lmax = mmax = 4,
     sphere and hidden channels 128, radial [384, 128, 128], training_workflow.py:
@@ -934,11 +934,11 @@ def reference_backbone_workload(dtype_name, seed=0):
     dev = torch.device("cuda:0")
     dt = {"bf16": torch.bfloat16, "fp32": torch.float32}[dtype_name]
     g = _graph("config2_graph")
-    L = Mm = 4
+    L = Mm = lmax
     C = H = 128
     torch.manual_seed(seed)
     mods = [Edgewise(C, H, L, Mm, [384, 128, 128], CoefficientMapping(L, Mm), None, 6.0, "source-target").to(dev)
-            for _ in range(REF_LAYERS)]
+            for _ in range(REF_LAYERS if layers is None else layers)]
     gen = torch.Generator().manual_seed(seed)
     ei = torch.from_numpy(np.stack([g.src, g.dst])).to(dev)
     vec = torch.from_numpy(g.edge_distance_vec()).float().to(dev)
@@ -971,10 +971,10 @@ def reference_backbone_pass(rw, backward=True, cached=True):
     return h
 
 
-def reference_backbone_leg(dtype_name, steps=5, warmup=2, cpu=True):
+def reference_backbone_leg(dtype_name, steps=5, warmup=2, cpu=True, lmax=4, layers=None):
     import torch
     from maloq_amd import message as M
-    rw = reference_backbone_workload(dtype_name)
+    rw = reference_backbone_workload(dtype_name, lmax=lmax, layers=layers)
     M.clear_plan_cache()
     built0 = M._PLANS.built
     reference_backbone_pass(rw, True)
@@ -982,15 +982,16 @@ def reference_backbone_leg(dtype_name, steps=5, warmup=2, cpu=True):
     t_step = time_steps(lambda: reference_backbone_pass(rw, True), steps, warmup)
     t_fwd = time_steps(lambda: reference_backbone_pass(rw, False), steps, warmup)
     t_fwd_nc = time_steps(lambda: reference_backbone_pass(rw, False, cached=False), steps, warmup)
-    E, n = rw["E"], REF_LAYERS
+    E, n = rw["E"], len(rw["mods"])
     fl = edgewise_flops_per_edge(rw["L"], rw["M"], rw["C"], rw["H"]) * E * n
     peak = PEAK_BF16 if dtype_name == "bf16" else PEAK_FP32
     out = {"metric": "edges/s per layer", "fwd_bwd": E * n / t_step, "fwd": E * n / t_fwd,
            "fwd_without_plan_cache": E * n / t_fwd_nc, "ms_per_pass_fwd_bwd": t_step * 1e3,
            "ms_per_pass_fwd": t_fwd * 1e3, "ms_per_pass_fwd_without_plan_cache": t_fwd_nc * 1e3,
            "plans_built_per_pass": plans_per_pass, "layers": n, "dtype": dtype_name,
-           "config": "config-2 graph (36 804 edges), Edgewise x4 at the reference's model shape: lmax = mmax = 4, "
-                     "C = H = 128, radial [384, 128, 128], dense wigner / wigner_inv, no plan= (reference call)",
+           "config": f"config-2 graph (36 804 edges), Edgewise x{n} at the reference's model shape: "
+                     f"lmax = mmax = {rw['L']}, C = H = 128, radial [384, 128, 128], dense wigner / wigner_inv, "
+                     "no plan= (reference call)",
            "roofline": {"scope": "whole forward pass (radial MLPs, Wigner-row gathers, prep, both GEMMs, fixups)",
                         "bound": "mfma", "achieved": fl / t_fwd / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
                         "frac": fl / t_fwd / peak, "flops_per_pass": fl}}
@@ -1095,7 +1096,6 @@ def profile_only(args):
         # wall time per training step through the module path and through the
         # registered operators: config 1 (132 edges) is bound by the host's
         # enqueue, config 2 by the GPU
-        import json
         res = {}
         for cfg in ("config1", "config2"):
             w = message_workload(args.dtype, cfg=cfg)
@@ -1107,7 +1107,6 @@ def profile_only(args):
         # the practical HBM ceiling of the box: torch's device copy (read +
         # write), fill (write) and sum (read) over one fp32 [E, d, C] array of
         # config 2 (471 MB), event-timed
-        import json
         n = 36804 * 25 * 128
         a = torch.ones(n, device="cuda")
         b = torch.empty_like(a)
@@ -1145,6 +1144,10 @@ def profile_only(args):
         rw = reference_backbone_workload(args.dtype)
         for _ in range(args.reps):
             reference_backbone_pass(rw, True)
+    elif args.only == "ref-layer6":
+        # one layer at lmax = mmax = 6; prints its bench leg (no CPU baseline)
+        print(json.dumps(reference_backbone_leg(args.dtype, steps=args.reps, warmup=1, cpu=False, lmax=6,
+                                                layers=1)), flush=True)
     elif args.only == "basis-tzvpd":
         print(json.dumps(wide_basis_leg(reps=args.reps, cpu=False)), flush=True)
     elif args.only in ("fwd", "step"):
@@ -1186,7 +1189,7 @@ def main(argv=None):
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-extras", action="store_true", help="headline only")
     ap.add_argument("--only", choices=["fwd", "step", "basis", "copy", "hbm", "host", "embed", "edgewise", "edgewise-step",
-                                       "rotate", "basis5", "basis-tzvpd", "ref-backbone", "ceiling"],
+                                       "rotate", "basis5", "basis-tzvpd", "ref-backbone", "ref-layer6", "ceiling"],
                     help="profiling mode: run one piece a few times and exit (no JSON line)")
     ap.add_argument("--cfg", default="config2", choices=sorted(MESSAGE_CONFIGS),
                     help="message-block configuration of --only fwd / step")
@@ -1316,6 +1319,10 @@ def main(argv=None):
             print(f"[bench] reference layer loop (Edgewise x{REF_LAYERS}, lmax = mmax = 4, {dtn}) ...",
                   file=sys.stderr, flush=True)
             result[f"reference_backbone_{dtn}"] = reference_backbone_leg(dtn, cpu=(dtn == "fp32" and not args.no_cpu))
+        for dtn in ("fp32", "bf16"):
+            print(f"[bench] reference layer at lmax = mmax = 6 (Edgewise x1, {dtn}) ...", file=sys.stderr, flush=True)
+            result[f"reference_layer_l6_{dtn}"] = reference_backbone_leg(
+                dtn, steps=3, warmup=1, cpu=(dtn == "fp32" and not args.no_cpu), lmax=6, layers=1)
         print("[bench] library GEMM ceiling of the SO(2) shapes ...", file=sys.stderr, flush=True)
         result["library_gemm_ceiling"] = library_gemm_ceiling(("bf16",))
     if not args.no_cpu:

@@ -141,7 +141,7 @@ def test_edgewise_two_conv_matches_oracle(lmax, mmax, dtype, use_rad, device):
                                                   (4, 2, torch.bfloat16, "node"), (2, 2, torch.bfloat16, "edge"),
                                                   (6, 2, torch.bfloat16, "node"), (6, 2, torch.bfloat16, "edge"),
                                                   (4, 4, torch.float32, "node"), (4, 4, torch.bfloat16, "edge"),
-                                                  (6, 6, torch.float32, "node")])
+                                                  (6, 6, torch.float32, "node"), (6, 6, torch.bfloat16, "node")])
 def test_edgewise_gradients_match_oracle_autograd(lmax, mmax, dtype, mode, device):
     """Gradients of the two-convolution block (x, radial scales, both
     convolutions' weights and biases) against fp64 autograd of the oracle."""
