@@ -60,3 +60,49 @@ def test_edgewise_is_rotation_equivariant(lmax, mmax, mode, device):
     err = ((out_r - want).abs().max() / want.abs().max()).item()
     print(f"  relative equivariance error {err:.2e}", flush=True)
     assert err < 1e-5, err
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind", ["energy", "force"])
+def test_heads_are_rotation_invariant_and_equivariant(kind, device):
+    """The reference test's energy and force checks on the heads' message pass
+    (maloq_amd.heads): rotating the structure leaves the energies unchanged
+    and rotates the forces (the l = 1 rows of the node output) by D^1(R)."""
+    import types
+    from maloq_amd import heads
+    from maloq_amd.synth import batch_of_molecules
+    from maloq_amd.wigner import extract_euler_angles
+    lmax = mmax = 4
+    C = H = 32
+    bb = types.SimpleNamespace(sphere_channels=C, hidden_channels=H, lmax=lmax, mmax=mmax,
+                               edge_channels_list=[8, 32, 32])
+    torch.manual_seed(0)
+    mod = (heads.HELM_Energy_Head(bb) if kind == "energy" else heads.HELM_Force_Head(bb)).to(device)
+    g = batch_of_molecules(3, lambda m: 7 + 2 * m, ["H", "C", "O"], [0.5, 0.3, 0.2], 5.0)
+    gen = torch.Generator().manual_seed(2)
+    N, E, d = g.num_nodes, g.num_edges, (lmax + 1) ** 2
+    x = torch.randn(N, d, C, generator=gen, dtype=torch.float64)
+    x_edge = torch.randn(E, 8, generator=gen).to(device)
+    ei = torch.from_numpy(np.stack([g.src, g.dst])).to(device)
+    counts = [int(np.sum(g.mol == m)) for m in range(3)]
+    batch = types.SimpleNamespace(edge_index=ei[None], num_atoms_in_molecule=torch.tensor(counts))
+    vec = torch.from_numpy(g.edge_distance_vec())
+    a, b, c = -1.2, 0.4, 2.1
+    R = torch.from_numpy(_ry(a) @ _rx(b) @ _ry(c))
+    t = lambda v: torch.tensor([v], dtype=torch.float64)
+    jd = orot.load_jd()
+    Dfull = torch.block_diag(*[orot.wigner_D(l, t(a), t(b), t(c), jd)[0] for l in range(lmax + 1)])
+
+    def run(xx, vv):
+        eul = extract_euler_angles(vv.float().to(device), seed=5)
+        emb = {"node_embeddings": xx.float().to(device), "x_edge": x_edge}
+        with torch.no_grad():
+            res = mod(emb, batch, eulers=eul)
+        return res["energies" if kind == "energy" else "forces"].double().cpu()
+
+    out = run(x, vec)
+    out_r = run(torch.einsum("ij,njc->nic", Dfull, x), vec @ R.T)
+    want = out if kind == "energy" else out @ Dfull[1:4, 1:4].T
+    err = ((out_r - want).abs().max() / want.abs().max()).item()
+    print(f"heads {kind}: relative error under rotation {err:.2e}", flush=True)
+    assert err < 1e-5, err
