@@ -9,6 +9,8 @@
 //
 // Operators and the reference interfaces they stand in for:
 //   edge_euler(edge_vec, seed)                   wigner_fused.py:403-486 (angles)
+//   edge_vec_to_wigner(edge_vec, jd, lmax, seed, ..)  edge_vec_to_wigner_fused, wigner_fused.py:403-486,
+//                                                and the (wigner, wigner_inv) pair, esen_osh.py:266-296
 //   wigner_from_euler(eulers, lmax, inverse)     rotation.py:189-225 eulers_to_wigner
 //   rotate(x, eulers, gather?, lmax, inverse)    bmm(wigner, x[src]), esen_block.py:181,191
 //   segment_sum(msg, perm, seg_ptr, n)           index_add_, esen_block.py:205
@@ -199,6 +201,62 @@ at::Tensor edge_euler(const at::Tensor& edge_vec, int64_t seed) {
              "maloq_edge_euler");
   }
   return eulers;
+}
+
+// Dense block-diagonal Wigner-D [E, d, d] from edge vectors in one launch,
+// with the packed J_0..J_lmax given by the caller (its Jd): [D] or, with
+// with_inverse, [D, D^T]; with_eulers appends the Euler triples used [E, 3].
+std::vector<at::Tensor> edge_vec_to_wigner(const at::Tensor& edge_vec, const at::Tensor& jd, int64_t lmax,
+                                           int64_t seed, bool with_inverse, bool with_eulers) {
+  TORCH_CHECK_VALUE(lmax >= 0 && lmax <= 8, "lmax must be 0-8, got ", lmax);
+  TORCH_CHECK_VALUE(edge_vec.dim() == 2 && edge_vec.size(1) == 3, "edge_distance_vec must be [E, 3], got ",
+                    edge_vec.sizes());
+  TORCH_CHECK_VALUE(edge_vec.scalar_type() == at::kFloat, "the HIP Wigner backend computes in fp32; got ",
+                    edge_vec.scalar_type());
+  require_gpu(edge_vec, "edge_vec");
+  int64_t need = 0;
+  for (int64_t l = 0; l <= lmax; ++l) need += (2 * l + 1) * (2 * l + 1);
+  TORCH_CHECK_VALUE(jd.scalar_type() == at::kFloat && jd.is_contiguous() && jd.numel() >= need,
+                    "jd must hold the packed fp32 J_0..J_lmax (", need, " floats)");
+  same_device(edge_vec, {jd});
+  const c10::DeviceGuard guard(edge_vec.device());
+  const int64_t E = edge_vec.size(0), d = (lmax + 1) * (lmax + 1);
+  std::vector<at::Tensor> res{at::empty({E, d, d}, edge_vec.options())};
+  if (with_inverse) res.push_back(at::empty({E, d, d}, edge_vec.options()));
+  if (with_eulers) res.push_back(at::empty({E, 3}, edge_vec.options()));
+  if (E == 0) return res;
+  const at::Tensor v = edge_vec.contiguous();
+  check_rc(maloq_edge_vec_to_wigner(v.data_ptr<float>(), E, static_cast<uint64_t>(seed), static_cast<int>(lmax),
+                                    jd.data_ptr<float>(), with_eulers ? res.back().data_ptr<float>() : nullptr,
+                                    res[0].data_ptr<float>(), with_inverse ? res[1].data_ptr<float>() : nullptr, 1,
+                                    stream_of(v)),
+           "maloq_edge_vec_to_wigner");
+  return res;
+}
+
+// The same into a caller's out [E, d, d] (contiguous fp32): only the diagonal
+// blocks are written, as the reference's out= contract states.
+void edge_vec_to_wigner_out(const at::Tensor& edge_vec, const at::Tensor& jd, int64_t lmax, int64_t seed,
+                            const at::Tensor& out) {
+  TORCH_CHECK_VALUE(lmax >= 0 && lmax <= 8, "lmax must be 0-8, got ", lmax);
+  TORCH_CHECK_VALUE(edge_vec.dim() == 2 && edge_vec.size(1) == 3 && edge_vec.scalar_type() == at::kFloat,
+                    "edge_distance_vec must be float32 [E, 3]");
+  require_gpu(edge_vec, "edge_vec");
+  const int64_t E = edge_vec.size(0), d = (lmax + 1) * (lmax + 1);
+  TORCH_CHECK_VALUE(out.dim() == 3 && out.size(0) == E && out.size(1) == d && out.size(2) == d &&
+                        out.is_contiguous() && out.scalar_type() == at::kFloat,
+                    "out must be contiguous float32 [E, d, d]");
+  int64_t need = 0;
+  for (int64_t l = 0; l <= lmax; ++l) need += (2 * l + 1) * (2 * l + 1);
+  TORCH_CHECK_VALUE(jd.scalar_type() == at::kFloat && jd.is_contiguous() && jd.numel() >= need,
+                    "jd must hold the packed fp32 J_0..J_lmax (", need, " floats)");
+  same_device(edge_vec, {jd, out});
+  const c10::DeviceGuard guard(edge_vec.device());
+  if (E == 0) return;
+  const at::Tensor v = edge_vec.contiguous();
+  check_rc(maloq_edge_vec_to_wigner(v.data_ptr<float>(), E, static_cast<uint64_t>(seed), static_cast<int>(lmax),
+                                    jd.data_ptr<float>(), nullptr, out.data_ptr<float>(), nullptr, 0, stream_of(v)),
+           "maloq_edge_vec_to_wigner");
 }
 
 at::Tensor wigner_from_euler(const at::Tensor& eulers, int64_t lmax, bool inverse) {
@@ -758,6 +816,9 @@ at::Tensor pack_index_cpu(int64_t code, int64_t lmax, int64_t mmax, bool gate, i
 TORCH_LIBRARY(maloq_hip, m) {
   m.def("edge_euler(Tensor edge_vec, int seed) -> Tensor");
   m.def("wigner_from_euler(Tensor eulers, int lmax, bool inverse) -> Tensor");
+  m.def("edge_vec_to_wigner(Tensor edge_vec, Tensor jd, int lmax, int seed, bool with_inverse, bool with_eulers) "
+        "-> Tensor[]");
+  m.def("edge_vec_to_wigner_out(Tensor edge_vec, Tensor jd, int lmax, int seed, Tensor(a!) out) -> ()");
   m.def("rotate(Tensor x, Tensor eulers, Tensor? gather, int lmax, bool inverse) -> Tensor");
   m.def("segment_sum(Tensor msg, Tensor perm, Tensor seg_ptr, int num_segments) -> Tensor");
   m.def("label_transform(Tensor x, Tensor blocks, Tensor? w, Tensor sched, Tensor? perm_in, Tensor? perm_out, "
@@ -785,6 +846,8 @@ TORCH_LIBRARY(maloq_hip, m) {
 TORCH_LIBRARY_IMPL(maloq_hip, CUDA, m) {
   m.impl("edge_euler", &edge_euler);
   m.impl("wigner_from_euler", &wigner_from_euler);
+  m.impl("edge_vec_to_wigner", &edge_vec_to_wigner);
+  m.impl("edge_vec_to_wigner_out", &edge_vec_to_wigner_out);
   m.impl("rotate", &rotate);
   m.impl("segment_sum", &segment_sum);
   m.impl("label_transform", &label_transform);

@@ -9,6 +9,7 @@ implementation, so that ``torch.compile`` and other graph capture see single
 ops with known output shapes, and the autograd formulas.
 
     maloq_hip::edge_euler(edge_vec, seed)                 extract_euler_angles
+    maloq_hip::edge_vec_to_wigner(edge_vec, jd, ..)       edge_vec_to_wigner_fused, (wigner, wigner_inv)
     maloq_hip::wigner_from_euler(eulers, lmax, inverse)   eulers_to_wigner (dense D or D^T)
     maloq_hip::rotate(x, eulers, gather?, lmax, inverse)  bmm(wigner, x[src]) / bmm(wigner_inv, z)
     maloq_hip::segment_sum(msg, perm, seg_ptr, n)         index_add_ in a fixed order
@@ -49,6 +50,24 @@ _ops = torch.ops.maloq_hip
 # ------------------------------------------------------------------ Wigner
 edge_euler = _ops.edge_euler
 wigner_from_euler = _ops.wigner_from_euler
+edge_vec_to_wigner = _ops.edge_vec_to_wigner
+edge_vec_to_wigner_out = _ops.edge_vec_to_wigner_out
+
+
+@register_fake("maloq_hip::edge_vec_to_wigner")
+def _(edge_vec, jd, lmax, seed, with_inverse, with_eulers):
+    E, d = edge_vec.shape[0], (lmax + 1) ** 2
+    res = [edge_vec.new_empty(E, d, d)]
+    if with_inverse:
+        res.append(edge_vec.new_empty(E, d, d))
+    if with_eulers:
+        res.append(edge_vec.new_empty(E, 3))
+    return res
+
+
+@register_fake("maloq_hip::edge_vec_to_wigner_out")
+def _(edge_vec, jd, lmax, seed, out):
+    return None
 
 
 @register_fake("maloq_hip::edge_euler")

@@ -81,6 +81,13 @@ def extract_euler_angles(edge_distance_vec: torch.Tensor, seed: int) -> torch.Te
     return eulers
 
 
+def _seed64(seed) -> int:
+    """The seed as the kernels take it (64-bit, two's complement for negatives),
+    in the signed range the operators' int argument carries."""
+    u = int(seed) & (2**64 - 1)
+    return u - 2**64 if u >= 2**63 else u
+
+
 def edge_vec_to_wigner_fused(edge_distance_vec, Jd, lmax: int = 4, seed: int | None = None, out=None):
     """Block-diagonal Wigner-D [E, d, d] from edge vectors in one HIP launch."""
     assert 0 <= lmax <= 8, f"lmax must be 0-8, got {lmax}"
@@ -94,16 +101,14 @@ def edge_vec_to_wigner_fused(edge_distance_vec, Jd, lmax: int = 4, seed: int | N
         assert out.shape == (E, d, d), f"out shape {tuple(out.shape)} != expected ({E}, {d}, {d})"
         assert out.is_contiguous(), "out must be contiguous (row-major stride)"
         assert out.dtype == torch.float32, "out must be float32"
-        wigner, write_zeros = out, 0
-    else:
-        wigner, write_zeros = torch.empty(E, d, d, device=device, dtype=torch.float32), 1
     if E == 0:
-        return wigner
+        return out if out is not None else torch.empty(E, d, d, device=device, dtype=torch.float32)
+    from . import ops
     jd = _packed_jd(Jd, lmax, device)
-    v = edge_distance_vec.contiguous()
-    _lib.call("maloq_edge_vec_to_wigner", _lib.ptr(v), E, int(seed) & (2**64 - 1), lmax,
-              _lib.ptr(jd), None, _lib.ptr(wigner), None, write_zeros, _lib.stream_of(device))
-    return wigner
+    if out is not None:
+        ops.edge_vec_to_wigner_out(edge_distance_vec, jd, lmax, _seed64(seed), out)
+        return out
+    return ops.edge_vec_to_wigner(edge_distance_vec, jd, lmax, _seed64(seed), False, False)[0]
 
 
 def wigner_and_inverse(edge_distance_vec, Jd, lmax: int, seed: int | None = None, eulers_out=None):
@@ -114,15 +119,15 @@ def wigner_and_inverse(edge_distance_vec, Jd, lmax: int, seed: int | None = None
     E, d, device = edge_distance_vec.shape[0], (lmax + 1) ** 2, edge_distance_vec.device
     if seed is None:
         seed = random.randint(0, 2**31 - 1)
-    w = torch.empty(E, d, d, device=device, dtype=torch.float32)
-    wi = torch.empty_like(w)
-    if E > 0:
-        jd = _packed_jd(Jd, lmax, device)
-        v = edge_distance_vec.contiguous()
-        _lib.call("maloq_edge_vec_to_wigner", _lib.ptr(v), E, int(seed) & (2**64 - 1), lmax,
-                  _lib.ptr(jd), _lib.ptr(eulers_out), _lib.ptr(w), _lib.ptr(wi), 1,
-                  _lib.stream_of(device))
-    return w, wi
+    if E == 0:
+        w = torch.empty(E, d, d, device=device, dtype=torch.float32)
+        return w, torch.empty_like(w)
+    from . import ops
+    res = ops.edge_vec_to_wigner(edge_distance_vec, _packed_jd(Jd, lmax, device), lmax, _seed64(seed), True,
+                                 eulers_out is not None)
+    if eulers_out is not None:
+        eulers_out.copy_(res[2])
+    return res[0], res[1]
 
 
 def wigner_from_eulers(eulers: torch.Tensor, Jd, lmax: int, inverse: bool = False):

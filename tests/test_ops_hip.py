@@ -12,7 +12,7 @@ import torch
 
 def test_ops_are_registered():
     import maloq_amd.ops  # noqa: F401
-    for name in ("edge_euler", "wigner_from_euler", "rotate", "segment_sum", "label_transform",
+    for name in ("edge_euler", "wigner_from_euler", "edge_vec_to_wigner", "edge_vec_to_wigner_out", "rotate", "segment_sum", "label_transform",
                  "message_block_fwd", "message_block_bwd", "basis_row_meta", "fock_to_irreps", "irreps_to_fock"):
         assert hasattr(torch.ops.maloq_hip, name), name
 
@@ -25,6 +25,13 @@ def test_opcheck(device):
     torch.library.opcheck(ops.edge_euler, (vec, 7), test_utils=("test_schema", "test_faketensor"))
     eul = ops.edge_euler(vec, 7)
     torch.library.opcheck(ops.wigner_from_euler, (eul, 3, False), test_utils=("test_schema", "test_faketensor"))
+    from maloq_amd.wigner import _packed_jd
+    jd = _packed_jd(None, 3, vec.device)
+    for inv, with_e in ((False, False), (True, True)):
+        torch.library.opcheck(ops.edge_vec_to_wigner, (vec, jd, 3, 7, inv, with_e),
+                              test_utils=("test_schema", "test_faketensor"))
+    torch.library.opcheck(ops.edge_vec_to_wigner_out, (vec, jd, 3, 7, torch.zeros(50, 16, 16, device=device)),
+                          test_utils=("test_schema", "test_faketensor"))
     x = torch.randn(9, 16, 8, generator=gen).to(device).requires_grad_()
     gather = torch.randint(0, 9, (50,), generator=gen).to(device)
     torch.library.opcheck(ops.rotate, (x, eul, gather, 3, False),
