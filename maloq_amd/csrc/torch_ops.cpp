@@ -18,6 +18,8 @@
 //   message_block_fwd(x, rad?, w0, b0?, wm, ...) Edgewise.forward_node with one SO(2)
 //                                                convolution, esen_block.py:146-208
 //   message_block_bwd(grad_out, ...)             its autograd backward (so2_layers.py:139-214)
+//   edgewise_fwd / edgewise_bwd(...)             the two-convolution Edgewise (esen_block.py:146-258),
+//                                                node and edge modes, forward and gradients
 //   basis_row_meta(...)                          the row plan of the fused Fock transforms
 //   fock_to_irreps(fock, ...)                    matrix2label + get_net_out,
 //                                                fock_targets_batched.py:335-464
@@ -175,7 +177,13 @@ const at::Tensor& pack_index_on(int code, int lmax, int mmax, bool gate, int c_i
   auto it = cache->find(key);
   if (it == cache->end()) {
     int64_t tot = 0;
-    std::vector<int64_t> idx = pack_index(code, lmax, mmax, gate, c_in, c_out, mode, &tot);
+    // mode 2: the transposed index, then the forward one (both packings from
+    // one launch; the transposed part, which a caller keeps, starts the buffer)
+    std::vector<int64_t> idx = pack_index(code, lmax, mmax, gate, c_in, c_out, mode == 2 ? 1 : mode, &tot);
+    if (mode == 2) {
+      std::vector<int64_t> f0 = pack_index(code, lmax, mmax, gate, c_in, c_out, 0, &tot);
+      idx.insert(idx.end(), f0.begin(), f0.end());
+    }
     for (int64_t v : idx) TORCH_CHECK(v >= 0 && v < tot, "weight packing index out of range");
     at::Tensor host = at::from_blob(idx.data(), {static_cast<int64_t>(idx.size())}, at::kLong).clone();
     it = cache->emplace(key, std::make_pair(host.to(dev), tot)).first;
@@ -485,6 +493,8 @@ at::Tensor edge_rows(int64_t E, int64_t rows, int64_t c, const at::TensorOptions
   return t;
 }
 
+// Weights in the kernels' fragment order: mode 0 the forward GEMM's, 1 the
+// input gradient's transposed GEMM's, 2 both in one launch (transposed first).
 at::Tensor pack_weights(int code, int64_t lmax, int64_t mmax, bool gate, int64_t c_in, int64_t c_out, int mode,
                         const at::Tensor& w0, at::TensorList wm, at::ScalarType dt) {
   int64_t total = 0;
@@ -501,9 +511,12 @@ at::Tensor pack_weights(int code, int64_t lmax, int64_t mmax, bool gate, int64_t
     sn.push_back(t.numel());
   }
   TORCH_CHECK_VALUE(have == total, "weight shapes do not match (lmax, mmax, channels)");
-  const int64_t c_k = mode == 0 ? c_in : c_out, c_n = mode == 0 ? c_out : c_in;
-  const int64_t want = maloq_message_wpack_bytes(code, static_cast<int>(lmax), static_cast<int>(mmax), gate,
-                                                 static_cast<int>(c_k), static_cast<int>(c_n));
+  // bytes: the forward packing (c_in -> c_out), the transposed one (c_out -> c_in), or both
+  const int64_t fwd_b = maloq_message_wpack_bytes(code, static_cast<int>(lmax), static_cast<int>(mmax), gate,
+                                                  static_cast<int>(c_in), static_cast<int>(c_out));
+  const int64_t tr_b = maloq_message_wpack_bytes(code, static_cast<int>(lmax), static_cast<int>(mmax), gate,
+                                                 static_cast<int>(c_out), static_cast<int>(c_in));
+  const int64_t want = mode == 0 ? fwd_b : (mode == 1 ? tr_b : fwd_b + tr_b);
   at::Tensor wpack = at::empty({idx.numel()}, w0.options().dtype(dt));
   TORCH_CHECK(wpack.numel() * wpack.element_size() == want, "packed weight size mismatch");
   check_rc(maloq_message_pack(code, static_cast<int>(sp.size()), sp.data(), sn.data(), idx.data_ptr<int64_t>(),
@@ -540,6 +553,67 @@ int dw_splits(bool bf16, int64_t lmax, int64_t mmax, bool gate, int64_t c_out, i
     }
   }
   return best;
+}
+
+// Weight and bias gradients of one SO(2) convolution from the saved rows:
+// [dW0, db0, dW_1 .. dW_mmax] (fp32, zeros for a graph without edges).  dz the
+// output-row gradients [*, d' (+ lmax gated), c_out], y the input rows
+// [*, d', c_in], both in the forward's dtype with E valid rows (bf16: the
+// padded workspaces of maloq_message_edge_rows).  Split-K over the edges,
+// partials summed in split order (deterministic).
+std::vector<at::Tensor> weight_grads(const at::Tensor& dz, const at::Tensor& y, int64_t E, int64_t lmax,
+                                     int64_t mmax, int64_t c_out, int64_t c_in, bool gate) {
+  const auto dt = dz.scalar_type();
+  const int code = dtype_code(dt);
+  const auto opt32 = dz.options().dtype(at::kFloat);
+  const int64_t extra = gate ? lmax * c_out : 0;
+  const int kr = maloq_message_kept_rows(static_cast<int>(lmax), static_cast<int>(mmax));
+  std::vector<at::Tensor> res;
+  if (E == 0) {
+    res.push_back(at::zeros({extra + (lmax + 1) * c_out, (lmax + 1) * c_in}, opt32));
+    res.push_back(at::zeros({extra + (lmax + 1) * c_out}, opt32));
+    for (int64_t m = 1; m <= mmax; ++m) res.push_back(at::zeros({2 * (lmax - m + 1) * c_out, (lmax - m + 1) * c_in}, opt32));
+    return res;
+  }
+  TORCH_CHECK(y.scalar_type() == dt && dz.size(0) >= E && y.size(0) >= E, "weight gradient: bad saved rows");
+  if (dt == at::kBFloat16)
+    TORCH_CHECK(dz.size(0) >= maloq_message_edge_rows(E) && y.size(0) == dz.size(0),
+                "bf16 weight gradient needs the padded workspaces");
+  void* st = stream_of(dz);
+  const int cus = at::cuda::getDeviceProperties(dz.device().index())->multiProcessorCount;
+  const int splits = dw_splits(dt == at::kBFloat16, lmax, mmax, gate, c_out, c_in, E, cus);
+  const int64_t dp = maloq_message_dw_partials_floats(static_cast<int>(lmax), static_cast<int>(mmax), gate ? 1 : 0,
+                                                      static_cast<int>(c_out), static_cast<int>(c_in), splits);
+  at::Tensor dparts = at::empty({dp > 1 ? dp : 1}, opt32);
+  at::Tensor dw0 = at::empty({extra + (lmax + 1) * c_out, (lmax + 1) * c_in}, opt32);
+  std::vector<at::Tensor> dwm;
+  std::vector<float*> dptr;
+  for (int64_t m = 1; m <= mmax; ++m) {
+    dwm.push_back(at::empty({2 * (lmax - m + 1) * c_out, (lmax - m + 1) * c_in}, opt32));
+    dptr.push_back(dwm.back().data_ptr<float>());
+  }
+  if (dptr.empty()) dptr.push_back(nullptr);
+  check_rc(maloq_message_dw(code, static_cast<int>(lmax), static_cast<int>(mmax), gate ? 1 : 0, dz.data_ptr(),
+                            y.data_ptr(), E, static_cast<int>(c_out), static_cast<int>(c_in), splits,
+                            dparts.data_ptr<float>(), dw0.data_ptr<float>(), dptr.data(), st),
+           "maloq_message_dw");
+  at::Tensor db0 = at::empty({extra + (lmax + 1) * c_out}, opt32);
+  const int rpe = static_cast<int>(dz.size(1));
+  // (first row, rows, output offset): the m = 0 rows, then a gated block's gate rows
+  std::vector<std::tuple<int, int, int64_t>> groups{{0, static_cast<int>(lmax + 1), extra}};
+  if (gate) groups.emplace_back(kr, static_cast<int>(lmax), 0);
+  int64_t cs_n = 1;
+  for (const auto& gr : groups)
+    cs_n = std::max(cs_n, maloq_message_colsum_partials_floats(std::get<1>(gr), static_cast<int>(c_out), E));
+  at::Tensor cs = at::empty({cs_n}, opt32);
+  for (const auto& gr : groups)
+    check_rc(maloq_message_colsum(code, dz.data_ptr(), rpe, std::get<0>(gr), std::get<1>(gr), static_cast<int>(c_out),
+                                  E, cs.data_ptr<float>(), db0.data_ptr<float>() + std::get<2>(gr), st),
+             "maloq_message_colsum");
+  res.push_back(dw0);
+  res.push_back(db0);
+  for (auto& t : dwm) res.push_back(t);
+  return res;
 }
 
 // Gradients of message_block_fwd from its saved rows: [grad_x fp32 [N, d, c_in],
@@ -603,49 +677,255 @@ std::vector<at::Tensor> message_block_bwd(const at::Tensor& grad_out, const c10:
                                 dz.data_ptr(), gate ? g->data_ptr() : nullptr, st),
            "maloq_message_bwd_dx");
   // weight and bias gradients
-  const int64_t extra = gate ? lmax * c_out : 0;
-  at::Tensor dw0, db0;
-  std::vector<at::Tensor> dwm;
-  if (E == 0) {
-    dw0 = at::zeros({extra + (lmax + 1) * c_out, (lmax + 1) * c_in}, opt32);
-    for (int64_t m = 1; m <= mmax; ++m) dwm.push_back(at::zeros({2 * (lmax - m + 1) * c_out, (lmax - m + 1) * c_in}, opt32));
-    db0 = at::zeros({extra + (lmax + 1) * c_out}, opt32);
-  } else {
-    if (dt == at::kBFloat16)
-      TORCH_CHECK(dz.size(0) >= maloq_message_edge_rows(E) && y.size(0) == dz.size(0),
-                  "bf16 weight gradient needs the padded workspaces");
-    const int cus = at::cuda::getDeviceProperties(grad_out.device().index())->multiProcessorCount;
-    const int splits = dw_splits(dt == at::kBFloat16, lmax, mmax, gate, c_out, c_in, E, cus);
-    const int64_t dp = maloq_message_dw_partials_floats(static_cast<int>(lmax), static_cast<int>(mmax), gate ? 1 : 0,
-                                                        static_cast<int>(c_out), static_cast<int>(c_in), splits);
-    at::Tensor dparts = at::empty({dp > 1 ? dp : 1}, opt32);
-    dw0 = at::empty({extra + (lmax + 1) * c_out, (lmax + 1) * c_in}, opt32);
-    std::vector<float*> dptr;
-    for (int64_t m = 1; m <= mmax; ++m) {
-      dwm.push_back(at::empty({2 * (lmax - m + 1) * c_out, (lmax - m + 1) * c_in}, opt32));
-      dptr.push_back(dwm.back().data_ptr<float>());
-    }
-    if (dptr.empty()) dptr.push_back(nullptr);
-    check_rc(maloq_message_dw(code, static_cast<int>(lmax), static_cast<int>(mmax), gate ? 1 : 0, dz.data_ptr(),
-                              y.data_ptr(), E, static_cast<int>(c_out), static_cast<int>(c_in), splits,
-                              dparts.data_ptr<float>(), dw0.data_ptr<float>(), dptr.data(), st),
-             "maloq_message_dw");
-    db0 = at::empty({extra + (lmax + 1) * c_out}, opt32);
-    const int rpe = static_cast<int>(dz.size(1));
-    // (first row, rows, output offset): the m = 0 rows, then a gated block's gate rows
-    std::vector<std::tuple<int, int, int64_t>> groups{{0, static_cast<int>(lmax + 1), extra}};
-    if (gate) groups.emplace_back(kr, static_cast<int>(lmax), 0);
-    int64_t cs_n = 1;
-    for (const auto& gr : groups)
-      cs_n = std::max(cs_n, maloq_message_colsum_partials_floats(std::get<1>(gr), static_cast<int>(c_out), E));
-    at::Tensor cs = at::empty({cs_n}, opt32);
-    for (const auto& gr : groups)
-      check_rc(maloq_message_colsum(code, dz.data_ptr(), rpe, std::get<0>(gr), std::get<1>(gr), static_cast<int>(c_out),
-                                    E, cs.data_ptr<float>(), db0.data_ptr<float>() + std::get<2>(gr), st),
-               "maloq_message_colsum");
+  std::vector<at::Tensor> wg = weight_grads(dz, y, E, lmax, mmax, c_out, c_in, gate);
+  std::vector<at::Tensor> res{gx, grad_rad};
+  for (auto& t : wg) res.push_back(t);
+  return res;
+}
+
+// ------------------------------------------------ two-convolution Edgewise
+// The reference's Edgewise (esen_block.py:146-258): message cat(x[src],
+// x[dst] [, x_message_edge]), gated SO(2) conv1 (radial scales), conv2, back to
+// the global frame and summed per destination node (node mode) or kept per
+// edge (edge mode, original edge order).  The graph arrives as the plan's
+// dst-sorted arrays (src, dst, seg_ptr) with perm (dst-sorted position ->
+// original edge); the frames as dst-sorted Euler triples or as the
+// reference's dense wigner [E, d, d] in the original order.  Returns [out, y,
+// r, z, dk, g, wp1t, wp2t]: the workspaces the backward reads and, with save,
+// both convolutions' transposed weight packings (empty when not kept).
+std::vector<at::Tensor> edgewise_fwd(const at::Tensor& x, const c10::optional<at::Tensor>& rad, const at::Tensor& w01,
+                                     const c10::optional<at::Tensor>& b01, at::TensorList wm1, const at::Tensor& w02,
+                                     const c10::optional<at::Tensor>& b02, at::TensorList wm2, const at::Tensor& src,
+                                     const at::Tensor& dst, const at::Tensor& seg_ptr, const at::Tensor& perm,
+                                     const c10::optional<at::Tensor>& eulers, const c10::optional<at::Tensor>& wigner,
+                                     const c10::optional<at::Tensor>& x_message_edge,
+                                     const c10::optional<at::Tensor>& wpack1_in,
+                                     const c10::optional<at::Tensor>& wpack2_in, int64_t lmax, int64_t mmax,
+                                     bool edge_mode, bool save) {
+  const auto dt = x.scalar_type();
+  const int code = dtype_code(dt);
+  require_gpu(x, "x");
+  require_gpu(w01, "w01");
+  TORCH_CHECK_VALUE(maloq_message_supported(static_cast<int>(lmax), static_cast<int>(mmax)),
+                    "no message kernels for lmax=", lmax, ", mmax=", mmax);
+  const int64_t d = (lmax + 1) * (lmax + 1);
+  TORCH_CHECK_VALUE(x.dim() == 3 && x.size(1) == d, "x must be [N, (lmax+1)^2, C]");
+  TORCH_CHECK_VALUE(eulers.has_value() != wigner.has_value(), "give exactly one of eulers and wigner");
+  TORCH_CHECK_VALUE(src.scalar_type() == at::kInt && dst.scalar_type() == at::kInt &&
+                        seg_ptr.scalar_type() == at::kLong && perm.scalar_type() == at::kLong,
+                    "the plan's src/dst must be int32, seg_ptr and perm int64");
+  const int64_t E = src.numel();
+  TORCH_CHECK_VALUE(dst.numel() == E && perm.numel() == E, "src, dst and perm must have one entry per edge");
+  TORCH_CHECK_VALUE(static_cast<int64_t>(wm1.size()) >= mmax && static_cast<int64_t>(wm2.size()) >= mmax,
+                    "wm1 and wm2 need mmax weights each");
+  same_device(x, {rad, w01, b01, w02, b02, src, dst, seg_ptr, perm, eulers, wigner, x_message_edge, wpack1_in,
+                  wpack2_in});
+  for (int64_t m = 0; m < mmax; ++m) same_device(x, {wm1[m], wm2[m]});
+  const c10::DeviceGuard guard(x.device());
+  const int64_t c_x = x.size(2), c_hidden = w01.size(0) / (2 * lmax + 1), c_out = w02.size(0) / (lmax + 1);
+  const int64_t npart = x_message_edge.has_value() ? 3 : 2;
+  const int kr = maloq_message_kept_rows(static_cast<int>(lmax), static_cast<int>(mmax));
+  const at::Device dev = x.device();
+  const auto opt32 = x.options().dtype(at::kFloat);
+  void* st = stream_of(x);
+  at::Tensor xm;
+  if (x_message_edge.has_value()) {
+    TORCH_CHECK_VALUE(x_message_edge->dim() == 3 && x_message_edge->size(0) == E && x_message_edge->size(1) == d &&
+                          x_message_edge->size(2) == c_x,
+                      "x_message_edge must be [E, d, C]");
+    xm = x_message_edge->to(dt).contiguous();
   }
-  std::vector<at::Tensor> res{gx, grad_rad, dw0, db0};
-  for (auto& t : dwm) res.push_back(t);
+  // with save, both packings of each convolution from one launch: the
+  // transposed ones are returned for the backward
+  // (a caller may pass the forward packings of fixed weights instead)
+  auto packs = [&](bool gate, int64_t ci, int64_t co, const at::Tensor& w0, at::TensorList wm,
+                   const c10::optional<at::Tensor>& given) {
+    const int64_t fb = maloq_message_wpack_bytes(code, static_cast<int>(lmax), static_cast<int>(mmax), gate,
+                                                 static_cast<int>(ci), static_cast<int>(co));
+    if (given.has_value() && !save) {
+      TORCH_CHECK_VALUE(given->scalar_type() == dt && given->is_contiguous() &&
+                            given->numel() * given->element_size() == fb,
+                        "weight packing of the wrong size");
+      return std::make_pair(*given, at::empty({0}, given->options()));
+    }
+    const at::Tensor p = pack_weights(code, lmax, mmax, gate, ci, co, save ? 2 : 0, w0, wm, dt);
+    if (!save) return std::make_pair(p, at::empty({0}, p.options()));
+    const int64_t n0 = fb / p.element_size(), n1 = p.numel() - n0;
+    return std::make_pair(p.narrow(0, n1, n0), p.narrow(0, 0, n1));
+  };
+  const auto pk1 = packs(true, npart * c_x, c_hidden, w01, wm1, wpack1_in);
+  const auto pk2 = packs(false, c_hidden, c_out, w02, wm2, wpack2_in);
+  const at::Tensor& wpack1 = pk1.first;
+  const at::Tensor& wpack2 = pk2.first;
+  // output rows: nodes, or one per edge (each edge its own segment)
+  const int64_t num_nodes = seg_ptr.numel() - 1;
+  at::Tensor seg_id, sp = seg_ptr;
+  int64_t rows = num_nodes;
+  if (edge_mode) {
+    rows = E;
+    seg_id = at::arange(E, x.options().dtype(at::kInt));
+    sp = at::arange(E + 1, x.options().dtype(at::kLong));
+  }
+  at::Tensor out = at::empty({rows, d, c_out}, opt32);
+  const int64_t pf = maloq_message_partials_floats(static_cast<int>(lmax), 0, E, static_cast<int>(c_out));
+  at::Tensor parts = at::empty({pf > 1 ? pf : 1}, opt32);
+  at::Tensor radc;
+  if (rad.has_value()) {
+    int64_t rw = 0;
+    for (int64_t m = 0; m <= mmax; ++m) rw += (lmax - m + 1) * npart * c_x;
+    TORCH_CHECK_VALUE(rad->dim() == 2 && rad->size(0) == E && rad->size(1) == rw,
+                      "rad must be [E, sum_m (lmax-m+1) npart C]");
+    radc = rad->to(dt).contiguous();
+  }
+  const int64_t E1 = E > 1 ? E : 1;
+  at::Tensor y = save ? edge_rows(E, kr, npart * c_x, x.options()) : at::empty({E1, kr, npart * c_x}, x.options());
+  at::Tensor z = save ? edge_rows(E, kr, c_hidden, x.options()) : at::empty({E1, kr, c_hidden}, x.options());
+  at::Tensor r = (save && rad.has_value()) ? at::empty({E1, kr, npart * c_x}, x.options()) : at::empty({0}, x.options());
+  const int ws = maloq_message_wigner_floats(static_cast<int>(lmax), static_cast<int>(mmax));
+  at::Tensor dk = at::empty({E1, ws}, opt32), eul;
+  if (wigner.has_value()) {
+    TORCH_CHECK_VALUE(wigner->dim() == 3 && wigner->size(0) == E && wigner->size(1) == d && wigner->size(2) == d,
+                      "wigner must be [E, d, d]");
+    const at::Tensor w = wigner->to(at::kFloat).contiguous();
+    if (E > 0)
+      check_rc(maloq_message_wigner_rows(static_cast<int>(lmax), static_cast<int>(mmax), w.data_ptr<float>(),
+                                         perm.data_ptr<int64_t>(), E, dk.data_ptr<float>(), st),
+               "maloq_message_wigner_rows");
+  } else {
+    TORCH_CHECK_VALUE(eulers->dim() == 2 && eulers->size(0) == E && eulers->size(1) == 3,
+                      "eulers must be [E, 3] (dst-sorted)");
+    eul = eulers->to(at::kFloat).contiguous();
+  }
+  at::Tensor g = save ? at::empty({E1, kr + lmax, c_hidden}, x.options()) : at::empty({0}, x.options());
+  at::Tensor b1, b2;
+  if (b01.has_value()) b1 = b01->to(at::kFloat).contiguous();
+  if (b02.has_value()) b2 = b02->to(at::kFloat).contiguous();
+  const at::Tensor mrow = xm.defined() ? perm.to(at::kInt).contiguous() : at::Tensor();
+  const at::Tensor xc = x.contiguous();
+  check_rc(maloq_message_edgewise_fwd(
+               code, static_cast<int>(lmax), static_cast<int>(mmax), xc.data_ptr(), static_cast<int>(c_x),
+               src.data_ptr<int32_t>(), dst.data_ptr<int32_t>(), seg_id.defined() ? seg_id.data_ptr<int32_t>() : nullptr,
+               E, eul.defined() ? eul.data_ptr<float>() : nullptr, radc.defined() ? radc.data_ptr() : nullptr,
+               wpack1.data_ptr(), b1.defined() ? b1.data_ptr<float>() : nullptr, static_cast<int>(c_hidden),
+               wpack2.data_ptr(), b2.defined() ? b2.data_ptr<float>() : nullptr, jd_on(dev), out.data_ptr<float>(),
+               rows, static_cast<int>(c_out), sp.data_ptr<int64_t>(), parts.data_ptr<float>(), y.data_ptr(),
+               r.numel() ? r.data_ptr() : nullptr, dk.data_ptr<float>(), g.numel() ? g.data_ptr() : nullptr,
+               z.data_ptr(), xm.defined() ? xm.data_ptr() : nullptr, mrow.defined() ? mrow.data_ptr<int32_t>() : nullptr,
+               st),
+           "maloq_message_edgewise_fwd");
+  if (edge_mode) {
+    // dst-sorted position p holds original edge perm[p]
+    at::Tensor per_edge = at::empty_like(out);
+    per_edge.index_copy_(0, perm, out);
+    out = per_edge;
+  }
+  return {out, y, r, z, dk, g, pk1.second, pk2.second};
+}
+
+// Gradients of edgewise_fwd from its saved rows: [grad_x fp32 [N, d, c_x],
+// grad_rad (empty unless asked), grad_x_message_edge (original edge order,
+// empty for two-part messages), then for conv1 and conv2 in turn dW0, db0,
+// dW_1 .. dW_mmax (fp32; both empty lists' worth of empties when not asked)].
+std::vector<at::Tensor> edgewise_bwd(const at::Tensor& grad_out, const c10::optional<at::Tensor>& rad,
+                                     const at::Tensor& w01, at::TensorList wm1, const at::Tensor& w02,
+                                     at::TensorList wm2, const at::Tensor& dst, const at::Tensor& bwd_src,
+                                     const at::Tensor& bwd_eidx, const at::Tensor& perm, const at::Tensor& seg_ptr,
+                                     const at::Tensor& seg_ptr_src, const at::Tensor& y,
+                                     const c10::optional<at::Tensor>& r, const at::Tensor& z, const at::Tensor& dk,
+                                     const at::Tensor& g, const c10::optional<at::Tensor>& wpack1_t,
+                                     const c10::optional<at::Tensor>& wpack2_t, int64_t num_nodes, int64_t c_x,
+                                     int64_t lmax, int64_t mmax, bool edge_mode, int64_t parts, bool need_rad_grad,
+                                     bool need_w1, bool need_w2) {
+  const auto dt = y.scalar_type();
+  const int code = dtype_code(dt);
+  require_gpu(grad_out, "grad_out");
+  TORCH_CHECK_VALUE(maloq_message_supported(static_cast<int>(lmax), static_cast<int>(mmax)),
+                    "no message kernels for lmax=", lmax, ", mmax=", mmax);
+  TORCH_CHECK_VALUE(parts == 2 || parts == 3, "parts must be 2 or 3");
+  const int64_t d = (lmax + 1) * (lmax + 1), E = dst.numel();
+  TORCH_CHECK_VALUE(dst.scalar_type() == at::kInt && bwd_src.scalar_type() == at::kInt &&
+                        bwd_eidx.scalar_type() == at::kInt && perm.scalar_type() == at::kLong &&
+                        seg_ptr.scalar_type() == at::kLong && seg_ptr_src.scalar_type() == at::kLong,
+                    "plan arrays: dst, bwd_src, bwd_eidx int32; perm, seg_ptr, seg_ptr_src int64");
+  TORCH_CHECK_VALUE(bwd_src.numel() == E && bwd_eidx.numel() == E && perm.numel() == E,
+                    "the plan arrays must have one entry per edge");
+  TORCH_CHECK_VALUE(seg_ptr.numel() == num_nodes + 1 && seg_ptr_src.numel() == num_nodes + 1,
+                    "seg_ptr and seg_ptr_src must hold num_nodes + 1 offsets");
+  TORCH_CHECK_VALUE(grad_out.dim() == 3 && grad_out.size(0) == (edge_mode ? E : num_nodes) && grad_out.size(1) == d,
+                    "grad_out must be [rows, d, C]");
+  TORCH_CHECK_VALUE(y.size(0) >= E && z.size(0) >= E && dk.size(0) >= E && g.size(0) >= E,
+                    "the saved rows must cover every edge");
+  TORCH_CHECK_VALUE(static_cast<int64_t>(wm1.size()) >= mmax && static_cast<int64_t>(wm2.size()) >= mmax,
+                    "wm1 and wm2 need mmax weights each");
+  same_device(grad_out, {rad, w01, w02, dst, bwd_src, bwd_eidx, perm, seg_ptr, seg_ptr_src, y, r, z, dk, g,
+                         wpack1_t, wpack2_t});
+  for (int64_t m = 0; m < mmax; ++m) same_device(grad_out, {wm1[m], wm2[m]});
+  const c10::DeviceGuard guard(grad_out.device());
+  const int64_t c_hidden = w01.size(0) / (2 * lmax + 1);
+  const int kr = maloq_message_kept_rows(static_cast<int>(lmax), static_cast<int>(mmax));
+  const auto opt32 = grad_out.options().dtype(at::kFloat);
+  void* st = stream_of(grad_out);
+  // the forward's transposed packings, or packed here
+  auto given = [&](const c10::optional<at::Tensor>& p, bool gate, int64_t ci, int64_t co) {
+    if (!p.has_value() || p->numel() == 0) return false;
+    const int64_t b = maloq_message_wpack_bytes(code, static_cast<int>(lmax), static_cast<int>(mmax), gate,
+                                                static_cast<int>(co), static_cast<int>(ci));
+    TORCH_CHECK_VALUE(p->scalar_type() == dt && p->is_contiguous() && p->numel() * p->element_size() == b,
+                      "transposed weight packing of the wrong size");
+    return true;
+  };
+  const at::Tensor wp1t = given(wpack1_t, true, parts * c_x, c_hidden)
+                              ? *wpack1_t : pack_weights(code, lmax, mmax, true, parts * c_x, c_hidden, 1, w01, wm1, dt);
+  const at::Tensor wp2t = given(wpack2_t, false, c_hidden, c_x)
+                              ? *wpack2_t : pack_weights(code, lmax, mmax, false, c_hidden, c_x, 1, w02, wm2, dt);
+  at::Tensor gq = grad_out.to(at::kFloat).contiguous(), grad_row;
+  if (edge_mode) {
+    gq = gq.index_select(0, perm);   // per-edge gradient rows in dst-sorted order
+    grad_row = at::arange(E, grad_out.options().dtype(at::kInt));
+  }
+  at::Tensor gxs = at::empty({num_nodes, d, c_x}, opt32), gxd = at::empty({num_nodes, d, c_x}, opt32);
+  const int64_t E1 = E > 1 ? E : 1;
+  at::Tensor gxm, edge_seg;
+  if (parts == 3) {
+    gxm = at::empty({E1, d, c_x}, opt32);
+    edge_seg = at::arange(E, grad_out.options().dtype(at::kInt));
+  }
+  const int64_t pf = maloq_message_partials_floats(static_cast<int>(lmax), 1, E, static_cast<int>(c_x));
+  at::Tensor pbuf = at::empty({pf > 1 ? pf : 1}, opt32);
+  at::Tensor radc, grad_rad = at::empty({0}, opt32);
+  if (rad.has_value()) {
+    radc = rad->to(dt).contiguous();
+    if (need_rad_grad) grad_rad = at::empty_like(radc);
+  }
+  at::Tensor dz2 = edge_rows(E, kr, c_x, y.options()), dz1 = edge_rows(E, kr + lmax, c_hidden, y.options());
+  const bool has_r = r.has_value() && r->numel() > 0;
+  check_rc(maloq_message_edgewise_bwd_dx(
+               code, static_cast<int>(lmax), static_cast<int>(mmax), gq.data_ptr<float>(), static_cast<int>(c_x),
+               dst.data_ptr<int32_t>(), grad_row.defined() ? grad_row.data_ptr<int32_t>() : nullptr,
+               bwd_src.data_ptr<int32_t>(), bwd_eidx.data_ptr<int32_t>(), E, dk.data_ptr<float>(),
+               radc.defined() ? radc.data_ptr() : nullptr, grad_rad.numel() ? grad_rad.data_ptr() : nullptr,
+               has_r ? r->data_ptr() : nullptr, g.data_ptr(), wp1t.data_ptr(), static_cast<int>(c_hidden),
+               wp2t.data_ptr(), jd_on(grad_out.device()), gxs.data_ptr<float>(), gxd.data_ptr<float>(), num_nodes,
+               seg_ptr.data_ptr<int64_t>(), seg_ptr_src.data_ptr<int64_t>(), pbuf.data_ptr<float>(), dz2.data_ptr(),
+               dz1.data_ptr(), edge_seg.defined() ? edge_seg.data_ptr<int32_t>() : nullptr,
+               gxm.defined() ? gxm.data_ptr<float>() : nullptr, st),
+           "maloq_message_edgewise_bwd_dx");
+  at::Tensor gx = gxs.add_(gxd);
+  at::Tensor gm = at::empty({0}, opt32);
+  if (parts == 3) {
+    gm = at::empty({E, d, c_x}, opt32);
+    gm.index_copy_(0, perm, gxm.narrow(0, 0, E));   // dst-sorted position p holds original edge perm[p]
+  }
+  std::vector<at::Tensor> res{gx, grad_rad, gm};
+  auto add = [&](bool need, const at::Tensor& dz, const at::Tensor& rows, int64_t co, int64_t ci, bool gate) {
+    if (need) {
+      for (auto& t : weight_grads(dz, rows, E, lmax, mmax, co, ci, gate)) res.push_back(t);
+    } else {
+      for (int64_t k = 0; k < 2 + mmax; ++k) res.push_back(at::empty({0}, opt32));
+    }
+  };
+  add(need_w1, dz1, y, c_hidden, parts * c_x, true);
+  add(need_w2, dz2, z, c_x, c_hidden, false);
   return res;
 }
 
@@ -828,6 +1108,14 @@ TORCH_LIBRARY(maloq_hip, m) {
   m.def("message_block_bwd(Tensor grad_out, Tensor? rad, Tensor w0, Tensor[] wm, Tensor bwd_src, "
         "Tensor bwd_dst, Tensor bwd_eidx, Tensor seg_ptr_src, Tensor y, Tensor dk, Tensor? r, Tensor? g, "
         "int num_nodes, int c_in, int lmax, int mmax, bool gate, bool need_rad_grad) -> Tensor[]");
+  m.def("edgewise_fwd(Tensor x, Tensor? rad, Tensor w01, Tensor? b01, Tensor[] wm1, Tensor w02, Tensor? b02, "
+        "Tensor[] wm2, Tensor src, Tensor dst, Tensor seg_ptr, Tensor perm, Tensor? eulers, Tensor? wigner, "
+        "Tensor? x_message_edge, Tensor? wpack1, Tensor? wpack2, int lmax, int mmax, bool edge_mode, bool save) "
+        "-> Tensor[]");
+  m.def("edgewise_bwd(Tensor grad_out, Tensor? rad, Tensor w01, Tensor[] wm1, Tensor w02, Tensor[] wm2, "
+        "Tensor dst, Tensor bwd_src, Tensor bwd_eidx, Tensor perm, Tensor seg_ptr, Tensor seg_ptr_src, Tensor y, "
+        "Tensor? r, Tensor z, Tensor dk, Tensor g, Tensor? wpack1_t, Tensor? wpack2_t, int num_nodes, int c_x, "
+        "int lmax, int mmax, bool edge_mode, int parts, bool need_rad_grad, bool need_w1, bool need_w2) -> Tensor[]");
   m.def("basis_row_meta(int ld, Tensor? block_data_offsets, Tensor off, Tensor Z, Tensor rows, Tensor cols, "
         "Tensor pair_kind, int maxe) -> Tensor");
   m.def("fock_to_irreps(Tensor fock, int ld, Tensor? block_data_offsets, Tensor? off, Tensor? Z, Tensor? rows, "
@@ -853,6 +1141,8 @@ TORCH_LIBRARY_IMPL(maloq_hip, CUDA, m) {
   m.impl("label_transform", &label_transform);
   m.impl("message_block_fwd", &message_block_fwd);
   m.impl("message_block_bwd", &message_block_bwd);
+  m.impl("edgewise_fwd", &edgewise_fwd);
+  m.impl("edgewise_bwd", &edgewise_bwd);
   m.impl("basis_row_meta", &basis_row_meta);
   m.impl("fock_to_irreps", &fock_to_irreps);
   m.impl("irreps_to_fock", &irreps_to_fock);

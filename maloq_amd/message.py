@@ -375,186 +375,98 @@ def edgewise_forward(x, plan, eulers, rad, conv1, conv2, lmax, mmax, wpack1=None
     scaled message rows), "r" (unscaled, when ``rad`` is given), "z" (the
     gated rows [E, d', c_hidden]), "dk" and "g" (the first convolution's
     pre-activations); "y" and "z" with the zeroed padding rows of
-    ``maloq_message_edge_rows``."""
+    ``maloq_message_edge_rows``, and "wp1t"/"wp2t" (both convolutions' transposed
+    weight packings, packed in the same launches as the forward ones).
+
+    The host side is the registered operator maloq_hip::edgewise_fwd (the C++
+    extension); ``wpack1``/``wpack2`` pass the forward packings of fixed
+    weights (without ``save``)."""
+    from . import ops
     dt = x.dtype
     if dt not in DTYPE_CODE:
         raise ValueError(f"unsupported dtype {dt}")
     _lib.require_cuda(x, eulers, conv1[0], conv2[0])
-    if not _lib.load().maloq_message_supported(lmax, mmax):
-        raise ValueError(f"no message kernels for lmax={lmax}, mmax={mmax}")
-    N, d, c_x = x.shape
-    assert d == (lmax + 1) ** 2, "x must be [N, (lmax+1)^2, C]"
-    c_hidden = conv1[0].shape[0] // (2 * lmax + 1)
-    c_out = conv2[0].shape[0] // (lmax + 1)
-    npart = 2 if x_message_edge is None else 3
-    xm = None
-    if x_message_edge is not None:
-        assert tuple(x_message_edge.shape) == (plan.num_edges, d, c_x), "x_message_edge must be [E, d, C]"
-        xm = x_message_edge.to(dt).contiguous()
-    if wpack1 is None:
-        wpack1 = pack_weights(conv1[0], conv1[2], lmax, mmax, True, npart * c_x, c_hidden, dt, 0)
-    if wpack2 is None:
-        wpack2 = pack_weights(conv2[0], conv2[2], lmax, mmax, False, c_hidden, c_out, dt, 0)
-    E = plan.num_edges
-    dev = x.device
-    kr = kept_rows(lmax, mmax)
     if node_or_edge not in ("node", "edge"):
         raise ValueError("node_or_edge must be 'node' or 'edge'")
-    if node_or_edge == "node":
-        rows, seg_id, seg_ptr = plan.num_nodes, None, plan.seg_ptr
-    else:
-        rows = E
-        seg_id = torch.arange(E, device=dev, dtype=torch.int32)
-        seg_ptr = torch.arange(E + 1, device=dev, dtype=torch.int64)
-    out = torch.empty(rows, d, c_out, device=dev, dtype=torch.float32)
-    lib = _lib.load()
-    parts = torch.empty(max(1, lib.maloq_message_partials_floats(lmax, 0, E, c_out)), device=dev,
-                        dtype=torch.float32)
-    if rad is not None:
-        assert rad.shape == (E, rad_width(lmax, mmax, npart * c_x)), "rad must be [E, sum_m (lmax-m+1) npart C]"
-        rad = rad.to(dt).contiguous()
+    if (eulers is None) == (wigner is None):
+        raise ValueError("give exactly one of eulers and wigner")
+    res = ops.edgewise_fwd(x, rad, conv1[0], conv1[1], list(conv1[2][:mmax]), conv2[0], conv2[1],
+                           list(conv2[2][:mmax]), plan.src, plan.dst, plan.seg_ptr, plan.perm, eulers, wigner,
+                           x_message_edge, None if save is not None else wpack1,
+                           None if save is not None else wpack2, lmax, mmax, node_or_edge == "edge",
+                           save is not None)
+    out, y, r, z, dk, g, wp1t, wp2t = res
     if save is not None:
-        y = _edge_rows(E, kr, npart * c_x, dev, dt)
-        z = _edge_rows(E, kr, c_hidden, dev, dt)
-    else:
-        y = torch.empty(max(E, 1), kr, npart * c_x, device=dev, dtype=dt)
-        z = torch.empty(max(E, 1), kr, c_hidden, device=dev, dtype=dt)
-    r = torch.empty(max(E, 1), kr, npart * c_x, device=dev, dtype=dt) \
-        if (save is not None and rad is not None) else None
-    eul, dk = _edge_frames(eulers, wigner, plan, lmax, mmax, dev)
-    gws = torch.empty(max(E, 1), kr + lmax, c_hidden, device=dev, dtype=dt) if save is not None else None
-    b1 = conv1[1].float().contiguous() if conv1[1] is not None else None
-    b2 = conv2[1].float().contiguous() if conv2[1] is not None else None
-    xc = x.contiguous()
-    mrow = plan.perm.int().contiguous() if xm is not None else None   # x_message_edge row per position
-    _lib.call("maloq_message_edgewise_fwd", DTYPE_CODE[dt], lmax, mmax, _lib.ptr(xc), c_x,
-              _lib.ptr(plan.src), _lib.ptr(plan.dst), _lib.ptr(seg_id), E, _lib.ptr(eul), _lib.ptr(rad),
-              _lib.ptr(wpack1), _lib.ptr(b1), c_hidden, _lib.ptr(wpack2), _lib.ptr(b2),
-              _lib.ptr(_jd_dev(lmax, dev)), _lib.ptr(out), rows, c_out, _lib.ptr(seg_ptr), _lib.ptr(parts),
-              _lib.ptr(y), _lib.ptr(r), _lib.ptr(dk), _lib.ptr(gws), _lib.ptr(z), _lib.ptr(xm),
-              _lib.ptr(mrow), _lib.stream_of(dev))
-    if save is not None:
-        save.update(y=y, r=r, z=z, dk=dk, g=gws)
-    if node_or_edge == "edge":
-        per_edge = torch.empty_like(out)
-        per_edge[plan.perm] = out     # dst-sorted position p holds original edge perm[p]
-        return per_edge
+        save.update(y=y, r=r if r.numel() else None, z=z, dk=dk, g=g, wp1t=wp1t, wp2t=wp2t)
     return out
 
 
 def edgewise_backward_dx(grad_out, x_shape, dt, plan, saved, rad, conv1, conv2, lmax, mmax,
-                         need_rad_grad=True, node_or_edge="node", parts=2, wpack1_t=None, wpack2_t=None):
-    """Input and radial gradients of :func:`edgewise_forward` from its saved
-    workspaces (maloq_message_edgewise_bwd_dx): (grad_x fp32 [N, d, C],
-    grad_rad or None, dz2 [E, d', C] the second convolution's output gradient,
-    dz1 [E, d' + lmax, c_hidden] the first one's (dL/dpre, then dL/dgate)),
-    dz2 and dz1 with the padding rows the weight gradient reads; with
-    ``parts=3`` (a "source-target-message" block) also the gradient of
-    x_message_edge [E, d, C] in the original edge order, fifth."""
+                         need_rad_grad=True, node_or_edge="node", parts=2, wpack1_t=None, wpack2_t=None,
+                         need_w=(False, False)):
+    """Gradients of :func:`edgewise_forward` from its saved workspaces (the
+    registered operator maloq_hip::edgewise_bwd): (grad_x fp32 [N, d, C],
+    grad_rad or None, grad_x_message_edge [E, d, C] in the original edge order
+    or None, (dW0, db0, [dW_m]) of conv1 or None, the same of conv2 or None);
+    ``need_w`` says which convolutions' weight gradients to form."""
+    from . import ops
     N, d, c_x = x_shape
-    c_hidden = conv1[0].shape[0] // (2 * lmax + 1)
-    dev = grad_out.device
-    E = plan.num_edges
-    kr = kept_rows(lmax, mmax)
-    wp1t = wpack1_t if wpack1_t is not None else \
-        pack_weights(conv1[0], conv1[2], lmax, mmax, True, parts * c_x, c_hidden, dt, 1)
-    wp2t = wpack2_t if wpack2_t is not None else pack_weights(conv2[0], conv2[2], lmax, mmax, False, c_hidden, c_x, dt, 1)
-    g = grad_out.float().contiguous()
-    grad_row = None
-    if node_or_edge == "edge":
-        g = g[plan.perm].contiguous()       # per-edge gradient rows in dst-sorted order
-        grad_row = torch.arange(E, device=dev, dtype=torch.int32)
-    gxs = torch.empty(N, d, c_x, device=dev, dtype=torch.float32)
-    gxd = torch.empty(N, d, c_x, device=dev, dtype=torch.float32)
-    gxm = torch.empty(max(E, 1), d, c_x, device=dev, dtype=torch.float32) if parts == 3 else None
-    edge_seg = torch.arange(E, device=dev, dtype=torch.int32) if parts == 3 else None
-    lib = _lib.load()
-    pbuf = torch.empty(max(1, lib.maloq_message_partials_floats(lmax, 1, E, c_x)), device=dev,
-                       dtype=torch.float32)
-    grad_rad = None
-    if rad is not None:
-        rad = rad.to(dt).contiguous()
-        if need_rad_grad:
-            grad_rad = torch.empty_like(rad)
-    dz2 = _edge_rows(E, kr, c_x, dev, dt)
-    dz1 = _edge_rows(E, kr + lmax, c_hidden, dev, dt)
-    _lib.call("maloq_message_edgewise_bwd_dx", DTYPE_CODE[dt], lmax, mmax, _lib.ptr(g), c_x, _lib.ptr(plan.dst),
-              _lib.ptr(grad_row), _lib.ptr(plan.bwd_src), _lib.ptr(plan.bwd_eidx), E, _lib.ptr(saved["dk"]),
-              _lib.ptr(rad), _lib.ptr(grad_rad), _lib.ptr(saved.get("r")), _lib.ptr(saved["g"]), _lib.ptr(wp1t),
-              c_hidden, _lib.ptr(wp2t), _lib.ptr(_jd_dev(lmax, dev)), _lib.ptr(gxs), _lib.ptr(gxd), N,
-              _lib.ptr(plan.seg_ptr), _lib.ptr(plan.seg_ptr_src), _lib.ptr(pbuf), _lib.ptr(dz2),
-              _lib.ptr(dz1), _lib.ptr(edge_seg), _lib.ptr(gxm), _lib.stream_of(dev))
-    gx = gxs.add_(gxd)
-    if parts == 2:
-        return gx, grad_rad, dz2, dz1
-    gm = torch.empty(E, d, c_x, device=dev, dtype=torch.float32)
-    gm[plan.perm] = gxm[:E]      # dst-sorted position p holds original edge perm[p]
-    return gx, grad_rad, dz2, dz1, gm
+    res = ops.edgewise_bwd(grad_out, rad, conv1[0], list(conv1[2][:mmax]), conv2[0], list(conv2[2][:mmax]), plan.dst,
+                           plan.bwd_src, plan.bwd_eidx, plan.perm, plan.seg_ptr, plan.seg_ptr_src, saved["y"],
+                           saved.get("r"), saved["z"], saved["dk"], saved["g"], wpack1_t, wpack2_t, N, c_x, lmax,
+                           mmax, node_or_edge == "edge", parts, bool(need_rad_grad and rad is not None),
+                           bool(need_w[0]), bool(need_w[1]))
+    gx, grad_rad, gm = res[:3]
+    k = 2 + mmax
+    w1, w2 = res[3:3 + k], res[3 + k:3 + 2 * k]
+    conv = lambda w: (w[0], w[1], list(w[2:])) if w[0].numel() else None
+    return (gx, grad_rad if grad_rad.numel() or (need_rad_grad and rad is not None) else None,
+            gm if parts == 3 else None, conv(w1), conv(w2))
 
 
 class _EdgewiseFn(torch.autograd.Function):
     """Autograd of the two-convolution block: gradients for x, rad and both
-    convolutions' weights and biases."""
+    convolutions' weights and biases (the registered operators
+    maloq_hip::edgewise_fwd / edgewise_bwd)."""
 
     @staticmethod
     def forward(ctx, x, rad, w01, b01, w02, b02, xm, plan, frames, lmax, mmax, node_or_edge, *wm):
-        saved = {}
+        saved = {} if any(ctx.needs_input_grad) else None
         wm1, wm2 = list(wm[:mmax]), list(wm[mmax:])
-        npart = 2 if xm is None else 3
-        c_x, c_hidden = x.shape[2], w01.shape[0] // (2 * lmax + 1)
-        # both packings of each convolution from one launch when a backward will
-        # run; the transposed ones wait for it
-        mode = "both" if any(ctx.needs_input_grad) else 0
-        p1 = pack_weights(w01, wm1, lmax, mmax, True, npart * c_x, c_hidden, x.dtype, mode)
-        p2 = pack_weights(w02, wm2, lmax, mmax, False, c_hidden, c_x, x.dtype, mode)
-        (wp1, wp1t), (wp2, wp2t) = (p1, p2) if mode == "both" else ((p1, None), (p2, None))
-        ctx.wpack_t = (wp1t, wp2t)
-        out = edgewise_forward(x, plan, frames[0], rad, (w01, b01, wm1), (w02, b02, wm2), lmax, mmax, wpack1=wp1,
-                               wpack2=wp2, save=saved, node_or_edge=node_or_edge, x_message_edge=xm, wigner=frames[1])
+        out = edgewise_forward(x, plan, frames[0], rad, (w01, b01, wm1), (w02, b02, wm2), lmax, mmax, save=saved,
+                               node_or_edge=node_or_edge, x_message_edge=xm, wigner=frames[1])
         ctx.plan, ctx.lmax, ctx.mmax, ctx.mode = plan, lmax, mmax, node_or_edge
         ctx.parts, ctx.xm_dtype = (2, None) if xm is None else (3, xm.dtype)
         ctx.x_shape, ctx.dt = tuple(x.shape), x.dtype
         ctx.has_b = (b01 is not None, b02 is not None)
-        ctx.save_for_backward(rad, w01, w02, saved["y"], saved["r"], saved["z"], saved["dk"], saved["g"], *wm)
+        if saved is not None:
+            ctx.save_for_backward(rad, w01, w02, saved["y"], saved["r"], saved["z"], saved["dk"], saved["g"],
+                                  saved["wp1t"], saved["wp2t"], *wm)
         return out
 
     @staticmethod
     def backward(ctx, g):
-        rad, w01, w02, y, r, z, dk, gs, *wm = ctx.saved_tensors
+        rad, w01, w02, y, r, z, dk, gs, wp1t, wp2t, *wm = ctx.saved_tensors
         plan, lmax, mmax = ctx.plan, ctx.lmax, ctx.mmax
         wm1, wm2 = list(wm[:mmax]), list(wm[mmax:])
-        res = edgewise_backward_dx(g, ctx.x_shape, ctx.dt, plan, {"dk": dk, "r": r, "g": gs}, rad,
-                                   (w01, None, wm1), (w02, None, wm2), lmax, mmax,
-                                   need_rad_grad=ctx.needs_input_grad[1], node_or_edge=ctx.mode, parts=ctx.parts,
-                                   wpack1_t=ctx.wpack_t[0], wpack2_t=ctx.wpack_t[1])
-        ctx.wpack_t = None
-        gx, grad_rad, dz2, dz1 = res[:4]
-        gxm = res[4].to(ctx.xm_dtype) if (ctx.parts == 3 and ctx.needs_input_grad[6]) else None
-        c_x = ctx.x_shape[2]
-        c_hidden = w01.shape[0] // (2 * lmax + 1)
-        E = plan.num_edges
         nig = ctx.needs_input_grad
+        need_w1 = nig[2] or nig[3] or any(nig[12:12 + mmax])
+        need_w2 = nig[4] or nig[5] or any(nig[12 + mmax:])
+        gx, grad_rad, gm, c1, c2 = edgewise_backward_dx(
+            g, ctx.x_shape, ctx.dt, plan, {"y": y, "r": r, "z": z, "dk": dk, "g": gs}, rad, (w01, None, wm1),
+            (w02, None, wm2), lmax, mmax, need_rad_grad=nig[1], node_or_edge=ctx.mode, parts=ctx.parts,
+            wpack1_t=wp1t, wpack2_t=wp2t, need_w=(need_w1, need_w2))
+        gxm = gm.to(ctx.xm_dtype) if (ctx.parts == 3 and nig[6]) else None
         dw01 = db01 = dw02 = db02 = None
         dwm1, dwm2 = [None] * mmax, [None] * mmax
-        if nig[2] or nig[3] or any(nig[12:12 + mmax]):
-            if E > 0:
-                dw01, dwm1, db01 = message_weight_grad(dz1, y, lmax, mmax, c_hidden, ctx.parts * c_x, num_edges=E,
-                                                       gate=True)
-            else:
-                dw01, dwm1 = torch.zeros_like(w01, dtype=torch.float32), [torch.zeros_like(w, dtype=torch.float32)
-                                                                          for w in wm1]
-                db01 = torch.zeros(w01.shape[0], device=w01.device)
+        if need_w1:
+            dw01, db01, dwm1 = c1
             dw01, dwm1 = dw01.to(w01.dtype), [d.to(w.dtype) for d, w in zip(dwm1, wm1)]
-        if nig[4] or nig[5] or any(nig[12 + mmax:]):
-            if E > 0:
-                dw02, dwm2, db02 = message_weight_grad(dz2, z, lmax, mmax, c_x, c_hidden, num_edges=E)
-            else:
-                dw02, dwm2 = torch.zeros_like(w02, dtype=torch.float32), [torch.zeros_like(w, dtype=torch.float32)
-                                                                          for w in wm2]
-                db02 = torch.zeros(w02.shape[0], device=w02.device)
+        if need_w2:
+            dw02, db02, dwm2 = c2
             dw02, dwm2 = dw02.to(w02.dtype), [d.to(w.dtype) for d, w in zip(dwm2, wm2)]
-        gxo = gx.to(ctx.dt) if ctx.needs_input_grad[0] else None
-        grad_rad = grad_rad if ctx.needs_input_grad[1] else None
+        gxo = gx.to(ctx.dt) if nig[0] else None
+        grad_rad = grad_rad if nig[1] else None
         return (gxo, grad_rad, dw01, db01 if ctx.has_b[0] else None, dw02, db02 if ctx.has_b[1] else None,
                 gxm, None, None, None, None, None, *dwm1, *dwm2)
 

@@ -16,6 +16,7 @@ ops with known output shapes, and the autograd formulas.
     maloq_hip::label_transform(x, ..)                     get_net_out / get_H on label rows
     maloq_hip::message_block_fwd(x, rad?, w0, b0?, wm, plan tensors, eulers, lmax, mmax, gate)
                                                           Edgewise.forward_node with one convolution
+    maloq_hip::edgewise_fwd / edgewise_bwd(..)            the two-convolution Edgewise, both modes
 
 Reference interfaces: helm/triton_kernels/wigner_fused.py:383-486,
 helm/common/rotation.py:19-39, helm/esen_block.py:146-208,
@@ -223,6 +224,59 @@ class _MessageOp(torch.autograd.Function):
             ctx.x_shape[0], ctx.x_shape[2], lmax, mmax, gate, need_rad)
         return (gx.to(ctx.dt), grad_rad if need_rad else None, dw0.to(w0.dtype), db0 if ctx.has_b0 else None,
                 None, None, None, None, None, *[d.to(w.dtype) for d, w in zip(dwm, wm)])
+
+
+# -------------------------------------------------- two-convolution Edgewise
+edgewise_fwd = _ops.edgewise_fwd
+edgewise_bwd = _ops.edgewise_bwd
+
+
+@register_fake("maloq_hip::edgewise_fwd")
+def _(x, rad, w01, b01, wm1, w02, b02, wm2, src, dst, seg_ptr, perm, eulers, wigner, x_message_edge, wpack1, wpack2,
+      lmax, mmax, edge_mode, save):
+    N, d, c_x = x.shape
+    E = src.shape[0]
+    E1 = max(E, 1)
+    npart = 2 if x_message_edge is None else 3
+    c_hidden, c_out = w01.shape[0] // (2 * lmax + 1), w02.shape[0] // (lmax + 1)
+    kr = M.kept_rows(lmax, mmax)
+    rows_y = int(_lib.load().maloq_message_edge_rows(E)) if save else E1
+    lib = _lib.load()
+    out = x.new_empty(E if edge_mode else seg_ptr.shape[0] - 1, d, c_out, dtype=torch.float32)
+    y = x.new_empty(rows_y, kr, npart * c_x)
+    z = x.new_empty(rows_y, kr, c_hidden)
+    r = x.new_empty(E1, kr, npart * c_x) if (save and rad is not None) else x.new_empty(0)
+    dk = x.new_empty(E1, M.wigner_floats(lmax, mmax), dtype=torch.float32)
+    g = x.new_empty(E1, kr + lmax, c_hidden) if save else x.new_empty(0)
+    code = M.DTYPE_CODE[x.dtype]
+    el = x.element_size()
+    wp1t = x.new_empty(lib.maloq_message_wpack_bytes(code, lmax, mmax, 1, c_hidden, npart * c_x) // el) \
+        if save else x.new_empty(0)
+    wp2t = x.new_empty(lib.maloq_message_wpack_bytes(code, lmax, mmax, 0, c_out, c_hidden) // el) \
+        if save else x.new_empty(0)
+    return [out, y, r, z, dk, g, wp1t, wp2t]
+
+
+@register_fake("maloq_hip::edgewise_bwd")
+def _(grad_out, rad, w01, wm1, w02, wm2, dst, bwd_src, bwd_eidx, perm, seg_ptr, seg_ptr_src, y, r, z, dk, g,
+      wpack1_t, wpack2_t, num_nodes, c_x, lmax, mmax, edge_mode, parts, need_rad_grad, need_w1, need_w2):
+    d = (lmax + 1) ** 2
+    E = dst.shape[0]
+    f32 = dict(dtype=torch.float32)
+    c_hidden = w01.shape[0] // (2 * lmax + 1)
+    res = [grad_out.new_empty(num_nodes, d, c_x, **f32),
+           rad.new_empty(rad.shape, dtype=y.dtype) if (rad is not None and need_rad_grad) else grad_out.new_empty(0, **f32),
+           grad_out.new_empty(E, d, c_x, **f32) if parts == 3 else grad_out.new_empty(0, **f32)]
+    for need, co, ci, gate in ((need_w1, c_hidden, parts * c_x, True), (need_w2, c_x, c_hidden, False)):
+        extra = lmax * co if gate else 0
+        if need:
+            res += [grad_out.new_empty(extra + (lmax + 1) * co, (lmax + 1) * ci, **f32),
+                    grad_out.new_empty(extra + (lmax + 1) * co, **f32)]
+            res += [grad_out.new_empty(2 * (lmax - m + 1) * co, (lmax - m + 1) * ci, **f32)
+                    for m in range(1, mmax + 1)]
+        else:
+            res += [grad_out.new_empty(0, **f32) for _ in range(2 + mmax)]
+    return res
 
 
 # ------------------------------------------------- fused Fock <-> irreps

@@ -214,3 +214,36 @@ def test_operators_refuse_inconsistent_arguments(device):
                            None, sched, 1, 25, None)
     with pytest.raises(ValueError, match="rows and cols"):
         ops.basis_row_meta(0, None, i32, i32, i32, i32[:2], i32, 1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode,parts", [("node", 2), ("edge", 3)])
+def test_edgewise_ops_opcheck(mode, parts, device):
+    """Schema and fake implementations of the two-convolution Edgewise
+    operators on the arguments maloq_amd.message passes."""
+    from maloq_amd import message as M
+    from maloq_amd import ops
+    from maloq_amd.wigner import extract_euler_angles
+    L, C, H, N, E = 2, 32, 32, 9, 40
+    gen = torch.Generator().manual_seed(9)
+    ei = torch.stack([torch.randint(0, N, (E,), generator=gen), torch.randint(0, N, (E,), generator=gen)]).to(device)
+    plan = M.MessagePlan(ei, N)
+    eul = plan.sort_edges(extract_euler_angles(torch.randn(E, 3, generator=gen).to(device), seed=1))
+    x = torch.randn(N, 9, C, generator=gen).to(device)
+    xm = torch.randn(E, 9, C, generator=gen).to(device) if parts == 3 else None
+    w01 = torch.randn(5 * H, 3 * parts * C, generator=gen).to(device) / 10
+    b01 = torch.randn(5 * H, generator=gen).to(device)
+    wm1 = [torch.randn(2 * (3 - m) * H, (3 - m) * parts * C, generator=gen).to(device) / 10 for m in (1, 2)]
+    w02 = torch.randn(3 * C, 3 * H, generator=gen).to(device) / 10
+    b02 = torch.randn(3 * C, generator=gen).to(device)
+    wm2 = [torch.randn(2 * (3 - m) * C, (3 - m) * H, generator=gen).to(device) / 10 for m in (1, 2)]
+    rad = torch.rand(E, M.rad_width(L, L, parts * C), generator=gen).to(device) + 0.5
+    args = (x, rad, w01, b01, wm1, w02, b02, wm2, plan.src, plan.dst, plan.seg_ptr, plan.perm, eul, None, xm, None,
+            None, L, L, mode == "edge", True)
+    torch.library.opcheck(ops.edgewise_fwd, args, test_utils=("test_schema", "test_faketensor"))
+    out, y, r, z, dk, g, wp1t, wp2t = ops.edgewise_fwd(*args)
+    gout = torch.randn(out.shape, generator=gen).to(device)
+    torch.library.opcheck(ops.edgewise_bwd, (gout, rad, w01, wm1, w02, wm2, plan.dst, plan.bwd_src, plan.bwd_eidx,
+                                             plan.perm, plan.seg_ptr, plan.seg_ptr_src, y, r, z, dk, g, wp1t, wp2t, N,
+                                             C, L, L, mode == "edge", parts, True, True, True),
+                          test_utils=("test_schema", "test_faketensor"))
