@@ -50,9 +50,16 @@ struct GPlan {
   static constexpr int gin(int l) { return (GATE && BWD && l >= 1) ? 1 : 0; }   // input gate row
   static constexpr int nq(int l) { return 1 + 2 * cmin(M, l); }
   static constexpr int nqa(int l) { return nq(l) + gin(l); }  // A row types of input degree l
-  static constexpr int ntype(int l) { return nq(l) + gt(l); }
+  // Gate rows apart (GW): a gated forward on 8 waves (lmax 6) puts the gate
+  // row of each degree l >= 1 in the wave with the fewest accumulators at that
+  // point (the wave left without a degree, then those of the light degrees),
+  // so the waves of the heavy degrees hold only their kept rows; the gate
+  // values reach a degree's wave through LDS after the K loop.
+  static constexpr bool GW = GATE && !BWD && NW == 8;
+  static constexpr int gacc(int l) { return GW ? 0 : gt(l); }  // gate row among degree l's accumulators
+  static constexpr int ntype(int l) { return nq(l) + gacc(l); }
   // accumulator type of row type q of degree l (0: m=0, [1: gate], then +1, -1, +2, ...)
-  static constexpr int qtype(int q, int l) { return q == 0 ? 0 : q + gt(l); }
+  static constexpr int qtype(int q, int l) { return q == 0 ? 0 : q + gacc(l); }
   static constexpr int DP = Plan<L, M, false, 4, 1>::DP;
   static constexpr int DPA = DP + ((GATE && BWD) ? L : 0);  // A rows per edge
   // A-source row of input row type q of degree l (gate rows follow the kept rows)
@@ -69,16 +76,22 @@ struct GPlan {
     return s;
   }
   static constexpr int nbfrag(int li) { return bbase(li, L + 1); }
+  // B registers of degree lo at li in its own wave (with GW the gate fragment
+  // is the gate wave's), and the packed position of that wave's fragment t
+  static constexpr int nblr(int li, int lo) { return nbl(li, lo) - gt(lo) + gacc(lo); }
+  static constexpr int bpos(int lo, int t) { return t == 0 ? 0 : t + gt(lo) - gacc(lo); }
   // MFMAs per row tile and K step summed over li: the schedule's weight of degree lo
   static constexpr int work(int lo) {
     int s = 0;
-    for (int li = 0; li <= L; ++li) s += 1 + gt(lo) + gin(li) + 4 * cmin(cmin(M, li), lo);
+    for (int li = 0; li <= L; ++li) s += 1 + gacc(lo) + gin(li) + 4 * cmin(cmin(M, li), lo);
     return s;
   }
   struct Tab {
     int owner[L + 1];
     int base[L + 1];   // first accumulator slot of degree l in its wave
     int nslots[NW];
+    int gowner[L + 1];  // GW: wave holding the gate row of degree l >= 1
+    int gbase[L + 1];   // GW: its accumulator slots gbase .. gbase + RT - 1 (one per row tile)
   };
   static constexpr Tab make() {
     Tab t{};
@@ -104,17 +117,39 @@ struct GPlan {
         }
       t.nslots[w] = s;
     }
+    if (GW)
+      for (int l = 1; l <= L; ++l) {
+        int w = 0;
+        for (int k = 1; k < NW; ++k)
+          if (t.nslots[k] < t.nslots[w]) w = k;
+        t.gowner[l] = w;
+        t.gbase[l] = t.nslots[w];
+        t.nslots[w] += RT;
+      }
     return t;
   }
   static constexpr Tab tab = make();
-  // B registers of wave w at li: degree lo's fragments start at wboff(w, li, lo)
+  static constexpr bool gown(int w, int l) { return GW && l >= 1 && tab.gowner[l] == w; }
+  static constexpr bool has_deg(int w) {
+    for (int l = 0; l <= L; ++l)
+      if (tab.owner[l] == w) return true;
+    return false;
+  }
+  // B registers of wave w at li: degree lo's fragments start at wboff(w, li, lo),
+  // then (GW) the gate fragment of each gate row it holds, at gboff(w, li, lo)
   static constexpr int wboff(int w, int li, int lo) {
     int s = 0;
     for (int k = 0; k < lo; ++k)
-      if (tab.owner[k] == w) s += nbl(li, k);
+      if (tab.owner[k] == w) s += nblr(li, k);
     return s;
   }
-  static constexpr int nbw(int w, int li) { return wboff(w, li, L + 1); }
+  static constexpr int gboff(int w, int li, int lo) {
+    int s = wboff(w, li, L + 1);
+    for (int k = 1; k < lo; ++k)
+      if (gown(w, k)) ++s;
+    return s;
+  }
+  static constexpr int nbw(int w, int li) { return gboff(w, li, L + 1); }
   static constexpr int NBW = [] {
     int m = 1;
     for (int w = 0; w < NW; ++w) m = nbw(w, L) > m ? nbw(w, L) : m;
@@ -173,7 +208,12 @@ struct Gemm {
   // per-wave epilogue staging: the 16-edge scan chunk or the 32 x 36 transpose tile
   static constexpr int PW = (P::CH * 64 > 32 * 36 ? P::CH * 64 : 32 * 36) * 4;
   static constexpr int WPS = (NW + 2) / 3;
-  static constexpr int SB = (P::A_BYTES > WPS * PW) ? P::A_BYTES : WPS * PW;
+  // Gate wave (P::GW): after the K loop the stages also carry tanh of the gate
+  // rows to the degree waves, degree l's RT x 16 x 64 floats in stage (l - 1) / GPS.
+  static constexpr int GPS = (L + 2) / 3;
+  static constexpr int GXB = P::GW ? GPS * RT * 16 * 64 * 4 : 0;
+  static constexpr int SB0 = (P::A_BYTES > WPS * PW) ? P::A_BYTES : WPS * PW;
+  static constexpr int SB = SB0 > GXB ? SB0 : GXB;
   static __device__ __forceinline__ float* wave_staging(int wave, char* st0, char* st1, char* st2) {
     const int k = wave / WPS;
     return reinterpret_cast<float*>((k == 0 ? st0 : (k == 1 ? st1 : st2)) + (wave - k * WPS) * PW);
@@ -269,12 +309,17 @@ struct Gemm {
     static_for<L + 1>([&](auto LO) {
       constexpr int lo = decltype(LO)::value;
       if constexpr (P::tab.owner[lo] == W) {
-        static_for<P::nbl(LI, lo)>([&](auto T) {
+        static_for<P::nblr(LI, lo)>([&](auto T) {
           constexpr int t = decltype(T)::value;
           b[P::wboff(W, LI, lo) + t] =
-              *reinterpret_cast<const frag_t*>(base + (P::bbase(LI, lo) + t) * FRAG);
+              *reinterpret_cast<const frag_t*>(base + (P::bbase(LI, lo) + P::bpos(lo, t)) * FRAG);
         });
       }
+    });
+    static_for<L + 1>([&](auto LO) {  // a gate fragment follows its degree's m = 0 fragment
+      constexpr int lo = decltype(LO)::value;
+      if constexpr (P::gown(W, lo))
+        b[P::gboff(W, LI, lo)] = *reinterpret_cast<const frag_t*>(base + (P::bbase(LI, lo) + 1) * FRAG);
     });
   }
 
@@ -295,13 +340,21 @@ struct Gemm {
                                                 const frag_t (&ag)[RT], const frag_t (&b)[P::NBW]) {
     static_for<L + 1>([&](auto LO) {
       constexpr int lo = decltype(LO)::value;
+      if constexpr (P::gown(W, lo))
+        static_for<RT>([&](auto R) {
+          constexpr int rt = decltype(R)::value;
+          mfma(acc[P::tab.gbase[lo] + rt], a0[rt], b[P::gboff(W, LI, lo)], TM{});
+        });
+    });
+    static_for<L + 1>([&](auto LO) {
+      constexpr int lo = decltype(LO)::value;
       if constexpr (P::tab.owner[lo] == W) {
         constexpr int bo = P::wboff(W, LI, lo);
         static_for<RT>([&](auto R) {
           constexpr int rt = decltype(R)::value;
           constexpr int sb = P::tab.base[lo] + rt * P::ntype(lo);
           mfma(acc[sb], a0[rt], b[bo], TM{});
-          if constexpr (P::gt(lo)) mfma(acc[sb + 1], a0[rt], b[bo + 1], TM{});
+          if constexpr (P::gacc(lo)) mfma(acc[sb + 1], a0[rt], b[bo + 1], TM{});
           if constexpr (P::gin(LI)) mfma(acc[sb], ag[rt], b[bo + 1], TM{});
         });
       }
@@ -316,7 +369,7 @@ struct Gemm {
     static_for<L + 1>([&](auto LO) {
       constexpr int lo = decltype(LO)::value;
       if constexpr (P::tab.owner[lo] == W && m <= lo) {
-        constexpr int bw = P::wboff(W, LI, lo) + 1 + P::gt(lo) + P::gin(LI) + 2 * (m - 1);
+        constexpr int bw = P::wboff(W, LI, lo) + 1 + P::gacc(lo) + P::gin(LI) + 2 * (m - 1);
         const frag_t wr = b[bw], wi = b[bw + 1];
         static_for<RT>([&](auto R) {
           constexpr int rt = decltype(R)::value;
@@ -393,7 +446,7 @@ struct Gemm {
     mma_m0<W, LI>(acc, a0, ag, bc);
     static_for<M>([&](auto MI) {
       constexpr int m = decltype(MI)::value + 1;
-      if constexpr (m <= LI) {
+      if constexpr (m <= LI && P::has_deg(W)) {
         frag_t ap[RT], am[RT];
         read_q<2 * m - 1>(ap, rd, lane);
         read_q<2 * m>(am, rd, lane);
@@ -454,7 +507,7 @@ struct Gemm {
       const float b0 = a.bias != nullptr ? a.bias[a.extra + lo * a.C_n + col] : 0.f;
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[sb][i] += b0;
-      if constexpr (P::gt(lo)) {
+      if constexpr (P::gacc(lo)) {
         const float bg = a.bias != nullptr ? a.bias[(lo - 1) * a.C_n + col] : 0.f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[sb + 1][i] += bg;
@@ -480,29 +533,115 @@ struct Gemm {
                             static_cast<int64_t>(ei >= 0 ? ei : 0) * RPE * a.C_n + cb * CB + 16 * h;
       static_for<P::ntype(lo)>([&](auto TI) {
         constexpr int t = decltype(TI)::value;  // accumulator type: 0, [gate], +1, -1, ...
-        if constexpr (ZOUT && P::gt(lo) && t == 1) return;
-        constexpr int row = (P::gt(lo) && t == 1) ? P::DP + lo - 1
-                                                  : P::mrow(t == 0 ? 0 : t - P::gt(lo), lo);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) tb[tsw(8 * (i >> 2) + 4 * h + (i & 3), co)] = acc[sb + t][i];
-        wave_sync();
-        if (ei >= 0) {
-          float v[16];
-#pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            const float4 t4 = *reinterpret_cast<const float4*>(tb + tsw(co, 16 * h + 4 * g4));
-            v[4 * g4] = t4.x; v[4 * g4 + 1] = t4.y; v[4 * g4 + 2] = t4.z; v[4 * g4 + 3] = t4.w;
-          }
-          float w8[8];
-#pragma unroll
-          for (int half = 0; half < 2; ++half) {
-#pragma unroll
-            for (int k = 0; k < 8; ++k) w8[k] = v[8 * half + k];
-            store_vec<TM, 8>(g + static_cast<int64_t>(row) * a.C_n + 8 * half, w8);
-          }
-        }
-        wave_sync();
+        if constexpr (ZOUT && P::gacc(lo) && t == 1) return;
+        constexpr int row = (P::gacc(lo) && t == 1) ? P::DP + lo - 1
+                                                    : P::mrow(t == 0 ? 0 : t - P::gacc(lo), lo);
+        store_block(acc[sb + t], g, ei, row, a.C_n, tb, co, h);
       });
+    });
+  }
+
+  // One 32-edge x 32-channel accumulator block v to row `row` of each edge's
+  // destination rows g (lane (co, h): edge co, channels 16h..16h+15; nothing
+  // for ei < 0), transposed through the wave's LDS tile tb.
+  static __device__ __forceinline__ void store_block(const f32x16& v, typename TM::raw* g, int ei, int row,
+                                                     int64_t C_n, float* tb, int co, int h) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) tb[tsw(8 * (i >> 2) + 4 * h + (i & 3), co)] = v[i];
+    wave_sync();
+    if (ei >= 0) {
+      float w[16];
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const float4 t4 = *reinterpret_cast<const float4*>(tb + tsw(co, 16 * h + 4 * g4));
+        w[4 * g4] = t4.x; w[4 * g4 + 1] = t4.y; w[4 * g4 + 2] = t4.z; w[4 * g4 + 3] = t4.w;
+      }
+      float w8[8];
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) w8[k] = w[8 * half + k];
+        store_vec<TM, 8>(g + static_cast<int64_t>(row) * C_n + 8 * half, w8);
+      }
+    }
+    wave_sync();
+  }
+
+  // ---- gate rows apart (P::GW): wave tab.gowner[l] holds the gate row of
+  // degree l, row tile rt, in accumulator tab.gbase[l] + rt.
+  // Gate bias, then (with a.gsave) the pre-activation gate rows to a.gsave
+  // [edge id][d' + L][C_n], row d' + l - 1.
+  template <int W>
+  static __device__ __forceinline__ void gate_rows(f32x16 (&acc)[P::MSLOT], const Smem& s, const Args& a,
+                                                   int cb, float* tb, int lane) {
+    const int co = lane & 31, h = lane >> 5, col = cb * CB + co;
+    static_for<L + 1>([&](auto LO) {
+      constexpr int lo = decltype(LO)::value;
+      if constexpr (P::gown(W, lo)) {
+        const float bg = a.bias != nullptr ? a.bias[(lo - 1) * a.C_n + col] : 0.f;
+        static_for<RT>([&](auto R) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) acc[P::tab.gbase[lo] + decltype(R)::value][i] += bg;
+        });
+      }
+    });
+    if (a.gsave == nullptr) return;
+    static_for<RT>([&](auto RTI) {
+      constexpr int rt = decltype(RTI)::value;
+      const int ei = s.eid[rt * 32 + co];
+      typename TM::raw* gp = reinterpret_cast<typename TM::raw*>(a.gsave) +
+                             static_cast<int64_t>(ei >= 0 ? ei : 0) * (P::DP + L) * a.C_n + cb * CB + 16 * h;
+      static_for<L + 1>([&](auto LO) {
+        constexpr int lo = decltype(LO)::value;
+        if constexpr (P::gown(W, lo)) store_block(acc[P::tab.gbase[lo] + rt], gp, ei, P::DP + lo - 1, a.C_n, tb, co, h);
+      });
+    });
+  }
+  // tanh of the gate row of degree g + 1, row tile rt: register i of lane at
+  // gx<g, rt>[i * 64 + lane]
+  template <int g, int rt>
+  static __device__ __forceinline__ float* gx(char* st0, char* st1, char* st2) {
+    constexpr int k = g / GPS;
+    return reinterpret_cast<float*>(k == 0 ? st0 : (k == 1 ? st1 : st2)) + ((g % GPS) * RT + rt) * 16 * 64;
+  }
+  template <int W>
+  static __device__ __forceinline__ void gate_out(const f32x16 (&acc)[P::MSLOT], char* st0, char* st1,
+                                                  char* st2, int lane) {
+    static_for<L + 1>([&](auto LO) {
+      constexpr int lo = decltype(LO)::value;
+      if constexpr (P::gown(W, lo))
+        static_for<RT>([&](auto R) {
+          constexpr int rt = decltype(R)::value;
+          float* x = gx<lo - 1, rt>(st0, st1, st2);
+#pragma unroll
+          for (int i = 0; i < 16; ++i) x[i * 64 + lane] = tanhf(acc[P::tab.gbase[lo] + rt][i]);
+        });
+    });
+  }
+  // A degree's GateActivation with the gate values from LDS.
+  template <int lo>
+  static __device__ __forceinline__ void gate_act_gw(f32x16 (&acc)[P::MSLOT], char* st0, char* st1,
+                                                     char* st2, int lane) {
+    static_for<RT>([&](auto RTI) {
+      constexpr int rt = decltype(RTI)::value;
+      constexpr int sb = P::tab.base[lo] + rt * P::ntype(lo);
+      if constexpr (lo == 0) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float z = acc[sb][i];
+          acc[sb][i] = z / (1.0f + __expf(-z));
+        }
+      } else {
+        const float* x = gx<lo - 1, rt>(st0, st1, st2);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float g = x[i * 64 + lane];
+          static_for<P::nq(lo)>([&](auto Q) {
+            constexpr int q = decltype(Q)::value;
+            acc[sb + P::qtype(q, lo)][i] *= g;
+          });
+        }
+      }
     });
   }
 
@@ -829,6 +968,37 @@ struct Gemm {
     const int le = lane < TE ? lane : TE - 1, ln = le + 1 < TE ? le + 1 : le;
     const uint64_t endmask = __ballot(lane < nvalid && (lane == nvalid - 1 || s.seg[ln] != s.seg[le]));
     const int col = cb * CB + (lane & 31);
+    if constexpr (P::GW) {
+      // bias and pre-activation rows; the gate values through the stages (every
+      // wave passes the three barriers); the activation; the stores
+      float* tb = wave_staging(wave, st0, st1, st2);
+      static_for<L + 1>([&](auto LO) {
+        constexpr int lo = decltype(LO)::value;
+        if constexpr (P::tab.owner[lo] == W) {
+          add_bias<lo>(acc, a, col);
+          if (a.gsave != nullptr) save_pre<lo>(acc, s, a, cb, tb, lane);
+        }
+      });
+      gate_rows<W>(acc, s, a, cb, tb, lane);
+      __syncthreads();  // staging reads done before the gate values overwrite it
+      gate_out<W>(acc, st0, st1, st2, lane);
+      __syncthreads();
+      static_for<L + 1>([&](auto LO) {
+        constexpr int lo = decltype(LO)::value;
+        if constexpr (P::tab.owner[lo] == W) gate_act_gw<lo>(acc, st0, st1, st2, lane);
+      });
+      __syncthreads();  // gate values read before the stages are staging again
+      static_for<L + 1>([&](auto LO) {
+        constexpr int lo = decltype(LO)::value;
+        if constexpr (P::tab.owner[lo] == W) {
+          if constexpr (MODE == FWD_EDGE)
+            save_pre<lo, true>(acc, s, a, cb, tb, lane);
+          else
+            rotate_sum<W, lo>(acc, s, wsh, a, cb, tb, lane, endmask);
+        }
+      });
+      return;
+    }
     static_for<L + 1>([&](auto LO) {
       constexpr int lo = decltype(LO)::value;
       if constexpr (P::tab.owner[lo] == W) {

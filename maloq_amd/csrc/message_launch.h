@@ -9,10 +9,11 @@ namespace msg {
 // workgroups per CU (the launch bound) for each shape:
 //   mmax < lmax, lmax <= 4 without gate: 4 waves x 64 edges, two workgroups
 //     per CU (256 registers per lane);
-//   gated, or lmax > 4: 32 edges, except the input gradient (BWD_DX): it has
-//     no extra accumulators (a gate's rows are an extra input row type), and
-//     at lmax 6 a wave owns one degree, so it takes 64-edge tiles everywhere
-//     (each weight fragment then serves twice the edges);
+//   gated, lmax <= 4: 32 edges, except the input gradient (BWD_DX): it has no
+//     extra accumulators (a gate's rows are an extra input row type);
+//   lmax 6 (mmax < lmax): 64 edges in every mode -- a wave owns one degree,
+//     and a gated forward's gate rows go to the eighth wave (GPlan::GW), so
+//     each weight fragment serves two row tiles;
 //   mmax = lmax (every output degree keeps all 2l + 1 row types, d' = d):
 //     32-edge tiles;
 //   one workgroup per CU: every lmax > 4 kernel (at two 4-wave workgroups per
@@ -30,14 +31,13 @@ struct Cfg {
   // two waves share a SIMD (the one-workgroup-per-CU kernel otherwise has a
   // single wave per SIMD to hide its latencies)
   static constexpr int NW = (L > 4 && !FULL) ? 8 : 4;
-  static constexpr int RT = FULL ? 1 : ((MODE == BWD_DX || (L <= 4 && !GATE)) ? 2 : 1);
+  static constexpr int RT = FULL ? 1 : ((MODE == BWD_DX || L > 4 || !GATE) ? 2 : 1);
   static constexpr int MINB = (L > 4 || (FULL && GATE && (MODE == FWD || MODE == FWD_EDGE))) ? 1 : 2;
 };
 
 inline int tile_edges(int lmax, int mmax, int gate, int mode = FWD) {
   if (mmax == lmax && lmax > 2) return 32;
-  if (mode == BWD_DX) return 64;
-  return (lmax <= 4 && !gate) ? 64 : 32;
+  return (mode == BWD_DX || lmax > 4 || !gate) ? 64 : 32;
 }
 // Every instantiation's tile has a multiple of 32 edges: partial-segment
 // buffers sized for 32-edge tiles fit them all.
