@@ -8,7 +8,8 @@ subgraph of the subset's in-edges) and through size-independent properties.
   forward and backward on a node subset, and bitwise run-to-run determinism of
   the whole graph's forward and gradients;
 * config 5: 2000-atom periodic SiO2 cell (6 A cutoff), lmax 4, C 256: bf16
-  forward, and fp32 / bf16 forward and backward, on a node subset; the 2s2p1d
+  forward, and bf16 forward and backward through the operators (the
+  benchmark's step), on a node subset; the 2s2p1d
   block-sparse basis transform on the whole cell: gather bit-exact against
   the oracle, round trip within 1e-6.
 
@@ -40,11 +41,16 @@ def _conv(lmax, mmax, c_in, c_out, gen, gate):
     return {"w0": w0, "b0": b0, "wm": wm, "c_out": c_out}
 
 
-def _subset_check(g, nodes, lmax, mmax, C, dtype, gate, device, backward, seed=0, determinism=False):
+def _subset_check(g, nodes, lmax, mmax, C, dtype, gate, device, backward, seed=0, determinism=False,
+                  via_ops=False):
     """Run the fused block on the whole graph g and compare the rows of
     ``nodes`` (and, with ``backward``, every gradient of a loss that only
-    sees those rows) with the oracle on their in-edges."""
+    sees those rows) with the oracle on their in-edges.  ``via_ops``: through
+    the registered operators (maloq_hip::message_block_fwd / _bwd), as the
+    benchmark's training step runs it."""
     from maloq_amd import message as M
+    from maloq_amd import ops as O
+    block = O.message_block if via_ops else M.message_block
     from maloq_amd.wigner import extract_euler_angles
     gen = torch.Generator().manual_seed(seed)
     N, E, d = g.num_nodes, g.num_edges, (lmax + 1) ** 2
@@ -77,7 +83,7 @@ def _subset_check(g, nodes, lmax, mmax, C, dtype, gate, device, backward, seed=0
               conv["w0"].float().to(device), conv["b0"].float().to(device)] + [w.float().to(device) for w in conv["wm"]]
         if backward:
             dl = [t.requires_grad_() for t in dl]
-        out = M.message_block(dl[0], plan, plan.sort_edges(eul), dl[1], dl[2], dl[3], dl[4:], lmax, mmax, gate=gate)
+        out = block(dl[0], plan, plan.sort_edges(eul), dl[1], dl[2], dl[3], dl[4:], lmax, mmax, gate=gate)
         if backward:
             out.backward(gout.float().to(device))
         torch.cuda.synchronize()
@@ -140,6 +146,17 @@ def test_config4_gated_lmax6_fwd_bwd(cfg4, device):
 def test_config5_c256_forward(cfg5, device):
     print("config 5 lmax=4 C=256 bf16", flush=True)
     _subset_check(cfg5, np.arange(0, 2000, 200), 4, 2, 256, torch.bfloat16, False, device, backward=False, seed=5)
+
+
+def test_config5_c256_fwd_bwd_bf16_operators(cfg5, device):
+    """The benchmark's config-5 training step itself (bf16, C = 256, through
+    the registered operators: the launches bench.py times) on the whole
+    2000-atom cell: the forward rows and every gradient (x, the radial rows,
+    the m = 0 weights and bias, the m > 0 weights) of a loss on a node subset,
+    against the fp64 oracle on the subset's in-edges."""
+    print("config 5 lmax=4 C=256 fwd+bwd bf16 through the operators", flush=True)
+    _subset_check(cfg5, np.arange(7, 2000, 250), 4, 2, 256, torch.bfloat16, False, device, backward=True, seed=6,
+                  via_ops=True)
 
 
 @pytest.mark.skip(reason="first run together with a GPU build that faulted the GPU (32-edge forward tiles at three "
