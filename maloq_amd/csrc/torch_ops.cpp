@@ -68,11 +68,20 @@ int dtype_code(at::ScalarType s) {
   return -1;
 }
 
-// Device pointer of an optional tensor of element type T (null if absent);
-// a tensor of another dtype is refused rather than reinterpreted.
+// Device pointer of an index tensor: of element type T (data_ptr refuses
+// another dtype rather than reinterpreting it) and densely packed, since the
+// kernels read it as a flat array.
+template <class T>
+T* iptr(const at::Tensor& t) {
+  TORCH_CHECK_VALUE(t.is_contiguous(), "index and table tensors must be contiguous, got sizes ", t.sizes(),
+                    " strides ", t.strides());
+  return t.data_ptr<T>();
+}
+
+// The same for an optional tensor (null if absent).
 template <class T>
 const T* cptr(const c10::optional<at::Tensor>& t) {
-  return t.has_value() ? t->data_ptr<T>() : nullptr;
+  return t.has_value() ? iptr<T>(*t) : nullptr;
 }
 
 // Every given tensor on the device of `ref` (the kernels take raw pointers).
@@ -318,7 +327,7 @@ at::Tensor rotate(const at::Tensor& x, const at::Tensor& eulers, const c10::opti
   if (E == 0) return out;
   const at::Tensor xc = x.contiguous();
   check_rc(maloq_rotate(code, code, static_cast<int>(lmax), xc.data_ptr(), static_cast<int>(C),
-                        g.defined() ? g.data_ptr<int32_t>() : nullptr, E, eul.data_ptr<float>(), nullptr,
+                        g.defined() ? iptr<int32_t>(g) : nullptr, E, eul.data_ptr<float>(), nullptr,
                         jd_on(x.device()), inverse ? 1 : 0, out.data_ptr(), stream_of(xc)),
            "maloq_rotate");
   return out;
@@ -344,7 +353,7 @@ at::Tensor segment_sum(const at::Tensor& msg, const at::Tensor& perm, const at::
   }
   at::Tensor out = at::empty(shape, msg.options().dtype(at::kFloat));
   const at::Tensor p = perm.to(at::kLong).contiguous(), s = seg_ptr.to(at::kLong).contiguous();
-  check_rc(maloq_segment_sum(m.data_ptr<float>(), p.data_ptr<int64_t>(), s.data_ptr<int64_t>(), num_segments,
+  check_rc(maloq_segment_sum(m.data_ptr<float>(), iptr<int64_t>(p), iptr<int64_t>(s), num_segments,
                              width, out.data_ptr<float>(), stream_of(m)),
            "maloq_segment_sum");
   return out;
@@ -373,7 +382,7 @@ at::Tensor label_transform(const at::Tensor& x, const at::Tensor& blocks, const 
   if (pre || post) ones = at::ones({xc.size(1)}, xc.options());
   auto gather = [&](const at::Tensor& y, const at::Tensor& src) {
     at::Tensor o = at::empty_like(y);
-    check_rc(maloq_gather_columns(y.data_ptr<float>(), y.size(1), y.size(0), src.data_ptr<int32_t>(),
+    check_rc(maloq_gather_columns(y.data_ptr<float>(), y.size(1), y.size(0), iptr<int32_t>(src),
                                   ones.data_ptr<float>(), static_cast<int>(y.size(1)), o.data_ptr<float>(),
                                   o.size(1), stream_of(y)),
              "maloq_gather_columns");
@@ -387,7 +396,7 @@ at::Tensor label_transform(const at::Tensor& x, const at::Tensor& blocks, const 
   check_rc(maloq_label_transform(xc.data_ptr<float>(), pre ? nullptr : cptr<int32_t>(perm_in),
                                  out.data_ptr<float>(), post ? nullptr : cptr<int32_t>(perm_out), xc.size(0),
                                  static_cast<int>(xc.size(1)), static_cast<int>(num_blocks),
-                                 blocks.data_ptr<int32_t>(), cptr<float>(w), sched.data_ptr<int32_t>(),
+                                 iptr<int32_t>(blocks), cptr<float>(w), iptr<int32_t>(sched),
                                  static_cast<int>(ngroups), static_cast<int>(group_cols), stream_of(xc)),
            "maloq_label_transform");
   return post ? gather(out, *perm_out) : out;
@@ -443,7 +452,7 @@ std::vector<at::Tensor> message_block_fwd(const at::Tensor& x, const c10::option
                                                  static_cast<int>(c_in), static_cast<int>(c_out));
   at::Tensor wpack = at::empty({idx.numel()}, x.options().dtype(dt));
   TORCH_CHECK(wpack.numel() * wpack.element_size() == want, "packed weight size mismatch");
-  check_rc(maloq_message_pack(code, static_cast<int>(sp.size()), sp.data(), sn.data(), idx.data_ptr<int64_t>(),
+  check_rc(maloq_message_pack(code, static_cast<int>(sp.size()), sp.data(), sn.data(), iptr<int64_t>(idx),
                               idx.numel(), wpack.data_ptr(), stream_of(x)),
            "maloq_message_pack");
   // outputs and workspaces
@@ -474,10 +483,10 @@ std::vector<at::Tensor> message_block_fwd(const at::Tensor& x, const c10::option
   if (b0.has_value()) bias = b0->to(at::kFloat).contiguous();
   const at::Tensor xc = x.contiguous();
   check_rc(maloq_message_fwd(code, static_cast<int>(lmax), static_cast<int>(mmax), gate ? 1 : 0, xc.data_ptr(),
-                             static_cast<int>(c_in), src.data_ptr<int32_t>(), dst.data_ptr<int32_t>(), E,
+                             static_cast<int>(c_in), iptr<int32_t>(src), iptr<int32_t>(dst), E,
                              eul.data_ptr<float>(), radc.defined() ? radc.data_ptr() : nullptr, wpack.data_ptr(),
                              bias.defined() ? bias.data_ptr<float>() : nullptr, jd_on(dev), out.data_ptr<float>(),
-                             num_nodes, static_cast<int>(c_out), seg_ptr.data_ptr<int64_t>(),
+                             num_nodes, static_cast<int>(c_out), iptr<int64_t>(seg_ptr),
                              parts.data_ptr<float>(), y.data_ptr(), rad.has_value() ? r.data_ptr() : nullptr,
                              dk.data_ptr<float>(), gate ? g.data_ptr() : nullptr, stream_of(xc)),
            "maloq_message_fwd");
@@ -519,7 +528,7 @@ at::Tensor pack_weights(int code, int64_t lmax, int64_t mmax, bool gate, int64_t
   const int64_t want = mode == 0 ? fwd_b : (mode == 1 ? tr_b : fwd_b + tr_b);
   at::Tensor wpack = at::empty({idx.numel()}, w0.options().dtype(dt));
   TORCH_CHECK(wpack.numel() * wpack.element_size() == want, "packed weight size mismatch");
-  check_rc(maloq_message_pack(code, static_cast<int>(sp.size()), sp.data(), sn.data(), idx.data_ptr<int64_t>(),
+  check_rc(maloq_message_pack(code, static_cast<int>(sp.size()), sp.data(), sn.data(), iptr<int64_t>(idx),
                               idx.numel(), wpack.data_ptr(), stream_of(w0)),
            "maloq_message_pack");
   return wpack;
@@ -668,12 +677,12 @@ std::vector<at::Tensor> message_block_bwd(const at::Tensor& grad_out, const c10:
   const at::Tensor gq = grad_out.to(at::kFloat).contiguous();
   const bool has_r = r.has_value() && r->numel() > 0;
   check_rc(maloq_message_bwd_dx(code, static_cast<int>(lmax), static_cast<int>(mmax), gate ? 1 : 0,
-                                gq.data_ptr<float>(), static_cast<int>(c_out), bwd_dst.data_ptr<int32_t>(),
-                                bwd_src.data_ptr<int32_t>(), bwd_eidx.data_ptr<int32_t>(), E, dk.data_ptr<float>(),
+                                gq.data_ptr<float>(), static_cast<int>(c_out), iptr<int32_t>(bwd_dst),
+                                iptr<int32_t>(bwd_src), iptr<int32_t>(bwd_eidx), E, dk.data_ptr<float>(),
                                 radc.defined() ? radc.data_ptr() : nullptr,
                                 grad_rad.numel() ? grad_rad.data_ptr() : nullptr, has_r ? r->data_ptr() : nullptr,
                                 wpack_t.data_ptr(), jd_on(grad_out.device()), gx.data_ptr<float>(), num_nodes,
-                                static_cast<int>(c_in), seg_ptr_src.data_ptr<int64_t>(), parts.data_ptr<float>(),
+                                static_cast<int>(c_in), iptr<int64_t>(seg_ptr_src), parts.data_ptr<float>(),
                                 dz.data_ptr(), gate ? g->data_ptr() : nullptr, st),
            "maloq_message_bwd_dx");
   // weight and bias gradients
@@ -789,7 +798,7 @@ std::vector<at::Tensor> edgewise_fwd(const at::Tensor& x, const c10::optional<at
     const at::Tensor w = wigner->to(at::kFloat).contiguous();
     if (E > 0)
       check_rc(maloq_message_wigner_rows(static_cast<int>(lmax), static_cast<int>(mmax), w.data_ptr<float>(),
-                                         perm.data_ptr<int64_t>(), E, dk.data_ptr<float>(), st),
+                                         iptr<int64_t>(perm), E, dk.data_ptr<float>(), st),
                "maloq_message_wigner_rows");
   } else {
     TORCH_CHECK_VALUE(eulers->dim() == 2 && eulers->size(0) == E && eulers->size(1) == 3,
@@ -804,13 +813,13 @@ std::vector<at::Tensor> edgewise_fwd(const at::Tensor& x, const c10::optional<at
   const at::Tensor xc = x.contiguous();
   check_rc(maloq_message_edgewise_fwd(
                code, static_cast<int>(lmax), static_cast<int>(mmax), xc.data_ptr(), static_cast<int>(c_x),
-               src.data_ptr<int32_t>(), dst.data_ptr<int32_t>(), seg_id.defined() ? seg_id.data_ptr<int32_t>() : nullptr,
+               iptr<int32_t>(src), iptr<int32_t>(dst), seg_id.defined() ? iptr<int32_t>(seg_id) : nullptr,
                E, eul.defined() ? eul.data_ptr<float>() : nullptr, radc.defined() ? radc.data_ptr() : nullptr,
                wpack1.data_ptr(), b1.defined() ? b1.data_ptr<float>() : nullptr, static_cast<int>(c_hidden),
                wpack2.data_ptr(), b2.defined() ? b2.data_ptr<float>() : nullptr, jd_on(dev), out.data_ptr<float>(),
-               rows, static_cast<int>(c_out), sp.data_ptr<int64_t>(), parts.data_ptr<float>(), y.data_ptr(),
+               rows, static_cast<int>(c_out), iptr<int64_t>(sp), parts.data_ptr<float>(), y.data_ptr(),
                r.numel() ? r.data_ptr() : nullptr, dk.data_ptr<float>(), g.numel() ? g.data_ptr() : nullptr,
-               z.data_ptr(), xm.defined() ? xm.data_ptr() : nullptr, mrow.defined() ? mrow.data_ptr<int32_t>() : nullptr,
+               z.data_ptr(), xm.defined() ? xm.data_ptr() : nullptr, mrow.defined() ? iptr<int32_t>(mrow) : nullptr,
                st),
            "maloq_message_edgewise_fwd");
   if (edge_mode) {
@@ -901,13 +910,13 @@ std::vector<at::Tensor> edgewise_bwd(const at::Tensor& grad_out, const c10::opti
   const bool has_r = r.has_value() && r->numel() > 0;
   check_rc(maloq_message_edgewise_bwd_dx(
                code, static_cast<int>(lmax), static_cast<int>(mmax), gq.data_ptr<float>(), static_cast<int>(c_x),
-               dst.data_ptr<int32_t>(), grad_row.defined() ? grad_row.data_ptr<int32_t>() : nullptr,
-               bwd_src.data_ptr<int32_t>(), bwd_eidx.data_ptr<int32_t>(), E, dk.data_ptr<float>(),
+               iptr<int32_t>(dst), grad_row.defined() ? iptr<int32_t>(grad_row) : nullptr,
+               iptr<int32_t>(bwd_src), iptr<int32_t>(bwd_eidx), E, dk.data_ptr<float>(),
                radc.defined() ? radc.data_ptr() : nullptr, grad_rad.numel() ? grad_rad.data_ptr() : nullptr,
                has_r ? r->data_ptr() : nullptr, g.data_ptr(), wp1t.data_ptr(), static_cast<int>(c_hidden),
                wp2t.data_ptr(), jd_on(grad_out.device()), gxs.data_ptr<float>(), gxd.data_ptr<float>(), num_nodes,
-               seg_ptr.data_ptr<int64_t>(), seg_ptr_src.data_ptr<int64_t>(), pbuf.data_ptr<float>(), dz2.data_ptr(),
-               dz1.data_ptr(), edge_seg.defined() ? edge_seg.data_ptr<int32_t>() : nullptr,
+               iptr<int64_t>(seg_ptr), iptr<int64_t>(seg_ptr_src), pbuf.data_ptr<float>(), dz2.data_ptr(),
+               dz1.data_ptr(), edge_seg.defined() ? iptr<int32_t>(edge_seg) : nullptr,
                gxm.defined() ? gxm.data_ptr<float>() : nullptr, st),
            "maloq_message_edgewise_bwd_dx");
   at::Tensor gx = gxs.add_(gxd);
@@ -944,9 +953,9 @@ at::Tensor basis_row_meta(int64_t ld, const c10::optional<at::Tensor>& bdo, cons
   const c10::DeviceGuard guard(rows.device());
   const int64_t R = rows.size(0);
   at::Tensor meta = at::empty({R > 1 ? R : 1, 4}, rows.options().dtype(at::kInt));
-  check_rc(maloq_basis_row_meta(ld, cptr<int64_t>(bdo), off.data_ptr<int32_t>(), Z.data_ptr<int32_t>(),
-                                rows.data_ptr<int32_t>(), cols.data_ptr<int32_t>(), R, pair_kind.data_ptr<int32_t>(),
-                                static_cast<int>(maxe), meta.data_ptr<int32_t>(), stream_of(rows)),
+  check_rc(maloq_basis_row_meta(ld, cptr<int64_t>(bdo), iptr<int32_t>(off), iptr<int32_t>(Z),
+                                iptr<int32_t>(rows), iptr<int32_t>(cols), R, iptr<int32_t>(pair_kind),
+                                static_cast<int>(maxe), iptr<int32_t>(meta), stream_of(rows)),
            "maloq_basis_row_meta");
   return meta;
 }
@@ -994,30 +1003,30 @@ at::Tensor fock_to_irreps(const at::Tensor& fock, int64_t ld, const c10::optiona
   const c10::DeviceGuard guard(fock.device());
   void* st = stream_of(fock);
   at::Tensor out = at::empty({num_rows, t}, fock.options());
-  const auto* kb = reinterpret_cast<const uint32_t*>(kind_blocks.data_ptr<int32_t>());
+  const auto* kb = reinterpret_cast<const uint32_t*>(iptr<int32_t>(kind_blocks));
   if (meta.has_value()) {
-    check_rc(maloq_fock_to_irreps(fock.data_ptr<float>(), ld, meta->data_ptr<int32_t>(), num_rows,
-                                  slots.data_ptr<int32_t>(), static_cast<int>(maxe), kb, out.data_ptr<float>(),
+    check_rc(maloq_fock_to_irreps(fock.data_ptr<float>(), ld, iptr<int32_t>(*meta), num_rows,
+                                  iptr<int32_t>(slots), static_cast<int>(maxe), kb, out.data_ptr<float>(),
                                   cptr<int32_t>(perm_out), static_cast<int>(t), static_cast<int>(num_blocks),
-                                  blocks.data_ptr<int32_t>(), cptr<float>(w), sched.data_ptr<int32_t>(),
+                                  iptr<int32_t>(blocks), cptr<float>(w), iptr<int32_t>(sched),
                                   static_cast<int>(ngroups), static_cast<int>(group_cols), st),
              "maloq_fock_to_irreps");
   } else {
     TORCH_CHECK_VALUE(off.has_value() && Z.has_value() && rows.has_value() && cols.has_value(),
                       "fock_to_irreps needs a row plan or the pair list");
-    check_rc(maloq_fock_to_irreps_pairs(fock.data_ptr<float>(), ld, cptr<int64_t>(bdo), off->data_ptr<int32_t>(),
-                                        Z->data_ptr<int32_t>(), rows->data_ptr<int32_t>(), cols->data_ptr<int32_t>(),
-                                        num_rows, pair_kind.data_ptr<int32_t>(), slots.data_ptr<int32_t>(),
+    check_rc(maloq_fock_to_irreps_pairs(fock.data_ptr<float>(), ld, cptr<int64_t>(bdo), iptr<int32_t>(*off),
+                                        iptr<int32_t>(*Z), iptr<int32_t>(*rows), iptr<int32_t>(*cols),
+                                        num_rows, iptr<int32_t>(pair_kind), iptr<int32_t>(slots),
                                         static_cast<int>(maxe), kb, out.data_ptr<float>(), cptr<int32_t>(perm_out),
-                                        static_cast<int>(t), static_cast<int>(num_blocks), blocks.data_ptr<int32_t>(),
-                                        cptr<float>(w), sched.data_ptr<int32_t>(), static_cast<int>(ngroups),
+                                        static_cast<int>(t), static_cast<int>(num_blocks), iptr<int32_t>(blocks),
+                                        cptr<float>(w), iptr<int32_t>(sched), static_cast<int>(ngroups),
                                         static_cast<int>(group_cols), st),
              "maloq_fock_to_irreps_pairs");
   }
   if (!perm_post.has_value()) return out;
   at::Tensor ones = at::ones({t}, fock.options());
   at::Tensor sorted = at::empty_like(out);
-  check_rc(maloq_gather_columns(out.data_ptr<float>(), t, num_rows, perm_post->data_ptr<int32_t>(),
+  check_rc(maloq_gather_columns(out.data_ptr<float>(), t, num_rows, iptr<int32_t>(*perm_post),
                                 ones.data_ptr<float>(), static_cast<int>(t), sorted.data_ptr<float>(), t, st),
            "maloq_gather_columns");
   return sorted;
@@ -1050,28 +1059,28 @@ void irreps_to_fock(const at::Tensor& net_out, const at::Tensor& fock, int64_t l
   if (perm_pre.has_value()) {
     at::Tensor ones = at::ones({t}, fock.options());
     at::Tensor u = at::empty_like(x);
-    check_rc(maloq_gather_columns(x.data_ptr<float>(), t, num_rows, perm_pre->data_ptr<int32_t>(),
+    check_rc(maloq_gather_columns(x.data_ptr<float>(), t, num_rows, iptr<int32_t>(*perm_pre),
                                   ones.data_ptr<float>(), static_cast<int>(t), u.data_ptr<float>(), t, st),
              "maloq_gather_columns");
     x = u;
   }
-  const auto* kb = reinterpret_cast<const uint32_t*>(kind_blocks.data_ptr<int32_t>());
+  const auto* kb = reinterpret_cast<const uint32_t*>(iptr<int32_t>(kind_blocks));
   if (meta.has_value()) {
     check_rc(maloq_irreps_to_fock(x.data_ptr<float>(), cptr<int32_t>(perm_in), fock.data_ptr<float>(), ld,
-                                  meta->data_ptr<int32_t>(), num_rows, slots.data_ptr<int32_t>(),
+                                  iptr<int32_t>(*meta), num_rows, iptr<int32_t>(slots),
                                   static_cast<int>(maxe), kb, static_cast<int>(t), static_cast<int>(num_blocks),
-                                  blocks.data_ptr<int32_t>(), cptr<float>(w), sched.data_ptr<int32_t>(),
+                                  iptr<int32_t>(blocks), cptr<float>(w), iptr<int32_t>(sched),
                                   static_cast<int>(ngroups), static_cast<int>(group_cols), st),
              "maloq_irreps_to_fock");
   } else {
     TORCH_CHECK_VALUE(off.has_value() && Z.has_value() && rows.has_value() && cols.has_value(),
                       "irreps_to_fock needs a row plan or the pair list");
     check_rc(maloq_irreps_to_fock_pairs(x.data_ptr<float>(), cptr<int32_t>(perm_in), fock.data_ptr<float>(), ld,
-                                        cptr<int64_t>(bdo), off->data_ptr<int32_t>(), Z->data_ptr<int32_t>(),
-                                        rows->data_ptr<int32_t>(), cols->data_ptr<int32_t>(), num_rows,
-                                        pair_kind.data_ptr<int32_t>(), slots.data_ptr<int32_t>(),
+                                        cptr<int64_t>(bdo), iptr<int32_t>(*off), iptr<int32_t>(*Z),
+                                        iptr<int32_t>(*rows), iptr<int32_t>(*cols), num_rows,
+                                        iptr<int32_t>(pair_kind), iptr<int32_t>(slots),
                                         static_cast<int>(maxe), kb, static_cast<int>(t), static_cast<int>(num_blocks),
-                                        blocks.data_ptr<int32_t>(), cptr<float>(w), sched.data_ptr<int32_t>(),
+                                        iptr<int32_t>(blocks), cptr<float>(w), iptr<int32_t>(sched),
                                         static_cast<int>(ngroups), static_cast<int>(group_cols), st),
              "maloq_irreps_to_fock_pairs");
   }

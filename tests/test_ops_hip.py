@@ -214,6 +214,9 @@ def test_operators_refuse_inconsistent_arguments(device):
                            None, sched, 1, 25, None)
     with pytest.raises(ValueError, match="rows and cols"):
         ops.basis_row_meta(0, None, i32, i32, i32, i32[:2], i32, 1)
+    # index tensors are read as flat arrays: a strided one is refused, not misread
+    with pytest.raises(ValueError, match="contiguous"):
+        ops.basis_row_meta(0, None, i32, i32, torch.zeros(8, dtype=torch.int32, device=device)[::2], i32, i32, 1)
 
 
 @pytest.mark.gpu
