@@ -606,8 +606,12 @@ struct Prep {
   }
 };
 
+// Three resident workgroups per CU (at most 170 registers): the compiler then
+// keeps the Wigner coefficients of degree 6 at mmax 6 in LDS instead of
+// holding all 169 of them in registers (212 -> 167 VGPRs, no spills); the
+// other shapes already fit.  The gated backward would spill under it.
 template <int L, int M, class TM, class TX, bool GATED = false>
-__global__ __launch_bounds__(PREP_NT) void prep_kernel(PrepArgs a) {
+__global__ __launch_bounds__(PREP_NT, GATED ? 1 : 3) void prep_kernel(PrepArgs a) {
   Prep<L, M, TM, TX, GATED>::run(a);
 }
 
