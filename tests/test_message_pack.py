@@ -163,3 +163,22 @@ def test_transposed_gated_packing_matches_autograd(dtype_code, lmax, mmax):
     got, _ = _model(packed, dtype_code, lmax, mmax, True, c_out, c_in, dy.numpy(), 1,
                     grows=dg.reshape(E, lmax, c_out).numpy())
     np.testing.assert_allclose(got, x.grad.numpy(), rtol=0, atol=1e-12)
+
+
+@pytest.mark.parametrize("lmax,mmax", [(2, 2), (4, 2), (4, 4), (6, 2), (6, 6)])
+@pytest.mark.parametrize("gate", [False, True])
+@pytest.mark.parametrize("dtype_code", [0, 1])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_pack_index_places_every_weight_once(lmax, mmax, gate, dtype_code, mode):
+    """The packed buffer is a permutation of cat(W0, W1, ..) for every built
+    shape: each weight element (gate rows included) lands in exactly one slot,
+    so no element is dropped or read twice by the GEMM, for channel counts that
+    differ on the two sides."""
+    for c_in, c_out in ((32, 32), (64, 32), (32, 96)):
+        r = M._pack_index(dtype_code, lmax, mmax, gate, c_in, c_out, mode)
+        idx = np.asarray(r[0] if isinstance(r, tuple) else r)
+        extra = lmax * c_out if gate else 0
+        total = (extra + (lmax + 1) * c_out) * (lmax + 1) * c_in + sum(
+            2 * (lmax - m + 1) * c_out * (lmax - m + 1) * c_in for m in range(1, mmax + 1))
+        assert idx.size == total and idx.min() >= 0
+        assert np.array_equal(np.bincount(idx, minlength=total), np.ones(total, np.int64)), (c_in, c_out)
