@@ -1,8 +1,9 @@
 """The registered PyTorch custom ops (namespace maloq_hip): schema, fake
 (meta) implementations and autograd registration checked by
-torch.library.opcheck; a whole rotate-in / rotate-out chain compiled with
-torch.compile(fullgraph=True) (no graph break: every op has a fake
-implementation); and each op against the module-level path it wraps, bitwise."""
+torch.library.opcheck; a whole rotate-in / rotate-out chain and an Edgewise
+forward + backward compiled with torch.compile(fullgraph=True) (no graph
+break: every op has a fake implementation); and each op against the
+module-level path it wraps, bitwise."""
 import math
 
 import numpy as np
@@ -250,3 +251,42 @@ def test_edgewise_ops_opcheck(mode, parts, device):
                                              plan.perm, plan.seg_ptr, plan.seg_ptr_src, y, r, z, dk, g, wp1t, wp2t, N,
                                              C, L, L, mode == "edge", parts, True, True, True),
                           test_utils=("test_schema", "test_faketensor"))
+
+
+@pytest.mark.gpu
+def test_compiled_edgewise_forward_and_backward_have_no_graph_break(device):
+    """maloq_hip::edgewise_fwd and edgewise_bwd traced together by
+    torch.compile(fullgraph=True): the fake implementations carry every shape
+    the graph needs (the saved workspaces included), and the compiled step
+    gives the eager result bit for bit."""
+    from maloq_amd import message as M
+    from maloq_amd.wigner import extract_euler_angles
+    L, C, H, N, E = 2, 32, 32, 9, 40
+    gen = torch.Generator().manual_seed(11)
+    ei = torch.stack([torch.randint(0, N, (E,), generator=gen), torch.randint(0, N, (E,), generator=gen)]).to(device)
+    plan = M.MessagePlan(ei, N)
+    eul = plan.sort_edges(extract_euler_angles(torch.randn(E, 3, generator=gen).to(device), seed=1))
+    x = torch.randn(N, 9, C, generator=gen).to(device)
+    w01 = torch.randn(5 * H, 3 * 2 * C, generator=gen).to(device) / 10
+    b01 = torch.randn(5 * H, generator=gen).to(device)
+    wm1 = [torch.randn(2 * (3 - m) * H, (3 - m) * 2 * C, generator=gen).to(device) / 10 for m in (1, 2)]
+    w02 = torch.randn(3 * C, 3 * H, generator=gen).to(device) / 10
+    b02 = torch.randn(3 * C, generator=gen).to(device)
+    wm2 = [torch.randn(2 * (3 - m) * C, (3 - m) * H, generator=gen).to(device) / 10 for m in (1, 2)]
+    rad = torch.rand(E, M.rad_width(L, L, 2 * C), generator=gen).to(device) + 0.5
+    gout = torch.randn(N, 9, C, generator=gen).to(device)
+
+    def step(x, rad, gout):
+        out, y, r, z, dk, g, wp1t, wp2t = torch.ops.maloq_hip.edgewise_fwd(
+            x, rad, w01, b01, wm1, w02, b02, wm2, plan.src, plan.dst, plan.seg_ptr, plan.perm, eul, None, None,
+            None, None, L, L, False, True)
+        res = torch.ops.maloq_hip.edgewise_bwd(
+            gout, rad, w01, wm1, w02, wm2, plan.dst, plan.bwd_src, plan.bwd_eidx, plan.perm, plan.seg_ptr,
+            plan.seg_ptr_src, y, r, z, dk, g, wp1t, wp2t, N, C, L, L, False, 2, True, True, True)
+        return [out] + list(res)
+
+    want = step(x, rad, gout)
+    got = torch.compile(step, backend="aot_eager", fullgraph=True)(x, rad, gout)
+    assert len(got) == len(want)
+    for a, b in zip(got, want):
+        assert a.shape == b.shape and torch.equal(a, b)
