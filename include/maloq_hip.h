@@ -452,7 +452,10 @@ int maloq_message_edgewise_bwd_dx(int dtype, int lmax, int mmax, const float* gr
  * which indexes dk (forward dk_ws), rad, grad_rad, r_saved (forward r_ws) and
  * dz_ws.  wpack_t: weights packed for the transposed GEMM.  dz_ws [E, d',
  * c_out] (dtype) receives the rotated output-gradient rows (for the weight
- * gradient).
+ * gradient).  dst_sorted (nullable): dst of each edge in the forward
+ * (dst-sorted) order; given, those rows are formed in that order, so that the
+ * ~E/N consecutive edges of one node read its grad_out rows from cache (the
+ * same values as without it).
  * Replaces the autograd backward of Edgewise.forward_node (esen_block.py:146-208). */
 int maloq_message_bwd_dx(int dtype, int lmax, int mmax, int gate, const float* grad_out,
                          int c_out, const int32_t* dst_by_src, const int32_t* src_sorted,
@@ -460,7 +463,7 @@ int maloq_message_bwd_dx(int dtype, int lmax, int mmax, int gate, const float* g
                          const void* rad, void* grad_rad, const void* r_saved,
                          const void* wpack_t, const float* jd, float* grad_x, int64_t num_nodes,
                          int c_in, const int64_t* seg_ptr_src, float* partials, void* dz_ws,
-                         const void* gate_saved, void* stream);
+                         const void* gate_saved, const int32_t* dst_sorted, void* stream);
 
 /* Rows to allocate for the saved SO(2) rows (y_ws of maloq_message_fwd, dz_ws of
  * maloq_message_bwd_dx) so that maloq_message_dw can read them in whole 128-edge

@@ -58,7 +58,7 @@ SIGNATURES = {
     "maloq_message_edgewise_bwd_dx": [_i32, _i32, _i32, _p, _i32, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p,
                                       _i32, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p],
     "maloq_message_bwd_dx": [_i32, _i32, _i32, _i32, _p, _i32, _p, _p, _p, _i64, _p, _p, _p, _p, _p,
-                             _p, _p, _i64, _i32, _p, _p, _p, _p, _p],
+                             _p, _p, _i64, _i32, _p, _p, _p, _p, _p, _p],
     "maloq_message_edge_rows": [_i64],
     "maloq_message_dw_partials_floats": [_i32, _i32, _i32, _i32, _i32, _i32],
     "maloq_message_dw": [_i32, _i32, _i32, _i32, _p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p],

@@ -371,7 +371,7 @@ extern "C" int maloq_message_bwd_dx(int dtype, int lmax, int mmax, int gate, con
                                     void* grad_rad, const void* r_saved, const void* wpack_t,
                                     const float* jd, float* grad_x, int64_t num_nodes, int c_in,
                                     const int64_t* seg_ptr_src, float* partials, void* dz_ws,
-                                    const void* gate_saved, void* stream) {
+                                    const void* gate_saved, const int32_t* dst_sorted, void* stream) {
   // kernel input channels = c_out (gradient side), output channels = c_in
   int rc = check_common(dtype, lmax, mmax, c_out, c_in, num_edges);
   if (rc) return rc;
@@ -384,7 +384,10 @@ extern "C" int maloq_message_bwd_dx(int dtype, int lmax, int mmax, int gate, con
     MALOQ_REQUIRE(rad == nullptr || r_saved != nullptr, "the radial gradient needs the saved rows");
     MALOQ_REQUIRE(!gate || gate_saved != nullptr, "the gated backward needs the saved pre-activations");
     PrepArgs p{};
-    p.x = grad_out; p.gidx = dst_by_src; p.eidx = edge_idx; p.eulers = nullptr; p.rad = nullptr;
+    // rows by edge id either way; in dst-sorted order the gathers of one node's
+    // grad_out rows are consecutive
+    p.x = grad_out; p.gidx = dst_sorted ? dst_sorted : dst_by_src; p.eidx = dst_sorted ? nullptr : edge_idx;
+    p.eulers = nullptr; p.rad = nullptr;
     p.jd = jd; p.y = dz_ws; p.r = nullptr; p.dk = const_cast<float*>(dk); p.build_d = 0;
     p.E = num_edges; p.C = c_out; p.gsave = gate ? gate_saved : nullptr;
     rc = prep_dispatch(lmax, mmax, dtype, BWD_DX, p, s);

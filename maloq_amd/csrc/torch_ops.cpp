@@ -628,14 +628,16 @@ std::vector<at::Tensor> weight_grads(const at::Tensor& dz, const at::Tensor& y, 
 // Gradients of message_block_fwd from its saved rows: [grad_x fp32 [N, d, c_in],
 // grad_rad (empty unless asked), dW0, db0, dW_1 .. dW_mmax] (fp32).  The
 // graph arrives as the plan's source-sorted arrays: bwd_src, bwd_dst,
-// bwd_eidx (dst-sorted position of each source-sorted edge), seg_ptr_src.
+// bwd_eidx (dst-sorted position of each source-sorted edge), seg_ptr_src;
+// dst (optional, the forward's dst-sorted destinations) lets the output
+// gradient's rotation read each node's rows once for its consecutive edges.
 std::vector<at::Tensor> message_block_bwd(const at::Tensor& grad_out, const c10::optional<at::Tensor>& rad,
                                           const at::Tensor& w0, at::TensorList wm, const at::Tensor& bwd_src,
                                           const at::Tensor& bwd_dst, const at::Tensor& bwd_eidx,
                                           const at::Tensor& seg_ptr_src, const at::Tensor& y, const at::Tensor& dk,
                                           const c10::optional<at::Tensor>& r, const c10::optional<at::Tensor>& g,
                                           int64_t num_nodes, int64_t c_in, int64_t lmax, int64_t mmax, bool gate,
-                                          bool need_rad_grad) {
+                                          bool need_rad_grad, const c10::optional<at::Tensor>& dst) {
   const auto dt = y.scalar_type();
   const int code = dtype_code(dt);
   require_gpu(grad_out, "grad_out");
@@ -653,10 +655,12 @@ std::vector<at::Tensor> message_block_bwd(const at::Tensor& grad_out, const c10:
                     "the gated backward needs the forward's pre-activation rows");
   TORCH_CHECK_VALUE(bwd_dst.numel() == bwd_src.numel() && bwd_eidx.numel() == bwd_src.numel(),
                     "the source-sorted arrays must have one entry per edge");
+  TORCH_CHECK_VALUE(!dst.has_value() || (dst->scalar_type() == at::kInt && dst->numel() == bwd_src.numel()),
+                    "dst must be int32 with one entry per edge");
   TORCH_CHECK_VALUE(seg_ptr_src.numel() == num_nodes + 1, "seg_ptr_src must hold num_nodes + 1 offsets");
   TORCH_CHECK_VALUE(y.dim() == 3 && y.size(0) >= bwd_src.numel() && dk.size(0) >= bwd_src.numel(),
                     "the saved rows must cover every edge");
-  same_device(grad_out, {rad, w0, bwd_src, bwd_dst, bwd_eidx, seg_ptr_src, y, dk, r, g});
+  same_device(grad_out, {rad, w0, bwd_src, bwd_dst, bwd_eidx, seg_ptr_src, y, dk, r, g, dst});
   for (int64_t m = 0; m < mmax; ++m) same_device(grad_out, {wm[m]});
   const c10::DeviceGuard guard(grad_out.device());
   const int64_t c_out = grad_out.size(2), E = bwd_src.size(0);
@@ -683,7 +687,7 @@ std::vector<at::Tensor> message_block_bwd(const at::Tensor& grad_out, const c10:
                                 grad_rad.numel() ? grad_rad.data_ptr() : nullptr, has_r ? r->data_ptr() : nullptr,
                                 wpack_t.data_ptr(), jd_on(grad_out.device()), gx.data_ptr<float>(), num_nodes,
                                 static_cast<int>(c_in), iptr<int64_t>(seg_ptr_src), parts.data_ptr<float>(),
-                                dz.data_ptr(), gate ? g->data_ptr() : nullptr, st),
+                                dz.data_ptr(), gate ? g->data_ptr() : nullptr, cptr<int32_t>(dst), st),
            "maloq_message_bwd_dx");
   // weight and bias gradients
   std::vector<at::Tensor> wg = weight_grads(dz, y, E, lmax, mmax, c_out, c_in, gate);
@@ -1116,7 +1120,8 @@ TORCH_LIBRARY(maloq_hip, m) {
         "Tensor seg_ptr, Tensor eulers, int lmax, int mmax, bool gate) -> Tensor[]");
   m.def("message_block_bwd(Tensor grad_out, Tensor? rad, Tensor w0, Tensor[] wm, Tensor bwd_src, "
         "Tensor bwd_dst, Tensor bwd_eidx, Tensor seg_ptr_src, Tensor y, Tensor dk, Tensor? r, Tensor? g, "
-        "int num_nodes, int c_in, int lmax, int mmax, bool gate, bool need_rad_grad) -> Tensor[]");
+        "int num_nodes, int c_in, int lmax, int mmax, bool gate, bool need_rad_grad, Tensor? dst=None) "
+        "-> Tensor[]");
   m.def("edgewise_fwd(Tensor x, Tensor? rad, Tensor w01, Tensor? b01, Tensor[] wm1, Tensor w02, Tensor? b02, "
         "Tensor[] wm2, Tensor src, Tensor dst, Tensor seg_ptr, Tensor perm, Tensor? eulers, Tensor? wigner, "
         "Tensor? x_message_edge, Tensor? wpack1, Tensor? wpack2, int lmax, int mmax, bool edge_mode, bool save) "

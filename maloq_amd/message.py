@@ -509,7 +509,8 @@ def message_backward_dx(grad_out, x_shape, dt, plan, saved, rad, w0, wm, lmax, m
               _lib.ptr(plan.bwd_dst), _lib.ptr(plan.bwd_src), _lib.ptr(plan.bwd_eidx), E,
               _lib.ptr(saved["dk"]), _lib.ptr(rad), _lib.ptr(grad_rad), _lib.ptr(saved.get("r")),
               _lib.ptr(wpack_t), _lib.ptr(_jd_dev(lmax, dev)), _lib.ptr(gx), N, c_in,
-              _lib.ptr(plan.seg_ptr_src), _lib.ptr(parts), _lib.ptr(dz), _lib.ptr(gs), _lib.stream_of(dev))
+              _lib.ptr(plan.seg_ptr_src), _lib.ptr(parts), _lib.ptr(dz), _lib.ptr(gs), _lib.ptr(plan.dst),
+              _lib.stream_of(dev))
     return gx, grad_rad, dz
 
 

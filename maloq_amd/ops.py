@@ -184,7 +184,7 @@ message_block_bwd = _ops.message_block_bwd
 
 @register_fake("maloq_hip::message_block_bwd")
 def _(grad_out, rad, w0, wm, bwd_src, bwd_dst, bwd_eidx, seg_ptr_src, y, dk, r, g, num_nodes, c_in, lmax, mmax,
-      gate, need_rad_grad):
+      gate, need_rad_grad, dst=None):
     d = (lmax + 1) ** 2
     c_out = grad_out.shape[2]
     f32 = dict(dtype=torch.float32)
@@ -221,7 +221,7 @@ class _MessageOp(torch.autograd.Function):
         need_rad = rad is not None and ctx.needs_input_grad[1]
         gx, grad_rad, dw0, db0, *dwm = message_block_bwd(
             gout, rad, w0, list(wm), plan.bwd_src, plan.bwd_dst, plan.bwd_eidx, plan.seg_ptr_src, y, dk, r, g,
-            ctx.x_shape[0], ctx.x_shape[2], lmax, mmax, gate, need_rad)
+            ctx.x_shape[0], ctx.x_shape[2], lmax, mmax, gate, need_rad, plan.dst)
         return (gx.to(ctx.dt), grad_rad if need_rad else None, dw0.to(w0.dtype), db0 if ctx.has_b0 else None,
                 None, None, None, None, None, *[d.to(w.dtype) for d, w in zip(dwm, wm)])
 
