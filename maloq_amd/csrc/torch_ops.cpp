@@ -403,14 +403,18 @@ at::Tensor label_transform(const at::Tensor& x, const at::Tensor& blocks, const 
 }
 
 // ----------------------------------------------------------- message block
-// Node output and the workspaces the backward reads: [out, y, r, dk, g]
-// (r empty without radial scales, g empty ungated); src, dst, seg_ptr and
+at::Tensor pack_weights(int code, int64_t lmax, int64_t mmax, bool gate, int64_t c_in, int64_t c_out, int mode,
+                        const at::Tensor& w0, at::TensorList wm, at::ScalarType dt);
+
+// Node output and the workspaces the backward reads: [out, y, r, dk, g, wpt]
+// (r empty without radial scales, g empty ungated, wpt the backward's
+// transposed weight packing with save_tr, else empty); src, dst, seg_ptr and
 // eulers are those of the dst-sorted graph plan.
 std::vector<at::Tensor> message_block_fwd(const at::Tensor& x, const c10::optional<at::Tensor>& rad,
                                           const at::Tensor& w0, const c10::optional<at::Tensor>& b0,
                                           at::TensorList wm, const at::Tensor& src, const at::Tensor& dst,
                                           const at::Tensor& seg_ptr, const at::Tensor& eulers, int64_t lmax,
-                                          int64_t mmax, bool gate) {
+                                          int64_t mmax, bool gate, bool save_tr) {
   const int code = dtype_code(x.scalar_type());
   require_gpu(x, "x");
   require_gpu(eulers, "eulers");
@@ -433,28 +437,19 @@ std::vector<at::Tensor> message_block_fwd(const at::Tensor& x, const c10::option
   const int kr = maloq_message_kept_rows(static_cast<int>(lmax), static_cast<int>(mmax));
   const auto dt = x.scalar_type();
   const at::Device dev = x.device();
-  // weights in fragment order
-  int64_t total = 0;
-  const at::Tensor& idx = pack_index_on(code, static_cast<int>(lmax), static_cast<int>(mmax), gate,
-                                        static_cast<int>(c_in), static_cast<int>(c_out), 0, dev, &total);
-  std::vector<at::Tensor> srcs{w0.detach().to(at::kFloat).contiguous()};
-  for (int64_t m = 0; m < mmax; ++m) srcs.push_back(wm[m].detach().to(at::kFloat).contiguous());
-  int64_t have = 0;
-  std::vector<const float*> sp;
-  std::vector<int64_t> sn;
-  for (const auto& t : srcs) {
-    have += t.numel();
-    sp.push_back(t.data_ptr<float>());
-    sn.push_back(t.numel());
+  // weights in fragment order; with save_tr also the transposed packing of the
+  // backward from the same launch (first in the buffer, returned last)
+  at::Tensor wpack, wpt = at::empty({0}, x.options());
+  if (save_tr) {
+    const at::Tensor p = pack_weights(code, lmax, mmax, gate, c_in, c_out, 2, w0, wm, dt);
+    const int64_t nf = maloq_message_wpack_bytes(code, static_cast<int>(lmax), static_cast<int>(mmax), gate,
+                                                 static_cast<int>(c_in), static_cast<int>(c_out)) /
+                       p.element_size();
+    wpt = p.narrow(0, 0, p.numel() - nf);
+    wpack = p.narrow(0, p.numel() - nf, nf);
+  } else {
+    wpack = pack_weights(code, lmax, mmax, gate, c_in, c_out, 0, w0, wm, dt);
   }
-  TORCH_CHECK_VALUE(have == total, "weight shapes do not match (lmax, mmax, channels)");
-  const int64_t want = maloq_message_wpack_bytes(code, static_cast<int>(lmax), static_cast<int>(mmax), gate,
-                                                 static_cast<int>(c_in), static_cast<int>(c_out));
-  at::Tensor wpack = at::empty({idx.numel()}, x.options().dtype(dt));
-  TORCH_CHECK(wpack.numel() * wpack.element_size() == want, "packed weight size mismatch");
-  check_rc(maloq_message_pack(code, static_cast<int>(sp.size()), sp.data(), sn.data(), iptr<int64_t>(idx),
-                              idx.numel(), wpack.data_ptr(), stream_of(x)),
-           "maloq_message_pack");
   // outputs and workspaces
   at::Tensor out = at::empty({num_nodes, d, c_out}, x.options().dtype(at::kFloat));
   const int64_t pf = maloq_message_partials_floats(static_cast<int>(lmax), gate ? 1 : 0, E, static_cast<int>(c_out));
@@ -490,7 +485,7 @@ std::vector<at::Tensor> message_block_fwd(const at::Tensor& x, const c10::option
                              parts.data_ptr<float>(), y.data_ptr(), rad.has_value() ? r.data_ptr() : nullptr,
                              dk.data_ptr<float>(), gate ? g.data_ptr() : nullptr, stream_of(xc)),
            "maloq_message_fwd");
-  return {out, y, r, dk, g};
+  return {out, y, r, dk, g, wpt};
 }
 
 // Saved rows of the bf16 weight gradient: rows past E are zero (it reads whole
@@ -637,7 +632,8 @@ std::vector<at::Tensor> message_block_bwd(const at::Tensor& grad_out, const c10:
                                           const at::Tensor& seg_ptr_src, const at::Tensor& y, const at::Tensor& dk,
                                           const c10::optional<at::Tensor>& r, const c10::optional<at::Tensor>& g,
                                           int64_t num_nodes, int64_t c_in, int64_t lmax, int64_t mmax, bool gate,
-                                          bool need_rad_grad, const c10::optional<at::Tensor>& dst) {
+                                          bool need_rad_grad, const c10::optional<at::Tensor>& dst,
+                                          const c10::optional<at::Tensor>& wpack_t) {
   const auto dt = y.scalar_type();
   const int code = dtype_code(dt);
   require_gpu(grad_out, "grad_out");
@@ -667,8 +663,19 @@ std::vector<at::Tensor> message_block_bwd(const at::Tensor& grad_out, const c10:
   const int kr = maloq_message_kept_rows(static_cast<int>(lmax), static_cast<int>(mmax));
   const auto opt32 = grad_out.options().dtype(at::kFloat);
   void* st = stream_of(grad_out);
-  // input gradient (and the radial gradient)
-  const at::Tensor wpack_t = pack_weights(code, lmax, mmax, gate, c_in, c_out, 1, w0, wm, dt);
+  // input gradient (and the radial gradient); the transposed packing saved by
+  // the forward (save_tr), or packed here
+  at::Tensor wpt;
+  if (wpack_t.has_value() && wpack_t->numel() > 0) {
+    const int64_t b = maloq_message_wpack_bytes(code, static_cast<int>(lmax), static_cast<int>(mmax), gate,
+                                                static_cast<int>(c_out), static_cast<int>(c_in));
+    TORCH_CHECK_VALUE(wpack_t->scalar_type() == dt && wpack_t->is_contiguous() &&
+                          wpack_t->numel() * wpack_t->element_size() == b && wpack_t->device() == grad_out.device(),
+                      "wpack_t is not the transposed packing of these weights");
+    wpt = *wpack_t;
+  } else {
+    wpt = pack_weights(code, lmax, mmax, gate, c_in, c_out, 1, w0, wm, dt);
+  }
   at::Tensor gx = at::empty({num_nodes, d, c_in}, opt32);
   const int64_t pf = maloq_message_partials_floats(static_cast<int>(lmax), gate ? 1 : 0, E, static_cast<int>(c_in));
   at::Tensor parts = at::empty({pf > 1 ? pf : 1}, opt32);
@@ -685,7 +692,7 @@ std::vector<at::Tensor> message_block_bwd(const at::Tensor& grad_out, const c10:
                                 iptr<int32_t>(bwd_src), iptr<int32_t>(bwd_eidx), E, dk.data_ptr<float>(),
                                 radc.defined() ? radc.data_ptr() : nullptr,
                                 grad_rad.numel() ? grad_rad.data_ptr() : nullptr, has_r ? r->data_ptr() : nullptr,
-                                wpack_t.data_ptr(), jd_on(grad_out.device()), gx.data_ptr<float>(), num_nodes,
+                                wpt.data_ptr(), jd_on(grad_out.device()), gx.data_ptr<float>(), num_nodes,
                                 static_cast<int>(c_in), iptr<int64_t>(seg_ptr_src), parts.data_ptr<float>(),
                                 dz.data_ptr(), gate ? g->data_ptr() : nullptr, cptr<int32_t>(dst), st),
            "maloq_message_bwd_dx");
@@ -1117,11 +1124,11 @@ TORCH_LIBRARY(maloq_hip, m) {
   m.def("label_transform(Tensor x, Tensor blocks, Tensor? w, Tensor sched, Tensor? perm_in, Tensor? perm_out, "
         "int num_blocks, int ngroups, int group_cols, Tensor? perm_inv) -> Tensor");
   m.def("message_block_fwd(Tensor x, Tensor? rad, Tensor w0, Tensor? b0, Tensor[] wm, Tensor src, Tensor dst, "
-        "Tensor seg_ptr, Tensor eulers, int lmax, int mmax, bool gate) -> Tensor[]");
+        "Tensor seg_ptr, Tensor eulers, int lmax, int mmax, bool gate, bool save_tr=False) -> Tensor[]");
   m.def("message_block_bwd(Tensor grad_out, Tensor? rad, Tensor w0, Tensor[] wm, Tensor bwd_src, "
         "Tensor bwd_dst, Tensor bwd_eidx, Tensor seg_ptr_src, Tensor y, Tensor dk, Tensor? r, Tensor? g, "
-        "int num_nodes, int c_in, int lmax, int mmax, bool gate, bool need_rad_grad, Tensor? dst=None) "
-        "-> Tensor[]");
+        "int num_nodes, int c_in, int lmax, int mmax, bool gate, bool need_rad_grad, Tensor? dst=None, "
+        "Tensor? wpack_t=None) -> Tensor[]");
   m.def("edgewise_fwd(Tensor x, Tensor? rad, Tensor w01, Tensor? b01, Tensor[] wm1, Tensor w02, Tensor? b02, "
         "Tensor[] wm2, Tensor src, Tensor dst, Tensor seg_ptr, Tensor perm, Tensor? eulers, Tensor? wigner, "
         "Tensor? x_message_edge, Tensor? wpack1, Tensor? wpack2, int lmax, int mmax, bool edge_mode, bool save) "

@@ -159,13 +159,14 @@ class _GetHOp(torch.autograd.Function):
 
 
 # ----------------------------------------------------------- message block
-# Node output and the workspaces the backward reads: [out, y, r, dk, g]
-# (r empty without radial scales, g empty ungated).
+# Node output and the workspaces the backward reads: [out, y, r, dk, g, wpt]
+# (r empty without radial scales, g empty ungated, wpt the transposed weight
+# packing of the backward with save_tr, else empty).
 message_block_fwd = _ops.message_block_fwd
 
 
 @register_fake("maloq_hip::message_block_fwd")
-def _(x, rad, w0, b0, wm, src, dst, seg_ptr, eulers, lmax, mmax, gate):
+def _(x, rad, w0, b0, wm, src, dst, seg_ptr, eulers, lmax, mmax, gate, save_tr=False):
     N, d, c_in = x.shape
     E = src.shape[0]
     c_out = w0.shape[0] // (lmax + 1 + (lmax if gate else 0))
@@ -176,7 +177,13 @@ def _(x, rad, w0, b0, wm, src, dst, seg_ptr, eulers, lmax, mmax, gate):
     r = x.new_empty(max(E, 1), kr, c_in) if rad is not None else x.new_empty(0)
     dk = x.new_empty(max(E, 1), M.wigner_floats(lmax, mmax), dtype=torch.float32)
     g = x.new_empty(max(E, 1), kr + lmax, c_out) if gate else x.new_empty(0)
-    return [out, y, r, dk, g]
+    if save_tr:
+        code = 1 if x.dtype == torch.bfloat16 else 0
+        nb = int(_lib.load().maloq_message_wpack_bytes(code, lmax, mmax, int(gate), c_out, c_in))
+        wpt = x.new_empty(nb // x.element_size())
+    else:
+        wpt = x.new_empty(0)
+    return [out, y, r, dk, g, wpt]
 
 
 message_block_bwd = _ops.message_block_bwd
@@ -184,7 +191,7 @@ message_block_bwd = _ops.message_block_bwd
 
 @register_fake("maloq_hip::message_block_bwd")
 def _(grad_out, rad, w0, wm, bwd_src, bwd_dst, bwd_eidx, seg_ptr_src, y, dk, r, g, num_nodes, c_in, lmax, mmax,
-      gate, need_rad_grad, dst=None):
+      gate, need_rad_grad, dst=None, wpack_t=None):
     d = (lmax + 1) ** 2
     c_out = grad_out.shape[2]
     f32 = dict(dtype=torch.float32)
@@ -207,21 +214,23 @@ def message_block(x, plan, eulers, rad, w0, b0, wm, lmax, mmax, gate=False):
 class _MessageOp(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, rad, w0, b0, plan, eulers, lmax, mmax, gate, *wm):
-        out, y, r, dk, g = message_block_fwd(x, rad, w0, b0, list(wm), plan.src, plan.dst, plan.seg_ptr, eulers,
-                                             lmax, mmax, gate)
+        # both weight packings from one launch when a backward will run
+        out, y, r, dk, g, wpt = message_block_fwd(x, rad, w0, b0, list(wm), plan.src, plan.dst, plan.seg_ptr,
+                                                  eulers, lmax, mmax, gate, any(ctx.needs_input_grad))
         ctx.plan, ctx.lmax, ctx.mmax, ctx.gate = plan, lmax, mmax, gate
         ctx.x_shape, ctx.dt, ctx.has_b0 = tuple(x.shape), x.dtype, b0 is not None
-        ctx.save_for_backward(rad, w0, y, dk, r if r.numel() else None, g if g.numel() else None, *wm)
+        ctx.save_for_backward(rad, w0, y, dk, r if r.numel() else None, g if g.numel() else None,
+                              wpt if wpt.numel() else None, *wm)
         return out
 
     @staticmethod
     def backward(ctx, gout):
-        rad, w0, y, dk, r, g, *wm = ctx.saved_tensors
+        rad, w0, y, dk, r, g, wpt, *wm = ctx.saved_tensors
         plan, lmax, mmax, gate = ctx.plan, ctx.lmax, ctx.mmax, ctx.gate
         need_rad = rad is not None and ctx.needs_input_grad[1]
         gx, grad_rad, dw0, db0, *dwm = message_block_bwd(
             gout, rad, w0, list(wm), plan.bwd_src, plan.bwd_dst, plan.bwd_eidx, plan.seg_ptr_src, y, dk, r, g,
-            ctx.x_shape[0], ctx.x_shape[2], lmax, mmax, gate, need_rad, plan.dst)
+            ctx.x_shape[0], ctx.x_shape[2], lmax, mmax, gate, need_rad, plan.dst, wpt)
         return (gx.to(ctx.dt), grad_rad if need_rad else None, dw0.to(w0.dtype), db0 if ctx.has_b0 else None,
                 None, None, None, None, None, *[d.to(w.dtype) for d, w in zip(dwm, wm)])
 

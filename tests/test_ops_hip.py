@@ -54,14 +54,18 @@ def test_opcheck(device):
     rad = torch.rand(E, M.rad_width(L, L, C), generator=gen).to(device)
     for gate in (False, True):
         w0g, b0g = (w0, b0) if gate else (w0[:(L + 1) * C], b0[:(L + 1) * C])
-        args = (xm, rad, w0g, b0g, wm, plan.src, plan.dst, plan.seg_ptr, plan.sort_edges(eul), L, L, gate)
-        torch.library.opcheck(ops.message_block_fwd, args, test_utils=("test_schema", "test_faketensor"))
-        out, y, r, dk, g = ops.message_block_fwd(*args)
-        gout = torch.randn(out.shape, generator=gen).to(device)
-        torch.library.opcheck(ops.message_block_bwd,
-                              (gout, rad, w0g, wm, plan.bwd_src, plan.bwd_dst, plan.bwd_eidx, plan.seg_ptr_src, y,
-                               dk, r, g if gate else None, N, C, L, L, gate, True),
-                              test_utils=("test_schema", "test_faketensor"))
+        for save_tr in (False, True):  # with save_tr the backward's weight packing comes along
+            args = (xm, rad, w0g, b0g, wm, plan.src, plan.dst, plan.seg_ptr, plan.sort_edges(eul), L, L, gate,
+                    save_tr)
+            torch.library.opcheck(ops.message_block_fwd, args, test_utils=("test_schema", "test_faketensor"))
+            out, y, r, dk, g, wpt = ops.message_block_fwd(*args)
+            assert (wpt.numel() > 0) == save_tr
+            gout = torch.randn(out.shape, generator=gen).to(device)
+            torch.library.opcheck(ops.message_block_bwd,
+                                  (gout, rad, w0g, wm, plan.bwd_src, plan.bwd_dst, plan.bwd_eidx, plan.seg_ptr_src,
+                                   y, dk, r, g if gate else None, N, C, L, L, gate, True, plan.dst,
+                                   wpt if save_tr else None),
+                                  test_utils=("test_schema", "test_faketensor"))
 
 
 @pytest.mark.gpu
