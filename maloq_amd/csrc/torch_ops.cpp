@@ -25,6 +25,8 @@
 //                                                fock_targets_batched.py:335-464
 //   irreps_to_fock(net_out, fock!, ...)          get_H + label2matrix (in place),
 //                                                splittrainer.py:1172-1233
+//   radial_fwd / radial_bwd(...)                 RadialMLP (radial.py:115-142), forward and
+//                                                its autograd backward
 // Private helpers (CPU): _jd_table(), _pack_index(...) expose the tables the
 // operators build, for tests.
 #include <ATen/ATen.h>
@@ -1111,6 +1113,121 @@ at::Tensor pack_index_cpu(int64_t code, int64_t lmax, int64_t mmax, bool gate, i
   return at::from_blob(idx.data(), {static_cast<int64_t>(idx.size())}, at::kLong).clone();
 }
 
+
+// ------------------------------------------------------------ radial MLP
+// The fused RadialMLP (radial.py:115-142): hidden layers Linear -> LayerNorm ->
+// SiLU, then the output Linear.  params: (W_i, b_i, gamma_i, beta_i) per
+// hidden layer, then (W_o, b_o); widths c_0 .. c_H, c_out.
+struct RadialShapes {
+  int nh;
+  std::vector<int> w;
+  std::vector<at::Tensor> p;  // fp32, contiguous
+  std::vector<const float*> W, b, g, bt;
+};
+
+RadialShapes radial_shapes(const at::Tensor& ref, at::TensorList params, at::IntArrayRef widths) {
+  RadialShapes r;
+  r.nh = static_cast<int>(widths.size()) - 2;
+  TORCH_CHECK_VALUE(r.nh >= 1, "RadialMLP needs at least one hidden layer");
+  TORCH_CHECK_VALUE(static_cast<int>(params.size()) == 4 * r.nh + 2,
+                    "params must be (W, b, LayerNorm weight, LayerNorm bias) per hidden layer, then W_o, b_o");
+  for (const auto v : widths) {
+    TORCH_CHECK_VALUE(v > 0 && v < (int64_t(1) << 30), "bad width ", v);
+    r.w.push_back(static_cast<int>(v));
+  }
+  TORCH_CHECK_VALUE(maloq_radial_bwd_partials_floats(0, r.nh, r.w.data(), 1) >= 0,
+                    "these widths are not supported by the fused radial kernels: ", maloq_last_error());
+  for (int i = 0; i < r.nh; ++i) {
+    const at::Tensor& W = params[4 * i];
+    TORCH_CHECK_VALUE(W.dim() == 2 && W.size(0) == widths[i + 1] && W.size(1) == widths[i],
+                      "hidden weight ", i, " must be [", widths[i + 1], ", ", widths[i], "]");
+    for (int k = 1; k < 4; ++k)
+      TORCH_CHECK_VALUE(params[4 * i + k].numel() == widths[i + 1], "hidden layer ", i, " vectors must have ",
+                        widths[i + 1], " entries");
+  }
+  const at::Tensor& Wo = params[4 * r.nh];
+  TORCH_CHECK_VALUE(Wo.dim() == 2 && Wo.size(0) == widths[r.nh + 1] && Wo.size(1) == widths[r.nh],
+                    "output weight must be [c_out, c_H]");
+  TORCH_CHECK_VALUE(params[4 * r.nh + 1].numel() == widths[r.nh + 1], "output bias must have c_out entries");
+  for (const auto& t : params) {
+    TORCH_CHECK_VALUE(t.device() == ref.device(), "all tensors must be on ", ref.device());
+    r.p.push_back(t.detach().to(at::kFloat).contiguous());
+  }
+  for (int i = 0; i < r.nh; ++i) {
+    r.W.push_back(r.p[4 * i].data_ptr<float>());
+    r.b.push_back(r.p[4 * i + 1].data_ptr<float>());
+    r.g.push_back(r.p[4 * i + 2].data_ptr<float>());
+    r.bt.push_back(r.p[4 * i + 3].data_ptr<float>());
+  }
+  return r;
+}
+
+// [out [E, c_out] (bf16 or fp32), wpack (the packed output weights, read by
+// radial_bwd), u_H [E, c_H] (the last hidden activation, empty unless save)].
+std::vector<at::Tensor> radial_fwd(const at::Tensor& x, at::TensorList params, at::IntArrayRef widths, double eps,
+                                   bool bf16, bool save) {
+  require_gpu(x, "x");
+  TORCH_CHECK_VALUE(x.dim() == 2 && widths.size() >= 3 && x.size(1) == widths[0], "x must be [E, c_0]");
+  const c10::DeviceGuard guard(x.device());
+  RadialShapes r = radial_shapes(x, params, widths);
+  const int code = bf16 ? 1 : 0;
+  const auto dt = bf16 ? at::kBFloat16 : at::kFloat;
+  const int64_t E = x.size(0), cH = widths[r.nh], cout = widths[r.nh + 1];
+  const at::Tensor xc = x.detach().to(at::kFloat).contiguous();
+  at::Tensor wpack = at::empty({maloq_radial_pack_bytes(code, static_cast<int>(cout), static_cast<int>(cH))},
+                               x.options().dtype(at::kByte));
+  at::Tensor out = at::empty({E, cout}, x.options().dtype(dt));
+  at::Tensor sv = save ? at::empty({E, cH}, x.options().dtype(dt)) : at::empty({0}, x.options().dtype(dt));
+  check_rc(maloq_radial_fwd(code, r.nh, r.w.data(), xc.data_ptr<float>(), E, r.W.data(), r.b.data(), r.g.data(),
+                            r.bt.data(), static_cast<float>(eps), r.p[4 * r.nh].data_ptr<float>(),
+                            r.p[4 * r.nh + 1].data_ptr<float>(), wpack.data_ptr(), out.data_ptr(),
+                            save ? sv.data_ptr() : nullptr, stream_of(x)),
+           "maloq_radial_fwd");
+  return {out, wpack, sv};
+}
+
+// Gradients from radial_fwd's wpack and u_H: [dx [E, c_0] (empty unless
+// need_dx), the hidden layers' gradients flat (per layer dW_i, db_i,
+// dgamma_i, dbeta_i), dW_o, db_o], fp32, deterministic.
+std::vector<at::Tensor> radial_bwd(const at::Tensor& grad, const at::Tensor& x, const at::Tensor& wpack,
+                                   const at::Tensor& save, at::TensorList params, at::IntArrayRef widths, double eps,
+                                   bool need_dx) {
+  require_gpu(grad, "grad");
+  const c10::DeviceGuard guard(grad.device());
+  RadialShapes r = radial_shapes(grad, params, widths);
+  const bool bf16 = save.scalar_type() == at::kBFloat16;
+  const int code = bf16 ? 1 : 0;
+  const auto dt = save.scalar_type();
+  const int64_t E = x.size(0), c0 = widths[0], cH = widths[r.nh], cout = widths[r.nh + 1];
+  TORCH_CHECK_VALUE(x.dim() == 2 && x.size(1) == c0 && grad.dim() == 2 && grad.size(0) == E &&
+                        grad.size(1) == cout && save.dim() == 2 && save.size(0) == E && save.size(1) == cH,
+                    "x [E, c_0], grad [E, c_out] and the saved u_H [E, c_H] must agree");
+  TORCH_CHECK_VALUE(wpack.scalar_type() == at::kByte && wpack.is_contiguous() &&
+                        wpack.numel() == maloq_radial_pack_bytes(code, static_cast<int>(cout), static_cast<int>(cH)),
+                    "wpack must be radial_fwd's packed weights");
+  same_device(grad, {x, wpack, save});
+  int64_t n_hid = 0;
+  for (int i = 0; i < r.nh; ++i) n_hid += widths[i + 1] * (widths[i] + 3);
+  const auto opt32 = grad.options().dtype(at::kFloat);
+  if (E == 0)  // no edges: every gradient is zero
+    return {need_dx ? at::zeros({E, c0}, opt32) : at::empty({0}, opt32), at::zeros({n_hid}, opt32),
+            at::zeros({cout, cH}, opt32), at::zeros({cout}, opt32)};
+  at::Tensor dx = need_dx ? at::empty({E, c0}, opt32) : at::empty({0}, opt32);
+  at::Tensor gh = at::empty({n_hid}, opt32), dwo = at::empty({cout, cH}, opt32), dbo = at::empty({cout}, opt32);
+  const at::Tensor xc = x.detach().to(at::kFloat).contiguous();
+  const at::Tensor gq = grad.to(dt).contiguous();
+  const at::Tensor sq = save.contiguous();
+  const int64_t pf = maloq_radial_bwd_partials_floats(code, r.nh, r.w.data(), E);
+  TORCH_CHECK(pf >= 0, "maloq_radial_bwd_partials_floats failed: ", maloq_last_error());
+  at::Tensor parts = at::empty({pf > 1 ? pf : 1}, opt32);
+  check_rc(maloq_radial_bwd(code, r.nh, r.w.data(), xc.data_ptr<float>(), E, r.W.data(), r.b.data(), r.g.data(),
+                            r.bt.data(), static_cast<float>(eps), wpack.data_ptr(), gq.data_ptr(), sq.data_ptr(),
+                            need_dx ? dx.data_ptr<float>() : nullptr, parts.data_ptr<float>(), gh.data_ptr<float>(),
+                            dwo.data_ptr<float>(), dbo.data_ptr<float>(), stream_of(grad)),
+           "maloq_radial_bwd");
+  return {dx, gh, dwo, dbo};
+}
+
 }  // namespace
 
 TORCH_LIBRARY(maloq_hip, m) {
@@ -1147,6 +1264,9 @@ TORCH_LIBRARY(maloq_hip, m) {
         "Tensor? Z, Tensor? rows, Tensor? cols, Tensor? meta, int num_rows, Tensor pair_kind, Tensor slots, "
         "int maxe, Tensor kind_blocks, Tensor? perm_in, int t, int num_blocks, Tensor blocks, Tensor? w, "
         "Tensor sched, int ngroups, int group_cols, Tensor? perm_pre) -> ()");
+  m.def("radial_fwd(Tensor x, Tensor[] params, int[] widths, float eps, bool bf16, bool save) -> Tensor[]");
+  m.def("radial_bwd(Tensor grad, Tensor x, Tensor wpack, Tensor save, Tensor[] params, int[] widths, float eps, "
+        "bool need_dx) -> Tensor[]");
   m.def("_jd_table() -> Tensor", &jd_table);
   m.def("_pack_index(int dtype_code, int lmax, int mmax, bool gate, int c_in, int c_out, int mode) -> Tensor",
         &pack_index_cpu);
@@ -1167,4 +1287,6 @@ TORCH_LIBRARY_IMPL(maloq_hip, CUDA, m) {
   m.impl("basis_row_meta", &basis_row_meta);
   m.impl("fock_to_irreps", &fock_to_irreps);
   m.impl("irreps_to_fock", &irreps_to_fock);
+  m.impl("radial_fwd", &radial_fwd);
+  m.impl("radial_bwd", &radial_bwd);
 }

@@ -17,10 +17,11 @@ ops with known output shapes, and the autograd formulas.
     maloq_hip::message_block_fwd(x, rad?, w0, b0?, wm, plan tensors, eulers, lmax, mmax, gate)
                                                           Edgewise.forward_node with one convolution
     maloq_hip::edgewise_fwd / edgewise_bwd(..)            the two-convolution Edgewise, both modes
+    maloq_hip::radial_fwd / radial_bwd(..)                the fused RadialMLP
 
 Reference interfaces: helm/triton_kernels/wigner_fused.py:383-486,
 helm/common/rotation.py:19-39, helm/esen_block.py:146-208,
-fock_utils/utils_tensor_decomp.py:154-169.
+helm/nn/radial.py:115-142, fock_utils/utils_tensor_decomp.py:154-169.
 """
 from __future__ import annotations
 
@@ -233,6 +234,32 @@ class _MessageOp(torch.autograd.Function):
             ctx.x_shape[0], ctx.x_shape[2], lmax, mmax, gate, need_rad, plan.dst, wpt)
         return (gx.to(ctx.dt), grad_rad if need_rad else None, dw0.to(w0.dtype), db0 if ctx.has_b0 else None,
                 None, None, None, None, None, *[d.to(w.dtype) for d, w in zip(dwm, wm)])
+
+
+# --------------------------------------------------------------- radial MLP
+# Fused RadialMLP: [out, wpack, u_H] forward, [dx, hidden grads (flat), dW_o,
+# db_o] backward (maloq_amd.radial holds the autograd wiring).
+radial_fwd = _ops.radial_fwd
+radial_bwd = _ops.radial_bwd
+
+
+@register_fake("maloq_hip::radial_fwd")
+def _(x, params, widths, eps, bf16, save):
+    E = x.shape[0]
+    dt = torch.bfloat16 if bf16 else torch.float32
+    nb = int(_lib.load().maloq_radial_pack_bytes(1 if bf16 else 0, widths[-1], widths[-2]))
+    return [x.new_empty(E, widths[-1], dtype=dt), x.new_empty(nb, dtype=torch.uint8),
+            x.new_empty(E, widths[-2], dtype=dt) if save else x.new_empty(0, dtype=dt)]
+
+
+@register_fake("maloq_hip::radial_bwd")
+def _(grad, x, wpack, save, params, widths, eps, need_dx):
+    E = x.shape[0]
+    n_hid = sum(widths[i + 1] * (widths[i] + 3) for i in range(len(widths) - 2))
+    f32 = dict(dtype=torch.float32)
+    return [grad.new_empty(E, widths[0], **f32) if need_dx else grad.new_empty(0, **f32),
+            grad.new_empty(n_hid, **f32), grad.new_empty(widths[-1], widths[-2], **f32),
+            grad.new_empty(widths[-1], **f32)]
 
 
 # -------------------------------------------------- two-convolution Edgewise

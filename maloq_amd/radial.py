@@ -119,68 +119,33 @@ def radial_mlp(inputs: torch.Tensor, mod: RadialMLP, out_dtype: torch.dtype | No
     return _RadialFn.apply(inputs, dt, widths, eps, *params)
 
 
-def _ptr_array(ts):
-    return (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])
-
-
 def _widths_array(widths):
     return (ctypes.c_int * len(widths))(*widths)
 
 
 class _RadialFn(torch.autograd.Function):
+    """Autograd of the fused MLP through the registered operators
+    maloq_hip::radial_fwd / radial_bwd."""
+
     @staticmethod
     def forward(ctx, x, dt, widths, eps, *params):
-        nh = len(widths) - 2
-        code = DTYPE_CODE[dt]
-        x = x.float().contiguous()
-        ps = [p.detach().float().contiguous() for p in params]
-        hid = [ps[4 * i: 4 * i + 4] for i in range(nh)]
-        wo, bo = ps[-2], ps[-1]
-        E, dev = x.shape[0], x.device
-        lib = _lib.load()
-        wpack = torch.empty(lib.maloq_radial_pack_bytes(code, widths[-1], widths[-2]), dtype=torch.uint8,
-                            device=dev)
-        out = torch.empty(E, widths[-1], dtype=dt, device=dev)
+        from . import ops
         need = any(ctx.needs_input_grad[:1] + ctx.needs_input_grad[4:])
-        save = torch.empty(E, widths[-2], dtype=dt, device=dev) if need else None
-        wa = _widths_array(widths)
-        _lib.call("maloq_radial_fwd", code, nh, wa, _lib.ptr(x), E,
-                  _ptr_array([h[0] for h in hid]), _ptr_array([h[1] for h in hid]),
-                  _ptr_array([h[2] for h in hid]), _ptr_array([h[3] for h in hid]), float(eps),
-                  _lib.ptr(wo), _lib.ptr(bo), _lib.ptr(wpack), _lib.ptr(out), _lib.ptr(save),
-                  _lib.stream_of(dev))
-        ctx.widths, ctx.eps, ctx.dt, ctx.code = widths, eps, dt, code
+        out, wpack, save = ops.radial_fwd(x, list(params), list(widths), float(eps), dt == torch.bfloat16, need)
+        ctx.widths, ctx.eps, ctx.dt = widths, eps, dt
         ctx.param_dtypes = [p.dtype for p in params]
         if need:
-            ctx.save_for_backward(x, wpack, save, *ps)
+            ctx.save_for_backward(x, wpack, save, *params)
         return out
 
     @staticmethod
     def backward(ctx, g):
+        from . import ops
         x, wpack, save, *ps = ctx.saved_tensors
-        widths, code = ctx.widths, ctx.code
+        widths = ctx.widths
         nh = len(widths) - 2
-        hid = [ps[4 * i: 4 * i + 4] for i in range(nh)]
-        E, dev = x.shape[0], x.device
-        cH, cout = widths[-2], widths[-1]
-        if E == 0:
-            grads = [torch.zeros_like(p) for p in ps]
-            dx = torch.zeros_like(x) if ctx.needs_input_grad[0] else None
-            return (dx, None, None, None, *[gr.to(d) for gr, d in zip(grads, ctx.param_dtypes)])
-        g = g.to(ctx.dt).contiguous()
-        lib = _lib.load()
-        wa = _widths_array(widths)
-        parts = torch.empty(lib.maloq_radial_bwd_partials_floats(code, nh, wa, E), dtype=torch.float32, device=dev)
-        n_hid = sum(widths[i + 1] * (widths[i] + 3) for i in range(nh))
-        gh = torch.empty(n_hid, dtype=torch.float32, device=dev)
-        dwo = torch.empty(cout, cH, dtype=torch.float32, device=dev)
-        dbo = torch.empty(cout, dtype=torch.float32, device=dev)
-        dx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
-        _lib.call("maloq_radial_bwd", code, nh, wa, _lib.ptr(x), E,
-                  _ptr_array([h[0] for h in hid]), _ptr_array([h[1] for h in hid]),
-                  _ptr_array([h[2] for h in hid]), _ptr_array([h[3] for h in hid]), float(ctx.eps),
-                  _lib.ptr(wpack), _lib.ptr(g), _lib.ptr(save), _lib.ptr(dx), _lib.ptr(parts),
-                  _lib.ptr(gh), _lib.ptr(dwo), _lib.ptr(dbo), _lib.stream_of(dev))
+        dx, gh, dwo, dbo = ops.radial_bwd(g, x, wpack, save, list(ps), list(widths), float(ctx.eps),
+                                          bool(ctx.needs_input_grad[0]))
         grads = []
         off = 0
         for i in range(nh):
@@ -192,4 +157,4 @@ class _RadialFn(torch.autograd.Function):
                 off += c
         grads += [dwo, dbo]
         grads = [gr.to(d) for gr, d in zip(grads, ctx.param_dtypes)]
-        return (dx, None, None, None, *grads)
+        return (dx.to(x.dtype) if ctx.needs_input_grad[0] else None, None, None, None, *grads)

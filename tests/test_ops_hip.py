@@ -294,3 +294,28 @@ def test_compiled_edgewise_forward_and_backward_have_no_graph_break(device):
     assert len(got) == len(want)
     for a, b in zip(got, want):
         assert a.shape == b.shape and torch.equal(a, b)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bf16", [False, True])
+def test_radial_ops_opcheck(bf16, device):
+    """Schema and fake implementations of maloq_hip::radial_fwd / radial_bwd
+    on the arguments maloq_amd.radial passes."""
+    from maloq_amd import ops
+    from maloq_amd.radial import RadialMLP
+    torch.manual_seed(3)
+    widths = [8, 64, 64, 128]
+    mod = RadialMLP(widths).to(device)
+    params = [p.detach() for li, ln in zip([m for m in mod.net if isinstance(m, torch.nn.Linear)][:-1],
+                                           [m for m in mod.net if isinstance(m, torch.nn.LayerNorm)])
+              for p in (li.weight, li.bias, ln.weight, ln.bias)]
+    lo = [m for m in mod.net if isinstance(m, torch.nn.Linear)][-1]
+    params += [lo.weight.detach(), lo.bias.detach()]
+    x = torch.randn(150, 8, device=device)
+    eps = [m for m in mod.net if isinstance(m, torch.nn.LayerNorm)][0].eps
+    args = (x, params, widths, eps, bf16, True)
+    torch.library.opcheck(ops.radial_fwd, args, test_utils=("test_schema", "test_faketensor"))
+    out, wpack, save = ops.radial_fwd(*args)
+    g = torch.randn(out.shape, device=device).to(out.dtype)
+    torch.library.opcheck(ops.radial_bwd, (g, x, wpack, save, params, widths, eps, True),
+                          test_utils=("test_schema", "test_faketensor"))
