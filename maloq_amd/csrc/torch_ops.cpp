@@ -27,6 +27,9 @@
 //                                                splittrainer.py:1172-1233
 //   radial_fwd / radial_bwd(...)                 RadialMLP (radial.py:115-142), forward and
 //                                                its autograd backward
+//   edge_m0_rows, edge_degree_embed[_],          EdgeDegreeEmbedding (embedding.py:17-141):
+//   edge_degree_embed_bwd(...)                   m = 0 rows, the embedding (node: in place or a
+//                                                copy of x; edge), the gradient wrt the radial rows
 // Private helpers (CPU): _jd_table(), _pack_index(...) expose the tables the
 // operators build, for tests.
 #include <ATen/ATen.h>
@@ -1228,6 +1231,121 @@ std::vector<at::Tensor> radial_bwd(const at::Tensor& grad, const at::Tensor& x, 
   return {dx, gh, dwo, dbo};
 }
 
+
+// ------------------------------------------------------ edge-degree embedding
+// EdgeDegreeEmbedding (embedding.py:17-141): the m = 0 rows of every edge's
+// Wigner blocks, then the rotated radial embedding summed into x per
+// destination node (in place, index_add_ order) or kept per edge.
+
+// rows [E, d] fp32 from exactly one of wigner_inv [E, d, d] and eulers [E, 3].
+at::Tensor edge_m0_rows(const c10::optional<at::Tensor>& wigner_inv, const c10::optional<at::Tensor>& eulers,
+                        int64_t lmax, int64_t num_edges) {
+  TORCH_CHECK_VALUE(wigner_inv.has_value() != eulers.has_value(), "give exactly one of wigner_inv and eulers");
+  TORCH_CHECK_VALUE(lmax >= 0 && lmax <= 6 && num_edges >= 0, "lmax must be 0..6");
+  const at::Tensor& ref = wigner_inv.has_value() ? *wigner_inv : *eulers;
+  require_gpu(ref, wigner_inv.has_value() ? "wigner_inv" : "eulers");
+  const int64_t d = (lmax + 1) * (lmax + 1);
+  at::Tensor w, e;
+  if (wigner_inv.has_value()) {
+    TORCH_CHECK_VALUE(wigner_inv->dim() == 3 && wigner_inv->size(0) == num_edges && wigner_inv->size(1) == d &&
+                          wigner_inv->size(2) == d,
+                      "wigner_inv must be [E, (lmax+1)^2, (lmax+1)^2]");
+    w = wigner_inv->to(at::kFloat).contiguous();
+  } else {
+    TORCH_CHECK_VALUE(eulers->dim() == 2 && eulers->size(0) == num_edges && eulers->size(1) == 3,
+                      "eulers must be [E, 3]");
+    e = eulers->to(at::kFloat).contiguous();
+  }
+  const c10::DeviceGuard guard(ref.device());
+  at::Tensor rows = at::empty({num_edges, d}, ref.options().dtype(at::kFloat));
+  check_rc(maloq_edge_m0_rows(static_cast<int>(lmax), num_edges, w.defined() ? w.data_ptr<float>() : nullptr,
+                              e.defined() ? e.data_ptr<float>() : nullptr, e.defined() ? jd_on(ref.device()) : nullptr,
+                              rows.data_ptr<float>(), stream_of(ref)),
+           "maloq_edge_m0_rows");
+  return rows;
+}
+
+// Shared checks of the embedding; returns the edge count.
+int64_t embed_checks(const at::Tensor& u, const at::Tensor& rows, const at::Tensor& x, int64_t lmax,
+                     int64_t channels) {
+  require_gpu(u, "u");
+  const int64_t E = u.size(0), d = (lmax + 1) * (lmax + 1);
+  TORCH_CHECK_VALUE(lmax >= 0 && lmax <= 6 && channels > 0, "lmax must be 0..6 and channels positive");
+  TORCH_CHECK_VALUE(u.dim() == 2 && u.size(1) == (lmax + 1) * channels, "u must be [E, (lmax+1) C]");
+  TORCH_CHECK_VALUE(rows.dim() == 2 && rows.size(0) == E && rows.size(1) == d && rows.scalar_type() == at::kFloat,
+                    "rows must be float32 [E, (lmax+1)^2]");
+  TORCH_CHECK_VALUE(x.dim() == 3 && x.size(1) == d && x.size(2) == channels, "x must be [N, (lmax+1)^2, C]");
+  dtype_code(u.scalar_type());
+  dtype_code(x.scalar_type());
+  same_device(u, {rows, x});
+  return E;
+}
+
+// Node mode, in place on x: x[dst_e] += emb_e / rescale in index_add_ order.
+void edge_degree_embed_(at::Tensor& x, const at::Tensor& u, const at::Tensor& rows, const at::Tensor& seg_ptr,
+                        const at::Tensor& perm, int64_t lmax, int64_t channels, double rescale) {
+  const int64_t E = embed_checks(u, rows, x, lmax, channels);
+  TORCH_CHECK_VALUE(x.is_contiguous(), "x must be contiguous for the in-place embedding");
+  TORCH_CHECK_VALUE(seg_ptr.scalar_type() == at::kLong && perm.scalar_type() == at::kLong &&
+                        seg_ptr.numel() == x.size(0) + 1 && perm.numel() == E,
+                    "seg_ptr [N + 1] and perm [E] must be int64 (the dst plan)");
+  same_device(u, {seg_ptr, perm});
+  const c10::DeviceGuard guard(u.device());
+  const at::Tensor uc = u.contiguous();
+  check_rc(maloq_edge_degree_embed(dtype_code(u.scalar_type()), dtype_code(x.scalar_type()), static_cast<int>(lmax),
+                                   uc.data_ptr(), E, static_cast<int>(channels), rows.data_ptr<float>(),
+                                   iptr<int64_t>(seg_ptr), iptr<int64_t>(perm), x.size(0), static_cast<float>(rescale),
+                                   x.data_ptr(), nullptr, stream_of(u)),
+           "maloq_edge_degree_embed");
+}
+
+// The same into a copy of x (node), or the per-edge embedding [E, d, C] in
+// the dtype of x (edge mode: x only gives the dtype and shape).
+at::Tensor edge_degree_embed(const at::Tensor& x, const at::Tensor& u, const at::Tensor& rows,
+                             const c10::optional<at::Tensor>& seg_ptr, const c10::optional<at::Tensor>& perm,
+                             int64_t lmax, int64_t channels, double rescale, bool node) {
+  const int64_t E = embed_checks(u, rows, x, lmax, channels);
+  if (node) {
+    TORCH_CHECK_VALUE(seg_ptr.has_value() && perm.has_value(), "node mode needs the dst plan (seg_ptr, perm)");
+    at::Tensor out = x.clone(at::MemoryFormat::Contiguous);
+    edge_degree_embed_(out, u, rows, *seg_ptr, *perm, lmax, channels, rescale);
+    return out;
+  }
+  const c10::DeviceGuard guard(u.device());
+  const int64_t d = (lmax + 1) * (lmax + 1);
+  at::Tensor emb = at::empty({E, d, channels}, x.options());
+  const at::Tensor uc = u.contiguous();
+  check_rc(maloq_edge_degree_embed(dtype_code(u.scalar_type()), dtype_code(x.scalar_type()), static_cast<int>(lmax),
+                                   uc.data_ptr(), E, static_cast<int>(channels), rows.data_ptr<float>(), nullptr,
+                                   nullptr, 0, static_cast<float>(rescale), x.data_ptr(), emb.data_ptr(), stream_of(u)),
+           "maloq_edge_degree_embed");
+  return emb;
+}
+
+// grad_u [E, (lmax+1) C] fp32 = scale sum_j D[l][j] grad[grad_rows[e]][l^2 + j]
+// (node mode: grad_rows = dst, scale = 1 / rescale; edge mode: the identity).
+at::Tensor edge_degree_embed_bwd(const at::Tensor& grad, const c10::optional<at::Tensor>& grad_rows,
+                                 const at::Tensor& rows, int64_t lmax, int64_t channels, double scale) {
+  require_gpu(grad, "grad");
+  const int64_t E = rows.size(0), d = (lmax + 1) * (lmax + 1);
+  TORCH_CHECK_VALUE(grad.dim() == 3 && grad.size(1) == d && grad.size(2) == channels,
+                    "grad must be [*, (lmax+1)^2, C]");
+  TORCH_CHECK_VALUE(rows.dim() == 2 && rows.size(1) == d && rows.scalar_type() == at::kFloat,
+                    "rows must be float32 [E, (lmax+1)^2]");
+  TORCH_CHECK_VALUE(grad_rows.has_value() ? (grad_rows->scalar_type() == at::kLong && grad_rows->numel() == E)
+                                          : grad.size(0) == E,
+                    "grad_rows must be int64 [E] (or grad [E, d, C] per edge)");
+  same_device(grad, {grad_rows, rows});
+  const c10::DeviceGuard guard(grad.device());
+  const at::Tensor gq = (grad.scalar_type() == at::kBFloat16 ? grad : grad.to(at::kFloat)).contiguous();
+  at::Tensor gu = at::empty({E, (lmax + 1) * channels}, grad.options().dtype(at::kFloat));
+  check_rc(maloq_edge_degree_embed_bwd(dtype_code(gq.scalar_type()), static_cast<int>(lmax), gq.data_ptr(),
+                                       cptr<int64_t>(grad_rows), E, static_cast<int>(channels), rows.data_ptr<float>(),
+                                       static_cast<float>(scale), gu.data_ptr<float>(), stream_of(grad)),
+           "maloq_edge_degree_embed_bwd");
+  return gu;
+}
+
 }  // namespace
 
 TORCH_LIBRARY(maloq_hip, m) {
@@ -1267,6 +1385,13 @@ TORCH_LIBRARY(maloq_hip, m) {
   m.def("radial_fwd(Tensor x, Tensor[] params, int[] widths, float eps, bool bf16, bool save) -> Tensor[]");
   m.def("radial_bwd(Tensor grad, Tensor x, Tensor wpack, Tensor save, Tensor[] params, int[] widths, float eps, "
         "bool need_dx) -> Tensor[]");
+  m.def("edge_m0_rows(Tensor? wigner_inv, Tensor? eulers, int lmax, int num_edges) -> Tensor");
+  m.def("edge_degree_embed(Tensor x, Tensor u, Tensor rows, Tensor? seg_ptr, Tensor? perm, int lmax, int channels, "
+        "float rescale, bool node) -> Tensor");
+  m.def("edge_degree_embed_(Tensor(a!) x, Tensor u, Tensor rows, Tensor seg_ptr, Tensor perm, int lmax, "
+        "int channels, float rescale) -> ()");
+  m.def("edge_degree_embed_bwd(Tensor grad, Tensor? grad_rows, Tensor rows, int lmax, int channels, float scale) "
+        "-> Tensor");
   m.def("_jd_table() -> Tensor", &jd_table);
   m.def("_pack_index(int dtype_code, int lmax, int mmax, bool gate, int c_in, int c_out, int mode) -> Tensor",
         &pack_index_cpu);
@@ -1289,4 +1414,8 @@ TORCH_LIBRARY_IMPL(maloq_hip, CUDA, m) {
   m.impl("irreps_to_fock", &irreps_to_fock);
   m.impl("radial_fwd", &radial_fwd);
   m.impl("radial_bwd", &radial_bwd);
+  m.impl("edge_m0_rows", &edge_m0_rows);
+  m.impl("edge_degree_embed", &edge_degree_embed);
+  m.impl("edge_degree_embed_", &edge_degree_embed_);
+  m.impl("edge_degree_embed_bwd", &edge_degree_embed_bwd);
 }

@@ -8,9 +8,9 @@ permuted to l-major (``einsum`` with ``to_m``), rotated back with
 (``x.index_add_(0, dst, emb / rescale_factor)``), or returned per edge.
 
 Here the radial function is the fused HIP :class:`~maloq_amd.radial.RadialMLP`
-and the rest is two launches: ``maloq_edge_m0_rows`` (the m = 0 row of every
-block of D, the only part of ``wigner_inv`` that meets a non-zero) and
-``maloq_edge_degree_embed`` (each edge adds a rank-one product per degree; the
+and the rest is two launches, each a ``maloq_hip`` operator: ``edge_m0_rows``
+(the m = 0 row of every block of D, the only part of ``wigner_inv`` that meets
+a non-zero) and ``edge_degree_embed`` (each edge adds a rank-one product per degree; the
 node sum runs per node in the stable dst-sorted order, deterministic, no
 atomics).  ``wigner_inv`` may be the
 reference's dense ``[E, d, d]`` tensor, or ``None`` with ``eulers=`` (the
@@ -25,7 +25,7 @@ import torch
 from torch import nn
 
 from . import _lib
-from .message import _jd_dev, plan_for
+from .message import plan_for
 from .radial import RadialMLP
 
 DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1}
@@ -104,32 +104,22 @@ def edge_degree_embed(x, u, edge_index, wigner_inv, lmax, rescale_factor, node_o
 
 
 def _m0_rows(wigner_inv, eul, lmax, E, dev):
-    """rows [E, d]: the m = 0 row of every block of D (maloq_edge_m0_rows)."""
-    rows = torch.empty(E, (lmax + 1) ** 2, dtype=torch.float32, device=dev)
-    jd = _jd_dev(lmax, dev) if eul is not None else None
-    _lib.call("maloq_edge_m0_rows", lmax, E, _lib.ptr(wigner_inv), _lib.ptr(eul), _lib.ptr(jd), _lib.ptr(rows),
-              _lib.stream_of(dev))
-    return rows
+    """rows [E, d]: the m = 0 row of every block of D."""
+    from . import ops
+    return ops.edge_m0_rows(wigner_inv, eul, lmax, E)
 
 
 def _forward(x, u, rows, lmax, C, rescale, node, plan, in_place):
-    dev = u.device
-    d = (lmax + 1) ** 2
-    if node:
-        out = x if in_place else x.clone()
-        out = out if out.is_contiguous() else out.contiguous()
-        _lib.call("maloq_edge_degree_embed", DTYPE_CODE[u.dtype], DTYPE_CODE[x.dtype], lmax, _lib.ptr(u),
-                  u.shape[0], C, _lib.ptr(rows), _lib.ptr(plan.seg_ptr), _lib.ptr(plan.perm), out.shape[0],
-                  rescale, _lib.ptr(out), None, _lib.stream_of(dev))
-        if in_place and out.data_ptr() != x.data_ptr():
-            x.copy_(out)
-            return x
-        return out
-    emb = torch.empty(u.shape[0], d, C, dtype=x.dtype, device=dev)
-    _lib.call("maloq_edge_degree_embed", DTYPE_CODE[u.dtype], DTYPE_CODE[x.dtype], lmax, _lib.ptr(u),
-              u.shape[0], C, _lib.ptr(rows), None, None, 0, rescale, _lib.ptr(x), _lib.ptr(emb),
-              _lib.stream_of(dev))
-    return emb
+    from . import ops
+    if node and in_place and x.is_contiguous():
+        ops.edge_degree_embed_(x, u, rows, plan.seg_ptr, plan.perm, lmax, C, rescale)
+        return x
+    out = ops.edge_degree_embed(x, u, rows, plan.seg_ptr if node else None, plan.perm if node else None,
+                                lmax, C, rescale, node)
+    if node and in_place:
+        x.copy_(out)
+        return x
+    return out
 
 
 class _EmbedFn(torch.autograd.Function):
@@ -143,19 +133,11 @@ class _EmbedFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, g):
+        from . import ops
         (rows,) = ctx.saved_tensors
-        lmax, C = ctx.lmax, ctx.C
-        E = rows.shape[0]
-        dev = g.device
-        g = g.contiguous()
-        if g.dtype not in DTYPE_CODE:
-            g = g.float()
         grad_u = None
         if ctx.needs_input_grad[1]:
-            grad_u = torch.empty(E, (lmax + 1) * C, dtype=torch.float32, device=dev)
-            _lib.call("maloq_edge_degree_embed_bwd", DTYPE_CODE[g.dtype], lmax, _lib.ptr(g), _lib.ptr(ctx.dst),
-                      E, C, _lib.ptr(rows), 1.0 / ctx.rescale if ctx.node else 1.0, _lib.ptr(grad_u),
-                      _lib.stream_of(dev))
-            grad_u = grad_u.to(ctx.u_dtype)
+            grad_u = ops.edge_degree_embed_bwd(g, ctx.dst, rows, ctx.lmax, ctx.C,
+                                               1.0 / ctx.rescale if ctx.node else 1.0).to(ctx.u_dtype)
         grad_x = g if (ctx.node and ctx.needs_input_grad[0]) else None
         return grad_x, grad_u, None, None, None, None, None, None, None

@@ -18,10 +18,13 @@ ops with known output shapes, and the autograd formulas.
                                                           Edgewise.forward_node with one convolution
     maloq_hip::edgewise_fwd / edgewise_bwd(..)            the two-convolution Edgewise, both modes
     maloq_hip::radial_fwd / radial_bwd(..)                the fused RadialMLP
+    maloq_hip::edge_m0_rows / edge_degree_embed[_] / edge_degree_embed_bwd(..)
+                                                          EdgeDegreeEmbedding (node or edge mode)
 
 Reference interfaces: helm/triton_kernels/wigner_fused.py:383-486,
 helm/common/rotation.py:19-39, helm/esen_block.py:146-208,
-helm/nn/radial.py:115-142, fock_utils/utils_tensor_decomp.py:154-169.
+helm/nn/radial.py:115-142, helm/nn/embedding.py:17-141,
+fock_utils/utils_tensor_decomp.py:154-169.
 """
 from __future__ import annotations
 
@@ -260,6 +263,39 @@ def _(grad, x, wpack, save, params, widths, eps, need_dx):
     return [grad.new_empty(E, widths[0], **f32) if need_dx else grad.new_empty(0, **f32),
             grad.new_empty(n_hid, **f32), grad.new_empty(widths[-1], widths[-2], **f32),
             grad.new_empty(widths[-1], **f32)]
+
+
+# ---------------------------------------------------- edge-degree embedding
+# EdgeDegreeEmbedding: m = 0 rows [E, d] fp32, the embedding (node: a copy of
+# x with the edges summed in, or in place; edge: [E, d, C]) and the gradient
+# wrt the radial rows (maloq_amd.embedding holds the autograd wiring).
+edge_m0_rows = _ops.edge_m0_rows
+edge_degree_embed = _ops.edge_degree_embed
+edge_degree_embed_ = _ops.edge_degree_embed_
+edge_degree_embed_bwd = _ops.edge_degree_embed_bwd
+
+
+@register_fake("maloq_hip::edge_m0_rows")
+def _(wigner_inv, eulers, lmax, num_edges):
+    ref = wigner_inv if wigner_inv is not None else eulers
+    return ref.new_empty(num_edges, (lmax + 1) ** 2, dtype=torch.float32)
+
+
+@register_fake("maloq_hip::edge_degree_embed")
+def _(x, u, rows, seg_ptr, perm, lmax, channels, rescale, node):
+    if node:
+        return torch.empty_like(x, memory_format=torch.contiguous_format)
+    return x.new_empty(u.shape[0], (lmax + 1) ** 2, channels)
+
+
+@register_fake("maloq_hip::edge_degree_embed_")
+def _(x, u, rows, seg_ptr, perm, lmax, channels, rescale):
+    return None
+
+
+@register_fake("maloq_hip::edge_degree_embed_bwd")
+def _(grad, grad_rows, rows, lmax, channels, scale):
+    return grad.new_empty(rows.shape[0], (lmax + 1) * channels, dtype=torch.float32)
 
 
 # -------------------------------------------------- two-convolution Edgewise

@@ -319,3 +319,37 @@ def test_radial_ops_opcheck(bf16, device):
     g = torch.randn(out.shape, device=device).to(out.dtype)
     torch.library.opcheck(ops.radial_bwd, (g, x, wpack, save, params, widths, eps, True),
                           test_utils=("test_schema", "test_faketensor"))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["node", "edge"])
+def test_embedding_ops_opcheck(mode, device):
+    """Schema and fake implementations of the EdgeDegreeEmbedding operators on
+    the arguments maloq_amd.embedding passes, and the in-place node variant
+    equal to the functional one."""
+    from maloq_amd import ops
+    from maloq_amd.message import MessagePlan
+    from maloq_amd.wigner import extract_euler_angles
+    torch.manual_seed(4)
+    lmax, C, N, E = 4, 32, 40, 300
+    ei = torch.randint(0, N, (2, E), device=device)
+    plan = MessagePlan(ei, N)
+    eul = extract_euler_angles(torch.randn(E, 3, device=device), seed=2)
+    torch.library.opcheck(ops.edge_m0_rows, (None, eul, lmax, E), test_utils=("test_schema", "test_faketensor"))
+    rows = ops.edge_m0_rows(None, eul, lmax, E)
+    u = torch.randn(E, (lmax + 1) * C, device=device)
+    x = torch.randn(N, (lmax + 1) ** 2, C, device=device)
+    node = mode == "node"
+    args = (x, u, rows, plan.seg_ptr if node else None, plan.perm if node else None, lmax, C, 0.5, node)
+    torch.library.opcheck(ops.edge_degree_embed, args, test_utils=("test_schema", "test_faketensor"))
+    out = ops.edge_degree_embed(*args)
+    if node:
+        xi = x.clone()
+        torch.library.opcheck(ops.edge_degree_embed_, (xi.clone(), u, rows, plan.seg_ptr, plan.perm, lmax, C, 0.5),
+                              test_utils=("test_schema", "test_faketensor"))
+        ops.edge_degree_embed_(xi, u, rows, plan.seg_ptr, plan.perm, lmax, C, 0.5)
+        assert torch.equal(xi, out)
+    g = torch.randn(out.shape, device=device)
+    grows = ei[1].contiguous() if node else None
+    torch.library.opcheck(ops.edge_degree_embed_bwd, (g, grows, rows, lmax, C, 2.0 if node else 1.0),
+                          test_utils=("test_schema", "test_faketensor"))

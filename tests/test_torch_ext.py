@@ -14,7 +14,7 @@ from maloq_amd.so3 import jd_matrices, pack_jd
 
 OPS = ("edge_euler", "wigner_from_euler", "edge_vec_to_wigner", "edge_vec_to_wigner_out", "rotate", "segment_sum", "label_transform", "message_block_fwd",
        "message_block_bwd", "edgewise_fwd", "edgewise_bwd", "basis_row_meta", "fock_to_irreps", "irreps_to_fock",
-       "radial_fwd", "radial_bwd")
+       "radial_fwd", "radial_bwd", "edge_m0_rows", "edge_degree_embed", "edge_degree_embed_", "edge_degree_embed_bwd")
 
 
 def test_operators_come_from_the_extension():
