@@ -61,6 +61,10 @@ struct DwCfg {
   static constexpr int NSUB = KE / KC;           // fragment columns per step
   static constexpr int FRAGS = (DW_T / 32) * NSUB;  // fragments per operand per step
   static constexpr int STAGE = 2 * FRAGS * FRAG;    // A + B bytes per step
+  // fp32: four waves per SIMD (the accumulators then live in VGPRs, 118 in
+  // all, no spills); bf16 keeps its registers (it runs only where the
+  // transpose-read kernel cannot)
+  static constexpr int MIN_WAVES = TM::VEC == 4 ? 4 : 1;
 };
 
 // Transposes a VEC x VEC block held as VEC rows of 16 bytes (row = edge,
@@ -90,7 +94,7 @@ __device__ __forceinline__ void transpose_block(const uint4 (&in)[4], uint4 (&ou
 }
 
 template <class TM>
-__global__ __launch_bounds__(256) void dw_kernel(DwArgs a) {
+__global__ __launch_bounds__(256, DwCfg<TM>::MIN_WAVES) void dw_kernel(DwArgs a) {
   using Cfg = DwCfg<TM>;
   constexpr int VEC = Cfg::VEC, KE = Cfg::KE, NSUB = Cfg::NSUB;
   __shared__ alignas(16) char smem[2 * Cfg::STAGE];

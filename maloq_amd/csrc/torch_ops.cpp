@@ -538,7 +538,7 @@ at::Tensor pack_weights(int code, int64_t lmax, int64_t mmax, bool gate, int64_t
 // partials are summed in split order).  bf16: 256 x 256 output tiles, one
 // workgroup per CU, the most splits that keep every workgroup in one round;
 // fp32: 128 x 128 tiles, the count that balances the workgroups over the CUs
-// (at most three per CU, >= 1024 edges per split).
+// (at most four per CU, the kernel's occupancy; >= 1024 edges per split).
 int dw_splits(bool bf16, int64_t lmax, int64_t mmax, bool gate, int64_t c_out, int64_t c_in, int64_t E, int cus) {
   std::vector<std::pair<int64_t, int64_t>> groups{{lmax + 1, lmax + 1}};
   for (int64_t m = 1; m <= mmax; ++m) groups.emplace_back(2 * (lmax - m + 1), 2 * (lmax - m + 1));
@@ -552,7 +552,7 @@ int dw_splits(bool bf16, int64_t lmax, int64_t mmax, bool gate, int64_t c_out, i
   double best_cost = 0;
   bool have = false;
   for (int s = 1; s <= 16; ++s) {
-    if (ntiles * s > 3 * cus || s > std::max<int64_t>(1, E / 1024)) continue;
+    if (ntiles * s > 4 * cus || s > std::max<int64_t>(1, E / 1024)) continue;
     const double cost = static_cast<double>(cdiv(ntiles * s, cus)) / s;
     // ties go to the larger split count
     if (!have || cost < best_cost || (cost == best_cost && s > best)) {

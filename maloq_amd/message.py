@@ -539,9 +539,9 @@ def message_weight_grad(dz, y, lmax, mmax, c_out, c_in, splits=None, num_edges=N
             # 128 x 128 output tiles: the split count that balances the
             # workgroups over the compute units (the busiest CU runs
             # ceil(tiles * splits / CUs) of them, each 1 / splits of the edges),
-            # at most three per CU, >= 1024 edges per split
+            # at most four per CU (the kernel's occupancy), >= 1024 edges per split
             ntiles = sum(-(-rz * c_out // 128) * -(-ry * c_in // 128) for rz, ry in groups)
-            cands = [s for s in range(1, 17) if ntiles * s <= 3 * cus and s <= max(1, E // 1024)] or [1]
+            cands = [s for s in range(1, 17) if ntiles * s <= 4 * cus and s <= max(1, E // 1024)] or [1]
             splits = min(cands, key=lambda s: (-(-ntiles * s // cus) / s, -s))
     lib = _lib.load()
     parts = torch.empty(max(1, lib.maloq_message_dw_partials_floats(lmax, mmax, int(gate), c_out, c_in,
