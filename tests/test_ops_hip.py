@@ -353,3 +353,29 @@ def test_embedding_ops_opcheck(mode, device):
     grows = ei[1].contiguous() if node else None
     torch.library.opcheck(ops.edge_degree_embed_bwd, (g, grows, rows, lmax, C, 2.0 if node else 1.0),
                           test_utils=("test_schema", "test_faketensor"))
+
+
+@pytest.mark.gpu
+def test_embedding_ops_refuse_bad_arguments(device):
+    """The embedding operators raise ValueError (TORCH_CHECK_VALUE) on the
+    argument errors the C++ layer checks, before any launch."""
+    from maloq_amd import ops
+    lmax, C, N, E = 2, 16, 5, 7
+    d = (lmax + 1) ** 2
+    u = torch.randn(E, (lmax + 1) * C, device=device)
+    x = torch.randn(N, d, C, device=device)
+    rows = torch.randn(E, d, device=device)
+    seg = torch.zeros(N + 1, dtype=torch.long, device=device)
+    perm = torch.arange(E, device=device)
+    with pytest.raises(ValueError):  # both Wigner sources
+        ops.edge_m0_rows(torch.zeros(E, d, d, device=device), torch.zeros(E, 3, device=device), lmax, E)
+    with pytest.raises(ValueError):  # rows in bf16
+        ops.edge_degree_embed(x, u, rows.bfloat16(), seg, perm, lmax, C, 1.0, True)
+    with pytest.raises(ValueError):  # node mode without the dst plan
+        ops.edge_degree_embed(x, u, rows, None, None, lmax, C, 1.0, True)
+    with pytest.raises(ValueError):  # u of the wrong width
+        ops.edge_degree_embed(x, u[:, :-1], rows, seg, perm, lmax, C, 1.0, True)
+    with pytest.raises(ValueError):  # seg_ptr of the wrong length
+        ops.edge_degree_embed_(x, u, rows, seg[:-1], perm, lmax, C, 1.0)
+    with pytest.raises(ValueError):  # grad_rows of the wrong length
+        ops.edge_degree_embed_bwd(x, perm[:-1], rows, lmax, C, 1.0)
