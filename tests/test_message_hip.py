@@ -145,11 +145,23 @@ def test_edgewise_two_conv_matches_oracle(lmax, mmax, dtype, use_rad, device):
 def test_edgewise_gradients_match_oracle_autograd(lmax, mmax, dtype, mode, device):
     """Gradients of the two-convolution block (x, radial scales, both
     convolutions' weights and biases) against fp64 autograd of the oracle."""
+    _edgewise_gradient_case(lmax, mmax, dtype, mode, device, C=32, H=64, seed=300 + lmax)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_edgewise_gradients_three_channel_blocks(dtype, device):
+    """96 channels: three 32-channel output blocks per edge tile (an odd count
+    in the workgroup -> (tile, channel block) mapping, a 192-channel conv1
+    input), every kernel of the block forward and backward."""
+    _edgewise_gradient_case(4, 2, dtype, "node", device, C=96, H=96, seed=311)
+
+
+def _edgewise_gradient_case(lmax, mmax, dtype, mode, device, C, H, seed):
     from maloq_amd import message as M
     from maloq_amd.wigner import extract_euler_angles
-    print(f"edgewise grad case lmax={lmax} mmax={mmax} dtype={dtype} mode={mode}", flush=True)
-    N, E, C, H = 21, 260, 32, 64
-    gen = torch.Generator().manual_seed(300 + lmax)
+    print(f"edgewise grad case lmax={lmax} mmax={mmax} dtype={dtype} mode={mode} C={C} H={H}", flush=True)
+    N, E = 21, 260
+    gen = torch.Generator().manual_seed(seed)
     d = (lmax + 1) ** 2
     x = torch.randn(N, d, C, generator=gen, dtype=torch.float64)
     ei = _graph(N, E, gen, star=(lmax == 4))
