@@ -134,6 +134,35 @@ def message_step(w, backward=True, ops=True):
     return out
 
 
+def graph_step_leg(cfg="config1", dtype="fp32", reps=50):
+    """The training step of `message_step` (through the operators) enqueued op
+    by op, and the same step captured once into a HIP graph (torch.cuda.graph)
+    and replayed: wall time per step, host enqueue included.  Small graphs are
+    bound by the host's enqueue of the step's ~20 launches; the replay
+    enqueues one graph."""
+    import torch
+    w = message_workload(dtype, cfg=cfg)
+    step = lambda: message_step(w, True)
+    t_eager = time_steps(step, reps, 5)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    t_graph = time_steps(graph.replay, reps, 5)
+    E = w["E"]
+    del graph, w
+    torch.cuda.empty_cache()
+    return {"metric": "edges/s (fused block fwd+bwd, wall time)", "cfg": cfg, "dtype": dtype, "edges": E,
+            "us_per_step_eager": t_eager * 1e6, "us_per_step_hip_graph": t_graph * 1e6,
+            "eager_edges_per_s": E / t_eager, "hip_graph_edges_per_s": E / t_graph}
+
+
 def time_steps(fn, steps, warmup):
     import torch
     for _ in range(warmup):
@@ -1148,6 +1177,9 @@ def profile_only(args):
         # one layer at lmax = mmax = 6; prints its bench leg (no CPU baseline)
         print(json.dumps(reference_backbone_leg(args.dtype, steps=args.reps, warmup=1, cpu=False, lmax=6,
                                                 layers=1)), flush=True)
+    elif args.only == "graph-step":
+        print(json.dumps({c: graph_step_leg(c, args.dtype, reps=max(args.reps, 10)) for c in ("config1", "config2")}),
+              flush=True)
     elif args.only == "basis-tzvpd":
         print(json.dumps(wide_basis_leg(reps=args.reps, cpu=False)), flush=True)
     elif args.only in ("fwd", "step"):
@@ -1188,7 +1220,7 @@ def main(argv=None):
                     help="precision of the headline (the reference computes in fp32)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-extras", action="store_true", help="headline only")
-    ap.add_argument("--only", choices=["fwd", "step", "basis", "copy", "hbm", "host", "embed", "edgewise", "edgewise-step",
+    ap.add_argument("--only", choices=["fwd", "step", "basis", "copy", "hbm", "host", "graph-step", "embed", "edgewise", "edgewise-step",
                                        "rotate", "basis5", "basis-tzvpd", "ref-backbone", "ref-layer6", "ceiling"],
                     help="profiling mode: run one piece a few times and exit (no JSON line)")
     ap.add_argument("--cfg", default="config2", choices=sorted(MESSAGE_CONFIGS),
@@ -1256,6 +1288,9 @@ def main(argv=None):
         result[f"config2_{other}"] = message_leg("config2", other, max(5, args.steps // 2), 3, cpu=False)
         print("[bench] config 1 rotation ...", file=sys.stderr, flush=True)
         result["config1_rotation"] = rotation_leg(cpu=not args.no_cpu)
+        print("[bench] training step replayed from a HIP graph (config 1, config 2) ...", file=sys.stderr, flush=True)
+        result["hip_graph_step"] = {c: graph_step_leg(c, "fp32", reps=50 if c == "config1" else 10)
+                                    for c in ("config1", "config2")}
         for cfg in ("config4", "config5"):
             print(f"[bench] {cfg} fused block (bf16) ...", file=sys.stderr, flush=True)
             result[cfg] = message_leg(cfg, "bf16", max(5, args.steps // 2), 3, cpu=not args.no_cpu)

@@ -1,0 +1,86 @@
+"""A whole training step of the fused block, captured once into a HIP graph
+(torch.cuda.graph over the maloq_hip operators) and replayed: the path for
+launch-bound small graphs such as config 1, where the host's enqueue of the
+step's kernels costs more than the kernels.  The step is the one the
+benchmark times: Euler angles, the fused RadialMLP, the block forward and
+backward.  Every replay, with eager work between replays, must give the eager
+step's output and gradients bit for bit (the kernels are deterministic)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _workload(dt, device):
+    from maloq_amd import message as M
+    from maloq_amd.radial import RadialMLP
+    from maloq_amd.synth import config1_graph
+    g = config1_graph()
+    L = Mm = 2
+    C = 32
+    gen = torch.Generator().manual_seed(0)
+    plan = M.MessagePlan(torch.from_numpy(np.stack([g.src, g.dst])).to(device), g.num_nodes)
+    vec = plan.sort_edges(torch.from_numpy(g.edge_distance_vec()).float().to(device))
+    offsets = torch.linspace(0.0, 5.0, 8, device=device)
+    coeff = -0.5 / float(offsets[1] - offsets[0]) ** 2
+    rbf = torch.exp(coeff * (vec.norm(dim=1, keepdim=True) - offsets) ** 2)
+    x = torch.randn(g.num_nodes, (L + 1) ** 2, C, generator=gen).to(device=device, dtype=dt).requires_grad_()
+    w0 = (torch.randn((L + 1) * C, (L + 1) * C, generator=gen) / math.sqrt((L + 1) * C)).to(device).requires_grad_()
+    b0 = torch.zeros((L + 1) * C, device=device, requires_grad=True)
+    wm = [(torch.randn(2 * (L - m + 1) * C, (L - m + 1) * C, generator=gen) / math.sqrt((L - m + 1) * C))
+          .to(device).requires_grad_() for m in (1, 2)]
+    torch.manual_seed(0)
+    radial = RadialMLP([8, 64, 64, M.rad_width(L, Mm, C)]).to(device)
+    gout = torch.randn(g.num_nodes, (L + 1) ** 2, C, generator=gen).to(device)
+    params = [x, w0, b0, *wm, *radial.parameters()]
+    return dict(plan=plan, vec=vec, rbf=rbf, x=x, w0=w0, b0=b0, wm=wm, radial=radial, gout=gout, dt=dt,
+                L=L, M=Mm, params=params)
+
+
+def _step(w):
+    from maloq_amd import ops
+    from maloq_amd.wigner import extract_euler_angles
+    eul = extract_euler_angles(w["vec"], seed=1234)
+    rad = w["radial"](w["rbf"], out_dtype=w["dt"])
+    out = ops.message_block(w["x"], w["plan"], eul, rad, w["w0"], w["b0"], w["wm"], w["L"], w["M"])
+    for t in w["params"]:
+        t.grad = None
+    out.backward(w["gout"])
+    return out
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_training_step_replays_from_a_hip_graph(dt, device):
+    print(f"graph capture case dtype={dt}", flush=True)
+    w = _workload(dt, device)
+    # warm-up on a side stream (the per-device tables are uploaded here, not
+    # during capture), then capture one step
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            _step(w)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_g = _step(w)
+    grads_g = [t.grad for t in w["params"]]
+    assert all(gr is not None for gr in grads_g)
+    # the eager step (new gradient tensors; the graph keeps its own)
+    ref = _step(w).detach().clone()
+    ref_grads = [t.grad.detach().clone() for t in w["params"]]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        # eager work between replays, on the same stream
+        _step(w)
+        (w["x"].detach().float() * 2).sum()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, ref), f"replay {rep}: output differs from the eager step"
+        for i, (a, b) in enumerate(zip(grads_g, ref_grads)):
+            assert torch.equal(a, b), f"replay {rep}: gradient {i} differs from the eager step"
