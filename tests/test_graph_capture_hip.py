@@ -1,10 +1,11 @@
-"""A whole training step of the fused block, captured once into a HIP graph
-(torch.cuda.graph over the maloq_hip operators) and replayed: the path for
-launch-bound small graphs such as config 1, where the host's enqueue of the
-step's kernels costs more than the kernels.  The step is the one the
-benchmark times: Euler angles, the fused RadialMLP, the block forward and
-backward.  Every replay, with eager work between replays, must give the eager
-step's output and gradients bit for bit (the kernels are deterministic)."""
+"""A whole training step of the fused block, and a forward + backward call of
+the drop-in Edgewise module, captured once into a HIP graph (torch.cuda.graph
+over the maloq_hip operators) and replayed: the path for launch-bound small
+graphs such as config 1, where the host's enqueue of the step's kernels costs
+more than the kernels.  The step is the one the benchmark times: Euler
+angles, the fused RadialMLP, the block forward and backward.  Every replay,
+with eager work between replays, must give the eager call's output and
+gradients bit for bit (the kernels are deterministic)."""
 import math
 
 import numpy as np
@@ -84,3 +85,63 @@ def test_training_step_replays_from_a_hip_graph(dt, device):
         assert torch.equal(out_g, ref), f"replay {rep}: output differs from the eager step"
         for i, (a, b) in enumerate(zip(grads_g, ref_grads)):
             assert torch.equal(a, b), f"replay {rep}: gradient {i} differs from the eager step"
+
+
+@pytest.mark.parametrize("lmax,mmax,C,H,ecl,dense", [
+    (4, 2, 32, 64, (8, 32, 32), False),
+    # the reference's example layer: lmax = mmax = 4, C = H = 128, radial
+    # [384, 128, 128] (torch layers ahead of the fused tail), dense wigner
+    (4, 4, 128, 128, (384, 128, 128), True)])
+def test_edgewise_layer_replays_from_a_hip_graph(lmax, mmax, C, H, ecl, dense, device):
+    """The drop-in Edgewise module, called as the reference's backbone calls
+    it (no plan=: the cached plan of the first call), forward and backward
+    captured into one HIP graph; every replay bitwise equal to the eager call."""
+    from maloq_amd.edgewise import Edgewise
+    from maloq_amd.so3 import CoefficientMapping
+    from maloq_amd.wigner import extract_euler_angles, wigner_from_eulers
+    print(f"graph capture Edgewise case lmax={lmax} mmax={mmax} C={C} dense={dense}", flush=True)
+    torch.manual_seed(0)
+    mod = Edgewise(C, H, lmax, mmax, list(ecl), CoefficientMapping(lmax, mmax), None, 6.0,
+                   "source-target").to(device)
+    gen = torch.Generator().manual_seed(7)
+    N, E = 23, 300
+    x = torch.randn(N, (lmax + 1) ** 2, C, generator=gen).to(device).requires_grad_()
+    ei = torch.stack([torch.randint(0, N, (E,), generator=gen), torch.randint(0, N - 2, (E,), generator=gen)])
+    ei = ei.to(device)
+    x_edge = torch.randn(E, ecl[0], generator=gen).to(device).requires_grad_()
+    eul = extract_euler_angles(torch.randn(E, 3, generator=gen).to(device), seed=5)
+    w = wigner_from_eulers(eul, None, lmax) if dense else None
+    winv = w.transpose(1, 2).contiguous() if dense else None
+    gout = torch.randn(N, (lmax + 1) ** 2, C, generator=gen).to(device)
+    leaves = [x, x_edge, *mod.parameters()]
+
+    def call():
+        out = mod(x, None, x_edge, ei, w, winv, "node", eulers=None if dense else eul)
+        for t in leaves:
+            t.grad = None
+        out.backward(gout)
+        return out
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            call()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_g = call()
+    grads_g = [t.grad for t in leaves]
+    ref = call().detach().clone()
+    ref_grads = [t.grad.detach().clone() for t in leaves]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        call()
+        (x.detach() * 3).sum()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, ref), f"replay {rep}: output differs from the eager call"
+        for i, (a, b) in enumerate(zip(grads_g, ref_grads)):
+            assert torch.equal(a, b), f"replay {rep}: gradient {i} differs from the eager call"
