@@ -57,34 +57,39 @@ def _step(w):
 def test_training_step_replays_from_a_hip_graph(dt, device):
     print(f"graph capture case dtype={dt}", flush=True)
     w = _workload(dt, device)
-    # warm-up on a side stream (the per-device tables are uploaded here, not
-    # during capture), then capture one step
+    _check_replays(lambda: _step(w), w["params"])
+
+
+def _check_replays(call, leaves):
+    """Warm-up (the per-device tables are uploaded here, not during capture),
+    capture of one call, the eager reference, and three replays with eager
+    work between them, all on one side stream (autograd's gradient
+    accumulators then stay on the stream they were made on)."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         for _ in range(3):
-            _step(w)
+            call()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            out_g = call()
+        grads_g = [t.grad for t in leaves]
+        assert all(gr is not None for gr in grads_g)
+        # the eager call (new gradient tensors; the graph keeps its own)
+        ref = call().detach().clone()
+        ref_grads = [t.grad.detach().clone() for t in leaves]
+        torch.cuda.synchronize()
+        for rep in range(3):
+            call()
+            (leaves[0].detach().float() * 2).sum()
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out_g, ref), f"replay {rep}: output differs from the eager call"
+            for i, (a, b) in enumerate(zip(grads_g, ref_grads)):
+                assert torch.equal(a, b), f"replay {rep}: gradient {i} differs from the eager call"
     torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        out_g = _step(w)
-    grads_g = [t.grad for t in w["params"]]
-    assert all(gr is not None for gr in grads_g)
-    # the eager step (new gradient tensors; the graph keeps its own)
-    ref = _step(w).detach().clone()
-    ref_grads = [t.grad.detach().clone() for t in w["params"]]
-    torch.cuda.synchronize()
-    for rep in range(3):
-        # eager work between replays, on the same stream
-        _step(w)
-        (w["x"].detach().float() * 2).sum()
-        torch.cuda.synchronize()
-        graph.replay()
-        torch.cuda.synchronize()
-        assert torch.equal(out_g, ref), f"replay {rep}: output differs from the eager step"
-        for i, (a, b) in enumerate(zip(grads_g, ref_grads)):
-            assert torch.equal(a, b), f"replay {rep}: gradient {i} differs from the eager step"
 
 
 @pytest.mark.parametrize("lmax,mmax,C,H,ecl,dense", [
@@ -122,26 +127,4 @@ def test_edgewise_layer_replays_from_a_hip_graph(lmax, mmax, C, H, ecl, dense, d
         out.backward(gout)
         return out
 
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        for _ in range(3):
-            call()
-    torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        out_g = call()
-    grads_g = [t.grad for t in leaves]
-    ref = call().detach().clone()
-    ref_grads = [t.grad.detach().clone() for t in leaves]
-    torch.cuda.synchronize()
-    for rep in range(3):
-        call()
-        (x.detach() * 3).sum()
-        torch.cuda.synchronize()
-        graph.replay()
-        torch.cuda.synchronize()
-        assert torch.equal(out_g, ref), f"replay {rep}: output differs from the eager call"
-        for i, (a, b) in enumerate(zip(grads_g, ref_grads)):
-            assert torch.equal(a, b), f"replay {rep}: gradient {i} differs from the eager call"
+    _check_replays(call, leaves)
