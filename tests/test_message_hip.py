@@ -148,12 +148,14 @@ def test_edgewise_gradients_match_oracle_autograd(lmax, mmax, dtype, mode, devic
     _edgewise_gradient_case(lmax, mmax, dtype, mode, device, C=32, H=64, seed=300 + lmax)
 
 
+@pytest.mark.parametrize("lmax,mmax", [(4, 2), (6, 2), (4, 4)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_edgewise_gradients_three_channel_blocks(dtype, device):
+def test_edgewise_gradients_three_channel_blocks(lmax, mmax, dtype, device):
     """96 channels: three 32-channel output blocks per edge tile (an odd count
     in the workgroup -> (tile, channel block) mapping, a 192-channel conv1
-    input), every kernel of the block forward and backward."""
-    _edgewise_gradient_case(4, 2, dtype, "node", device, C=96, H=96, seed=311)
+    input), every kernel of the block forward and backward; lmax 6 runs the
+    8-wave kernels with the gate rows on the light waves."""
+    _edgewise_gradient_case(lmax, mmax, dtype, "node", device, C=96, H=96, seed=311 + lmax + mmax)
 
 
 def _edgewise_gradient_case(lmax, mmax, dtype, mode, device, C, H, seed):
