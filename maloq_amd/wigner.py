@@ -72,13 +72,8 @@ def _check_vec(edge_distance_vec):
 def extract_euler_angles(edge_distance_vec: torch.Tensor, seed: int) -> torch.Tensor:
     """[E, 3] (alpha, beta, gamma) exactly as the Wigner kernel computes them."""
     _check_vec(edge_distance_vec)
-    E = edge_distance_vec.shape[0]
-    eulers = torch.empty(E, 3, device=edge_distance_vec.device, dtype=torch.float32)
-    if E > 0:
-        v = edge_distance_vec.contiguous()
-        _lib.call("maloq_edge_euler", _lib.ptr(v), E, int(seed) & (2**64 - 1), _lib.ptr(eulers),
-                  _lib.stream_of(v.device))
-    return eulers
+    from . import ops
+    return ops.edge_euler(edge_distance_vec, _seed64(seed))
 
 
 def _seed64(seed) -> int:
@@ -136,6 +131,9 @@ def wigner_from_eulers(eulers: torch.Tensor, Jd, lmax: int, inverse: bool = Fals
     _lib.require_cuda(eulers)
     if eulers.dtype != torch.float32 or eulers.dim() != 2 or eulers.shape[1] != 3:
         raise ValueError("eulers must be float32 [E, 3]")
+    if Jd is None:  # the closed-form J tables the operator carries
+        from . import ops
+        return ops.wigner_from_euler(eulers, lmax, inverse)
     E, d = eulers.shape[0], (lmax + 1) ** 2
     w = torch.empty(E, d, d, device=eulers.device, dtype=torch.float32)
     if E > 0:
