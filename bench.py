@@ -134,6 +134,81 @@ def message_step(w, backward=True, ops=True):
     return out
 
 
+def fock_head_leg(reps=10):
+    """Fock_Irreps_Head (esen_osh.py:522-1064) forward, and forward + backward,
+    on the config-3 batch (64 molecules; lmax 4 node and edge embeddings of
+    width C = 128, the reference's model width), and the label-side eval
+    formats on the same batch: the padding mask, sort_by_m of one molecule's
+    Fock matrix, and the CSR export of the whole block list."""
+    import numpy as np
+    import torch
+    from maloq_amd import synth
+    from maloq_amd.fock_utils import create_label_unpadding_mask, sort_by_m, sparse_block_matrix_to_csr_arrays
+    from maloq_amd.irreps_head import Fock_Irreps_Head
+    from maloq_amd.matrix2labels import SparseBlockMatrix
+    bw = basis_workload()
+    t, dev, T = bw["tables"], bw["data"].device, bw["T"]
+    Z, rows, cols = bw["Z"], bw["rows"], bw["cols"]
+    off_site = rows != cols
+    src, dst = rows[off_site], cols[off_site]
+    N, E = len(Z), int(off_site.sum())
+    lmax, C = 4, 128
+    torch.manual_seed(0)
+    head = Fock_Irreps_Head("+".join(f"{C}x{l}e" for l in range(lmax + 1)), t.req_output_irreps, lmax, C,
+                            ls_list=t.ls_list).to(dev)
+    d = (lmax + 1) ** 2
+    emb = {"node_embeddings": torch.randn(N, d, C, device=dev, requires_grad=True),
+           "edge_embeddings": torch.randn(E, d, C, device=dev, requires_grad=True)}
+
+    def fwd():
+        with torch.no_grad():
+            return head(emb, None)
+    node, edge = fwd()
+    gn, ge = torch.randn_like(node), torch.randn_like(edge)
+
+    def step():
+        n_, e_ = head(emb, None)
+        torch.autograd.backward([n_, e_], [gn, ge])
+    t_fwd = kernel_time_events(fwd, reps)
+    t_step = kernel_time_events(step, reps)
+    # the head reads the embeddings and writes the label rows (and the reverse
+    # in the backward): its algorithmic bytes per forward
+    fwd_bytes = (N + E) * (d * C + T) * 4
+    out = {"metric": "label rows/s", "config": f"config 3 batch: {N} atoms, {E} atom pairs, T = {T}, C = {C}",
+           "fwd_rows_per_s": (N + E) / t_fwd, "fwd_bwd_rows_per_s": (N + E) / t_step,
+           "us_fwd": t_fwd * 1e6, "us_fwd_bwd": t_step * 1e6,
+           "roofline": {"scope": "whole forward (per-l linears, gate, column gather)", "bound": "hbm",
+                        "achieved": fwd_bytes / t_fwd / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                        "frac": fwd_bytes / t_fwd / PEAK_HBM, "bytes_per_call": fwd_bytes}}
+    # padding mask of the batch (host tables + one launch), wall time
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        create_label_unpadding_mask(t.orbital_template, Z, src, dst, T, dev)
+    torch.cuda.synchronize()
+    out["us_label_mask"] = (time.perf_counter() - t0) / reps * 1e6
+    # sort_by_m of the largest molecule's dense Fock matrix
+    z, p = max(bw["mols"], key=lambda m: len(m[0]))
+    H, _ = synth.dense_hamiltonian(z, p, t.orbitals_per_atom(z), seed=0, cutoff=8.0)
+    Hd = torch.from_numpy(H.astype(np.float32)).to(dev)
+    sort_by_m(Hd, CFG3_BASIS, z)
+    ts = kernel_time_events(lambda: sort_by_m(Hd, CFG3_BASIS, z), reps)
+    out["sort_by_m"] = {"n": int(H.shape[0]), "us": ts * 1e6, "GBps": 2 * Hd.numel() * 4 / ts / 1e9}
+    # CSR arrays of the whole block list (device arrays; the scipy object is a host copy)
+    sbm = SparseBlockMatrix(data=bw["data"], block_data_offsets=bw["bdo"],
+                            fock_block_rows=torch.from_numpy(rows).to(dev),
+                            fock_block_cols=torch.from_numpy(cols).to(dev),
+                            fock_block_offsets=torch.from_numpy(bw["off"]).to(dev))
+    sparse_block_matrix_to_csr_arrays(sbm)
+    tc = kernel_time_events(lambda: sparse_block_matrix_to_csr_arrays(sbm), reps)
+    nnz = bw["data"].numel()
+    out["csr_export"] = {"nnz": nnz, "us": tc * 1e6,
+                         "GBps": (4 * nnz + (4 + 8) * nnz) / tc / 1e9}  # values in, values + column indices out
+    del bw, head, emb
+    torch.cuda.empty_cache()
+    return out
+
+
 def graph_step_leg(cfg="config1", dtype="fp32", reps=50):
     """The training step of `message_step` (through the operators) enqueued op
     by op, and the same step captured once into a HIP graph (torch.cuda.graph)
@@ -1176,6 +1251,8 @@ def profile_only(args):
         # one layer at lmax = mmax = 6; prints its bench leg (no CPU baseline)
         print(json.dumps(reference_backbone_leg(args.dtype, steps=args.reps, warmup=1, cpu=False, lmax=6,
                                                 layers=1)), flush=True)
+    elif args.only == "fock-head":
+        print(json.dumps(fock_head_leg(reps=max(args.reps, 5))), flush=True)
     elif args.only == "graph-step":
         print(json.dumps({c: graph_step_leg(c, args.dtype, reps=max(args.reps, 10)) for c in ("config1", "config2")}),
               flush=True)
@@ -1219,7 +1296,7 @@ def main(argv=None):
                     help="precision of the headline (the reference computes in fp32)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-extras", action="store_true", help="headline only")
-    ap.add_argument("--only", choices=["fwd", "step", "basis", "copy", "hbm", "host", "graph-step", "embed", "edgewise", "edgewise-step",
+    ap.add_argument("--only", choices=["fwd", "step", "basis", "copy", "hbm", "host", "graph-step", "fock-head", "embed", "edgewise", "edgewise-step",
                                        "rotate", "basis5", "basis-tzvpd", "ref-backbone", "ref-layer6", "ceiling"],
                     help="profiling mode: run one piece a few times and exit (no JSON line)")
     ap.add_argument("--cfg", default="config2", choices=sorted(MESSAGE_CONFIGS),
@@ -1314,6 +1391,8 @@ def main(argv=None):
         del sw
         print("[bench] basis transform (config 3 molecules, def2-TZVPD template) ...", file=sys.stderr, flush=True)
         result["def2_tzvpd_basis_transform"] = wide_basis_leg(cpu=not args.no_cpu)
+        print("[bench] Fock_Irreps_Head and eval formats (config 3) ...", file=sys.stderr, flush=True)
+        result["fock_irreps_head"] = fock_head_leg()
         print("[bench] edge-degree embedding (config 2) ...", file=sys.stderr, flush=True)
         ew = embed_workload()
         s = torch.cuda.current_stream()

@@ -284,6 +284,37 @@ class _Gather(torch.autograd.Function):
         return dz, None
 
 
+class _RowLinear(torch.autograd.Function):
+    """y = x W (+ b) over many rows.  The weight gradient x^T dy is a reduction
+    over all rows, which the library runs as one product on a few dozen
+    workgroups (2.7 ms for 97 k rows); here it is summed over fixed chunks of
+    rows by one batched product (deterministic: the chunking depends only on
+    the row count)."""
+
+    @staticmethod
+    def forward(ctx, x, w, b):
+        ctx.save_for_backward(x, w)
+        ctx.has_b = b is not None
+        return torch.addmm(b, x, w) if b is not None else x @ w
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, w = ctx.saved_tensors
+        gx = gy @ w.t() if ctx.needs_input_grad[0] else None
+        gw = None
+        if ctx.needs_input_grad[1]:
+            rows = x.shape[0]
+            nc = max(1, min(256, rows // 2048))
+            k = -(-rows // nc)
+            pad = nc * k - rows
+            xp = torch.nn.functional.pad(x, (0, 0, 0, pad)) if pad else x
+            gp = torch.nn.functional.pad(gy, (0, 0, 0, pad)) if pad else gy
+            gw = torch.bmm(xp.reshape(nc, k, x.shape[1]).transpose(1, 2).contiguous(),
+                           gp.reshape(nc, k, gy.shape[1]).contiguous()).sum(0)
+        gb = gy.sum(0) if ctx.has_b and ctx.needs_input_grad[2] else None
+        return gx, gw, gb
+
+
 class _GateFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, s, lmax, act):
@@ -410,16 +441,22 @@ class Fock_Irreps_Head(nn.Module):
             raise ValueError(f"embeddings must be float32 [rows, {(self.lmax + 1) ** 2}, {self.sphere_channels}]")
         x = x.contiguous()
         ls = self.lin_scalars_learnable[spin]
-        s = torch.addmm(ls.bias, x[:, 0, :], ls.matrix()) if ls.bias.numel() else x[:, 0, :] @ ls.matrix()
+        s = _RowLinear.apply(x[:, 0, :], ls.matrix(), ls.bias if ls.bias.numel() else None)
         g = _GateFn.apply(x, s.contiguous(), self.lmax, self._act)
+        # one flat [rows (2l+1), C] x [C, mul_l] GEMM per degree: split (its
+        # backward is one concatenation) rather than slices of g (whose
+        # gradients would each be a zero-filled full-size tensor, summed), and
+        # no batched [2l+1, C] products per row
+        gl = torch.split(g, [2 * l + 1 for l in range(self.lmax + 1)], dim=1)
+        rows, C = x.shape[0], x.shape[2]
         zs = []
         for l, lin in enumerate(lin_layers):
             if lin.mul_out == 0:
                 continue
-            y = torch.matmul(g[:, l * l:(l + 1) ** 2, :], lin.matrix())   # [rows, 2l+1, mul_l]
+            y = _RowLinear.apply(gl[l].reshape(rows * (2 * l + 1), C), lin.matrix(), None)   # [rows (2l+1), mul_l]
             if l == 0 and lin.bias.numel():
                 y = y + lin.bias
-            zs.append(y.reshape(x.shape[0], (2 * l + 1) * lin.mul_out))
+            zs.append(y.view(rows, (2 * l + 1) * lin.mul_out))
         return torch.cat(zs, dim=1)
 
     def _process(self, x, lin_layers, spin, stream):
