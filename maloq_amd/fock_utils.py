@@ -215,19 +215,36 @@ def m_order_permutation(orbital_basis, atomic_numbers, direction="orca_to_e3nn")
     return np.asarray(src, np.int32), np.asarray(sign, np.float32)
 
 
+_PERM_CACHE: dict = {}
+
+
+def _signed_permutation_on(orbital_basis, atomic_numbers, direction, dev):
+    """m_order_permutation as device arrays, kept per (basis, atomic numbers,
+    direction, device): an eval loop over molecules of repeated composition
+    builds and uploads each permutation once."""
+    key = (tuple(sorted((int(z), tuple(int(l) for l in ls)) for z, ls in orbital_basis.items())),
+           tuple(int(z) for z in atomic_numbers), direction, str(dev))
+    hit = _PERM_CACHE.get(key)
+    if hit is None:
+        src, sign = m_order_permutation(orbital_basis, atomic_numbers, direction)
+        if len(_PERM_CACHE) > 256:
+            _PERM_CACHE.clear()
+        hit = _PERM_CACHE[key] = (_i32(src, dev), torch.from_numpy(sign).to(dev))
+    return hit
+
+
 def sort_by_m(hamiltonian, orbital_basis, atomic_numbers, direction="orca_to_e3nn"):
     """The Hamiltonian [n, n] (fp32, on the GPU) with every shell's m-components
     reordered and reflected (utils_orca_out.py:402-465); a new tensor."""
     _lib.require_cuda(hamiltonian)
     if hamiltonian.dtype != torch.float32 or hamiltonian.dim() != 2 or hamiltonian.stride(1) != 1:
         raise ValueError("hamiltonian must be a float32 [n, n] tensor with unit column stride")
-    src, sign = m_order_permutation(orbital_basis, atomic_numbers, direction)
-    n = hamiltonian.shape[0]
-    if len(src) != n or hamiltonian.shape[1] != n:
-        raise ValueError(f"the basis has {len(src)} functions, the matrix is {tuple(hamiltonian.shape)}")
     dev = hamiltonian.device
+    src_d, sign_d = _signed_permutation_on(orbital_basis, atomic_numbers, direction, dev)
+    n = hamiltonian.shape[0]
+    if src_d.shape[0] != n or hamiltonian.shape[1] != n:
+        raise ValueError(f"the basis has {src_d.shape[0]} functions, the matrix is {tuple(hamiltonian.shape)}")
     out = torch.empty(n, n, device=dev, dtype=torch.float32)
-    src_d, sign_d = _i32(src, dev), torch.from_numpy(sign).to(dev)   # alive across the launch
     _lib.call("maloq_signed_permute", _lib.ptr(hamiltonian), n, hamiltonian.stride(0), _lib.ptr(src_d),
               _lib.ptr(sign_d), _lib.ptr(out), n, _lib.stream_of(dev))
     return out
